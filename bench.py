@@ -1,0 +1,317 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X block-quantised projection path.
+
+Metric: "Q8_0 decode GEMV GB/s (% HBM peak); prefill GEMM int8
+TOPS (% MFMA peak)".
+
+step     One decode token's projections of a Llama-3-8B-shaped model with Q8_0
+         weights (BASELINE config 1 shapes, 32 layers + lm_head): per layer
+         Q|K|V as one batched GEMV (4096->4096, 4096->1024, 4096->1024), o
+         (4096->4096), gate|up as one batched GEMV (4096->14336 x2) and down
+         (14336->4096); then lm_head (4096->128256).  7.97 GB of weights, all
+         resident in HBM and distinct (no cache reuse between launches), fp32
+         N(0,1) activations.  The step's 129 launches are captured once in a
+         HIP graph and replayed.
+value    whole-step algorithmic bytes (weights + x + y per launch) / step time.
+roofline dominant kernel: the Q8_0 GEMV at 4096x14336 (down projection, the
+         north-star target shape), timed per launch with HIP events on the
+         launch stream while the stream is kept busy, rotating over the 32
+         layers' distinct down matrices (2 GB).
+secondary int8 prefill GEMM at M=2048, gate/up shape
+         14336x4096 and down shape 4096x14336, as TOPS vs the int8 MFMA peak.
+cpu_baseline the reference's own AVX2 ComputePool path (compiled from the
+         reference sources into oracle/_ref) on this host's cores, on one
+         layer's seven projections; falls back to the C oracle if absent.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+       python bench.py --summarize-trace kernel_trace.csv   (rocprofv3 helper)
+"""
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+INT8_PEAK_TOPS = 5000.0        # MI355X dense int8 MFMA (POP/s x 1000)
+
+HIDDEN, FFN, KV, VOCAB, LAYERS = 4096, 14336, 1024, 128256, 32
+
+
+def gemv_bytes(fmt_rb, rows, cols):
+    return rows * fmt_rb + 4 * cols + 4 * rows
+
+
+def summarize_trace(path):
+    """Group a rocprofv3 kernel_trace.csv by (kernel, grid, LDS) -> count, avg, total."""
+    import csv
+    groups = {}
+    with open(path) as f:
+        for row in csv.DictReader(f):
+            name = row.get("Kernel_Name", "?")
+            grid = row.get("Grid_Size_X", row.get("Grid_Size", "?"))
+            lds = row.get("LDS_Block_Size", row.get("Lds_Size", row.get("LDS_Size", "?")))
+            dur = int(row["End_Timestamp"]) - int(row["Start_Timestamp"])
+            g = groups.setdefault((name, grid, lds), [])
+            g.append(dur)
+    print(f"{'count':>6} {'avg_us':>10} {'total_ms':>10}  grid  lds  kernel")
+    for (name, grid, lds), d in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+        print(f"{len(d):6d} {np.mean(d) / 1e3:10.2f} {sum(d) / 1e6:10.3f}  {grid} {lds}  {name[:110]}")
+
+
+def cpu_baseline(seconds=8.0):
+    """Reference CPU path (oracle/_ref) on one layer's seven Q8_0 projections."""
+    from oracle import oracle as O
+    o = O.Oracle()
+    kind = "reference"
+    try:
+        r = O.Reference()
+        if not r.has_avx2():
+            raise RuntimeError("no AVX2")
+    except Exception:
+        r, kind = None, "port"
+    shapes = [(HIDDEN, HIDDEN), (KV, HIDDEN), (KV, HIDDEN), (HIDDEN, HIDDEN), (FFN, HIDDEN), (FFN, HIDDEN), (HIDDEN, FFN)]
+    ws = [o.gen_weights(O.Q8_0, 0xC0 + i, rr, cc) for i, (rr, cc) in enumerate(shapes)]
+    xs = {c: o.gen_normal(0xC1 + c, c) for c in (HIDDEN, FFN)}
+    nbytes = sum(gemv_bytes(o.row_bytes(O.Q8_0, c), rr, c) for rr, c in shapes)
+    workers = max(1, min(16, os.cpu_count() or 1, 32))
+
+    def one_pass():
+        for w, (rr, cc) in zip(ws, shapes):
+            if r is not None:
+                r.gemv(O.Q8_0, w, xs[cc], rr, cc, workers)
+            else:
+                o.gemv_f32(O.Q8_0, w, xs[cc], rr, cc)
+
+    one_pass()
+    times, t_end = [], time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < 6:
+        t0 = time.perf_counter()
+        one_pass()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times[1:])
+    return {"value": round(nbytes / med / 1e9, 2), "unit": "GB/s", "cores": workers if r is not None else 1,
+            "kind": kind,
+            "sample": f"one Llama-3-8B layer's 7 Q8_0 decode GEMVs ({nbytes / 1e6:.1f} MB), "
+                      f"{len(times)} passes, median of all but the first; "
+                      + ("reference quant::gemv (AVX2 + ComputePool) built from its sources"
+                         if r is not None else "scalar C oracle")}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--summarize-trace")
+    args = ap.parse_args()
+    if args.summarize_trace:
+        summarize_trace(args.summarize_trace)
+        return 0
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this path has no multi-GPU leg in this build "
+              "(row-sharding design only; see DESIGN.md)", file=sys.stderr)
+        return 2
+
+    import torch
+    from zeninfer_amd import zq
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    st = zq.init()
+    if st != 0:
+        raise RuntimeError(f"zq_hip_init: {zq.status_string(st)}")
+    info = zq.info()
+    Q8 = zq.Q8_0
+    rbh, rbf = zq.row_bytes(Q8, HIDDEN), zq.row_bytes(Q8, FFN)
+
+    def weights(rows, cols, seed):
+        t = torch.empty(zq.weight_bytes(Q8, rows, cols), dtype=torch.uint8, device=dev)
+        zq.synth_weights_dev(Q8, seed, t, rows, cols)
+        return t
+
+    print(f"[bench] device {info['name']} {info['arch']} CUs={info['compute_units']}", file=sys.stderr, flush=True)
+    layers = []
+    for l in range(LAYERS):
+        s = 1000 * (l + 1)
+        layers.append({"q": weights(HIDDEN, HIDDEN, s + 1), "k": weights(KV, HIDDEN, s + 2),
+                       "v": weights(KV, HIDDEN, s + 3), "o": weights(HIDDEN, HIDDEN, s + 4),
+                       "gate": weights(FFN, HIDDEN, s + 5), "up": weights(FFN, HIDDEN, s + 6),
+                       "down": weights(HIDDEN, FFN, s + 7)})
+    lm_head = weights(VOCAB, HIDDEN, 7)
+    x_h = torch.empty(HIDDEN, device=dev)
+    x_f = torch.empty(FFN, device=dev)
+    zq.synth_normal_dev(11, x_h, HIDDEN)
+    zq.synth_normal_dev(12, x_f, FFN)
+    y_q, y_k, y_v, y_o = (torch.empty(n, device=dev) for n in (HIDDEN, KV, KV, HIDDEN))
+    y_g, y_u, y_d = (torch.empty(n, device=dev) for n in (FFN, FFN, HIDDEN))
+    y_lm = torch.empty(VOCAB, device=dev)
+    torch.cuda.synchronize()
+    print("[bench] weights generated", file=sys.stderr, flush=True)
+
+    stream = torch.cuda.current_stream()
+
+    def step():
+        for L in layers:
+            zq.gemv_batch_dev(Q8, x_h, [(L["q"], y_q, HIDDEN), (L["k"], y_k, KV), (L["v"], y_v, KV)], HIDDEN, stream)
+            zq.gemv_dev(Q8, L["o"], x_h, y_o, HIDDEN, HIDDEN, stream)
+            zq.gemv_batch_dev(Q8, x_h, [(L["gate"], y_g, FFN), (L["up"], y_u, FFN)], HIDDEN, stream)
+            zq.gemv_dev(Q8, L["down"], x_f, y_d, HIDDEN, FFN, stream)
+        zq.gemv_dev(Q8, lm_head, x_h, y_lm, VOCAB, HIDDEN, stream)
+
+    layer_bytes = (gemv_bytes(rbh, HIDDEN, HIDDEN) * 2 + gemv_bytes(rbh, KV, HIDDEN) * 2
+                   + gemv_bytes(rbh, FFN, HIDDEN) * 2 + gemv_bytes(rbf, HIDDEN, FFN))
+    # batched launches read x once: subtract the duplicate x reads of the batch members
+    layer_bytes -= 4 * HIDDEN * 2 + 4 * HIDDEN * 1
+    step_bytes = LAYERS * layer_bytes + gemv_bytes(rbh, VOCAB, HIDDEN)
+
+    # eager reference output, then capture the step as a graph
+    step()
+    torch.cuda.synchronize()
+    eager_lm = y_lm.clone()
+    eager_d = y_d.clone()
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    cap.wait_stream(stream)
+    with torch.cuda.stream(cap):
+        with torch.cuda.graph(graph, stream=cap):
+            stream = cap
+            step()
+    stream = torch.cuda.current_stream()
+    torch.cuda.synchronize()
+    for _ in range(max(1, args.warmup)):
+        graph.replay()
+    torch.cuda.synchronize()
+    graph_ok = bool(torch.equal(y_lm, eager_lm) and torch.equal(y_d, eager_d))
+
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    ev0.record()
+    for _ in range(args.steps):
+        graph.replay()
+    ev1.record()
+    torch.cuda.synchronize()
+    ms_step = ev0.elapsed_time(ev1) / args.steps
+    value = step_bytes / (ms_step * 1e-3) / 1e9
+    print(f"[bench] step {ms_step:.3f} ms  {value:.1f} GB/s  graph_ok={graph_ok}", file=sys.stderr, flush=True)
+
+    # ---- roofline leg: per-launch timing of the 4096 x 14336 down GEMV ----
+    def timed_launches(launch, n):
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(n + 1)]
+        torch.cuda._sleep(int(2e7))  # keep the stream busy while the launches are queued
+        for i in range(n):
+            evs[i].record()
+            launch(i)
+        evs[n].record()
+        torch.cuda.synchronize()
+        per = [evs[i].elapsed_time(evs[i + 1]) for i in range(n)]
+        return per, evs[0].elapsed_time(evs[n]) / n
+
+    down_bytes = gemv_bytes(rbf, HIDDEN, FFN)
+    per, _ = timed_launches(lambda i: zq.gemv_dev(Q8, layers[i % LAYERS]["down"], x_f, y_d, HIDDEN, FFN), 4 * LAYERS)
+    down_ms = statistics.mean(per[LAYERS:])  # drop the first rotation
+    down_gbs = down_bytes / (down_ms * 1e-3) / 1e9
+
+    # per-shape GB/s (informational), same method
+    per_shape = {}
+    for name, key, rows, cols, x in (("q/o 4096x4096", "q", HIDDEN, HIDDEN, x_h), ("k/v 1024x4096", "k", KV, HIDDEN, x_h),
+                                     ("gate/up 14336x4096", "gate", FFN, HIDDEN, x_h),
+                                     ("down 4096x14336", "down", HIDDEN, FFN, x_f)):
+        yb = torch.empty(rows, device=dev)
+        p, _ = timed_launches(lambda i: zq.gemv_dev(Q8, layers[i % LAYERS][key], x, yb, rows, cols), 2 * LAYERS)
+        ms = statistics.mean(p[LAYERS:])
+        per_shape[name] = {"us": round(ms * 1e3, 2),
+                           "GB/s": round(gemv_bytes(zq.row_bytes(Q8, cols), rows, cols) / (ms * 1e-3) / 1e9, 1)}
+    p, _ = timed_launches(lambda i: zq.gemv_dev(Q8, lm_head, x_h, y_lm, VOCAB, HIDDEN), 8)
+    ms = statistics.mean(p[1:])
+    per_shape["lm_head 128256x4096"] = {"us": round(ms * 1e3, 2),
+                                        "GB/s": round(gemv_bytes(rbh, VOCAB, HIDDEN) / (ms * 1e-3) / 1e9, 1)}
+
+    # ---- secondary: int8 prefill GEMM at M = 2048 --------------------------
+    M = 2048
+    gemm = {}
+    X = torch.empty(M * FFN, device=dev)
+    zq.synth_normal_dev(21, X, M * FFN)
+    for name, key, N, K in (("gate/up 14336x4096", "gate", FFN, HIDDEN), ("down 4096x14336", "down", HIDDEN, FFN)):
+        wsb = zq.gemm_workspace_bytes(Q8, M, K, zq.ACT_INT8)
+        ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+        Y = torch.empty(M * N, device=dev)
+        xq = ws[: M * K]
+        xs = ws[((M * K + 255) // 256) * 256:].view(torch.float32)
+        Xk = X[: M * K]
+        zq.quantize_acts_dev(Xk, xq, xs, M, K)
+        # GEMM kernel alone (activations already quantised), rotating over 8 layers
+        from zeninfer_amd.zq import lib as _lib
+        L = _lib()
+        sptr = torch.cuda.current_stream().cuda_stream
+
+        def launch(i, key=key, N=N, K=K, Y=Y):
+            st = L.zq_hip_gemm_dev  # noqa: F841 (kept for symmetry)
+            zq.gemm_dev(Q8, layers[i % 8][key], Xk, Y, M, N, K, zq.ACT_INT8, ws, wsb, sptr)
+
+        # full call (quantise + GEMM) per launch
+        per_full, _ = timed_launches(launch, 24)
+        full_ms = statistics.mean(per_full[8:])
+        ops = 2.0 * M * N * K
+        gemm[name] = {"ms_incl_quantize": round(full_ms, 4),
+                      "TOPS_incl_quantize": round(ops / (full_ms * 1e-3) / 1e12, 1)}
+    # the int8 GEMM kernel alone, via rocprof-comparable per-launch events:
+    # quantise once, then time launch_gemm via the block of GEMM-only calls
+    gemm_kernel = {}
+    for name, key, N, K in (("gate/up 14336x4096", "gate", FFN, HIDDEN),):
+        ops = 2.0 * M * N * K
+        # full-call time minus the quantiser's own time, measured alone
+        qx = torch.empty(M * K, dtype=torch.int8, device=dev)
+        qs = torch.empty(M * K // 32, device=dev)
+        pq, _ = timed_launches(lambda i: zq.quantize_acts_dev(X[: M * K], qx, qs, M, K), 16)
+        q_ms = statistics.mean(pq[4:])
+        k_ms = gemm[name]["ms_incl_quantize"] - q_ms
+        gemm_kernel = {"shape": f"M={M} N={N} K={K}", "gemm_ms": round(k_ms, 4), "quantize_ms": round(q_ms, 4),
+                       "TOPS": round(ops / (k_ms * 1e-3) / 1e12, 1),
+                       "frac_int8_peak": round(ops / (k_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4)}
+
+    cpu = None
+    if not args.no_cpu:
+        try:
+            cpu = cpu_baseline()
+        except Exception as e:  # reported, never fatal to the GPU measurement
+            cpu = {"error": str(e)}
+
+    out = {
+        "metric": "Q8_0 decode GEMV GB/s (% HBM peak); prefill GEMM int8 TOPS (% MFMA peak)",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded SplitMix64/Box-Muller Q8_0 weights generated on the device, N(0,1) fp32 activations)",
+        "config": {"workload": "config 1: Llama-3-8B-shaped Q8_0 decode projections, batch 1, one token = "
+                               "32 layers x (QKV batch, o, gate|up batch, down) + lm_head, HIP-graph replay",
+                   "weights_bytes_per_step": int(step_bytes), "launches_per_step": LAYERS * 4 + 1,
+                   "frac_hbm_peak_step": round(value / HBM_PEAK_GBS, 4), "graph_matches_eager": graph_ok},
+        "roofline": {"bound": "hbm", "achieved": round(down_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(down_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "gemv_pairs_kernel<Q8_0> at 4096x14336 (down projection)",
+                     "avg_launch_us": round(down_ms * 1e3, 2), "algorithmic_bytes_per_launch": down_bytes},
+        "per_shape_gemv": per_shape,
+        "secondary": {"prefill_gemm_int8_M2048": gemm, "gemm_kernel": gemm_kernel,
+                      "int8_peak_tops": INT8_PEAK_TOPS},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,176 @@
+/*
+ * zq_hip.h -- C ABI of the MI355X (gfx950) block-quantised projection
+ * backend: Q8_0 / Q4_0 / Q6_K decode GEMV and quantised prefill GEMM over
+ * GGML blocks kept resident in HBM in their native layout.
+ *
+ * This header contains no HIP or C++ types: plain pointers, sizes and int
+ * status codes, so the reference's compiler-agnostic dispatch layer
+ * (src/quant.cpp) can call it from any translation unit, the same way it
+ * reaches the backend declared in include/zen/hip_backend.h:6-14.
+ *
+ * Citations are to the ZenInfer reference tree (file:line) whose interface
+ * each entry point replaces.  Conventions carried over from that slot:
+ *   - nothing throws across this boundary; every call returns a status;
+ *   - ZQ_DECLINED means "not taken, run your CPU route", exactly where the
+ *     reference's zen::hip::* returned false and quant.cpp fell through
+ *     (src/quant.cpp:1007-1012, 1656-1659);
+ *   - host-pointer entry points are synchronous and key device residency by
+ *     the weight pointer plus (format, rows, cols) (hip_backend.h:52-58): a
+ *     tensor must keep its host address and bytes for as long as it is used;
+ *     a reused address with a different shape is re-uploaded, with the same
+ *     shape it is NOT re-read (call zq_hip_release first);
+ *   - one process-wide mutex serialises the host-pointer entry points
+ *     (src/backends/hip/hip_backend.hip:232-233); initialisation is lazy,
+ *     cached and failure-latched until zq_hip_shutdown (:392-436).
+ * The *_dev entry points take device pointers and a hipStream_t (as void*,
+ * NULL = the null stream), only enqueue work and never synchronise.
+ */
+#ifndef ZQ_HIP_H
+#define ZQ_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+#define ZQ_OK 0
+#define ZQ_DECLINED 1          /* valid call the backend does not take: use the CPU route */
+#define ZQ_ERR_ARG (-1)        /* invalid arguments (null pointer, bad shape/format)       */
+#define ZQ_ERR_NO_DEVICE (-2)  /* no usable gfx950 device / init failed                    */
+#define ZQ_ERR_OOM (-3)        /* device or host allocation failed                         */
+#define ZQ_ERR_HIP (-4)        /* a HIP runtime call or kernel launch failed               */
+
+/* ---- weight formats: GGML type ids (src/gguf.cpp:370-393) ---------------- */
+#define ZQ_FMT_Q4_0 2   /* 32 el / 18 B: fp16 d + 16 B nibbles   (src/quant.cpp:253)  */
+#define ZQ_FMT_Q8_0 8   /* 32 el / 34 B: fp16 d + 32 int8        (src/quant.cpp:257)  */
+#define ZQ_FMT_Q6_K 14  /* 256 el / 210 B super-block            (src/quant.cpp:259)  */
+
+/* ---- GEMM activation handling -------------------------------------------- */
+#define ZQ_ACT_DEFAULT 0 /* Q8_0/Q4_0: int8 (the D3D12 default q8_0_gemm_i8 route,
+                            src/backends/d3d12/d3d12_backend.cpp:845-854); Q6_K: fp32 */
+#define ZQ_ACT_INT8 1    /* per-32 int8 activations, kernels/avx2.cpp:502-524 quantiser */
+#define ZQ_ACT_F32 2     /* fp32 activations, the reference CPU GEMM arithmetic          */
+
+/* Bytes of slack every device weight buffer must carry past its last block
+ * (the library's own uploads always do; see zq_weight_bytes). */
+#define ZQ_WEIGHT_TAIL_PAD 64
+
+/* Adapter description.  Replaces zen::hip::AdapterInfo (include/zen/hip_backend.h:17-24). */
+typedef struct zq_hip_info {
+    char name[128];
+    char arch[64];           /* gcnArchName, e.g. gfx950:sramecc+:xnack- */
+    uint64_t vram_bytes;
+    int compute_units;
+    int wave_size;
+    int lds_per_block;
+    int clock_khz;
+    int mem_clock_khz;
+    int mem_bus_width;
+} zq_hip_info;
+
+/* Counters.  Replaces zen::hip::Stats (include/zen/hip_backend.h:25-41). */
+typedef struct zq_hip_stats {
+    uint64_t dispatches;      /* kernels launched                        */
+    uint64_t submits;         /* host-pointer calls that ran on the GPU  */
+    uint64_t batches;         /* batched GEMV submissions                */
+    uint64_t uploads;         /* weight tensors uploaded                 */
+    uint64_t upload_bytes;
+    uint64_t resident_bytes;  /* currently resident weight bytes         */
+    uint64_t resident_tensors;
+    uint64_t evictions;
+    uint64_t declined;        /* calls answered ZQ_DECLINED              */
+    uint64_t errors;
+    uint64_t upload_us;
+    uint64_t transfer_us;     /* activation H2D + output D2H, host clock */
+    uint64_t wait_us;         /* stream synchronisation                  */
+} zq_hip_stats;
+
+/* One projection of a batched GEMV.  Replaces zen::hip::GemvTask
+ * (include/zen/hip_backend.h:62-71); all tasks share x and cols. */
+typedef struct zq_gemv_task {
+    const uint8_t* weights;  /* host pointer (zq_hip_gemv_batch) or device pointer (_dev) */
+    float* y;
+    size_t rows;
+} zq_gemv_task;
+#define ZQ_MAX_BATCH 8       /* zen::hip::kMaxBatch (include/zen/hip_backend.h:72) */
+
+/* ---- lifecycle (include/zen/hip_backend.h:46-50) -------------------------- */
+/* 1 when ZEN_BACKEND is hip|rocm|amd or ZEN_HIP=1 (hip_backend.hip:266-282). */
+int zq_hip_opted_in(void);
+/* Lazy, cached, failure-latched init of device 0 (zen::hip::init). */
+int zq_hip_init(void);
+/* 1 when opted in and a usable device initialised (zen::hip::enabled). */
+int zq_hip_enabled(void);
+/* Frees residency and staging, clears the failure latch (zen::hip::shutdown). */
+void zq_hip_shutdown(void);
+int zq_hip_get_info(zq_hip_info* out);          /* zen::hip::info  */
+int zq_hip_get_stats(zq_hip_stats* out);        /* zen::hip::stats */
+void zq_hip_reset_stats(void);
+const char* zq_hip_status_string(int status);
+
+/* ---- layout helpers (src/quant.cpp:894-943) ------------------------------- */
+size_t zq_row_bytes(int fmt, size_t cols);                 /* 0 if cols is not block-aligned */
+size_t zq_weight_bytes(int fmt, size_t rows, size_t cols); /* rows*row_bytes + ZQ_WEIGHT_TAIL_PAD */
+/* Host-pointer calls with rows*cols below this many elements are declined so
+ * the CPU keeps tiny projections (hip_backend.hip:49, 939); default 262144,
+ * env ZEN_HIP_MIN_ELEMENTS.  Returns the previous value. */
+size_t zq_hip_set_min_elements(size_t elements);
+
+/* ---- host-pointer projections (synchronous) ------------------------------ */
+/* y[rows] = W[rows x cols] . x[cols], fp32 activations.
+ * Replaces zen::hip::gemv_q8_0 (include/zen/hip_backend.h:59-60), called from
+ * quant::gemv (src/quant.cpp:1007-1012), for Q8_0, Q4_0 and Q6_K. */
+int zq_hip_gemv(int fmt, const uint8_t* weights, const float* x, float* y, size_t rows, size_t cols);
+/* Several projections sharing x, one submission.  Replaces
+ * zen::hip::gemv_q8_0_batch (include/zen/hip_backend.h:74), called from
+ * quant::gemv_batch (src/quant.cpp:1457-1467). */
+int zq_hip_gemv_batch(int fmt, const float* x, const zq_gemv_task* tasks, size_t count, size_t cols);
+/* Y[tokens x rows] = X[tokens x cols] . W^T, token-major.  Replaces
+ * zen::hip::gemm_q8_0 (include/zen/hip_backend.h:61-62), called from
+ * quant::gemm (src/quant.cpp:1656-1659). */
+int zq_hip_gemm(int fmt, const uint8_t* weights, const float* X, float* Y, size_t tokens, size_t rows,
+                size_t cols, int act_mode);
+/* gate|up -> SiLU(gate)*up -> down with the FFN activation kept on the
+ * device.  Replaces zen::hip::gemv_q8_0_ffn (include/zen/hip_backend.h:80-82),
+ * called from quant::ffn_gemv (src/quant.cpp:1566-1571). */
+int zq_hip_ffn_gemv(int fmt, const uint8_t* gate, const uint8_t* up, const uint8_t* down, const float* x,
+                    float* y, size_t ffn_rows, size_t cols, size_t out_rows);
+/* Drops the device copy of one weight tensor (the D3D12 slot's
+ * release_q8_0_weights, include/zen/d3d12_backend.h:87-91). */
+int zq_hip_release(const uint8_t* weights);
+int zq_hip_release_all(void);
+
+/* ---- device-pointer projections (asynchronous on `stream`) --------------- */
+/* Weight buffers must be readable ZQ_WEIGHT_TAIL_PAD bytes past the last block. */
+int zq_hip_gemv_dev(int fmt, const void* weights, const float* x, float* y, size_t rows, size_t cols,
+                    void* stream);
+int zq_hip_gemv_batch_dev(int fmt, const float* x, const zq_gemv_task* tasks, size_t count, size_t cols,
+                          void* stream);
+/* Workspace (device bytes) a zq_hip_gemm_dev call needs: int8 activations and
+ * their scales for ZQ_ACT_INT8, 0 for ZQ_ACT_F32. */
+size_t zq_hip_gemm_workspace_bytes(int fmt, size_t tokens, size_t cols, int act_mode);
+int zq_hip_gemm_dev(int fmt, const void* weights, const float* X, float* Y, size_t tokens, size_t rows,
+                    size_t cols, int act_mode, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- bit-exact tier hooks (device pointers, asynchronous) ---------------- */
+/* Per-32 activation quantiser, kernels/avx2.cpp:502-524: xq[tokens*cols],
+ * xs[tokens*cols/32]. */
+int zq_hip_quantize_acts_dev(const float* X, int8_t* xq, float* xs, size_t tokens, size_t cols, void* stream);
+/* Per-block int32 dots of the int8 GEMM, taken from its MFMA results:
+ * out[(t*rows + r)*(cols/32) + b].  Q8_0 and Q4_0. */
+int zq_hip_block_dots_dev(int fmt, const void* weights, const int8_t* xq, int32_t* out, size_t tokens,
+                          size_t rows, size_t cols, void* stream);
+/* Dequantised weights, row-major fp32 (src/quant.cpp:391-416, 500-517). */
+int zq_hip_dequantize_dev(int fmt, const void* weights, float* out, size_t rows, size_t cols, void* stream);
+
+/* ---- synthetic inputs on the device (bench workloads) -------------------- */
+int zq_hip_synth_weights_dev(int fmt, uint64_t seed, void* weights, size_t rows, size_t cols, void* stream);
+int zq_hip_synth_normal_dev(uint64_t seed, float* out, size_t n, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ZQ_HIP_H */

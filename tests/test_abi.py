@@ -1,0 +1,71 @@
+"""CPU tier: the C-ABI library loads and exports every symbol include/zq_hip.h
+declares (no compute calls without a GPU), and host-side argument checks
+answer without touching a device."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "zq_hip.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(zq_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_entry_points():
+    syms = declared_symbols()
+    for s in ("zq_hip_gemv", "zq_hip_gemm", "zq_hip_gemv_batch", "zq_hip_init", "zq_hip_release",
+              "zq_hip_gemv_dev", "zq_hip_gemm_dev", "zq_hip_block_dots_dev", "zq_hip_dequantize_dev"):
+        assert s in syms
+
+
+def test_library_exports_every_declared_symbol():
+    from zeninfer_amd import zq
+    lib = zq.lib()
+    missing = [s for s in declared_symbols() if not hasattr(lib, s)]
+    assert not missing, missing
+    assert set(declared_symbols()) == set(zq.SIGNATURES), "Python binding out of sync with the header"
+
+
+def test_layout_helpers_without_device():
+    from zeninfer_amd import zq
+    assert zq.row_bytes(zq.Q8_0, 4096) == 4352
+    assert zq.row_bytes(zq.Q8_0, 14336) == 15232
+    assert zq.row_bytes(zq.Q4_0, 4096) == 2304
+    assert zq.row_bytes(zq.Q6_K, 4096) == 3360
+    assert zq.row_bytes(zq.Q6_K, 4000) == 0 and zq.row_bytes(zq.Q8_0, 100) == 0 and zq.row_bytes(99, 4096) == 0
+    assert zq.weight_bytes(zq.Q8_0, 2, 64) == 2 * 68 + zq.WEIGHT_TAIL_PAD
+
+
+def test_argument_errors_without_device():
+    from zeninfer_amd import zq
+    L = zq.lib()
+    # null pointers / bad shapes are rejected before any device work
+    assert L.zq_hip_gemv(zq.Q8_0, None, None, None, 4, 64) == -1
+    assert L.zq_hip_gemm(zq.Q8_0, None, None, None, 1, 4, 64, 0) == -1
+    assert L.zq_hip_gemv_dev(zq.Q8_0, 0, 0, 0, 4, 100, None) == -1
+    assert zq.status_string(1) == "declined"
+    assert L.zq_hip_gemm_workspace_bytes(zq.Q8_0, 4, 4096, zq.ACT_INT8) == 4 * 4096 + 4 * 128 * 4
+    assert L.zq_hip_gemm_workspace_bytes(zq.Q8_0, 4, 4096, zq.ACT_F32) == 0
+    assert L.zq_hip_gemm_workspace_bytes(zq.Q6_K, 4, 4096, zq.ACT_DEFAULT) == 0
+
+
+def test_opt_in_semantics(monkeypatch):
+    # ZEN_BACKEND=hip|rocm|amd or ZEN_HIP=1 (src/backends/hip/hip_backend.hip:266-282)
+    from zeninfer_amd import zq
+    L = zq.lib()
+    for k in ("ZEN_BACKEND", "ZEN_HIP"):
+        monkeypatch.delenv(k, raising=False)
+    assert L.zq_hip_opted_in() == 0
+    for v in ("hip", "rocm", "amd"):
+        monkeypatch.setenv("ZEN_BACKEND", v)
+        assert L.zq_hip_opted_in() == 1
+    monkeypatch.setenv("ZEN_BACKEND", "cpu")
+    assert L.zq_hip_opted_in() == 0
+    monkeypatch.setenv("ZEN_HIP", "1")
+    assert L.zq_hip_opted_in() == 1

@@ -1,0 +1,279 @@
+"""GPU tier: the HIP path against the pinned C oracle, through the C ABI.
+
+Bit-exact: dequantised weights, int8 activations + scales, per-block integer
+dots (read from the GEMM's own MFMA results).  Tolerance (|g-c| <= 1e-4 +
+1e-5*|c|): fp32 GEMV/GEMM outputs against the oracle's restatement of the
+reference CPU kernels on the same seeded inputs.  Full BASELINE sizes are
+checked on sampled rows / tokens (rows and tokens are independent, so a
+sampled row must equal the oracle's value for that row).
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tests.tolerance import assert_close
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+DEV = "cuda:0"
+
+
+def to_dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def dev_weights(zq, fmt, w_np, rows, cols):
+    """Device buffer with the library's tail padding (zq_weight_bytes)."""
+    buf = torch.zeros(zq.weight_bytes(fmt, rows, cols), dtype=torch.uint8, device=DEV)
+    buf[: w_np.size] = to_dev(w_np)
+    return buf
+
+
+@pytest.fixture(autouse=True)
+def _small_shapes_allowed(zq):
+    prev = zq.set_min_elements(0)
+    yield
+    zq.set_min_elements(prev)
+
+
+# ------------------------------------------------------------- bit-exact ---
+@pytest.mark.parametrize("fmt,rows,cols", [(O.Q8_0, 37, 256), (O.Q8_0, 3, 96), (O.Q4_0, 37, 256),
+                                           (O.Q4_0, 5, 160), (O.Q6_K, 9, 768), (O.Q6_K, 3, 256)])
+def test_dequantize_bit_exact(zq, orc, fmt, rows, cols):
+    w = orc.gen_weights(fmt, 100 + rows, rows, cols)
+    # force binary16 subnormal and special scales into a few blocks
+    bb = O.BLOCK[fmt][1]
+    soff = 208 if fmt == O.Q6_K else 0
+    for i, h in enumerate((0x0001, 0x03FF, 0x8400, 0x0000)):
+        w[i * bb + soff], w[i * bb + soff + 1] = h & 0xFF, h >> 8
+    out = torch.empty(rows * cols, dtype=torch.float32, device=DEV)
+    zq.dequantize_dev(fmt, dev_weights(zq, fmt, w, rows, cols), out, rows, cols)
+    got = out.cpu().numpy()
+    want = orc.dequantize(fmt, w, rows * cols)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_quantize_acts_bit_exact(zq, orc):
+    m, k = 37, 4096
+    x = orc.gen_normal(7, m * k)
+    x[:32] = [127, 2.5, -2.5, 0.5, -0.5, 1.5, -1.5, 126.5] + [0.0] * 24   # exact ties
+    x[32:64] = 0.0                                                          # amax == 0
+    x[64:96] = np.float32(1e-30)
+    xd = to_dev(x)
+    xq = torch.empty(m * k, dtype=torch.int8, device=DEV)
+    xs = torch.empty(m * k // 32, dtype=torch.float32, device=DEV)
+    zq.quantize_acts_dev(xd, xq, xs, m, k)
+    q_ref, s_ref = orc.quantize_acts(x, m, k)
+    assert np.array_equal(xq.cpu().numpy(), q_ref)
+    assert np.array_equal(xs.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("fmt,m,n,k", [(O.Q8_0, 5, 37, 256), (O.Q8_0, 130, 131, 192), (O.Q8_0, 1, 128, 4096),
+                                       (O.Q4_0, 7, 70, 320), (O.Q4_0, 129, 3, 128)])
+def test_block_dots_bit_exact(zq, orc, fmt, m, n, k):
+    w = orc.gen_weights(fmt, 3 + n, n, k)
+    x = orc.gen_normal(4 + m, m * k)
+    xq_np, _ = orc.quantize_acts(x, m, k)
+    out = torch.empty(m * n * (k // 32), dtype=torch.int32, device=DEV)
+    zq.block_dots_dev(fmt, dev_weights(zq, fmt, w, n, k), to_dev(xq_np), out, m, n, k)
+    assert np.array_equal(out.cpu().numpy(), orc.block_dots(fmt, w, xq_np, m, n, k))
+
+
+def test_block_dots_extremes(zq, orc):
+    # |q| = 127 everywhere with saturated activations: largest block sums
+    m, n, k = 2, 4, 128
+    w = orc.gen_weights(O.Q8_0, 1, n, k).reshape(n, k // 32, 34)
+    w[:, :, 2:] = np.array([127, -127, -128, 127] * 8, np.int8).view(np.uint8)
+    w = w.reshape(-1)
+    xq = np.tile(np.array([127, -127], np.int8), m * k // 2)
+    out = torch.empty(m * n * (k // 32), dtype=torch.int32, device=DEV)
+    zq.block_dots_dev(O.Q8_0, dev_weights(zq, O.Q8_0, w, n, k), to_dev(xq), out, m, n, k)
+    assert np.array_equal(out.cpu().numpy(), orc.block_dots(O.Q8_0, w, xq, m, n, k))
+
+
+# ----------------------------------------------------------------- GEMV ---
+GEMV_SHAPES = [
+    (O.Q8_0, 4096, 4096),   # config 0
+    (O.Q8_0, 1024, 4096),   # k / v
+    (O.Q8_0, 4097, 4096),   # ragged rows
+    (O.Q8_0, 1, 64),        # smallest pair shape
+    (O.Q8_0, 33, 96),       # odd block count -> block-lane kernel
+    (O.Q8_0, 5, 14336),     # down-projection width
+    (O.Q4_0, 1000, 4096), (O.Q4_0, 7, 14336), (O.Q4_0, 9, 160),
+    (O.Q6_K, 1000, 4096), (O.Q6_K, 7, 14336), (O.Q6_K, 3, 256),
+]
+
+
+@pytest.mark.parametrize("fmt,rows,cols", GEMV_SHAPES)
+def test_gemv_host_api(zq, orc, fmt, rows, cols):
+    w = orc.gen_weights(fmt, 1000 + rows, rows, cols)
+    x = orc.gen_normal(2000 + cols, cols)
+    got = zq.gemv(fmt, w, x, rows, cols)
+    assert_close(got, orc.gemv_f32(fmt, w, x, rows, cols), f"gemv fmt={fmt} {rows}x{cols}")
+    zq.release(w)
+
+
+@pytest.mark.parametrize("rpw", ["1", "2", "4"])
+def test_gemv_rows_per_wave_variants(zq, orc, rpw):
+    # every row-grouping instantiation is reachable through the device API
+    import subprocess, sys, os
+    code = f"""
+import sys, numpy as np, torch
+sys.path.insert(0, {os.getcwd()!r})
+from oracle import oracle as O
+from zeninfer_amd import zq
+from tests.tolerance import assert_close
+o = O.Oracle(); zq.init()
+for fmt, rows, cols in ((O.Q8_0, 4099, 4096), (O.Q4_0, 515, 1024), (O.Q6_K, 515, 1024)):
+    w = o.gen_weights(fmt, 5, rows, cols); x = o.gen_normal(6, cols)
+    wd = torch.zeros(zq.weight_bytes(fmt, rows, cols), dtype=torch.uint8, device='cuda:0'); wd[:w.size] = torch.from_numpy(w).cuda()
+    y = torch.empty(rows, device='cuda:0')
+    zq.gemv_dev(fmt, wd, torch.from_numpy(x).cuda(), y, rows, cols); torch.cuda.synchronize()
+    assert_close(y.cpu().numpy(), o.gemv_f32(fmt, w, x, rows, cols), 'rpw')
+print('ok')
+"""
+    env = dict(os.environ, ZQ_GEMV_ROWS_PER_WAVE=rpw)
+    r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0 and "ok" in r.stdout, r.stdout + r.stderr
+
+
+def test_gemv_batch_qkv(zq, orc):
+    cols = 4096
+    rows = [4096, 1024, 1024]
+    ws = [orc.gen_weights(O.Q8_0, 50 + i, r, cols) for i, r in enumerate(rows)]
+    x = orc.gen_normal(51, cols)
+    ys = zq.gemv_batch(O.Q8_0, ws, x, rows, cols)
+    for w, y, r in zip(ws, ys, rows):
+        assert_close(y, orc.gemv_f32(O.Q8_0, w, x, r, cols), "gemv_batch")
+    before = zq.stats()["batches"]
+    zq.gemv_batch(O.Q8_0, ws, x, rows, cols)
+    assert zq.stats()["batches"] == before + 1
+
+
+def test_gemv_full_size_sampled_rows(zq, orc):
+    # config 1 gate/up (14336 x 4096) and down (4096 x 14336) at full size,
+    # weights generated on the device; sampled rows checked against the oracle
+    for rows, cols, seed in ((14336, 4096, 71), (4096, 14336, 72)):
+        wd = torch.zeros(zq.weight_bytes(O.Q8_0, rows, cols), dtype=torch.uint8, device=DEV)
+        zq.synth_weights_dev(O.Q8_0, seed, wd, rows, cols)
+        x = orc.gen_normal(seed, cols)
+        y = torch.empty(rows, device=DEV)
+        zq.gemv_dev(O.Q8_0, wd, to_dev(x), y, rows, cols)
+        w_all = wd[: rows * zq.row_bytes(O.Q8_0, cols)].cpu().numpy()
+        rb = zq.row_bytes(O.Q8_0, cols)
+        pick = np.sort(np.random.default_rng(seed).choice(rows, 48, replace=False))
+        sub = np.concatenate([w_all[r * rb:(r + 1) * rb] for r in pick])
+        assert_close(y.cpu().numpy()[pick], orc.gemv_f32(O.Q8_0, sub, x, len(pick), cols), "full-size gemv")
+
+
+def test_device_synth_matches_host_generator(zq, orc):
+    for fmt, rows, cols in ((O.Q8_0, 64, 4096), (O.Q4_0, 64, 4096), (O.Q6_K, 16, 4096)):
+        wd = torch.zeros(zq.weight_bytes(fmt, rows, cols), dtype=torch.uint8, device=DEV)
+        zq.synth_weights_dev(fmt, 99, wd, rows, cols)
+        got = wd[: rows * zq.row_bytes(fmt, cols)].cpu().numpy()
+        want = orc.gen_weights(fmt, 99, rows, cols)
+        # scales go through double log/cos on two different math libraries:
+        # allow a rare last-ulp difference in a scale, never in quant bytes
+        diff = np.nonzero(got != want)[0]
+        assert diff.size <= max(2, got.size // 100000), diff[:10]
+
+
+# ----------------------------------------------------------------- GEMM ---
+@pytest.mark.parametrize("fmt,m,n,k", [(O.Q8_0, 3, 300, 4096), (O.Q8_0, 130, 257, 1024), (O.Q8_0, 32, 128, 14336),
+                                       (O.Q8_0, 2, 64, 192), (O.Q4_0, 17, 200, 4096), (O.Q4_0, 129, 130, 256)])
+def test_gemm_int8(zq, orc, fmt, m, n, k):
+    w = orc.gen_weights(fmt, 300 + n, n, k)
+    X = orc.gen_normal(301 + m, m * k)
+    got = zq.gemm(fmt, w, X, m, n, k, zq.ACT_INT8)
+    assert_close(got, orc.gemm_i8(fmt, w, X, m, n, k), f"gemm_i8 fmt={fmt} {m}x{n}x{k}")
+    zq.release(w)
+
+
+@pytest.mark.parametrize("fmt,m,n,k", [(O.Q8_0, 5, 300, 4096), (O.Q8_0, 130, 129, 1024), (O.Q4_0, 9, 150, 4096),
+                                       (O.Q6_K, 17, 200, 4096), (O.Q6_K, 129, 33, 512), (O.Q8_0, 3, 40, 96)])
+def test_gemm_f32(zq, orc, fmt, m, n, k):
+    w = orc.gen_weights(fmt, 400 + n, n, k)
+    X = orc.gen_normal(401 + m, m * k)
+    got = zq.gemm(fmt, w, X, m, n, k, zq.ACT_F32)
+    assert_close(got, orc.gemm_f32(fmt, w, X, m, n, k), f"gemm_f32 fmt={fmt} {m}x{n}x{k}")
+    zq.release(w)
+
+
+def test_gemm_full_size_sampled(zq, orc):
+    # config 2 at M = 2048, N x K = 14336 x 4096, int8 activations, device path
+    m, n, k = 2048, 14336, 4096
+    wd = torch.zeros(zq.weight_bytes(O.Q8_0, n, k), dtype=torch.uint8, device=DEV)
+    zq.synth_weights_dev(O.Q8_0, 81, wd, n, k)
+    X = orc.gen_normal(82, m * k)
+    Y = torch.empty(m * n, device=DEV)
+    ws_bytes = zq.gemm_workspace_bytes(O.Q8_0, m, k, zq.ACT_INT8)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=DEV)
+    zq.gemm_dev(O.Q8_0, wd, to_dev(X), Y, m, n, k, zq.ACT_INT8, ws, ws_bytes)
+    Yh = Y.cpu().numpy().reshape(m, n)
+    rb = zq.row_bytes(O.Q8_0, k)
+    rng = np.random.default_rng(83)
+    rows = np.sort(rng.choice(n, 24, replace=False))
+    toks = np.sort(rng.choice(m, 6, replace=False))
+    w_all = wd[: n * rb].cpu().numpy()
+    sub = np.concatenate([w_all[r * rb:(r + 1) * rb] for r in rows])
+    Xs = X.reshape(m, k)[toks].reshape(-1)
+    want = orc.gemm_i8(O.Q8_0, sub, Xs, len(toks), len(rows), k).reshape(len(toks), len(rows))
+    assert_close(Yh[np.ix_(toks, rows)].reshape(-1), want.reshape(-1), "full-size gemm_i8")
+
+
+def test_gemm_declines_unsupported(zq, orc):
+    w = orc.gen_weights(O.Q6_K, 1, 8, 256)
+    X = orc.gen_normal(2, 3 * 256)
+    with pytest.raises(zq.ZQError) as e:
+        zq.gemm(O.Q6_K, w, X, 3, 8, 256, zq.ACT_INT8)
+    assert e.value.status == zq.DECLINED
+
+
+# ----------------------------------------------------- host-API contract ---
+def test_residency_and_release(zq, orc):
+    zq.release_all()
+    zq.reset_stats()
+    w = orc.gen_weights(O.Q8_0, 5, 256, 1024)
+    x = orc.gen_normal(6, 1024)
+    y1 = zq.gemv(O.Q8_0, w, x, 256, 1024)
+    y2 = zq.gemv(O.Q8_0, w, x, 256, 1024)
+    s = zq.stats()
+    assert s["uploads"] == 1 and s["submits"] == 2 and s["resident_tensors"] == 1
+    assert np.array_equal(y1, y2)
+    # same address, same shape: not re-read (the documented contract) until released
+    w[:34] = 0
+    y3 = zq.gemv(O.Q8_0, w, x, 256, 1024)
+    assert np.array_equal(y3, y1)
+    assert zq.release(w) == 0
+    y4 = zq.gemv(O.Q8_0, w, x, 256, 1024)
+    assert y4[0] == 0.0 and zq.stats()["uploads"] == 2
+    # same address, different shape: re-uploaded
+    y5 = zq.gemv(O.Q8_0, w, x[:512], 512, 512)
+    assert zq.stats()["uploads"] == 3
+    assert_close(y5, orc.gemv_f32(O.Q8_0, w, x[:512], 512, 512), "reshaped")
+    zq.release_all()
+    assert zq.stats()["resident_tensors"] == 0
+
+
+def test_small_shapes_declined_by_default(zq, orc):
+    zq.set_min_elements(262144)
+    w = orc.gen_weights(O.Q8_0, 5, 16, 256)
+    with pytest.raises(zq.ZQError) as e:
+        zq.gemv(O.Q8_0, w, orc.gen_normal(1, 256), 16, 256)
+    assert e.value.status == zq.DECLINED
+
+
+def test_ffn_gemv(zq, orc):
+    cols, ffn, out = 1024, 2816, 1024
+    g = orc.gen_weights(O.Q8_0, 61, ffn, cols)
+    u = orc.gen_weights(O.Q8_0, 62, ffn, cols)
+    d = orc.gen_weights(O.Q8_0, 63, out, ffn)
+    x = orc.gen_normal(64, cols)
+    y = zq.ffn_gemv(O.Q8_0, g, u, d, x, ffn, cols, out)
+    gv = orc.gemv_f32(O.Q8_0, g, x, ffn, cols).astype(np.float64)
+    uv = orc.gemv_f32(O.Q8_0, u, x, ffn, cols).astype(np.float64)
+    act = (gv / (1 + np.exp(-gv)) * uv).astype(np.float32)
+    want = orc.gemv_f32(O.Q8_0, d, act, out, ffn)
+    # SiLU is a transcendental: compare at the GEMV bar scaled by the input size
+    assert np.max(np.abs(y - want) / (1e-3 + np.abs(want))) < 1e-3

@@ -1,0 +1,601 @@
+// zq_backend.hip -- the C-ABI runtime: device init, weight residency in HBM,
+// activation staging, stream handling and statistics.  Kernels live in
+// zq_gemv.hip, zq_gemm.hip and zq_misc.hip.
+//
+// Residency: a weight tensor is uploaded once, byte-for-byte in its GGML
+// block layout (no repack), into one hipMalloc allocation of
+// rows*row_bytes + ZQ_WEIGHT_TAIL_PAD bytes, and stays there until released,
+// evicted or shutdown.  The key is the host pointer; the entry also records
+// (format, rows, cols) and a different shape at the same address re-uploads
+// (reference contract, include/zen/hip_backend.h:52-58).  When the budget
+// (80% of device memory, as hip_backend.hip:459-475) would be exceeded,
+// every resident tensor is evicted first.
+#include <hip/hip_runtime.h>
+
+#include <chrono>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <new>
+#include <unordered_map>
+
+#include "../../include/zq_hip.h"
+#include "zq_internal.hpp"
+
+namespace {
+
+using Clock = std::chrono::steady_clock;
+uint64_t us_since(Clock::time_point t0) {
+    return static_cast<uint64_t>(std::chrono::duration_cast<std::chrono::microseconds>(Clock::now() - t0).count());
+}
+
+struct Resident {
+    int fmt;
+    size_t rows, cols, bytes;
+    uint8_t* dev;
+};
+
+struct Backend {
+    std::mutex mu;
+    bool initialised = false;
+    bool failed = false;
+    int device = 0;
+    zq_hip_info info{};
+    zq_hip_stats stats{};
+    hipStream_t stream = nullptr;
+    size_t budget = 0;
+    size_t min_elements = 262144;
+    std::unordered_map<const uint8_t*, Resident> resident;
+    // staging
+    void* dev_scratch = nullptr;  // activations in, outputs out, int8 workspace
+    size_t dev_scratch_bytes = 0;
+    void* host_pinned = nullptr;
+    size_t host_pinned_bytes = 0;
+};
+
+Backend& B() {
+    static Backend b;
+    return b;
+}
+
+int fail_hip(Backend& b) {
+    ++b.stats.errors;
+    return ZQ_ERR_HIP;
+}
+
+bool env_opted_in() {
+    const char* be = std::getenv("ZEN_BACKEND");
+    if (be && (!std::strcmp(be, "hip") || !std::strcmp(be, "rocm") || !std::strcmp(be, "amd"))) return true;
+    const char* h = std::getenv("ZEN_HIP");
+    return h && h[0] == '1';
+}
+
+int init_locked(Backend& b) {
+    if (b.initialised) return ZQ_OK;
+    if (b.failed) return ZQ_ERR_NO_DEVICE;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count < 1) {
+        b.failed = true;
+        return ZQ_ERR_NO_DEVICE;
+    }
+    const char* dv = std::getenv("ZEN_HIP_DEVICE");
+    b.device = dv ? std::atoi(dv) : 0;
+    if (b.device < 0 || b.device >= count || hipSetDevice(b.device) != hipSuccess) {
+        b.failed = true;
+        return ZQ_ERR_NO_DEVICE;
+    }
+    hipDeviceProp_t p{};
+    if (hipGetDeviceProperties(&p, b.device) != hipSuccess) {
+        b.failed = true;
+        return ZQ_ERR_NO_DEVICE;
+    }
+    if (std::strncmp(p.gcnArchName, "gfx950", 6) != 0) {  // code objects are built for gfx950 only
+        b.failed = true;
+        return ZQ_ERR_NO_DEVICE;
+    }
+    std::snprintf(b.info.name, sizeof(b.info.name), "%s", p.name);
+    std::snprintf(b.info.arch, sizeof(b.info.arch), "%s", p.gcnArchName);
+    b.info.vram_bytes = p.totalGlobalMem;
+    b.info.compute_units = p.multiProcessorCount;
+    b.info.wave_size = p.warpSize;
+    b.info.lds_per_block = static_cast<int>(p.sharedMemPerBlock);
+    b.info.clock_khz = p.clockRate;
+    b.info.mem_clock_khz = p.memoryClockRate;
+    b.info.mem_bus_width = p.memoryBusWidth;
+    if (hipStreamCreateWithFlags(&b.stream, hipStreamNonBlocking) != hipSuccess) {
+        b.failed = true;
+        return ZQ_ERR_NO_DEVICE;
+    }
+    b.budget = static_cast<size_t>(static_cast<double>(p.totalGlobalMem) * 0.8);
+    if (const char* me = std::getenv("ZEN_HIP_MIN_ELEMENTS")) b.min_elements = std::strtoull(me, nullptr, 10);
+    b.initialised = true;
+    return ZQ_OK;
+}
+
+void free_resident(Backend& b) {
+    for (auto& kv : b.resident) (void)hipFree(kv.second.dev);
+    b.stats.evictions += b.resident.size();
+    b.resident.clear();
+    b.stats.resident_bytes = 0;
+    b.stats.resident_tensors = 0;
+}
+
+// Device copy of a host weight tensor, uploading on first use.
+int ensure_resident(Backend& b, int fmt, const uint8_t* w, size_t rows, size_t cols, const uint8_t** out) {
+    auto it = b.resident.find(w);
+    if (it != b.resident.end()) {
+        if (it->second.fmt == fmt && it->second.rows == rows && it->second.cols == cols) {
+            *out = it->second.dev;
+            return ZQ_OK;
+        }
+        (void)hipFree(it->second.dev);
+        b.stats.resident_bytes -= it->second.bytes;
+        --b.stats.resident_tensors;
+        b.resident.erase(it);
+    }
+    const size_t payload = rows * zq::row_bytes(fmt, cols);
+    const size_t bytes = payload + ZQ_WEIGHT_TAIL_PAD;
+    if (bytes > b.budget) return ZQ_DECLINED;
+    if (b.stats.resident_bytes + bytes > b.budget) free_resident(b);
+    const auto t0 = Clock::now();
+    uint8_t* dev = nullptr;
+    if (hipMalloc(&dev, bytes) != hipSuccess) {
+        free_resident(b);
+        if (hipMalloc(&dev, bytes) != hipSuccess) return ZQ_ERR_OOM;
+    }
+    if (hipMemcpy(dev, w, payload, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemset(dev + payload, 0, ZQ_WEIGHT_TAIL_PAD) != hipSuccess) {
+        (void)hipFree(dev);
+        return fail_hip(b);
+    }
+    b.resident.emplace(w, Resident{fmt, rows, cols, bytes, dev});
+    b.stats.uploads++;
+    b.stats.upload_bytes += payload;
+    b.stats.resident_bytes += bytes;
+    b.stats.resident_tensors++;
+    b.stats.upload_us += us_since(t0);
+    *out = dev;
+    return ZQ_OK;
+}
+
+int ensure_scratch(Backend& b, size_t dev_bytes, size_t host_bytes) {
+    if (dev_bytes > b.dev_scratch_bytes) {
+        if (b.dev_scratch) (void)hipFree(b.dev_scratch);
+        b.dev_scratch = nullptr;
+        b.dev_scratch_bytes = 0;
+        if (hipMalloc(&b.dev_scratch, dev_bytes) != hipSuccess) return ZQ_ERR_OOM;
+        b.dev_scratch_bytes = dev_bytes;
+    }
+    if (host_bytes > b.host_pinned_bytes) {
+        if (b.host_pinned) (void)hipHostFree(b.host_pinned);
+        b.host_pinned = nullptr;
+        b.host_pinned_bytes = 0;
+        if (hipHostMalloc(&b.host_pinned, host_bytes, hipHostMallocDefault) != hipSuccess) return ZQ_ERR_OOM;
+        b.host_pinned_bytes = host_bytes;
+    }
+    return ZQ_OK;
+}
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+bool valid_fmt(int fmt) { return fmt == ZQ_FMT_Q4_0 || fmt == ZQ_FMT_Q8_0 || fmt == ZQ_FMT_Q6_K; }
+
+int resolve_act(int fmt, int act_mode) {
+    if (act_mode == ZQ_ACT_DEFAULT) return fmt == ZQ_FMT_Q6_K ? ZQ_ACT_F32 : ZQ_ACT_INT8;
+    return act_mode;
+}
+
+// GEMM support check shared by the host and device entry points.
+int gemm_supported(int fmt, size_t cols, int act) {
+    if (act != ZQ_ACT_INT8 && act != ZQ_ACT_F32) return ZQ_ERR_ARG;
+    if (act == ZQ_ACT_INT8 && (fmt == ZQ_FMT_Q6_K || cols % 64)) return ZQ_DECLINED;
+    return ZQ_OK;
+}
+
+// Enqueue a GEMM whose operands are all on the device.
+int enqueue_gemm(int fmt, const uint8_t* w, const float* X, float* Y, size_t tokens, size_t rows, size_t cols, int act,
+                 void* ws, size_t ws_bytes, hipStream_t s, uint64_t* dispatches) {
+    if (act == ZQ_ACT_INT8) {
+        const size_t qbytes = align_up(tokens * cols, 256);
+        const size_t need = qbytes + tokens * (cols / 32) * sizeof(float);
+        if (!ws || ws_bytes < need) return ZQ_ERR_ARG;
+        int8_t* xq = static_cast<int8_t*>(ws);
+        float* xs = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + qbytes);
+        if (zq::launch_quantize_acts(X, xq, xs, tokens, cols, s) != hipSuccess) return ZQ_ERR_HIP;
+        if (zq::launch_gemm_i8(fmt, w, xq, xs, Y, tokens, rows, cols, s) != hipSuccess) return ZQ_ERR_HIP;
+        *dispatches += 2;
+        return ZQ_OK;
+    }
+    if (zq::launch_gemm_f32(fmt, w, X, Y, tokens, rows, cols, s) != hipSuccess) return ZQ_ERR_HIP;
+    *dispatches += 1;
+    return ZQ_OK;
+}
+
+}  // namespace
+
+namespace zq {
+hipError_t launch_silu_mul(const float* gate, const float* up, float* out, size_t n, hipStream_t stream);
+}
+
+extern "C" {
+
+int zq_hip_opted_in(void) { return env_opted_in() ? 1 : 0; }
+
+int zq_hip_init(void) {
+    Backend& b = B();
+    std::lock_guard<std::mutex> lock(b.mu);
+    return init_locked(b);
+}
+
+int zq_hip_enabled(void) {
+    if (!env_opted_in()) return 0;
+    return zq_hip_init() == ZQ_OK ? 1 : 0;
+}
+
+void zq_hip_shutdown(void) {
+    Backend& b = B();
+    std::lock_guard<std::mutex> lock(b.mu);
+    if (b.initialised) {
+        (void)hipStreamSynchronize(b.stream);
+        free_resident(b);
+        if (b.dev_scratch) (void)hipFree(b.dev_scratch);
+        if (b.host_pinned) (void)hipHostFree(b.host_pinned);
+        (void)hipStreamDestroy(b.stream);
+    }
+    b.dev_scratch = nullptr;
+    b.dev_scratch_bytes = 0;
+    b.host_pinned = nullptr;
+    b.host_pinned_bytes = 0;
+    b.stream = nullptr;
+    b.initialised = false;
+    b.failed = false;
+}
+
+int zq_hip_get_info(zq_hip_info* out) {
+    if (!out) return ZQ_ERR_ARG;
+    Backend& b = B();
+    std::lock_guard<std::mutex> lock(b.mu);
+    const int st = init_locked(b);
+    if (st != ZQ_OK) return st;
+    *out = b.info;
+    return ZQ_OK;
+}
+
+int zq_hip_get_stats(zq_hip_stats* out) {
+    if (!out) return ZQ_ERR_ARG;
+    Backend& b = B();
+    std::lock_guard<std::mutex> lock(b.mu);
+    *out = b.stats;
+    return ZQ_OK;
+}
+
+void zq_hip_reset_stats(void) {
+    Backend& b = B();
+    std::lock_guard<std::mutex> lock(b.mu);
+    const uint64_t rb = b.stats.resident_bytes, rt = b.stats.resident_tensors;
+    b.stats = zq_hip_stats{};
+    b.stats.resident_bytes = rb;
+    b.stats.resident_tensors = rt;
+}
+
+const char* zq_hip_status_string(int status) {
+    switch (status) {
+    case ZQ_OK: return "ok";
+    case ZQ_DECLINED: return "declined";
+    case ZQ_ERR_ARG: return "invalid argument";
+    case ZQ_ERR_NO_DEVICE: return "no usable gfx950 device";
+    case ZQ_ERR_OOM: return "out of memory";
+    case ZQ_ERR_HIP: return "HIP runtime error";
+    default: return "unknown status";
+    }
+}
+
+size_t zq_row_bytes(int fmt, size_t cols) { return zq::row_bytes(fmt, cols); }
+
+size_t zq_weight_bytes(int fmt, size_t rows, size_t cols) {
+    const size_t rb = zq::row_bytes(fmt, cols);
+    return rb && rows ? rows * rb + ZQ_WEIGHT_TAIL_PAD : 0;
+}
+
+size_t zq_hip_set_min_elements(size_t elements) {
+    Backend& b = B();
+    std::lock_guard<std::mutex> lock(b.mu);
+    const size_t prev = b.min_elements;
+    b.min_elements = elements;
+    return prev;
+}
+
+int zq_hip_gemv_batch(int fmt, const float* x, const zq_gemv_task* tasks, size_t count, size_t cols) {
+    if (!x || !tasks || count < 1 || count > ZQ_MAX_BATCH || !valid_fmt(fmt) || !zq::row_bytes(fmt, cols))
+        return ZQ_ERR_ARG;
+    size_t total_rows = 0;
+    for (size_t i = 0; i < count; ++i) {
+        if (!tasks[i].weights || !tasks[i].y || !tasks[i].rows || tasks[i].rows > (1u << 30)) return ZQ_ERR_ARG;
+        total_rows += tasks[i].rows;
+    }
+    Backend& b = B();
+    std::lock_guard<std::mutex> lock(b.mu);
+    try {
+        int st = init_locked(b);
+        if (st != ZQ_OK) return st;
+        if (total_rows * cols < b.min_elements) {
+            ++b.stats.declined;
+            return ZQ_DECLINED;
+        }
+        zq::GemvTask dt[zq::kMaxTasks];
+        for (size_t i = 0; i < count; ++i) {
+            const uint8_t* dw = nullptr;
+            st = ensure_resident(b, fmt, tasks[i].weights, tasks[i].rows, cols, &dw);
+            if (st == ZQ_DECLINED) ++b.stats.declined;
+            if (st != ZQ_OK) return st;
+            dt[i] = zq::GemvTask{dw, nullptr, static_cast<uint32_t>(tasks[i].rows)};
+        }
+        const size_t xbytes = align_up(cols * sizeof(float), 256);
+        const size_t ybytes = total_rows * sizeof(float);
+        st = ensure_scratch(b, xbytes + ybytes, xbytes + ybytes);
+        if (st != ZQ_OK) return st;
+        float* dx = static_cast<float*>(b.dev_scratch);
+        float* dy = reinterpret_cast<float*>(static_cast<uint8_t*>(b.dev_scratch) + xbytes);
+        float* hx = static_cast<float*>(b.host_pinned);
+        float* hy = reinterpret_cast<float*>(static_cast<uint8_t*>(b.host_pinned) + xbytes);
+        size_t off = 0;
+        for (size_t i = 0; i < count; ++i) {
+            dt[i].y = dy + off;
+            off += tasks[i].rows;
+        }
+        auto t0 = Clock::now();
+        std::memcpy(hx, x, cols * sizeof(float));
+        if (hipMemcpyAsync(dx, hx, cols * sizeof(float), hipMemcpyHostToDevice, b.stream) != hipSuccess)
+            return fail_hip(b);
+        if (zq::launch_gemv(fmt, dt, static_cast<int>(count), dx, cols, b.stream) != hipSuccess) return fail_hip(b);
+        ++b.stats.dispatches;
+        if (hipMemcpyAsync(hy, dy, ybytes, hipMemcpyDeviceToHost, b.stream) != hipSuccess) return fail_hip(b);
+        const auto t1 = Clock::now();
+        if (hipStreamSynchronize(b.stream) != hipSuccess) return fail_hip(b);
+        b.stats.wait_us += us_since(t1);
+        off = 0;
+        for (size_t i = 0; i < count; ++i) {
+            std::memcpy(tasks[i].y, hy + off, tasks[i].rows * sizeof(float));
+            off += tasks[i].rows;
+        }
+        b.stats.transfer_us += us_since(t0);
+        ++b.stats.submits;
+        if (count > 1) ++b.stats.batches;
+        return ZQ_OK;
+    } catch (const std::bad_alloc&) {
+        return ZQ_ERR_OOM;
+    } catch (...) {
+        return ZQ_ERR_HIP;
+    }
+}
+
+int zq_hip_gemv(int fmt, const uint8_t* weights, const float* x, float* y, size_t rows, size_t cols) {
+    if (!weights || !y) return ZQ_ERR_ARG;
+    const zq_gemv_task t{weights, y, rows};
+    return zq_hip_gemv_batch(fmt, x, &t, 1, cols);
+}
+
+int zq_hip_gemm(int fmt, const uint8_t* weights, const float* X, float* Y, size_t tokens, size_t rows, size_t cols,
+                int act_mode) {
+    if (!weights || !X || !Y || !tokens || !rows || !valid_fmt(fmt) || !zq::row_bytes(fmt, cols) ||
+        tokens > (1u << 24) || rows > (1u << 24))
+        return ZQ_ERR_ARG;
+    const int act = resolve_act(fmt, act_mode);
+    Backend& b = B();
+    std::lock_guard<std::mutex> lock(b.mu);
+    try {
+        int st = init_locked(b);
+        if (st != ZQ_OK) return st;
+        st = gemm_supported(fmt, cols, act);
+        if (st == ZQ_DECLINED) ++b.stats.declined;
+        if (st != ZQ_OK) return st;
+        if (tokens * rows * cols < b.min_elements) {
+            ++b.stats.declined;
+            return ZQ_DECLINED;
+        }
+        const uint8_t* dw = nullptr;
+        st = ensure_resident(b, fmt, weights, rows, cols, &dw);
+        if (st == ZQ_DECLINED) ++b.stats.declined;
+        if (st != ZQ_OK) return st;
+        const size_t xbytes = align_up(tokens * cols * sizeof(float), 256);
+        const size_t ybytes = align_up(tokens * rows * sizeof(float), 256);
+        const size_t wsbytes = zq_hip_gemm_workspace_bytes(fmt, tokens, cols, act);
+        st = ensure_scratch(b, xbytes + ybytes + wsbytes, xbytes + ybytes);
+        if (st != ZQ_OK) return st;
+        uint8_t* base = static_cast<uint8_t*>(b.dev_scratch);
+        float* dx = reinterpret_cast<float*>(base);
+        float* dy = reinterpret_cast<float*>(base + xbytes);
+        void* ws = wsbytes ? base + xbytes + ybytes : nullptr;
+        float* hx = static_cast<float*>(b.host_pinned);
+        float* hy = reinterpret_cast<float*>(static_cast<uint8_t*>(b.host_pinned) + xbytes);
+        auto t0 = Clock::now();
+        std::memcpy(hx, X, tokens * cols * sizeof(float));
+        if (hipMemcpyAsync(dx, hx, tokens * cols * sizeof(float), hipMemcpyHostToDevice, b.stream) != hipSuccess)
+            return fail_hip(b);
+        st = enqueue_gemm(fmt, dw, dx, dy, tokens, rows, cols, act, ws, wsbytes, b.stream, &b.stats.dispatches);
+        if (st != ZQ_OK) {
+            ++b.stats.errors;
+            return st;
+        }
+        if (hipMemcpyAsync(hy, dy, tokens * rows * sizeof(float), hipMemcpyDeviceToHost, b.stream) != hipSuccess)
+            return fail_hip(b);
+        const auto t1 = Clock::now();
+        if (hipStreamSynchronize(b.stream) != hipSuccess) return fail_hip(b);
+        b.stats.wait_us += us_since(t1);
+        std::memcpy(Y, hy, tokens * rows * sizeof(float));
+        b.stats.transfer_us += us_since(t0);
+        ++b.stats.submits;
+        return ZQ_OK;
+    } catch (const std::bad_alloc&) {
+        return ZQ_ERR_OOM;
+    } catch (...) {
+        return ZQ_ERR_HIP;
+    }
+}
+
+int zq_hip_ffn_gemv(int fmt, const uint8_t* gate, const uint8_t* up, const uint8_t* down, const float* x, float* y,
+                    size_t ffn_rows, size_t cols, size_t out_rows) {
+    if (!gate || !up || !down || !x || !y || !ffn_rows || !out_rows || !valid_fmt(fmt) ||
+        !zq::row_bytes(fmt, cols) || !zq::row_bytes(fmt, ffn_rows) || ffn_rows > (1u << 24) ||
+        out_rows > (1u << 24))
+        return ZQ_ERR_ARG;
+    Backend& b = B();
+    std::lock_guard<std::mutex> lock(b.mu);
+    try {
+        int st = init_locked(b);
+        if (st != ZQ_OK) return st;
+        if ((2 * ffn_rows * cols + out_rows * ffn_rows) < b.min_elements) {
+            ++b.stats.declined;
+            return ZQ_DECLINED;
+        }
+        const uint8_t *dg = nullptr, *du = nullptr, *dd = nullptr;
+        if ((st = ensure_resident(b, fmt, gate, ffn_rows, cols, &dg)) != ZQ_OK ||
+            (st = ensure_resident(b, fmt, up, ffn_rows, cols, &du)) != ZQ_OK ||
+            (st = ensure_resident(b, fmt, down, out_rows, ffn_rows, &dd)) != ZQ_OK) {
+            if (st == ZQ_DECLINED) ++b.stats.declined;
+            return st;
+        }
+        // a second upload may have evicted the first: re-resolve all three
+        if ((st = ensure_resident(b, fmt, gate, ffn_rows, cols, &dg)) != ZQ_OK ||
+            (st = ensure_resident(b, fmt, up, ffn_rows, cols, &du)) != ZQ_OK)
+            return st;
+        const size_t xbytes = align_up(cols * sizeof(float), 256);
+        const size_t hbytes = align_up(ffn_rows * sizeof(float), 256);
+        const size_t ybytes = align_up(out_rows * sizeof(float), 256);
+        st = ensure_scratch(b, xbytes + 3 * hbytes + ybytes, xbytes + ybytes);
+        if (st != ZQ_OK) return st;
+        uint8_t* base = static_cast<uint8_t*>(b.dev_scratch);
+        float* dx = reinterpret_cast<float*>(base);
+        float* dgate = reinterpret_cast<float*>(base + xbytes);
+        float* dup = reinterpret_cast<float*>(base + xbytes + hbytes);
+        float* dact = reinterpret_cast<float*>(base + xbytes + 2 * hbytes);
+        float* dy = reinterpret_cast<float*>(base + xbytes + 3 * hbytes);
+        float* hx = static_cast<float*>(b.host_pinned);
+        float* hy = reinterpret_cast<float*>(static_cast<uint8_t*>(b.host_pinned) + xbytes);
+        auto t0 = Clock::now();
+        std::memcpy(hx, x, cols * sizeof(float));
+        if (hipMemcpyAsync(dx, hx, cols * sizeof(float), hipMemcpyHostToDevice, b.stream) != hipSuccess)
+            return fail_hip(b);
+        zq::GemvTask gu[2] = {{dg, dgate, static_cast<uint32_t>(ffn_rows)}, {du, dup, static_cast<uint32_t>(ffn_rows)}};
+        if (zq::launch_gemv(fmt, gu, 2, dx, cols, b.stream) != hipSuccess) return fail_hip(b);
+        if (zq::launch_silu_mul(dgate, dup, dact, ffn_rows, b.stream) != hipSuccess) return fail_hip(b);
+        zq::GemvTask dn{dd, dy, static_cast<uint32_t>(out_rows)};
+        if (zq::launch_gemv(fmt, &dn, 1, dact, ffn_rows, b.stream) != hipSuccess) return fail_hip(b);
+        b.stats.dispatches += 3;
+        if (hipMemcpyAsync(hy, dy, out_rows * sizeof(float), hipMemcpyDeviceToHost, b.stream) != hipSuccess)
+            return fail_hip(b);
+        const auto t1 = Clock::now();
+        if (hipStreamSynchronize(b.stream) != hipSuccess) return fail_hip(b);
+        b.stats.wait_us += us_since(t1);
+        std::memcpy(y, hy, out_rows * sizeof(float));
+        b.stats.transfer_us += us_since(t0);
+        ++b.stats.submits;
+        return ZQ_OK;
+    } catch (const std::bad_alloc&) {
+        return ZQ_ERR_OOM;
+    } catch (...) {
+        return ZQ_ERR_HIP;
+    }
+}
+
+int zq_hip_release(const uint8_t* weights) {
+    if (!weights) return ZQ_ERR_ARG;
+    Backend& b = B();
+    std::lock_guard<std::mutex> lock(b.mu);
+    auto it = b.resident.find(weights);
+    if (it == b.resident.end()) return ZQ_DECLINED;
+    if (b.stream) (void)hipStreamSynchronize(b.stream);
+    (void)hipFree(it->second.dev);
+    b.stats.resident_bytes -= it->second.bytes;
+    --b.stats.resident_tensors;
+    b.resident.erase(it);
+    return ZQ_OK;
+}
+
+int zq_hip_release_all(void) {
+    Backend& b = B();
+    std::lock_guard<std::mutex> lock(b.mu);
+    if (b.stream) (void)hipStreamSynchronize(b.stream);
+    free_resident(b);
+    return ZQ_OK;
+}
+
+// ---------------------------------------------------------------- device --
+int zq_hip_gemv_batch_dev(int fmt, const float* x, const zq_gemv_task* tasks, size_t count, size_t cols,
+                          void* stream) {
+    if (!x || !tasks || count < 1 || count > ZQ_MAX_BATCH || !valid_fmt(fmt) || !zq::row_bytes(fmt, cols))
+        return ZQ_ERR_ARG;
+    zq::GemvTask dt[zq::kMaxTasks];
+    for (size_t i = 0; i < count; ++i) {
+        if (!tasks[i].weights || !tasks[i].y || !tasks[i].rows || tasks[i].rows > (1u << 30)) return ZQ_ERR_ARG;
+        dt[i] = zq::GemvTask{tasks[i].weights, tasks[i].y, static_cast<uint32_t>(tasks[i].rows)};
+    }
+    if (zq::launch_gemv(fmt, dt, static_cast<int>(count), x, cols, static_cast<hipStream_t>(stream)) != hipSuccess)
+        return ZQ_ERR_HIP;
+    return ZQ_OK;
+}
+
+int zq_hip_gemv_dev(int fmt, const void* weights, const float* x, float* y, size_t rows, size_t cols, void* stream) {
+    const zq_gemv_task t{static_cast<const uint8_t*>(weights), y, rows};
+    return zq_hip_gemv_batch_dev(fmt, x, &t, 1, cols, stream);
+}
+
+size_t zq_hip_gemm_workspace_bytes(int fmt, size_t tokens, size_t cols, int act_mode) {
+    if (!valid_fmt(fmt) || !zq::row_bytes(fmt, cols)) return 0;
+    if (resolve_act(fmt, act_mode) != ZQ_ACT_INT8) return 0;
+    return align_up(tokens * cols, 256) + tokens * (cols / 32) * sizeof(float);
+}
+
+int zq_hip_gemm_dev(int fmt, const void* weights, const float* X, float* Y, size_t tokens, size_t rows, size_t cols,
+                    int act_mode, void* workspace, size_t workspace_bytes, void* stream) {
+    if (!weights || !X || !Y || !tokens || !rows || !valid_fmt(fmt) || !zq::row_bytes(fmt, cols) ||
+        tokens > (1u << 24) || rows > (1u << 24))
+        return ZQ_ERR_ARG;
+    const int act = resolve_act(fmt, act_mode);
+    const int st = gemm_supported(fmt, cols, act);
+    if (st != ZQ_OK) return st;
+    uint64_t d = 0;
+    return enqueue_gemm(fmt, static_cast<const uint8_t*>(weights), X, Y, tokens, rows, cols, act, workspace,
+                        workspace_bytes, static_cast<hipStream_t>(stream), &d);
+}
+
+int zq_hip_quantize_acts_dev(const float* X, int8_t* xq, float* xs, size_t tokens, size_t cols, void* stream) {
+    if (!X || !xq || !xs || !tokens || !cols || cols % 32) return ZQ_ERR_ARG;
+    return zq::launch_quantize_acts(X, xq, xs, tokens, cols, static_cast<hipStream_t>(stream)) == hipSuccess
+               ? ZQ_OK
+               : ZQ_ERR_HIP;
+}
+
+int zq_hip_block_dots_dev(int fmt, const void* weights, const int8_t* xq, int32_t* out, size_t tokens, size_t rows,
+                          size_t cols, void* stream) {
+    if (!weights || !xq || !out || !tokens || !rows || !valid_fmt(fmt) || !zq::row_bytes(fmt, cols)) return ZQ_ERR_ARG;
+    if (fmt == ZQ_FMT_Q6_K || cols % 64) return ZQ_DECLINED;
+    return zq::launch_block_dots(fmt, static_cast<const uint8_t*>(weights), xq, out, tokens, rows, cols,
+                                 static_cast<hipStream_t>(stream)) == hipSuccess
+               ? ZQ_OK
+               : ZQ_ERR_HIP;
+}
+
+int zq_hip_dequantize_dev(int fmt, const void* weights, float* out, size_t rows, size_t cols, void* stream) {
+    if (!weights || !out || !rows || !valid_fmt(fmt) || !zq::row_bytes(fmt, cols)) return ZQ_ERR_ARG;
+    return zq::launch_dequantize(fmt, static_cast<const uint8_t*>(weights), out, rows, cols,
+                                 static_cast<hipStream_t>(stream)) == hipSuccess
+               ? ZQ_OK
+               : ZQ_ERR_HIP;
+}
+
+int zq_hip_synth_weights_dev(int fmt, uint64_t seed, void* weights, size_t rows, size_t cols, void* stream) {
+    if (!weights || !rows || !valid_fmt(fmt) || !zq::row_bytes(fmt, cols)) return ZQ_ERR_ARG;
+    return zq::launch_synth_weights(fmt, seed, static_cast<uint8_t*>(weights), rows, cols,
+                                    static_cast<hipStream_t>(stream)) == hipSuccess
+               ? ZQ_OK
+               : ZQ_ERR_HIP;
+}
+
+int zq_hip_synth_normal_dev(uint64_t seed, float* out, size_t n, void* stream) {
+    if (!out || !n) return ZQ_ERR_ARG;
+    return zq::launch_synth_normal(seed, out, n, static_cast<hipStream_t>(stream)) == hipSuccess ? ZQ_OK : ZQ_ERR_HIP;
+}
+
+}  // extern "C"

@@ -1,0 +1,110 @@
+// zq_device.hpp -- device-side helpers shared by the gfx950 kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+namespace zq {
+
+// GGML type ids (src/gguf.cpp:370-393 of the reference: 2=Q4_0, 8=Q8_0, 14=Q6_K).
+constexpr int kQ4_0 = 2;
+constexpr int kQ8_0 = 8;
+constexpr int kQ6_K = 14;
+
+constexpr int kWave = 64;
+
+// binary16 -> binary32.  v_cvt_f32_f16 is exact for every binary16 input,
+// subnormals included (fp16 denormals are enabled in the HIP default mode).
+__device__ __forceinline__ float half_bits_to_float(uint32_t bits16) {
+    return __half2float(__ushort_as_half(static_cast<unsigned short>(bits16 & 0xffffu)));
+}
+
+// Sign-extended byte k of a dword as float (one v_cvt_f32_i32 with SDWA sext).
+__device__ __forceinline__ float sbyte(uint32_t v, int k) {
+    return static_cast<float>(static_cast<int8_t>(v >> (8 * k)));
+}
+
+// 32 bits starting at an arbitrary byte address, from two naturally aligned
+// dword loads and one v_alignbyte.  Used where GGML block boundaries put
+// fields at addresses that are 2 mod 4.
+__device__ __forceinline__ uint32_t load_u32_any(const uint8_t* p) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    const uint32_t* base = reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3));
+    const uint32_t lo = base[0];
+    const uint32_t sh = static_cast<uint32_t>(a & 3u);
+    if (sh == 0) return lo;
+    const uint32_t hi = base[1];
+    return __builtin_amdgcn_alignbyte(hi, lo, sh);
+}
+
+// 32 bits from a 2-byte-aligned address as two 16-bit loads; never reads
+// past p+3, so it is safe on the last bytes of a buffer.
+__device__ __forceinline__ uint32_t load_u32_a2(const uint8_t* p) {
+    const uint16_t* h = reinterpret_cast<const uint16_t*>(p);
+    return uint32_t(h[0]) | (uint32_t(h[1]) << 16);
+}
+
+__host__ __device__ inline size_t row_bytes_dev(int fmt, size_t cols) {
+    return fmt == kQ8_0 ? cols / 32 * 34 : fmt == kQ4_0 ? cols / 32 * 18 : cols / 256 * 210;
+}
+
+// Exact dequantisation of the 32 consecutive elements [k0, k0+32) of one
+// weight row (k0 % 32 == 0), to the values of the reference's dequantize:
+// Q8_0 int8(q)*d (src/quant.cpp:410-416), Q4_0 (n-8)*d (:391-397), Q6_K
+// (d*sc)*(q-32) (:500-517).  Reads stay inside the blocks they decode.
+template <int FMT>
+__device__ __forceinline__ void dequant32(const uint8_t* row, uint32_t k0, float (&o)[32]) {
+    if constexpr (FMT == kQ8_0) {
+        const uint8_t* p = row + size_t(k0 >> 5) * 34;
+        const float d = half_bits_to_float(*reinterpret_cast<const uint16_t*>(p));
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t u = load_u32_a2(p + 2 + 4 * i);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) o[4 * i + k] = sbyte(u, k) * d;
+        }
+    } else if constexpr (FMT == kQ4_0) {
+        const uint8_t* p = row + size_t(k0 >> 5) * 18;
+        const float d = half_bits_to_float(*reinterpret_cast<const uint16_t*>(p));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t u = load_u32_a2(p + 2 + 4 * i);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t byte = (u >> (8 * k)) & 0xffu;
+                o[4 * i + k] = float(int(byte & 15u) - 8) * d;
+                o[16 + 4 * i + k] = float(int(byte >> 4) - 8) * d;
+            }
+        }
+    } else {
+        const uint8_t* p = row + size_t(k0 >> 8) * 210;
+        const uint32_t in_sb = k0 & 255u;
+        const uint32_t h = in_sb >> 7, grp = (in_sb >> 5) & 3u;
+        const float d = half_bits_to_float(*reinterpret_cast<const uint16_t*>(p + 208));
+        const int8_t* sc = reinterpret_cast<const int8_t*>(p + 192);
+        const float ds0 = d * float(sc[h * 8 + grp * 2]);
+        const float ds1 = d * float(sc[h * 8 + grp * 2 + 1]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t lo = load_u32_a2(p + h * 64 + (grp & 1u) * 32 + 4 * i);
+            const uint32_t hi = load_u32_a2(p + 128 + h * 32 + 4 * i);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                uint32_t l = (lo >> (8 * k)) & 0xffu;
+                if (grp >= 2) l >>= 4;
+                const uint32_t hb = ((hi >> (8 * k)) >> (2 * grp)) & 3u;
+                const int q = int((l & 15u) | (hb << 4)) - 32;
+                o[4 * i + k] = (i < 4 ? ds0 : ds1) * float(q);
+            }
+        }
+    }
+}
+
+// Wave64 sum: xor-butterfly over 6 steps, every lane ends with the total.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+}  // namespace zq

@@ -1,0 +1,396 @@
+// zq_gemv.hip -- decode GEMV (batch 1, fp32 activations) over native GGML
+// blocks for gfx950.
+//
+// Weights stay in their GGUF block layout in HBM: Q8_0 = 34-byte blocks
+// (fp16 d, 32 x int8), Q4_0 = 18-byte blocks (fp16 d, 16 bytes of nibbles),
+// Q6_K = 210-byte super-blocks (ql[128] | qh[64] | int8 sc[16] | fp16 d).
+//
+// Q8_0 / Q4_0 (cols % 64 == 0): one lane owns a PAIR of consecutive blocks.
+// A pair is 68 B (Q8_0) / 36 B (Q4_0), a multiple of 4 bytes, so every pair
+// starts dword-aligned even though single blocks alternate between 0 and 2
+// mod 4.  Inside a pair every field sits at a fixed byte position, so the
+// lane decodes with static byte selects (v_cvt_f32_i32 with SDWA sext) and
+// one v_alignbyte per misaligned dword; no repack on upload.  The 64 lanes of
+// a wave cover 64 consecutive pairs = 4352 contiguous bytes of a Q8_0 row
+// (exactly one row at K=4096), so a wave's loads touch whole cache lines.
+//
+// The activation vector is staged once per workgroup in LDS with a 4-float
+// pad after every 64 floats: lane L reads its pair's 64 floats with
+// ds_read_b128 at a 68-dword stride, which spreads 8 consecutive lanes over
+// all 32 banks.  Each wave processes R rows at a time so the x values read
+// from LDS are reused R times from registers, and R rows x 68 B per lane are
+// in flight per iteration.  The per-lane partial sums are reduced across the
+// wave with a butterfly (ds_swizzle/DPP), then one lane stores R outputs.
+//
+// Q6_K: one lane owns a 16-element unit (half h, l-quad l0) of a super-block:
+// 3 data dwords (ql low/high streams and qh), 4 int8 sub-scales and d.  The
+// four 4-element groups are decoded byte-parallel: q = lo4 | hi2 << 4, then
+// ((q ^ 0x20) << 2) is 4*(q-32) as a signed byte.
+#include "zq_device.hpp"
+#include "zq_internal.hpp"
+
+#include <algorithm>
+#include <cstdlib>
+
+namespace zq {
+
+size_t row_bytes(int fmt, size_t cols) {
+    switch (fmt) {
+    case kQ4_0: return (cols && cols % 32 == 0) ? cols / 32 * 18 : 0;
+    case kQ8_0: return (cols && cols % 32 == 0) ? cols / 32 * 34 : 0;
+    case kQ6_K: return (cols && cols % 256 == 0) ? cols / 256 * 210 : 0;
+    default: return 0;
+    }
+}
+
+namespace {
+
+struct TaskTable {
+    GemvTask t[kMaxTasks];
+    uint32_t group_start[kMaxTasks + 1];  // prefix sums of per-task row groups
+    int count;
+};
+
+constexpr int kThreads = 256;
+constexpr int kWavesPerBlock = kThreads / kWave;
+constexpr int kPadStride = 68;  // floats per 64-float x chunk in LDS
+
+// Locate the task owning row-group g (count <= 8, linear scan).
+__device__ __forceinline__ int find_task(const TaskTable& tt, uint32_t g) {
+    int i = 0;
+#pragma unroll
+    for (int k = 1; k < kMaxTasks; ++k)
+        if (k < tt.count && g >= tt.group_start[k]) i = k;
+    return i;
+}
+
+// Stage x (cols floats) into LDS.  Padded layout when PAD: chunk c of 64
+// floats at c*68.
+template <bool PAD>
+__device__ __forceinline__ void stage_x(float* xs, const float* __restrict__ x, uint32_t cols) {
+    for (uint32_t i = threadIdx.x; i < cols; i += kThreads) {
+        const uint32_t dst = PAD ? (i >> 6) * kPadStride + (i & 63u) : i;
+        xs[dst] = x[i];
+    }
+    __syncthreads();
+}
+
+// ---------------------------------------------------------------- Q8_0 ---
+// Dot of one 68-byte Q8_0 block pair with 64 x values.
+//   dword 0      : d0 (bytes 0-1) | q0 q1
+//   dwords 1..7  : q2 .. q29
+//   dword 8      : q30 q31 | d1 (bytes 2-3)
+//   dwords 9..16 : second block's 32 quants
+__device__ __forceinline__ float q8_pair_dot(const uint32_t (&q)[17], const float (&xv)[64]) {
+    float s0 = 0.0f, s1 = 0.0f;
+    s0 = fmaf(sbyte(q[0], 2), xv[0], s0);
+    s0 = fmaf(sbyte(q[0], 3), xv[1], s0);
+#pragma unroll
+    for (int i = 1; i < 8; ++i) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) s0 = fmaf(sbyte(q[i], k), xv[4 * i - 2 + k], s0);
+    }
+    s0 = fmaf(sbyte(q[8], 0), xv[30], s0);
+    s0 = fmaf(sbyte(q[8], 1), xv[31], s0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) s1 = fmaf(sbyte(q[9 + i], k), xv[32 + 4 * i + k], s1);
+    }
+    const float d0 = half_bits_to_float(q[0]);
+    const float d1 = half_bits_to_float(q[8] >> 16);
+    return fmaf(d1, s1, d0 * s0);
+}
+
+// Dot of one 36-byte Q4_0 block pair with 64 x values.
+//   dword 0     : d0 | n0 n1      dwords 1..3 : n2 .. n13
+//   dword 4     : n14 n15 | d1    dwords 5..8 : second block's 16 bytes
+// Byte j holds element j (low nibble) and j+16 (high nibble); value (n-8)*d.
+// ((n ^ 8) << 4) read as a signed byte is 16*(n-8): exact, scaled out by d/16.
+__device__ __forceinline__ float q4_block_dot(const uint32_t (&u)[4], const float* xv) {
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t lo = ((u[i] << 4) & 0xF0F0F0F0u) ^ 0x80808080u;
+        const uint32_t hi = (u[i] & 0xF0F0F0F0u) ^ 0x80808080u;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            s = fmaf(sbyte(lo, k), xv[4 * i + k], s);
+            s = fmaf(sbyte(hi, k), xv[16 + 4 * i + k], s);
+        }
+    }
+    return s;
+}
+__device__ __forceinline__ float q4_pair_dot(const uint32_t (&q)[9], const float (&xv)[64]) {
+    uint32_t a[4], b[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        a[i] = __builtin_amdgcn_alignbyte(q[i + 1], q[i], 2);
+        b[i] = q[5 + i];
+    }
+    const float s0 = q4_block_dot(a, xv);
+    const float s1 = q4_block_dot(b, xv + 32);
+    const float d0 = half_bits_to_float(q[0]) * 0.0625f;
+    const float d1 = half_bits_to_float(q[4] >> 16) * 0.0625f;
+    return fmaf(d1, s1, d0 * s0);
+}
+
+// Pair-lane kernel for Q8_0 (DW=17) and Q4_0 (DW=9).
+template <int FMT, int R>
+__global__ __launch_bounds__(kThreads) void gemv_pairs_kernel(TaskTable tt, const float* __restrict__ x,
+                                                              uint32_t cols, uint32_t total_groups) {
+    constexpr int DW = FMT == kQ8_0 ? 17 : 9;
+    extern __shared__ float xs[];
+    stage_x<true>(xs, x, cols);
+    const uint32_t pairs = cols >> 6;
+    const uint32_t rb = pairs * DW * 4;
+    const int lane = threadIdx.x & 63;
+    const uint32_t wave = threadIdx.x >> 6;
+    for (uint32_t g = blockIdx.x * kWavesPerBlock + wave; g < total_groups; g += gridDim.x * kWavesPerBlock) {
+        const int ti = find_task(tt, g);
+        const GemvTask task = tt.t[ti];
+        const uint32_t r0 = (g - tt.group_start[ti]) * R;
+        float acc[R];
+        const uint8_t* rowp[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            acc[r] = 0.0f;
+            const uint32_t row = min(r0 + r, task.rows - 1);
+            rowp[r] = task.w + (size_t)row * rb;
+        }
+        for (uint32_t p = lane; p < pairs; p += kWave) {
+            uint32_t q[R][DW];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const uint32_t* src = reinterpret_cast<const uint32_t*>(rowp[r] + (size_t)p * DW * 4);
+#pragma unroll
+                for (int i = 0; i < DW; ++i) q[r][i] = __builtin_nontemporal_load(src + i);
+            }
+            float xv[64];
+            const float4* xp = reinterpret_cast<const float4*>(xs + p * kPadStride);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float4 v = xp[i];
+                xv[4 * i] = v.x; xv[4 * i + 1] = v.y; xv[4 * i + 2] = v.z; xv[4 * i + 3] = v.w;
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                if constexpr (FMT == kQ8_0) acc[r] += q8_pair_dot(q[r], xv);
+                else acc[r] += q4_pair_dot(q[r], xv);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float v = wave_sum(acc[r]);
+            if (lane == r && r0 + r < task.rows) task.y[r0 + r] = v;
+        }
+    }
+}
+
+// ---------------------------------------------------------------- Q6_K ---
+// One lane = one 16-element unit (super-block sb, half h, l-quad l0).
+template <int R>
+__global__ __launch_bounds__(kThreads) void gemv_q6k_kernel(TaskTable tt, const float* __restrict__ x,
+                                                            uint32_t cols, uint32_t total_groups) {
+    extern __shared__ float xs[];
+    stage_x<false>(xs, x, cols);
+    const uint32_t nsb = cols >> 8;
+    const uint32_t units = nsb * 16;
+    const uint32_t rb = nsb * 210;
+    const int lane = threadIdx.x & 63;
+    const uint32_t wave = threadIdx.x >> 6;
+    for (uint32_t g = blockIdx.x * kWavesPerBlock + wave; g < total_groups; g += gridDim.x * kWavesPerBlock) {
+        const int ti = find_task(tt, g);
+        const GemvTask task = tt.t[ti];
+        const uint32_t r0 = (g - tt.group_start[ti]) * R;
+        float acc[R];
+        const uint8_t* rowp[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            acc[r] = 0.0f;
+            rowp[r] = task.w + (size_t)min(r0 + r, task.rows - 1) * rb;
+        }
+        for (uint32_t u = lane; u < units; u += kWave) {
+            const uint32_t sb = u >> 4, h = (u >> 3) & 1u, l0 = (u & 7u) * 4u;
+            const uint32_t xbase = sb * 256 + h * 128 + l0;
+            float xv[4][4];
+#pragma unroll
+            for (int gi = 0; gi < 4; ++gi) {
+                const float4 v = *reinterpret_cast<const float4*>(xs + xbase + gi * 32);
+                xv[gi][0] = v.x; xv[gi][1] = v.y; xv[gi][2] = v.z; xv[gi][3] = v.w;
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const uint8_t* sbp = rowp[r] + (size_t)sb * 210;
+                const uint32_t qlA = load_u32_any(sbp + h * 64 + l0);
+                const uint32_t qlB = load_u32_any(sbp + h * 64 + 32 + l0);
+                const uint32_t qh = load_u32_any(sbp + 128 + h * 32 + l0);
+                const uint32_t sc0 = load_u32_any(sbp + 192 + h * 8);
+                const uint32_t sc1 = load_u32_any(sbp + 196 + h * 8);
+                const float d = half_bits_to_float(*reinterpret_cast<const uint16_t*>(sbp + 208)) * 0.25f;
+                const uint32_t shsel = l0 >> 4;  // which of the two 16-element sub-blocks
+                float part = 0.0f;
+#pragma unroll
+                for (int gi = 0; gi < 4; ++gi) {
+                    uint32_t lo = (gi & 1) ? qlB : qlA;
+                    if (gi >= 2) lo >>= 4;
+                    lo &= 0x0F0F0F0Fu;
+                    const uint32_t hi = ((qh >> (2 * gi)) & 0x03030303u) << 4;
+                    const uint32_t v = ((lo | hi) ^ 0x20202020u) << 2;  // 4*(q-32) per byte
+                    float s = 0.0f;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) s = fmaf(sbyte(v, k), xv[gi][k], s);
+                    const uint32_t scw = gi < 2 ? sc0 : sc1;
+                    const float sc = sbyte(scw, (2 * gi + shsel) & 3);
+                    part = fmaf(d * sc, s, part);
+                }
+                acc[r] += part;
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float v = wave_sum(acc[r]);
+            if (lane == r && r0 + r < task.rows) task.y[r0 + r] = v;
+        }
+    }
+}
+
+// ------------------------------------------------------------- generic ---
+// Lane-per-block fallback for Q8_0 / Q4_0 rows whose block count is odd or
+// whose base is not dword-aligned.  x is read from global memory.
+template <int FMT>
+__global__ __launch_bounds__(kThreads) void gemv_block_kernel(TaskTable tt, const float* __restrict__ x,
+                                                              uint32_t cols, uint32_t total_groups) {
+    constexpr uint32_t BB = FMT == kQ8_0 ? 34 : 18;
+    const uint32_t nb = cols >> 5;
+    const uint32_t rb = nb * BB;
+    const int lane = threadIdx.x & 63;
+    const uint32_t wave = threadIdx.x >> 6;
+    for (uint32_t g = blockIdx.x * kWavesPerBlock + wave; g < total_groups; g += gridDim.x * kWavesPerBlock) {
+        const int ti = find_task(tt, g);
+        const GemvTask task = tt.t[ti];
+        const uint32_t row = g - tt.group_start[ti];
+        const uint8_t* rp = task.w + (size_t)row * rb;
+        float acc = 0.0f;
+        for (uint32_t b = lane; b < nb; b += kWave) {
+            const uint8_t* p = rp + (size_t)b * BB;
+            const float d = half_bits_to_float(uint32_t(p[0]) | (uint32_t(p[1]) << 8));
+            const float* xb = x + b * 32;
+            float s = 0.0f;
+            if constexpr (FMT == kQ8_0) {
+                for (int j = 0; j < 32; ++j) s = fmaf(float(int8_t(p[2 + j])), xb[j], s);
+            } else {
+                for (int j = 0; j < 16; ++j) {
+                    s = fmaf(float(int(p[2 + j] & 15) - 8), xb[j], s);
+                    s = fmaf(float(int(p[2 + j] >> 4) - 8), xb[j + 16], s);
+                }
+            }
+            acc = fmaf(d, s, acc);
+        }
+        const float v = wave_sum(acc);
+        if (lane == 0) task.y[row] = v;
+    }
+}
+
+int rows_per_wave(uint32_t total_rows) {
+    static const int forced = [] {
+        const char* e = getenv("ZQ_GEMV_ROWS_PER_WAVE");
+        const int v = e ? atoi(e) : 0;
+        return (v == 1 || v == 2 || v == 4) ? v : 0;
+    }();
+    if (forced) return forced;
+    if (total_rows >= 8192) return 4;
+    if (total_rows >= 2048) return 2;
+    return 1;
+}
+
+template <int FMT, int R>
+hipError_t launch_pairs(TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream) {
+    uint32_t groups = 0;
+    for (int i = 0; i < tt.count; ++i) {
+        tt.group_start[i] = groups;
+        groups += (tt.t[i].rows + R - 1) / R;
+    }
+    tt.group_start[tt.count] = groups;
+    const uint32_t blocks = std::min<uint32_t>((groups + kWavesPerBlock - 1) / kWavesPerBlock, 4096u);
+    const size_t lds = size_t(cols >> 6) * kPadStride * sizeof(float);
+    hipLaunchKernelGGL((gemv_pairs_kernel<FMT, R>), dim3(blocks), dim3(kThreads), lds, stream, tt, x, cols, groups);
+    return hipGetLastError();
+}
+template <int R>
+hipError_t launch_q6k(TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream) {
+    uint32_t groups = 0;
+    for (int i = 0; i < tt.count; ++i) {
+        tt.group_start[i] = groups;
+        groups += (tt.t[i].rows + R - 1) / R;
+    }
+    tt.group_start[tt.count] = groups;
+    const uint32_t blocks = std::min<uint32_t>((groups + kWavesPerBlock - 1) / kWavesPerBlock, 4096u);
+    hipLaunchKernelGGL((gemv_q6k_kernel<R>), dim3(blocks), dim3(kThreads), size_t(cols) * sizeof(float), stream, tt,
+                       x, cols, groups);
+    return hipGetLastError();
+}
+template <int FMT>
+hipError_t launch_blocks(TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream) {
+    uint32_t groups = 0;
+    for (int i = 0; i < tt.count; ++i) {
+        tt.group_start[i] = groups;
+        groups += tt.t[i].rows;
+    }
+    tt.group_start[tt.count] = groups;
+    const uint32_t blocks = std::min<uint32_t>((groups + kWavesPerBlock - 1) / kWavesPerBlock, 4096u);
+    hipLaunchKernelGGL((gemv_block_kernel<FMT>), dim3(blocks), dim3(kThreads), 0, stream, tt, x, cols, groups);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+// LDS budget of one workgroup for the staged activation vector.
+static size_t lds_limit() {
+    static const size_t limit = [] {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) != hipSuccess) return size_t(65536);
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0)
+            return size_t(65536);
+        return size_t(v);
+    }();
+    return limit;
+}
+
+hipError_t launch_gemv(int fmt, const GemvTask* tasks, int count, const float* x, size_t cols,
+                       hipStream_t stream) {
+    if (count < 1 || count > kMaxTasks || !x || !row_bytes(fmt, cols) || cols > (1u << 24))
+        return hipErrorInvalidValue;
+    TaskTable tt{};
+    tt.count = count;
+    uint32_t total_rows = 0;
+    bool aligned = true;
+    for (int i = 0; i < count; ++i) {
+        if (!tasks[i].w || !tasks[i].y || !tasks[i].rows) return hipErrorInvalidValue;
+        tt.t[i] = tasks[i];
+        total_rows += tasks[i].rows;
+        aligned = aligned && (reinterpret_cast<uintptr_t>(tasks[i].w) & 3u) == 0;
+    }
+    const uint32_t c = static_cast<uint32_t>(cols);
+    const int R = rows_per_wave(total_rows);
+    if (fmt == kQ6_K) {
+        if (size_t(c) * 4 > lds_limit() || (reinterpret_cast<uintptr_t>(x) & 15u)) return hipErrorInvalidValue;
+        for (int i = 0; i < count; ++i)
+            if (reinterpret_cast<uintptr_t>(tasks[i].w) & 1u) return hipErrorInvalidValue;
+        if (R == 4) return launch_q6k<4>(tt, x, c, stream);
+        if (R == 2) return launch_q6k<2>(tt, x, c, stream);
+        return launch_q6k<1>(tt, x, c, stream);
+    }
+    const bool pairs_ok = aligned && (c % 64 == 0) && size_t(c / 64) * kPadStride * 4 <= lds_limit();
+    if (!pairs_ok) return fmt == kQ8_0 ? launch_blocks<kQ8_0>(tt, x, c, stream) : launch_blocks<kQ4_0>(tt, x, c, stream);
+    if (fmt == kQ8_0) {
+        if (R == 4) return launch_pairs<kQ8_0, 4>(tt, x, c, stream);
+        if (R == 2) return launch_pairs<kQ8_0, 2>(tt, x, c, stream);
+        return launch_pairs<kQ8_0, 1>(tt, x, c, stream);
+    }
+    if (R == 4) return launch_pairs<kQ4_0, 4>(tt, x, c, stream);
+    if (R == 2) return launch_pairs<kQ4_0, 2>(tt, x, c, stream);
+    return launch_pairs<kQ4_0, 1>(tt, x, c, stream);
+}
+
+}  // namespace zq

@@ -1,0 +1,51 @@
+// zq_internal.hpp -- launch interface between the C-ABI runtime (zq_backend.hip)
+// and the kernel translation units.  Host-only declarations; no HIP types
+// beyond hipStream_t / hipError_t cross this header.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace zq {
+
+// One projection of a batched decode GEMV: all tasks share the input vector
+// and the column count (the Q|K|V and gate|up pattern).
+struct GemvTask {
+    const uint8_t* w;  // device pointer, native GGML blocks, row-major
+    float* y;          // device pointer, rows floats
+    uint32_t rows;
+};
+constexpr int kMaxTasks = 8;
+
+// Row bytes of one GGML row (0 when cols does not divide into blocks).
+size_t row_bytes(int fmt, size_t cols);
+
+// Decode GEMV with fp32 activations: y_i = W_i . x for every task.
+hipError_t launch_gemv(int fmt, const GemvTask* tasks, int count, const float* x,
+                       size_t cols, hipStream_t stream);
+
+// Per-32-element activation quantiser (int8 + fp32 scale per block).
+hipError_t launch_quantize_acts(const float* X, int8_t* xq, float* xs, size_t M, size_t K,
+                                hipStream_t stream);
+
+// Prefill GEMM on int8 activations already quantised by launch_quantize_acts.
+// Y is token-major [M][N].
+hipError_t launch_gemm_i8(int fmt, const uint8_t* w, const int8_t* xq, const float* xs,
+                          float* Y, size_t M, size_t N, size_t K, hipStream_t stream);
+
+// Prefill GEMM on fp32 activations (the reference CPU arithmetic).
+hipError_t launch_gemm_f32(int fmt, const uint8_t* w, const float* X, float* Y, size_t M,
+                           size_t N, size_t K, hipStream_t stream);
+
+// Bit-exact tier helpers.
+hipError_t launch_dequantize(int fmt, const uint8_t* w, float* out, size_t rows, size_t cols,
+                             hipStream_t stream);
+hipError_t launch_block_dots(int fmt, const uint8_t* w, const int8_t* xq, int32_t* out,
+                             size_t M, size_t N, size_t K, hipStream_t stream);
+
+// Synthetic inputs generated on the device (bench workloads).
+hipError_t launch_synth_weights(int fmt, uint64_t seed, uint8_t* w, size_t rows, size_t cols,
+                                hipStream_t stream);
+hipError_t launch_synth_normal(uint64_t seed, float* out, size_t n, hipStream_t stream);
+
+}  // namespace zq

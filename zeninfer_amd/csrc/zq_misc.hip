@@ -1,0 +1,151 @@
+// zq_misc.hip -- dequantisation (bit-exact tier) and synthetic-input
+// generation on the device.
+#include "zq_device.hpp"
+#include "zq_internal.hpp"
+
+namespace zq {
+namespace {
+
+constexpr int kThreads = 256;
+
+// One thread per 32-element run; out is row-major fp32 [rows][cols].
+template <int FMT>
+__global__ __launch_bounds__(kThreads) void dequantize_kernel(const uint8_t* __restrict__ w, float* __restrict__ out,
+                                                              size_t rows, size_t cols) {
+    const size_t runs_per_row = cols / 32;
+    const size_t id = size_t(blockIdx.x) * kThreads + threadIdx.x;
+    if (id >= rows * runs_per_row) return;
+    const size_t r = id / runs_per_row, run = id % runs_per_row;
+    float o[32];
+    dequant32<FMT>(w + r * row_bytes_dev(FMT, cols), uint32_t(run * 32), o);
+    float4* dst = reinterpret_cast<float4*>(out + r * cols + run * 32);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dst[i] = make_float4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+}
+
+// ------------------------------------------------------ synthetic data ---
+// Counter-based SplitMix64: draw i of stream `seed` equals the (i+1)-th
+// output of the sequential generator seeded with `seed`.
+__device__ __forceinline__ uint64_t splitmix64_at(uint64_t seed, uint64_t i) {
+    uint64_t z = seed + (i + 1) * 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+// Box-Muller in double from draws 2i and 2i+1.
+__device__ __forceinline__ double normal_at(uint64_t seed, uint64_t i) {
+    const uint64_t a = splitmix64_at(seed, 2 * i), b = splitmix64_at(seed, 2 * i + 1);
+    const double u1 = (double(a >> 11) + 1.0) * (1.0 / 9007199254740992.0);
+    const double u2 = double(b >> 11) * (1.0 / 9007199254740992.0);
+    return sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2);
+}
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float v) { return __half_as_ushort(__float2half_rn(v)); }
+
+__device__ __forceinline__ uint64_t seed_quant(uint64_t s) { return s ^ 0x51ull; }
+__device__ __forceinline__ uint64_t seed_scale(uint64_t s) { return s ^ 0x5CA1Eull; }
+__device__ __forceinline__ uint64_t seed_sub(uint64_t s) { return s ^ 0x5B5Cull; }
+
+// One thread per block / super-block.  Recipes:
+//   Q8_0: q ~ U{-127..127}, d = fp16(|N(0,1)| * 0.002)
+//   Q4_0: nibble ~ U{0..15}, d = fp16(|N(0,1)| * 0.02)
+//   Q6_K: q ~ U{0..63}, sc ~ U{-32..31}, d = fp16(|N(0,1)| * 0.001)
+template <int FMT>
+__global__ __launch_bounds__(kThreads) void synth_kernel(uint64_t seed, uint8_t* __restrict__ w, size_t nblocks) {
+    const size_t g = size_t(blockIdx.x) * kThreads + threadIdx.x;
+    if (g >= nblocks) return;
+    if constexpr (FMT == kQ8_0) {
+        uint8_t* p = w + g * 34;
+        const uint16_t h = f32_to_f16_bits(float(fabs(normal_at(seed_scale(seed), g)) * 0.002));
+        p[0] = uint8_t(h); p[1] = uint8_t(h >> 8);
+        for (int j = 0; j < 32; ++j) {
+            const uint64_t u = splitmix64_at(seed_quant(seed), g * 32 + j);
+            p[2 + j] = uint8_t(int8_t(int((u >> 32) % 255u) - 127));
+        }
+    } else if constexpr (FMT == kQ4_0) {
+        uint8_t* p = w + g * 18;
+        const uint16_t h = f32_to_f16_bits(float(fabs(normal_at(seed_scale(seed), g)) * 0.02));
+        p[0] = uint8_t(h); p[1] = uint8_t(h >> 8);
+        for (int j = 0; j < 16; ++j) p[2 + j] = uint8_t(splitmix64_at(seed_quant(seed), g * 16 + j) >> 56);
+    } else {
+        uint8_t* p = w + g * 210;
+        for (int i = 0; i < 16; ++i) {
+            const uint64_t u = splitmix64_at(seed_sub(seed), g * 16 + i);
+            p[192 + i] = uint8_t(int8_t(int((u >> 32) % 64u) - 32));
+        }
+        const uint16_t h = f32_to_f16_bits(float(fabs(normal_at(seed_scale(seed), g)) * 0.001));
+        p[208] = uint8_t(h); p[209] = uint8_t(h >> 8);
+        for (int half = 0; half < 2; ++half)
+            for (int l = 0; l < 32; ++l) {
+                unsigned q[4];
+                for (int grp = 0; grp < 4; ++grp) {
+                    const size_t e = size_t(half) * 128 + size_t(grp) * 32 + size_t(l);
+                    q[grp] = unsigned(splitmix64_at(seed_quant(seed), g * 256 + e) >> 58);
+                }
+                p[half * 64 + l] = uint8_t((q[0] & 15u) | ((q[2] & 15u) << 4));
+                p[half * 64 + 32 + l] = uint8_t((q[1] & 15u) | ((q[3] & 15u) << 4));
+                p[128 + half * 32 + l] = uint8_t((q[0] >> 4) | ((q[1] >> 4) << 2) | ((q[2] >> 4) << 4) | ((q[3] >> 4) << 6));
+            }
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void synth_normal_kernel(uint64_t seed, float* __restrict__ out, size_t n) {
+    const size_t i = size_t(blockIdx.x) * kThreads + threadIdx.x;
+    if (i < n) out[i] = float(normal_at(seed, i));
+}
+
+// SiLU(gate) * up, the FFN activation between gate|up and down
+// (g / (1 + e^-g)) * u.
+__global__ __launch_bounds__(kThreads) void silu_mul_kernel(const float* __restrict__ g, const float* __restrict__ u,
+                                                            float* __restrict__ o, size_t n) {
+    const size_t i = size_t(blockIdx.x) * kThreads + threadIdx.x;
+    if (i < n) {
+        const float gv = g[i];
+        o[i] = gv / (1.0f + expf(-gv)) * u[i];
+    }
+}
+
+}  // namespace
+
+hipError_t launch_silu_mul(const float* gate, const float* up, float* out, size_t n, hipStream_t stream) {
+    if (!gate || !up || !out || !n) return hipErrorInvalidValue;
+    const dim3 grid(static_cast<uint32_t>((n + kThreads - 1) / kThreads));
+    hipLaunchKernelGGL(silu_mul_kernel, grid, dim3(kThreads), 0, stream, gate, up, out, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_dequantize(int fmt, const uint8_t* w, float* out, size_t rows, size_t cols, hipStream_t stream) {
+    if (!w || !out || !rows || !row_bytes(fmt, cols) || (reinterpret_cast<uintptr_t>(w) & 1u) ||
+        (reinterpret_cast<uintptr_t>(out) & 15u))
+        return hipErrorInvalidValue;
+    const size_t n = rows * (cols / 32);
+    const dim3 grid(static_cast<uint32_t>((n + kThreads - 1) / kThreads));
+    switch (fmt) {
+    case kQ8_0: hipLaunchKernelGGL(dequantize_kernel<kQ8_0>, grid, dim3(kThreads), 0, stream, w, out, rows, cols); break;
+    case kQ4_0: hipLaunchKernelGGL(dequantize_kernel<kQ4_0>, grid, dim3(kThreads), 0, stream, w, out, rows, cols); break;
+    case kQ6_K: hipLaunchKernelGGL(dequantize_kernel<kQ6_K>, grid, dim3(kThreads), 0, stream, w, out, rows, cols); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_synth_weights(int fmt, uint64_t seed, uint8_t* w, size_t rows, size_t cols, hipStream_t stream) {
+    if (!w || !rows || !row_bytes(fmt, cols)) return hipErrorInvalidValue;
+    const size_t nblocks = rows * cols / (fmt == kQ6_K ? 256 : 32);
+    const dim3 grid(static_cast<uint32_t>((nblocks + kThreads - 1) / kThreads));
+    switch (fmt) {
+    case kQ8_0: hipLaunchKernelGGL(synth_kernel<kQ8_0>, grid, dim3(kThreads), 0, stream, seed, w, nblocks); break;
+    case kQ4_0: hipLaunchKernelGGL(synth_kernel<kQ4_0>, grid, dim3(kThreads), 0, stream, seed, w, nblocks); break;
+    case kQ6_K: hipLaunchKernelGGL(synth_kernel<kQ6_K>, grid, dim3(kThreads), 0, stream, seed, w, nblocks); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_synth_normal(uint64_t seed, float* out, size_t n, hipStream_t stream) {
+    if (!out || !n) return hipErrorInvalidValue;
+    const dim3 grid(static_cast<uint32_t>((n + kThreads - 1) / kThreads));
+    hipLaunchKernelGGL(synth_normal_kernel, grid, dim3(kThreads), 0, stream, seed, out, n);
+    return hipGetLastError();
+}
+
+}  // namespace zq

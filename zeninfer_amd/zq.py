@@ -1,0 +1,251 @@
+"""Python binding of the C ABI in include/zq_hip.h (ctypes).
+
+The library must be built (``zeninfer_amd.build``); loading fails loudly when
+it is missing -- there is no CPU fallback on this path.  Host-pointer calls
+take numpy arrays; the *_dev calls take torch tensors (device memory and
+streams only) or raw integer device pointers.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+from .build import LIB
+
+Q4_0, Q8_0, Q6_K = 2, 8, 14
+FORMATS = {"Q4_0": Q4_0, "Q8_0": Q8_0, "Q6_K": Q6_K}
+BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q6_K: (256, 210)}
+ACT_DEFAULT, ACT_INT8, ACT_F32 = 0, 1, 2
+OK, DECLINED = 0, 1
+WEIGHT_TAIL_PAD = 64
+MAX_BATCH = 8
+
+_P = ctypes.c_void_p
+_S = ctypes.c_size_t
+
+
+class ZQError(RuntimeError):
+    def __init__(self, status, what):
+        self.status = status
+        super().__init__(f"{what}: status {status} ({status_string(status)})")
+
+
+class Info(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char * 128), ("arch", ctypes.c_char * 64), ("vram_bytes", ctypes.c_uint64),
+                ("compute_units", ctypes.c_int), ("wave_size", ctypes.c_int), ("lds_per_block", ctypes.c_int),
+                ("clock_khz", ctypes.c_int), ("mem_clock_khz", ctypes.c_int), ("mem_bus_width", ctypes.c_int)]
+
+
+class Stats(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint64) for n in (
+        "dispatches", "submits", "batches", "uploads", "upload_bytes", "resident_bytes", "resident_tensors",
+        "evictions", "declined", "errors", "upload_us", "transfer_us", "wait_us")]
+
+
+class GemvTask(ctypes.Structure):
+    _fields_ = [("weights", _P), ("y", _P), ("rows", _S)]
+
+
+# Every symbol include/zq_hip.h declares, with (restype, argtypes).
+SIGNATURES = {
+    "zq_hip_opted_in": (ctypes.c_int, []),
+    "zq_hip_init": (ctypes.c_int, []),
+    "zq_hip_enabled": (ctypes.c_int, []),
+    "zq_hip_shutdown": (None, []),
+    "zq_hip_get_info": (ctypes.c_int, [ctypes.POINTER(Info)]),
+    "zq_hip_get_stats": (ctypes.c_int, [ctypes.POINTER(Stats)]),
+    "zq_hip_reset_stats": (None, []),
+    "zq_hip_status_string": (ctypes.c_char_p, [ctypes.c_int]),
+    "zq_row_bytes": (_S, [ctypes.c_int, _S]),
+    "zq_weight_bytes": (_S, [ctypes.c_int, _S, _S]),
+    "zq_hip_set_min_elements": (_S, [_S]),
+    "zq_hip_gemv": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _S, _S]),
+    "zq_hip_gemv_batch": (ctypes.c_int, [ctypes.c_int, _P, ctypes.POINTER(GemvTask), _S, _S]),
+    "zq_hip_gemm": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _S, _S, _S, ctypes.c_int]),
+    "zq_hip_ffn_gemv": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _P, _P, _S, _S, _S]),
+    "zq_hip_release": (ctypes.c_int, [_P]),
+    "zq_hip_release_all": (ctypes.c_int, []),
+    "zq_hip_gemv_dev": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _S, _S, _P]),
+    "zq_hip_gemv_batch_dev": (ctypes.c_int, [ctypes.c_int, _P, ctypes.POINTER(GemvTask), _S, _S, _P]),
+    "zq_hip_gemm_workspace_bytes": (_S, [ctypes.c_int, _S, _S, ctypes.c_int]),
+    "zq_hip_gemm_dev": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _S, _S, _S, ctypes.c_int, _P, _S, _P]),
+    "zq_hip_quantize_acts_dev": (ctypes.c_int, [_P, _P, _P, _S, _S, _P]),
+    "zq_hip_block_dots_dev": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _S, _S, _S, _P]),
+    "zq_hip_dequantize_dev": (ctypes.c_int, [ctypes.c_int, _P, _P, _S, _S, _P]),
+    "zq_hip_synth_weights_dev": (ctypes.c_int, [ctypes.c_int, ctypes.c_uint64, _P, _S, _S, _P]),
+    "zq_hip_synth_normal_dev": (ctypes.c_int, [ctypes.c_uint64, _P, _S, _P]),
+}
+
+_lib = None
+
+
+def lib():
+    """The loaded libzq_hip.so; raises when it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB):
+            raise RuntimeError(f"{LIB} is missing: build it with `python -m zeninfer_amd.build` "
+                               "(there is no CPU fallback for this path)")
+        L = ctypes.CDLL(LIB)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def status_string(status):
+    try:
+        return lib().zq_hip_status_string(status).decode()
+    except Exception:  # pragma: no cover - only while the library is missing
+        return "?"
+
+
+def check(status, what):
+    if status != OK:
+        raise ZQError(status, what)
+    return status
+
+
+def _np_ptr(a):
+    return a.ctypes.data_as(_P)
+
+
+def _dptr(t):
+    """Device pointer of a torch tensor or a raw integer address."""
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    return t.data_ptr()
+
+
+def _stream(stream):
+    if stream is None:
+        return None
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream
+
+
+# ---- lifecycle -------------------------------------------------------------
+def init():
+    return lib().zq_hip_init()
+
+
+def info():
+    i = Info()
+    check(lib().zq_hip_get_info(ctypes.byref(i)), "zq_hip_get_info")
+    return {f: (getattr(i, f).decode() if isinstance(getattr(i, f), bytes) else getattr(i, f)) for f, _ in Info._fields_}
+
+
+def stats():
+    s = Stats()
+    check(lib().zq_hip_get_stats(ctypes.byref(s)), "zq_hip_get_stats")
+    return {f: getattr(s, f) for f, _ in Stats._fields_}
+
+
+def reset_stats():
+    lib().zq_hip_reset_stats()
+
+
+def shutdown():
+    lib().zq_hip_shutdown()
+
+
+def row_bytes(fmt, cols):
+    return lib().zq_row_bytes(fmt, cols)
+
+
+def weight_bytes(fmt, rows, cols):
+    return lib().zq_weight_bytes(fmt, rows, cols)
+
+
+def set_min_elements(n):
+    return lib().zq_hip_set_min_elements(n)
+
+
+# ---- host-pointer API (numpy) ---------------------------------------------
+def gemv(fmt, w, x, rows, cols):
+    y = np.empty(rows, np.float32)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    check(lib().zq_hip_gemv(fmt, _np_ptr(w), _np_ptr(x), _np_ptr(y), rows, cols), "zq_hip_gemv")
+    return y
+
+
+def gemv_batch(fmt, ws, x, rows, cols):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    ys = [np.empty(r, np.float32) for r in rows]
+    tasks = (GemvTask * len(ws))(*[GemvTask(w.ctypes.data, y.ctypes.data, r) for w, y, r in zip(ws, ys, rows)])
+    check(lib().zq_hip_gemv_batch(fmt, _np_ptr(x), tasks, len(ws), cols), "zq_hip_gemv_batch")
+    return ys
+
+
+def gemm(fmt, w, X, tokens, rows, cols, act=ACT_DEFAULT):
+    Y = np.empty(tokens * rows, np.float32)
+    X = np.ascontiguousarray(X, dtype=np.float32)
+    check(lib().zq_hip_gemm(fmt, _np_ptr(w), _np_ptr(X), _np_ptr(Y), tokens, rows, cols, act), "zq_hip_gemm")
+    return Y
+
+
+def ffn_gemv(fmt, gate, up, down, x, ffn_rows, cols, out_rows):
+    y = np.empty(out_rows, np.float32)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    check(lib().zq_hip_ffn_gemv(fmt, _np_ptr(gate), _np_ptr(up), _np_ptr(down), _np_ptr(x), _np_ptr(y),
+                                ffn_rows, cols, out_rows), "zq_hip_ffn_gemv")
+    return y
+
+
+def release(w):
+    return lib().zq_hip_release(_np_ptr(w))
+
+
+def release_all():
+    return lib().zq_hip_release_all()
+
+
+# ---- device-pointer API (torch tensors or raw addresses) ------------------
+def gemv_dev(fmt, w, x, y, rows, cols, stream=None):
+    return check(lib().zq_hip_gemv_dev(fmt, _dptr(w), _dptr(x), _dptr(y), rows, cols, _stream(stream)),
+                 "zq_hip_gemv_dev")
+
+
+def gemv_batch_dev(fmt, x, tasks, cols, stream=None):
+    """tasks: list of (weights, y, rows)."""
+    arr = (GemvTask * len(tasks))(*[GemvTask(_dptr(w), _dptr(y), r) for w, y, r in tasks])
+    return check(lib().zq_hip_gemv_batch_dev(fmt, _dptr(x), arr, len(tasks), cols, _stream(stream)),
+                 "zq_hip_gemv_batch_dev")
+
+
+def gemm_workspace_bytes(fmt, tokens, cols, act=ACT_DEFAULT):
+    return lib().zq_hip_gemm_workspace_bytes(fmt, tokens, cols, act)
+
+
+def gemm_dev(fmt, w, X, Y, tokens, rows, cols, act=ACT_DEFAULT, workspace=None, workspace_bytes=0, stream=None):
+    return check(lib().zq_hip_gemm_dev(fmt, _dptr(w), _dptr(X), _dptr(Y), tokens, rows, cols, act,
+                                       _dptr(workspace), workspace_bytes, _stream(stream)), "zq_hip_gemm_dev")
+
+
+def quantize_acts_dev(X, xq, xs, tokens, cols, stream=None):
+    return check(lib().zq_hip_quantize_acts_dev(_dptr(X), _dptr(xq), _dptr(xs), tokens, cols, _stream(stream)),
+                 "zq_hip_quantize_acts_dev")
+
+
+def block_dots_dev(fmt, w, xq, out, tokens, rows, cols, stream=None):
+    return check(lib().zq_hip_block_dots_dev(fmt, _dptr(w), _dptr(xq), _dptr(out), tokens, rows, cols,
+                                             _stream(stream)), "zq_hip_block_dots_dev")
+
+
+def dequantize_dev(fmt, w, out, rows, cols, stream=None):
+    return check(lib().zq_hip_dequantize_dev(fmt, _dptr(w), _dptr(out), rows, cols, _stream(stream)),
+                 "zq_hip_dequantize_dev")
+
+
+def synth_weights_dev(fmt, seed, w, rows, cols, stream=None):
+    return check(lib().zq_hip_synth_weights_dev(fmt, seed, _dptr(w), rows, cols, _stream(stream)),
+                 "zq_hip_synth_weights_dev")
+
+
+def synth_normal_dev(seed, out, n, stream=None):
+    return check(lib().zq_hip_synth_normal_dev(seed, _dptr(out), n, _stream(stream)), "zq_hip_synth_normal_dev")
