@@ -14,14 +14,16 @@ step     One decode token's projections of a Llama-3-8B-shaped model with Q8_0
          HIP graph and replayed.
 value    whole-step algorithmic bytes (weights + x + y per launch) / step time.
 roofline dominant kernel: the Q8_0 GEMV at 4096x14336 (down projection, the
-         north-star target shape), timed per launch with HIP events on the
-         launch stream while the stream is kept busy, rotating over the 32
-         layers' distinct down matrices (2 GB).
+         north-star target shape): 96 back-to-back launches rotating over the
+         32 layers' distinct down matrices (2 GB), bracketed by HIP events on
+         the launch stream (a spin kernel holds the stream while the host
+         queues them), so the average includes the inter-kernel gap.
 secondary int8 prefill GEMM at M=2048, gate/up shape
          14336x4096 and down shape 4096x14336, as TOPS vs the int8 MFMA peak.
 cpu_baseline the reference's own AVX2 ComputePool path (compiled from the
-         reference sources into oracle/_ref) on this host's cores, on one
-         layer's seven projections; falls back to the C oracle if absent.
+         reference sources into oracle/_ref) on this host's cores (up to 16
+         threads, the box's CPU share), on four layers' projections (0.93 GB);
+         falls back to the C oracle if the reference build is absent.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
        python bench.py --summarize-trace kernel_trace.csv   (rocprofv3 helper)
@@ -65,8 +67,9 @@ def summarize_trace(path):
         print(f"{len(d):6d} {np.mean(d) / 1e3:10.2f} {sum(d) / 1e6:10.3f}  {grid} {lds}  {name[:110]}")
 
 
-def cpu_baseline(seconds=8.0):
-    """Reference CPU path (oracle/_ref) on one layer's seven Q8_0 projections."""
+def cpu_baseline(seconds=10.0, layers=4):
+    """Reference CPU path (oracle/_ref) on `layers` layers' seven Q8_0
+    projections each (~0.93 GB, more than a server CPU's last-level cache)."""
     from oracle import oracle as O
     o = O.Oracle()
     kind = "reference"
@@ -76,7 +79,7 @@ def cpu_baseline(seconds=8.0):
             raise RuntimeError("no AVX2")
     except Exception:
         r, kind = None, "port"
-    shapes = [(HIDDEN, HIDDEN), (KV, HIDDEN), (KV, HIDDEN), (HIDDEN, HIDDEN), (FFN, HIDDEN), (FFN, HIDDEN), (HIDDEN, FFN)]
+    shapes = [(HIDDEN, HIDDEN), (KV, HIDDEN), (KV, HIDDEN), (HIDDEN, HIDDEN), (FFN, HIDDEN), (FFN, HIDDEN), (HIDDEN, FFN)] * layers
     ws = [o.gen_weights(O.Q8_0, 0xC0 + i, rr, cc) for i, (rr, cc) in enumerate(shapes)]
     xs = {c: o.gen_normal(0xC1 + c, c) for c in (HIDDEN, FFN)}
     nbytes = sum(gemv_bytes(o.row_bytes(O.Q8_0, c), rr, c) for rr, c in shapes)
@@ -98,7 +101,7 @@ def cpu_baseline(seconds=8.0):
     med = statistics.median(times[1:])
     return {"value": round(nbytes / med / 1e9, 2), "unit": "GB/s", "cores": workers if r is not None else 1,
             "kind": kind,
-            "sample": f"one Llama-3-8B layer's 7 Q8_0 decode GEMVs ({nbytes / 1e6:.1f} MB), "
+            "sample": f"{layers} Llama-3-8B layers' Q8_0 decode GEMVs (7 per layer, {nbytes / 1e6:.1f} MB), "
                       f"{len(times)} passes, median of all but the first; "
                       + ("reference quant::gemv (AVX2 + ComputePool) built from its sources"
                          if r is not None else "scalar C oracle")}
@@ -202,20 +205,25 @@ def main():
     print(f"[bench] step {ms_step:.3f} ms  {value:.1f} GB/s  graph_ok={graph_ok}", file=sys.stderr, flush=True)
 
     # ---- roofline leg: per-launch timing of the 4096 x 14336 down GEMV ----
-    def timed_launches(launch, n):
-        evs = [torch.cuda.Event(enable_timing=True) for _ in range(n + 1)]
-        torch.cuda._sleep(int(2e7))  # keep the stream busy while the launches are queued
-        for i in range(n):
-            evs[i].record()
+    def timed_launches(launch, n, skip):
+        """Average time per launch of n back-to-back launches (after `skip`
+        untimed ones), bracketed by HIP events on the launch stream; a spin
+        kernel keeps the stream busy while the host queues them, so host
+        launch overhead is not in the interval (inter-kernel gaps are)."""
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(int(3e7))
+        for i in range(skip):
             launch(i)
-        evs[n].record()
+        ev0.record()
+        for i in range(skip, skip + n):
+            launch(i)
+        ev1.record()
         torch.cuda.synchronize()
-        per = [evs[i].elapsed_time(evs[i + 1]) for i in range(n)]
-        return per, evs[0].elapsed_time(evs[n]) / n
+        return ev0.elapsed_time(ev1) / n
 
     down_bytes = gemv_bytes(rbf, HIDDEN, FFN)
-    per, _ = timed_launches(lambda i: zq.gemv_dev(Q8, layers[i % LAYERS]["down"], x_f, y_d, HIDDEN, FFN), 4 * LAYERS)
-    down_ms = statistics.mean(per[LAYERS:])  # drop the first rotation
+    down_ms = timed_launches(lambda i: zq.gemv_dev(Q8, layers[i % LAYERS]["down"], x_f, y_d, HIDDEN, FFN),
+                             4 * LAYERS, LAYERS)
     down_gbs = down_bytes / (down_ms * 1e-3) / 1e9
 
     # per-shape GB/s (informational), same method
@@ -224,57 +232,35 @@ def main():
                                      ("gate/up 14336x4096", "gate", FFN, HIDDEN, x_h),
                                      ("down 4096x14336", "down", HIDDEN, FFN, x_f)):
         yb = torch.empty(rows, device=dev)
-        p, _ = timed_launches(lambda i: zq.gemv_dev(Q8, layers[i % LAYERS][key], x, yb, rows, cols), 2 * LAYERS)
-        ms = statistics.mean(p[LAYERS:])
+        ms = timed_launches(lambda i: zq.gemv_dev(Q8, layers[i % LAYERS][key], x, yb, rows, cols), 2 * LAYERS, LAYERS)
         per_shape[name] = {"us": round(ms * 1e3, 2),
                            "GB/s": round(gemv_bytes(zq.row_bytes(Q8, cols), rows, cols) / (ms * 1e-3) / 1e9, 1)}
-    p, _ = timed_launches(lambda i: zq.gemv_dev(Q8, lm_head, x_h, y_lm, VOCAB, HIDDEN), 8)
-    ms = statistics.mean(p[1:])
+    ms = timed_launches(lambda i: zq.gemv_dev(Q8, lm_head, x_h, y_lm, VOCAB, HIDDEN), 8, 1)
     per_shape["lm_head 128256x4096"] = {"us": round(ms * 1e3, 2),
                                         "GB/s": round(gemv_bytes(rbh, VOCAB, HIDDEN) / (ms * 1e-3) / 1e9, 1)}
 
-    # ---- secondary: int8 prefill GEMM at M = 2048 --------------------------
+    # ---- secondary: int8 prefill GEMM at M = 2048 (config 2) ---------------
     M = 2048
-    gemm = {}
     X = torch.empty(M * FFN, device=dev)
     zq.synth_normal_dev(21, X, M * FFN)
+    gemm = {}
     for name, key, N, K in (("gate/up 14336x4096", "gate", FFN, HIDDEN), ("down 4096x14336", "down", HIDDEN, FFN)):
         wsb = zq.gemm_workspace_bytes(Q8, M, K, zq.ACT_INT8)
         ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
         Y = torch.empty(M * N, device=dev)
-        xq = ws[: M * K]
-        xs = ws[((M * K + 255) // 256) * 256:].view(torch.float32)
         Xk = X[: M * K]
-        zq.quantize_acts_dev(Xk, xq, xs, M, K)
-        # GEMM kernel alone (activations already quantised), rotating over 8 layers
-        from zeninfer_amd.zq import lib as _lib
-        L = _lib()
-        sptr = torch.cuda.current_stream().cuda_stream
-
-        def launch(i, key=key, N=N, K=K, Y=Y):
-            st = L.zq_hip_gemm_dev  # noqa: F841 (kept for symmetry)
-            zq.gemm_dev(Q8, layers[i % 8][key], Xk, Y, M, N, K, zq.ACT_INT8, ws, wsb, sptr)
-
-        # full call (quantise + GEMM) per launch
-        per_full, _ = timed_launches(launch, 24)
-        full_ms = statistics.mean(per_full[8:])
+        xq = torch.empty(M * K, dtype=torch.int8, device=dev)
+        xs = torch.empty(M * K // 32, device=dev)
+        full_ms = timed_launches(lambda i: zq.gemm_dev(Q8, layers[i % 8][key], Xk, Y, M, N, K, zq.ACT_INT8, ws, wsb),
+                                 16, 8)
+        q_ms = timed_launches(lambda i: zq.quantize_acts_dev(Xk, xq, xs, M, K), 16, 4)
         ops = 2.0 * M * N * K
-        gemm[name] = {"ms_incl_quantize": round(full_ms, 4),
-                      "TOPS_incl_quantize": round(ops / (full_ms * 1e-3) / 1e12, 1)}
-    # the int8 GEMM kernel alone, via rocprof-comparable per-launch events:
-    # quantise once, then time launch_gemm via the block of GEMM-only calls
-    gemm_kernel = {}
-    for name, key, N, K in (("gate/up 14336x4096", "gate", FFN, HIDDEN),):
-        ops = 2.0 * M * N * K
-        # full-call time minus the quantiser's own time, measured alone
-        qx = torch.empty(M * K, dtype=torch.int8, device=dev)
-        qs = torch.empty(M * K // 32, device=dev)
-        pq, _ = timed_launches(lambda i: zq.quantize_acts_dev(X[: M * K], qx, qs, M, K), 16)
-        q_ms = statistics.mean(pq[4:])
-        k_ms = gemm[name]["ms_incl_quantize"] - q_ms
-        gemm_kernel = {"shape": f"M={M} N={N} K={K}", "gemm_ms": round(k_ms, 4), "quantize_ms": round(q_ms, 4),
-                       "TOPS": round(ops / (k_ms * 1e-3) / 1e12, 1),
-                       "frac_int8_peak": round(ops / (k_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4)}
+        k_ms = full_ms - q_ms
+        gemm[name] = {"shape": f"M={M} N={N} K={K}", "ms_per_call": round(full_ms, 4), "quantize_ms": round(q_ms, 4),
+                      "gemm_ms": round(k_ms, 4),
+                      "TOPS_per_call": round(ops / (full_ms * 1e-3) / 1e12, 1),
+                      "TOPS_gemm": round(ops / (k_ms * 1e-3) / 1e12, 1),
+                      "frac_int8_peak": round(ops / (k_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4)}
 
     cpu = None
     if not args.no_cpu:
@@ -302,11 +288,11 @@ def main():
                    "frac_hbm_peak_step": round(value / HBM_PEAK_GBS, 4), "graph_matches_eager": graph_ok},
         "roofline": {"bound": "hbm", "achieved": round(down_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(down_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "gemv_pairs_kernel<Q8_0> at 4096x14336 (down projection)",
+                     "kernel": "gemv_stream_kernel<Q8_0> (4 column slices x 16 waves) at 4096x14336, the down projection",
                      "avg_launch_us": round(down_ms * 1e3, 2), "algorithmic_bytes_per_launch": down_bytes},
         "per_shape_gemv": per_shape,
-        "secondary": {"prefill_gemm_int8_M2048": gemm, "gemm_kernel": gemm_kernel,
-                      "int8_peak_tops": INT8_PEAK_TOPS},
+        "secondary": {"metric": "prefill GEMM int8 TOPS (% MFMA peak), config 2 at M=2048",
+                      "prefill_gemm_int8_M2048": gemm, "int8_peak_tops": INT8_PEAK_TOPS},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out))

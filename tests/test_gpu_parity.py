@@ -45,7 +45,8 @@ def test_dequantize_bit_exact(zq, orc, fmt, rows, cols):
     # force binary16 subnormal and special scales into a few blocks
     bb = O.BLOCK[fmt][1]
     soff = 208 if fmt == O.Q6_K else 0
-    for i, h in enumerate((0x0001, 0x03FF, 0x8400, 0x0000)):
+    nblk = w.size // bb
+    for i, h in enumerate((0x0001, 0x03FF, 0x8400, 0x0000)[:nblk]):
         w[i * bb + soff], w[i * bb + soff + 1] = h & 0xFF, h >> 8
     out = torch.empty(rows * cols, dtype=torch.float32, device=DEV)
     zq.dequantize_dev(fmt, dev_weights(zq, fmt, w, rows, cols), out, rows, cols)
@@ -242,7 +243,7 @@ def test_residency_and_release(zq, orc):
     assert s["uploads"] == 1 and s["submits"] == 2 and s["resident_tensors"] == 1
     assert np.array_equal(y1, y2)
     # same address, same shape: not re-read (the documented contract) until released
-    w[:34] = 0
+    w[: zq.row_bytes(O.Q8_0, 1024)] = 0   # zero row 0 entirely
     y3 = zq.gemv(O.Q8_0, w, x, 256, 1024)
     assert np.array_equal(y3, y1)
     assert zq.release(w) == 0
@@ -273,7 +274,10 @@ def test_ffn_gemv(zq, orc):
     y = zq.ffn_gemv(O.Q8_0, g, u, d, x, ffn, cols, out)
     gv = orc.gemv_f32(O.Q8_0, g, x, ffn, cols).astype(np.float64)
     uv = orc.gemv_f32(O.Q8_0, u, x, ffn, cols).astype(np.float64)
-    act = (gv / (1 + np.exp(-gv)) * uv).astype(np.float32)
-    want = orc.gemv_f32(O.Q8_0, d, act, out, ffn)
-    # SiLU is a transcendental: compare at the GEMV bar scaled by the input size
-    assert np.max(np.abs(y - want) / (1e-3 + np.abs(want))) < 1e-3
+    act = gv / (1 + np.exp(-gv)) * uv
+    dd = orc.dequantize(O.Q8_0, d, out * ffn).reshape(out, ffn).astype(np.float64)
+    want = dd @ act
+    # SiLU goes through expf: bound the error by the sum of |terms| of the down
+    # projection (the GEMV bar relative to the magnitude that is summed)
+    mag = np.abs(dd) @ np.abs(act)
+    assert np.all(np.abs(y - want) <= 1e-4 + 1e-5 * mag), np.max(np.abs(y - want) / (1e-4 + 1e-5 * mag))

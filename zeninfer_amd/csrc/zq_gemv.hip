@@ -51,6 +51,11 @@ struct TaskTable {
     int count;
 };
 
+#ifndef ZQ_GEMV_NT
+#define ZQ_GEMV_NT 0
+#endif
+__device__ __forceinline__ constexpr bool use_nt() { return ZQ_GEMV_NT != 0; }
+
 constexpr int kThreads = 256;
 constexpr int kWavesPerBlock = kThreads / kWave;
 constexpr int kPadStride = 68;  // floats per 64-float x chunk in LDS
@@ -164,7 +169,7 @@ __global__ __launch_bounds__(kThreads) void gemv_pairs_kernel(TaskTable tt, cons
             for (int r = 0; r < R; ++r) {
                 const uint32_t* src = reinterpret_cast<const uint32_t*>(rowp[r] + (size_t)p * DW * 4);
 #pragma unroll
-                for (int i = 0; i < DW; ++i) q[r][i] = __builtin_nontemporal_load(src + i);
+                for (int i = 0; i < DW; ++i) q[r][i] = use_nt() ? __builtin_nontemporal_load(src + i) : src[i];
             }
             float xv[64];
             const float4* xp = reinterpret_cast<const float4*>(xs + p * kPadStride);
@@ -184,6 +189,280 @@ __global__ __launch_bounds__(kThreads) void gemv_pairs_kernel(TaskTable tt, cons
             const float v = wave_sum(acc[r]);
             if (lane == r && r0 + r < task.rows) task.y[r0 + r] = v;
         }
+    }
+}
+
+// x-in-registers pair kernel (cols % 64 == 0, up to 256 pairs = 16384 cols).
+// A row is split into S column slices of W = ceil(pairs/S) <= 64 pairs; a
+// "team" of S waves covers one row, wave s owning slice s, and lane L of it
+// owning pair s*W + L for every row the kernel visits.  So each lane loads
+// its 64 x values ONCE (from LDS when S == 1, where the workgroup's four
+// waves share one staged copy; straight from global memory otherwise) and
+// keeps them in VGPRs, and the loop body only streams weights: R rows x DW
+// dwords per lane per iteration, software-pipelined one iteration ahead.
+// The workgroup walks row blocks of RB = (4/S)*R rows with a grid-stride
+// loop whose trip count is uniform across the workgroup, so the S > 1
+// cross-wave reduction can use __syncthreads (double-buffered by parity).
+template <int FMT, int R, int S>
+__global__ __launch_bounds__(kThreads) void gemv_xreg_kernel(TaskTable tt, const float* __restrict__ x,
+                                                             uint32_t cols, uint32_t total_blocks) {
+    constexpr int DW = FMT == kQ8_0 ? 17 : 9;
+    constexpr int TEAMS = kWavesPerBlock / S;
+    extern __shared__ float xs[];
+    __shared__ float red[2][kWavesPerBlock][R];
+    const uint32_t pairs = cols >> 6;
+    const uint32_t W = (pairs + S - 1) / S;
+    const uint32_t rb = pairs * DW * 4;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int team = wave / S, slice = wave % S;
+    const uint32_t p = slice * W + lane;
+    const bool active = uint32_t(lane) < W && p < pairs;
+
+    // row block -> (task, first row of this team)
+    auto locate = [&](uint32_t blk, const uint8_t*(&rowp)[R], uint32_t& row0, int& ti) {
+        ti = find_task(tt, blk);
+        const GemvTask& t = tt.t[ti];
+        row0 = (blk - tt.group_start[ti]) * (TEAMS * R) + team * R;
+#pragma unroll
+        for (int r = 0; r < R; ++r) rowp[r] = t.w + (size_t)min(row0 + r, t.rows - 1) * rb + (size_t)p * DW * 4;
+    };
+    auto load = [&](const uint8_t*(&rowp)[R], uint32_t (&q)[R][DW]) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint32_t* src = reinterpret_cast<const uint32_t*>(rowp[r]);
+#pragma unroll
+            for (int i = 0; i < DW; ++i) q[r][i] = active ? (use_nt() ? __builtin_nontemporal_load(src + i) : src[i]) : 0u;
+        }
+    };
+
+    uint32_t blk = blockIdx.x;
+    uint32_t q[R][DW];
+    const uint8_t* rowp[R];
+    uint32_t row0 = 0;
+    int ti = 0;
+    if (blk < total_blocks) {
+        locate(blk, rowp, row0, ti);
+        load(rowp, q);  // weight loads go out before x is fetched
+    }
+    float xv[64];
+    if constexpr (S == 1) {
+        for (uint32_t i = threadIdx.x; i < (cols >> 2); i += kThreads) {
+            const float4 v = reinterpret_cast<const float4*>(x)[i];
+            *reinterpret_cast<float4*>(xs + (i >> 4) * kPadStride + ((i & 15u) << 2)) = v;
+        }
+        __syncthreads();
+        const float4* xp = reinterpret_cast<const float4*>(xs + (active ? p : 0) * kPadStride);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float4 v = xp[i];
+            xv[4 * i] = v.x; xv[4 * i + 1] = v.y; xv[4 * i + 2] = v.z; xv[4 * i + 3] = v.w;
+        }
+    } else {
+        const float4* xp = reinterpret_cast<const float4*>(x + (size_t)(active ? p : 0) * 64);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float4 v = xp[i];
+            xv[4 * i] = v.x; xv[4 * i + 1] = v.y; xv[4 * i + 2] = v.z; xv[4 * i + 3] = v.w;
+        }
+    }
+    int parity = 0;
+    while (blk < total_blocks) {
+        const uint32_t nblk = blk + gridDim.x;
+        uint32_t qn[R][DW];
+        const uint8_t* rowpn[R];
+        uint32_t row0n = 0;
+        int tin = 0;
+        if (nblk < total_blocks) {
+            locate(nblk, rowpn, row0n, tin);
+            load(rowpn, qn);
+        }
+        float acc[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            if constexpr (FMT == kQ8_0) acc[r] = q8_pair_dot(q[r], xv);
+            else acc[r] = q4_pair_dot(q[r], xv);
+            acc[r] = wave_sum(acc[r]);
+        }
+        const GemvTask& t = tt.t[ti];
+        if constexpr (S == 1) {
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                if (lane == r && row0 + r < t.rows) t.y[row0 + r] = acc[r];
+        } else {
+            if (lane == 0) {
+#pragma unroll
+                for (int r = 0; r < R; ++r) red[parity][wave][r] = acc[r];
+            }
+            __syncthreads();
+            if (slice == 0 && lane < R) {
+                float v = 0.0f;
+#pragma unroll
+                for (int s2 = 0; s2 < S; ++s2) v += red[parity][team * S + s2][lane];
+                if (row0 + lane < t.rows) t.y[row0 + lane] = v;
+            }
+            parity ^= 1;
+        }
+        blk = nblk;
+        if (blk < total_blocks) {
+            row0 = row0n;
+            ti = tin;
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int i = 0; i < DW; ++i) q[r][i] = qn[r][i];
+        }
+    }
+}
+
+// Coalesced streaming pair kernel: the x-in-registers organisation of
+// gemv_xreg_kernel, but weights are fetched with lane-contiguous dwordx4
+// loads (each load instruction covers 1 KiB of consecutive bytes) into a
+// per-wave LDS buffer, and every lane then reads its own pair back with DW
+// ds_read_b32 at a DW-dword stride (17 or 9: odd, so the 64 lanes hit 64
+// distinct banks).  Requires the slice-row byte ranges to be 16 B aligned:
+// cols % 256 == 0 and a 16 B aligned weight base.  The next row block's
+// loads are issued before the current block is decoded.
+template <int FMT, int R, int S, int NW>
+__global__ __launch_bounds__(NW * 64) void gemv_stream_kernel(TaskTable tt, const float* __restrict__ x,
+                                                               uint32_t cols, uint32_t total_blocks) {
+    constexpr int DW = FMT == kQ8_0 ? 17 : 9;
+    constexpr int NT = NW * 64;
+    constexpr int TEAMS = NW / S;
+    constexpr int UMAX = 64 * DW / 4;        // 16 B units of a full 64-pair slice-row
+    constexpr int NU = (UMAX + 63) / 64;     // dwordx4 loads per lane per row
+    constexpr int WBUF = 64 * DW;            // dwords per slice-row buffer
+    extern __shared__ uint32_t lds[];        // [waves][R][WBUF] then (S == 1) the padded x
+    __shared__ float red[2][NW][R];
+    const uint32_t pairs = cols >> 6;
+    const uint32_t W = min(64u, (((pairs + S - 1) / S) + 3u) & ~3u);
+    const uint32_t rb = pairs * DW * 4;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int team = wave / S, slice = wave % S;
+    const uint32_t p0 = slice * W;
+    const uint32_t np = p0 < pairs ? min(W, pairs - p0) : 0u;   // pairs in this wave's slice (multiple of 4)
+    const uint32_t nunits = np * DW / 4;
+    const bool active = uint32_t(lane) < np;
+    uint32_t* buf = lds + wave * (R * WBUF);
+    float* xs = reinterpret_cast<float*>(lds + NW * R * WBUF);
+
+    auto locate = [&](uint32_t blk, const uint8_t*(&rowp)[R], uint32_t& row0, int& ti) {
+        ti = find_task(tt, blk);
+        const GemvTask& t = tt.t[ti];
+        row0 = (blk - tt.group_start[ti]) * (TEAMS * R) + team * R;
+#pragma unroll
+        for (int r = 0; r < R; ++r) rowp[r] = t.w + (size_t)min(row0 + r, t.rows - 1) * rb + (size_t)p0 * DW * 4;
+    };
+    auto load = [&](const uint8_t*(&rowp)[R], uint4 (&u)[R][NU]) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint4* src = reinterpret_cast<const uint4*>(rowp[r]);
+#pragma unroll
+            for (int i = 0; i < NU; ++i) {
+                const uint32_t unit = lane + 64 * i;
+                u[r][i] = unit < nunits ? src[unit]
+                                        : make_uint4(0, 0, 0, 0);
+            }
+        }
+    };
+    auto stash = [&](const uint4 (&u)[R][NU]) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int i = 0; i < NU; ++i) {
+                const uint32_t unit = lane + 64 * i;
+                if (unit < uint32_t(UMAX)) reinterpret_cast<uint4*>(buf + r * WBUF)[unit] = u[r][i];
+            }
+    };
+
+    uint32_t blk = blockIdx.x;
+    uint4 u[R][NU];
+    const uint8_t* rowp[R];
+    uint32_t row0 = 0;
+    int ti = 0;
+    if (blk < total_blocks) {
+        locate(blk, rowp, row0, ti);
+        load(rowp, u);
+    }
+    float xv[64];
+    const uint32_t p = p0 + lane;
+    if constexpr (S == 1) {
+        for (uint32_t i = threadIdx.x; i < (cols >> 2); i += NT) {
+            const float4 v = reinterpret_cast<const float4*>(x)[i];
+            *reinterpret_cast<float4*>(xs + (i >> 4) * kPadStride + ((i & 15u) << 2)) = v;
+        }
+        __syncthreads();
+        const float4* xp = reinterpret_cast<const float4*>(xs + (active ? p : 0) * kPadStride);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float4 v = xp[i];
+            xv[4 * i] = v.x; xv[4 * i + 1] = v.y; xv[4 * i + 2] = v.z; xv[4 * i + 3] = v.w;
+        }
+    } else if constexpr (NW > S) {
+        // several teams share the slices: stage x once per workgroup
+        for (uint32_t i = threadIdx.x; i < (cols >> 2); i += NT) {
+            const float4 v = reinterpret_cast<const float4*>(x)[i];
+            *reinterpret_cast<float4*>(xs + (i >> 4) * kPadStride + ((i & 15u) << 2)) = v;
+        }
+        __syncthreads();
+        const float4* xp = reinterpret_cast<const float4*>(xs + (active ? p : 0) * kPadStride);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float4 v = xp[i];
+            xv[4 * i] = v.x; xv[4 * i + 1] = v.y; xv[4 * i + 2] = v.z; xv[4 * i + 3] = v.w;
+        }
+    } else {
+        const float4* xp = reinterpret_cast<const float4*>(x + (size_t)(active ? p : 0) * 64);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float4 v = xp[i];
+            xv[4 * i] = v.x; xv[4 * i + 1] = v.y; xv[4 * i + 2] = v.z; xv[4 * i + 3] = v.w;
+        }
+    }
+    int parity = 0;
+    while (blk < total_blocks) {
+        stash(u);
+        const uint32_t nblk = blk + gridDim.x;
+        const uint8_t* rowpn[R];
+        uint32_t row0n = 0;
+        int tin = 0;
+        if (nblk < total_blocks) {
+            locate(nblk, rowpn, row0n, tin);
+            load(rowpn, u);
+        }
+        float acc[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            uint32_t q[DW];
+#pragma unroll
+            for (int j = 0; j < DW; ++j) q[j] = active ? buf[r * WBUF + DW * lane + j] : 0u;
+            if constexpr (FMT == kQ8_0) acc[r] = q8_pair_dot(q, xv);
+            else acc[r] = q4_pair_dot(q, xv);
+            acc[r] = wave_sum(acc[r]);
+        }
+        const GemvTask& t = tt.t[ti];
+        if constexpr (S == 1) {
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                if (lane == r && row0 + r < t.rows) t.y[row0 + r] = acc[r];
+        } else {
+            if (lane == 0) {
+#pragma unroll
+                for (int r = 0; r < R; ++r) red[parity][wave][r] = acc[r];
+            }
+            __syncthreads();
+            if (slice == 0 && lane < R) {
+                float v = 0.0f;
+#pragma unroll
+                for (int s2 = 0; s2 < S; ++s2) v += red[parity][team * S + s2][lane];
+                if (row0 + lane < t.rows) t.y[row0 + lane] = v;
+            }
+            parity ^= 1;
+        }
+        blk = nblk;
+        row0 = row0n;
+        ti = tin;
     }
 }
 
@@ -304,6 +583,17 @@ int rows_per_wave(uint32_t total_rows) {
     return 1;
 }
 
+int xreg_rows(uint32_t total_rows) {
+    static const int forced = [] {
+        const char* e = getenv("ZQ_GEMV_ROWS_PER_WAVE");
+        const int v = e ? atoi(e) : 0;
+        return (v == 1 || v == 2 || v == 4) ? v : 0;
+    }();
+    if (forced) return forced;
+    (void)total_rows;
+    return 1;
+}
+
 template <int FMT, int R>
 hipError_t launch_pairs(TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream) {
     uint32_t groups = 0;
@@ -317,6 +607,109 @@ hipError_t launch_pairs(TaskTable& tt, const float* x, uint32_t cols, hipStream_
     hipLaunchKernelGGL((gemv_pairs_kernel<FMT, R>), dim3(blocks), dim3(kThreads), lds, stream, tt, x, cols, groups);
     return hipGetLastError();
 }
+// LDS budget of one workgroup for the staged activation vector.
+size_t lds_limit() {
+    static const size_t limit = [] {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) != hipSuccess) return size_t(65536);
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0)
+            return size_t(65536);
+        return size_t(v);
+    }();
+    return limit;
+}
+
+int cu_count() {
+    static const int n = [] {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
+            return 256;
+        return v;
+    }();
+    return n;
+}
+int wg_per_cu() {
+    static const int v = [] {
+        const char* e = getenv("ZQ_GEMV_WG_PER_CU");
+        const int k = e ? atoi(e) : 0;
+        return (k >= 1 && k <= 64) ? k : 4;
+    }();
+    return v;
+}
+
+template <int FMT, int R, int S, int NW>
+hipError_t launch_stream(TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream) {
+    constexpr uint32_t RB = (NW / S) * R;
+    constexpr int DW = FMT == kQ8_0 ? 17 : 9;
+    uint32_t blocks = 0;
+    for (int i = 0; i < tt.count; ++i) {
+        tt.group_start[i] = blocks;
+        blocks += (tt.t[i].rows + RB - 1) / RB;
+    }
+    tt.group_start[tt.count] = blocks;
+    const uint32_t grid = std::min<uint32_t>(blocks, uint32_t(cu_count() * (NW == 16 ? 1 : wg_per_cu())));
+    size_t lds = size_t(NW) * R * 64 * DW * 4;
+    if (S == 1 || NW > S) lds += size_t(cols >> 6) * kPadStride * sizeof(float);
+    if (lds > lds_limit()) return hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL((gemv_stream_kernel<FMT, R, S, NW>), dim3(grid), dim3(NW * 64), lds, stream, tt, x, cols, blocks);
+    return hipGetLastError();
+}
+int stream_waves() {
+    static const int v = [] {
+        const char* e = getenv("ZQ_GEMV_WAVES");
+        const int k = e ? atoi(e) : 0;
+        return (k == 4 || k == 16) ? k : 16;
+    }();
+    return v;
+}
+template <int FMT, int S>
+hipError_t launch_stream_r(int R, TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream) {
+    if (stream_waves() == 16) {
+        hipError_t e = hipErrorInvalidConfiguration;
+        if (R == 2) e = launch_stream<FMT, 2, S, 16>(tt, x, cols, stream);
+        if (e == hipErrorInvalidConfiguration) e = launch_stream<FMT, 1, S, 16>(tt, x, cols, stream);
+        if (e != hipErrorInvalidConfiguration) return e;
+    }
+    if (R == 4) return launch_stream<FMT, 4, S, 4>(tt, x, cols, stream);
+    if (R == 2) return launch_stream<FMT, 2, S, 4>(tt, x, cols, stream);
+    return launch_stream<FMT, 1, S, 4>(tt, x, cols, stream);
+}
+template <int FMT>
+hipError_t launch_stream_any(int R, TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream) {
+    const uint32_t pairs = cols >> 6;
+    if (pairs <= 64) return launch_stream_r<FMT, 1>(R, tt, x, cols, stream);
+    if (pairs <= 128) return launch_stream_r<FMT, 2>(R, tt, x, cols, stream);
+    return launch_stream_r<FMT, 4>(R, tt, x, cols, stream);
+}
+
+template <int FMT, int R, int S>
+hipError_t launch_xreg(TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream) {
+    constexpr uint32_t RB = (kWavesPerBlock / S) * R;
+    uint32_t blocks = 0;
+    for (int i = 0; i < tt.count; ++i) {
+        tt.group_start[i] = blocks;
+        blocks += (tt.t[i].rows + RB - 1) / RB;
+    }
+    tt.group_start[tt.count] = blocks;
+    const uint32_t grid = std::min<uint32_t>(blocks, uint32_t(cu_count() * wg_per_cu()));
+    const size_t lds = S == 1 ? size_t(cols >> 6) * kPadStride * sizeof(float) : 0;
+    hipLaunchKernelGGL((gemv_xreg_kernel<FMT, R, S>), dim3(grid), dim3(kThreads), lds, stream, tt, x, cols, blocks);
+    return hipGetLastError();
+}
+template <int FMT, int S>
+hipError_t launch_xreg_r(int R, TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream) {
+    if (R == 4) return launch_xreg<FMT, 4, S>(tt, x, cols, stream);
+    if (R == 2) return launch_xreg<FMT, 2, S>(tt, x, cols, stream);
+    return launch_xreg<FMT, 1, S>(tt, x, cols, stream);
+}
+template <int FMT>
+hipError_t launch_xreg_any(int R, TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream) {
+    const uint32_t pairs = cols >> 6;
+    if (pairs <= 64) return launch_xreg_r<FMT, 1>(R, tt, x, cols, stream);
+    if (pairs <= 128) return launch_xreg_r<FMT, 2>(R, tt, x, cols, stream);
+    return launch_xreg_r<FMT, 4>(R, tt, x, cols, stream);
+}
+
 template <int R>
 hipError_t launch_q6k(TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream) {
     uint32_t groups = 0;
@@ -345,18 +738,6 @@ hipError_t launch_blocks(TaskTable& tt, const float* x, uint32_t cols, hipStream
 
 }  // namespace
 
-// LDS budget of one workgroup for the staged activation vector.
-static size_t lds_limit() {
-    static const size_t limit = [] {
-        int dev = 0, v = 0;
-        if (hipGetDevice(&dev) != hipSuccess) return size_t(65536);
-        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0)
-            return size_t(65536);
-        return size_t(v);
-    }();
-    return limit;
-}
-
 hipError_t launch_gemv(int fmt, const GemvTask* tasks, int count, const float* x, size_t cols,
                        hipStream_t stream) {
     if (count < 1 || count > kMaxTasks || !x || !row_bytes(fmt, cols) || cols > (1u << 24))
@@ -380,6 +761,21 @@ hipError_t launch_gemv(int fmt, const GemvTask* tasks, int count, const float* x
         if (R == 4) return launch_q6k<4>(tt, x, c, stream);
         if (R == 2) return launch_q6k<2>(tt, x, c, stream);
         return launch_q6k<1>(tt, x, c, stream);
+    }
+    static const int kernel_choice = [] {  // 's' stream (default), 'x' xreg, 'l' legacy
+        const char* e = getenv("ZQ_GEMV_KERNEL");
+        return e ? int(e[0]) : int('s');
+    }();
+    const bool x16 = (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+    bool w16 = true;
+    for (int i = 0; i < count; ++i) w16 = w16 && (reinterpret_cast<uintptr_t>(tasks[i].w) & 15u) == 0;
+    if (kernel_choice == 's' && w16 && x16 && c % 256 == 0 && c / 64 <= 256) {
+        const int Rx = xreg_rows(total_rows);
+        return fmt == kQ8_0 ? launch_stream_any<kQ8_0>(Rx, tt, x, c, stream) : launch_stream_any<kQ4_0>(Rx, tt, x, c, stream);
+    }
+    if (kernel_choice != 'l' && aligned && x16 && c % 64 == 0 && c / 64 <= 256) {
+        const int Rx = xreg_rows(total_rows);
+        return fmt == kQ8_0 ? launch_xreg_any<kQ8_0>(Rx, tt, x, c, stream) : launch_xreg_any<kQ4_0>(Rx, tt, x, c, stream);
     }
     const bool pairs_ok = aligned && (c % 64 == 0) && size_t(c / 64) * kPadStride * 4 <= lds_limit();
     if (!pairs_ok) return fmt == kQ8_0 ? launch_blocks<kQ8_0>(tt, x, c, stream) : launch_blocks<kQ4_0>(tt, x, c, stream);

@@ -83,10 +83,11 @@ def lib():
     """The loaded libzq_hip.so; raises when it has not been built."""
     global _lib
     if _lib is None:
-        if not os.path.exists(LIB):
-            raise RuntimeError(f"{LIB} is missing: build it with `python -m zeninfer_amd.build` "
+        path = os.environ.get("ZQ_HIP_LIB", LIB)  # alternate build of the same library (A/B runs)
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} is missing: build it with `python -m zeninfer_amd.build` "
                                "(there is no CPU fallback for this path)")
-        L = ctypes.CDLL(LIB)
+        L = ctypes.CDLL(path)
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(L, name)
             fn.restype = res
