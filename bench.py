@@ -245,7 +245,7 @@ def main():
     zq.synth_normal_dev(21, X, M * FFN)
     gemm = {}
     for name, key, N, K in (("gate/up 14336x4096", "gate", FFN, HIDDEN), ("down 4096x14336", "down", HIDDEN, FFN)):
-        wsb = zq.gemm_workspace_bytes(Q8, M, K, zq.ACT_INT8)
+        wsb = zq.gemm_workspace_bytes(Q8, M, N, K, zq.ACT_INT8)
         ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
         Y = torch.empty(M * N, device=dev)
         Xk = X[: M * K]

@@ -50,9 +50,12 @@ def test_argument_errors_without_device():
     assert L.zq_hip_gemm(zq.Q8_0, None, None, None, 1, 4, 64, 0) == -1
     assert L.zq_hip_gemv_dev(zq.Q8_0, 0, 0, 0, 4, 100, None) == -1
     assert zq.status_string(1) == "declined"
-    assert L.zq_hip_gemm_workspace_bytes(zq.Q8_0, 4, 4096, zq.ACT_INT8) == 4 * 4096 + 4 * 128 * 4
-    assert L.zq_hip_gemm_workspace_bytes(zq.Q8_0, 4, 4096, zq.ACT_F32) == 0
-    assert L.zq_hip_gemm_workspace_bytes(zq.Q6_K, 4, 4096, zq.ACT_DEFAULT) == 0
+    # int8 activations + scales (256-byte aligned sections) + split-K partials for small grids
+    ws = L.zq_hip_gemm_workspace_bytes(zq.Q8_0, 4, 4096, 4096, zq.ACT_INT8)
+    assert ws >= 4 * 4096 + 4 * 128 * 4 and ws % 4 == 0
+    assert L.zq_hip_gemm_workspace_bytes(zq.Q8_0, 2048, 14336, 4096, zq.ACT_INT8) == 2048 * 4096 + 2048 * 128 * 4
+    assert L.zq_hip_gemm_workspace_bytes(zq.Q8_0, 4, 4096, 4096, zq.ACT_F32) == 0
+    assert L.zq_hip_gemm_workspace_bytes(zq.Q6_K, 4, 4096, 4096, zq.ACT_DEFAULT) == 0
 
 
 def test_opt_in_semantics(monkeypatch):

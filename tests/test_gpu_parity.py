@@ -208,7 +208,7 @@ def test_gemm_full_size_sampled(zq, orc):
     zq.synth_weights_dev(O.Q8_0, 81, wd, n, k)
     X = orc.gen_normal(82, m * k)
     Y = torch.empty(m * n, device=DEV)
-    ws_bytes = zq.gemm_workspace_bytes(O.Q8_0, m, k, zq.ACT_INT8)
+    ws_bytes = zq.gemm_workspace_bytes(O.Q8_0, m, n, k, zq.ACT_INT8)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=DEV)
     zq.gemm_dev(O.Q8_0, wd, to_dev(X), Y, m, n, k, zq.ACT_INT8, ws, ws_bytes)
     Yh = Y.cpu().numpy().reshape(m, n)

@@ -198,13 +198,15 @@ int enqueue_gemm(int fmt, const uint8_t* w, const float* X, float* Y, size_t tok
                  void* ws, size_t ws_bytes, hipStream_t s, uint64_t* dispatches) {
     if (act == ZQ_ACT_INT8) {
         const size_t qbytes = align_up(tokens * cols, 256);
-        const size_t need = qbytes + tokens * (cols / 32) * sizeof(float);
-        if (!ws || ws_bytes < need) return ZQ_ERR_ARG;
+        const size_t sbytes = align_up(tokens * (cols / 32) * sizeof(float), 256);
+        const size_t pbytes = zq::gemm_i8_partial_bytes(tokens, rows, cols);
+        if (!ws || ws_bytes < qbytes + sbytes + pbytes) return ZQ_ERR_ARG;
         int8_t* xq = static_cast<int8_t*>(ws);
         float* xs = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + qbytes);
+        float* part = pbytes ? reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + qbytes + sbytes) : nullptr;
         if (zq::launch_quantize_acts(X, xq, xs, tokens, cols, s) != hipSuccess) return ZQ_ERR_HIP;
-        if (zq::launch_gemm_i8(fmt, w, xq, xs, Y, tokens, rows, cols, s) != hipSuccess) return ZQ_ERR_HIP;
-        *dispatches += 2;
+        if (zq::launch_gemm_i8(fmt, w, xq, xs, Y, part, tokens, rows, cols, s) != hipSuccess) return ZQ_ERR_HIP;
+        *dispatches += pbytes ? 3 : 2;
         return ZQ_OK;
     }
     if (zq::launch_gemm_f32(fmt, w, X, Y, tokens, rows, cols, s) != hipSuccess) return ZQ_ERR_HIP;
@@ -400,7 +402,7 @@ int zq_hip_gemm(int fmt, const uint8_t* weights, const float* X, float* Y, size_
         if (st != ZQ_OK) return st;
         const size_t xbytes = align_up(tokens * cols * sizeof(float), 256);
         const size_t ybytes = align_up(tokens * rows * sizeof(float), 256);
-        const size_t wsbytes = zq_hip_gemm_workspace_bytes(fmt, tokens, cols, act);
+        const size_t wsbytes = zq_hip_gemm_workspace_bytes(fmt, tokens, rows, cols, act);
         st = ensure_scratch(b, xbytes + ybytes + wsbytes, xbytes + ybytes);
         if (st != ZQ_OK) return st;
         uint8_t* base = static_cast<uint8_t*>(b.dev_scratch);
@@ -541,10 +543,11 @@ int zq_hip_gemv_dev(int fmt, const void* weights, const float* x, float* y, size
     return zq_hip_gemv_batch_dev(fmt, x, &t, 1, cols, stream);
 }
 
-size_t zq_hip_gemm_workspace_bytes(int fmt, size_t tokens, size_t cols, int act_mode) {
-    if (!valid_fmt(fmt) || !zq::row_bytes(fmt, cols)) return 0;
+size_t zq_hip_gemm_workspace_bytes(int fmt, size_t tokens, size_t rows, size_t cols, int act_mode) {
+    if (!valid_fmt(fmt) || !zq::row_bytes(fmt, cols) || !tokens || !rows) return 0;
     if (resolve_act(fmt, act_mode) != ZQ_ACT_INT8) return 0;
-    return align_up(tokens * cols, 256) + tokens * (cols / 32) * sizeof(float);
+    return align_up(tokens * cols, 256) + align_up(tokens * (cols / 32) * sizeof(float), 256) +
+           zq::gemm_i8_partial_bytes(tokens, rows, cols);
 }
 
 int zq_hip_gemm_dev(int fmt, const void* weights, const float* X, float* Y, size_t tokens, size_t rows, size_t cols,

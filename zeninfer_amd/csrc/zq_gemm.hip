@@ -26,6 +26,9 @@
 #include "zq_device.hpp"
 #include "zq_internal.hpp"
 
+#include <algorithm>
+#include <cstdlib>
+
 namespace zq {
 namespace {
 
@@ -36,7 +39,7 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 constexpr int kThreads = 256;
 constexpr int BM = 128;             // tokens per tile
 constexpr int BN = 128;             // weight rows per tile
-constexpr int KB = 4;               // 32-element blocks per K stage
+constexpr int KB = 8;               // 32-element blocks per K stage
 constexpr int ROWB = KB * 32 + 16;  // LDS bytes per tile row (16 B pad)
 
 // ------------------------------------------------- activation quantiser ---
@@ -85,94 +88,160 @@ __global__ __launch_bounds__(kThreads) void quantize_acts_kernel(const float* __
 }
 
 // ------------------------------------------------------- tile mapping ---
-__device__ __forceinline__ void tile_of(uint32_t tiles_m, uint32_t tiles_n, uint32_t& tm, uint32_t& tn) {
+__device__ __forceinline__ void tile_of(uint32_t tiles_m, uint32_t tiles_n, uint32_t id, uint32_t& tm, uint32_t& tn) {
     const uint32_t total = tiles_m * tiles_n;
-    uint32_t slot = blockIdx.x;
+    uint32_t slot = id;
     if (total % 8u == 0) {
         const uint32_t per_xcd = total / 8u;
-        slot = (blockIdx.x % 8u) * per_xcd + blockIdx.x / 8u;
+        slot = (id % 8u) * per_xcd + id / 8u;
     }
     tn = slot / tiles_m;
     tm = slot % tiles_m;
 }
 
 // ------------------------------------------------------- int8 GEMM -------
-// Weight staging for one (row, block pair) into LDS as int8 + fp32 scales.
-// Q8_0 pair (68 B): block a quants are bytes 2..33 (alignbyte by 2), block b
-// quants are dwords 9..16.  Q4_0 pair (36 B): nibble bytes per block become
-// 32 int8 values n-8 (elements 0..15 = low nibbles, 16..31 = high nibbles).
-template <int FMT>
-__device__ __forceinline__ void stage_weight_pair(const uint8_t* src, bool valid, int8_t* lds_row, float& d0,
-                                                  float& d1) {
-    uint32_t out[16];
-    if (FMT == kQ8_0) {
-        uint32_t q[17];
-        const uint32_t* s = reinterpret_cast<const uint32_t*>(src);
-#pragma unroll
-        for (int i = 0; i < 17; ++i) q[i] = valid ? s[i] : 0u;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) out[i] = __builtin_amdgcn_alignbyte(q[i + 1], q[i], 2);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) out[8 + i] = q[9 + i];
-        d0 = half_bits_to_float(q[0]);
-        d1 = half_bits_to_float(q[8] >> 16);
-    } else {
-        uint32_t q[9];
-        const uint32_t* s = reinterpret_cast<const uint32_t*>(src);
-#pragma unroll
-        for (int i = 0; i < 9; ++i) q[i] = valid ? s[i] : 0x88888888u;
-        uint32_t a[4], b[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            a[i] = __builtin_amdgcn_alignbyte(q[i + 1], q[i], 2);
-            b[i] = q[5 + i];
-        }
-        // byte-wise n - 8 for n in [0,15]: ((n | 0x80) - 8) ^ 0x80, no borrow across bytes
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            out[i] = (((a[i] & 0x0F0F0F0Fu) | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
-            out[4 + i] = ((((a[i] >> 4) & 0x0F0F0F0Fu) | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
-            out[8 + i] = (((b[i] & 0x0F0F0F0Fu) | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
-            out[12 + i] = ((((b[i] >> 4) & 0x0F0F0F0Fu) | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
-        }
-        d0 = half_bits_to_float(q[0]);
-        d1 = half_bits_to_float(q[4] >> 16);
-    }
-    if (!valid) { d0 = 0.0f; d1 = 0.0f; }
-    uint4* dst = reinterpret_cast<uint4*>(lds_row);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) dst[i] = make_uint4(out[4 * i], out[4 * i + 1], out[4 * i + 2], out[4 * i + 3]);
-}
-
 // DOTS = true is the bit-exact test mode: instead of accumulating, the
 // kernel stores every per-block int32 MFMA result to dots[(m*N + n)*nb + b].
+//
+// Pipeline per K stage (KB = 4 blocks): the stage's activations, weights and
+// scales were fetched into registers during the previous stage's compute;
+// they are written to LDS (weights converted from native blocks), then the
+// next stage's global loads are issued, then the 4 blocks are computed.
+// Epilogue per (32x32 tile, block): the scale products dx[m]*dw[n] come from
+// one fp32 outer-product MFMA (v_mfma_f32_32x32x2f32 with the second K slot
+// zero), which lands them in exactly the accumulator layout, so the VALU
+// work is one v_cvt_f32_i32 and one v_fma per output element and block.
+//
+// Split-K: with ksplit > 1 the grid is ksplit x tiles; workgroup group `split`
+// covers stages [split*spw, (split+1)*spw) and stores its partial tile to
+// Y + split*M*N (a workspace), summed afterwards in fixed order by
+// splitk_reduce_kernel, so results do not depend on scheduling.
 template <int FMT, bool DOTS>
-__global__ __launch_bounds__(kThreads) void gemm_i8_kernel(const uint8_t* __restrict__ W, const int8_t* __restrict__ XQ,
+__global__ __launch_bounds__(kThreads, 2) void gemm_i8_kernel(const uint8_t* __restrict__ W, const int8_t* __restrict__ XQ,
                                                            const float* __restrict__ XS, float* __restrict__ Y,
                                                            int32_t* __restrict__ dots, uint32_t M, uint32_t N,
-                                                           uint32_t K, uint32_t tiles_m, uint32_t tiles_n) {
+                                                           uint32_t K, uint32_t tiles_m, uint32_t tiles_n,
+                                                           uint32_t ksplit, uint32_t stages_per_split) {
     constexpr uint32_t PB = FMT == kQ8_0 ? 68 : 36;  // bytes per block pair
+    constexpr int PW = FMT == kQ8_0 ? 17 : 9;         // dwords per block pair
     __shared__ __align__(16) int8_t As[BM * ROWB];
     __shared__ __align__(16) int8_t Bs[BN * ROWB];
     __shared__ __align__(16) float Sx[KB][BM];
     __shared__ __align__(16) float Sw[KB][BN];
 
+    const uint32_t total_tiles = tiles_m * tiles_n;
+    const uint32_t split = blockIdx.x / total_tiles;
     uint32_t tm, tn;
-    tile_of(tiles_m, tiles_n, tm, tn);
+    tile_of(tiles_m, tiles_n, blockIdx.x % total_tiles, tm, tn);
     const uint32_t m0 = tm * BM, n0 = tn * BN;
     const uint32_t nb = K >> 5;
     const uint32_t rb = (nb >> 1) * PB;
+    const uint32_t kb_begin = split * stages_per_split * KB;
+    const uint32_t kb_end = min(nb, kb_begin + stages_per_split * KB);
+    float* Yout = Y + (ksplit > 1 ? size_t(split) * M * N : 0);
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int l32 = lane & 31, lh = lane >> 5;
 
-    // loader coordinates
+    // loader coordinates: 2 threads per tile row; thread (row, half) moves the
+    // half's 4 blocks (2 pairs) of activations and weights, and 4 scales
+    constexpr int SPT = KB * BM / kThreads;  // activation scales per thread
     const int ld_row = tid >> 1, ld_half = tid & 1;
-    const uint32_t a_row = min(m0 + ld_row, M - 1);
-    const uint32_t b_row = min(n0 + ld_row, N - 1);
-    const int8_t* a_src = XQ + size_t(a_row) * K;
-    const uint8_t* b_src = W + size_t(b_row) * rb;
+    const int8_t* a_src = XQ + size_t(min(m0 + ld_row, M - 1)) * K;
+    const uint8_t* b_src = W + size_t(min(n0 + ld_row, N - 1)) * rb;
+    const float* s_src[SPT];
+#pragma unroll
+    for (int r = 0; r < SPT; ++r) s_src[r] = DOTS ? nullptr : XS + size_t(min(m0 + ((tid + r * kThreads) % BM), M - 1)) * nb;
+
+    uint4 ra[2][4];
+    uint32_t rw[2][PW];
+    float rs[SPT] = {};
+    // Loads are unconditional (block index clamped into the row, nb is even),
+    // so the compiler emits no branch / vmcnt(0) around them; blocks past the
+    // end of K are neutralised through zero scales in commit().
+    auto fetch = [&](uint32_t kb) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t blk = min(kb + 4 * ld_half + 2 * h, nb - 2);
+            const uint4* sa = reinterpret_cast<const uint4*>(a_src + size_t(blk) * 32);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) ra[h][i] = sa[i];
+            const uint32_t* sw = reinterpret_cast<const uint32_t*>(b_src + size_t(blk >> 1) * PB);
+#pragma unroll
+            for (int i = 0; i < PW; ++i) rw[h][i] = sw[i];
+        }
+        if constexpr (!DOTS) {  // the DOTS launch has no scale buffer (XS is null)
+#pragma unroll
+            for (int r = 0; r < SPT; ++r) {
+                const uint32_t kk = (tid + r * kThreads) / BM;
+                rs[r] = s_src[r][min(kb + kk, nb - 1)];
+            }
+        }
+    };
+    auto commit_pair = [&](uint32_t kb, int h) {
+        const uint32_t* rwp = rw[h];
+        uint4* da = reinterpret_cast<uint4*>(As + ld_row * ROWB + ld_half * 128 + h * 64);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) da[i] = ra[h][i];
+        uint32_t out[16];
+        float d0, d1;
+        if constexpr (FMT == kQ8_0) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) out[i] = __builtin_amdgcn_alignbyte(rwp[i + 1], rwp[i], 2);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) out[8 + i] = rwp[9 + i];
+            d0 = half_bits_to_float(rwp[0]);
+            d1 = half_bits_to_float(rwp[8] >> 16);
+        } else {
+            uint32_t qa[4], qb[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                qa[i] = __builtin_amdgcn_alignbyte(rwp[i + 1], rwp[i], 2);
+                qb[i] = rwp[5 + i];
+            }
+            // byte-wise n - 8 for n in [0,15]: ((n | 0x80) - 8) ^ 0x80, no borrow across bytes
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                out[i] = (((qa[i] & 0x0F0F0F0Fu) | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
+                out[4 + i] = ((((qa[i] >> 4) & 0x0F0F0F0Fu) | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
+                out[8 + i] = (((qb[i] & 0x0F0F0F0Fu) | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
+                out[12 + i] = ((((qb[i] >> 4) & 0x0F0F0F0Fu) | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
+            }
+            d0 = half_bits_to_float(rwp[0]);
+            d1 = half_bits_to_float(rwp[4] >> 16);
+        }
+        const int bl = 4 * ld_half + 2 * h;  // block index within the stage
+        if (kb + bl >= nb) { d0 = 0.0f; d1 = 0.0f; }
+        uint4* db = reinterpret_cast<uint4*>(Bs + ld_row * ROWB + bl * 32);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) db[i] = make_uint4(out[4 * i], out[4 * i + 1], out[4 * i + 2], out[4 * i + 3]);
+        Sw[bl][ld_row] = d0;
+        Sw[bl + 1][ld_row] = d1;
+    };
+    auto commit = [&](uint32_t kb) {
+        // Opaque register fence: the conversion below must not be hoisted up to
+        // the prefetch loads (that would make the compiler wait for them right
+        // after issuing them, before the compute loop).
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int i = 0; i < PW; ++i) asm volatile("" : "+v"(rw[h][i]));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(ra[h][i].x), "+v"(ra[h][i].y), "+v"(ra[h][i].z), "+v"(ra[h][i].w));
+        }
+#pragma unroll
+        for (int r = 0; r < SPT; ++r) asm volatile("" : "+v"(rs[r]));
+        commit_pair(kb, 0);
+        commit_pair(kb, 1);
+        if constexpr (!DOTS) {
+#pragma unroll
+            for (int r = 0; r < SPT; ++r) {
+                const int idx = tid + r * kThreads;
+                Sx[idx / BM][idx % BM] = kb + idx / BM < nb ? rs[r] : 0.0f;
+            }
+        }
+    };
 
     v16f acc[2][2];
 #pragma unroll
@@ -182,54 +251,28 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_kernel(const uint8_t* __rest
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
     const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    const v16f fzero = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 
-    for (uint32_t kb = 0; kb < nb; kb += KB) {
+    if (kb_begin < kb_end) fetch(kb_begin);
+    else return;
+    for (uint32_t kb = kb_begin; kb < kb_end; kb += KB) {
         __syncthreads();
-        // activations: 64 bytes (2 blocks) per thread
-        {
-            const uint32_t blk = kb + 2 * ld_half;
-            const bool valid = blk < nb;
-            const uint4* s = reinterpret_cast<const uint4*>(a_src + size_t(blk) * 32);
-            uint4* d = reinterpret_cast<uint4*>(As + ld_row * ROWB + ld_half * 64);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) d[i] = valid ? s[i] : make_uint4(0, 0, 0, 0);
-        }
-        // activation scales: KB*BM = 512 floats, 2 per thread
-#pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            const int idx = tid + r * kThreads;
-            const int kk = idx / BM, row = idx % BM;
-            const uint32_t blk = kb + kk;
-            Sx[kk][row] = blk < nb ? XS[size_t(min(m0 + row, M - 1)) * nb + blk] : 0.0f;
-        }
-        // weights: one block pair per thread
-        {
-            const uint32_t blk = kb + 2 * ld_half;
-            const bool valid = blk < nb;
-            float d0, d1;
-            stage_weight_pair<FMT>(b_src + size_t(blk >> 1) * PB, valid, Bs + ld_row * ROWB + ld_half * 64, d0, d1);
-            Sw[2 * ld_half][ld_row] = d0;
-            Sw[2 * ld_half + 1][ld_row] = d1;
-        }
+        commit(kb);
         __syncthreads();
-#pragma unroll
+        fetch(min(kb + KB, kb_end - 1));  // unconditional: the last one re-reads in-range data, unused
+#pragma unroll 1
         for (int b = 0; b < KB; ++b) {
             v4i a[2], w[2];
-            float sw[2];
-            float sx[2][16];
+            float dxl[2], dwl[2];
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
                 a[i] = *reinterpret_cast<const v4i*>(As + (wm * 64 + i * 32 + l32) * ROWB + b * 32 + lh * 16);
-#pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const float4 s4 = *reinterpret_cast<const float4*>(&Sx[b][wm * 64 + i * 32 + 8 * g + 4 * lh]);
-                    sx[i][4 * g] = s4.x; sx[i][4 * g + 1] = s4.y; sx[i][4 * g + 2] = s4.z; sx[i][4 * g + 3] = s4.w;
-                }
+                dxl[i] = lh ? 0.0f : Sx[b][wm * 64 + i * 32 + l32];
             }
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 w[j] = *reinterpret_cast<const v4i*>(Bs + (wn * 64 + j * 32 + l32) * ROWB + b * 32 + lh * 16);
-                sw[j] = Sw[b][wn * 64 + j * 32 + l32];
+                dwl[j] = lh ? 0.0f : Sw[b][wn * 64 + j * 32 + l32];
             }
 #pragma unroll
             for (int i = 0; i < 2; ++i)
@@ -245,8 +288,9 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_kernel(const uint8_t* __rest
                             if (m < M && n < N && blk < nb) dots[(size_t(m) * N + n) * nb + blk] = c[v];
                         }
                     } else {
+                        const v16f sc = __builtin_amdgcn_mfma_f32_32x32x2f32(dxl[i], dwl[j], fzero, 0, 0, 0);
 #pragma unroll
-                        for (int v = 0; v < 16; ++v) acc[i][j][v] = fmaf(float(c[v]), sx[i][v] * sw[j], acc[i][j][v]);
+                        for (int v = 0; v < 16; ++v) acc[i][j][v] = fmaf(float(c[v]), sc[v], acc[i][j][v]);
                     }
                 }
         }
@@ -261,9 +305,18 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_kernel(const uint8_t* __rest
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const uint32_t m = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
-                if (m < M && n < N) Y[size_t(m) * N + n] = acc[i][j][v];
+                if (m < M && n < N) Yout[size_t(m) * N + n] = acc[i][j][v];
             }
         }
+}
+
+__global__ __launch_bounds__(kThreads) void splitk_reduce_kernel(const float* __restrict__ part, float* __restrict__ Y,
+                                                                 size_t n, uint32_t ksplit) {
+    const size_t i = size_t(blockIdx.x) * kThreads + threadIdx.x;
+    if (i >= n) return;
+    float acc = part[i];
+    for (uint32_t s = 1; s < ksplit; ++s) acc += part[size_t(s) * n + i];
+    Y[i] = acc;
 }
 
 // ------------------------------------------------------- fp32 GEMM -------
@@ -277,7 +330,7 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(const uint8_t* __res
     __shared__ __align__(16) float As[BM * FROW];
     __shared__ __align__(16) float Bs[BN * FROW];
     uint32_t tm, tn;
-    tile_of(tiles_m, tiles_n, tm, tn);
+    tile_of(tiles_m, tiles_n, blockIdx.x, tm, tn);
     const uint32_t m0 = tm * BM, n0 = tn * BN;
     const size_t rb = row_bytes_dev(FMT, K);
     const int tid = threadIdx.x;
@@ -350,44 +403,76 @@ hipError_t launch_quantize_acts(const float* X, int8_t* xq, float* xs, size_t M,
     return hipGetLastError();
 }
 
+// Split factor so the grid reaches about two workgroups per CU (the LDS
+// budget allows two), keeping at least two K stages per split.
+static uint32_t choose_ksplit(uint32_t tiles, uint32_t nb) {
+    static const int forced = [] {
+        const char* e = getenv("ZQ_GEMM_KSPLIT");
+        return e ? atoi(e) : 0;
+    }();
+    const uint32_t stages = (nb + KB - 1) / KB;
+    uint32_t ks = forced > 0 ? uint32_t(forced) : (512 + tiles - 1) / tiles;
+    ks = std::max(1u, std::min(ks, std::max(1u, stages / 2)));
+    return ks;
+}
+
+size_t gemm_i8_partial_bytes(size_t M, size_t N, size_t K) {
+    const uint32_t tiles = uint32_t(((M + BM - 1) / BM) * ((N + BN - 1) / BN));
+    const uint32_t ks = choose_ksplit(tiles, uint32_t(K / 32));
+    return ks > 1 ? size_t(ks) * M * N * sizeof(float) : 0;
+}
+
 static hipError_t launch_i8_common(int fmt, const uint8_t* w, const int8_t* xq, const float* xs, float* Y,
-                                   int32_t* dots, size_t M, size_t N, size_t K, hipStream_t stream) {
+                                   int32_t* dots, float* partial, size_t M, size_t N, size_t K, hipStream_t stream) {
     if (!w || !xq || !M || !N || !K || K % 64 || M > (1u << 24) || N > (1u << 24) || K > (1u << 24))
         return hipErrorInvalidValue;
     if (fmt != kQ8_0 && fmt != kQ4_0) return hipErrorInvalidValue;
     if ((reinterpret_cast<uintptr_t>(w) & 3u) || (reinterpret_cast<uintptr_t>(xq) & 15u)) return hipErrorInvalidValue;
     const uint32_t tiles_m = static_cast<uint32_t>((M + BM - 1) / BM);
     const uint32_t tiles_n = static_cast<uint32_t>((N + BN - 1) / BN);
-    const dim3 grid(tiles_m * tiles_n);
+    const uint32_t nb = uint32_t(K / 32);
+    const uint32_t stages = (nb + KB - 1) / KB;
     const uint32_t m = uint32_t(M), n = uint32_t(N), k = uint32_t(K);
     if (dots) {
+        const dim3 grid(tiles_m * tiles_n);
         if (fmt == kQ8_0)
             hipLaunchKernelGGL((gemm_i8_kernel<kQ8_0, true>), grid, dim3(kThreads), 0, stream, w, xq, xs, Y, dots, m, n,
-                               k, tiles_m, tiles_n);
+                               k, tiles_m, tiles_n, 1u, stages);
         else
             hipLaunchKernelGGL((gemm_i8_kernel<kQ4_0, true>), grid, dim3(kThreads), 0, stream, w, xq, xs, Y, dots, m, n,
-                               k, tiles_m, tiles_n);
-    } else {
-        if (!xs || !Y) return hipErrorInvalidValue;
-        if (fmt == kQ8_0)
-            hipLaunchKernelGGL((gemm_i8_kernel<kQ8_0, false>), grid, dim3(kThreads), 0, stream, w, xq, xs, Y, dots, m,
-                               n, k, tiles_m, tiles_n);
-        else
-            hipLaunchKernelGGL((gemm_i8_kernel<kQ4_0, false>), grid, dim3(kThreads), 0, stream, w, xq, xs, Y, dots, m,
-                               n, k, tiles_m, tiles_n);
+                               k, tiles_m, tiles_n, 1u, stages);
+        return hipGetLastError();
     }
+    if (!xs || !Y) return hipErrorInvalidValue;
+    uint32_t ks = choose_ksplit(tiles_m * tiles_n, nb);
+    if (ks > 1 && !partial) ks = 1;
+    const uint32_t spw = (stages + ks - 1) / ks;
+    ks = (stages + spw - 1) / spw;  // no empty splits
+    float* out = ks > 1 ? partial : Y;
+    const dim3 grid(tiles_m * tiles_n * ks);
+    if (fmt == kQ8_0)
+        hipLaunchKernelGGL((gemm_i8_kernel<kQ8_0, false>), grid, dim3(kThreads), 0, stream, w, xq, xs, out, dots, m, n,
+                           k, tiles_m, tiles_n, ks, spw);
+    else
+        hipLaunchKernelGGL((gemm_i8_kernel<kQ4_0, false>), grid, dim3(kThreads), 0, stream, w, xq, xs, out, dots, m, n,
+                           k, tiles_m, tiles_n, ks, spw);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || ks == 1) return e;
+    const size_t total = M * N;
+    const dim3 rgrid(static_cast<uint32_t>((total + kThreads - 1) / kThreads));
+    hipLaunchKernelGGL(splitk_reduce_kernel, rgrid, dim3(kThreads), 0, stream, partial, Y, total, ks);
     return hipGetLastError();
 }
 
-hipError_t launch_gemm_i8(int fmt, const uint8_t* w, const int8_t* xq, const float* xs, float* Y, size_t M, size_t N,
-                          size_t K, hipStream_t stream) {
-    return launch_i8_common(fmt, w, xq, xs, Y, nullptr, M, N, K, stream);
+hipError_t launch_gemm_i8(int fmt, const uint8_t* w, const int8_t* xq, const float* xs, float* Y, float* partial,
+                          size_t M, size_t N, size_t K, hipStream_t stream) {
+    return launch_i8_common(fmt, w, xq, xs, Y, nullptr, partial, M, N, K, stream);
 }
 
 hipError_t launch_block_dots(int fmt, const uint8_t* w, const int8_t* xq, int32_t* out, size_t M, size_t N, size_t K,
                              hipStream_t stream) {
     if (!out) return hipErrorInvalidValue;
-    return launch_i8_common(fmt, w, xq, nullptr, nullptr, out, M, N, K, stream);
+    return launch_i8_common(fmt, w, xq, nullptr, nullptr, out, nullptr, M, N, K, stream);
 }
 
 hipError_t launch_gemm_f32(int fmt, const uint8_t* w, const float* X, float* Y, size_t M, size_t N, size_t K,

@@ -29,9 +29,11 @@ hipError_t launch_quantize_acts(const float* X, int8_t* xq, float* xs, size_t M,
                                 hipStream_t stream);
 
 // Prefill GEMM on int8 activations already quantised by launch_quantize_acts.
-// Y is token-major [M][N].
+// Y is token-major [M][N].  `partial` (gemm_i8_partial_bytes, may be 0) is
+// the split-K workspace; with partial == nullptr the GEMM runs unsplit.
+size_t gemm_i8_partial_bytes(size_t M, size_t N, size_t K);
 hipError_t launch_gemm_i8(int fmt, const uint8_t* w, const int8_t* xq, const float* xs,
-                          float* Y, size_t M, size_t N, size_t K, hipStream_t stream);
+                          float* Y, float* partial, size_t M, size_t N, size_t K, hipStream_t stream);
 
 // Prefill GEMM on fp32 activations (the reference CPU arithmetic).
 hipError_t launch_gemm_f32(int fmt, const uint8_t* w, const float* X, float* Y, size_t M,

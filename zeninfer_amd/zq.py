@@ -67,7 +67,7 @@ SIGNATURES = {
     "zq_hip_release_all": (ctypes.c_int, []),
     "zq_hip_gemv_dev": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _S, _S, _P]),
     "zq_hip_gemv_batch_dev": (ctypes.c_int, [ctypes.c_int, _P, ctypes.POINTER(GemvTask), _S, _S, _P]),
-    "zq_hip_gemm_workspace_bytes": (_S, [ctypes.c_int, _S, _S, ctypes.c_int]),
+    "zq_hip_gemm_workspace_bytes": (_S, [ctypes.c_int, _S, _S, _S, ctypes.c_int]),
     "zq_hip_gemm_dev": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _S, _S, _S, ctypes.c_int, _P, _S, _P]),
     "zq_hip_quantize_acts_dev": (ctypes.c_int, [_P, _P, _P, _S, _S, _P]),
     "zq_hip_block_dots_dev": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _S, _S, _S, _P]),
@@ -219,8 +219,8 @@ def gemv_batch_dev(fmt, x, tasks, cols, stream=None):
                  "zq_hip_gemv_batch_dev")
 
 
-def gemm_workspace_bytes(fmt, tokens, cols, act=ACT_DEFAULT):
-    return lib().zq_hip_gemm_workspace_bytes(fmt, tokens, cols, act)
+def gemm_workspace_bytes(fmt, tokens, rows, cols, act=ACT_DEFAULT):
+    return lib().zq_hip_gemm_workspace_bytes(fmt, tokens, rows, cols, act)
 
 
 def gemm_dev(fmt, w, X, Y, tokens, rows, cols, act=ACT_DEFAULT, workspace=None, workspace_bytes=0, stream=None):
