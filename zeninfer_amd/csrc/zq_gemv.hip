@@ -355,18 +355,14 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_kernel(TaskTable tt, cons
         for (int r = 0; r < R; ++r)
             rowp[r] = t.w + (size_t)min(row0 + r, t.rows - 1) * rb + (size_t)(np ? p0 : 0) * DW * 4;
     };
-    const uint32_t last_unit = nunits ? nunits - 1 : 0;
     auto load = [&](const uint8_t*(&rowp)[R], uint4 (&u)[R][NU]) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const uint4* src = reinterpret_cast<const uint4*>(rowp[r]);
 #pragma unroll
             for (int i = 0; i < NU; ++i) {
-                // clamp instead of predicating: an unconditional load keeps the
-                // compiler from wrapping it in a branch that waits on vmcnt(0);
-                // the duplicate units land in LDS slots no active lane reads
-                const uint32_t unit = min(uint32_t(lane + 64 * i), last_unit);
-                u[r][i] = src[unit];
+                const uint32_t unit = lane + 64 * i;
+                u[r][i] = unit < nunits ? src[unit] : make_uint4(0, 0, 0, 0);
             }
         }
     };
