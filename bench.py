@@ -25,8 +25,14 @@ cpu_baseline the reference's own AVX2 ComputePool path (compiled from the
          threads, the box's CPU share), on four layers' projections (0.93 GB);
          falls back to the C oracle if the reference build is absent.
 
+traffic  HBM bytes per launch of the dominant kernel from two rocprofv3 --pmc
+         passes (FETCH_SIZE, WRITE_SIZE) over `bench.py --pmc-workload`, each
+         scaled by what the counter reads for a 256 MiB device copy in the
+         same run; the committed result is profiles/traffic_gemv_q8_0_4096x14336.json.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
        python bench.py --summarize-trace kernel_trace.csv   (rocprofv3 helper)
+       python bench.py --pmc-workload                       (short run for --pmc passes)
 """
 import argparse
 import json
@@ -65,6 +71,55 @@ def summarize_trace(path):
     print(f"{'count':>6} {'avg_us':>10} {'total_ms':>10}  grid  lds  kernel")
     for (name, grid, lds), d in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
         print(f"{len(d):6d} {np.mean(d) / 1e3:10.2f} {sum(d) / 1e6:10.3f}  {grid} {lds}  {name[:110]}")
+
+
+def pmc_workload():
+    """Few launches for rocprofv3 --pmc passes: a 256 MiB device copy (counter
+    calibration), the 4096x14336 Q8_0 down GEMV on 4 distinct matrices, and
+    the int8 GEMM at M=2048 on 3 distinct 14336x4096 matrices."""
+    import torch
+    from zeninfer_amd import zq
+    zq.init()
+    dev, Q8 = "cuda:0", zq.Q8_0
+    a = torch.ones(64 * 1024 * 1024, device=dev)
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    b.copy_(a)
+    torch.cuda.synchronize()
+
+    def W(rows, cols, seed):
+        t = torch.empty(zq.weight_bytes(Q8, rows, cols), dtype=torch.uint8, device=dev)
+        zq.synth_weights_dev(Q8, seed, t, rows, cols)
+        return t
+    ws = [W(HIDDEN, FFN, 10 + i) for i in range(4)]
+    x = torch.empty(FFN, device=dev)
+    zq.synth_normal_dev(1, x, FFN)
+    y = torch.empty(HIDDEN, device=dev)
+    torch.cuda.synchronize()
+    for w in ws:
+        zq.gemv_dev(Q8, w, x, y, HIDDEN, FFN)
+    torch.cuda.synchronize()
+    del ws
+    M, N, K = 2048, FFN, HIDDEN
+    wg = [W(N, K, 50 + i) for i in range(3)]
+    X = torch.empty(M * K, device=dev)
+    zq.synth_normal_dev(2, X, M * K)
+    Y = torch.empty(M * N, device=dev)
+    wsb = zq.gemm_workspace_bytes(Q8, M, N, K, zq.ACT_INT8)
+    wsp = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    for w in wg:
+        zq.gemm_dev(Q8, w, X, Y, M, N, K, zq.ACT_INT8, wsp, wsb)
+    torch.cuda.synchronize()
+
+
+def measured_traffic():
+    """Traffic per launch of the dominant kernel from the committed profile, or None."""
+    path = os.path.join(ROOT, "profiles", "traffic_gemv_q8_0_4096x14336.json")
+    try:
+        with open(path) as f:
+            return int(json.load(f)["per_launch"]["traffic_bytes"])
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def cpu_baseline(seconds=10.0, layers=4):
@@ -114,9 +169,13 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--summarize-trace")
+    ap.add_argument("--pmc-workload", action="store_true")
     args = ap.parse_args()
     if args.summarize_trace:
         summarize_trace(args.summarize_trace)
+        return 0
+    if args.pmc_workload:
+        pmc_workload()
         return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this path has no multi-GPU leg in this build "
@@ -287,7 +346,7 @@ def main():
                    "weights_bytes_per_step": int(step_bytes), "launches_per_step": LAYERS * 4 + 1,
                    "frac_hbm_peak_step": round(value / HBM_PEAK_GBS, 4), "graph_matches_eager": graph_ok},
         "roofline": {"bound": "hbm", "achieved": round(down_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(down_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(down_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "kernel": "gemv_stream_kernel<Q8_0> (4 column slices x 16 waves) at 4096x14336, the down projection",
                      "avg_launch_us": round(down_ms * 1e3, 2), "algorithmic_bytes_per_launch": down_bytes},
         "per_shape_gemv": per_shape,
