@@ -534,6 +534,133 @@ __global__ __launch_bounds__(kThreads) void gemv_q6k_kernel(TaskTable tt, const 
     }
 }
 
+// Q6_K streaming kernel (cols % 2048 == 0, 16 B aligned rows).  A row is cut
+// into chunks of 8 super-blocks (1680 B, a multiple of 16 B); a team of S =
+// chunks-per-row waves covers a row, wave s owning chunk s, so each lane's x
+// values (two 16-element units: 32 floats) stay in VGPRs for the whole
+// kernel.  Each chunk is fetched with lane-contiguous dwordx4 loads into a
+// per-wave LDS buffer; lane L then decodes units L and L+64 of the chunk
+// (super-block u/16, half (u/8)%2, l-quad 4*(u%8)) from LDS.  Fields of odd
+// super-blocks sit at 2 mod 4 and are assembled with v_alignbyte.
+template <int S, int NW>
+__global__ __launch_bounds__(NW * 64) void gemv_q6k_stream_kernel(TaskTable tt, const float* __restrict__ x,
+                                                                 uint32_t cols, uint32_t total_blocks) {
+    constexpr int TEAMS = NW / S;
+    constexpr uint32_t CHUNK = 8 * 210;                  // bytes
+    constexpr uint32_t CUNITS = CHUNK / 16;              // 105 dwordx4 units
+    constexpr uint32_t BUFW = CHUNK / 4 + 4;             // dwords per wave buffer (+pad for alignbyte reads)
+    extern __shared__ uint32_t lds[];
+    __shared__ float red[2][NW];
+    const uint32_t rb = (cols >> 8) * 210;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int team = wave / S, slice = wave % S;
+    uint32_t* buf = lds + wave * BUFW;
+    const uint8_t* bbytes = reinterpret_cast<const uint8_t*>(buf);
+
+    auto locate = [&](uint32_t blk, const uint8_t*& rowp, uint32_t& row, int& ti) {
+        ti = find_task(tt, blk);
+        const GemvTask& t = tt.t[ti];
+        row = (blk - tt.group_start[ti]) * TEAMS + team;
+        rowp = t.w + (size_t)min(row, t.rows - 1) * rb + (size_t)slice * CHUNK;
+    };
+    auto load = [&](const uint8_t* rowp, uint4 (&u)[2]) {
+        const uint4* src = reinterpret_cast<const uint4*>(rowp);
+        u[0] = src[lane];
+        u[1] = lane + 64 < int(CUNITS) ? src[lane + 64] : make_uint4(0, 0, 0, 0);
+    };
+    // x for this lane's two units, kept in registers
+    float xv[2][4][4];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const uint32_t uu = lane + 64 * k;
+        const uint32_t sb = slice * 8 + (uu >> 4), h = (uu >> 3) & 1u, l0 = (uu & 7u) * 4u;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const float4 v = *reinterpret_cast<const float4*>(x + sb * 256 + h * 128 + g * 32 + l0);
+            xv[k][g][0] = v.x; xv[k][g][1] = v.y; xv[k][g][2] = v.z; xv[k][g][3] = v.w;
+        }
+    }
+    auto lds_u32 = [&](uint32_t off) -> uint32_t {  // 32 bits at a 2-byte aligned chunk offset
+        const uint32_t a = off & ~3u;
+        const uint32_t lo = buf[a >> 2];
+        if ((off & 3u) == 0) return lo;
+        return __builtin_amdgcn_alignbyte(buf[(a >> 2) + 1], lo, 2);
+    };
+
+    uint32_t blk = blockIdx.x;
+    uint4 u[2];
+    const uint8_t* rowp = nullptr;
+    uint32_t row = 0;
+    int ti = 0;
+    if (blk < total_blocks) {
+        locate(blk, rowp, row, ti);
+        load(rowp, u);
+    }
+    int parity = 0;
+    while (blk < total_blocks) {
+        reinterpret_cast<uint4*>(buf)[lane] = u[0];
+        if (lane + 64 < int(CUNITS)) reinterpret_cast<uint4*>(buf)[lane + 64] = u[1];
+        const uint32_t nblk = blk + gridDim.x;
+        const uint8_t* rowpn = nullptr;
+        uint32_t rown = 0;
+        int tin = 0;
+        if (nblk < total_blocks) {
+            locate(nblk, rowpn, rown, tin);
+            load(rowpn, u);
+        }
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const uint32_t uu = lane + 64 * k;
+            const uint32_t sbl = uu >> 4, h = (uu >> 3) & 1u, l0 = (uu & 7u) * 4u;
+            const uint32_t base = sbl * 210;
+            const uint32_t qlA = lds_u32(base + h * 64 + l0);
+            const uint32_t qlB = lds_u32(base + h * 64 + 32 + l0);
+            const uint32_t qh = lds_u32(base + 128 + h * 32 + l0);
+            const uint32_t sc0 = lds_u32(base + 192 + h * 8);
+            const uint32_t sc1 = lds_u32(base + 196 + h * 8);
+            const uint32_t dbits = uint32_t(bbytes[base + 208]) | (uint32_t(bbytes[base + 209]) << 8);
+            const float d = half_bits_to_float(dbits) * 0.25f;
+            const uint32_t shsel = l0 >> 4;
+            float part = 0.0f;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                uint32_t lo = (g & 1) ? qlB : qlA;
+                if (g >= 2) lo >>= 4;
+                lo &= 0x0F0F0F0Fu;
+                const uint32_t hi = ((qh >> (2 * g)) & 0x03030303u) << 4;
+                const uint32_t v = ((lo | hi) ^ 0x20202020u) << 2;  // 4*(q-32) per byte
+                float sum = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) sum = fmaf(sbyte(v, e), xv[k][g][e], sum);
+                const float sc = sbyte(g < 2 ? sc0 : sc1, (2 * g + shsel) & 3);
+                part = fmaf(d * sc, sum, part);
+            }
+            acc += part;
+        }
+        acc = wave_sum(acc);
+        const GemvTask& t = tt.t[ti];
+        if constexpr (S == 1) {
+            if (lane == 0 && row < t.rows) t.y[row] = acc;
+        } else {
+            if (lane == 0) red[parity][wave] = acc;
+            __syncthreads();
+            if (slice == 0 && lane == 0) {
+                float v = 0.0f;
+#pragma unroll
+                for (int s2 = 0; s2 < S; ++s2) v += red[parity][team * S + s2];
+                if (row < t.rows) t.y[row] = v;
+            }
+            parity ^= 1;
+        }
+        blk = nblk;
+        rowp = rowpn;
+        row = rown;
+        ti = tin;
+    }
+}
+
 // ------------------------------------------------------------- generic ---
 // Lane-per-block fallback for Q8_0 / Q4_0 rows whose block count is odd or
 // whose base is not dword-aligned.  x is read from global memory.
@@ -723,6 +850,35 @@ hipError_t launch_q6k(TaskTable& tt, const float* x, uint32_t cols, hipStream_t 
                        x, cols, groups);
     return hipGetLastError();
 }
+template <int S, int NW>
+hipError_t launch_q6k_stream(TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream) {
+    constexpr uint32_t TEAMS = NW / S;
+    uint32_t blocks = 0;
+    for (int i = 0; i < tt.count; ++i) {
+        tt.group_start[i] = blocks;
+        blocks += (tt.t[i].rows + TEAMS - 1) / TEAMS;
+    }
+    tt.group_start[tt.count] = blocks;
+    const uint32_t grid = std::min<uint32_t>(blocks, uint32_t(cu_count()));
+    const size_t lds = size_t(NW) * (8 * 210 / 4 + 4) * 4;
+    hipLaunchKernelGGL((gemv_q6k_stream_kernel<S, NW>), dim3(grid), dim3(NW * 64), lds, stream, tt, x, cols, blocks);
+    return hipGetLastError();
+}
+// chunks per row -> (S, waves per workgroup); nullopt-like false when unsupported
+hipError_t launch_q6k_stream_any(TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream) {
+    switch ((cols >> 8) / 8) {
+    case 1: return launch_q6k_stream<1, 16>(tt, x, cols, stream);
+    case 2: return launch_q6k_stream<2, 16>(tt, x, cols, stream);
+    case 3: return launch_q6k_stream<3, 15>(tt, x, cols, stream);
+    case 4: return launch_q6k_stream<4, 16>(tt, x, cols, stream);
+    case 5: return launch_q6k_stream<5, 15>(tt, x, cols, stream);
+    case 6: return launch_q6k_stream<6, 12>(tt, x, cols, stream);
+    case 7: return launch_q6k_stream<7, 14>(tt, x, cols, stream);
+    case 8: return launch_q6k_stream<8, 16>(tt, x, cols, stream);
+    default: return hipErrorInvalidConfiguration;
+    }
+}
+
 template <int FMT>
 hipError_t launch_blocks(TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream) {
     uint32_t groups = 0;
@@ -755,7 +911,18 @@ hipError_t launch_gemv(int fmt, const GemvTask* tasks, int count, const float* x
     const uint32_t c = static_cast<uint32_t>(cols);
     const int R = rows_per_wave(total_rows);
     if (fmt == kQ6_K) {
-        if (size_t(c) * 4 > lds_limit() || (reinterpret_cast<uintptr_t>(x) & 15u)) return hipErrorInvalidValue;
+        if (reinterpret_cast<uintptr_t>(x) & 15u) return hipErrorInvalidValue;
+        bool w16 = true;
+        for (int i = 0; i < count; ++i) w16 = w16 && (reinterpret_cast<uintptr_t>(tasks[i].w) & 15u) == 0;
+        static const bool q6_legacy = [] {
+            const char* e = getenv("ZQ_GEMV_KERNEL");
+            return e && e[0] == 'l';
+        }();
+        if (!q6_legacy && w16 && c % 2048 == 0 && c / 2048 <= 8) {
+            const hipError_t e = launch_q6k_stream_any(tt, x, c, stream);
+            if (e != hipErrorInvalidConfiguration) return e;
+        }
+        if (size_t(c) * 4 > lds_limit()) return hipErrorInvalidValue;
         for (int i = 0; i < count; ++i)
             if (reinterpret_cast<uintptr_t>(tasks[i].w) & 1u) return hipErrorInvalidValue;
         if (R == 4) return launch_q6k<4>(tt, x, c, stream);
