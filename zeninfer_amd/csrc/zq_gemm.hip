@@ -35,10 +35,14 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v32f __attribute__((ext_vector_type(32)));
 
 constexpr int kThreads = 256;
 constexpr int BM = 128;             // tokens per tile
 constexpr int BN = 128;             // weight rows per tile
+#ifndef ZQ_GEMM_DIAG
+#define ZQ_GEMM_DIAG 0  // diagnostic builds only: bit 0 drops the epilogue, bit 1 the K streaming
+#endif
 constexpr int KB = 8;               // 32-element blocks per K stage
 constexpr int ROWB = KB * 32 + 16;  // LDS bytes per tile row (16 B pad)
 
@@ -260,39 +264,62 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_i8_kernel(const uint8_t* __r
         commit(kb);
         __syncthreads();
         fetch(min(kb + KB, kb_end - 1));  // unconditional: the last one re-reads in-range data, unused
-#pragma unroll 1
-        for (int b = 0; b < KB; ++b) {
+        // Operands of block b+1 are read from LDS while block b computes, and
+        // tile t+1's two MFMAs are issued before tile t's VALU epilogue, so
+        // the matrix pipe, LDS and VALU overlap inside one wave.
+        struct Ops {
             v4i a[2], w[2];
-            float dxl[2], dwl[2];
+            float dx[2], dw[2];
+        };
+        auto read_ops = [&](int b, Ops& o) {
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
-                a[i] = *reinterpret_cast<const v4i*>(As + (wm * 64 + i * 32 + l32) * ROWB + b * 32 + lh * 16);
-                dxl[i] = lh ? 0.0f : Sx[b][wm * 64 + i * 32 + l32];
+                o.a[i] = *reinterpret_cast<const v4i*>(As + (wm * 64 + i * 32 + l32) * ROWB + b * 32 + lh * 16);
+                o.dx[i] = lh ? 0.0f : Sx[b][wm * 64 + i * 32 + l32];
             }
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-                w[j] = *reinterpret_cast<const v4i*>(Bs + (wn * 64 + j * 32 + l32) * ROWB + b * 32 + lh * 16);
-                dwl[j] = lh ? 0.0f : Sw[b][wn * 64 + j * 32 + l32];
+                o.w[j] = *reinterpret_cast<const v4i*>(Bs + (wn * 64 + j * 32 + l32) * ROWB + b * 32 + lh * 16);
+                o.dw[j] = lh ? 0.0f : Sw[b][wn * 64 + j * 32 + l32];
             }
+        };
+        Ops cur;
+        read_ops(0, cur);
+#pragma unroll 1
+        for (int b = 0; b < KB; ++b) {
+            Ops nxt;
+            read_ops(b + 1 < KB ? b + 1 : b, nxt);
+            if constexpr (DOTS) {
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+                for (int t = 0; t < 4; ++t) {
+                    const int i = t >> 1, j = t & 1;
+                    const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.a[i], cur.w[j], zero, 0, 0, 0);
+                    const uint32_t n = n0 + wn * 64 + j * 32 + l32;
+                    const uint32_t blk = kb + b;
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], w[j], zero, 0, 0, 0);
-                    if constexpr (DOTS) {
-                        const uint32_t n = n0 + wn * 64 + j * 32 + l32;
-                        const uint32_t blk = kb + b;
-#pragma unroll
-                        for (int v = 0; v < 16; ++v) {
-                            const uint32_t m = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
-                            if (m < M && n < N && blk < nb) dots[(size_t(m) * N + n) * nb + blk] = c[v];
-                        }
-                    } else {
-                        const v16f sc = __builtin_amdgcn_mfma_f32_32x32x2f32(dxl[i], dwl[j], fzero, 0, 0, 0);
-#pragma unroll
-                        for (int v = 0; v < 16; ++v) acc[i][j][v] = fmaf(float(c[v]), sc[v], acc[i][j][v]);
+                    for (int v = 0; v < 16; ++v) {
+                        const uint32_t m = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+                        if (m < M && n < N && blk < nb) dots[(size_t(m) * N + n) * nb + blk] = c[v];
                     }
                 }
+            } else {
+                v16i c[2];
+                v16f sc[2];
+                c[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.a[0], cur.w[0], zero, 0, 0, 0);
+                sc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(cur.dx[0], cur.dw[0], fzero, 0, 0, 0);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const int i = t >> 1, j = t & 1;
+                    if (t < 3) {
+                        const int i2 = (t + 1) >> 1, j2 = (t + 1) & 1;
+                        c[(t + 1) & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.a[i2], cur.w[j2], zero, 0, 0, 0);
+                        sc[(t + 1) & 1] = __builtin_amdgcn_mfma_f32_32x32x2f32(cur.dx[i2], cur.dw[j2], fzero, 0, 0, 0);
+                    }
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) acc[i][j][v] = fmaf(float(c[t & 1][v]), sc[t & 1][v], acc[i][j][v]);
+                }
+            }
+            cur = nxt;
         }
     }
     if constexpr (DOTS) return;
@@ -317,6 +344,262 @@ __global__ __launch_bounds__(kThreads) void splitk_reduce_kernel(const float* __
     float acc = part[i];
     for (uint32_t s = 1; s < ksplit; ++s) acc += part[size_t(s) * n + i];
     Y[i] = acc;
+}
+
+// Q8_0 int8 GEMM with direct-to-LDS staging (K % 256 == 0, 16 B aligned
+// weight rows).  512 threads = 8 waves in 2 (tokens) x 4 (rows), each wave a
+// 64 x 32 output tile (two 32x32 MFMA tiles).  A K stage is 8 blocks.
+//
+// Staging: global_load_lds_dwordx4 moves 16 B per lane from HBM straight into
+// LDS (64 lanes -> 1 KiB contiguous), so stages cost no VGPRs and no LDS
+// store instructions.  LDS holds two stages; stage s+1 streams into one
+// buffer while stage s is computed from the other, with one barrier a stage.
+//  * activations: 128 rows x 256 B, the 16 B columns of row r XOR-swizzled
+//    by (r & 15) so the MFMA A reads (32 consecutive rows, one column) hit
+//    distinct banks without row padding;
+//  * weights: 128 rows x 272 B, the raw native blocks (8 x 34 B contiguous in
+//    the row), units of 16 B in row-major order; the B operand of block b,
+//    half h is assembled at read time: odd blocks start dword-aligned
+//    (4 dword reads), even blocks at 2 mod 4 (5 reads + 4 v_alignbyte);
+//  * activation scales: [8][128] floats, one 4 B lane load each.
+// Epilogue: per block one 2-block outer-product MFMA gives dx*dw for both
+// tiles in the accumulator layout, then one cvt + one fma per element.
+constexpr int QTH = 512;
+constexpr int QA_BYTES = BM * KB * 32;                 // 32768
+constexpr int QWROW = KB * 34;                         // 272 raw bytes of a weight row per stage
+constexpr int QWD = QWROW / 4;                         // 68 dwords
+// Weight row r starts at LDS dword r*QW_STRIDE + QW_SHIFT*(r/8).  With an odd
+// stride the MFMA B reads (32 rows, one dword each) fall on distinct banks:
+// measured zero LDS bank conflicts for the whole kernel at stride 69.
+#ifndef ZQ_W_STRIDE
+#define ZQ_W_STRIDE 69
+#define ZQ_W_SHIFT 0
+#endif
+constexpr int QW_STRIDE = ZQ_W_STRIDE, QW_SHIFT = ZQ_W_SHIFT;
+static_assert(QW_STRIDE >= QWD + QW_SHIFT * 15 || QW_SHIFT == 0, "rows must not overlap");
+constexpr int QW_DWORDS = (BN - 1) * QW_STRIDE + QW_SHIFT * ((BN - 1) / 8) + QWD + 1;  // +1: 5th dword read
+constexpr int QW_LOADS = (QW_DWORDS + 63) / 64;        // 64-lane dword loads per stage
+constexpr int QW_PER_WAVE = (QW_LOADS + QTH / 64 - 1) / (QTH / 64);
+constexpr int QW_BYTES = (QW_LOADS * 64 * 4 + 15) / 16 * 16;
+constexpr int QS_BYTES = KB * BM * 4;                  // 4096
+constexpr int QBUF = QA_BYTES + QW_BYTES + QS_BYTES;   // bytes per stage buffer
+static_assert(2 * QBUF <= 160 * 1024, "two stage buffers must fit the 160 KiB LDS");
+static_assert(QA_BYTES % 16 == 0 && QW_BYTES % 16 == 0, "LDS regions stay 16 B aligned");
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Word 3 of a raw buffer resource on gfx9-family parts (32-bit data format,
+// no swizzle, stride 0): offsets are plain byte offsets from the base.
+constexpr int kBufferWord3 = 0x00020000;
+
+template <bool DOTS>
+__global__ __launch_bounds__(QTH, 2) void gemm_q8_coalesced_kernel(
+    const uint8_t* __restrict__ W, const int8_t* __restrict__ XQ, const float* __restrict__ XS,
+    float* __restrict__ Y, int32_t* __restrict__ dots, uint32_t M, uint32_t N, uint32_t K, uint32_t tiles_m,
+    uint32_t tiles_n, uint32_t ksplit, uint32_t stages_per_split) {
+    __shared__ __align__(16) uint8_t lds[2 * QBUF];
+
+    const uint32_t total_tiles = tiles_m * tiles_n;
+    const uint32_t split = blockIdx.x / total_tiles;
+    uint32_t tm, tn;
+    tile_of(tiles_m, tiles_n, blockIdx.x % total_tiles, tm, tn);
+    const uint32_t m0 = tm * BM, n0 = tn * BN;
+    const uint32_t nb = K >> 5;
+    const uint32_t rb = nb * 34;
+    const uint32_t kb_begin = split * stages_per_split * KB;
+    const uint32_t kb_end = min(nb, kb_begin + stages_per_split * KB);
+    float* Yout = Y + (ksplit > 1 ? size_t(split) * M * N : 0);
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 2, wn = wave & 3;
+    const int l32 = lane & 31, lh = lane >> 5;
+
+    // Direct loads go through buffer resources based at this tile's first
+    // activation row, weight row and scale row: per-lane 32-bit offsets
+    // (computed once) plus the stage's scalar offset.  Rows past M or N are
+    // clamped to the last one.
+    constexpr int A_LOADS = QA_BYTES / 1024 / (QTH / 64);   // 4 per wave
+    constexpr int S_LOADS = QS_BYTES / 256 / (QTH / 64);    // 2 per wave
+    const __amdgpu_buffer_rsrc_t a_rsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(XQ + size_t(m0) * K), 0, -1, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t w_rsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(W + size_t(n0) * rb), 0, -1, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t s_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(DOTS ? XQ : reinterpret_cast<const int8_t*>(XS + size_t(m0) * nb)), 0, -1, kBufferWord3);
+    uint32_t a_off[A_LOADS];
+#pragma unroll
+    for (int i = 0; i < A_LOADS; ++i) {
+        const int unit = (wave * A_LOADS + i) * 64 + lane;  // physical 16 B slot
+        const int row = unit >> 4, col = (unit & 15) ^ (row & 15);
+        a_off[i] = (min(m0 + row, M - 1) - m0) * K + col * 16;
+    }
+    // Weight dword loads: LDS dword p of the region holds raw dword d of row r
+    // (p = r*QW_STRIDE + QW_SHIFT*(r/8) + d); gap dwords load a harmless dword.
+    uint32_t w_off[QW_PER_WAVE];
+#pragma unroll
+    for (int i = 0; i < QW_PER_WAVE; ++i) {
+        const uint32_t p = uint32_t((wave + 8 * i) * 64 + lane);
+        uint32_t r = min(p / QW_STRIDE, uint32_t(BN - 1));
+        if (p < r * QW_STRIDE + QW_SHIFT * (r >> 3) && r > 0) --r;
+        uint32_t d = p - (r * QW_STRIDE + QW_SHIFT * (r >> 3));
+        if (d >= uint32_t(QWD)) d = 0;
+        w_off[i] = (min(n0 + r, N - 1) - n0) * rb + d * 4;
+    }
+    uint32_t s_off[S_LOADS];
+#pragma unroll
+    for (int i = 0; i < S_LOADS; ++i) {
+        const int idx = (wave * S_LOADS + i) * 64 + lane;  // = b * 128 + m
+        s_off[i] = ((min(m0 + uint32_t(idx & (BM - 1)), M - 1) - m0) * nb + (idx >> 7)) * 4;
+    }
+    auto stage_in = [&](uint32_t kb, int buf) {
+        uint8_t* base = lds + buf * QBUF;
+#pragma unroll
+        for (int i = 0; i < A_LOADS; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_void*)(base + (wave * A_LOADS + i) * 1024), 16,
+                                                     a_off[i], kb * 32, 0, 0);
+#pragma unroll
+        for (int i = 0; i < QW_PER_WAVE; ++i)
+            if (wave + 8 * i < QW_LOADS)  // wave-uniform
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_void*)(base + QA_BYTES + (wave + 8 * i) * 256), 4,
+                                                         w_off[i], kb * 34, 0, 0);
+        if constexpr (!DOTS) {
+#pragma unroll
+            for (int i = 0; i < S_LOADS; ++i)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    s_rsrc, (lds_void*)(base + QA_BYTES + QW_BYTES + (wave * S_LOADS + i) * 256), 4, s_off[i], kb * 4,
+                    0, 0);
+        }
+    };
+
+    v16f acc[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][v] = 0.0f;
+    const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    v32f szero;
+#pragma unroll
+    for (int v = 0; v < 32; ++v) szero[v] = 0.0f;
+    const uint32_t nrow = wn * 32 + l32;  // this lane's weight row within the tile
+    const uint32_t wrow = nrow * QW_STRIDE + QW_SHIFT * (nrow >> 3);  // its first LDS dword
+
+    // LDS operands of one block, read one step ahead of their MFMAs.
+    struct Ops {
+        v4i a[2];
+        uint32_t t[5];  // raw weight dwords (4 used for odd blocks)
+        uint32_t dwh;   // fp16 weight scale bits
+        float dx;
+    };
+    auto read_ops = [&](const uint8_t* base, int b, int odd, Ops& o) {
+        const uint32_t* Bw = reinterpret_cast<const uint32_t*>(base + QA_BYTES) + wrow;
+        const int off = (b * 34 + 2 + lh * 16) >> 2;
+#pragma unroll
+        for (int i = 0; i < 4 + (odd ? 0 : 1); ++i) o.t[i] = Bw[off + i];
+        o.dwh = reinterpret_cast<const uint16_t*>(Bw)[b * 17];
+        o.dx = DOTS ? 0.0f
+                    : reinterpret_cast<const float*>(base + QA_BYTES + QW_BYTES)[b * BM + wm * 64 + lh * 32 + l32];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int row = wm * 64 + i * 32 + l32, col = (b * 2 + lh) ^ (row & 15);
+            o.a[i] = *reinterpret_cast<const v4i*>(base + row * 256 + col * 16);
+        }
+    };
+    // In-flight results of one block: the two tiles' int32 dots and, from one
+    // 2-block outer-product MFMA (block i = lane half i: dx of tile i's rows
+    // times dw of the wave's columns), both tiles' dx*dw in the same layout.
+    struct Blk {
+        v16i c[2];
+        v32f s;
+    };
+    auto issue = [&](const Ops& o, int odd, Blk& r) {
+        v4i w;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[i] = odd ? int(o.t[i]) : int(__builtin_amdgcn_alignbyte(o.t[i + 1], o.t[i], 2));
+#pragma unroll
+        for (int i = 0; i < 2; ++i) r.c[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a[i], w, zero, 0, 0, 0);
+        if constexpr (!DOTS)
+            r.s = __builtin_amdgcn_mfma_f32_32x32x1f32(o.dx, half_bits_to_float(uint16_t(o.dwh)), szero, 0, 0, 0);
+    };
+    auto retire = [&](const Blk& r) {
+#if ZQ_GEMM_DIAG & 1
+#pragma unroll
+        for (int i = 0; i < 2; ++i) acc[i][0] = fmaf(float(r.c[i][0] ^ r.c[i][15]), r.s[16 * i] + r.s[16 * i + 15], acc[i][0]);
+#else
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][v] = fmaf(float(r.c[i][v]), r.s[16 * i + v], acc[i][v]);
+#endif
+    };
+
+    if (kb_begin >= kb_end) return;
+    stage_in(kb_begin, 0);
+    int buf = 0;
+    for (uint32_t kb = kb_begin; kb < kb_end; kb += KB, buf ^= 1) {
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's direct loads of stage kb landed
+        __syncthreads();                     // ... and everyone's; the other buffer is free again
+#if ZQ_GEMM_DIAG & 2
+        if (kb == kb_begin && kb + KB < kb_end) stage_in(kb + KB, buf ^ 1);
+#else
+        if (kb + KB < kb_end) stage_in(kb + KB, buf ^ 1);
+#endif
+        const uint8_t* base = lds + buf * QBUF;
+        // Waves sharing a SIMD start the stage at different block pairs, so
+        // one wave's MFMAs overlap the other's VALU epilogue instead of both
+        // running the same phase in lockstep after the barrier.
+        const int rot = (wave & 1) * (KB / 2);
+        if constexpr (DOTS) {
+#pragma unroll 1
+            for (int it = 0; it < KB; it += 2) {
+#pragma unroll
+                for (int bp = 0; bp < 2; ++bp) {
+                    const int b = ((it + rot) & (KB - 1)) + bp;
+                    Ops o;
+                    Blk r;
+                    read_ops(base, b, bp, o);
+                    issue(o, bp, r);
+                    const uint32_t n = n0 + nrow;
+#pragma unroll
+                    for (int i = 0; i < 2; ++i)
+#pragma unroll
+                        for (int v = 0; v < 16; ++v) {
+                            const uint32_t m = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+                            if (m < M && n < N) dots[(size_t(m) * N + n) * nb + kb + b] = r.c[i][v];
+                        }
+                }
+            }
+        } else {
+            // Three-step software pipeline over the stage's blocks: LDS reads
+            // of block b+2, MFMAs of block b+1 and the cvt/fma epilogue of
+            // block b are in flight together.
+            Ops oe, oo;
+            Blk p, q;
+            read_ops(base, rot, 0, oe);
+            read_ops(base, rot + 1, 1, oo);
+            issue(oe, 0, p);
+#pragma unroll 1
+            for (int it = 0; it < KB - 2; it += 2) {
+                read_ops(base, (it + 2 + rot) & (KB - 1), 0, oe);
+                issue(oo, 1, q);
+                retire(p);
+                read_ops(base, (it + 3 + rot) & (KB - 1), 1, oo);
+                issue(oe, 0, p);
+                retire(q);
+            }
+            issue(oo, 1, q);
+            retire(p);
+            retire(q);
+        }
+    }
+    if constexpr (DOTS) return;
+    const uint32_t n = n0 + nrow;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const uint32_t m = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+            if (m < M && n < N) Yout[size_t(m) * N + n] = acc[i][v];
+        }
 }
 
 // ------------------------------------------------------- fp32 GEMM -------
@@ -433,9 +716,20 @@ static hipError_t launch_i8_common(int fmt, const uint8_t* w, const int8_t* xq, 
     const uint32_t nb = uint32_t(K / 32);
     const uint32_t stages = (nb + KB - 1) / KB;
     const uint32_t m = uint32_t(M), n = uint32_t(N), k = uint32_t(K);
+    static const bool legacy = [] {
+        const char* e = getenv("ZQ_GEMM_KERNEL");
+        return e && e[0] == 'l';
+    }();
+    // The direct-load kernel addresses a tile with 32-bit offsets from its
+    // first row: 129 activation rows and 129 weight rows must stay below 2 GiB.
+    const bool offsets_fit = size_t(BM + 1) * K < (size_t(1) << 31) && size_t(BN + 1) * (K / 32 * 34) < (size_t(1) << 31);
+    const bool coalesced = !legacy && fmt == kQ8_0 && K % 256 == 0 && offsets_fit;
     if (dots) {
         const dim3 grid(tiles_m * tiles_n);
-        if (fmt == kQ8_0)
+        if (coalesced)
+            hipLaunchKernelGGL((gemm_q8_coalesced_kernel<true>), grid, dim3(QTH), 0, stream, w, xq, xs, Y, dots,
+                               m, n, k, tiles_m, tiles_n, 1u, stages);
+        else if (fmt == kQ8_0)
             hipLaunchKernelGGL((gemm_i8_kernel<kQ8_0, true>), grid, dim3(kThreads), 0, stream, w, xq, xs, Y, dots, m, n,
                                k, tiles_m, tiles_n, 1u, stages);
         else
@@ -450,7 +744,10 @@ static hipError_t launch_i8_common(int fmt, const uint8_t* w, const int8_t* xq, 
     ks = (stages + spw - 1) / spw;  // no empty splits
     float* out = ks > 1 ? partial : Y;
     const dim3 grid(tiles_m * tiles_n * ks);
-    if (fmt == kQ8_0)
+    if (coalesced)
+        hipLaunchKernelGGL((gemm_q8_coalesced_kernel<false>), grid, dim3(QTH), 0, stream, w, xq, xs, out, dots, m,
+                           n, k, tiles_m, tiles_n, ks, spw);
+    else if (fmt == kQ8_0)
         hipLaunchKernelGGL((gemm_i8_kernel<kQ8_0, false>), grid, dim3(kThreads), 0, stream, w, xq, xs, out, dots, m, n,
                            k, tiles_m, tiles_n, ks, spw);
     else
