@@ -41,7 +41,8 @@ constexpr int kThreads = 256;
 constexpr int BM = 128;             // tokens per tile
 constexpr int BN = 128;             // weight rows per tile
 #ifndef ZQ_GEMM_DIAG
-#define ZQ_GEMM_DIAG 0  // diagnostic builds only: bit 0 drops the epilogue, bit 1 the K streaming
+#define ZQ_GEMM_DIAG 0  // diagnostic builds only: bit 0 thins the epilogue, bit 1 drops the K streaming,
+                        // bit 2 records per-workgroup timestamps past the end of Y
 #endif
 constexpr int KB = 8;               // 32-element blocks per K stage
 constexpr int ROWB = KB * 32 + 16;  // LDS bytes per tile row (16 B pad)
@@ -533,6 +534,9 @@ __global__ __launch_bounds__(QTH, 2) void gemm_q8_coalesced_kernel(
     };
 
     if (kb_begin >= kb_end) return;
+#if ZQ_GEMM_DIAG & 4
+    const uint64_t diag_c0 = __builtin_amdgcn_s_memtime(), diag_t0 = __builtin_amdgcn_s_memrealtime();
+#endif
     stage_in(kb_begin, 0);
     int buf = 0;
     for (uint32_t kb = kb_begin; kb < kb_end; kb += KB, buf ^= 1) {
@@ -600,6 +604,19 @@ __global__ __launch_bounds__(QTH, 2) void gemm_q8_coalesced_kernel(
             const uint32_t m = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
             if (m < M && n < N) Yout[size_t(m) * N + n] = acc[i][v];
         }
+#if ZQ_GEMM_DIAG & 4
+    // diagnostic builds only: start/end ticks, shader cycles and hardware ids
+    // of this workgroup, written past the end of Y
+    __syncthreads();
+    if (tid == 0) {
+        uint64_t* o = reinterpret_cast<uint64_t*>(Yout + size_t(M) * N) + 4 * blockIdx.x;  // caller over-allocates Y
+        o[0] = diag_t0;
+        o[1] = __builtin_amdgcn_s_memrealtime();
+        o[2] = __builtin_amdgcn_s_memtime() - diag_c0;
+        o[3] = (uint64_t(__builtin_amdgcn_s_getreg((23 << 0) | (0 << 6) | (31 << 11))) << 32) |  // XCC_ID
+               __builtin_amdgcn_s_getreg((4 << 0) | (0 << 6) | (31 << 11));                    // HW_ID
+    }
+#endif
 }
 
 // ------------------------------------------------------- fp32 GEMM -------

@@ -1,0 +1,137 @@
+// issue_rates.hip -- measures, on the GPU it runs on, the per-SIMD cost of the
+// instruction mixes the int8 GEMM epilogue is built from: int8 and fp32
+// MFMAs, plain fp32 VALU FMAs, cvt+fma pairs, and MFMAs interleaved with
+// independent VALU work (to see whether the two co-execute).
+//
+// One workgroup per CU (96 KiB of dynamic LDS is reserved to force it), 1, 2
+// or 4 waves per SIMD; every wave runs the same loop and the workgroup's time
+// is taken from before its first to after its last wave (s_memtime, shader
+// clock).  Build and run:
+//   hipcc --offload-arch=gfx950 -O3 -Xclang -target-feature -Xclang -packed-fp32-ops \
+//         -o /tmp/issue_rates zeninfer_amd/probes/issue_rates.hip && /tmp/issue_rates
+#include <hip/hip_runtime.h>
+#include <cstdio>
+#include <cstdlib>
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v32f __attribute__((ext_vector_type(32)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+constexpr int ITERS = 2000;
+constexpr int LDS_RESERVE = 98304;
+
+#define CHECK(x)                                                                    \
+    do {                                                                            \
+        hipError_t e_ = (x);                                                        \
+        if (e_ != hipSuccess) {                                                     \
+            fprintf(stderr, "%s failed: %s\n", #x, hipGetErrorString(e_));          \
+            exit(1);                                                                \
+        }                                                                           \
+    } while (0)
+
+template <int KIND>
+__global__ void mix(float* out, unsigned long long* cyc, int seed) {
+    extern __shared__ float reserve[];
+    if (seed == 12345) reserve[threadIdx.x] = 1.0f;  // never true; keeps the reservation live
+    v4i a = {seed, seed + 1, seed + 2, int(threadIdx.x)};
+    v16i ci[4] = {};
+    v16f cf[4] = {};
+    v32f c2 = {};
+    const float x0 = threadIdx.x, x1 = x0 + 1, x3 = x0 + 3, y = seed * 0.5f;
+    float acc[16];
+    for (int i = 0; i < 16; ++i) acc[i] = i * x0;
+    __syncthreads();
+    const unsigned long long t0 = __builtin_amdgcn_s_memtime();
+    for (int it = 0; it < ITERS; ++it) {
+        if constexpr (KIND == 0) {  // 4 independent v_mfma_i32_32x32x32_i8
+#pragma unroll
+            for (int j = 0; j < 4; ++j) ci[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, a, ci[j], 0, 0, 0);
+        } else if constexpr (KIND == 1) {  // v_mfma_f32_32x32x1_2b_f32
+#pragma unroll
+            for (int j = 0; j < 4; ++j) c2 = __builtin_amdgcn_mfma_f32_32x32x1f32(x0 + j, x1, c2, 0, 0, 0);
+        } else if constexpr (KIND == 2) {  // v_mfma_f32_32x32x16_bf16
+            v8bf b;
+            for (int q = 0; q < 8; ++q) b[q] = (__bf16)(x0 + q);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) cf[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, b, cf[j], 0, 0, 0);
+        } else if constexpr (KIND == 3) {  // fp32 fma, 16 independent chains
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int j = 0; j < 16; ++j) acc[j] = fmaf(acc[j], y, x3);
+        } else if constexpr (KIND == 4) {  // cvt + fma pairs (the GEMM epilogue)
+#pragma unroll
+            for (int r = 0; r < 2; ++r)
+#pragma unroll
+                for (int j = 0; j < 16; ++j) acc[j] = fmaf(float(ci[0][j] + r), y, acc[j]);
+        } else if constexpr (KIND == 5 || KIND == 6) {  // int8 MFMA + 16 / 48 independent fma
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                ci[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, a, ci[j], 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < (KIND == 5 ? 1 : 3); ++r)
+#pragma unroll
+                    for (int q = 0; q < 16; ++q) acc[q] = fmaf(acc[q], y, x3);
+            }
+        } else if constexpr (KIND == 7) {  // fp32 2-block MFMA + 16 independent fma
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                c2 = __builtin_amdgcn_mfma_f32_32x32x1f32(x0 + j, x1, c2, 0, 0, 0);
+#pragma unroll
+                for (int q = 0; q < 16; ++q) acc[q] = fmaf(acc[q], y, x3);
+            }
+        }
+    }
+    float s = 0;
+    for (int j = 0; j < 4; ++j)
+        for (int v = 0; v < 16; ++v) s += float(ci[j][v]) + cf[j][v];
+    for (int v = 0; v < 32; ++v) s += c2[v];
+    for (int i = 0; i < 16; ++i) s += acc[i];
+    out[blockIdx.x * blockDim.x + threadIdx.x] = s;
+    __syncthreads();
+    const unsigned long long t1 = __builtin_amdgcn_s_memtime();
+    if (threadIdx.x == 0) cyc[blockIdx.x] = t1 - t0;
+}
+
+template <int KIND>
+void run(const char* name, int waves_per_simd, int insts_per_iter, int cus) {
+    float* out;
+    unsigned long long* cyc;
+    const int threads = 256 * waves_per_simd;
+    CHECK(hipMalloc(&out, size_t(cus) * threads * 4));
+    CHECK(hipMalloc(&cyc, size_t(cus) * 8));
+    CHECK(hipFuncSetAttribute((const void*)mix<KIND>, hipFuncAttributeMaxDynamicSharedMemorySize, LDS_RESERVE));
+    hipLaunchKernelGGL(mix<KIND>, dim3(cus), dim3(threads), LDS_RESERVE, 0, out, cyc, 3);
+    CHECK(hipGetLastError());
+    CHECK(hipDeviceSynchronize());
+    unsigned long long* h = new unsigned long long[cus];
+    CHECK(hipMemcpy(h, cyc, size_t(cus) * 8, hipMemcpyDeviceToHost));
+    double m = 0;
+    for (int i = 0; i < cus; ++i) m += double(h[i]);
+    m /= cus;
+    printf("| %-34s | %d | %7.1f |\n", name, waves_per_simd, m / (double(ITERS) * insts_per_iter * waves_per_simd));
+    delete[] h;
+    CHECK(hipFree(out));
+    CHECK(hipFree(cyc));
+}
+
+int main() {
+    hipDeviceProp_t p;
+    CHECK(hipGetDeviceProperties(&p, 0));
+    printf("%s (%s), %d CUs; cycles per instruction per SIMD (s_memtime)\n\n", p.name, p.gcnArchName,
+           p.multiProcessorCount);
+    printf("| mix (per unit) | waves/SIMD | cycles |\n|---|---|---|\n");
+    const int cus = p.multiProcessorCount;
+    for (int w = 1; w <= 4; w *= 2) {
+        run<0>("mfma_i32_32x32x32_i8", w, 4, cus);
+        run<1>("mfma_f32_32x32x1_2b_f32", w, 4, cus);
+        run<2>("mfma_f32_32x32x16_bf16", w, 4, cus);
+        run<3>("fp32 fma", w, 64, cus);
+        run<4>("cvt_f32_i32 + fma (per instruction)", w, 32, cus);
+        run<5>("i8 MFMA + 16 fma (per MFMA)", w, 4, cus);
+        run<6>("i8 MFMA + 48 fma (per MFMA)", w, 4, cus);
+        run<7>("f32 2b MFMA + 16 fma (per MFMA)", w, 4, cus);
+    }
+    return 0;
+}
