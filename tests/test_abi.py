@@ -9,10 +9,11 @@ import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "zq_hip.h")
+GGUF_HEADER = os.path.join(ROOT, "include", "zq_gguf.h")
 
 
-def declared_symbols():
-    text = open(HEADER).read()
+def declared_symbols(header=HEADER):
+    text = open(header).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(zq_[a-z0-9_]+)\s*\(", text)))
 
@@ -30,6 +31,10 @@ def test_library_exports_every_declared_symbol():
     missing = [s for s in declared_symbols() if not hasattr(lib, s)]
     assert not missing, missing
     assert set(declared_symbols()) == set(zq.SIGNATURES), "Python binding out of sync with the header"
+    gguf = declared_symbols(GGUF_HEADER)
+    missing = [s for s in gguf if not hasattr(lib, s)]
+    assert not missing, missing
+    assert set(gguf) == set(zq.GGUF_SIGNATURES), "Python binding out of sync with include/zq_gguf.h"
 
 
 def test_layout_helpers_without_device():

@@ -1,0 +1,273 @@
+"""CPU tier: the GGUF loader (include/zq_gguf.h) against the reference's parse
+core.
+
+- Known-answer cases are the reference's own parser tests
+  (tests/core_tests.cpp:648-703, 746-820 of the reference), rebuilt as byte
+  images here: invalid magic, minimal v3, BOOL + IQ4_NL, the GGML type-size
+  table, the metadata nesting cap, the u64 width gate, hostile / empty / stub
+  buffers and memory-vs-file agreement.
+- Differential: the reference's inspect_bytes (compiled from its sources into
+  oracle/_ref) and ours describe the same images identically -- ok flag,
+  error text and, when ok, header, config, metadata map and tensor table --
+  over the writer's files and a few thousand structured mutations of them
+  (the mutation classes of tests/fuzz_gguf.cpp: header fields, metadata
+  types / counts / string lengths, tensor directory, truncation).
+- Round trip: payload bytes read back through the mapping are the bytes the
+  writer wrote.
+"""
+import ctypes
+import os
+import struct
+
+import numpy as np
+import pytest
+
+from zeninfer_amd import gguf as G
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+REF_LIB = os.path.join(ROOT, "oracle", "_ref", "libzenref.so")
+
+
+def u32(v):
+    return struct.pack("<I", v)
+
+
+def u64(v):
+    return struct.pack("<Q", v)
+
+
+def gstr(s):
+    b = s.encode() if isinstance(s, str) else s
+    return u64(len(b)) + b
+
+
+def pad32(b):
+    return b + bytes((-len(b)) % 32)
+
+
+def parse(data, layout=0):
+    try:
+        return G.GGUFFile(data=data, q8_1_layout=layout)
+    except G.GGUFError as e:
+        return e
+
+
+# ---- known answers (reference tests/core_tests.cpp) ------------------------
+
+def test_invalid_magic(tmp_path):
+    p = tmp_path / "bad.gguf"
+    p.write_bytes(b"NOPE")
+    with pytest.raises(G.GGUFError, match="magic"):
+        G.GGUFFile(p)
+
+
+def test_minimal_v3_file(tmp_path):
+    img = b"GGUF" + u32(3) + u64(0) + u64(1) + gstr("general.architecture") + u32(8) + gstr("qwen3")
+    p = tmp_path / "min.gguf"
+    p.write_bytes(pad32(img))
+    g = G.GGUFFile(p)
+    c = g.config()
+    assert c["architecture"] == "qwen3" and c["data_offset"] >= 4 + 4 + 8 + 8
+    assert g.tensors() == []
+
+
+def test_bool_metadata_and_iq4_nl_size(tmp_path):
+    img = (b"GGUF" + u32(3) + u64(1) + u64(2) + gstr("general.architecture") + u32(8) + gstr("llama")
+           + gstr("tokenizer.ggml.add_bos_token") + u32(7) + b"\x01"
+           + gstr("test.weight") + u32(1) + u64(32) + u32(20) + u64(0))
+    p = tmp_path / "iq4.gguf"
+    p.write_bytes(pad32(img) + bytes(18))
+    t = G.GGUFFile(p).tensors()
+    assert len(t) == 1 and t[0]["byte_size"] == 18
+
+
+@pytest.mark.parametrize("gtype,elements,expected", [
+    (16, 256, 66), (17, 256, 74), (18, 256, 98), (19, 256, 50), (20, 32, 18), (21, 256, 110), (22, 256, 82),
+    (23, 256, 136), (24, 1, 1), (25, 1, 2), (26, 1, 4), (27, 1, 8), (28, 1, 8), (29, 256, 56), (30, 1, 2),
+    (34, 256, 54), (35, 256, 66), (9, 32, 36), (39, 32, 17), (40, 64, 36), (41, 128, 18), (42, 64, 18),
+    (43, 1, 1), (8, 32, 34), (2, 32, 18), (14, 256, 210),
+    (4, 256, 0), (5, 256, 0), (31, 256, 0), (32, 256, 0), (33, 256, 0), (36, 256, 0), (37, 256, 0), (38, 256, 0)])
+def test_ggml_type_table(gtype, elements, expected):
+    img = (b"GGUF" + u32(3) + u64(1) + u64(1) + gstr("general.architecture") + u32(8) + gstr("llama")
+           + gstr("weight") + u32(1) + u64(elements) + u32(gtype) + u64(0))
+    img = pad32(img) + bytes(expected)
+    r = parse(img, layout=1)
+    if expected:
+        assert not isinstance(r, Exception), r
+        assert r.tensors()[0]["byte_size"] == expected
+    else:
+        assert isinstance(r, G.GGUFError) and "unsupported or invalid GGML type" in str(r)
+
+
+def test_q8_1_requires_explicit_layout():
+    img = (b"GGUF" + u32(3) + u64(1) + u64(0) + gstr("w") + u32(1) + u64(32) + u32(9) + u64(0))
+    img = pad32(img) + bytes(40)
+    assert isinstance(parse(img), G.GGUFError)
+    assert parse(img, layout=1).tensors()[0]["byte_size"] == 36
+    assert parse(img, layout=2).tensors()[0]["byte_size"] == 40
+
+
+def test_metadata_nesting_cap_file_and_memory_agree(tmp_path):
+    img = b"GGUF" + u32(3) + u64(0) + u64(1) + gstr("crafted.nested") + u32(9)
+    img += (u32(9) + u64(1)) * 80 + u32(8) + u64(0)
+    p = tmp_path / "deep.gguf"
+    p.write_bytes(img)
+    with pytest.raises(G.GGUFError) as ef:
+        G.GGUFFile(p)
+    em = parse(img)
+    assert isinstance(em, G.GGUFError) and str(em) == str(ef.value)
+
+
+def test_u64_width_gate():
+    key = b"llama.embedding_length"
+    img = b"GGUF" + u32(3) + u64(0) + u64(1) + gstr(key) + u32(10) + u64((1 << 32) + 4096)
+    g = parse(pad32(img))
+    assert g.config()["embedding_length"] == 0
+
+
+def test_hostile_empty_and_stub_buffers():
+    hostile = b"GGUF" + u32(3) + u64(0) + u64(1) + u64(1 << 24)
+    assert isinstance(parse(hostile), G.GGUFError)
+    assert isinstance(parse(b""), G.GGUFError)
+    assert isinstance(parse(b"GG"), G.GGUFError)
+    minimal = pad32(b"GGUF" + u32(3) + u64(0) + u64(1) + gstr("general.architecture") + u32(8) + gstr("llama"))
+    g = parse(minimal)
+    assert g.config()["architecture"] == "llama" and g.config()["data_offset"] == len(minimal)
+
+
+# ---- round trip and differential against the reference ---------------------
+
+SHAPE = G.LlamaShape(embedding=256, layers=2, heads=4, kv_heads=2, ffn=512, vocab=512, context=256)
+
+
+@pytest.fixture(scope="module")
+def tiny_image(tmp_path_factory):
+    p = tmp_path_factory.mktemp("gguf") / "tiny.gguf"
+    G.synthetic_llama(p, SHAPE, seed=11)
+    return p, p.read_bytes()
+
+
+def test_writer_round_trip(tiny_image):
+    path, data = tiny_image
+    g = G.GGUFFile(path)
+    c = g.config()
+    assert (c["embedding_length"], c["block_count"], c["head_count"], c["head_count_kv"], c["feed_forward_length"],
+            c["vocabulary_size"]) == (256, 2, 4, 2, 512, 512)
+    names = [t["name"] for t in g.tensors()]
+    assert names[0] == "token_embd.weight" and names[-1] == "output.weight" and len(names) == 3 + 9 * 2
+    # payloads: the directory offsets index the bytes the writer laid down
+    for t in g.tensors():
+        start = c["data_offset"] + t["offset"]
+        assert g.tensor_bytes(t["name"]) == data[start:start + t["byte_size"]]
+    q = g.tensor("blk.1.attn_q.weight")
+    assert q["dims"] == [256, 256] and q["ggml_type"] == 8 and q["byte_size"] == 256 * 8 * 34
+
+
+def test_q8_0_quantizer_known_values():
+    w = np.zeros((1, 32), np.float32)
+    w[0, 0], w[0, 1], w[0, 2] = 1.27, -0.635, 0.005
+    b = np.frombuffer(G.quantize_q8_0(w), np.uint8)
+    d = b[:2].view(np.float16)[0]
+    q = b[2:].view(np.int8)
+    assert d == np.float16(0.01) and q[0] == 127 and q[1] == -64 and q[2] == 0  # rint(-63.5) -> -64 (even)
+
+
+@pytest.fixture(scope="module")
+def ref():
+    if not os.path.exists(REF_LIB):
+        pytest.skip("oracle/_ref not built (needs the reference sources)")
+    L = ctypes.CDLL(REF_LIB)
+    L.zr_gguf_describe.restype = ctypes.c_size_t
+    L.zr_gguf_describe.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_char_p, ctypes.c_size_t]
+    return L
+
+
+def ref_describe(L, data, layout=0):
+    buf = ctypes.create_string_buffer(data, len(data)) if data else None
+    n = L.zr_gguf_describe(buf, len(data), layout, None, 0)
+    out = ctypes.create_string_buffer(n + 1)
+    L.zr_gguf_describe(buf, len(data), layout, out, n + 1)
+    return out.raw[:n].decode(errors="replace")
+
+
+def our_describe(data, layout=0):
+    r = parse(data, layout)
+    if isinstance(r, Exception):
+        return f"ok=0\nerror={r}\n"
+    return r.describe()
+
+
+def test_differential_on_writer_output(ref, tiny_image):
+    _, data = tiny_image
+    assert ref_describe(ref, data) == our_describe(data)
+
+
+def _mutations(data, rng, n):
+    """Structured mutations: header fields, counts, metadata / directory bytes,
+    type and length words, truncation -- each image differs from the valid one
+    in one place."""
+    hdr_end, size = 24, len(data)
+
+    def pos(align=1):
+        return int(rng.integers(hdr_end, size - 8)) & ~(align - 1)
+
+    for _ in range(n):
+        b = bytearray(data)
+        kind = rng.integers(0, 7)
+        if kind == 0:   # header field
+            b[int(rng.integers(4, hdr_end))] = int(rng.integers(0, 256))
+        elif kind == 1:  # tensor / metadata count
+            off = int(rng.choice([8, 16]))
+            b[off:off + 8] = struct.pack("<Q", int(rng.choice([0, 1, 4, 5, 11, 12, 1000001, 2 ** 40])))
+        elif kind == 2:  # one bit anywhere past the header
+            b[pos()] ^= 1 << int(rng.integers(0, 8))
+        elif kind == 3:  # a type / length word
+            off = pos()
+            b[off:off + 4] = struct.pack("<I", int(rng.choice([0, 4, 7, 8, 9, 12, 13, 20, 142, 255, 2 ** 24 + 1])))
+        elif kind == 4:  # a length / offset / dimension quad-word
+            off = pos()
+            b[off:off + 8] = struct.pack("<Q", int(rng.choice([0, 1, 31, 64, 2 ** 24, 2 ** 32 + 1, 2 ** 63])))
+        elif kind == 5:  # truncation
+            b = b[:int(rng.integers(0, size))]
+        else:           # a random byte
+            b[pos()] = int(rng.integers(0, 256))
+        yield bytes(b)
+
+
+def test_differential_structured_mutations(ref):
+    # a small model keeps each image ~200 KB so thousands of parses stay fast
+    shape = G.LlamaShape(embedding=64, layers=1, heads=2, kv_heads=1, ffn=64, vocab=64, context=64)
+    w = G.GGUFWriter()
+    w.add_meta("general.architecture", G.STRING, "llama")
+    w.add_meta("llama.embedding_length", G.U32, shape.embedding)
+    w.add_meta("llama.rope.freq_base", G.F32, 500000.0)
+    w.add_meta("general.alignment", G.U32, 32)
+    w.add_meta("tokenizer.ggml.tokens", G.ARRAY, (G.STRING, ["a", "b", "c"]))
+    w.add_meta("tokenizer.ggml.scores", G.ARRAY, (G.F32, [0.0, 1.0, 2.0]))
+    w.add_meta("llama.feed_forward_length", G.ARRAY, (G.U32, [64]))
+    w.add_meta("general.weird", G.ARRAY, (G.ARRAY, [(G.U8, [1, 2]), (G.U8, [3])]))
+    w.add_meta("general.f64", G.F64, 1.5)
+    w.add_meta("general.i8", G.I8, -3)
+    w.add_meta("general.flag", G.BOOL, 1)
+    for i in range(4):
+        w.add_tensor(f"blk.0.t{i}", [64, 2], G.GGML_Q8_0, bytes(range(256))[:136] * 1)
+    w.add_tensor("norm", [64], G.GGML_F32, bytes(256))
+    base = w.to_bytes()
+    assert ref_describe(ref, base) == our_describe(base)
+    rng = np.random.default_rng(2024)
+    n_ok = n_err = 0
+    for img in _mutations(base, rng, 3000):
+        r = ref_describe(ref, img)
+        if "\x00" in r:
+            # a key with an embedded NUL: the C accessors stop at it, so only the
+            # verdict and the error text are comparable
+            o = parse(img)
+            assert r.startswith("ok=1") == (not isinstance(o, Exception)), r[:200]
+            if isinstance(o, Exception):  # the ABI's error text ends at the first NUL
+                assert r[len("ok=0\nerror="):].split("\x00")[0].rstrip("\n") == str(o)
+            continue
+        o = our_describe(img)
+        assert r == o, (r[:300], o[:300])
+        n_ok += r.startswith("ok=1")
+        n_err += r.startswith("ok=0")
+    assert n_ok > 100 and n_err > 100  # both outcomes exercised

@@ -76,6 +76,33 @@ SIGNATURES = {
     "zq_hip_synth_normal_dev": (ctypes.c_int, [ctypes.c_uint64, _P, _S, _P]),
 }
 
+class GGUFTensor(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("n_dims", ctypes.c_uint32), ("dims", ctypes.c_uint64 * 4),
+                ("ggml_type", ctypes.c_uint32), ("offset", ctypes.c_uint64), ("byte_size", ctypes.c_uint64),
+                ("data", _P)]
+
+
+class GGUFConfig(ctypes.Structure):
+    _fields_ = [("version", ctypes.c_uint32), ("data_offset", ctypes.c_uint64), ("file_size", ctypes.c_uint64)] + [
+        (n, ctypes.c_uint32) for n in ("embedding_length", "block_count", "head_count", "head_count_kv",
+                                       "feed_forward_length", "context_length", "vocabulary_size", "bos_token_id",
+                                       "eos_token_id")] + [("architecture", ctypes.c_char * 64), ("name", ctypes.c_char * 128)]
+
+
+# Every symbol include/zq_gguf.h declares.
+GGUF_SIGNATURES = {
+    "zq_gguf_open": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_int, ctypes.POINTER(_P), ctypes.c_char_p, _S]),
+    "zq_gguf_open_bytes": (ctypes.c_int, [_P, _S, ctypes.c_int, ctypes.POINTER(_P), ctypes.c_char_p, _S]),
+    "zq_gguf_close": (None, [_P]),
+    "zq_gguf_get_config": (ctypes.c_int, [_P, ctypes.POINTER(GGUFConfig)]),
+    "zq_gguf_tensor_count": (_S, [_P]),
+    "zq_gguf_get_tensor": (ctypes.c_int, [_P, _S, ctypes.POINTER(GGUFTensor)]),
+    "zq_gguf_find_tensor": (ctypes.c_int, [_P, ctypes.c_char_p, ctypes.POINTER(GGUFTensor)]),
+    "zq_gguf_meta_count": (_S, [_P]),
+    "zq_gguf_meta_key": (ctypes.c_char_p, [_P, _S]),
+    "zq_gguf_meta_value": (ctypes.c_char_p, [_P, ctypes.c_char_p]),
+}
+
 _lib = None
 
 
@@ -88,7 +115,7 @@ def lib():
             raise RuntimeError(f"{path} is missing: build it with `python -m zeninfer_amd.build` "
                                "(there is no CPU fallback for this path)")
         L = ctypes.CDLL(path)
-        for name, (res, args) in SIGNATURES.items():
+        for name, (res, args) in {**SIGNATURES, **GGUF_SIGNATURES}.items():
             fn = getattr(L, name)
             fn.restype = res
             fn.argtypes = args
