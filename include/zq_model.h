@@ -1,0 +1,80 @@
+/*
+ * zq_model.h -- C ABI of the device-resident Llama-layout decoder: weights
+ * uploaded once into HBM in their native GGML block layout, KV cache and
+ * activations kept on the device, projections through the zq_hip kernels
+ * (quantised GEMV for decode, int8 or fp32 GEMM for prefill), decode steps
+ * replayed as one HIP graph.
+ *
+ * It replaces the reference's dense runtime for the llama architecture
+ * (include/zen/dense_transformer_runtime.h:20-78;
+ * src/adapters/dense_transformer_runtime.cpp:673 load, :2296 forward_batch,
+ * :3670 forward, :4652 generate) on the path its D3D12 backend accelerates
+ * (include/zen/d3d12_backend.h:174-360).
+ *
+ * Status codes are those of zq_hip.h.  One zq_model is used by one thread at
+ * a time; calls are synchronous (they return once results are on the host).
+ */
+#ifndef ZQ_MODEL_H
+#define ZQ_MODEL_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "zq_gguf.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct zq_model zq_model;
+
+/* Prefill projection arithmetic. */
+#define ZQ_PREFILL_INT8 0 /* per-32 int8 activations: the reference GPU route
+                             (shaders/q8_0_gemm_i8.hlsl, d3d12_backend.cpp:845-854) */
+#define ZQ_PREFILL_F32 1  /* fp32 activations: the reference CPU forward_batch */
+
+/* RuntimeConfig fields of a llama model (include/zen/runtime_types.h:8-40). */
+typedef struct zq_model_config {
+    uint32_t embedding;
+    uint32_t layers;
+    uint32_t heads;
+    uint32_t kv_heads;
+    uint32_t head_dim;
+    uint32_t ffn;
+    uint32_t vocab;
+    uint32_t context;       /* model context length (metadata) */
+    uint32_t max_positions; /* KV-cache capacity allocated on the device */
+    uint32_t rope_dim;
+    float rope_base;
+    float rms_epsilon;
+    uint32_t eos_token;
+    int weight_format;      /* GGML type of the projections (8 = Q8_0) */
+} zq_model_config;
+
+/* Load a llama-architecture GGUF: validate shapes, upload every tensor once.
+ * max_positions bounds prompt + generation (the KV-cache capacity); 0 means
+ * min(context, 4096).  On failure returns < 0 and a message in err. */
+int zq_model_load_gguf(const zq_gguf* gguf, uint32_t max_positions, zq_model_config* cfg_out, zq_model** model,
+                       char* err, size_t err_cap);
+/* A random-init model of the given shape generated directly on the device
+ * (Q8_0 weights with the bench generator, unit norms): the config-4 shape
+ * without an 8.5 GB file.  cfg->max_positions is the KV capacity. */
+int zq_model_create_synthetic(const zq_model_config* cfg, uint64_t seed, zq_model** model, char* err, size_t err_cap);
+void zq_model_free(zq_model* model);
+int zq_model_set_prefill_mode(zq_model* model, int mode);
+/* Prefill `n` tokens from position 0 (the cache is reset).  Logits of the
+ * last token to `logits` (vocab floats, may be NULL); greedy id to *next. */
+int zq_model_prefill(zq_model* model, const uint32_t* tokens, size_t n, float* logits, uint32_t* next);
+/* One decode step at the next position. */
+int zq_model_decode(zq_model* model, uint32_t token, float* logits, uint32_t* next);
+/* Greedy generate (generate(), :4652-4808): prefill, then up to max_new
+ * tokens, stopping after EOS.  Wall times of the two phases in ms. */
+int zq_model_generate(zq_model* model, const uint32_t* prompt, size_t n, uint32_t max_new, uint32_t* out,
+                      size_t* n_out, double* prefill_ms, double* decode_ms);
+/* Device bytes held: weights, KV cache, activations. */
+int zq_model_memory(zq_model* model, uint64_t* weight_bytes, uint64_t* cache_bytes, uint64_t* activation_bytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ZQ_MODEL_H */

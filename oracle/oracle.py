@@ -215,3 +215,61 @@ class Reference:
 
 def reference_available():
     return os.path.exists(REF_PATH)
+
+
+class ReferenceModel:
+    """The reference's own DenseTransformerRuntime (load / forward_batch /
+    forward / generate), compiled from its sources into oracle/_ref.  Test
+    infrastructure: the end-to-end checker of the device-resident model."""
+
+    def __init__(self, path, lib_path=REF_PATH):
+        if not os.path.exists(lib_path):
+            raise RuntimeError(f"reference library missing: {lib_path}")
+        L = ctypes.CDLL(lib_path)
+        L.zr_model_load.restype = _P
+        L.zr_model_load.argtypes = [ctypes.c_char_p, ctypes.c_char_p, _S]
+        L.zr_model_free.argtypes = [_P]
+        L.zr_model_config.argtypes = [_P, _P]
+        L.zr_model_prefill.restype = ctypes.c_int
+        L.zr_model_prefill.argtypes = [_P, _P, _S, _S, _P]
+        L.zr_model_step.restype = ctypes.c_int
+        L.zr_model_step.argtypes = [_P, ctypes.c_uint32, ctypes.c_uint32, _P]
+        L.zr_model_generate.restype = ctypes.c_int
+        L.zr_model_generate.argtypes = [_P, _P, _S, ctypes.c_uint32, _P, _P, _P, _P]
+        self.L = L
+        err = ctypes.create_string_buffer(512)
+        self.h = L.zr_model_load(str(path).encode(), err, 512)
+        if not self.h:
+            raise RuntimeError(f"reference load failed: {err.value.decode()}")
+        c = (ctypes.c_uint32 * 9)()
+        L.zr_model_config(self.h, c)
+        self.config = dict(zip(("embedding", "layers", "heads", "kv_heads", "head_dim", "ffn", "vocab", "context",
+                                "eos"), list(c)))
+
+    def close(self):
+        if self.h:
+            self.L.zr_model_free(self.h)
+            self.h = None
+
+    def prefill(self, tokens, capacity):
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        out = np.empty(self.config["vocab"], np.float32)
+        if not self.L.zr_model_prefill(self.h, _ptr(t), t.size, capacity, _ptr(out)):
+            raise RuntimeError("reference forward_batch failed")
+        return out
+
+    def step(self, token, pos):
+        out = np.empty(self.config["vocab"], np.float32)
+        if not self.L.zr_model_step(self.h, int(token), int(pos), _ptr(out)):
+            raise RuntimeError("reference forward failed")
+        return out
+
+    def generate(self, prompt, max_new):
+        p = np.ascontiguousarray(prompt, dtype=np.uint32)
+        out = np.empty(max(max_new, 1), np.uint32)
+        n = ctypes.c_size_t()
+        pm, dm = ctypes.c_double(), ctypes.c_double()
+        if not self.L.zr_model_generate(self.h, _ptr(p), p.size, max_new, _ptr(out), ctypes.byref(n),
+                                        ctypes.byref(pm), ctypes.byref(dm)):
+            raise RuntimeError("reference generate failed")
+        return out[:n.value].tolist(), pm.value, dm.value

@@ -10,6 +10,7 @@ import pytest
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "zq_hip.h")
 GGUF_HEADER = os.path.join(ROOT, "include", "zq_gguf.h")
+MODEL_HEADER = os.path.join(ROOT, "include", "zq_model.h")
 
 
 def declared_symbols(header=HEADER):
@@ -35,6 +36,10 @@ def test_library_exports_every_declared_symbol():
     missing = [s for s in gguf if not hasattr(lib, s)]
     assert not missing, missing
     assert set(gguf) == set(zq.GGUF_SIGNATURES), "Python binding out of sync with include/zq_gguf.h"
+    model = declared_symbols(MODEL_HEADER)
+    missing = [s for s in model if not hasattr(lib, s)]
+    assert not missing, missing
+    assert set(model) == set(zq.MODEL_SIGNATURES), "Python binding out of sync with include/zq_model.h"
 
 
 def test_layout_helpers_without_device():

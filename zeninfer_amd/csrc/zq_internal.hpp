@@ -51,3 +51,21 @@ hipError_t launch_synth_weights(int fmt, uint64_t seed, uint8_t* w, size_t rows,
 hipError_t launch_synth_normal(uint64_t seed, float* out, size_t n, hipStream_t stream);
 
 }  // namespace zq
+
+namespace zq {
+// Decoder-layer kernels (zq_layer.hip).  Token ids and the first position are
+// read from device memory, so a captured decode step replays unchanged.
+hipError_t launch_embed(int fmt, const void* table, const uint32_t* tokens, uint32_t vocab, float* x, uint32_t E,
+                        uint32_t T, hipStream_t stream);
+hipError_t launch_rmsnorm(const float* x, const float* w, float* y, uint32_t rows, uint32_t n, float eps,
+                          hipStream_t stream);
+hipError_t launch_rope_kv(float* q, const float* k, const float* v, float* kc, float* vc, const float* cos_tab,
+                          const float* sin_tab, const uint32_t* pos0, uint32_t T, uint32_t H, uint32_t KH, uint32_t D,
+                          uint32_t pairs, bool adjacent, hipStream_t stream);
+hipError_t launch_attention(const float* q, const float* kc, const float* vc, float* out, const uint32_t* pos0,
+                            uint32_t T, uint32_t H, uint32_t KH, uint32_t D, uint32_t max_pos, float scale,
+                            hipStream_t stream);
+hipError_t launch_add(float* x, const float* y, size_t n, hipStream_t stream);
+hipError_t launch_argmax(const float* x, uint32_t n, uint32_t* out, hipStream_t stream);
+hipError_t launch_silu_mul(const float* gate, const float* up, float* out, size_t n, hipStream_t stream);
+}  // namespace zq

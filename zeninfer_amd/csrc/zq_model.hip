@@ -1,0 +1,603 @@
+// zq_model.hip -- the device-resident Llama-layout decoder behind
+// include/zq_model.h.
+//
+// Everything a forward pass touches lives in HBM: the weights in their native
+// GGML blocks (one arena, uploaded once from the mapped GGUF), the fp32 KV
+// cache, the RoPE cos/sin table, the activations and the GEMM workspace.  The
+// host only sends token ids and positions (4-byte copies) and reads back ids
+// and, on request, logits.  A decode step is captured once as a HIP graph and
+// replayed: token id and position are read by the kernels from device memory,
+// so the graph never changes.
+//
+// Forward semantics follow the reference runtime's llama path
+// (src/adapters/dense_transformer_runtime.cpp of the reference):
+//   load (:673-925): llama metadata keys, head_dim = embedding / heads,
+//     rope.dimension_count (default head_dim), rope.freq_base (default 1e4),
+//     attention.layer_norm_rms_epsilon (default 1e-5), output.weight falling
+//     back to token_embd.weight, adjacent RoPE pairs for llama;
+//   forward (:3670-4606) / forward_batch (:2296-): embed -> per layer
+//     { x += W_o . attn(rope(W_q h), rope(W_k h), W_v h), h = rms(x) ;
+//       x += W_down . (silu(W_gate h) * W_up h), h = rms(x) } -> rms -> W_out;
+//   generate (:4652-4808): prefill, then greedy tokens until EOS or max_new.
+#include "../../include/zq_hip.h"
+#include "../../include/zq_model.h"
+#include "zq_device.hpp"
+#include "zq_internal.hpp"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+namespace {
+
+constexpr uint32_t kPrefillChunk = 1024;  // tokens per prefill pass (activations sized for this)
+constexpr size_t kAlign = 256;
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+struct Weight {
+    const uint8_t* p = nullptr;
+    int fmt = 0;
+    uint32_t rows = 0, cols = 0;
+};
+
+struct Layer {
+    Weight q, k, v, o, gate, up, down;
+    const float* attn_norm = nullptr;
+    const float* ffn_norm = nullptr;
+    float* kc = nullptr;
+    float* vc = nullptr;
+};
+
+}  // namespace
+
+struct zq_model {
+    zq_model_config cfg{};
+    int prefill_mode = ZQ_PREFILL_INT8;
+    hipStream_t stream = nullptr;
+    std::vector<void*> allocs;
+    uint64_t weight_bytes = 0, cache_bytes = 0, act_bytes = 0;
+
+    std::vector<Layer> layers;
+    Weight embd, out;
+    const float* out_norm = nullptr;
+    float* cos_tab = nullptr;
+    float* sin_tab = nullptr;
+    uint32_t pairs = 0;
+    float attn_scale = 1.0f;
+
+    // device scalars and host mirrors (pinned)
+    uint32_t* tokens_dev = nullptr;  // kPrefillChunk ids
+    uint32_t* pos_dev = nullptr;
+    uint32_t* next_dev = nullptr;
+    uint32_t* host_small = nullptr;  // [0] pos, [1] next, [2..] token staging
+
+    // activations (rows = kPrefillChunk)
+    float *x = nullptr, *h = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *tmp = nullptr;
+    float *gate = nullptr, *up = nullptr, *act = nullptr, *logits = nullptr;
+    int8_t* xq = nullptr;
+    float* xs = nullptr;
+    float* partial = nullptr;
+
+    uint32_t cur_pos = 0;  // positions held in the cache
+    bool use_graph = true;
+    hipGraphExec_t decode_exec = nullptr;
+    hipGraph_t decode_graph = nullptr;
+
+    ~zq_model() {
+        if (stream) (void)hipStreamSynchronize(stream);
+        if (decode_exec) (void)hipGraphExecDestroy(decode_exec);
+        if (decode_graph) (void)hipGraphDestroy(decode_graph);
+        for (void* p : allocs) (void)hipFree(p);
+        if (host_small) (void)hipHostFree(host_small);
+        if (stream) (void)hipStreamDestroy(stream);
+    }
+};
+
+namespace {
+
+void set_err(char* err, size_t cap, const std::string& m) {
+    if (err && cap) std::snprintf(err, cap, "%s", m.c_str());
+}
+
+// The reference's rope_table for the unscaled / linear cases (:260-284): angle
+// = position * base^(-2i/rotary_dim) in float, cos/sin in float.
+void build_rope_table(uint32_t positions, uint32_t rotary_dim, float base, float linear_factor, std::vector<float>& cs,
+                      std::vector<float>& sn) {
+    rotary_dim -= rotary_dim % 2;
+    const uint32_t half = rotary_dim / 2;
+    cs.resize(size_t(positions) * half);
+    sn.resize(size_t(positions) * half);
+    std::vector<float> freq(half);
+    for (uint32_t i = 0; i < half; ++i) freq[i] = std::pow(base, -2.0f * float(i) / float(rotary_dim));
+    for (uint32_t p = 0; p < positions; ++p)
+        for (uint32_t i = 0; i < half; ++i) {
+            float position = float(p);
+            if (linear_factor > 0.0f) position /= std::max(1.0f, linear_factor);
+            const float angle = position * freq[i];
+            cs[size_t(p) * half + i] = std::cos(angle);
+            sn[size_t(p) * half + i] = std::sin(angle);
+        }
+}
+
+bool dev_alloc(zq_model& m, void** p, size_t bytes) {
+    if (hipMalloc(p, std::max<size_t>(bytes, 1)) != hipSuccess) return false;
+    m.allocs.push_back(*p);
+    return true;
+}
+
+// Activation buffers, GEMM workspace, device scalars, KV cache, RoPE table.
+bool alloc_runtime(zq_model& m, std::string& e) {
+    const auto& c = m.cfg;
+    const size_t T = kPrefillChunk, E = c.embedding, QW = size_t(c.heads) * c.head_dim,
+                 KW = size_t(c.kv_heads) * c.head_dim, F = c.ffn;
+    const size_t widest = std::max({E, QW, F});
+    struct B { float** p; size_t n; };
+    const B bufs[] = {{&m.x, T * E}, {&m.h, T * E}, {&m.q, T * QW}, {&m.k, T * KW}, {&m.v, T * KW}, {&m.att, T * QW},
+                      {&m.tmp, T * E}, {&m.gate, T * F}, {&m.up, T * F}, {&m.act, T * F}, {&m.logits, c.vocab}};
+    size_t total = 0;
+    for (const B& b : bufs) total += align_up(b.n * 4, kAlign);
+    // int8 activations + scales + split-K partials for the widest projection
+    size_t partial = 0;
+    for (uint32_t M = 1; M <= kPrefillChunk; ++M)
+        for (auto nk : {std::pair<size_t, size_t>{QW, E}, {KW, E}, {E, QW}, {F, E}, {E, F}})
+            partial = std::max(partial, zq::gemm_i8_partial_bytes(M, nk.first, nk.second));
+    const size_t xq_bytes = align_up(T * widest, kAlign), xs_bytes = align_up(T * widest / 32 * 4, kAlign);
+    total += xq_bytes + xs_bytes + align_up(partial, kAlign) + 3 * kAlign + align_up(T * 4, kAlign);
+    void* arena;
+    if (!dev_alloc(m, &arena, total)) { e = "device allocation failed (activations)"; return false; }
+    m.act_bytes = total;
+    uint8_t* p = static_cast<uint8_t*>(arena);
+    for (const B& b : bufs) { *b.p = reinterpret_cast<float*>(p); p += align_up(b.n * 4, kAlign); }
+    m.xq = reinterpret_cast<int8_t*>(p); p += xq_bytes;
+    m.xs = reinterpret_cast<float*>(p); p += xs_bytes;
+    m.partial = partial ? reinterpret_cast<float*>(p) : nullptr; p += align_up(partial, kAlign);
+    m.pos_dev = reinterpret_cast<uint32_t*>(p); p += kAlign;
+    m.next_dev = reinterpret_cast<uint32_t*>(p); p += kAlign;
+    p += kAlign;
+    m.tokens_dev = reinterpret_cast<uint32_t*>(p);
+
+    // KV cache: [layer][position][kv_heads * head_dim] for K and V
+    const size_t per = size_t(c.max_positions) * KW * 4;
+    void* kv;
+    if (!dev_alloc(m, &kv, 2 * per * c.layers)) { e = "device allocation failed (KV cache)"; return false; }
+    m.cache_bytes = 2 * per * c.layers;
+    for (uint32_t l = 0; l < c.layers; ++l) {
+        m.layers[l].kc = reinterpret_cast<float*>(static_cast<uint8_t*>(kv) + 2 * l * per);
+        m.layers[l].vc = reinterpret_cast<float*>(static_cast<uint8_t*>(kv) + (2 * l + 1) * per);
+    }
+    // RoPE table
+    std::vector<float> cs, sn;
+    build_rope_table(c.max_positions, c.rope_dim, c.rope_base, 0.0f, cs, sn);
+    m.pairs = c.rope_dim / 2;
+    void* rt;
+    if (!dev_alloc(m, &rt, 2 * cs.size() * 4)) { e = "device allocation failed (RoPE table)"; return false; }
+    m.cos_tab = static_cast<float*>(rt);
+    m.sin_tab = m.cos_tab + cs.size();
+    if (hipMemcpy(m.cos_tab, cs.data(), cs.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(m.sin_tab, sn.data(), sn.size() * 4, hipMemcpyHostToDevice) != hipSuccess) {
+        e = "RoPE table upload failed";
+        return false;
+    }
+    if (hipHostMalloc(reinterpret_cast<void**>(&m.host_small), (8 + kPrefillChunk) * 4) != hipSuccess) {
+        e = "pinned allocation failed";
+        return false;
+    }
+    m.attn_scale = 1.0f / std::sqrt(float(c.head_dim));
+    return true;
+}
+
+bool init_common(zq_model& m, std::string& e) {
+    const auto& c = m.cfg;
+    if (!c.embedding || !c.layers || !c.heads || !c.kv_heads || !c.head_dim || !c.ffn || !c.vocab || !c.max_positions) {
+        e = "invalid model dimensions";
+        return false;
+    }
+    if (c.heads % c.kv_heads) { e = "heads must be a multiple of kv_heads"; return false; }
+    if (c.head_dim % 64 || c.head_dim > 256) { e = "head_dim must be a multiple of 64, at most 256"; return false; }
+    if (c.rope_dim == 0 || c.rope_dim > c.head_dim || c.rope_dim % 2) { e = "Invalid rotary dimension"; return false; }
+    if (size_t(c.max_positions) * 4 > 96 * 1024) { e = "max_positions above 24576"; return false; }
+    if (c.embedding % 32 || c.ffn % 32 || (size_t(c.heads) * c.head_dim) % 32) { e = "dimensions must divide into 32-blocks"; return false; }
+    if (zq_hip_init() != ZQ_OK) { e = "no usable gfx950 device"; return false; }
+    if (hipStreamCreateWithFlags(&m.stream, hipStreamNonBlocking) != hipSuccess) { e = "stream creation failed"; return false; }
+    const char* g = std::getenv("ZQ_MODEL_GRAPH");
+    m.use_graph = !(g && g[0] == '0');
+    m.layers.resize(c.layers);
+    return true;
+}
+
+// y[M][N] = X[M][K] . W^T through the GEMM (prefill) -- X already quantised
+// into xq/xs when `quantized` (int8 mode).
+hipError_t project(zq_model& m, const Weight& w, const float* X, float* Y, uint32_t M, bool quantized) {
+    if (quantized) return zq::launch_gemm_i8(w.fmt, w.p, m.xq, m.xs, Y, m.partial, M, w.rows, w.cols, m.stream);
+    return zq::launch_gemm_f32(w.fmt, w.p, X, Y, M, w.rows, w.cols, m.stream);
+}
+
+bool int8_ok(int fmt) { return fmt == zq::kQ8_0 || fmt == zq::kQ4_0; }
+
+// Quantise X[M][K] once for every projection that reads it in int8 mode.
+hipError_t quantize_for(zq_model& m, std::initializer_list<const Weight*> ws, const float* X, uint32_t M, uint32_t K,
+                        bool& quantized) {
+    quantized = m.prefill_mode == ZQ_PREFILL_INT8;
+    for (const Weight* w : ws) quantized = quantized && int8_ok(w->fmt);
+    if (!quantized) return hipSuccess;
+    return zq::launch_quantize_acts(X, m.xq, m.xs, M, K, m.stream);
+}
+
+#define HIPCHK(x)                              \
+    do {                                       \
+        const hipError_t e_ = (x);             \
+        if (e_ != hipSuccess) return e_;       \
+    } while (0)
+
+// Decoder layers over T tokens at positions pos0 .. pos0+T-1 (pos0 in device
+// memory); x holds the embeddings on entry and the residual stream on exit.
+hipError_t enqueue_layers(zq_model& m, uint32_t T) {
+    const auto& c = m.cfg;
+    const uint32_t E = c.embedding, QW = c.heads * c.head_dim, KW = c.kv_heads * c.head_dim, F = c.ffn;
+    for (uint32_t l = 0; l < c.layers; ++l) {
+        Layer& L = m.layers[l];
+        HIPCHK(zq::launch_rmsnorm(m.x, L.attn_norm, m.h, T, E, c.rms_epsilon, m.stream));
+        if (T == 1) {
+            // decode: the three projections share x -> one batched GEMV per format
+            zq::GemvTask t[3] = {{L.q.p, m.q, QW}, {L.k.p, m.k, KW}, {L.v.p, m.v, KW}};
+            if (L.q.fmt == L.k.fmt && L.k.fmt == L.v.fmt) {
+                HIPCHK(zq::launch_gemv(L.q.fmt, t, 3, m.h, E, m.stream));
+            } else {
+                HIPCHK(zq::launch_gemv(L.q.fmt, &t[0], 1, m.h, E, m.stream));
+                HIPCHK(zq::launch_gemv(L.k.fmt, &t[1], 1, m.h, E, m.stream));
+                HIPCHK(zq::launch_gemv(L.v.fmt, &t[2], 1, m.h, E, m.stream));
+            }
+        } else {
+            bool qz;
+            HIPCHK(quantize_for(m, {&L.q, &L.k, &L.v}, m.h, T, E, qz));
+            HIPCHK(project(m, L.q, m.h, m.q, T, qz));
+            HIPCHK(project(m, L.k, m.h, m.k, T, qz));
+            HIPCHK(project(m, L.v, m.h, m.v, T, qz));
+        }
+        HIPCHK(zq::launch_rope_kv(m.q, m.k, m.v, L.kc, L.vc, m.cos_tab, m.sin_tab, m.pos_dev, T, c.heads, c.kv_heads,
+                                  c.head_dim, m.pairs, true, m.stream));
+        HIPCHK(zq::launch_attention(m.q, L.kc, L.vc, m.att, m.pos_dev, T, c.heads, c.kv_heads, c.head_dim,
+                                    c.max_positions, m.attn_scale, m.stream));
+        if (T == 1) {
+            zq::GemvTask t = {L.o.p, m.tmp, E};
+            HIPCHK(zq::launch_gemv(L.o.fmt, &t, 1, m.att, QW, m.stream));
+        } else {
+            bool qz;
+            HIPCHK(quantize_for(m, {&L.o}, m.att, T, QW, qz));
+            HIPCHK(project(m, L.o, m.att, m.tmp, T, qz));
+        }
+        HIPCHK(zq::launch_add(m.x, m.tmp, size_t(T) * E, m.stream));
+        HIPCHK(zq::launch_rmsnorm(m.x, L.ffn_norm, m.h, T, E, c.rms_epsilon, m.stream));
+        if (T == 1) {
+            zq::GemvTask t[2] = {{L.gate.p, m.gate, F}, {L.up.p, m.up, F}};
+            if (L.gate.fmt == L.up.fmt) {
+                HIPCHK(zq::launch_gemv(L.gate.fmt, t, 2, m.h, E, m.stream));
+            } else {
+                HIPCHK(zq::launch_gemv(L.gate.fmt, &t[0], 1, m.h, E, m.stream));
+                HIPCHK(zq::launch_gemv(L.up.fmt, &t[1], 1, m.h, E, m.stream));
+            }
+        } else {
+            bool qz;
+            HIPCHK(quantize_for(m, {&L.gate, &L.up}, m.h, T, E, qz));
+            HIPCHK(project(m, L.gate, m.h, m.gate, T, qz));
+            HIPCHK(project(m, L.up, m.h, m.up, T, qz));
+        }
+        HIPCHK(zq::launch_silu_mul(m.gate, m.up, m.act, size_t(T) * F, m.stream));
+        if (T == 1) {
+            zq::GemvTask t = {L.down.p, m.tmp, E};
+            HIPCHK(zq::launch_gemv(L.down.fmt, &t, 1, m.act, F, m.stream));
+        } else {
+            bool qz;
+            HIPCHK(quantize_for(m, {&L.down}, m.act, T, F, qz));
+            HIPCHK(project(m, L.down, m.act, m.tmp, T, qz));
+        }
+        HIPCHK(zq::launch_add(m.x, m.tmp, size_t(T) * E, m.stream));
+    }
+    return hipSuccess;
+}
+
+// Final norm of row `row`, the output projection and the greedy id.
+hipError_t enqueue_head(zq_model& m, uint32_t row) {
+    const auto& c = m.cfg;
+    HIPCHK(zq::launch_rmsnorm(m.x + size_t(row) * c.embedding, m.out_norm, m.h, 1, c.embedding, c.rms_epsilon, m.stream));
+    zq::GemvTask t = {m.out.p, m.logits, c.vocab};
+    HIPCHK(zq::launch_gemv(m.out.fmt, &t, 1, m.h, c.embedding, m.stream));
+    return zq::launch_argmax(m.logits, c.vocab, m.next_dev, m.stream);
+}
+
+hipError_t enqueue_decode(zq_model& m) {
+    HIPCHK(zq::launch_embed(m.embd.fmt, m.embd.p, m.tokens_dev, m.cfg.vocab, m.x, m.cfg.embedding, 1, m.stream));
+    HIPCHK(enqueue_layers(m, 1));
+    return enqueue_head(m, 0);
+}
+
+int finish_outputs(zq_model& m, float* logits, uint32_t* next) {
+    if (hipMemcpyAsync(&m.host_small[1], m.next_dev, 4, hipMemcpyDeviceToHost, m.stream) != hipSuccess) return ZQ_ERR_HIP;
+    if (logits && hipMemcpyAsync(logits, m.logits, size_t(m.cfg.vocab) * 4, hipMemcpyDeviceToHost, m.stream) != hipSuccess)
+        return ZQ_ERR_HIP;
+    if (hipStreamSynchronize(m.stream) != hipSuccess) return ZQ_ERR_HIP;
+    if (next) *next = m.host_small[1];
+    return ZQ_OK;
+}
+
+int prefill(zq_model& m, const uint32_t* tokens, size_t n, float* logits, uint32_t* next) {
+    if (!tokens || !n || n > m.cfg.max_positions) return ZQ_ERR_ARG;
+    for (size_t i = 0; i < n; ++i)
+        if (tokens[i] >= m.cfg.vocab) return ZQ_ERR_ARG;
+    m.cur_pos = 0;
+    for (size_t s = 0; s < n; s += kPrefillChunk) {
+        const uint32_t T = uint32_t(std::min<size_t>(kPrefillChunk, n - s));
+        m.host_small[0] = uint32_t(s);
+        std::memcpy(&m.host_small[8], tokens + s, size_t(T) * 4);
+        if (hipMemcpyAsync(m.pos_dev, &m.host_small[0], 4, hipMemcpyHostToDevice, m.stream) != hipSuccess ||
+            hipMemcpyAsync(m.tokens_dev, &m.host_small[8], size_t(T) * 4, hipMemcpyHostToDevice, m.stream) != hipSuccess)
+            return ZQ_ERR_HIP;
+        if (zq::launch_embed(m.embd.fmt, m.embd.p, m.tokens_dev, m.cfg.vocab, m.x, m.cfg.embedding, T, m.stream) != hipSuccess ||
+            enqueue_layers(m, T) != hipSuccess)
+            return ZQ_ERR_HIP;
+        if (s + T == n && enqueue_head(m, T - 1) != hipSuccess) return ZQ_ERR_HIP;
+        // the staging words are reused by the next chunk: wait for the copies
+        if (s + T < n && hipStreamSynchronize(m.stream) != hipSuccess) return ZQ_ERR_HIP;
+    }
+    m.cur_pos = uint32_t(n);
+    return finish_outputs(m, logits, next);
+}
+
+int decode(zq_model& m, uint32_t token, float* logits, uint32_t* next) {
+    if (token >= m.cfg.vocab || m.cur_pos >= m.cfg.max_positions) return ZQ_ERR_ARG;
+    m.host_small[0] = m.cur_pos;
+    m.host_small[8] = token;
+    if (hipMemcpyAsync(m.pos_dev, &m.host_small[0], 4, hipMemcpyHostToDevice, m.stream) != hipSuccess ||
+        hipMemcpyAsync(m.tokens_dev, &m.host_small[8], 4, hipMemcpyHostToDevice, m.stream) != hipSuccess)
+        return ZQ_ERR_HIP;
+    if (m.use_graph) {
+        if (!m.decode_exec) {
+            if (hipStreamBeginCapture(m.stream, hipStreamCaptureModeThreadLocal) != hipSuccess) return ZQ_ERR_HIP;
+            const hipError_t e = enqueue_decode(m);
+            hipGraph_t g = nullptr;
+            const hipError_t e2 = hipStreamEndCapture(m.stream, &g);
+            if (e != hipSuccess || e2 != hipSuccess || !g) {
+                if (g) (void)hipGraphDestroy(g);
+                return ZQ_ERR_HIP;
+            }
+            m.decode_graph = g;
+            if (hipGraphInstantiate(&m.decode_exec, g, nullptr, nullptr, 0) != hipSuccess) {
+                m.decode_exec = nullptr;
+                return ZQ_ERR_HIP;
+            }
+        }
+        if (hipGraphLaunch(m.decode_exec, m.stream) != hipSuccess) return ZQ_ERR_HIP;
+    } else if (enqueue_decode(m) != hipSuccess) {
+        return ZQ_ERR_HIP;
+    }
+    const int st = finish_outputs(m, logits, next);
+    if (st == ZQ_OK) ++m.cur_pos;
+    return st;
+}
+
+}  // namespace
+
+extern "C" {
+
+int zq_model_load_gguf(const zq_gguf* g, uint32_t max_positions, zq_model_config* cfg_out, zq_model** model,
+                       char* err, size_t err_cap) {
+    if (!g || !model) return ZQ_ERR_ARG;
+    *model = nullptr;
+    zq_gguf_config gc;
+    zq_gguf_get_config(g, &gc);
+    auto fail = [&](const std::string& m, int st = ZQ_ERR_ARG) { set_err(err, err_cap, m); return st; };
+    if (std::strcmp(gc.architecture, "llama") != 0) return fail("only the llama architecture is supported");
+    auto meta_f = [&](const char* k, float fb) {
+        const char* v = zq_gguf_meta_value(g, k);
+        if (!v) return fb;
+        char* end = nullptr;
+        const float f = std::strtof(v, &end);
+        return end != v ? f : fb;
+    };
+    auto meta_u = [&](const char* k, uint32_t fb) {
+        const char* v = zq_gguf_meta_value(g, k);
+        if (!v) return fb;
+        char* end = nullptr;
+        const unsigned long u = std::strtoul(v, &end, 10);
+        return end != v ? uint32_t(u) : fb;
+    };
+    auto* m = new zq_model;
+    zq_model_config& c = m->cfg;
+    c.embedding = gc.embedding_length;
+    c.layers = gc.block_count;
+    c.heads = gc.head_count;
+    c.kv_heads = gc.head_count_kv ? gc.head_count_kv : gc.head_count;
+    c.ffn = gc.feed_forward_length;
+    c.context = gc.context_length;
+    c.head_dim = c.heads ? meta_u("llama.attention.key_length", 0) : 0;
+    if (!c.head_dim && c.heads) c.head_dim = c.embedding / c.heads;
+    c.rope_dim = meta_u("llama.rope.dimension_count", c.head_dim);
+    c.rope_base = meta_f("llama.rope.freq_base", 10000.0f);
+    c.rms_epsilon = meta_f("llama.attention.layer_norm_rms_epsilon", 1.0e-5f);
+    c.eos_token = gc.eos_token_id;
+    c.max_positions = max_positions ? max_positions : std::min<uint32_t>(c.context ? c.context : 4096, 4096);
+    if (c.context && c.max_positions > c.context) c.max_positions = c.context;
+    if (zq_gguf_meta_value(g, "llama.rope.scaling.type")) {
+        const std::string st = zq_gguf_meta_value(g, "llama.rope.scaling.type");
+        if (!st.empty() && st != "none") { delete m; return fail("RoPE scaling type not supported: " + st); }
+    }
+    // vocab from the embedding table
+    zq_gguf_tensor te, to, tn;
+    if (zq_gguf_find_tensor(g, "token_embd.weight", &te) != ZQ_OK) { delete m; return fail("missing token_embd.weight"); }
+    c.vocab = te.n_dims == 2 ? uint32_t(te.dims[1]) : 0;
+    const bool tied = zq_gguf_find_tensor(g, "output.weight", &to) != ZQ_OK;
+    if (tied) to = te;
+    if (zq_gguf_find_tensor(g, "output_norm.weight", &tn) != ZQ_OK) { delete m; return fail("missing output_norm.weight"); }
+    std::string e;
+    if (!init_common(*m, e)) { delete m; return fail(e, ZQ_ERR_NO_DEVICE); }
+    const uint32_t E = c.embedding, QW = c.heads * c.head_dim, KW = c.kv_heads * c.head_dim, F = c.ffn;
+
+    // collect every tensor with its expected shape
+    struct Need { std::string name; uint32_t rows, cols; Weight* w; const float** f32; };
+    std::vector<Need> needs;
+    needs.push_back({"token_embd.weight", c.vocab, E, &m->embd, nullptr});
+    needs.push_back({tied ? "token_embd.weight" : "output.weight", c.vocab, E, &m->out, nullptr});
+    needs.push_back({"output_norm.weight", 1, E, nullptr, &m->out_norm});
+    for (uint32_t l = 0; l < c.layers; ++l) {
+        const std::string p = "blk." + std::to_string(l) + ".";
+        Layer& L = m->layers[l];
+        needs.push_back({p + "attn_norm.weight", 1, E, nullptr, &L.attn_norm});
+        needs.push_back({p + "ffn_norm.weight", 1, E, nullptr, &L.ffn_norm});
+        needs.push_back({p + "attn_q.weight", QW, E, &L.q, nullptr});
+        needs.push_back({p + "attn_k.weight", KW, E, &L.k, nullptr});
+        needs.push_back({p + "attn_v.weight", KW, E, &L.v, nullptr});
+        needs.push_back({p + "attn_output.weight", E, QW, &L.o, nullptr});
+        needs.push_back({p + "ffn_gate.weight", F, E, &L.gate, nullptr});
+        needs.push_back({p + "ffn_up.weight", F, E, &L.up, nullptr});
+        needs.push_back({p + "ffn_down.weight", E, F, &L.down, nullptr});
+    }
+    std::vector<zq_gguf_tensor> ts(needs.size());
+    size_t arena = 0;
+    for (size_t i = 0; i < needs.size(); ++i) {
+        const Need& n = needs[i];
+        if (zq_gguf_find_tensor(g, n.name.c_str(), &ts[i]) != ZQ_OK) { delete m; return fail("missing tensor " + n.name); }
+        const zq_gguf_tensor& t = ts[i];
+        const uint64_t rows = t.n_dims >= 2 ? t.dims[1] : 1;
+        if (t.dims[0] != n.cols || rows != n.rows || t.n_dims > 2) { delete m; return fail("unexpected shape of " + n.name); }
+        if (n.f32 && t.ggml_type != 0) { delete m; return fail("norm tensors must be F32: " + n.name); }
+        if (n.w) {
+            const bool embd = n.w == &m->embd;
+            const int ty = int(t.ggml_type);
+            if (embd ? !(ty == zq::kQ8_0 || ty == 0) : !(ty == zq::kQ8_0 || ty == zq::kQ4_0 || ty == zq::kQ6_K)) {
+                delete m;
+                return fail("unsupported tensor type " + std::to_string(ty) + " for " + n.name);
+            }
+            if (n.w == &m->out && !(ty == zq::kQ8_0 || ty == zq::kQ4_0 || ty == zq::kQ6_K)) {
+                delete m;
+                return fail("output projection must be Q8_0, Q4_0 or Q6_K");
+            }
+        }
+        arena += align_up(size_t(t.byte_size) + ZQ_WEIGHT_TAIL_PAD, kAlign);
+    }
+    void* base;
+    if (!dev_alloc(*m, &base, arena)) { delete m; return fail("device allocation failed (weights)", ZQ_ERR_OOM); }
+    m->weight_bytes = arena;
+    uint8_t* p = static_cast<uint8_t*>(base);
+    for (size_t i = 0; i < needs.size(); ++i) {
+        const zq_gguf_tensor& t = ts[i];
+        if (hipMemcpy(p, t.data, size_t(t.byte_size), hipMemcpyHostToDevice) != hipSuccess) {
+            delete m;
+            return fail("weight upload failed", ZQ_ERR_HIP);
+        }
+        const Need& n = needs[i];
+        if (n.w) *n.w = Weight{p, int(t.ggml_type), n.rows, n.cols};
+        if (n.f32) *n.f32 = reinterpret_cast<const float*>(p);
+        p += align_up(size_t(t.byte_size) + ZQ_WEIGHT_TAIL_PAD, kAlign);
+    }
+    c.weight_format = m->layers.empty() ? m->out.fmt : m->layers[0].q.fmt;
+    if (!alloc_runtime(*m, e)) { delete m; return fail(e, ZQ_ERR_OOM); }
+    if (cfg_out) *cfg_out = c;
+    *model = m;
+    set_err(err, err_cap, "");
+    return ZQ_OK;
+}
+
+int zq_model_create_synthetic(const zq_model_config* cfg, uint64_t seed, zq_model** model, char* err, size_t err_cap) {
+    if (!cfg || !model) return ZQ_ERR_ARG;
+    *model = nullptr;
+    auto* m = new zq_model;
+    m->cfg = *cfg;
+    zq_model_config& c = m->cfg;
+    if (!c.head_dim && c.heads) c.head_dim = c.embedding / c.heads;
+    if (!c.rope_dim) c.rope_dim = c.head_dim;
+    if (!c.rope_base) c.rope_base = 10000.0f;
+    if (!c.rms_epsilon) c.rms_epsilon = 1e-5f;
+    c.weight_format = zq::kQ8_0;
+    std::string e;
+    if (!init_common(*m, e)) { delete m; set_err(err, err_cap, e); return ZQ_ERR_NO_DEVICE; }
+    const uint32_t E = c.embedding, QW = c.heads * c.head_dim, KW = c.kv_heads * c.head_dim, F = c.ffn;
+    struct W { Weight* w; uint32_t rows, cols; };
+    std::vector<W> ws = {{&m->embd, c.vocab, E}, {&m->out, c.vocab, E}};
+    for (auto& L : m->layers)
+        for (auto x : {W{&L.q, QW, E}, W{&L.k, KW, E}, W{&L.v, KW, E}, W{&L.o, E, QW}, W{&L.gate, F, E},
+                       W{&L.up, F, E}, W{&L.down, E, F}})
+            ws.push_back(x);
+    size_t arena = align_up(size_t(E) * 4, kAlign);  // one shared unit norm vector
+    for (const W& w : ws) arena += align_up(zq_weight_bytes(zq::kQ8_0, w.rows, w.cols), kAlign);
+    void* base;
+    if (!dev_alloc(*m, &base, arena)) { delete m; set_err(err, err_cap, "device allocation failed (weights)"); return ZQ_ERR_OOM; }
+    m->weight_bytes = arena;
+    uint8_t* p = static_cast<uint8_t*>(base);
+    std::vector<float> ones(E, 1.0f);
+    if (hipMemcpy(p, ones.data(), size_t(E) * 4, hipMemcpyHostToDevice) != hipSuccess) { delete m; return ZQ_ERR_HIP; }
+    const float* unit = reinterpret_cast<const float*>(p);
+    p += align_up(size_t(E) * 4, kAlign);
+    m->out_norm = unit;
+    for (auto& L : m->layers) L.attn_norm = L.ffn_norm = unit;
+    uint64_t s = seed;
+    for (const W& w : ws) {
+        *w.w = Weight{p, zq::kQ8_0, w.rows, w.cols};
+        if (zq::launch_synth_weights(zq::kQ8_0, s++, p, w.rows, w.cols, m->stream) != hipSuccess) { delete m; return ZQ_ERR_HIP; }
+        p += align_up(zq_weight_bytes(zq::kQ8_0, w.rows, w.cols), kAlign);
+    }
+    if (hipStreamSynchronize(m->stream) != hipSuccess) { delete m; return ZQ_ERR_HIP; }
+    if (!alloc_runtime(*m, e)) { delete m; set_err(err, err_cap, e); return ZQ_ERR_OOM; }
+    *model = m;
+    set_err(err, err_cap, "");
+    return ZQ_OK;
+}
+
+void zq_model_free(zq_model* m) { delete m; }
+
+int zq_model_set_prefill_mode(zq_model* m, int mode) {
+    if (!m || (mode != ZQ_PREFILL_INT8 && mode != ZQ_PREFILL_F32)) return ZQ_ERR_ARG;
+    m->prefill_mode = mode;
+    return ZQ_OK;
+}
+
+int zq_model_prefill(zq_model* m, const uint32_t* tokens, size_t n, float* logits, uint32_t* next) {
+    if (!m) return ZQ_ERR_ARG;
+    return prefill(*m, tokens, n, logits, next);
+}
+
+int zq_model_decode(zq_model* m, uint32_t token, float* logits, uint32_t* next) {
+    if (!m) return ZQ_ERR_ARG;
+    return decode(*m, token, logits, next);
+}
+
+int zq_model_generate(zq_model* m, const uint32_t* prompt, size_t n, uint32_t max_new, uint32_t* out, size_t* n_out,
+                      double* prefill_ms, double* decode_ms) {
+    if (!m || !prompt || !n || (max_new && !out) || !n_out) return ZQ_ERR_ARG;
+    if (n + max_new > m->cfg.max_positions) return ZQ_ERR_ARG;
+    using clk = std::chrono::steady_clock;
+    const auto t0 = clk::now();
+    uint32_t next = 0;
+    int st = prefill(*m, prompt, n, nullptr, &next);
+    if (st != ZQ_OK) return st;
+    const auto t1 = clk::now();
+    size_t count = 0;
+    for (uint32_t i = 0; i < max_new; ++i) {
+        out[count++] = next;
+        if (next == m->cfg.eos_token || i + 1 == max_new) break;
+        st = decode(*m, next, nullptr, &next);
+        if (st != ZQ_OK) return st;
+    }
+    const auto t2 = clk::now();
+    *n_out = count;
+    if (prefill_ms) *prefill_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
+    if (decode_ms) *decode_ms = std::chrono::duration<double, std::milli>(t2 - t1).count();
+    return ZQ_OK;
+}
+
+int zq_model_memory(zq_model* m, uint64_t* weight_bytes, uint64_t* cache_bytes, uint64_t* activation_bytes) {
+    if (!m) return ZQ_ERR_ARG;
+    if (weight_bytes) *weight_bytes = m->weight_bytes;
+    if (cache_bytes) *cache_bytes = m->cache_bytes;
+    if (activation_bytes) *activation_bytes = m->act_bytes;
+    return ZQ_OK;
+}
+
+}  // extern "C"

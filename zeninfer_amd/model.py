@@ -1,0 +1,95 @@
+"""Python handle of the device-resident decoder (include/zq_model.h).
+
+``Model.from_gguf(GGUFFile(...))`` uploads a llama-architecture GGUF once;
+``Model.synthetic(config)`` builds a random-init model directly in HBM.  Every
+call goes through the HIP library; there is no CPU fallback.  The interface
+mirrors the reference runtime's (DenseTransformerRuntime::forward_batch /
+forward / generate, include/zen/dense_transformer_runtime.h:20-78).
+"""
+import ctypes
+
+import numpy as np
+
+from . import zq
+
+PREFILL_INT8, PREFILL_F32 = 0, 1
+
+
+class ModelError(RuntimeError):
+    pass
+
+
+class Model:
+    def __init__(self, handle, cfg):
+        self._L = zq.lib()
+        self._h = handle
+        self.config = {n: getattr(cfg, n) for n, _ in cfg._fields_}
+
+    @classmethod
+    def from_gguf(cls, gguf, max_positions=0):
+        L = zq.lib()
+        cfg = zq.ModelConfig()
+        h = ctypes.c_void_p()
+        err = ctypes.create_string_buffer(512)
+        st = L.zq_model_load_gguf(gguf._h, max_positions, ctypes.byref(cfg), ctypes.byref(h), err, 512)
+        if st != 0:
+            raise ModelError(f"model load failed ({st}): {err.value.decode()}")
+        return cls(h, cfg)
+
+    @classmethod
+    def synthetic(cls, seed=0x5EED0004, **shape):
+        L = zq.lib()
+        cfg = zq.ModelConfig()
+        for k, v in shape.items():
+            setattr(cfg, k, v)
+        h = ctypes.c_void_p()
+        err = ctypes.create_string_buffer(512)
+        st = L.zq_model_create_synthetic(ctypes.byref(cfg), seed, ctypes.byref(h), err, 512)
+        if st != 0:
+            raise ModelError(f"synthetic model failed ({st}): {err.value.decode()}")
+        return cls(h, cfg)
+
+    def close(self):
+        if self._h:
+            self._L.zq_model_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_prefill_mode(self, mode):
+        zq.check(self._L.zq_model_set_prefill_mode(self._h, mode), "set_prefill_mode")
+
+    def prefill(self, tokens, logits=True):
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        out = np.empty(self.config["vocab"], np.float32) if logits else None
+        nxt = ctypes.c_uint32()
+        zq.check(self._L.zq_model_prefill(self._h, t.ctypes.data_as(ctypes.c_void_p), t.size,
+                                          out.ctypes.data_as(ctypes.c_void_p) if logits else None, ctypes.byref(nxt)),
+                 "prefill")
+        return nxt.value, out
+
+    def decode(self, token, logits=True):
+        out = np.empty(self.config["vocab"], np.float32) if logits else None
+        nxt = ctypes.c_uint32()
+        zq.check(self._L.zq_model_decode(self._h, int(token), out.ctypes.data_as(ctypes.c_void_p) if logits else None,
+                                         ctypes.byref(nxt)), "decode")
+        return nxt.value, out
+
+    def generate(self, prompt, max_new):
+        p = np.ascontiguousarray(prompt, dtype=np.uint32)
+        out = np.empty(max(max_new, 1), np.uint32)
+        n = ctypes.c_size_t()
+        pm, dm = ctypes.c_double(), ctypes.c_double()
+        zq.check(self._L.zq_model_generate(self._h, p.ctypes.data_as(ctypes.c_void_p), p.size, max_new,
+                                           out.ctypes.data_as(ctypes.c_void_p), ctypes.byref(n), ctypes.byref(pm),
+                                           ctypes.byref(dm)), "generate")
+        return out[:n.value].tolist(), pm.value, dm.value
+
+    def memory(self):
+        w, c, a = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_uint64()
+        zq.check(self._L.zq_model_memory(self._h, ctypes.byref(w), ctypes.byref(c), ctypes.byref(a)), "memory")
+        return {"weights": w.value, "kv_cache": c.value, "activations": a.value}

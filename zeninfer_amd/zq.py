@@ -103,6 +103,29 @@ GGUF_SIGNATURES = {
     "zq_gguf_meta_value": (ctypes.c_char_p, [_P, ctypes.c_char_p]),
 }
 
+class ModelConfig(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint32) for n in ("embedding", "layers", "heads", "kv_heads", "head_dim", "ffn", "vocab",
+                                               "context", "max_positions", "rope_dim")] + [
+        ("rope_base", ctypes.c_float), ("rms_epsilon", ctypes.c_float), ("eos_token", ctypes.c_uint32),
+        ("weight_format", ctypes.c_int)]
+
+
+# Every symbol include/zq_model.h declares.
+MODEL_SIGNATURES = {
+    "zq_model_load_gguf": (ctypes.c_int, [_P, ctypes.c_uint32, ctypes.POINTER(ModelConfig), ctypes.POINTER(_P),
+                                          ctypes.c_char_p, _S]),
+    "zq_model_create_synthetic": (ctypes.c_int, [ctypes.POINTER(ModelConfig), ctypes.c_uint64, ctypes.POINTER(_P),
+                                                 ctypes.c_char_p, _S]),
+    "zq_model_free": (None, [_P]),
+    "zq_model_set_prefill_mode": (ctypes.c_int, [_P, ctypes.c_int]),
+    "zq_model_prefill": (ctypes.c_int, [_P, _P, _S, _P, ctypes.POINTER(ctypes.c_uint32)]),
+    "zq_model_decode": (ctypes.c_int, [_P, ctypes.c_uint32, _P, ctypes.POINTER(ctypes.c_uint32)]),
+    "zq_model_generate": (ctypes.c_int, [_P, _P, _S, ctypes.c_uint32, _P, ctypes.POINTER(_S),
+                                         ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]),
+    "zq_model_memory": (ctypes.c_int, [_P, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64),
+                                       ctypes.POINTER(ctypes.c_uint64)]),
+}
+
 _lib = None
 
 
@@ -115,7 +138,7 @@ def lib():
             raise RuntimeError(f"{path} is missing: build it with `python -m zeninfer_amd.build` "
                                "(there is no CPU fallback for this path)")
         L = ctypes.CDLL(path)
-        for name, (res, args) in {**SIGNATURES, **GGUF_SIGNATURES}.items():
+        for name, (res, args) in {**SIGNATURES, **GGUF_SIGNATURES, **MODEL_SIGNATURES}.items():
             fn = getattr(L, name)
             fn.restype = res
             fn.argtypes = args
