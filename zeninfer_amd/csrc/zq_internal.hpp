@@ -65,7 +65,18 @@ hipError_t launch_rope_kv(float* q, const float* k, const float* v, float* kc, f
 hipError_t launch_attention(const float* q, const float* kc, const float* vc, float* out, const uint32_t* pos0,
                             uint32_t T, uint32_t H, uint32_t KH, uint32_t D, uint32_t max_pos, float scale,
                             hipStream_t stream);
+// Decode attention split over 32-position chunks (+ combine); `part` holds
+// attention_decode_partial_floats(H, D, max_pos) floats.
+size_t attention_decode_partial_floats(uint32_t H, uint32_t D, uint32_t max_pos);
+hipError_t launch_attention_decode(const float* q, const float* kc, const float* vc, float* part, float* out,
+                                   const uint32_t* pos, uint32_t H, uint32_t KH, uint32_t D, uint32_t max_pos,
+                                   float scale, hipStream_t stream);
 hipError_t launch_add(float* x, const float* y, size_t n, hipStream_t stream);
-hipError_t launch_argmax(const float* x, uint32_t n, uint32_t* out, hipStream_t stream);
+// x += r, then y = rmsnorm(x) * w (rows of n)
+hipError_t launch_add_rmsnorm(float* x, const float* r, const float* w, float* y, uint32_t rows, uint32_t n, float eps,
+                              hipStream_t stream);
+// Greedy id over n values; `partial` holds argmax_partial_bytes().
+size_t argmax_partial_bytes();
+hipError_t launch_argmax(const float* x, uint32_t n, uint32_t* out, void* partial, hipStream_t stream);
 hipError_t launch_silu_mul(const float* gate, const float* up, float* out, size_t n, hipStream_t stream);
 }  // namespace zq

@@ -74,17 +74,29 @@ __global__ __launch_bounds__(kT) void embed_f32_kernel(const float* __restrict__
     x[size_t(t) * E + e] = tok < vocab ? table[size_t(tok) * E + e] : 0.0f;
 }
 
-// One workgroup per row.
-__global__ __launch_bounds__(kT) void rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w,
-                                                     float* __restrict__ y, uint32_t n, float eps) {
-    __shared__ double red[kT / 64];
-    const float* xr = x + size_t(blockIdx.x) * n;
+// One workgroup of 1024 threads per row.  With ADD the residual update
+// x += r comes first (x is written back) and the norm is of the updated row.
+constexpr int kNormT = 1024;
+template <bool ADD>
+__global__ __launch_bounds__(kNormT) void rmsnorm_kernel(float* __restrict__ x, const float* __restrict__ r,
+                                                         const float* __restrict__ w, float* __restrict__ y, uint32_t n,
+                                                         float eps) {
+    __shared__ double red[kNormT / 64];
+    float* xr = x + size_t(blockIdx.x) * n;
     float* yr = y + size_t(blockIdx.x) * n;
+    const float* rr = ADD ? r + size_t(blockIdx.x) * n : nullptr;
     double ss = 0.0;
-    for (uint32_t i = threadIdx.x; i < n; i += kT) ss += double(xr[i]) * double(xr[i]);
+    for (uint32_t i = threadIdx.x; i < n; i += kNormT) {
+        float v = xr[i];
+        if constexpr (ADD) {
+            v += rr[i];
+            xr[i] = v;
+        }
+        ss += double(v) * double(v);
+    }
     ss = block_sum_d(ss, red);
     const float inv = 1.0f / sqrtf(float(ss / double(n)) + eps);
-    for (uint32_t i = threadIdx.x; i < n; i += kT) yr[i] = xr[i] * inv * w[i];
+    for (uint32_t i = threadIdx.x; i < n; i += kNormT) yr[i] = xr[i] * inv * w[i];
 }
 
 // RoPE on q (in place) and k, then k and v appended to the caches at
@@ -188,40 +200,170 @@ __global__ __launch_bounds__(kT) void attention_kernel(const float* __restrict__
     }
 }
 
+// Decode attention (one query token at position pos), split over positions:
+// workgroup (kh, s) covers positions [s*C, s*C + C) of kv head kh for all G
+// query heads that share it, reading every K and V row once.  It writes, per
+// query head, the chunk's max score m, sum l = sum exp(score - m) and
+// acc[d] = sum exp(score - m) * v[d]; attention_combine_kernel merges the
+// chunks: out = sum_s exp(m_s - M) acc_s / sum_s exp(m_s - M) l_s.  Equal to
+// the single-pass softmax of the reference up to rounding.
+constexpr int kAttnChunk = 32;
+constexpr int kAttnMaxG = 8;
+
+template <int D>
+__global__ __launch_bounds__(kT) void attention_decode_kernel(const float* __restrict__ q, const float* __restrict__ kc,
+                                                              const float* __restrict__ vc, float* __restrict__ part,
+                                                              const uint32_t* __restrict__ pos_ptr, uint32_t H,
+                                                              uint32_t KH, float scale, uint32_t splits) {
+    constexpr int C = kAttnChunk;
+    constexpr int LPP = kT / C;  // lanes per position in the score phase (8)
+    constexpr int DPL = D / LPP; // elements per lane (16 for D = 128)
+    __shared__ float qs[kAttnMaxG][D];
+    __shared__ float sc[kAttnMaxG][C];
+    __shared__ float red[kAttnMaxG][kT];
+    const uint32_t kh = blockIdx.x, s = blockIdx.y;
+    const uint32_t pos = *pos_ptr;
+    const uint32_t p0 = s * C;
+    if (p0 > pos) return;  // chunk past the current position: nothing to contribute
+    const uint32_t n = min(uint32_t(C), pos + 1 - p0);
+    const uint32_t G = H / KH;
+    const uint32_t KW = KH * D;
+    for (uint32_t i = threadIdx.x; i < G * D; i += kT) qs[i / D][i % D] = q[size_t(kh * G + i / D) * D + i % D];
+    __syncthreads();
+    // scores: thread (p, j) handles elements [j*DPL, j*DPL + DPL) of position p0 + p
+    {
+        const uint32_t p = threadIdx.x / LPP, j = threadIdx.x % LPP;
+        float kv[DPL];
+        if (p < n) {
+            const float4* kr = reinterpret_cast<const float4*>(kc + size_t(p0 + p) * KW + size_t(kh) * D + j * DPL);
+#pragma unroll
+            for (int i = 0; i < DPL / 4; ++i) {
+                const float4 f = kr[i];
+                kv[4 * i] = f.x; kv[4 * i + 1] = f.y; kv[4 * i + 2] = f.z; kv[4 * i + 3] = f.w;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < DPL; ++i) kv[i] = 0.0f;
+        }
+        for (uint32_t g = 0; g < G; ++g) {
+            float d = 0.0f;
+#pragma unroll
+            for (int i = 0; i < DPL; ++i) d = fmaf(qs[g][j * DPL + i], kv[i], d);
+#pragma unroll
+            for (int o = LPP / 2; o > 0; o >>= 1) d += __shfl_xor(d, o);
+            if (j == 0 && p < n) sc[g][p] = d * scale;
+        }
+    }
+    __syncthreads();
+    // chunk softmax per head: threads of wave 0 take one head each
+    float* outp = part + size_t(kh * G) * splits * (D + 2);
+    if (threadIdx.x < G) {
+        const uint32_t g = threadIdx.x;
+        float m = -INFINITY;
+        for (uint32_t p = 0; p < n; ++p) m = fmaxf(m, sc[g][p]);
+        float l = 0.0f;
+        for (uint32_t p = 0; p < n; ++p) {
+            const float e = expf(sc[g][p] - m);
+            sc[g][p] = e;
+            l += e;
+        }
+        float* o = outp + (size_t(g) * splits + s) * (D + 2);
+        o[D] = m;
+        o[D + 1] = l;
+    }
+    __syncthreads();
+    // acc[g][d] = sum_p e[g][p] * v[p][d]; thread (d, half) sums half the positions
+    {
+        constexpr int HALVES = kT / D;  // 2 for D = 128
+        const uint32_t d = threadIdx.x % D, half = threadIdx.x / D;
+        float acc[kAttnMaxG];
+#pragma unroll
+        for (int g = 0; g < kAttnMaxG; ++g) acc[g] = 0.0f;
+        for (uint32_t p = half; p < n; p += HALVES) {
+            const float vv = vc[size_t(p0 + p) * KW + size_t(kh) * D + d];
+#pragma unroll
+            for (int g = 0; g < kAttnMaxG; ++g)
+                if (g < int(G)) acc[g] = fmaf(sc[g][p], vv, acc[g]);
+        }
+        if (HALVES > 1) {
+            for (uint32_t g = 0; g < G; ++g) red[g][threadIdx.x] = acc[g];
+            __syncthreads();
+            if (half == 0)
+                for (uint32_t g = 0; g < G; ++g) {
+                    float t = 0.0f;
+                    for (int k = 0; k < HALVES; ++k) t += red[g][d + k * D];
+                    outp[(size_t(g) * splits + s) * (D + 2) + d] = t;
+                }
+        } else {
+            for (uint32_t g = 0; g < G; ++g) outp[(size_t(g) * splits + s) * (D + 2) + d] = acc[g];
+        }
+    }
+}
+
+// out[h][d] from the chunk partials of head h (one workgroup per head).
+__global__ __launch_bounds__(kT) void attention_combine_kernel(const float* __restrict__ part, float* __restrict__ out,
+                                                               const uint32_t* __restrict__ pos_ptr, uint32_t D,
+                                                               uint32_t splits) {
+    const uint32_t h = blockIdx.x;
+    const uint32_t ns = *pos_ptr / kAttnChunk + 1;
+    const float* ph = part + size_t(h) * splits * (D + 2);
+    float M = -INFINITY;
+    for (uint32_t s = 0; s < ns; ++s) M = fmaxf(M, ph[size_t(s) * (D + 2) + D]);
+    double L = 0.0;
+    for (uint32_t s = 0; s < ns; ++s) L += double(ph[size_t(s) * (D + 2) + D + 1]) * double(expf(ph[size_t(s) * (D + 2) + D] - M));
+    const float inv = 1.0f / float(L);
+    for (uint32_t d = threadIdx.x; d < D; d += kT) {
+        float acc = 0.0f;
+        for (uint32_t s = 0; s < ns; ++s) acc = fmaf(ph[size_t(s) * (D + 2) + d], expf(ph[size_t(s) * (D + 2) + D] - M), acc);
+        out[size_t(h) * D + d] = acc * inv;
+    }
+}
+
 __global__ __launch_bounds__(kT) void add_kernel(float* __restrict__ x, const float* __restrict__ y, size_t n) {
     const size_t i = size_t(blockIdx.x) * kT + threadIdx.x;
     if (i < n) x[i] += y[i];
 }
 
-// One workgroup of 1024 threads: lowest index among the finite maxima.
-__global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ x, uint32_t n, uint32_t* __restrict__ out) {
-    __shared__ float bv[16];
-    __shared__ uint32_t bi[16];
+// Greedy id: the lowest index among the finite maxima.  Stage 1: kArgBlocks
+// workgroups each reduce a strided share into (value, index); stage 2 reduces
+// the partials.  "Better" = larger value, or equal value and lower index.
+constexpr int kArgBlocks = 128;
+__device__ __forceinline__ void better(float& bv, uint32_t& bi, float ov, uint32_t oi) {
+    if (oi != 0xffffffffu && (bi == 0xffffffffu || ov > bv || (ov == bv && oi < bi))) {
+        bv = ov;
+        bi = oi;
+    }
+}
+__device__ __forceinline__ void block_best(float& best, uint32_t& idx, float* sv, uint32_t* si) {
+    for (int o = 32; o > 0; o >>= 1) better(best, idx, __shfl_xor(best, o), __shfl_xor(idx, o));
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) { sv[w] = best; si[w] = idx; }
+    __syncthreads();
+    if (threadIdx.x == 0)
+        for (int i = 1; i < kT / 64; ++i) better(best, idx, sv[i], si[i]);
+}
+__global__ __launch_bounds__(kT) void argmax_partial_kernel(const float* __restrict__ x, uint32_t n,
+                                                            float* __restrict__ pv, uint32_t* __restrict__ pi) {
+    __shared__ float sv[kT / 64];
+    __shared__ uint32_t si[kT / 64];
     float best = -INFINITY;
     uint32_t idx = 0xffffffffu;
-    for (uint32_t i = threadIdx.x; i < n; i += 1024) {
+    for (uint32_t i = blockIdx.x * kT + threadIdx.x; i < n; i += kArgBlocks * kT) {
         const float v = x[i];
-        if (isfinite(v) && (v > best || idx == 0xffffffffu)) {
-            if (v > best || idx == 0xffffffffu) { best = v; idx = i; }
-        }
+        if (isfinite(v)) better(best, idx, v, i);
     }
-    // wave reduce: larger value wins, ties -> lower index
-    for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(best, o);
-        const uint32_t oi = __shfl_xor(idx, o);
-        if (oi != 0xffffffffu && (idx == 0xffffffffu || ov > best || (ov == best && oi < idx))) { best = ov; idx = oi; }
-    }
-    const int w = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) { bv[w] = best; bi[w] = idx; }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        for (int i = 1; i < 16; ++i)
-            if (bi[i] != 0xffffffffu && (idx == 0xffffffffu || bv[i] > best || (bv[i] == best && bi[i] < idx))) {
-                best = bv[i];
-                idx = bi[i];
-            }
-        *out = idx == 0xffffffffu ? 0u : idx;
-    }
+    block_best(best, idx, sv, si);
+    if (threadIdx.x == 0) { pv[blockIdx.x] = best; pi[blockIdx.x] = idx; }
+}
+__global__ __launch_bounds__(kT) void argmax_final_kernel(const float* __restrict__ pv, const uint32_t* __restrict__ pi,
+                                                          uint32_t* __restrict__ out) {
+    __shared__ float sv[kT / 64];
+    __shared__ uint32_t si[kT / 64];
+    float best = -INFINITY;
+    uint32_t idx = 0xffffffffu;
+    if (threadIdx.x < kArgBlocks) better(best, idx, pv[threadIdx.x], pi[threadIdx.x]);
+    block_best(best, idx, sv, si);
+    if (threadIdx.x == 0) *out = idx == 0xffffffffu ? 0u : idx;
 }
 
 }  // namespace
@@ -246,7 +388,15 @@ hipError_t launch_embed(int fmt, const void* table, const uint32_t* tokens, uint
 hipError_t launch_rmsnorm(const float* x, const float* w, float* y, uint32_t rows, uint32_t n, float eps,
                           hipStream_t stream) {
     if (!x || !w || !y || !rows || !n) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kT), 0, stream, x, w, y, n, eps);
+    hipLaunchKernelGGL(rmsnorm_kernel<false>, dim3(rows), dim3(kNormT), 0, stream, const_cast<float*>(x), nullptr, w, y,
+                       n, eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_add_rmsnorm(float* x, const float* r, const float* w, float* y, uint32_t rows, uint32_t n, float eps,
+                              hipStream_t stream) {
+    if (!x || !r || !w || !y || !rows || !n) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rmsnorm_kernel<true>, dim3(rows), dim3(kNormT), 0, stream, x, r, w, y, n, eps);
     return hipGetLastError();
 }
 
@@ -272,15 +422,46 @@ hipError_t launch_attention(const float* q, const float* kc, const float* vc, fl
     return hipGetLastError();
 }
 
+size_t attention_decode_partial_floats(uint32_t H, uint32_t D, uint32_t max_pos) {
+    const uint32_t splits = (max_pos + kAttnChunk - 1) / kAttnChunk;
+    return size_t(H) * splits * (D + 2);
+}
+
+hipError_t launch_attention_decode(const float* q, const float* kc, const float* vc, float* part, float* out,
+                                   const uint32_t* pos, uint32_t H, uint32_t KH, uint32_t D, uint32_t max_pos,
+                                   float scale, hipStream_t stream) {
+    if (!q || !kc || !vc || !part || !out || !pos || !H || !KH || H % KH || H / KH > uint32_t(kAttnMaxG) || !max_pos)
+        return hipErrorInvalidValue;
+    const uint32_t splits = (max_pos + kAttnChunk - 1) / kAttnChunk;
+    const dim3 grid(KH, splits);
+    switch (D) {
+    case 64: hipLaunchKernelGGL(attention_decode_kernel<64>, grid, dim3(kT), 0, stream, q, kc, vc, part, pos, H, KH, scale, splits); break;
+    case 128: hipLaunchKernelGGL(attention_decode_kernel<128>, grid, dim3(kT), 0, stream, q, kc, vc, part, pos, H, KH, scale, splits); break;
+    case 256: hipLaunchKernelGGL(attention_decode_kernel<256>, grid, dim3(kT), 0, stream, q, kc, vc, part, pos, H, KH, scale, splits); break;
+    default: return hipErrorInvalidValue;
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(attention_combine_kernel, dim3(H), dim3(kT), 0, stream, part, out, pos, D, splits);
+    return hipGetLastError();
+}
+
 hipError_t launch_add(float* x, const float* y, size_t n, hipStream_t stream) {
     if (!x || !y || !n) return hipErrorInvalidValue;
     hipLaunchKernelGGL(add_kernel, dim3(uint32_t((n + kT - 1) / kT)), dim3(kT), 0, stream, x, y, n);
     return hipGetLastError();
 }
 
-hipError_t launch_argmax(const float* x, uint32_t n, uint32_t* out, hipStream_t stream) {
-    if (!x || !n || !out) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, stream, x, n, out);
+size_t argmax_partial_bytes() { return size_t(kArgBlocks) * 8; }
+
+hipError_t launch_argmax(const float* x, uint32_t n, uint32_t* out, void* partial, hipStream_t stream) {
+    if (!x || !n || !out || !partial) return hipErrorInvalidValue;
+    float* pv = static_cast<float*>(partial);
+    uint32_t* pi = reinterpret_cast<uint32_t*>(pv + kArgBlocks);
+    hipLaunchKernelGGL(argmax_partial_kernel, dim3(kArgBlocks), dim3(kT), 0, stream, x, n, pv, pi);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(kT), 0, stream, pv, pi, out);
     return hipGetLastError();
 }
 

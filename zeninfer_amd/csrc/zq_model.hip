@@ -85,6 +85,8 @@ struct zq_model {
     int8_t* xq = nullptr;
     float* xs = nullptr;
     float* partial = nullptr;
+    float* attn_part = nullptr;  // decode attention chunk partials
+    void* argmax_part = nullptr;
 
     uint32_t cur_pos = 0;  // positions held in the cache
     bool use_graph = true;
@@ -150,7 +152,9 @@ bool alloc_runtime(zq_model& m, std::string& e) {
         for (auto nk : {std::pair<size_t, size_t>{QW, E}, {KW, E}, {E, QW}, {F, E}, {E, F}})
             partial = std::max(partial, zq::gemm_i8_partial_bytes(M, nk.first, nk.second));
     const size_t xq_bytes = align_up(T * widest, kAlign), xs_bytes = align_up(T * widest / 32 * 4, kAlign);
-    total += xq_bytes + xs_bytes + align_up(partial, kAlign) + 3 * kAlign + align_up(T * 4, kAlign);
+    const size_t attn_bytes = align_up(zq::attention_decode_partial_floats(c.heads, c.head_dim, c.max_positions) * 4, kAlign);
+    const size_t arg_bytes = align_up(zq::argmax_partial_bytes(), kAlign);
+    total += xq_bytes + xs_bytes + align_up(partial, kAlign) + 3 * kAlign + align_up(T * 4, kAlign) + attn_bytes + arg_bytes;
     void* arena;
     if (!dev_alloc(m, &arena, total)) { e = "device allocation failed (activations)"; return false; }
     m.act_bytes = total;
@@ -159,6 +163,8 @@ bool alloc_runtime(zq_model& m, std::string& e) {
     m.xq = reinterpret_cast<int8_t*>(p); p += xq_bytes;
     m.xs = reinterpret_cast<float*>(p); p += xs_bytes;
     m.partial = partial ? reinterpret_cast<float*>(p) : nullptr; p += align_up(partial, kAlign);
+    m.attn_part = reinterpret_cast<float*>(p); p += attn_bytes;
+    m.argmax_part = p; p += arg_bytes;
     m.pos_dev = reinterpret_cast<uint32_t*>(p); p += kAlign;
     m.next_dev = reinterpret_cast<uint32_t*>(p); p += kAlign;
     p += kAlign;
@@ -238,13 +244,15 @@ hipError_t quantize_for(zq_model& m, std::initializer_list<const Weight*> ws, co
     } while (0)
 
 // Decoder layers over T tokens at positions pos0 .. pos0+T-1 (pos0 in device
-// memory); x holds the embeddings on entry and the residual stream on exit.
+// memory).  On entry x holds the embeddings; on exit x is the residual stream
+// and h = rmsnorm(x) * output_norm, every residual add fused into the norm
+// that follows it.
 hipError_t enqueue_layers(zq_model& m, uint32_t T) {
     const auto& c = m.cfg;
     const uint32_t E = c.embedding, QW = c.heads * c.head_dim, KW = c.kv_heads * c.head_dim, F = c.ffn;
+    HIPCHK(zq::launch_rmsnorm(m.x, m.layers[0].attn_norm, m.h, T, E, c.rms_epsilon, m.stream));
     for (uint32_t l = 0; l < c.layers; ++l) {
         Layer& L = m.layers[l];
-        HIPCHK(zq::launch_rmsnorm(m.x, L.attn_norm, m.h, T, E, c.rms_epsilon, m.stream));
         if (T == 1) {
             // decode: the three projections share x -> one batched GEMV per format
             zq::GemvTask t[3] = {{L.q.p, m.q, QW}, {L.k.p, m.k, KW}, {L.v.p, m.v, KW}};
@@ -264,18 +272,19 @@ hipError_t enqueue_layers(zq_model& m, uint32_t T) {
         }
         HIPCHK(zq::launch_rope_kv(m.q, m.k, m.v, L.kc, L.vc, m.cos_tab, m.sin_tab, m.pos_dev, T, c.heads, c.kv_heads,
                                   c.head_dim, m.pairs, true, m.stream));
-        HIPCHK(zq::launch_attention(m.q, L.kc, L.vc, m.att, m.pos_dev, T, c.heads, c.kv_heads, c.head_dim,
-                                    c.max_positions, m.attn_scale, m.stream));
         if (T == 1) {
+            HIPCHK(zq::launch_attention_decode(m.q, L.kc, L.vc, m.attn_part, m.att, m.pos_dev, c.heads, c.kv_heads,
+                                               c.head_dim, c.max_positions, m.attn_scale, m.stream));
             zq::GemvTask t = {L.o.p, m.tmp, E};
             HIPCHK(zq::launch_gemv(L.o.fmt, &t, 1, m.att, QW, m.stream));
         } else {
+            HIPCHK(zq::launch_attention(m.q, L.kc, L.vc, m.att, m.pos_dev, T, c.heads, c.kv_heads, c.head_dim,
+                                        c.max_positions, m.attn_scale, m.stream));
             bool qz;
             HIPCHK(quantize_for(m, {&L.o}, m.att, T, QW, qz));
             HIPCHK(project(m, L.o, m.att, m.tmp, T, qz));
         }
-        HIPCHK(zq::launch_add(m.x, m.tmp, size_t(T) * E, m.stream));
-        HIPCHK(zq::launch_rmsnorm(m.x, L.ffn_norm, m.h, T, E, c.rms_epsilon, m.stream));
+        HIPCHK(zq::launch_add_rmsnorm(m.x, m.tmp, L.ffn_norm, m.h, T, E, c.rms_epsilon, m.stream));
         if (T == 1) {
             zq::GemvTask t[2] = {{L.gate.p, m.gate, F}, {L.up.p, m.up, F}};
             if (L.gate.fmt == L.up.fmt) {
@@ -299,18 +308,19 @@ hipError_t enqueue_layers(zq_model& m, uint32_t T) {
             HIPCHK(quantize_for(m, {&L.down}, m.act, T, F, qz));
             HIPCHK(project(m, L.down, m.act, m.tmp, T, qz));
         }
-        HIPCHK(zq::launch_add(m.x, m.tmp, size_t(T) * E, m.stream));
+        const float* next_norm = l + 1 < c.layers ? m.layers[l + 1].attn_norm : m.out_norm;
+        HIPCHK(zq::launch_add_rmsnorm(m.x, m.tmp, next_norm, m.h, T, E, c.rms_epsilon, m.stream));
     }
     return hipSuccess;
 }
 
-// Final norm of row `row`, the output projection and the greedy id.
+// The output projection of row `row` of h (already output-normed) and the
+// greedy id.
 hipError_t enqueue_head(zq_model& m, uint32_t row) {
     const auto& c = m.cfg;
-    HIPCHK(zq::launch_rmsnorm(m.x + size_t(row) * c.embedding, m.out_norm, m.h, 1, c.embedding, c.rms_epsilon, m.stream));
     zq::GemvTask t = {m.out.p, m.logits, c.vocab};
-    HIPCHK(zq::launch_gemv(m.out.fmt, &t, 1, m.h, c.embedding, m.stream));
-    return zq::launch_argmax(m.logits, c.vocab, m.next_dev, m.stream);
+    HIPCHK(zq::launch_gemv(m.out.fmt, &t, 1, m.h + size_t(row) * c.embedding, c.embedding, m.stream));
+    return zq::launch_argmax(m.logits, c.vocab, m.next_dev, m.argmax_part, m.stream);
 }
 
 hipError_t enqueue_decode(zq_model& m) {
