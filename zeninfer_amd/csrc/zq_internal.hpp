@@ -68,9 +68,12 @@ hipError_t launch_attention(const float* q, const float* kc, const float* vc, fl
 // Decode attention split over 32-position chunks (+ combine); `part` holds
 // attention_decode_partial_floats(H, D, max_pos) floats.
 size_t attention_decode_partial_floats(uint32_t H, uint32_t D, uint32_t max_pos);
-hipError_t launch_attention_decode(const float* q, const float* kc, const float* vc, float* part, float* out,
-                                   const uint32_t* pos, uint32_t H, uint32_t KH, uint32_t D, uint32_t max_pos,
-                                   float scale, hipStream_t stream);
+// RoPE (adjacent pairs) of q and the new key, the KV append at *pos and the
+// attention of the one query token, fused.
+hipError_t launch_attention_decode(const float* q, const float* knew, const float* vnew, float* kc, float* vc,
+                                   const float* cos_tab, const float* sin_tab, float* part, float* out,
+                                   const uint32_t* pos, uint32_t H, uint32_t KH, uint32_t D, uint32_t pairs,
+                                   uint32_t max_pos, float scale, hipStream_t stream);
 hipError_t launch_add(float* x, const float* y, size_t n, hipStream_t stream);
 // x += r, then y = rmsnorm(x) * w (rows of n)
 hipError_t launch_add_rmsnorm(float* x, const float* r, const float* w, float* y, uint32_t rows, uint32_t n, float eps,

@@ -200,25 +200,34 @@ __global__ __launch_bounds__(kT) void attention_kernel(const float* __restrict__
     }
 }
 
-// Decode attention (one query token at position pos), split over positions:
-// workgroup (kh, s) covers positions [s*C, s*C + C) of kv head kh for all G
-// query heads that share it, reading every K and V row once.  It writes, per
-// query head, the chunk's max score m, sum l = sum exp(score - m) and
-// acc[d] = sum exp(score - m) * v[d]; attention_combine_kernel merges the
-// chunks: out = sum_s exp(m_s - M) acc_s / sum_s exp(m_s - M) l_s.  Equal to
+// Decode attention (one query token at position pos) with RoPE and the KV
+// append fused in, split over positions: workgroup (kh, s) covers positions
+// [s*C, s*C + C) of kv head kh for the G query heads that share it, reading
+// each K and V row once.  Every workgroup rotates the G query rows in LDS;
+// the workgroup whose chunk holds `pos` also rotates the new key, appends key
+// and value to the caches and uses them from LDS.  All global loads of a
+// workgroup are issued up front, so its cost is about one memory latency.
+// Per query head it writes the chunk's max score m, l = sum exp(score - m)
+// and acc[d] = sum exp(score - m) * v[d]; attention_combine_kernel merges the
+// chunks, out = sum_s exp(m_s - M) acc_s / sum_s exp(m_s - M) l_s, equal to
 // the single-pass softmax of the reference up to rounding.
 constexpr int kAttnChunk = 32;
 constexpr int kAttnMaxG = 8;
 
 template <int D>
-__global__ __launch_bounds__(kT) void attention_decode_kernel(const float* __restrict__ q, const float* __restrict__ kc,
-                                                              const float* __restrict__ vc, float* __restrict__ part,
-                                                              const uint32_t* __restrict__ pos_ptr, uint32_t H,
-                                                              uint32_t KH, float scale, uint32_t splits) {
+__global__ __launch_bounds__(kT) void attention_decode_kernel(
+    const float* __restrict__ q, const float* __restrict__ knew, const float* __restrict__ vnew, float* __restrict__ kc,
+    float* __restrict__ vc, const float* __restrict__ cos_tab, const float* __restrict__ sin_tab,
+    float* __restrict__ part, const uint32_t* __restrict__ pos_ptr, uint32_t H, uint32_t KH, uint32_t pairs,
+    float scale, uint32_t splits) {
     constexpr int C = kAttnChunk;
-    constexpr int LPP = kT / C;  // lanes per position in the score phase (8)
-    constexpr int DPL = D / LPP; // elements per lane (16 for D = 128)
+    constexpr int LPP = kT / C;       // lanes per position in the score phase (8)
+    constexpr int DPL = D / LPP;      // key elements per lane (16 for D = 128)
+    constexpr int HALVES = kT / D;    // position groups in the value phase
+    constexpr int VPT = C / HALVES;   // value rows per thread
+    constexpr int QPT = kAttnMaxG * D / kT;
     __shared__ float qs[kAttnMaxG][D];
+    __shared__ float kn[D], vn[D];
     __shared__ float sc[kAttnMaxG][C];
     __shared__ float red[kAttnMaxG][kT];
     const uint32_t kh = blockIdx.x, s = blockIdx.y;
@@ -226,39 +235,86 @@ __global__ __launch_bounds__(kT) void attention_decode_kernel(const float* __res
     const uint32_t p0 = s * C;
     if (p0 > pos) return;  // chunk past the current position: nothing to contribute
     const uint32_t n = min(uint32_t(C), pos + 1 - p0);
+    const bool owns_new = pos < p0 + C;
     const uint32_t G = H / KH;
     const uint32_t KW = KH * D;
-    for (uint32_t i = threadIdx.x; i < G * D; i += kT) qs[i / D][i % D] = q[size_t(kh * G + i / D) * D + i % D];
-    __syncthreads();
-    // scores: thread (p, j) handles elements [j*DPL, j*DPL + DPL) of position p0 + p
+    const int tid = threadIdx.x;
+
+    // ---- issue every global load ----
+    const uint32_t sp = tid / LPP, sj = tid % LPP;  // score phase: position, slice
+    float kv[DPL];
     {
-        const uint32_t p = threadIdx.x / LPP, j = threadIdx.x % LPP;
-        float kv[DPL];
-        if (p < n) {
-            const float4* kr = reinterpret_cast<const float4*>(kc + size_t(p0 + p) * KW + size_t(kh) * D + j * DPL);
+        const uint32_t pp = sp < n ? p0 + sp : p0;
+        const float4* kr = reinterpret_cast<const float4*>(kc + size_t(pp) * KW + size_t(kh) * D + sj * DPL);
 #pragma unroll
-            for (int i = 0; i < DPL / 4; ++i) {
-                const float4 f = kr[i];
-                kv[4 * i] = f.x; kv[4 * i + 1] = f.y; kv[4 * i + 2] = f.z; kv[4 * i + 3] = f.w;
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < DPL; ++i) kv[i] = 0.0f;
-        }
-        for (uint32_t g = 0; g < G; ++g) {
-            float d = 0.0f;
-#pragma unroll
-            for (int i = 0; i < DPL; ++i) d = fmaf(qs[g][j * DPL + i], kv[i], d);
-#pragma unroll
-            for (int o = LPP / 2; o > 0; o >>= 1) d += __shfl_xor(d, o);
-            if (j == 0 && p < n) sc[g][p] = d * scale;
+        for (int i = 0; i < DPL / 4; ++i) {
+            const float4 f = kr[i];
+            kv[4 * i] = f.x; kv[4 * i + 1] = f.y; kv[4 * i + 2] = f.z; kv[4 * i + 3] = f.w;
         }
     }
+    const uint32_t vd = tid % D, vh = tid / D;      // value phase: element, position group
+    float vv[VPT];
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const uint32_t p = vh + i * HALVES;
+        vv[i] = vc[size_t(p0 + (p < n ? p : 0)) * KW + size_t(kh) * D + vd];
+    }
+    float qr[QPT];
+#pragma unroll
+    for (int i = 0; i < QPT; ++i) {
+        const uint32_t e = tid + i * kT;
+        qr[i] = e < G * D ? q[size_t(kh * G) * D + e] : 0.0f;
+    }
+    float knr = 0.0f, vnr = 0.0f;
+    if (owns_new && tid < D) {
+        knr = knew[size_t(kh) * D + tid];
+        vnr = vnew[size_t(kh) * D + tid];
+    }
+    const float* cs = cos_tab + size_t(pos) * pairs;
+    const float* sn = sin_tab + size_t(pos) * pairs;
+
+    // ---- RoPE (adjacent pairs) on q and the new key, in LDS ----
+#pragma unroll
+    for (int i = 0; i < QPT; ++i) {
+        const uint32_t e = tid + i * kT;
+        if (e < G * D) qs[e / D][e % D] = qr[i];
+    }
+    if (owns_new && tid < D) { kn[tid] = knr; vn[tid] = vnr; }
     __syncthreads();
-    // chunk softmax per head: threads of wave 0 take one head each
+    for (uint32_t j = tid; j < G * pairs; j += kT) {
+        const uint32_t g = j / pairs, i = j - g * pairs;
+        const float a = qs[g][2 * i], b = qs[g][2 * i + 1], c = cs[i], sv = sn[i];
+        qs[g][2 * i] = a * c - b * sv;
+        qs[g][2 * i + 1] = a * sv + b * c;
+    }
+    if (owns_new && tid < pairs) {
+        const float a = kn[2 * tid], b = kn[2 * tid + 1], c = cs[tid], sv = sn[tid];
+        kn[2 * tid] = a * c - b * sv;
+        kn[2 * tid + 1] = a * sv + b * c;
+    }
+    __syncthreads();
+    if (owns_new && tid < D) {  // append to the caches for later steps
+        kc[size_t(pos) * KW + size_t(kh) * D + tid] = kn[tid];
+        vc[size_t(pos) * KW + size_t(kh) * D + tid] = vn[tid];
+    }
+    // ---- scores ----
+    if (sp < n && p0 + sp == pos) {
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) kv[i] = kn[sj * DPL + i];
+    }
+    for (uint32_t g = 0; g < G; ++g) {
+        float d = 0.0f;
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) d = fmaf(qs[g][sj * DPL + i], kv[i], d);
+#pragma unroll
+        for (int o = LPP / 2; o > 0; o >>= 1) d += __shfl_xor(d, o);
+        if (sj == 0 && sp < n) sc[g][sp] = d * scale;
+    }
+    __syncthreads();
+    // ---- chunk softmax: one thread per head ----
     float* outp = part + size_t(kh * G) * splits * (D + 2);
-    if (threadIdx.x < G) {
-        const uint32_t g = threadIdx.x;
+    if (tid < int(G)) {
+        const uint32_t g = tid;
         float m = -INFINITY;
         for (uint32_t p = 0; p < n; ++p) m = fmaxf(m, sc[g][p]);
         float l = 0.0f;
@@ -272,50 +328,63 @@ __global__ __launch_bounds__(kT) void attention_decode_kernel(const float* __res
         o[D + 1] = l;
     }
     __syncthreads();
-    // acc[g][d] = sum_p e[g][p] * v[p][d]; thread (d, half) sums half the positions
-    {
-        constexpr int HALVES = kT / D;  // 2 for D = 128
-        const uint32_t d = threadIdx.x % D, half = threadIdx.x / D;
-        float acc[kAttnMaxG];
+    // ---- acc[g][d] = sum_p e[g][p] * v[p][d] ----
+    float acc[kAttnMaxG];
 #pragma unroll
-        for (int g = 0; g < kAttnMaxG; ++g) acc[g] = 0.0f;
-        for (uint32_t p = half; p < n; p += HALVES) {
-            const float vv = vc[size_t(p0 + p) * KW + size_t(kh) * D + d];
+    for (int g = 0; g < kAttnMaxG; ++g) acc[g] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const uint32_t p = vh + i * HALVES;
+        if (p < n) {
+            const float v = p0 + p == pos ? vn[vd] : vv[i];
 #pragma unroll
             for (int g = 0; g < kAttnMaxG; ++g)
-                if (g < int(G)) acc[g] = fmaf(sc[g][p], vv, acc[g]);
+                if (g < int(G)) acc[g] = fmaf(sc[g][p], v, acc[g]);
         }
-        if (HALVES > 1) {
-            for (uint32_t g = 0; g < G; ++g) red[g][threadIdx.x] = acc[g];
-            __syncthreads();
-            if (half == 0)
-                for (uint32_t g = 0; g < G; ++g) {
-                    float t = 0.0f;
-                    for (int k = 0; k < HALVES; ++k) t += red[g][d + k * D];
-                    outp[(size_t(g) * splits + s) * (D + 2) + d] = t;
-                }
-        } else {
-            for (uint32_t g = 0; g < G; ++g) outp[(size_t(g) * splits + s) * (D + 2) + d] = acc[g];
-        }
+    }
+    if (HALVES > 1) {
+        for (uint32_t g = 0; g < G; ++g) red[g][tid] = acc[g];
+        __syncthreads();
+        if (vh == 0)
+            for (uint32_t g = 0; g < G; ++g) {
+                float t = 0.0f;
+                for (int k = 0; k < HALVES; ++k) t += red[g][vd + k * D];
+                outp[(size_t(g) * splits + s) * (D + 2) + vd] = t;
+            }
+    } else {
+        for (uint32_t g = 0; g < G; ++g) outp[(size_t(g) * splits + s) * (D + 2) + vd] = acc[g];
     }
 }
 
-// out[h][d] from the chunk partials of head h (one workgroup per head).
+// out[h][d] from the chunk partials of head h: one workgroup per head, all
+// partials read into LDS in one pass.
 __global__ __launch_bounds__(kT) void attention_combine_kernel(const float* __restrict__ part, float* __restrict__ out,
                                                                const uint32_t* __restrict__ pos_ptr, uint32_t D,
                                                                uint32_t splits) {
+    extern __shared__ float ps[];  // ns * (D + 2)
+    __shared__ float wgt[1024];
+    __shared__ float inv_l;
     const uint32_t h = blockIdx.x;
     const uint32_t ns = *pos_ptr / kAttnChunk + 1;
     const float* ph = part + size_t(h) * splits * (D + 2);
-    float M = -INFINITY;
-    for (uint32_t s = 0; s < ns; ++s) M = fmaxf(M, ph[size_t(s) * (D + 2) + D]);
-    double L = 0.0;
-    for (uint32_t s = 0; s < ns; ++s) L += double(ph[size_t(s) * (D + 2) + D + 1]) * double(expf(ph[size_t(s) * (D + 2) + D] - M));
-    const float inv = 1.0f / float(L);
+    for (uint32_t i = threadIdx.x; i < ns * (D + 2); i += kT) ps[i] = ph[i];
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float M = -INFINITY;
+        for (uint32_t s = 0; s < ns; ++s) M = fmaxf(M, ps[s * (D + 2) + D]);
+        double L = 0.0;
+        for (uint32_t s = 0; s < ns; ++s) {
+            const float w = expf(ps[s * (D + 2) + D] - M);
+            wgt[s] = w;
+            L += double(ps[s * (D + 2) + D + 1]) * double(w);
+        }
+        inv_l = 1.0f / float(L);
+    }
+    __syncthreads();
     for (uint32_t d = threadIdx.x; d < D; d += kT) {
         float acc = 0.0f;
-        for (uint32_t s = 0; s < ns; ++s) acc = fmaf(ph[size_t(s) * (D + 2) + d], expf(ph[size_t(s) * (D + 2) + D] - M), acc);
-        out[size_t(h) * D + d] = acc * inv;
+        for (uint32_t s = 0; s < ns; ++s) acc = fmaf(ps[s * (D + 2) + d], wgt[s], acc);
+        out[size_t(h) * D + d] = acc * inv_l;
     }
 }
 
@@ -427,22 +496,31 @@ size_t attention_decode_partial_floats(uint32_t H, uint32_t D, uint32_t max_pos)
     return size_t(H) * splits * (D + 2);
 }
 
-hipError_t launch_attention_decode(const float* q, const float* kc, const float* vc, float* part, float* out,
-                                   const uint32_t* pos, uint32_t H, uint32_t KH, uint32_t D, uint32_t max_pos,
-                                   float scale, hipStream_t stream) {
-    if (!q || !kc || !vc || !part || !out || !pos || !H || !KH || H % KH || H / KH > uint32_t(kAttnMaxG) || !max_pos)
+hipError_t launch_attention_decode(const float* q, const float* knew, const float* vnew, float* kc, float* vc,
+                                   const float* cos_tab, const float* sin_tab, float* part, float* out,
+                                   const uint32_t* pos, uint32_t H, uint32_t KH, uint32_t D, uint32_t pairs,
+                                   uint32_t max_pos, float scale, hipStream_t stream) {
+    if (!q || !knew || !vnew || !kc || !vc || !cos_tab || !sin_tab || !part || !out || !pos || !H || !KH || H % KH ||
+        H / KH > uint32_t(kAttnMaxG) || !max_pos || !pairs || pairs > D / 2)
         return hipErrorInvalidValue;
     const uint32_t splits = (max_pos + kAttnChunk - 1) / kAttnChunk;
+    if (splits > 1024 || size_t(splits) * (D + 2) * 4 > 64 * 1024) return hipErrorInvalidValue;
     const dim3 grid(KH, splits);
+#define ZQ_ATTN(DD)                                                                                                   \
+    hipLaunchKernelGGL(attention_decode_kernel<DD>, grid, dim3(kT), 0, stream, q, knew, vnew, kc, vc, cos_tab, sin_tab, \
+                       part, pos, H, KH, pairs, scale, splits)
     switch (D) {
-    case 64: hipLaunchKernelGGL(attention_decode_kernel<64>, grid, dim3(kT), 0, stream, q, kc, vc, part, pos, H, KH, scale, splits); break;
-    case 128: hipLaunchKernelGGL(attention_decode_kernel<128>, grid, dim3(kT), 0, stream, q, kc, vc, part, pos, H, KH, scale, splits); break;
-    case 256: hipLaunchKernelGGL(attention_decode_kernel<256>, grid, dim3(kT), 0, stream, q, kc, vc, part, pos, H, KH, scale, splits); break;
+    case 64: ZQ_ATTN(64); break;
+    case 128: ZQ_ATTN(128); break;
+    case 256: ZQ_ATTN(256); break;
     default: return hipErrorInvalidValue;
     }
+#undef ZQ_ATTN
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(attention_combine_kernel, dim3(H), dim3(kT), 0, stream, part, out, pos, D, splits);
+    // the partials of the chunks up to the current position go through LDS
+    hipLaunchKernelGGL(attention_combine_kernel, dim3(H), dim3(kT), size_t(splits) * (D + 2) * 4, stream, part, out,
+                       pos, D, splits);
     return hipGetLastError();
 }
 

@@ -270,14 +270,15 @@ hipError_t enqueue_layers(zq_model& m, uint32_t T) {
             HIPCHK(project(m, L.k, m.h, m.k, T, qz));
             HIPCHK(project(m, L.v, m.h, m.v, T, qz));
         }
-        HIPCHK(zq::launch_rope_kv(m.q, m.k, m.v, L.kc, L.vc, m.cos_tab, m.sin_tab, m.pos_dev, T, c.heads, c.kv_heads,
-                                  c.head_dim, m.pairs, true, m.stream));
         if (T == 1) {
-            HIPCHK(zq::launch_attention_decode(m.q, L.kc, L.vc, m.attn_part, m.att, m.pos_dev, c.heads, c.kv_heads,
-                                               c.head_dim, c.max_positions, m.attn_scale, m.stream));
+            HIPCHK(zq::launch_attention_decode(m.q, m.k, m.v, L.kc, L.vc, m.cos_tab, m.sin_tab, m.attn_part, m.att,
+                                               m.pos_dev, c.heads, c.kv_heads, c.head_dim, m.pairs, c.max_positions,
+                                               m.attn_scale, m.stream));
             zq::GemvTask t = {L.o.p, m.tmp, E};
             HIPCHK(zq::launch_gemv(L.o.fmt, &t, 1, m.att, QW, m.stream));
         } else {
+            HIPCHK(zq::launch_rope_kv(m.q, m.k, m.v, L.kc, L.vc, m.cos_tab, m.sin_tab, m.pos_dev, T, c.heads,
+                                      c.kv_heads, c.head_dim, m.pairs, true, m.stream));
             HIPCHK(zq::launch_attention(m.q, L.kc, L.vc, m.att, m.pos_dev, T, c.heads, c.kv_heads, c.head_dim,
                                         c.max_positions, m.attn_scale, m.stream));
             bool qz;
