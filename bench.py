@@ -20,6 +20,9 @@ roofline dominant kernel: the Q8_0 GEMV at 4096x14336 (down projection, the
          queues them), so the average includes the inter-kernel gap.
 secondary int8 prefill GEMM at M=2048, gate/up shape
          14336x4096 and down shape 4096x14336, as TOPS vs the int8 MFMA peak.
+model_config4 BASELINE config 4 on the device-resident decoder (zq_model.h):
+         prefill tok/s for a 512-token prompt and decode tok/s for 128
+         greedy tokens of a Llama-3-8B-shaped random-init Q8_0 model.
 cpu_baseline the reference's own AVX2 ComputePool path (compiled from the
          reference sources into oracle/_ref) on this host's cores (up to 16
          threads, the box's CPU share), on four layers' projections (0.93 GB);
@@ -160,6 +163,33 @@ def cpu_baseline(seconds=10.0, layers=4):
                       f"{len(times)} passes, median of all but the first; "
                       + ("reference quant::gemv (AVX2 + ComputePool) built from its sources"
                          if r is not None else "scalar C oracle")}
+
+
+def model_config4():
+    """BASELINE config 4 through the device-resident decoder (include/zq_model.h):
+    a random-init Llama-3-8B-shaped Q8_0 model generated on the device (no
+    8.5 GB file), a 512-token random prompt (seeded), then 128 greedily decoded
+    tokens (EOS disabled so all 128 are produced).  Two runs; the second is
+    reported (the first captures the decode graph)."""
+    import numpy as np
+    from zeninfer_amd.model import Model, PREFILL_INT8
+    m = Model.synthetic(seed=0x5EED0004, embedding=HIDDEN, layers=LAYERS, heads=32, kv_heads=8, ffn=FFN,
+                        vocab=VOCAB, context=8192, max_positions=1024, rope_base=500000.0, rms_epsilon=1e-5,
+                        eos_token=0xFFFFFFFF)
+    m.set_prefill_mode(PREFILL_INT8)
+    prompt = np.random.default_rng(0x5EED0004).integers(0, VOCAB, size=512).tolist()
+    for _ in range(2):
+        toks, pm, dm = m.generate(prompt, 128)
+    mem = m.memory()
+    m.close()
+    steps = len(toks) - 1
+    return {"workload": "config 4: Llama-3-8B-shaped dense forward, random-init Q8_0 weights generated on the device, "
+                        "512-token random prompt, 128 greedy tokens (int8-activation prefill GEMM, fp32 GEMV decode, "
+                        "decode step replayed as one HIP graph)",
+            "prefill_ms": round(pm, 2), "prefill_tok_s": round(512 / (pm * 1e-3), 1),
+            "decode_ms_per_token": round(dm / steps, 4), "decode_tok_s": round(steps / (dm * 1e-3), 1),
+            "tokens": len(toks), "weights_bytes": mem["weights"], "kv_cache_bytes": mem["kv_cache"],
+            "decode_weight_GB_s": round(mem["weights"] / (dm / steps * 1e-3) / 1e9, 1)}
 
 
 def main():
@@ -321,6 +351,9 @@ def main():
                       "TOPS_gemm": round(ops / (k_ms * 1e-3) / 1e12, 1),
                       "frac_int8_peak": round(ops / (k_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4)}
 
+    # ---- config 4: the device-resident decoder, prefill 512 + 128 greedy tokens
+    model4 = model_config4()
+
     cpu = None
     if not args.no_cpu:
         try:
@@ -352,6 +385,7 @@ def main():
         "per_shape_gemv": per_shape,
         "secondary": {"metric": "prefill GEMM int8 TOPS (% MFMA peak), config 2 at M=2048",
                       "prefill_gemm_int8_M2048": gemm, "int8_peak_tops": INT8_PEAK_TOPS},
+        "model_config4": model4,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out))
