@@ -46,11 +46,14 @@ extern "C" {
 /* ---- weight formats: GGML type ids (src/gguf.cpp:370-393) ---------------- */
 #define ZQ_FMT_Q4_0 2   /* 32 el / 18 B: fp16 d + 16 B nibbles   (src/quant.cpp:253)  */
 #define ZQ_FMT_Q8_0 8   /* 32 el / 34 B: fp16 d + 32 int8        (src/quant.cpp:257)  */
+#define ZQ_FMT_Q4_K 12  /* 256 el / 144 B super-block            (src/quant.cpp:273)  */
+#define ZQ_FMT_Q5_K 13  /* 256 el / 176 B super-block            (src/quant.cpp:274)  */
 #define ZQ_FMT_Q6_K 14  /* 256 el / 210 B super-block            (src/quant.cpp:259)  */
 
 /* ---- GEMM activation handling -------------------------------------------- */
 #define ZQ_ACT_DEFAULT 0 /* Q8_0/Q4_0: int8 (the D3D12 default q8_0_gemm_i8 route,
-                            src/backends/d3d12/d3d12_backend.cpp:845-854); Q6_K: fp32 */
+                            src/backends/d3d12/d3d12_backend.cpp:845-854); Q6_K, Q4_K,
+                            Q5_K: fp32 (their only reference routes) */
 #define ZQ_ACT_INT8 1    /* per-32 int8 activations, kernels/avx2.cpp:502-524 quantiser */
 #define ZQ_ACT_F32 2     /* fp32 activations, the reference CPU GEMM arithmetic          */
 

@@ -12,8 +12,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
 REF_PATH = os.path.join(HERE, "_ref", "libzenref.so")
 
-Q4_0, Q8_0, Q6_K = 2, 8, 14
-BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q6_K: (256, 210)}
+Q4_0, Q8_0, Q4_K, Q5_K, Q6_K = 2, 8, 12, 13, 14
+BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210)}
 
 _P = ctypes.c_void_p
 _S = ctypes.c_size_t
@@ -47,7 +47,7 @@ class Oracle:
         L.zqo_splitmix64_at.argtypes = [_U64, _U64]
         L.zqo_normal_at.restype = ctypes.c_double
         L.zqo_normal_at.argtypes = [_U64, _U64]
-        for name in ("zqo_gen_q8_0", "zqo_gen_q4_0", "zqo_gen_q6_k"):
+        for name in ("zqo_gen_q8_0", "zqo_gen_q4_0", "zqo_gen_q6_k", "zqo_gen_q4_k", "zqo_gen_q5_k"):
             getattr(L, name).argtypes = [_U64, _S, _S, _P]
         L.zqo_gen_normal_f32.argtypes = [_U64, _S, _P]
         L.zqo_decode_fp16.argtypes = [_P, _P, _S]
@@ -89,7 +89,8 @@ class Oracle:
         if not rb:
             raise ValueError("cols not a multiple of the block size")
         out = np.empty(rows * rb, np.uint8)
-        fn = {Q8_0: self.L.zqo_gen_q8_0, Q4_0: self.L.zqo_gen_q4_0, Q6_K: self.L.zqo_gen_q6_k}[fmt]
+        fn = {Q8_0: self.L.zqo_gen_q8_0, Q4_0: self.L.zqo_gen_q4_0, Q6_K: self.L.zqo_gen_q6_k,
+              Q4_K: self.L.zqo_gen_q4_k, Q5_K: self.L.zqo_gen_q5_k}[fmt]
         fn(seed, rows, cols, _ptr(out))
         return out
 

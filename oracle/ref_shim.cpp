@@ -28,6 +28,8 @@ const zen::quant::Format* fmt_of(int ggml_type) {
     switch (ggml_type) {  // ggml type ids, src/gguf.cpp:370-393
     case 2: return zen::quant::find("Q4_0");
     case 8: return zen::quant::find("Q8_0");
+    case 12: return zen::quant::find("Q4_K");
+    case 13: return zen::quant::find("Q5_K");
     case 14: return zen::quant::find("Q6_K");
     default: return nullptr;
     }

@@ -2,7 +2,7 @@
  * zq_oracle.c -- TEST INFRASTRUCTURE ONLY (the checker, never the product).
  *
  * A plain-C restatement of ZenInfer's CPU algorithms for the block-quantised
- * projection path (Q8_0 / Q4_0 / Q6_K GEMV and GEMM).  Only tests/, the
+ * projection path (Q8_0 / Q4_0 / Q6_K / Q4_K / Q5_K GEMV and GEMM).  Only tests/, the
  * smoke check in __graft_entry__.py and the cpu_baseline leg of bench.py may
  * load this library.  The HIP product path never links or calls it.
  *
@@ -42,6 +42,8 @@
 
 #define ZQO_Q4_0 2
 #define ZQO_Q8_0 8
+#define ZQO_Q4_K 12
+#define ZQO_Q5_K 13
 #define ZQO_Q6_K 14
 
 /* ---------------------------------------------------------------- fp16 --- */
@@ -104,12 +106,15 @@ void zqo_encode_fp16(const float* src, uint16_t* dst, size_t n) { for (size_t i 
 static uint16_t rd16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
 
 /* -------------------------------------------------------------- layout --- */
-/* row_bytes: src/quant.cpp:894-943 (Q4_0 :917, Q8_0 :921, Q6_K :940). */
+/* row_bytes: src/quant.cpp:894-943 (Q4_0 :917, Q8_0 :921, Q4_K :919,
+ * Q5_K :920, Q6_K :940). */
 size_t zqo_row_bytes(int fmt, size_t cols) {
     size_t blk, bytes;
     switch (fmt) {
     case ZQO_Q4_0: blk = 32; bytes = 18; break;
     case ZQO_Q8_0: blk = 32; bytes = 34; break;
+    case ZQO_Q4_K: blk = 256; bytes = 144; break;
+    case ZQO_Q5_K: blk = 256; bytes = 176; break;
     case ZQO_Q6_K: blk = 256; bytes = 210; break;
     default: return 0;
     }
@@ -195,8 +200,53 @@ void zqo_gen_q6_k(uint64_t seed, size_t rows, size_t cols, uint8_t* out) {
     }
 }
 
+/* Q4_K / Q5_K (config-3 style; the reference names no generator for them):
+ * fp16 d = |N|*0.001 and dmin = |N|*0.001, twelve bytes of uniformly random
+ * packed 6-bit scales/mins, quants U{0..15} (Q4_K) or U{0..31} (Q5_K, the
+ * fifth bit in the qh plane).  Every byte of the packed fields is a uniform
+ * draw, so all scale/min bit positions are exercised. */
+static void gen_kquant(uint64_t seed, size_t rows, size_t cols, uint8_t* out, int q5) {
+    size_t nb = cols / 256, bb = q5 ? 176 : 144, qs = q5 ? 48 : 16;
+    for (size_t g = 0; g < rows * nb; ++g) {
+        uint8_t* p = out + g * bb;
+        uint16_t d = zqo_float_to_half((float)(fabs(zqo_normal_at(SEED_SCALE(seed), 2 * g)) * 0.001));
+        uint16_t m = zqo_float_to_half((float)(fabs(zqo_normal_at(SEED_SCALE(seed), 2 * g + 1)) * 0.001));
+        p[0] = (uint8_t)d; p[1] = (uint8_t)(d >> 8); p[2] = (uint8_t)m; p[3] = (uint8_t)(m >> 8);
+        for (int i = 0; i < 12; ++i) p[4 + i] = (uint8_t)(zqo_splitmix64_at(SEED_SUB(seed), g * 12 + i) >> 56);
+        for (size_t i = 16; i < qs; ++i) p[i] = (uint8_t)(zqo_splitmix64_at(SEED_QUANT(seed) ^ 0xB17ull, g * 32 + (i - 16)) >> 56);
+        for (int i = 0; i < 128; ++i) p[qs + i] = (uint8_t)(zqo_splitmix64_at(SEED_QUANT(seed), g * 128 + i) >> 56);
+    }
+}
+void zqo_gen_q4_k(uint64_t seed, size_t rows, size_t cols, uint8_t* out) { gen_kquant(seed, rows, cols, out, 0); }
+void zqo_gen_q5_k(uint64_t seed, size_t rows, size_t cols, uint8_t* out) { gen_kquant(seed, rows, cols, out, 1); }
+
+/* k_scale_min: src/quant.cpp:133-141 (the 12-byte packed 6-bit scale/min
+ * pairs of Q4_K / Q5_K). */
+static void k_scale_min(unsigned j, const uint8_t* q, unsigned* sc, unsigned* mn) {
+    if (j < 4) { *sc = q[j] & 63u; *mn = q[j + 4] & 63u; }
+    else {
+        *sc = (q[j + 4] & 15u) | ((unsigned)(q[j - 4] >> 6) << 4);
+        *mn = (q[j + 4] >> 4) | ((unsigned)(q[j] >> 6) << 4);
+    }
+}
+/* Element e (0..255) of a Q4_K / Q5_K super-block as its integer quant and
+ * group index: group j = e/32 reads the low (j even) or high (j odd) nibble
+ * of qs[(j/2)*32 + e%32]; Q5_K adds bit j of qh[e%32] as bit 4
+ * (src/quant.cpp:439-476). */
+static unsigned kquant_q(const uint8_t* p, unsigned e, int q5) {
+    unsigned j = e / 32, l = e % 32;
+    const uint8_t* qs = p + (q5 ? 48 : 16);
+    unsigned q = (qs[(j / 2) * 32 + l] >> ((j & 1u) * 4)) & 15u;
+    if (q5) q |= ((p[16 + l] >> j) & 1u) << 4;
+    return q;
+}
+
 /* ----------------------------------------------------------- dequantize -- */
-/* Q4_0: src/quant.cpp:391-397.  Q8_0: :410-416.  Q6_K: :500-517. */
+/* Q4_0: src/quant.cpp:391-397.  Q8_0: :410-416.  Q6_K: :500-517.
+ * Q4_K: :439-457, Q5_K: :458-476: value = (d*sc)*q - dmin*m.  d*sc and
+ * dmin*m are exact (11-bit by 6-bit significands) and so is (d*sc)*q (a
+ * further 5 bits), so the one rounding is the subtraction, whether or not a
+ * compiler fuses the multiply into it. */
 int zqo_dequantize(int fmt, const uint8_t* src, size_t n, float* dst) {
     switch (fmt) {
     case ZQO_Q4_0:
@@ -217,6 +267,24 @@ int zqo_dequantize(int fmt, const uint8_t* src, size_t n, float* dst) {
             for (int j = 0; j < 32; ++j) dst[b * 32 + j] = (float)(int8_t)p[2 + j] * d;
         }
         return 1;
+    case ZQO_Q4_K:
+    case ZQO_Q5_K: {
+        int q5 = fmt == ZQO_Q5_K;
+        size_t bb = q5 ? 176 : 144;
+        if (n % 256) return 0;
+        for (size_t b = 0; b < n / 256; ++b) {
+            const uint8_t* p = src + b * bb;
+            float d = zqo_half_to_float(rd16(p)), dmin = zqo_half_to_float(rd16(p + 2));
+            for (unsigned e = 0; e < 256; ++e) {
+                unsigned sc, mn;
+                k_scale_min(e / 32, p + 4, &sc, &mn);
+                float ds = d * (float)sc, ms = dmin * (float)mn;
+                float t = ds * (float)kquant_q(p, e, q5);
+                dst[b * 256 + e] = t - ms;
+            }
+        }
+        return 1;
+    }
     case ZQO_Q6_K:
         if (n % 256) return 0;
         for (size_t b = 0; b < n / 256; ++b) {
@@ -277,7 +345,7 @@ void zqo_quantize_acts(const float* x, size_t m, size_t k, int8_t* xq, float* xs
  *         (build-defined; quant.cpp:500-517 values, d applied outside).
  * out is [m][n][k/32] int32, computed in int64 and checked to fit. */
 int zqo_block_dots(int fmt, const uint8_t* w, const int8_t* xq, size_t m, size_t n, size_t k, int32_t* out) {
-    size_t rb = zqo_row_bytes(fmt, k); if (!rb || k % 32) return 0;
+    size_t rb = zqo_row_bytes(fmt, k); if (!rb || k % 32 || fmt == ZQO_Q4_K || fmt == ZQO_Q5_K) return 0;
     size_t nb = k / 32;
     float* row = NULL; (void)row;
     int* qi = (int*)malloc(sizeof(int) * k);
@@ -378,6 +446,33 @@ static float gemv_row_q6_k(const uint8_t* row, const float* x, size_t cols) {
     for (int i = 0; i < 8; ++i) v[i] = (sums[0][i] + sums[1][i]) + (sums[2][i] + sums[3][i]);
     return hsum8(v);
 }
+/* Q4_K / Q5_K: gemv_q4k_q5k_avx2, kernels/avx2.cpp:329-378.  Four 8-lane
+ * accumulators: element group*32 + chunk*8 + i of every super-block goes to
+ * acc[chunk][i] as fma(w, x, acc) with w = (d*sc)*q - dmin*m (exact product,
+ * one rounding); the end is hsum_ps256((acc0 + acc1) + (acc2 + acc3)). */
+static float gemv_row_kquant(const uint8_t* row, const float* x, size_t cols, int q5) {
+    float acc[4][8] = {{0}};
+    size_t bb = q5 ? 176 : 144;
+    for (size_t b = 0; b < cols / 256; ++b) {
+        const uint8_t* p = row + b * bb;
+        float d = zqo_half_to_float(rd16(p)), dm = zqo_half_to_float(rd16(p + 2));
+        for (unsigned group = 0; group < 8; ++group) {
+            unsigned sc, mn;
+            k_scale_min(group, p + 4, &sc, &mn);
+            float ds = d * (float)sc, ms = dm * (float)mn;
+            for (unsigned chunk = 0; chunk < 4; ++chunk)
+                for (unsigned i = 0; i < 8; ++i) {
+                    unsigned e = group * 32 + chunk * 8 + i;
+                    float t = ds * (float)kquant_q(p, e, q5);
+                    float w = t - ms;
+                    acc[chunk][i] = fmaf(w, x[b * 256 + e], acc[chunk][i]);
+                }
+        }
+    }
+    float v[8];
+    for (int i = 0; i < 8; ++i) v[i] = (acc[0][i] + acc[1][i]) + (acc[2][i] + acc[3][i]);
+    return hsum8(v);
+}
 /* gemv_avx2 on one fp32 row: kernels/avx2.cpp:16-39 (four 8-lane
  * accumulators over 32-column strides, sequential lane sum). */
 static float dot_gemv_avx2(const float* row, const float* x, size_t k) {
@@ -396,7 +491,8 @@ static float dot_gemv_avx2(const float* row, const float* x, size_t k) {
 
 /* quant::gemv with fp32 activations (the reference default):
  * Q8_0 -> gemv_q8_0_avx2 (src/quant.cpp:1080-1133), Q6_K -> gemv_q6k_avx2
- * (:1039-1054), Q4_0 -> dequantise row + gemv_avx2 (:1135-1162). */
+ * (:1039-1054), Q4_K / Q5_K -> gemv_q4k_q5k_avx2 (:1016-1032), Q4_0 ->
+ * dequantise row + gemv_avx2 (:1135-1162). */
 int zqo_gemv_f32(int fmt, const uint8_t* w, const float* x, float* y, size_t rows, size_t cols) {
     size_t rb = zqo_row_bytes(fmt, cols); if (!rb) return 0;
     float* tmp = NULL;
@@ -405,6 +501,7 @@ int zqo_gemv_f32(int fmt, const uint8_t* w, const float* x, float* y, size_t row
         const uint8_t* row = w + r * rb;
         if (fmt == ZQO_Q8_0) y[r] = gemv_row_q8_0(row, x, cols);
         else if (fmt == ZQO_Q6_K) y[r] = gemv_row_q6_k(row, x, cols);
+        else if (fmt == ZQO_Q4_K || fmt == ZQO_Q5_K) y[r] = gemv_row_kquant(row, x, cols, fmt == ZQO_Q5_K);
         else { zqo_dequantize(fmt, row, cols, tmp); y[r] = dot_gemv_avx2(tmp, x, cols); }
     }
     free(tmp);
@@ -462,23 +559,26 @@ static float dot_main_order(const float* row, const float* x, size_t k) {
  *    otherwise gemm_q8_0_avx2 (kernels/avx2.cpp:772-840): row pairs x token
  *      quads use the main order, leftover tokens and an odd last row use
  *      dot_f32_avx2.
- *  Q6_K -> gemm_q6k_kblk_avx2 = gemm_kblk_impl (:1729-1770, :1470-1545):
- *    rows in groups of 4 main order, trailing rows dot_f32_avx2.
+ *  Q6_K -> gemm_q6k_kblk_avx2 = gemm_kblk_impl (:1729-1770, :1470-1545),
+ *  Q4_K -> gemm_q4k_kblk_avx2 (:1613-1628), Q5_K -> gemm_q5k_kblk_avx2
+ *    (:1605-1611), both gemm_kblk_impl over panels that dequantise to the
+ *    dequantize() values (:1351-1435): rows in groups of 4 main order,
+ *    trailing rows dot_f32_avx2.
  *  Q4_0 -> generic route (src/quant.cpp:1747-1776): dequantise row, then
  *    gemv_avx2 per token.
- *  tokens == 1 is the gemv route. */
+ *  tokens == 1: every fast route needs tokens >= 2 (:1661, :1701, :1715), so
+ *    a single token takes the generic route too. */
 int zqo_gemm_f32(int fmt, const uint8_t* w, const float* X, float* Y, size_t m, size_t n, size_t k) {
     size_t rb = zqo_row_bytes(fmt, k); if (!rb) return 0;
-    if (m == 1) return zqo_gemv_f32(fmt, w, X, Y, n, k);
     float* row = (float*)malloc(sizeof(float) * k); if (!row) return 0;
-    int kblk = fmt == ZQO_Q6_K || (fmt == ZQO_Q8_0 && m * k >= 131072);
+    int kblk = fmt == ZQO_Q6_K || fmt == ZQO_Q4_K || fmt == ZQO_Q5_K || (fmt == ZQO_Q8_0 && m * k >= 131072);
     size_t rows_main = kblk ? n / 4 * 4 : n / 2 * 2;
     for (size_t r = 0; r < n; ++r) {
         zqo_dequantize(fmt, w + r * rb, k, row);
         for (size_t t = 0; t < m; ++t) {
             const float* x = X + t * k;
             float v;
-            if (fmt == ZQO_Q4_0) v = dot_gemv_avx2(row, x, k);
+            if (fmt == ZQO_Q4_0 || m == 1) v = dot_gemv_avx2(row, x, k);
             else if (r >= rows_main) v = dot_f32_avx2(row, x, k);
             else if (kblk) v = dot_main_order(row, x, k);
             else v = t < m / 4 * 4 ? dot_main_order(row, x, k) : dot_f32_avx2(row, x, k);
@@ -498,7 +598,7 @@ int zqo_gemm_f32(int fmt, const uint8_t* w, const float* X, float* Y, size_t m, 
  * zqo_block_dots (Q6_K: d_w is the super-block d; the int8 sub-scales are
  * inside the integer dot). */
 int zqo_gemm_i8(int fmt, const uint8_t* w, const float* X, float* Y, size_t m, size_t n, size_t k) {
-    size_t rb = zqo_row_bytes(fmt, k); if (!rb || k % 32) return 0;
+    size_t rb = zqo_row_bytes(fmt, k); if (!rb || k % 32 || fmt == ZQO_Q4_K || fmt == ZQO_Q5_K) return 0;
     size_t nb = k / 32;
     int8_t* xq = (int8_t*)malloc(m * k); float* xs = (float*)malloc(sizeof(float) * m * nb);
     int32_t* dots = NULL;

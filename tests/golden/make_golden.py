@@ -30,7 +30,9 @@ CASES = [  # (fmt, rows, cols, tokens)
     (O.Q8_0, 33, 256, 5), (O.Q8_0, 8, 4096, 3), (O.Q8_0, 5, 96, 2),
     (O.Q4_0, 33, 256, 5), (O.Q4_0, 7, 1024, 4),
     (O.Q6_K, 33, 256, 5), (O.Q6_K, 6, 1280, 3),
+    (O.Q4_K, 33, 256, 5), (O.Q4_K, 6, 1280, 3), (O.Q5_K, 33, 256, 5), (O.Q5_K, 7, 768, 4),
 ]
+NAME = {O.Q8_0: "q8", O.Q4_0: "q4", O.Q6_K: "q6", O.Q4_K: "k4", O.Q5_K: "k5"}
 
 
 def int8_route(path_npz):
@@ -59,7 +61,7 @@ np.savez({path_npz + '.i8.npz'!r}, **out)
 def main():
     O.build()
     o, r = O.Oracle(), O.Reference()
-    name = {O.Q8_0: "q8", O.Q4_0: "q4", O.Q6_K: "q6"}
+    name = NAME
     data = {}
     for i, (fmt, rows, cols, tokens) in enumerate(CASES):
         p = f"{name[fmt]}_{rows}x{cols}"
@@ -71,6 +73,7 @@ def main():
         data[p + "_ref_dequant"] = r.dequantize(fmt, w, rows * cols)
         data[p + "_ref_gemv"] = r.gemv(fmt, w, X[:cols], rows, cols, 1)
         data[p + "_ref_gemm"] = r.gemm(fmt, w, X, tokens, rows, cols, 1)
+        data[p + "_ref_gemm1"] = r.gemm(fmt, w, X[:cols], 1, rows, cols, 1)
     tmp = os.path.join(HERE, "ref_vectors.npz")
     np.savez_compressed(tmp, **data)
     data.update(int8_route(tmp))

@@ -128,6 +128,114 @@ def test_dequant_closed_form(orc, fmt):
     assert np.array_equal(got.view(np.uint32), _np_dequant(fmt, w, 9, 512).view(np.uint32))
 
 
+# ------------------------------------------------------ Q4_K / Q5_K ----
+def test_kquant_kat(orc):
+    """tests/core_tests.cpp:134-159: d=1, dmin=0, scales 1, nibbles 1/2; the
+    Q5_K variant sets qh[0] bit 0, which lifts element 0 by 16."""
+    q4 = np.zeros(144, np.uint8)
+    q4[0:4] = [0x00, 0x3C, 0x00, 0x00]
+    q4[4:8] = 1
+    q4[12:16] = 1
+    q4[16:] = 0x21
+    out = orc.dequantize(O.Q4_K, q4, 256)
+    assert np.array_equal(out, np.where((np.arange(256) // 32) % 2 == 0, 1.0, 2.0).astype(np.float32))
+    q5 = np.zeros(176, np.uint8)
+    q5[0:4] = [0x00, 0x3C, 0x00, 0x00]
+    q5[4:8] = 1
+    q5[12:16] = 1
+    q5[16] = 1
+    q5[48:] = 0x21
+    want = np.where((np.arange(256) // 32) % 2 == 0, 1.0, 2.0).astype(np.float32)
+    want[0] += 16
+    assert np.array_equal(orc.dequantize(O.Q5_K, q5, 256), want)
+
+
+def _build_q5k(rng, rows, cols):
+    """Constructive Q5_K after tests/q5k_gemm_tests.cpp:12-30: d=0.25,
+    dmin=0.5, every scale and min 1, so element = 0.25*q - 0.5 for the
+    independently drawn q in 0..31, packed nibble by nibble and bit by bit."""
+    nb = cols // 256
+    w = np.zeros((rows, nb, 176), np.uint8)
+    q = rng.integers(0, 32, size=(rows, nb, 8, 32))  # [row, sb, group, lane]
+    w[:, :, 0:4] = [0x00, 0x34, 0x00, 0x38]
+    w[:, :, 4:12] = 1
+    w[:, :, 12:16] = 0x11
+    for g in range(8):
+        nib = (q[:, :, g, :] & 15).astype(np.uint8)
+        sl = slice(48 + (g // 2) * 32, 48 + (g // 2) * 32 + 32)
+        w[:, :, sl] |= nib << 4 if g % 2 else nib
+        w[:, :, 16:48] |= ((q[:, :, g, :] >> 4) << g).astype(np.uint8)
+    known = (0.25 * q - 0.5).astype(np.float32).reshape(rows, cols)
+    return w.reshape(-1), known
+
+
+def test_q5_k_constructive(orc):
+    rng = np.random.default_rng(12)
+    for rows, cols in ((1, 256), (5, 768), (67, 768)):
+        w, known = _build_q5k(rng, rows, cols)
+        got = orc.dequantize(O.Q5_K, w, rows * cols).reshape(rows, cols)
+        assert np.array_equal(got, known)
+        for tokens in (1, 2, 3, 8):
+            x = (rng.integers(0, 256, size=tokens * cols) - 128).astype(np.float32) / 128
+            ref = known.astype(np.float64) @ x.reshape(tokens, cols).T.astype(np.float64)
+            mag = np.abs(known.astype(np.float64)) @ np.abs(x.reshape(tokens, cols).T.astype(np.float64))
+            y = orc.gemm_f32(O.Q5_K, w, x, tokens, rows, cols).reshape(tokens, rows)
+            assert (np.abs(y - ref.T) <= 2e-5 * np.maximum(1.0, mag.T)).all()
+
+
+def _np_kquant_dequant(w, rows, cols, q5):
+    """Textbook decoder of the GGML K-quant layout, independent of the C
+    oracle: 6-bit scale/min pairs (j<4: q[j]&63, q[j+4]&63; j>=4: low/high
+    nibble of q[j+4] with the top two bits of q[j-4] / q[j]), value
+    (d*sc)*q - dmin*m."""
+    bb = 176 if q5 else 144
+    b = w.reshape(rows, cols // 256, bb)
+    d = b[:, :, 0:2].copy().view(np.float16).astype(np.float32)[..., 0]
+    dm = b[:, :, 2:4].copy().view(np.float16).astype(np.float32)[..., 0]
+    s = b[:, :, 4:16].astype(np.uint32)
+    sc = np.empty(b.shape[:2] + (8,), np.uint32)
+    mn = np.empty_like(sc)
+    for j in range(8):
+        if j < 4:
+            sc[..., j], mn[..., j] = s[..., j] & 63, s[..., j + 4] & 63
+        else:
+            sc[..., j] = (s[..., j + 4] & 15) | ((s[..., j - 4] >> 6) << 4)
+            mn[..., j] = (s[..., j + 4] >> 4) | ((s[..., j] >> 6) << 4)
+    qs = b[:, :, (48 if q5 else 16):].reshape(rows, cols // 256, 4, 32).astype(np.uint32)
+    q = np.empty(b.shape[:2] + (8, 32), np.uint32)
+    for j in range(8):
+        q[:, :, j] = (qs[:, :, j // 2] >> (4 * (j % 2))) & 15
+        if q5:
+            q[:, :, j] |= ((b[:, :, 16:48].astype(np.uint32) >> j) & 1) << 4
+    ds = (d[..., None] * sc.astype(np.float32)).astype(np.float32)
+    ms = (dm[..., None] * mn.astype(np.float32)).astype(np.float32)
+    v = (ds[..., None] * q.astype(np.float32)).astype(np.float32) - ms[..., None]
+    return v.astype(np.float32).reshape(rows, cols)
+
+
+@pytest.mark.parametrize("fmt", [O.Q4_K, O.Q5_K])
+def test_kquant_closed_form_random_blocks(orc, fmt):
+    """Random bytes with finite scales incl. fp16 subnormals and negative d,
+    as in tests/core_tests.cpp:202-216."""
+    rows, cols = 67, 768
+    bb = 176 if fmt == O.Q5_K else 144
+    rng = np.random.default_rng(13)
+    w = rng.integers(0, 256, size=(rows, cols // 256, bb), dtype=np.uint8)
+    for r in range(rows):
+        for b in range(cols // 256):
+            ds = 0x0001 if b % 3 == 0 else (0xA800 if r % 2 else 0x2800)
+            dm = 0x2000 if b % 2 else 0x1800
+            w[r, b, 0:4] = [ds & 255, ds >> 8, dm & 255, dm >> 8]
+    w = w.reshape(-1)
+    got = orc.dequantize(fmt, w, rows * cols).reshape(rows, cols)
+    assert np.array_equal(got.view(np.uint32), _np_kquant_dequant(w, rows, cols, fmt == O.Q5_K).view(np.uint32))
+    x = np.array([float(int((c * 17) % 101) - 50) * 0.013 for c in range(cols)], np.float32)
+    y = orc.gemv_f32(fmt, w, x, rows, cols)
+    ref = got.astype(np.float64) @ x.astype(np.float64)
+    mag = np.abs(got.astype(np.float64)) @ np.abs(x.astype(np.float64))
+    assert (np.abs(y - ref) <= 2e-5 * np.maximum(1.0, mag)).all()
+
+
 # ------------------------------------------------- activation quantiser ----
 def _np_quantize(x, m, k):
     """kernels/avx2.cpp:502-524 in numpy float32 arithmetic."""
@@ -188,7 +296,7 @@ def _golden():
     return dict(np.load(os.path.join(GOLDEN, "ref_vectors.npz")))
 
 
-FMT_OF = {"q8": O.Q8_0, "q4": O.Q4_0, "q6": O.Q6_K}
+FMT_OF = {"q8": O.Q8_0, "q4": O.Q4_0, "q6": O.Q6_K, "k4": O.Q4_K, "k5": O.Q5_K}
 
 
 def _cases():
@@ -208,25 +316,26 @@ def test_oracle_matches_reference_golden(orc, case):
     # bit equality with the reference's AVX2 kernels (same fp32 operation order)
     assert np.array_equal(orc.gemv_f32(fmt, w, X[:cols], rows, cols), g[case + "_ref_gemv"])
     assert np.array_equal(orc.gemm_f32(fmt, w, X, tokens, rows, cols), g[case + "_ref_gemm"])
+    assert np.array_equal(orc.gemm_f32(fmt, w, X[:cols], 1, rows, cols), g[case + "_ref_gemm1"])
     if case + "_ref_gemm_i8" in g:
         assert np.array_equal(orc.gemm_i8(fmt, w, X, tokens, rows, cols), g[case + "_ref_gemm_i8"])
 
 
 def _cases_index(case):
-    from tests.golden.make_golden import CASES
-    name = {O.Q8_0: "q8", O.Q4_0: "q4", O.Q6_K: "q6"}
-    keys = [f"{name[f]}_{r}x{c}" for f, r, c, _ in CASES]
+    from tests.golden.make_golden import CASES, NAME
+    keys = [f"{NAME[f]}_{r}x{c}" for f, r, c, _ in CASES]
     return keys.index(case)
 
 
 @pytest.mark.parametrize("fmt,rows,cols", [(O.Q8_0, 67, 1024), (O.Q4_0, 35, 768), (O.Q6_K, 35, 1280),
-                                           (O.Q8_0, 130, 4096)])
+                                           (O.Q8_0, 130, 4096), (O.Q4_K, 67, 768), (O.Q4_K, 9, 4096),
+                                           (O.Q5_K, 67, 768), (O.Q5_K, 10, 4096)])
 def test_oracle_matches_compiled_reference(orc, ref, fmt, rows, cols):
     w = orc.gen_weights(fmt, 21, rows, cols)
     x = orc.gen_normal(22, 9 * cols)
     assert np.array_equal(orc.dequantize(fmt, w, rows * cols), ref.dequantize(fmt, w, rows * cols))
     assert np.array_equal(orc.gemv_f32(fmt, w, x[:cols], rows, cols), ref.gemv(fmt, w, x[:cols], rows, cols))
-    for m in (2, 5, 9):
+    for m in (1, 2, 5, 9):
         assert np.array_equal(orc.gemm_f32(fmt, w, x[:m * cols], m, rows, cols), ref.gemm(fmt, w, x[:m * cols], m, rows, cols))
 
 
@@ -239,7 +348,8 @@ def test_fp16_codec_matches_compiled_reference(orc, ref):
 
 
 # --------------------------------------------------- double references -----
-@pytest.mark.parametrize("fmt,cols", [(O.Q8_0, 4096), (O.Q4_0, 4096), (O.Q6_K, 4096), (O.Q8_0, 14336)])
+@pytest.mark.parametrize("fmt,cols", [(O.Q8_0, 4096), (O.Q4_0, 4096), (O.Q6_K, 4096), (O.Q8_0, 14336),
+                                      (O.Q4_K, 4096), (O.Q5_K, 14336)])
 def test_fp32_paths_within_tolerance_of_double(orc, fmt, cols):
     rows, m = 16, 3
     w = orc.gen_weights(fmt, 31, rows, cols)

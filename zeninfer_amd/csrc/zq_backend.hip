@@ -179,17 +179,23 @@ int ensure_scratch(Backend& b, size_t dev_bytes, size_t host_bytes) {
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
-bool valid_fmt(int fmt) { return fmt == ZQ_FMT_Q4_0 || fmt == ZQ_FMT_Q8_0 || fmt == ZQ_FMT_Q6_K; }
+bool valid_fmt(int fmt) {
+    return fmt == ZQ_FMT_Q4_0 || fmt == ZQ_FMT_Q8_0 || fmt == ZQ_FMT_Q4_K || fmt == ZQ_FMT_Q5_K || fmt == ZQ_FMT_Q6_K;
+}
+// Formats with an int8-activation GEMM (per-32 blocks).  The K-quants keep
+// fp32 activations, as every reference route for them does (the CPU
+// gemm_q4k/q5k_kblk_avx2 and the D3D12 shaders/q8_0_gemm_q4k.hlsl).
+bool int8_fmt(int fmt) { return fmt == ZQ_FMT_Q4_0 || fmt == ZQ_FMT_Q8_0; }
 
 int resolve_act(int fmt, int act_mode) {
-    if (act_mode == ZQ_ACT_DEFAULT) return fmt == ZQ_FMT_Q6_K ? ZQ_ACT_F32 : ZQ_ACT_INT8;
+    if (act_mode == ZQ_ACT_DEFAULT) return int8_fmt(fmt) ? ZQ_ACT_INT8 : ZQ_ACT_F32;
     return act_mode;
 }
 
 // GEMM support check shared by the host and device entry points.
 int gemm_supported(int fmt, size_t cols, int act) {
     if (act != ZQ_ACT_INT8 && act != ZQ_ACT_F32) return ZQ_ERR_ARG;
-    if (act == ZQ_ACT_INT8 && (fmt == ZQ_FMT_Q6_K || cols % 64)) return ZQ_DECLINED;
+    if (act == ZQ_ACT_INT8 && (!int8_fmt(fmt) || cols % 64)) return ZQ_DECLINED;
     return ZQ_OK;
 }
 
@@ -573,7 +579,7 @@ int zq_hip_quantize_acts_dev(const float* X, int8_t* xq, float* xs, size_t token
 int zq_hip_block_dots_dev(int fmt, const void* weights, const int8_t* xq, int32_t* out, size_t tokens, size_t rows,
                           size_t cols, void* stream) {
     if (!weights || !xq || !out || !tokens || !rows || !valid_fmt(fmt) || !zq::row_bytes(fmt, cols)) return ZQ_ERR_ARG;
-    if (fmt == ZQ_FMT_Q6_K || cols % 64) return ZQ_DECLINED;
+    if (!int8_fmt(fmt) || cols % 64) return ZQ_DECLINED;
     return zq::launch_block_dots(fmt, static_cast<const uint8_t*>(weights), xq, out, tokens, rows, cols,
                                  static_cast<hipStream_t>(stream)) == hipSuccess
                ? ZQ_OK

@@ -6,9 +6,12 @@
 
 namespace zq {
 
-// GGML type ids (src/gguf.cpp:370-393 of the reference: 2=Q4_0, 8=Q8_0, 14=Q6_K).
+// GGML type ids (src/gguf.cpp:370-393 of the reference: 2=Q4_0, 8=Q8_0,
+// 12=Q4_K, 13=Q5_K, 14=Q6_K).
 constexpr int kQ4_0 = 2;
 constexpr int kQ8_0 = 8;
+constexpr int kQ4_K = 12;
+constexpr int kQ5_K = 13;
 constexpr int kQ6_K = 14;
 
 constexpr int kWave = 64;
@@ -45,13 +48,31 @@ __device__ __forceinline__ uint32_t load_u32_a2(const uint8_t* p) {
 }
 
 __host__ __device__ inline size_t row_bytes_dev(int fmt, size_t cols) {
-    return fmt == kQ8_0 ? cols / 32 * 34 : fmt == kQ4_0 ? cols / 32 * 18 : cols / 256 * 210;
+    return fmt == kQ8_0   ? cols / 32 * 34
+           : fmt == kQ4_0 ? cols / 32 * 18
+           : fmt == kQ4_K ? cols / 256 * 144
+           : fmt == kQ5_K ? cols / 256 * 176
+                          : cols / 256 * 210;
+}
+
+// Q4_K / Q5_K packed 6-bit scale and min of group j (0..7) from the 12 bytes
+// at s (src/quant.cpp:133-141 of the reference).
+__device__ __forceinline__ void kquant_scale_min(const uint8_t* s, uint32_t j, uint32_t& sc, uint32_t& mn) {
+    if (j < 4) {
+        sc = s[j] & 63u;
+        mn = s[j + 4] & 63u;
+    } else {
+        sc = (s[j + 4] & 15u) | (uint32_t(s[j - 4] >> 6) << 4);
+        mn = (s[j + 4] >> 4) | (uint32_t(s[j] >> 6) << 4);
+    }
 }
 
 // Exact dequantisation of the 32 consecutive elements [k0, k0+32) of one
 // weight row (k0 % 32 == 0), to the values of the reference's dequantize:
 // Q8_0 int8(q)*d (src/quant.cpp:410-416), Q4_0 (n-8)*d (:391-397), Q6_K
-// (d*sc)*(q-32) (:500-517).  Reads stay inside the blocks they decode.
+// (d*sc)*(q-32) (:500-517), Q4_K / Q5_K (d*sc)*q - dmin*m (:439-476; d*sc,
+// dmin*m and (d*sc)*q are exact, the subtraction is the one rounding).
+// Reads stay inside the blocks they decode.
 template <int FMT>
 __device__ __forceinline__ void dequant32(const uint8_t* row, uint32_t k0, float (&o)[32]) {
     if constexpr (FMT == kQ8_0) {
@@ -74,6 +95,27 @@ __device__ __forceinline__ void dequant32(const uint8_t* row, uint32_t k0, float
                 const uint32_t byte = (u >> (8 * k)) & 0xffu;
                 o[4 * i + k] = float(int(byte & 15u) - 8) * d;
                 o[16 + 4 * i + k] = float(int(byte >> 4) - 8) * d;
+            }
+        }
+    } else if constexpr (FMT == kQ4_K || FMT == kQ5_K) {
+        constexpr uint32_t BB = FMT == kQ5_K ? 176 : 144;
+        const uint8_t* p = row + size_t(k0 >> 8) * BB;
+        const uint32_t j = (k0 & 255u) >> 5;  // group
+        uint32_t sc, mn;
+        kquant_scale_min(p + 4, j, sc, mn);
+        const float ds = half_bits_to_float(*reinterpret_cast<const uint16_t*>(p)) * float(sc);
+        const float ms = half_bits_to_float(*reinterpret_cast<const uint16_t*>(p + 2)) * float(mn);
+        const uint8_t* qs = p + (FMT == kQ5_K ? 48 : 16) + (j >> 1) * 32;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t u = *reinterpret_cast<const uint32_t*>(qs + 4 * i);
+            uint32_t hb = 0;
+            if constexpr (FMT == kQ5_K) hb = *reinterpret_cast<const uint32_t*>(p + 16 + 4 * i);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                uint32_t q = (u >> (8 * k + 4 * (j & 1u))) & 15u;
+                if constexpr (FMT == kQ5_K) q |= ((hb >> (8 * k + j)) & 1u) << 4;
+                o[4 * i + k] = __fsub_rn(__fmul_rn(ds, float(q)), ms);
             }
         }
     } else {

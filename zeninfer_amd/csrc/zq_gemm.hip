@@ -794,6 +794,7 @@ hipError_t launch_gemm_f32(int fmt, const uint8_t* w, const float* X, float* Y, 
     if (!w || !X || !Y || !M || !N || !row_bytes(fmt, K) || M > (1u << 24) || N > (1u << 24) || K > (1u << 24))
         return hipErrorInvalidValue;
     if ((reinterpret_cast<uintptr_t>(w) & 1u) || (reinterpret_cast<uintptr_t>(X) & 15u)) return hipErrorInvalidValue;
+    if ((fmt == kQ4_K || fmt == kQ5_K) && (reinterpret_cast<uintptr_t>(w) & 3u)) return hipErrorInvalidValue;
     const uint32_t tiles_m = static_cast<uint32_t>((M + BM - 1) / BM);
     const uint32_t tiles_n = static_cast<uint32_t>((N + BN - 1) / BN);
     const dim3 grid(tiles_m * tiles_n);
@@ -808,6 +809,14 @@ hipError_t launch_gemm_f32(int fmt, const uint8_t* w, const float* X, float* Y, 
         break;
     case kQ6_K:
         hipLaunchKernelGGL(gemm_f32_kernel<kQ6_K>, grid, dim3(kThreads), 0, stream, w, X, Y, uint32_t(M), uint32_t(N),
+                           uint32_t(K), tiles_m, tiles_n);
+        break;
+    case kQ4_K:
+        hipLaunchKernelGGL(gemm_f32_kernel<kQ4_K>, grid, dim3(kThreads), 0, stream, w, X, Y, uint32_t(M), uint32_t(N),
+                           uint32_t(K), tiles_m, tiles_n);
+        break;
+    case kQ5_K:
+        hipLaunchKernelGGL(gemm_f32_kernel<kQ5_K>, grid, dim3(kThreads), 0, stream, w, X, Y, uint32_t(M), uint32_t(N),
                            uint32_t(K), tiles_m, tiles_n);
         break;
     default: return hipErrorInvalidValue;

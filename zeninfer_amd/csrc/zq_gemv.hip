@@ -22,6 +22,13 @@
 // in flight per iteration.  The per-lane partial sums are reduced across the
 // wave with a butterfly (ds_swizzle/DPP), then one lane stores R outputs.
 //
+// Q4_K / Q5_K (144 / 176-byte super-blocks: fp16 d, fp16 dmin, 12 bytes of
+// packed 6-bit scales/mins, [Q5_K: 32 bytes of fifth bits], 128 bytes of
+// nibbles): one lane owns a 16-byte unit of nibbles, i.e. 16 elements of an
+// even group and the 16 matching elements of the next odd group.  Its 32 x
+// values and their two sums stay in VGPRs, so per row the lane needs only
+// sum(q*x) per group: w*x summed = (d*sc)*sum(q*x) - (dmin*m)*sum(x).
+//
 // Q6_K: one lane owns a 16-element unit (half h, l-quad l0) of a super-block:
 // 3 data dwords (ql low/high streams and qh), 4 int8 sub-scales and d.  The
 // four 4-element groups are decoded byte-parallel: q = lo4 | hi2 << 4, then
@@ -38,6 +45,8 @@ size_t row_bytes(int fmt, size_t cols) {
     switch (fmt) {
     case kQ4_0: return (cols && cols % 32 == 0) ? cols / 32 * 18 : 0;
     case kQ8_0: return (cols && cols % 32 == 0) ? cols / 32 * 34 : 0;
+    case kQ4_K: return (cols && cols % 256 == 0) ? cols / 256 * 144 : 0;
+    case kQ5_K: return (cols && cols % 256 == 0) ? cols / 256 * 176 : 0;
     case kQ6_K: return (cols && cols % 256 == 0) ? cols / 256 * 210 : 0;
     default: return 0;
     }
@@ -677,6 +686,211 @@ __global__ __launch_bounds__(NW * 64) void gemv_q6k_stream_kernel(TaskTable tt, 
     }
 }
 
+
+// ------------------------------------------------------------ Q4_K / Q5_K ---
+// A lane's fixed unit: super-block sb, nibble unit c (0..7) -> group pair
+// j2 = c/2 (groups 2*j2 low nibbles, 2*j2+1 high nibbles), byte offset
+// l0 = 16*(c%2) inside the 32-byte group pair.
+struct KUnit {
+    uint32_t hoff, qoff, boff, j2;
+};
+template <int FMT>
+__device__ __forceinline__ KUnit kquant_unit(uint32_t u) {
+    constexpr uint32_t BB = FMT == kQ5_K ? 176 : 144;
+    constexpr uint32_t QOFF = FMT == kQ5_K ? 48 : 16;
+    const uint32_t sb = u >> 3, c = u & 7u, j2 = c >> 1, l0 = (c & 1u) * 16u;
+    return KUnit{sb * BB, sb * BB + QOFF + j2 * 32 + l0, sb * BB + 16 + l0, j2};
+}
+// The unit's 32 x values (16 of group 2*j2, 16 of group 2*j2+1) and their sums.
+__device__ __forceinline__ void kquant_x(const float* __restrict__ x, uint32_t u, bool active, float (&xl)[16],
+                                         float (&xh)[16], float& sxl, float& sxh) {
+    const uint32_t sb = u >> 3, c = u & 7u;
+    const float* p = x + sb * 256 + (c >> 1) * 64 + (c & 1u) * 16;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float4 a = active ? reinterpret_cast<const float4*>(p)[i] : make_float4(0, 0, 0, 0);
+        const float4 b = active ? reinterpret_cast<const float4*>(p + 32)[i] : make_float4(0, 0, 0, 0);
+        xl[4 * i] = a.x; xl[4 * i + 1] = a.y; xl[4 * i + 2] = a.z; xl[4 * i + 3] = a.w;
+        xh[4 * i] = b.x; xh[4 * i + 1] = b.y; xh[4 * i + 2] = b.z; xh[4 * i + 3] = b.w;
+    }
+    sxl = 0.0f;
+    sxh = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        sxl += xl[i];
+        sxh += xh[i];
+    }
+}
+// Dot of one unit of one row.  h = the super-block's first 16 bytes (d, dmin,
+// scales), q = the unit's 16 nibble bytes, b = the 16 fifth-bit bytes (Q5_K).
+// Scale/min of group j (src/quant.cpp:133-141): j < 4 from scales[j] and
+// scales[j+4]; j >= 4 from the nibbles of scales[j+4] with the top two bits
+// of scales[j-4] / scales[j].  In the 16-byte header scales[i] is byte i+4,
+// so with jj = j & 3: a = byte jj of h.y, b = byte jj of h.z, c = byte jj of h.w.
+template <int FMT>
+__device__ __forceinline__ float kquant_dot(const uint4& h, const uint4& q, const uint4& b, const float (&xl)[16],
+                                            const float (&xh)[16], float sxl, float sxh, uint32_t j2) {
+    const bool upper = j2 >= 2;
+    const uint32_t sh0 = 16u * (j2 & 1u), sh1 = sh0 + 8u;  // 8 * (j & 3) for j = 2*j2, 2*j2+1
+    auto scale_min = [&](uint32_t sh, float& sc, float& mn) {
+        const uint32_t a = h.y >> sh, bb = h.z >> sh, c = h.w >> sh;
+        const uint32_t s = upper ? ((c & 15u) | ((a >> 2) & 0x30u)) : (a & 63u);
+        const uint32_t m = upper ? (((c >> 4) & 15u) | ((bb >> 2) & 0x30u)) : (bb & 63u);
+        sc = float(s);
+        mn = float(m);
+    };
+    float sc0, mn0, sc1, mn1;
+    scale_min(sh0, sc0, mn0);
+    scale_min(sh1, sc1, mn1);
+    const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+    const uint32_t bw[4] = {b.x, b.y, b.z, b.w};
+    float slo = 0.0f, shi = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        uint32_t lo = qw[i] & 0x0F0F0F0Fu;
+        uint32_t hi = (qw[i] >> 4) & 0x0F0F0F0Fu;
+        if constexpr (FMT == kQ5_K) {
+            lo |= ((bw[i] >> (2 * j2)) & 0x01010101u) << 4;
+            hi |= ((bw[i] >> (2 * j2 + 1)) & 0x01010101u) << 4;
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            slo = fmaf(float((lo >> (8 * k)) & 0xffu), xl[4 * i + k], slo);
+            shi = fmaf(float((hi >> (8 * k)) & 0xffu), xh[4 * i + k], shi);
+        }
+    }
+    const float d = half_bits_to_float(h.x), dm = half_bits_to_float(h.x >> 16);
+    const float mins = fmaf(dm * mn0, sxl, dm * mn1 * sxh);
+    return fmaf(d * sc0, slo, fmaf(d * sc1, shi, -mins));
+}
+
+// Streaming K-quant GEMV (16-byte aligned rows and x).  A row's units are cut
+// into S slices of 64; a team of S waves covers a row, wave s owning slice s,
+// so a lane's unit (and x) is fixed for the whole kernel.  The lanes of a
+// wave load 8 consecutive super-blocks: the nibble units with lane-contiguous
+// dwordx4 loads, the headers (and Q5_K fifth-bit units) as dwordx4 loads that
+// 8 (4) lanes share.  The next row block's loads are issued before the
+// current one is decoded; slices are summed through LDS.
+template <int FMT, int R, int S, int NW>
+__global__ __launch_bounds__(NW * 64) void gemv_kquant_stream_kernel(TaskTable tt, const float* __restrict__ x,
+                                                                     uint32_t cols, uint32_t total_blocks) {
+    constexpr uint32_t BB = FMT == kQ5_K ? 176 : 144;
+    constexpr int TEAMS = NW / S;
+    __shared__ float red[2][NW][R];
+    const uint32_t units = cols >> 5;
+    const uint32_t rb = (cols >> 8) * BB;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int team = wave / S, slice = wave % S;
+    const uint32_t u = slice * 64 + lane;
+    const bool active = u < units;
+    const KUnit ku = kquant_unit<FMT>(active ? u : 0u);
+    float xl[16], xh[16], sxl, sxh;
+    kquant_x(x, active ? u : 0u, active, xl, xh, sxl, sxh);
+
+    auto locate = [&](uint32_t blk, const uint8_t*(&rowp)[R], uint32_t& row0, int& ti) {
+        ti = find_task(tt, blk);
+        const GemvTask& t = tt.t[ti];
+        row0 = (blk - tt.group_start[ti]) * (TEAMS * R) + team * R;
+#pragma unroll
+        for (int r = 0; r < R; ++r) rowp[r] = t.w + (size_t)min(row0 + r, t.rows - 1) * rb;
+    };
+    auto load = [&](const uint8_t*(&rowp)[R], uint4 (&h)[R], uint4 (&q)[R], uint4 (&b)[R]) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            h[r] = stream_load(reinterpret_cast<const uint4*>(rowp[r] + ku.hoff));
+            q[r] = stream_load(reinterpret_cast<const uint4*>(rowp[r] + ku.qoff));
+            if constexpr (FMT == kQ5_K) b[r] = stream_load(reinterpret_cast<const uint4*>(rowp[r] + ku.boff));
+            else b[r] = make_uint4(0, 0, 0, 0);
+        }
+    };
+
+    uint32_t blk = blockIdx.x;
+    uint4 h[R], q[R], b[R];
+    const uint8_t* rowp[R];
+    uint32_t row0 = 0;
+    int ti = 0;
+    if (blk < total_blocks) {
+        locate(blk, rowp, row0, ti);
+        load(rowp, h, q, b);
+    }
+    int parity = 0;
+    while (blk < total_blocks) {
+        uint4 hc[R], qc[R], bc[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) { hc[r] = h[r]; qc[r] = q[r]; bc[r] = b[r]; }
+        const uint32_t nblk = blk + gridDim.x;
+        const uint8_t* rowpn[R];
+        uint32_t row0n = 0;
+        int tin = 0;
+        if (nblk < total_blocks) {
+            locate(nblk, rowpn, row0n, tin);
+            load(rowpn, h, q, b);
+        }
+        float acc[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            acc[r] = active ? kquant_dot<FMT>(hc[r], qc[r], bc[r], xl, xh, sxl, sxh, ku.j2) : 0.0f;
+            acc[r] = wave_sum(acc[r]);
+        }
+        const GemvTask& t = tt.t[ti];
+        if constexpr (S == 1) {
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                if (lane == r && row0 + r < t.rows) t.y[row0 + r] = acc[r];
+        } else {
+            if (lane == 0) {
+#pragma unroll
+                for (int r = 0; r < R; ++r) red[parity][wave][r] = acc[r];
+            }
+            __syncthreads();
+            if (slice == 0 && lane < R) {
+                float v = 0.0f;
+#pragma unroll
+                for (int s2 = 0; s2 < S; ++s2) v += red[parity][team * S + s2][lane];
+                if (row0 + lane < t.rows) t.y[row0 + lane] = v;
+            }
+            parity ^= 1;
+        }
+        blk = nblk;
+        row0 = row0n;
+        ti = tin;
+    }
+}
+
+// Generic K-quant GEMV: any cols % 256 == 0 with dword-aligned rows; one wave
+// per row, lanes stride over the row's units, x read from global memory.
+template <int FMT>
+__global__ __launch_bounds__(kThreads) void gemv_kquant_generic_kernel(TaskTable tt, const float* __restrict__ x,
+                                                                       uint32_t cols, uint32_t total_groups) {
+    constexpr uint32_t BB = FMT == kQ5_K ? 176 : 144;
+    const uint32_t units = cols >> 5;
+    const uint32_t rb = (cols >> 8) * BB;
+    const int lane = threadIdx.x & 63;
+    const uint32_t wave = threadIdx.x >> 6;
+    auto ld4 = [](const uint8_t* p) {
+        const uint32_t* d = reinterpret_cast<const uint32_t*>(p);
+        return make_uint4(d[0], d[1], d[2], d[3]);
+    };
+    for (uint32_t g = blockIdx.x * kWavesPerBlock + wave; g < total_groups; g += gridDim.x * kWavesPerBlock) {
+        const int ti = find_task(tt, g);
+        const GemvTask task = tt.t[ti];
+        const uint32_t row = g - tt.group_start[ti];
+        const uint8_t* rp = task.w + (size_t)row * rb;
+        float acc = 0.0f;
+        for (uint32_t u = lane; u < units; u += kWave) {
+            const KUnit ku = kquant_unit<FMT>(u);
+            float xl[16], xh[16], sxl, sxh;
+            kquant_x(x, u, true, xl, xh, sxl, sxh);
+            const uint4 h = ld4(rp + ku.hoff), q = ld4(rp + ku.qoff);
+            const uint4 b = FMT == kQ5_K ? ld4(rp + ku.boff) : make_uint4(0, 0, 0, 0);
+            acc += kquant_dot<FMT>(h, q, b, xl, xh, sxl, sxh, ku.j2);
+        }
+        acc = wave_sum(acc);
+        if (lane == 0) task.y[row] = acc;
+    }
+}
+
 // ------------------------------------------------------------- generic ---
 // Lane-per-block fallback for Q8_0 / Q4_0 rows whose block count is odd or
 // whose base is not dword-aligned.  x is read from global memory.
@@ -895,6 +1109,52 @@ hipError_t launch_q6k_stream_any(TaskTable& tt, const float* x, uint32_t cols, h
     }
 }
 
+template <int FMT, int R, int S, int NW>
+hipError_t launch_kquant_stream(TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream) {
+    constexpr uint32_t RB = (NW / S) * R;
+    uint32_t blocks = 0;
+    for (int i = 0; i < tt.count; ++i) {
+        tt.group_start[i] = blocks;
+        blocks += (tt.t[i].rows + RB - 1) / RB;
+    }
+    tt.group_start[tt.count] = blocks;
+    const uint32_t grid = std::min<uint32_t>(blocks, uint32_t(cu_count()));
+    hipLaunchKernelGGL((gemv_kquant_stream_kernel<FMT, R, S, NW>), dim3(grid), dim3(NW * 64), 0, stream, tt, x, cols,
+                       blocks);
+    return hipGetLastError();
+}
+template <int FMT, int R>
+hipError_t launch_kquant_stream_s(TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream) {
+    switch ((cols + 2047) / 2048) {  // 64-unit slices per row
+    case 1: return launch_kquant_stream<FMT, R, 1, 16>(tt, x, cols, stream);
+    case 2: return launch_kquant_stream<FMT, R, 2, 16>(tt, x, cols, stream);
+    case 3: return launch_kquant_stream<FMT, R, 3, 15>(tt, x, cols, stream);
+    case 4: return launch_kquant_stream<FMT, R, 4, 16>(tt, x, cols, stream);
+    case 5: return launch_kquant_stream<FMT, R, 5, 15>(tt, x, cols, stream);
+    case 6: return launch_kquant_stream<FMT, R, 6, 12>(tt, x, cols, stream);
+    case 7: return launch_kquant_stream<FMT, R, 7, 14>(tt, x, cols, stream);
+    case 8: return launch_kquant_stream<FMT, R, 8, 16>(tt, x, cols, stream);
+    default: return hipErrorInvalidConfiguration;
+    }
+}
+template <int FMT>
+hipError_t launch_kquant(int R, bool stream_ok, TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream) {
+    if (stream_ok) {
+        const hipError_t e = R >= 2 ? launch_kquant_stream_s<FMT, 2>(tt, x, cols, stream)
+                                    : launch_kquant_stream_s<FMT, 1>(tt, x, cols, stream);
+        if (e != hipErrorInvalidConfiguration) return e;
+    }
+    uint32_t groups = 0;
+    for (int i = 0; i < tt.count; ++i) {
+        tt.group_start[i] = groups;
+        groups += tt.t[i].rows;
+    }
+    tt.group_start[tt.count] = groups;
+    const uint32_t blocks = std::min<uint32_t>((groups + kWavesPerBlock - 1) / kWavesPerBlock, 4096u);
+    hipLaunchKernelGGL((gemv_kquant_generic_kernel<FMT>), dim3(blocks), dim3(kThreads), 0, stream, tt, x, cols, groups);
+    return hipGetLastError();
+}
+
 template <int FMT>
 hipError_t launch_blocks(TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream) {
     uint32_t groups = 0;
@@ -926,6 +1186,22 @@ hipError_t launch_gemv(int fmt, const GemvTask* tasks, int count, const float* x
     }
     const uint32_t c = static_cast<uint32_t>(cols);
     const int R = rows_per_wave(total_rows);
+    if (fmt == kQ4_K || fmt == kQ5_K) {
+        if (reinterpret_cast<uintptr_t>(x) & 15u) return hipErrorInvalidValue;
+        bool w16 = true;
+        for (int i = 0; i < count; ++i) {
+            if (reinterpret_cast<uintptr_t>(tasks[i].w) & 3u) return hipErrorInvalidValue;
+            w16 = w16 && (reinterpret_cast<uintptr_t>(tasks[i].w) & 15u) == 0;
+        }
+        static const int forced = [] {
+            const char* e = getenv("ZQ_GEMV_ROWS_PER_WAVE");
+            const int v = e ? atoi(e) : 0;
+            return (v == 1 || v == 2) ? v : 0;
+        }();
+        const int Rk = forced ? forced : (total_rows >= 4096 ? 2 : 1);
+        return fmt == kQ4_K ? launch_kquant<kQ4_K>(Rk, w16, tt, x, c, stream)
+                            : launch_kquant<kQ5_K>(Rk, w16, tt, x, c, stream);
+    }
     if (fmt == kQ6_K) {
         if (reinterpret_cast<uintptr_t>(x) & 15u) return hipErrorInvalidValue;
         bool w16 = true;

@@ -49,6 +49,9 @@ __device__ __forceinline__ uint64_t seed_sub(uint64_t s) { return s ^ 0x5B5Cull;
 //   Q8_0: q ~ U{-127..127}, d = fp16(|N(0,1)| * 0.002)
 //   Q4_0: nibble ~ U{0..15}, d = fp16(|N(0,1)| * 0.02)
 //   Q6_K: q ~ U{0..63}, sc ~ U{-32..31}, d = fp16(|N(0,1)| * 0.001)
+//   Q4_K / Q5_K: d, dmin = fp16(|N(0,1)| * 0.001) (draws 2g, 2g+1), the 12
+//     packed scale bytes, the Q5_K fifth-bit bytes and the 128 nibble bytes
+//     each a uniform byte
 template <int FMT>
 __global__ __launch_bounds__(kThreads) void synth_kernel(uint64_t seed, uint8_t* __restrict__ w, size_t nblocks) {
     const size_t g = size_t(blockIdx.x) * kThreads + threadIdx.x;
@@ -66,6 +69,15 @@ __global__ __launch_bounds__(kThreads) void synth_kernel(uint64_t seed, uint8_t*
         const uint16_t h = f32_to_f16_bits(float(fabs(normal_at(seed_scale(seed), g)) * 0.02));
         p[0] = uint8_t(h); p[1] = uint8_t(h >> 8);
         for (int j = 0; j < 16; ++j) p[2 + j] = uint8_t(splitmix64_at(seed_quant(seed), g * 16 + j) >> 56);
+    } else if constexpr (FMT == kQ4_K || FMT == kQ5_K) {
+        constexpr int BB = FMT == kQ5_K ? 176 : 144, QS = FMT == kQ5_K ? 48 : 16;
+        uint8_t* p = w + g * BB;
+        const uint16_t d = f32_to_f16_bits(float(fabs(normal_at(seed_scale(seed), 2 * g)) * 0.001));
+        const uint16_t m = f32_to_f16_bits(float(fabs(normal_at(seed_scale(seed), 2 * g + 1)) * 0.001));
+        p[0] = uint8_t(d); p[1] = uint8_t(d >> 8); p[2] = uint8_t(m); p[3] = uint8_t(m >> 8);
+        for (int i = 0; i < 12; ++i) p[4 + i] = uint8_t(splitmix64_at(seed_sub(seed), g * 12 + i) >> 56);
+        for (int i = 16; i < QS; ++i) p[i] = uint8_t(splitmix64_at(seed_quant(seed) ^ 0xB17ull, g * 32 + (i - 16)) >> 56);
+        for (int i = 0; i < 128; ++i) p[QS + i] = uint8_t(splitmix64_at(seed_quant(seed), g * 128 + i) >> 56);
     } else {
         uint8_t* p = w + g * 210;
         for (int i = 0; i < 16; ++i) {
@@ -117,12 +129,15 @@ hipError_t launch_dequantize(int fmt, const uint8_t* w, float* out, size_t rows,
     if (!w || !out || !rows || !row_bytes(fmt, cols) || (reinterpret_cast<uintptr_t>(w) & 1u) ||
         (reinterpret_cast<uintptr_t>(out) & 15u))
         return hipErrorInvalidValue;
+    if ((fmt == kQ4_K || fmt == kQ5_K) && (reinterpret_cast<uintptr_t>(w) & 3u)) return hipErrorInvalidValue;
     const size_t n = rows * (cols / 32);
     const dim3 grid(static_cast<uint32_t>((n + kThreads - 1) / kThreads));
     switch (fmt) {
     case kQ8_0: hipLaunchKernelGGL(dequantize_kernel<kQ8_0>, grid, dim3(kThreads), 0, stream, w, out, rows, cols); break;
     case kQ4_0: hipLaunchKernelGGL(dequantize_kernel<kQ4_0>, grid, dim3(kThreads), 0, stream, w, out, rows, cols); break;
     case kQ6_K: hipLaunchKernelGGL(dequantize_kernel<kQ6_K>, grid, dim3(kThreads), 0, stream, w, out, rows, cols); break;
+    case kQ4_K: hipLaunchKernelGGL(dequantize_kernel<kQ4_K>, grid, dim3(kThreads), 0, stream, w, out, rows, cols); break;
+    case kQ5_K: hipLaunchKernelGGL(dequantize_kernel<kQ5_K>, grid, dim3(kThreads), 0, stream, w, out, rows, cols); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -130,12 +145,14 @@ hipError_t launch_dequantize(int fmt, const uint8_t* w, float* out, size_t rows,
 
 hipError_t launch_synth_weights(int fmt, uint64_t seed, uint8_t* w, size_t rows, size_t cols, hipStream_t stream) {
     if (!w || !rows || !row_bytes(fmt, cols)) return hipErrorInvalidValue;
-    const size_t nblocks = rows * cols / (fmt == kQ6_K ? 256 : 32);
+    const size_t nblocks = rows * cols / (fmt == kQ4_0 || fmt == kQ8_0 ? 32 : 256);
     const dim3 grid(static_cast<uint32_t>((nblocks + kThreads - 1) / kThreads));
     switch (fmt) {
     case kQ8_0: hipLaunchKernelGGL(synth_kernel<kQ8_0>, grid, dim3(kThreads), 0, stream, seed, w, nblocks); break;
     case kQ4_0: hipLaunchKernelGGL(synth_kernel<kQ4_0>, grid, dim3(kThreads), 0, stream, seed, w, nblocks); break;
     case kQ6_K: hipLaunchKernelGGL(synth_kernel<kQ6_K>, grid, dim3(kThreads), 0, stream, seed, w, nblocks); break;
+    case kQ4_K: hipLaunchKernelGGL(synth_kernel<kQ4_K>, grid, dim3(kThreads), 0, stream, seed, w, nblocks); break;
+    case kQ5_K: hipLaunchKernelGGL(synth_kernel<kQ5_K>, grid, dim3(kThreads), 0, stream, seed, w, nblocks); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

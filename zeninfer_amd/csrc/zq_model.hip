@@ -405,7 +405,7 @@ int zq_model_load_gguf(const zq_gguf* g, uint32_t max_positions, zq_model_config
     zq_gguf_config gc;
     zq_gguf_get_config(g, &gc);
     auto fail = [&](const std::string& m, int st = ZQ_ERR_ARG) { set_err(err, err_cap, m); return st; };
-    if (std::strcmp(gc.architecture, "llama") != 0) return fail("only the llama architecture is supported");
+    if (std::strcmp(gc.architecture, "llama") != 0) return fail("only the llama architecture is supported", ZQ_DECLINED);
     auto meta_f = [&](const char* k, float fb) {
         const char* v = zq_gguf_meta_value(g, k);
         if (!v) return fb;
@@ -484,11 +484,11 @@ int zq_model_load_gguf(const zq_gguf* g, uint32_t max_positions, zq_model_config
             const int ty = int(t.ggml_type);
             if (embd ? !(ty == zq::kQ8_0 || ty == 0) : !(ty == zq::kQ8_0 || ty == zq::kQ4_0 || ty == zq::kQ6_K)) {
                 delete m;
-                return fail("unsupported tensor type " + std::to_string(ty) + " for " + n.name);
+                return fail("unsupported tensor type " + std::to_string(ty) + " for " + n.name, ZQ_DECLINED);
             }
             if (n.w == &m->out && !(ty == zq::kQ8_0 || ty == zq::kQ4_0 || ty == zq::kQ6_K)) {
                 delete m;
-                return fail("output projection must be Q8_0, Q4_0 or Q6_K");
+                return fail("output projection must be Q8_0, Q4_0 or Q6_K", ZQ_DECLINED);
             }
         }
         arena += align_up(size_t(t.byte_size) + ZQ_WEIGHT_TAIL_PAD, kAlign);

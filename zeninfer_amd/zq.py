@@ -12,9 +12,9 @@ import numpy as np
 
 from .build import LIB
 
-Q4_0, Q8_0, Q6_K = 2, 8, 14
-FORMATS = {"Q4_0": Q4_0, "Q8_0": Q8_0, "Q6_K": Q6_K}
-BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q6_K: (256, 210)}
+Q4_0, Q8_0, Q4_K, Q5_K, Q6_K = 2, 8, 12, 13, 14
+FORMATS = {"Q4_0": Q4_0, "Q8_0": Q8_0, "Q4_K": Q4_K, "Q5_K": Q5_K, "Q6_K": Q6_K}
+BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210)}
 ACT_DEFAULT, ACT_INT8, ACT_F32 = 0, 1, 2
 OK, DECLINED = 0, 1
 WEIGHT_TAIL_PAD = 64
