@@ -20,6 +20,9 @@ roofline dominant kernel: the Q8_0 GEMV at 4096x14336 (down projection, the
          queues them), so the average includes the inter-kernel gap.
 secondary int8 prefill GEMM at M=2048, gate/up shape
          14336x4096 and down shape 4096x14336, as TOPS vs the int8 MFMA peak.
+formats_config3 BASELINE config 3 (Q4_0, Q6_K) plus Q4_K / Q5_K: GEMV GB/s and
+         GEMM (M = 512) TOPS at both FFN shapes; and the Q8_0 int8 GEMM at
+         M = 32, 128, 512 (the rest of the config 2 sweep).
 model_config4 BASELINE config 4 on the device-resident decoder (zq_model.h):
          prefill tok/s for a 512-token prompt and decode tok/s for 128
          greedy tokens of a Llama-3-8B-shaped random-init Q8_0 model.
@@ -51,6 +54,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 INT8_PEAK_TOPS = 5000.0        # MI355X dense int8 MFMA (POP/s x 1000)
+FP32_PEAK_TFLOPS = 157.3       # MI355X dense fp32 MFMA
 
 HIDDEN, FFN, KV, VOCAB, LAYERS = 4096, 14336, 1024, 128256, 32
 
@@ -163,6 +167,88 @@ def cpu_baseline(seconds=10.0, layers=4):
                       f"{len(times)} passes, median of all but the first; "
                       + ("reference quant::gemv (AVX2 + ComputePool) built from its sources"
                          if r is not None else "scalar C oracle")}
+
+
+def timed_launches_on(torch, launch, n, skip):
+    """Average time per launch of n back-to-back launches (after `skip`
+    untimed ones), bracketed by HIP events on the launch stream; a spin
+    kernel keeps the stream busy while the host queues them, so host
+    launch overhead is not in the interval (inter-kernel gaps are)."""
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(int(3e7))
+    for i in range(skip):
+        launch(i)
+    ev0.record()
+    for i in range(skip, skip + n):
+        launch(i)
+    ev1.record()
+    torch.cuda.synchronize()
+    return ev0.elapsed_time(ev1) / n
+
+
+def format_sweep(torch, zq, dev):
+    """BASELINE config 3 (Q4_0, Q6_K) plus the K-quants Q4_K / Q5_K: GEMV
+    (batch 1) and GEMM (M = 512) at 4096->14336 and 14336->4096, weights
+    generated on the device with the oracle's recipes, rotated over enough
+    distinct replicas (>= 320 MB) that no launch reads from the MALL.  The
+    GEMM uses each format's default activations: int8 for Q4_0, fp32 for the
+    super-block formats (their only reference routes), reported against the
+    int8 or the fp32 MFMA peak.  Also the Q8_0 GEMM M sweep of config 2."""
+    out = {}
+    X = torch.empty(512 * FFN, device=dev)
+    zq.synth_normal_dev(31, X, 512 * FFN)
+    xv = torch.empty(FFN, device=dev)
+    zq.synth_normal_dev(32, xv, FFN)
+    for fname, fmt in (("Q4_0", zq.Q4_0), ("Q6_K", zq.Q6_K), ("Q4_K", zq.Q4_K), ("Q5_K", zq.Q5_K)):
+        res = {}
+        for shape, N, K in (("gate/up 14336x4096", FFN, HIDDEN), ("down 4096x14336", HIDDEN, FFN)):
+            rb = zq.row_bytes(fmt, K)
+            nrep = max(2, -(-320_000_000 // (N * rb)))
+            ws = []
+            for r in range(nrep):
+                t = torch.empty(zq.weight_bytes(fmt, N, K), dtype=torch.uint8, device=dev)
+                zq.synth_weights_dev(fmt, 0x5EED0003 + 17 * r, t, N, K)
+                ws.append(t)
+            y = torch.empty(N, device=dev)
+            ms = timed_launches_on(torch, lambda i: zq.gemv_dev(fmt, ws[i % nrep], xv[:K], y, N, K), 4 * nrep, nrep)
+            entry = {"gemv_us": round(ms * 1e3, 2), "gemv_GB_s": round(gemv_bytes(rb, N, K) / (ms * 1e-3) / 1e9, 1)}
+            act = zq.ACT_INT8 if fmt == zq.Q4_0 else zq.ACT_F32
+            wsb = zq.gemm_workspace_bytes(fmt, 512, N, K, act)
+            wsp = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+            Y = torch.empty(512 * N, device=dev)
+            ms = timed_launches_on(torch, lambda i: zq.gemm_dev(fmt, ws[i % nrep], X[: 512 * K], Y, 512, N, K, act,
+                                                                wsp, wsb), 2 * nrep, 2)
+            tops = 2.0 * 512 * N * K / (ms * 1e-3) / 1e12
+            entry.update({"gemm_M512_ms": round(ms, 4), "gemm_M512_TOPS": round(tops, 1),
+                          "gemm_act": "int8" if act == zq.ACT_INT8 else "f32",
+                          "gemm_frac_peak": round(tops / (INT8_PEAK_TOPS if act == zq.ACT_INT8 else FP32_PEAK_TFLOPS), 4)})
+            res[shape] = entry
+            del ws
+            torch.cuda.empty_cache()
+        out[fname] = res
+    # config 2: Q8_0 GEMM, int8 activations, M sweep
+    sweep = {}
+    for N, K in ((FFN, HIDDEN), (HIDDEN, FFN)):
+        rb = zq.row_bytes(zq.Q8_0, K)
+        ws = []
+        for r in range(6):
+            t = torch.empty(zq.weight_bytes(zq.Q8_0, N, K), dtype=torch.uint8, device=dev)
+            zq.synth_weights_dev(zq.Q8_0, 0x5EED0002 + r, t, N, K)
+            ws.append(t)
+        for M in (32, 128, 512):
+            wsb = zq.gemm_workspace_bytes(zq.Q8_0, M, N, K, zq.ACT_INT8)
+            wsp = torch.empty(wsb, dtype=torch.uint8, device=dev)
+            Y = torch.empty(M * N, device=dev)
+            ms = timed_launches_on(torch, lambda i: zq.gemm_dev(zq.Q8_0, ws[i % 6], X[: M * K], Y, M, N, K,
+                                                                zq.ACT_INT8, wsp, wsb), 12, 6)
+            ops = 2.0 * M * N * K
+            wbytes = N * rb + 4 * M * K + 4 * M * N
+            sweep[f"M={M} N={N} K={K}"] = {"ms": round(ms, 4), "TOPS": round(ops / (ms * 1e-3) / 1e12, 1),
+                                           "GB_s": round(wbytes / (ms * 1e-3) / 1e9, 1)}
+        del ws
+        torch.cuda.empty_cache()
+    out["q8_0_gemm_int8_M_sweep"] = sweep
+    return out
 
 
 def model_config4():
@@ -294,21 +380,7 @@ def main():
     print(f"[bench] step {ms_step:.3f} ms  {value:.1f} GB/s  graph_ok={graph_ok}", file=sys.stderr, flush=True)
 
     # ---- roofline leg: per-launch timing of the 4096 x 14336 down GEMV ----
-    def timed_launches(launch, n, skip):
-        """Average time per launch of n back-to-back launches (after `skip`
-        untimed ones), bracketed by HIP events on the launch stream; a spin
-        kernel keeps the stream busy while the host queues them, so host
-        launch overhead is not in the interval (inter-kernel gaps are)."""
-        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda._sleep(int(3e7))
-        for i in range(skip):
-            launch(i)
-        ev0.record()
-        for i in range(skip, skip + n):
-            launch(i)
-        ev1.record()
-        torch.cuda.synchronize()
-        return ev0.elapsed_time(ev1) / n
+    timed_launches = lambda launch, n, skip: timed_launches_on(torch, launch, n, skip)
 
     down_bytes = gemv_bytes(rbf, HIDDEN, FFN)
     down_ms = timed_launches(lambda i: zq.gemv_dev(Q8, layers[i % LAYERS]["down"], x_f, y_d, HIDDEN, FFN),
@@ -351,6 +423,10 @@ def main():
                       "TOPS_gemm": round(ops / (k_ms * 1e-3) / 1e12, 1),
                       "frac_int8_peak": round(ops / (k_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4)}
 
+    # ---- config 3 formats + config 2 M sweep ----------------------------------
+    formats = format_sweep(torch, zq, dev)
+    print(f"[bench] formats {json.dumps(formats)}", file=sys.stderr, flush=True)
+
     # ---- config 4: the device-resident decoder, prefill 512 + 128 greedy tokens
     model4 = model_config4()
 
@@ -385,6 +461,7 @@ def main():
         "per_shape_gemv": per_shape,
         "secondary": {"metric": "prefill GEMM int8 TOPS (% MFMA peak), config 2 at M=2048",
                       "prefill_gemm_int8_M2048": gemm, "int8_peak_tops": INT8_PEAK_TOPS},
+        "formats_config3": formats,
         "model_config4": model4,
         "cpu_baseline": cpu,
     }

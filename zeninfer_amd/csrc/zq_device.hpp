@@ -4,6 +4,8 @@
 #include <hip/hip_fp16.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace zq {
 
 // GGML type ids (src/gguf.cpp:370-393 of the reference: 2=Q4_0, 8=Q8_0,
@@ -142,11 +144,67 @@ __device__ __forceinline__ void dequant32(const uint8_t* row, uint32_t k0, float
     }
 }
 
-// Wave64 sum: xor-butterfly over 6 steps, every lane ends with the total.
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+// Cross-lane reductions on DPP (quad_perm, row_half_mirror, row_mirror move
+// data between lanes of a 16-lane row inside the VALU, a few cycles each)
+// plus v_readlane for the four rows; ds_bpermute (what __shfl_xor lowers
+// to) costs an LDS round trip per step.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = uint32_t(__builtin_amdgcn_update_dpp(0, int(uint32_t(b)), CTRL, 0xF, 0xF, false));
+    const uint32_t hi = uint32_t(__builtin_amdgcn_update_dpp(0, int(uint32_t(b >> 32)), CTRL, 0xF, 0xF, false));
+    return __builtin_bit_cast(double, (uint64_t(hi) << 32) | lo);
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // lane i <-> 7-i in each 8
+constexpr int kDppMirror = 0x140;     // lane i <-> 15-i in each 16
+
+// Sum over aligned groups of G lanes (G = 2, 4, 8, 16): every lane of a
+// group ends with the group's sum.  After the two quad steps every lane holds
+// its quad's sum, and the mirrors pair each lane with one of the other quad
+// (half-row) of its group.
+template <int G, typename T>
+__device__ __forceinline__ T group_sum(T v) {
+    static_assert(G == 1 || G == 2 || G == 4 || G == 8 || G == 16, "group of 1..16 lanes");
+    auto step = [](T a, auto ctrl) {
+        if constexpr (sizeof(T) == 8) return a + dpp_d<decltype(ctrl)::value>(a);
+        else return a + dpp_f<decltype(ctrl)::value>(a);
+    };
+    if constexpr (G >= 2) v = step(v, std::integral_constant<int, kDppXor1>{});
+    if constexpr (G >= 4) v = step(v, std::integral_constant<int, kDppXor2>{});
+    if constexpr (G >= 8) v = step(v, std::integral_constant<int, kDppHalfMirror>{});
+    if constexpr (G >= 16) v = step(v, std::integral_constant<int, kDppMirror>{});
     return v;
+}
+__device__ __forceinline__ float readlane_f(float v, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+__device__ __forceinline__ double readlane_d(double v, int l) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(b)), l));
+    const uint32_t hi = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(b >> 32)), l));
+    return __builtin_bit_cast(double, (uint64_t(hi) << 32) | lo);
+}
+// Wave64 sum: every lane ends with the total (rows summed in lane order).
+__device__ __forceinline__ float wave_sum(float v) {
+    v = group_sum<16>(v);
+    return ((readlane_f(v, 0) + readlane_f(v, 16)) + readlane_f(v, 32)) + readlane_f(v, 48);
+}
+__device__ __forceinline__ double wave_sum(double v) {
+    v = group_sum<16>(v);
+    return ((readlane_d(v, 0) + readlane_d(v, 16)) + readlane_d(v, 32)) + readlane_d(v, 48);
+}
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_f<kDppXor1>(v));
+    v = fmaxf(v, dpp_f<kDppXor2>(v));
+    v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
+    v = fmaxf(v, dpp_f<kDppMirror>(v));
+    return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
 }
 
 }  // namespace zq

@@ -81,6 +81,24 @@ __device__ __forceinline__ uint4 stream_load(const uint4* p) {
     }
 }
 
+// Diagnostic build only (-DZQ_GEMV_DIAG): wave 0 of each of the first 1024
+// workgroups of gemv_stream_kernel records the constant-rate clock at kernel
+// entry, once x is in registers, at the top of each of its first 14 row
+// blocks and at exit; zq_gemv_diag_read copies the table out.
+#ifdef ZQ_GEMV_DIAG
+__device__ uint64_t g_gemv_diag[1024][20];
+#define ZQ_DIAG_MARK(k)                                                       \
+    do {                                                                      \
+        const int zq_diag_k = (k);                                            \
+        if (threadIdx.x == 0 && blockIdx.x < 1024 && zq_diag_k < 20)          \
+            g_gemv_diag[blockIdx.x][zq_diag_k] = __builtin_amdgcn_s_memrealtime(); \
+    } while (0)
+#else
+#define ZQ_DIAG_MARK(k) \
+    do {                \
+    } while (0)
+#endif
+
 constexpr int kThreads = 256;
 constexpr int kWavesPerBlock = kThreads / kWave;
 constexpr int kPadStride = 68;  // floats per 64-float x chunk in LDS
@@ -348,7 +366,7 @@ __global__ __launch_bounds__(kThreads) void gemv_xreg_kernel(TaskTable tt, const
 // distinct banks).  Requires the slice-row byte ranges to be 16 B aligned:
 // cols % 256 == 0 and a 16 B aligned weight base.  The next row block's
 // loads are issued before the current block is decoded.
-template <int FMT, int R, int S, int NW>
+template <int FMT, int R, int S, int NW, int D>
 __global__ __launch_bounds__(NW * 64) void gemv_stream_kernel(TaskTable tt, const float* __restrict__ x,
                                                                uint32_t cols, uint32_t total_blocks) {
     constexpr int DW = FMT == kQ8_0 ? 17 : 9;
@@ -357,8 +375,11 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_kernel(TaskTable tt, cons
     constexpr int UMAX = 64 * DW / 4;        // 16 B units of a full 64-pair slice-row
     constexpr int NU = (UMAX + 63) / 64;     // dwordx4 loads per lane per row
     constexpr int WBUF = 64 * DW;            // dwords per slice-row buffer
-    extern __shared__ uint32_t lds[];        // [waves][R][WBUF] then (S == 1) the padded x
+    constexpr bool XLDS = S == 1 || NW > S;  // teams share the x slices: stage x once per workgroup
+    constexpr int XPT = XLDS ? (S * 1024 + NT - 1) / NT : 16;  // float4 of x per thread (cols <= S * 4096)
+    extern __shared__ uint32_t lds[];        // [waves][R][WBUF]; the padded x is staged over it first
     __shared__ float red[2][NW][R];
+    ZQ_DIAG_MARK(0);
     const uint32_t pairs = cols >> 6;
     const uint32_t W = min(64u, (((pairs + S - 1) / S) + 3u) & ~3u);
     const uint32_t rb = pairs * DW * 4;
@@ -369,8 +390,9 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_kernel(TaskTable tt, cons
     const uint32_t np = p0 < pairs ? min(W, pairs - p0) : 0u;   // pairs in this wave's slice (multiple of 4)
     const uint32_t nunits = np * DW / 4;
     const bool active = uint32_t(lane) < np;
+    const uint32_t p = p0 + lane;
     uint32_t* buf = lds + wave * (R * WBUF);
-    float* xs = reinterpret_cast<float*>(lds + NW * R * WBUF);
+    float* xs = reinterpret_cast<float*>(lds);
 
     auto locate = [&](uint32_t blk, const uint8_t*(&rowp)[R], uint32_t& row0, int& ti) {
         ti = find_task(tt, blk);
@@ -380,15 +402,15 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_kernel(TaskTable tt, cons
         for (int r = 0; r < R; ++r)
             rowp[r] = t.w + (size_t)min(row0 + r, t.rows - 1) * rb + (size_t)(np ? p0 : 0) * DW * 4;
     };
+    // Units past the slice re-read the slice's last unit (same cache line, no
+    // branch): their copies land past what the active lanes read back.
     auto load = [&](const uint8_t*(&rowp)[R], uint4 (&u)[R][NU]) {
+        const uint32_t last = nunits ? nunits - 1 : 0u;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const uint4* src = reinterpret_cast<const uint4*>(rowp[r]);
 #pragma unroll
-            for (int i = 0; i < NU; ++i) {
-                const uint32_t unit = lane + 64 * i;
-                u[r][i] = unit < nunits ? stream_load(src + unit) : make_uint4(0, 0, 0, 0);
-            }
+            for (int i = 0; i < NU; ++i) u[r][i] = stream_load(src + min(uint32_t(lane + 64 * i), last));
         }
     };
     auto stash = [&](const uint4 (&u)[R][NU]) {
@@ -401,21 +423,39 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_kernel(TaskTable tt, cons
             }
     };
 
+    // x is loaded first: loads retire in issue order, so x must not queue
+    // behind the weight blocks.
+    const uint32_t nx4 = cols >> 2;
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    float4 xr[XPT];
+#pragma unroll
+    for (int k = 0; k < XPT; ++k) {
+        if constexpr (XLDS) {
+            const uint32_t idx = threadIdx.x + uint32_t(k) * NT;
+            xr[k] = x4[min(idx, nx4 - 1)];
+        } else {
+            xr[k] = x4[(active ? p : 0u) * 16 + k];
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep the x loads ahead of the weight loads
+    // D row blocks in flight
     uint32_t blk = blockIdx.x;
-    uint4 u[R][NU];
-    const uint8_t* rowp[R];
-    uint32_t row0 = 0;
-    int ti = 0;
-    if (blk < total_blocks) {
-        locate(blk, rowp, row0, ti);
-        load(rowp, u);
+    uint4 u[D][R][NU];
+    uint32_t row0s[D];
+    int tis[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) {  // branch-free, so the x loads stay first: a slot past the end re-reads the last block
+        const uint32_t b = min(blk + uint32_t(d) * gridDim.x, total_blocks - 1);
+        const uint8_t* rowp[R];
+        locate(b, rowp, row0s[d], tis[d]);
+        load(rowp, u[d]);
     }
     float xv[64];
-    const uint32_t p = p0 + lane;
-    if constexpr (S == 1) {
-        for (uint32_t i = threadIdx.x; i < (cols >> 2); i += NT) {
-            const float4 v = reinterpret_cast<const float4*>(x)[i];
-            *reinterpret_cast<float4*>(xs + (i >> 4) * kPadStride + ((i & 15u) << 2)) = v;
+    if constexpr (XLDS) {
+#pragma unroll
+        for (int k = 0; k < XPT; ++k) {  // out-of-range threads rewrite the last float4 with the same value
+            const uint32_t i = min(threadIdx.x + uint32_t(k) * NT, nx4 - 1);
+            *reinterpret_cast<float4*>(xs + (i >> 4) * kPadStride + ((i & 15u) << 2)) = xr[k];
         }
         __syncthreads();
         const float4* xp = reinterpret_cast<const float4*>(xs + (active ? p : 0) * kPadStride);
@@ -424,71 +464,71 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_kernel(TaskTable tt, cons
             const float4 v = xp[i];
             xv[4 * i] = v.x; xv[4 * i + 1] = v.y; xv[4 * i + 2] = v.z; xv[4 * i + 3] = v.w;
         }
-    } else if constexpr (NW > S) {
-        // several teams share the slices: stage x once per workgroup
-        for (uint32_t i = threadIdx.x; i < (cols >> 2); i += NT) {
-            const float4 v = reinterpret_cast<const float4*>(x)[i];
-            *reinterpret_cast<float4*>(xs + (i >> 4) * kPadStride + ((i & 15u) << 2)) = v;
-        }
-        __syncthreads();
-        const float4* xp = reinterpret_cast<const float4*>(xs + (active ? p : 0) * kPadStride);
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const float4 v = xp[i];
-            xv[4 * i] = v.x; xv[4 * i + 1] = v.y; xv[4 * i + 2] = v.z; xv[4 * i + 3] = v.w;
-        }
+        __syncthreads();  // the x staging area is the weight buffers
     } else {
-        const float4* xp = reinterpret_cast<const float4*>(x + (size_t)(active ? p : 0) * 64);
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            const float4 v = xp[i];
-            xv[4 * i] = v.x; xv[4 * i + 1] = v.y; xv[4 * i + 2] = v.z; xv[4 * i + 3] = v.w;
+            xv[4 * i] = xr[i].x; xv[4 * i + 1] = xr[i].y; xv[4 * i + 2] = xr[i].z; xv[4 * i + 3] = xr[i].w;
         }
     }
+    ZQ_DIAG_MARK(1);
     int parity = 0;
+    [[maybe_unused]] int diag_it = 0;
+    // one row block from ring slot d (a compile-time index, so the slot's
+    // registers are never addressed dynamically)
+    auto step = [&](auto dc) {
+        constexpr int d = decltype(dc)::value;
+        {
+            {
+                ZQ_DIAG_MARK(2 + min(diag_it++, 16));
+                stash(u[d]);
+                const uint32_t row0 = row0s[d];
+                const int ti = tis[d];
+                const uint32_t nblk = blk + uint32_t(D) * gridDim.x;
+                if (nblk < total_blocks) {
+                    const uint8_t* rowp[R];
+                    locate(nblk, rowp, row0s[d], tis[d]);
+                    load(rowp, u[d]);
+                }
+                float acc[R];
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    uint32_t q[DW];
+#pragma unroll
+                    for (int j = 0; j < DW; ++j) q[j] = active ? buf[r * WBUF + DW * lane + j] : 0u;
+                    if constexpr (FMT == kQ8_0) acc[r] = q8_pair_dot(q, xv);
+                    else acc[r] = q4_pair_dot(q, xv);
+                    acc[r] = wave_sum(acc[r]);
+                }
+                const GemvTask& t = tt.t[ti];
+                if constexpr (S == 1) {
+#pragma unroll
+                    for (int r = 0; r < R; ++r)
+                        if (lane == r && row0 + r < t.rows) t.y[row0 + r] = acc[r];
+                } else {
+                    if (lane == 0) {
+#pragma unroll
+                        for (int r = 0; r < R; ++r) red[parity][wave][r] = acc[r];
+                    }
+                    __syncthreads();
+                    if (slice == 0 && lane < R) {
+                        float v = 0.0f;
+#pragma unroll
+                        for (int s2 = 0; s2 < S; ++s2) v += red[parity][team * S + s2][lane];
+                        if (row0 + lane < t.rows) t.y[row0 + lane] = v;
+                    }
+                    parity ^= 1;
+                }
+                blk += gridDim.x;
+            }
+        }
+    };
     while (blk < total_blocks) {
-        stash(u);
-        const uint32_t nblk = blk + gridDim.x;
-        const uint8_t* rowpn[R];
-        uint32_t row0n = 0;
-        int tin = 0;
-        if (nblk < total_blocks) {
-            locate(nblk, rowpn, row0n, tin);
-            load(rowpn, u);
-        }
-        float acc[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            uint32_t q[DW];
-#pragma unroll
-            for (int j = 0; j < DW; ++j) q[j] = active ? buf[r * WBUF + DW * lane + j] : 0u;
-            if constexpr (FMT == kQ8_0) acc[r] = q8_pair_dot(q, xv);
-            else acc[r] = q4_pair_dot(q, xv);
-            acc[r] = wave_sum(acc[r]);
-        }
-        const GemvTask& t = tt.t[ti];
-        if constexpr (S == 1) {
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-                if (lane == r && row0 + r < t.rows) t.y[row0 + r] = acc[r];
-        } else {
-            if (lane == 0) {
-#pragma unroll
-                for (int r = 0; r < R; ++r) red[parity][wave][r] = acc[r];
-            }
-            __syncthreads();
-            if (slice == 0 && lane < R) {
-                float v = 0.0f;
-#pragma unroll
-                for (int s2 = 0; s2 < S; ++s2) v += red[parity][team * S + s2][lane];
-                if (row0 + lane < t.rows) t.y[row0 + lane] = v;
-            }
-            parity ^= 1;
-        }
-        blk = nblk;
-        row0 = row0n;
-        ti = tin;
+        step(std::integral_constant<int, 0>{});
+        if constexpr (D > 1) if (blk < total_blocks) step(std::integral_constant<int, 1>{});
+        if constexpr (D > 2) if (blk < total_blocks) step(std::integral_constant<int, 2>{});
     }
+    ZQ_DIAG_MARK(19);
 }
 
 // ---------------------------------------------------------------- Q6_K ---
@@ -994,7 +1034,7 @@ int wg_per_cu() {
     return v;
 }
 
-template <int FMT, int R, int S, int NW>
+template <int FMT, int R, int S, int NW, int D>
 hipError_t launch_stream(TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream) {
     constexpr uint32_t RB = (NW / S) * R;
     constexpr int DW = FMT == kQ8_0 ? 17 : 9;
@@ -1004,32 +1044,28 @@ hipError_t launch_stream(TaskTable& tt, const float* x, uint32_t cols, hipStream
         blocks += (tt.t[i].rows + RB - 1) / RB;
     }
     tt.group_start[tt.count] = blocks;
-    const uint32_t grid = std::min<uint32_t>(blocks, uint32_t(cu_count() * (NW == 16 ? 1 : wg_per_cu())));
     size_t lds = size_t(NW) * R * 64 * DW * 4;
-    if (S == 1 || NW > S) lds += size_t(cols >> 6) * kPadStride * sizeof(float);
+    if (S == 1 || NW > S) lds = std::max(lds, size_t(cols >> 6) * kPadStride * sizeof(float));
     if (lds > lds_limit()) return hipErrorInvalidConfiguration;
-    hipLaunchKernelGGL((gemv_stream_kernel<FMT, R, S, NW>), dim3(grid), dim3(NW * 64), lds, stream, tt, x, cols, blocks);
+    static const int resident = [lds] {
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_stream_kernel<FMT, R, S, NW, D>, NW * 64, lds) !=
+                hipSuccess || n < 1)
+            n = 1;
+        return n;
+    }();
+    const uint32_t grid = std::min<uint32_t>(blocks, uint32_t(cu_count() * (NW == 16 ? 1 : resident)));
+    hipLaunchKernelGGL((gemv_stream_kernel<FMT, R, S, NW, D>), dim3(grid), dim3(NW * 64), lds, stream, tt, x, cols,
+                       blocks);
     return hipGetLastError();
 }
-int stream_waves() {
-    static const int v = [] {
-        const char* e = getenv("ZQ_GEMV_WAVES");
-        const int k = e ? atoi(e) : 0;
-        return (k == 4 || k == 16) ? k : 16;
-    }();
-    return v;
-}
+// One workgroup of 16 waves per CU, one row block prefetched (D = 1): the
+// steady state already streams at ~6.9 TB/s on MI355X; deeper register rings
+// (8 waves x 2-3 blocks, 16 waves x 2 blocks) measured slower.
 template <int FMT, int S>
 hipError_t launch_stream_r(int R, TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream) {
-    if (stream_waves() == 16) {
-        hipError_t e = hipErrorInvalidConfiguration;
-        if (R == 2) e = launch_stream<FMT, 2, S, 16>(tt, x, cols, stream);
-        if (e == hipErrorInvalidConfiguration) e = launch_stream<FMT, 1, S, 16>(tt, x, cols, stream);
-        if (e != hipErrorInvalidConfiguration) return e;
-    }
-    if (R == 4) return launch_stream<FMT, 4, S, 4>(tt, x, cols, stream);
-    if (R == 2) return launch_stream<FMT, 2, S, 4>(tt, x, cols, stream);
-    return launch_stream<FMT, 1, S, 4>(tt, x, cols, stream);
+    (void)R;
+    return launch_stream<FMT, 1, S, 16, 1>(tt, x, cols, stream);
 }
 template <int FMT>
 hipError_t launch_stream_any(int R, TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream) {
@@ -1249,3 +1285,9 @@ hipError_t launch_gemv(int fmt, const GemvTask* tasks, int count, const float* x
 }
 
 }  // namespace zq
+
+#ifdef ZQ_GEMV_DIAG
+extern "C" int zq_gemv_diag_read(uint64_t* out) {
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(zq::g_gemv_diag), sizeof(zq::g_gemv_diag)) == hipSuccess ? 0 : -4;
+}
+#endif

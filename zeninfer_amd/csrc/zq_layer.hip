@@ -27,7 +27,7 @@ namespace {
 constexpr int kT = 256;
 
 __device__ __forceinline__ double block_sum_d(double v, double* red) {
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    v = wave_sum(v);
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
     __syncthreads();
     if (lane == 0) red[w] = v;
@@ -38,7 +38,7 @@ __device__ __forceinline__ double block_sum_d(double v, double* red) {
 }
 
 __device__ __forceinline__ float block_max_f(float v, float* red) {
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    v = wave_max(v);
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
     __syncthreads();
     if (lane == 0) red[w] = v;
@@ -306,8 +306,7 @@ __global__ __launch_bounds__(kT) void attention_decode_kernel(
         float d = 0.0f;
 #pragma unroll
         for (int i = 0; i < DPL; ++i) d = fmaf(qs[g][sj * DPL + i], kv[i], d);
-#pragma unroll
-        for (int o = LPP / 2; o > 0; o >>= 1) d += __shfl_xor(d, o);
+        d = group_sum<LPP>(d);
         if (sj == 0 && sp < n) sc[g][sp] = d * scale;
     }
     __syncthreads();
