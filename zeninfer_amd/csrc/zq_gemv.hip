@@ -99,6 +99,17 @@ __device__ uint64_t g_gemv_diag[1024][20];
     } while (0)
 #endif
 
+// 16 B load through a raw buffer resource covering `bytes` from a
+// wave-uniform base: lanes past the end read 0 and generate no memory
+// request (the non-temporal bit is aux bit 1 on gfx950).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t span_rsrc(const uint8_t* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base), 0, int(bytes), 0x00020000);
+}
+__device__ __forceinline__ uint4 span_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, ZQ_GEMV_STREAM_NT != 0 ? 2 : 0);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 constexpr int kThreads = 256;
 constexpr int kWavesPerBlock = kThreads / kWave;
 constexpr int kPadStride = 68;  // floats per 64-float x chunk in LDS
@@ -384,7 +395,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_kernel(TaskTable tt, cons
     const uint32_t W = min(64u, (((pairs + S - 1) / S) + 3u) & ~3u);
     const uint32_t rb = pairs * DW * 4;
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int team = wave / S, slice = wave % S;
     const uint32_t p0 = slice * W;
     const uint32_t np = p0 < pairs ? min(W, pairs - p0) : 0u;   // pairs in this wave's slice (multiple of 4)
@@ -402,15 +413,13 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_kernel(TaskTable tt, cons
         for (int r = 0; r < R; ++r)
             rowp[r] = t.w + (size_t)min(row0 + r, t.rows - 1) * rb + (size_t)(np ? p0 : 0) * DW * 4;
     };
-    // Units past the slice re-read the slice's last unit (same cache line, no
-    // branch): their copies land past what the active lanes read back.
+    // units past the slice read 0 without a memory request
     auto load = [&](const uint8_t*(&rowp)[R], uint4 (&u)[R][NU]) {
-        const uint32_t last = nunits ? nunits - 1 : 0u;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const uint4* src = reinterpret_cast<const uint4*>(rowp[r]);
+            const __amdgpu_buffer_rsrc_t rs = span_rsrc(rowp[r], nunits * 16);
 #pragma unroll
-            for (int i = 0; i < NU; ++i) u[r][i] = stream_load(src + min(uint32_t(lane + 64 * i), last));
+            for (int i = 0; i < NU; ++i) u[r][i] = span_load16(rs, uint32_t(lane + 64 * i) * 16);
         }
     };
     auto stash = [&](const uint4 (&u)[R][NU]) {
@@ -607,34 +616,22 @@ __global__ __launch_bounds__(kThreads) void gemv_q6k_kernel(TaskTable tt, const 
 // per-wave LDS buffer; lane L then decodes units L and L+64 of the chunk
 // (super-block u/16, half (u/8)%2, l-quad 4*(u%8)) from LDS.  Fields of odd
 // super-blocks sit at 2 mod 4 and are assembled with v_alignbyte.
-template <int S, int NW>
+template <int R, int S, int NW>
 __global__ __launch_bounds__(NW * 64) void gemv_q6k_stream_kernel(TaskTable tt, const float* __restrict__ x,
                                                                  uint32_t cols, uint32_t total_blocks) {
     constexpr int TEAMS = NW / S;
     constexpr uint32_t CHUNK = 8 * 210;                  // bytes
     constexpr uint32_t CUNITS = CHUNK / 16;              // 105 dwordx4 units
-    constexpr uint32_t BUFW = CHUNK / 4 + 4;             // dwords per wave buffer (+pad for alignbyte reads)
-    extern __shared__ uint32_t lds[];
-    __shared__ float red[2][NW];
+    constexpr uint32_t BUFW = CHUNK / 4 + 4;             // dwords per row buffer (+pad for alignbyte reads)
+    extern __shared__ uint32_t lds[];                    // [waves][R][BUFW]
+    __shared__ float red[2][NW][R];
     const uint32_t rb = (cols >> 8) * 210;
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int team = wave / S, slice = wave % S;
-    uint32_t* buf = lds + wave * BUFW;
-    const uint8_t* bbytes = reinterpret_cast<const uint8_t*>(buf);
+    uint32_t* wbuf = lds + wave * (R * BUFW);
 
-    auto locate = [&](uint32_t blk, const uint8_t*& rowp, uint32_t& row, int& ti) {
-        ti = find_task(tt, blk);
-        const GemvTask& t = tt.t[ti];
-        row = (blk - tt.group_start[ti]) * TEAMS + team;
-        rowp = t.w + (size_t)min(row, t.rows - 1) * rb + (size_t)slice * CHUNK;
-    };
-    auto load = [&](const uint8_t* rowp, uint4 (&u)[2]) {
-        const uint4* src = reinterpret_cast<const uint4*>(rowp);
-        u[0] = stream_load(src + lane);
-        u[1] = lane + 64 < int(CUNITS) ? stream_load(src + lane + 64) : make_uint4(0, 0, 0, 0);
-    };
-    // x for this lane's two units, kept in registers
+    // x for this lane's two units, kept in registers; loaded before any weights
     float xv[2][4][4];
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
@@ -646,86 +643,113 @@ __global__ __launch_bounds__(NW * 64) void gemv_q6k_stream_kernel(TaskTable tt, 
             xv[k][g][0] = v.x; xv[k][g][1] = v.y; xv[k][g][2] = v.z; xv[k][g][3] = v.w;
         }
     }
-    auto lds_u32 = [&](uint32_t off) -> uint32_t {  // 32 bits at a 2-byte aligned chunk offset
-        const uint32_t a = off & ~3u;
-        const uint32_t lo = buf[a >> 2];
-        if ((off & 3u) == 0) return lo;
-        return __builtin_amdgcn_alignbyte(buf[(a >> 2) + 1], lo, 2);
+    __builtin_amdgcn_sched_barrier(0);
+    auto locate = [&](uint32_t blk, const uint8_t*(&rowp)[R], uint32_t& row0, int& ti) {
+        ti = find_task(tt, blk);
+        const GemvTask& t = tt.t[ti];
+        row0 = (blk - tt.group_start[ti]) * (TEAMS * R) + team * R;
+#pragma unroll
+        for (int r = 0; r < R; ++r) rowp[r] = t.w + (size_t)min(row0 + r, t.rows - 1) * rb + (size_t)slice * CHUNK;
+    };
+    // the second unit of lanes past the chunk reads 0 without a memory request
+    auto load = [&](const uint8_t*(&rowp)[R], uint4 (&u)[R][2]) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const __amdgpu_buffer_rsrc_t rs = span_rsrc(rowp[r], CUNITS * 16);
+            u[r][0] = span_load16(rs, uint32_t(lane) * 16);
+            u[r][1] = span_load16(rs, uint32_t(lane + 64) * 16);
+        }
     };
 
     uint32_t blk = blockIdx.x;
-    uint4 u[2];
-    const uint8_t* rowp = nullptr;
-    uint32_t row = 0;
+    uint4 u[R][2];
+    uint32_t row0 = 0;
     int ti = 0;
-    if (blk < total_blocks) {
-        locate(blk, rowp, row, ti);
+    {
+        const uint8_t* rowp[R];
+        locate(min(blk, total_blocks - 1), rowp, row0, ti);
         load(rowp, u);
     }
     int parity = 0;
     while (blk < total_blocks) {
-        reinterpret_cast<uint4*>(buf)[lane] = u[0];
-        if (lane + 64 < int(CUNITS)) reinterpret_cast<uint4*>(buf)[lane + 64] = u[1];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            reinterpret_cast<uint4*>(wbuf + r * BUFW)[lane] = u[r][0];
+            if (lane + 64 < int(CUNITS)) reinterpret_cast<uint4*>(wbuf + r * BUFW)[lane + 64] = u[r][1];
+        }
         const uint32_t nblk = blk + gridDim.x;
-        const uint8_t* rowpn = nullptr;
-        uint32_t rown = 0;
-        int tin = 0;
+        const uint32_t row0c = row0;
+        const int tic = ti;
         if (nblk < total_blocks) {
-            locate(nblk, rowpn, rown, tin);
-            load(rowpn, u);
+            const uint8_t* rowp[R];
+            locate(nblk, rowp, row0, ti);
+            load(rowp, u);
         }
-        float acc = 0.0f;
+        float acc[R];
 #pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            const uint32_t uu = lane + 64 * k;
-            const uint32_t sbl = uu >> 4, h = (uu >> 3) & 1u, l0 = (uu & 7u) * 4u;
-            const uint32_t base = sbl * 210;
-            const uint32_t qlA = lds_u32(base + h * 64 + l0);
-            const uint32_t qlB = lds_u32(base + h * 64 + 32 + l0);
-            const uint32_t qh = lds_u32(base + 128 + h * 32 + l0);
-            const uint32_t sc0 = lds_u32(base + 192 + h * 8);
-            const uint32_t sc1 = lds_u32(base + 196 + h * 8);
-            const uint32_t dbits = uint32_t(bbytes[base + 208]) | (uint32_t(bbytes[base + 209]) << 8);
-            const float d = half_bits_to_float(dbits) * 0.25f;
-            const uint32_t shsel = l0 >> 4;
-            float part = 0.0f;
+        for (int r = 0; r < R; ++r) {
+            const uint32_t* buf = wbuf + r * BUFW;
+            const uint8_t* bbytes = reinterpret_cast<const uint8_t*>(buf);
+            auto lds_u32 = [&](uint32_t off) -> uint32_t {  // 32 bits at a 2-byte aligned chunk offset
+                const uint32_t a = off & ~3u;
+                const uint32_t lo = buf[a >> 2];
+                if ((off & 3u) == 0) return lo;
+                return __builtin_amdgcn_alignbyte(buf[(a >> 2) + 1], lo, 2);
+            };
+            float a = 0.0f;
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                uint32_t lo = (g & 1) ? qlB : qlA;
-                if (g >= 2) lo >>= 4;
-                lo &= 0x0F0F0F0Fu;
-                const uint32_t hi = ((qh >> (2 * g)) & 0x03030303u) << 4;
-                const uint32_t v = ((lo | hi) ^ 0x20202020u) << 2;  // 4*(q-32) per byte
-                float sum = 0.0f;
+            for (int k = 0; k < 2; ++k) {
+                const uint32_t uu = lane + 64 * k;
+                const uint32_t sbl = uu >> 4, h = (uu >> 3) & 1u, l0 = (uu & 7u) * 4u;
+                const uint32_t base = sbl * 210;
+                const uint32_t qlA = lds_u32(base + h * 64 + l0);
+                const uint32_t qlB = lds_u32(base + h * 64 + 32 + l0);
+                const uint32_t qh = lds_u32(base + 128 + h * 32 + l0);
+                const uint32_t sc0 = lds_u32(base + 192 + h * 8);
+                const uint32_t sc1 = lds_u32(base + 196 + h * 8);
+                const uint32_t dbits = uint32_t(bbytes[base + 208]) | (uint32_t(bbytes[base + 209]) << 8);
+                const float d = half_bits_to_float(dbits) * 0.25f;
+                const uint32_t shsel = l0 >> 4;
+                float part = 0.0f;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) sum = fmaf(sbyte(v, e), xv[k][g][e], sum);
-                const float sc = sbyte(g < 2 ? sc0 : sc1, (2 * g + shsel) & 3);
-                part = fmaf(d * sc, sum, part);
+                for (int g = 0; g < 4; ++g) {
+                    uint32_t lo = (g & 1) ? qlB : qlA;
+                    if (g >= 2) lo >>= 4;
+                    lo &= 0x0F0F0F0Fu;
+                    const uint32_t hi = ((qh >> (2 * g)) & 0x03030303u) << 4;
+                    const uint32_t v = ((lo | hi) ^ 0x20202020u) << 2;  // 4*(q-32) per byte
+                    float sum = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) sum = fmaf(sbyte(v, e), xv[k][g][e], sum);
+                    const float sc = sbyte(g < 2 ? sc0 : sc1, (2 * g + shsel) & 3);
+                    part = fmaf(d * sc, sum, part);
+                }
+                a += part;
             }
-            acc += part;
+            acc[r] = wave_sum(a);
         }
-        acc = wave_sum(acc);
-        const GemvTask& t = tt.t[ti];
+        const GemvTask& t = tt.t[tic];
         if constexpr (S == 1) {
-            if (lane == 0 && row < t.rows) t.y[row] = acc;
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                if (lane == r && row0c + r < t.rows) t.y[row0c + r] = acc[r];
         } else {
-            if (lane == 0) red[parity][wave] = acc;
+            if (lane == 0) {
+#pragma unroll
+                for (int r = 0; r < R; ++r) red[parity][wave][r] = acc[r];
+            }
             __syncthreads();
-            if (slice == 0 && lane == 0) {
+            if (slice == 0 && lane < R) {
                 float v = 0.0f;
 #pragma unroll
-                for (int s2 = 0; s2 < S; ++s2) v += red[parity][team * S + s2];
-                if (row < t.rows) t.y[row] = v;
+                for (int s2 = 0; s2 < S; ++s2) v += red[parity][team * S + s2][lane];
+                if (row0c + lane < t.rows) t.y[row0c + lane] = v;
             }
             parity ^= 1;
         }
         blk = nblk;
-        rowp = rowpn;
-        row = rown;
-        ti = tin;
     }
 }
-
 
 // ------------------------------------------------------------ Q4_K / Q5_K ---
 // A lane's fixed unit: super-block sb, nibble unit c (0..7) -> group pair
@@ -770,14 +794,16 @@ __device__ __forceinline__ void kquant_x(const float* __restrict__ x, uint32_t u
 template <int FMT>
 __device__ __forceinline__ float kquant_dot(const uint4& h, const uint4& q, const uint4& b, const float (&xl)[16],
                                             const float (&xh)[16], float sxl, float sxh, uint32_t j2) {
-    const bool upper = j2 >= 2;
-    const uint32_t sh0 = 16u * (j2 & 1u), sh1 = sh0 + 8u;  // 8 * (j & 3) for j = 2*j2, 2*j2+1
+    // lane constants: groups 2*j2 and 2*j2+1 sit at byte (j & 3) of the
+    // scale words; the upper four groups take the split encoding
+    const uint32_t upper = j2 >= 2 ? ~0u : 0u;
+    const uint32_t sh0 = 16u * (j2 & 1u), sh1 = sh0 + 8u;
     auto scale_min = [&](uint32_t sh, float& sc, float& mn) {
         const uint32_t a = h.y >> sh, bb = h.z >> sh, c = h.w >> sh;
-        const uint32_t s = upper ? ((c & 15u) | ((a >> 2) & 0x30u)) : (a & 63u);
-        const uint32_t m = upper ? (((c >> 4) & 15u) | ((bb >> 2) & 0x30u)) : (bb & 63u);
-        sc = float(s);
-        mn = float(m);
+        const uint32_t s_lo = a & 63u, m_lo = bb & 63u;
+        const uint32_t s_hi = (c & 15u) | ((a >> 2) & 0x30u), m_hi = ((c >> 4) & 15u) | ((bb >> 2) & 0x30u);
+        sc = float((s_lo & ~upper) | (s_hi & upper));
+        mn = float((m_lo & ~upper) | (m_hi & upper));
     };
     float sc0, mn0, sc1, mn1;
     scale_min(sh0, sc0, mn0);
@@ -793,6 +819,8 @@ __device__ __forceinline__ float kquant_dot(const uint4& h, const uint4& q, cons
             lo |= ((bw[i] >> (2 * j2)) & 0x01010101u) << 4;
             hi |= ((bw[i] >> (2 * j2 + 1)) & 0x01010101u) << 4;
         }
+        // opaque to the combiner, so each byte converts with one v_cvt_f32_ubyteN
+        asm volatile("" : "+v"(lo), "+v"(hi));
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             slo = fmaf(float((lo >> (8 * k)) & 0xffu), xl[4 * i + k], slo);
@@ -804,80 +832,129 @@ __device__ __forceinline__ float kquant_dot(const uint4& h, const uint4& q, cons
     return fmaf(d * sc0, slo, fmaf(d * sc1, shi, -mins));
 }
 
-// Streaming K-quant GEMV (16-byte aligned rows and x).  A row's units are cut
-// into S slices of 64; a team of S waves covers a row, wave s owning slice s,
-// so a lane's unit (and x) is fixed for the whole kernel.  The lanes of a
-// wave load 8 consecutive super-blocks: the nibble units with lane-contiguous
-// dwordx4 loads, the headers (and Q5_K fifth-bit units) as dwordx4 loads that
-// 8 (4) lanes share.  The next row block's loads are issued before the
-// current one is decoded; slices are summed through LDS.
+// Streaming K-quant GEMV (16-byte aligned rows and x).  A row is cut into
+// slices of 8 super-blocks (64 nibble units); a team of S waves covers a row,
+// wave s owning slice s, so a lane's unit (and its x) is fixed for the whole
+// kernel.  Each slice-row (1152 / 1408 B) is fetched with lane-contiguous
+// dwordx4 loads (every byte once, two loads per lane), stashed in a per-wave
+// LDS buffer, and each lane reads its header, nibble unit and fifth-bit unit
+// back with ds_read_b128.  R rows per team per block; the next block's loads
+// are issued before the current one is decoded; slices are summed in LDS.
 template <int FMT, int R, int S, int NW>
 __global__ __launch_bounds__(NW * 64) void gemv_kquant_stream_kernel(TaskTable tt, const float* __restrict__ x,
                                                                      uint32_t cols, uint32_t total_blocks) {
     constexpr uint32_t BB = FMT == kQ5_K ? 176 : 144;
+    constexpr uint32_t QOFF = FMT == kQ5_K ? 48 : 16;
+    constexpr uint32_t CUNITS = 8 * BB / 16;  // 16 B units of a full slice-row (72 / 88)
     constexpr int TEAMS = NW / S;
+    extern __shared__ uint4 klds[];           // [waves][R][CUNITS]
     __shared__ float red[2][NW][R];
-    const uint32_t units = cols >> 5;
-    const uint32_t rb = (cols >> 8) * BB;
+    ZQ_DIAG_MARK(0);
+    const uint32_t nsb = cols >> 8;
+    const uint32_t rb = nsb * BB;
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int team = wave / S, slice = wave % S;
+    const uint32_t sb0 = slice * 8;
+    const uint32_t nsb_s = sb0 < nsb ? min(8u, nsb - sb0) : 0u;  // super-blocks in this slice
+    const uint32_t nunits = nsb_s * (BB / 16);
     const uint32_t u = slice * 64 + lane;
-    const bool active = u < units;
-    const KUnit ku = kquant_unit<FMT>(active ? u : 0u);
-    float xl[16], xh[16], sxl, sxh;
-    kquant_x(x, active ? u : 0u, active, xl, xh, sxl, sxh);
+    const bool active = uint32_t(lane >> 3) < nsb_s;
+    uint4* buf = klds + wave * (R * CUNITS);
 
+    // x first (loads retire in issue order)
+    float xl[16], xh[16], sxl, sxh;
+    {
+        const uint32_t uu = active ? u : 0u;
+        const uint32_t sb = uu >> 3, c = uu & 7u;
+        const float4* p = reinterpret_cast<const float4*>(x + sb * 256 + (c >> 1) * 64 + (c & 1u) * 16);
+        float4 a[4], b[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            a[i] = p[i];
+            b[i] = p[8 + i];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            xl[4 * i] = a[i].x; xl[4 * i + 1] = a[i].y; xl[4 * i + 2] = a[i].z; xl[4 * i + 3] = a[i].w;
+            xh[4 * i] = b[i].x; xh[4 * i + 1] = b[i].y; xh[4 * i + 2] = b[i].z; xh[4 * i + 3] = b[i].w;
+        }
+    }
     auto locate = [&](uint32_t blk, const uint8_t*(&rowp)[R], uint32_t& row0, int& ti) {
         ti = find_task(tt, blk);
         const GemvTask& t = tt.t[ti];
         row0 = (blk - tt.group_start[ti]) * (TEAMS * R) + team * R;
 #pragma unroll
-        for (int r = 0; r < R; ++r) rowp[r] = t.w + (size_t)min(row0 + r, t.rows - 1) * rb;
+        for (int r = 0; r < R; ++r) rowp[r] = t.w + (size_t)min(row0 + r, t.rows - 1) * rb + (size_t)sb0 * BB * (nsb_s != 0);
     };
-    auto load = [&](const uint8_t*(&rowp)[R], uint4 (&h)[R], uint4 (&q)[R], uint4 (&b)[R]) {
+    // units past the slice read 0 without a memory request
+    auto load = [&](const uint8_t*(&rowp)[R], uint4 (&v)[R][2]) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            h[r] = stream_load(reinterpret_cast<const uint4*>(rowp[r] + ku.hoff));
-            q[r] = stream_load(reinterpret_cast<const uint4*>(rowp[r] + ku.qoff));
-            if constexpr (FMT == kQ5_K) b[r] = stream_load(reinterpret_cast<const uint4*>(rowp[r] + ku.boff));
-            else b[r] = make_uint4(0, 0, 0, 0);
+            const __amdgpu_buffer_rsrc_t rs = span_rsrc(rowp[r], nunits * 16);
+            v[r][0] = span_load16(rs, uint32_t(lane) * 16);
+            v[r][1] = span_load16(rs, uint32_t(lane + 64) * 16);
         }
     };
-
+    auto stash = [&](const uint4 (&v)[R][2]) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            buf[r * CUNITS + lane] = v[r][0];
+            if (lane + 64 < int(CUNITS)) buf[r * CUNITS + lane + 64] = v[r][1];
+        }
+    };
     uint32_t blk = blockIdx.x;
-    uint4 h[R], q[R], b[R];
-    const uint8_t* rowp[R];
+    uint4 v[R][2];
     uint32_t row0 = 0;
     int ti = 0;
-    if (blk < total_blocks) {
-        locate(blk, rowp, row0, ti);
-        load(rowp, h, q, b);
+    {
+        const uint8_t* rowp[R];
+        locate(min(blk, total_blocks - 1), rowp, row0, ti);
+        load(rowp, v);
     }
+    sxl = 0.0f;
+    sxh = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        sxl += xl[i];
+        sxh += xh[i];
+    }
+    const uint32_t sbl = uint32_t(lane >> 3), c = uint32_t(lane & 7), j2 = c >> 1, l0 = (c & 1u) * 16;
+    const uint32_t hidx = sbl * (BB / 16), qidx = (sbl * BB + QOFF + j2 * 32 + l0) / 16,
+                   bidx = (sbl * BB + 16 + l0) / 16;
+    ZQ_DIAG_MARK(1);
+    [[maybe_unused]] int diag_it = 0;
     int parity = 0;
     while (blk < total_blocks) {
-        uint4 hc[R], qc[R], bc[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r) { hc[r] = h[r]; qc[r] = q[r]; bc[r] = b[r]; }
+        ZQ_DIAG_MARK(2 + min(diag_it++, 16));
+        stash(v);
         const uint32_t nblk = blk + gridDim.x;
-        const uint8_t* rowpn[R];
-        uint32_t row0n = 0;
-        int tin = 0;
+        const uint32_t row0c = row0;
+        const int tic = ti;
         if (nblk < total_blocks) {
-            locate(nblk, rowpn, row0n, tin);
-            load(rowpn, h, q, b);
+            const uint8_t* rowp[R];
+            locate(nblk, rowp, row0, ti);
+            load(rowp, v);
         }
         float acc[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            acc[r] = active ? kquant_dot<FMT>(hc[r], qc[r], bc[r], xl, xh, sxl, sxh, ku.j2) : 0.0f;
+            const uint4* rb4 = buf + r * CUNITS;
+            const uint4 h = rb4[hidx], q = rb4[qidx];
+            const uint4 bq = FMT == kQ5_K ? rb4[bidx] : make_uint4(0, 0, 0, 0);
+#ifdef ZQ_GEMV_DIAG_NOCOMPUTE
+            acc[r] = active ? __uint_as_float((h.x ^ q.y ^ bq.z) & 0x3fffffffu) * xl[0] : 0.0f;
+#else
+            acc[r] = active ? kquant_dot<FMT>(h, q, bq, xl, xh, sxl, sxh, j2) : 0.0f;
+#endif
             acc[r] = wave_sum(acc[r]);
         }
-        const GemvTask& t = tt.t[ti];
+        const GemvTask& t = tt.t[tic];
         if constexpr (S == 1) {
 #pragma unroll
             for (int r = 0; r < R; ++r)
-                if (lane == r && row0 + r < t.rows) t.y[row0 + r] = acc[r];
+                if (lane == r && row0c + r < t.rows) t.y[row0c + r] = acc[r];
         } else {
             if (lane == 0) {
 #pragma unroll
@@ -885,17 +962,16 @@ __global__ __launch_bounds__(NW * 64) void gemv_kquant_stream_kernel(TaskTable t
             }
             __syncthreads();
             if (slice == 0 && lane < R) {
-                float v = 0.0f;
+                float sum = 0.0f;
 #pragma unroll
-                for (int s2 = 0; s2 < S; ++s2) v += red[parity][team * S + s2][lane];
-                if (row0 + lane < t.rows) t.y[row0 + lane] = v;
+                for (int s2 = 0; s2 < S; ++s2) sum += red[parity][team * S + s2][lane];
+                if (row0c + lane < t.rows) t.y[row0c + lane] = sum;
             }
             parity ^= 1;
         }
         blk = nblk;
-        row0 = row0n;
-        ti = tin;
     }
+    ZQ_DIAG_MARK(19);
 }
 
 // Generic K-quant GEMV: any cols % 256 == 0 with dword-aligned rows; one wave
@@ -1116,38 +1192,43 @@ hipError_t launch_q6k(TaskTable& tt, const float* x, uint32_t cols, hipStream_t 
                        x, cols, groups);
     return hipGetLastError();
 }
-template <int S, int NW>
+template <int R, int S, int NW>
 hipError_t launch_q6k_stream(TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream) {
     constexpr uint32_t TEAMS = NW / S;
     uint32_t blocks = 0;
     for (int i = 0; i < tt.count; ++i) {
         tt.group_start[i] = blocks;
-        blocks += (tt.t[i].rows + TEAMS - 1) / TEAMS;
+        blocks += (tt.t[i].rows + TEAMS * R - 1) / (TEAMS * R);
     }
     tt.group_start[tt.count] = blocks;
     const uint32_t grid = std::min<uint32_t>(blocks, uint32_t(cu_count()));
-    const size_t lds = size_t(NW) * (8 * 210 / 4 + 4) * 4;
-    hipLaunchKernelGGL((gemv_q6k_stream_kernel<S, NW>), dim3(grid), dim3(NW * 64), lds, stream, tt, x, cols, blocks);
+    const size_t lds = size_t(NW) * R * (8 * 210 / 4 + 4) * 4;
+    hipLaunchKernelGGL((gemv_q6k_stream_kernel<R, S, NW>), dim3(grid), dim3(NW * 64), lds, stream, tt, x, cols, blocks);
     return hipGetLastError();
 }
-// chunks per row -> (S, waves per workgroup); nullopt-like false when unsupported
-hipError_t launch_q6k_stream_any(TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream) {
+// chunks per row -> (S, waves per workgroup)
+template <int R>
+hipError_t launch_q6k_stream_s(TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream) {
     switch ((cols >> 8) / 8) {
-    case 1: return launch_q6k_stream<1, 16>(tt, x, cols, stream);
-    case 2: return launch_q6k_stream<2, 16>(tt, x, cols, stream);
-    case 3: return launch_q6k_stream<3, 15>(tt, x, cols, stream);
-    case 4: return launch_q6k_stream<4, 16>(tt, x, cols, stream);
-    case 5: return launch_q6k_stream<5, 15>(tt, x, cols, stream);
-    case 6: return launch_q6k_stream<6, 12>(tt, x, cols, stream);
-    case 7: return launch_q6k_stream<7, 14>(tt, x, cols, stream);
-    case 8: return launch_q6k_stream<8, 16>(tt, x, cols, stream);
+    case 1: return launch_q6k_stream<R, 1, 16>(tt, x, cols, stream);
+    case 2: return launch_q6k_stream<R, 2, 16>(tt, x, cols, stream);
+    case 3: return launch_q6k_stream<R, 3, 15>(tt, x, cols, stream);
+    case 4: return launch_q6k_stream<R, 4, 16>(tt, x, cols, stream);
+    case 5: return launch_q6k_stream<R, 5, 15>(tt, x, cols, stream);
+    case 6: return launch_q6k_stream<R, 6, 12>(tt, x, cols, stream);
+    case 7: return launch_q6k_stream<R, 7, 14>(tt, x, cols, stream);
+    case 8: return launch_q6k_stream<R, 8, 16>(tt, x, cols, stream);
     default: return hipErrorInvalidConfiguration;
     }
+}
+hipError_t launch_q6k_stream_any(TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream, uint32_t total_rows) {
+    return total_rows >= 4096 ? launch_q6k_stream_s<4>(tt, x, cols, stream) : launch_q6k_stream_s<1>(tt, x, cols, stream);
 }
 
 template <int FMT, int R, int S, int NW>
 hipError_t launch_kquant_stream(TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream) {
     constexpr uint32_t RB = (NW / S) * R;
+    constexpr uint32_t CUNITS = 8 * (FMT == kQ5_K ? 176 : 144) / 16;
     uint32_t blocks = 0;
     for (int i = 0; i < tt.count; ++i) {
         tt.group_start[i] = blocks;
@@ -1155,7 +1236,8 @@ hipError_t launch_kquant_stream(TaskTable& tt, const float* x, uint32_t cols, hi
     }
     tt.group_start[tt.count] = blocks;
     const uint32_t grid = std::min<uint32_t>(blocks, uint32_t(cu_count()));
-    hipLaunchKernelGGL((gemv_kquant_stream_kernel<FMT, R, S, NW>), dim3(grid), dim3(NW * 64), 0, stream, tt, x, cols,
+    const size_t lds = size_t(NW) * R * CUNITS * 16;
+    hipLaunchKernelGGL((gemv_kquant_stream_kernel<FMT, R, S, NW>), dim3(grid), dim3(NW * 64), lds, stream, tt, x, cols,
                        blocks);
     return hipGetLastError();
 }
@@ -1176,7 +1258,7 @@ hipError_t launch_kquant_stream_s(TaskTable& tt, const float* x, uint32_t cols, 
 template <int FMT>
 hipError_t launch_kquant(int R, bool stream_ok, TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream) {
     if (stream_ok) {
-        const hipError_t e = R >= 2 ? launch_kquant_stream_s<FMT, 2>(tt, x, cols, stream)
+        const hipError_t e = R >= 4 ? launch_kquant_stream_s<FMT, 4>(tt, x, cols, stream)
                                     : launch_kquant_stream_s<FMT, 1>(tt, x, cols, stream);
         if (e != hipErrorInvalidConfiguration) return e;
     }
@@ -1232,9 +1314,9 @@ hipError_t launch_gemv(int fmt, const GemvTask* tasks, int count, const float* x
         static const int forced = [] {
             const char* e = getenv("ZQ_GEMV_ROWS_PER_WAVE");
             const int v = e ? atoi(e) : 0;
-            return (v == 1 || v == 2) ? v : 0;
+            return (v == 1 || v == 4) ? v : 0;
         }();
-        const int Rk = forced ? forced : (total_rows >= 4096 ? 2 : 1);
+        const int Rk = forced ? forced : (total_rows >= 4096 ? 4 : 1);
         return fmt == kQ4_K ? launch_kquant<kQ4_K>(Rk, w16, tt, x, c, stream)
                             : launch_kquant<kQ5_K>(Rk, w16, tt, x, c, stream);
     }
@@ -1247,7 +1329,7 @@ hipError_t launch_gemv(int fmt, const GemvTask* tasks, int count, const float* x
             return e && e[0] == 'l';
         }();
         if (!q6_legacy && w16 && c % 2048 == 0 && c / 2048 <= 8) {
-            const hipError_t e = launch_q6k_stream_any(tt, x, c, stream);
+            const hipError_t e = launch_q6k_stream_any(tt, x, c, stream, total_rows);
             if (e != hipErrorInvalidConfiguration) return e;
         }
         if (size_t(c) * 4 > lds_limit()) return hipErrorInvalidValue;
