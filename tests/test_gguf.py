@@ -271,3 +271,18 @@ def test_differential_structured_mutations(ref):
         n_ok += r.startswith("ok=1")
         n_err += r.startswith("ok=0")
     assert n_ok > 100 and n_err > 100  # both outcomes exercised
+
+
+@pytest.mark.parametrize("q5", [False, True])
+def test_kquant_writer_round_trip(q5):
+    """The writer's K-quant packer (the inverse of k_scale_min) read back by
+    the oracle's dequantiser: within half a quantisation step of the input,
+    which a misplaced scale or min bit would exceed by orders of magnitude."""
+    from oracle import oracle as O
+    o = O.Oracle()
+    rng = np.random.default_rng(21)
+    w = rng.uniform(-0.12, 0.12, size=(16, 768)).astype(np.float32)
+    b = np.frombuffer(G.quantize_kquant(w, q5), np.uint8)
+    deq = o.dequantize(O.Q5_K if q5 else O.Q4_K, b, w.size).reshape(w.shape)
+    step = 0.24 / (31 if q5 else 15)
+    assert np.abs(deq - w).max() <= 0.5 * step * 1.15

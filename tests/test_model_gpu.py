@@ -162,3 +162,40 @@ def test_synthetic_model_runs(zq):
     _, lg = m.prefill([1, 2, 3, 4])
     assert np.isfinite(lg).all()
     m.close()
+
+
+@pytest.mark.parametrize("ptype", [G.GGML_Q4_K, G.GGML_Q5_K])
+def test_kquant_model_matches_reference(tmp_path, zq, ptype):
+    """A Q4_K / Q5_K llama (projections and output K-quants, Q8_0 embedding):
+    prefill and decode logits of the device model within the fp32 bar of the
+    reference runtime, and greedy generation token-identical.  K-quant
+    projections always take fp32 activations (their only reference routes),
+    whatever the prefill mode."""
+    if not os.path.exists(REF_LIB):
+        pytest.skip("oracle/_ref not built")
+    from oracle.oracle import ReferenceModel
+    from zeninfer_amd.model import PREFILL_INT8
+    path = tmp_path / f"tiny_{ptype}.gguf"
+    G.synthetic_llama(path, SHAPE, seed=11, proj_type=ptype)
+    ref = ReferenceModel(path)
+    m = load(path, PREFILL_INT8)
+    assert m.config["weight_format"] == ptype
+    nxt, lg = m.prefill(PROMPT)
+    lr = ref.prefill(PROMPT, capacity=128)
+    ok, err, scale = close_to(lg, lr, 1e-4)
+    print(f"fmt {ptype} prefill: max err {err:.3e} of {scale:.3f}")
+    assert ok and nxt == int(np.argmax(lr))
+    tok = nxt
+    for step in range(4):
+        nxt, lg = m.decode(tok)
+        lr = ref.step(tok, len(PROMPT) + step)
+        ok, err, scale = close_to(lg, lr, 1e-4)
+        assert ok and nxt == int(np.argmax(lr)), (step, err)
+        tok = nxt
+    m.close()
+    m = load(path, PREFILL_INT8)
+    ours, _, _ = m.generate(PROMPT, 16)
+    theirs, _, _ = ref.generate(PROMPT, 16)
+    assert ours == theirs
+    m.close()
+    ref.close()

@@ -482,13 +482,15 @@ int zq_model_load_gguf(const zq_gguf* g, uint32_t max_positions, zq_model_config
         if (n.w) {
             const bool embd = n.w == &m->embd;
             const int ty = int(t.ggml_type);
-            if (embd ? !(ty == zq::kQ8_0 || ty == 0) : !(ty == zq::kQ8_0 || ty == zq::kQ4_0 || ty == zq::kQ6_K)) {
+            const bool proj_ok = ty == zq::kQ8_0 || ty == zq::kQ4_0 || ty == zq::kQ4_K || ty == zq::kQ5_K ||
+                                 ty == zq::kQ6_K;
+            if (embd ? !(ty == zq::kQ8_0 || ty == 0) : !proj_ok) {
                 delete m;
                 return fail("unsupported tensor type " + std::to_string(ty) + " for " + n.name, ZQ_DECLINED);
             }
-            if (n.w == &m->out && !(ty == zq::kQ8_0 || ty == zq::kQ4_0 || ty == zq::kQ6_K)) {
+            if (n.w == &m->out && !proj_ok) {
                 delete m;
-                return fail("output projection must be Q8_0, Q4_0 or Q6_K", ZQ_DECLINED);
+                return fail("output projection must be Q8_0, Q4_0, Q4_K, Q5_K or Q6_K", ZQ_DECLINED);
             }
         }
         arena += align_up(size_t(t.byte_size) + ZQ_WEIGHT_TAIL_PAD, kAlign);

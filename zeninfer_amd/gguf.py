@@ -23,7 +23,7 @@ import numpy as np
 # metadata value types (src/gguf.cpp:21 of the reference)
 U8, I8, U16, I16, U32, I32, F32, BOOL, STRING, ARRAY, U64, I64, F64 = range(13)
 # ggml tensor types used here
-GGML_F32, GGML_F16, GGML_Q4_0, GGML_Q8_0, GGML_Q6_K = 0, 1, 2, 8, 14
+GGML_F32, GGML_F16, GGML_Q4_0, GGML_Q8_0, GGML_Q4_K, GGML_Q5_K, GGML_Q6_K = 0, 1, 2, 8, 12, 13, 14
 
 _SCALAR = {U8: "<B", I8: "<b", U16: "<H", I16: "<h", U32: "<I", I32: "<i", F32: "<f", BOOL: "<B",
            U64: "<Q", I64: "<q", F64: "<d"}
@@ -104,6 +104,53 @@ def quantize_q8_0(w: np.ndarray) -> bytes:
     return out.tobytes()
 
 
+def quantize_kquant(w: np.ndarray, q5: bool = False) -> bytes:
+    """Row-major fp32 [rows, cols] (cols % 256 == 0) to GGML Q4_K / Q5_K
+    super-blocks: per 32-element group a 6-bit scale and min, per super-block
+    fp16 d and dmin, element = d*sc*q - dmin*m with q in 0..15 (0..31).  A
+    plain min/max quantiser (no search); the packing is the inverse of the
+    reference's k_scale_min (src/quant.cpp:133-141)."""
+    qmax = 31 if q5 else 15
+    g = w.reshape(-1, 8, 32).astype(np.float32)              # [super-blocks, groups, 32]
+    lo = np.minimum(g.min(axis=2), 0.0)                      # the offset is subtracted: min <= 0
+    hi = g.max(axis=2)
+    scale = np.maximum(hi - lo, 1e-12) / qmax                # per group
+    minv = -lo                                               # >= 0
+    d = scale.max(axis=1) / 63.0
+    dm = minv.max(axis=1) / 63.0
+    d16 = d.astype(np.float16)
+    dm16 = dm.astype(np.float16)
+    d32, dm32 = d16.astype(np.float32), dm16.astype(np.float32)
+    sc = np.clip(np.rint(scale / np.where(d32 > 0, d32, 1)[:, None]), 0, 63).astype(np.uint32)
+    mn = np.clip(np.rint(minv / np.where(dm32 > 0, dm32, 1)[:, None]), 0, 63).astype(np.uint32)
+    eff_s = d32[:, None] * sc.astype(np.float32)
+    eff_m = dm32[:, None] * mn.astype(np.float32)
+    q = np.rint((g + eff_m[:, :, None]) / np.where(eff_s > 0, eff_s, 1)[:, :, None])
+    q = np.clip(q, 0, qmax).astype(np.uint32)                # [sb, group, 32]
+    nsb = g.shape[0]
+    scales = np.zeros((nsb, 12), np.uint32)
+    for j in range(4):
+        scales[:, j] = sc[:, j] | ((sc[:, j + 4] >> 4) << 6)
+        scales[:, j + 4] = mn[:, j] | ((mn[:, j + 4] >> 4) << 6)
+        scales[:, j + 8] = (sc[:, j + 4] & 15) | ((mn[:, j + 4] & 15) << 4)
+    qs = np.zeros((nsb, 4, 32), np.uint32)
+    for j in range(8):
+        qs[:, j // 2] |= (q[:, j] & 15) << (4 * (j % 2))
+    out = np.zeros((nsb, 176 if q5 else 144), np.uint8)
+    out[:, 0:2] = d16.view(np.uint8).reshape(-1, 2)
+    out[:, 2:4] = dm16.view(np.uint8).reshape(-1, 2)
+    out[:, 4:16] = scales.astype(np.uint8)
+    if q5:
+        qh = np.zeros((nsb, 32), np.uint32)
+        for j in range(8):
+            qh |= ((q[:, j] >> 4) & 1) << j
+        out[:, 16:48] = qh.astype(np.uint8)
+        out[:, 48:] = qs.reshape(nsb, 128).astype(np.uint8)
+    else:
+        out[:, 16:] = qs.reshape(nsb, 128).astype(np.uint8)
+    return out.tobytes()
+
+
 @dataclass
 class LlamaShape:
     embedding: int = 4096
@@ -118,9 +165,10 @@ class LlamaShape:
 
 
 def synthetic_llama(path, shape: LlamaShape, seed: int = 0x5EED0004, weight_scale: float = 0.12,
-                    name: str = "synthetic-llama-q8_0") -> int:
-    """Write a random-init Llama-layout GGUF with Q8_0 projections, Q8_0 token
-    embedding and output, and F32 norms.  Returns the file size in bytes."""
+                    name: str = "synthetic-llama-q8_0", proj_type: int = GGML_Q8_0) -> int:
+    """Write a random-init Llama-layout GGUF with Q8_0 (or, with proj_type,
+    Q4_K / Q5_K) projections and output, a Q8_0 token embedding and F32
+    norms.  Returns the file size in bytes."""
     s = shape
     rng = np.random.default_rng(seed)
     hd = s.embedding // s.heads
@@ -138,14 +186,17 @@ def synthetic_llama(path, shape: LlamaShape, seed: int = 0x5EED0004, weight_scal
     ]:
         w.add_meta(key, t, v)
 
-    def proj(name, rows, cols):
+    def proj(name, rows, cols, ty=proj_type):
         m = rng.uniform(-weight_scale, weight_scale, size=(rows, cols)).astype(np.float32)
-        w.add_tensor(name, [cols, rows], GGML_Q8_0, quantize_q8_0(m))
+        if ty == GGML_Q8_0:
+            w.add_tensor(name, [cols, rows], GGML_Q8_0, quantize_q8_0(m))
+        else:
+            w.add_tensor(name, [cols, rows], ty, quantize_kquant(m, ty == GGML_Q5_K))
 
     def norm(name, n):
         w.add_tensor(name, [n], GGML_F32, rng.uniform(0.85, 1.15, size=n).astype(np.float32).tobytes())
 
-    proj("token_embd.weight", s.vocab, s.embedding)
+    proj("token_embd.weight", s.vocab, s.embedding, GGML_Q8_0)
     for l in range(s.layers):
         p = f"blk.{l}."
         norm(p + "attn_norm.weight", s.embedding)
