@@ -199,3 +199,28 @@ def test_kquant_model_matches_reference(tmp_path, zq, ptype):
     assert ours == theirs
     m.close()
     ref.close()
+
+
+def test_fused_decode_equals_unfused(tiny_path, zq):
+    """The decode step with the norms and SiLU folded into the GEMVs against
+    the separate-kernel step (ZQ_MODEL_FUSED=0): the same arithmetic except
+    the order of the double-precision sum of squares, so logits agree to a
+    few fp32 ulps and the greedy tokens are identical."""
+    from zeninfer_amd.model import PREFILL_F32
+    runs = []
+    for fused in ("1", "0"):
+        os.environ["ZQ_MODEL_FUSED"] = fused
+        try:
+            m = load(tiny_path, PREFILL_F32)
+        finally:
+            os.environ.pop("ZQ_MODEL_FUSED", None)
+        nxt, _ = m.prefill(PROMPT)
+        seq = []
+        for _ in range(8):
+            nxt, lg = m.decode(nxt)
+            seq.append((nxt, lg.copy()))
+        runs.append(seq)
+        m.close()
+    for (ta, la), (tb, lb) in zip(*runs):
+        assert ta == tb
+        assert np.abs(la - lb).max() <= 1e-5 * np.abs(lb).max() + 1e-6

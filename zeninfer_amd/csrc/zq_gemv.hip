@@ -377,9 +377,9 @@ __global__ __launch_bounds__(kThreads) void gemv_xreg_kernel(TaskTable tt, const
 // distinct banks).  Requires the slice-row byte ranges to be 16 B aligned:
 // cols % 256 == 0 and a 16 B aligned weight base.  The next row block's
 // loads are issued before the current block is decoded.
-template <int FMT, int R, int S, int NW, int D>
+template <int FMT, int R, int S, int NW, int D, int XK>
 __global__ __launch_bounds__(NW * 64) void gemv_stream_kernel(TaskTable tt, const float* __restrict__ x,
-                                                               uint32_t cols, uint32_t total_blocks) {
+                                                               uint32_t cols, uint32_t total_blocks, XPrologue pro) {
     constexpr int DW = FMT == kQ8_0 ? 17 : 9;
     constexpr int NT = NW * 64;
     constexpr int TEAMS = NW / S;
@@ -432,16 +432,22 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_kernel(TaskTable tt, cons
             }
     };
 
-    // x is loaded first: loads retire in issue order, so x must not queue
-    // behind the weight blocks.
+    // x (or its producer's operands) is loaded first: loads retire in issue
+    // order, so x must not queue behind the weight blocks.
+    static_assert(XK == kXPlain || XLDS, "x prologues run on the LDS-staged path");
     const uint32_t nx4 = cols >> 2;
-    const float4* x4 = reinterpret_cast<const float4*>(x);
-    float4 xr[XPT];
+    const float4* x4 = reinterpret_cast<const float4*>(XK == kXPlain ? x : pro.a);
+    float4 xr[XPT], xb[XK == kXPlain ? 1 : XPT], xw[XK == kAddNorm ? XPT : 1];
 #pragma unroll
     for (int k = 0; k < XPT; ++k) {
         if constexpr (XLDS) {
-            const uint32_t idx = threadIdx.x + uint32_t(k) * NT;
-            xr[k] = x4[min(idx, nx4 - 1)];
+            const uint32_t idx = min(threadIdx.x + uint32_t(k) * NT, nx4 - 1);
+            xr[k] = x4[idx];
+            if constexpr (XK == kSiluMul) xb[k] = reinterpret_cast<const float4*>(pro.b)[idx];
+            if constexpr (XK == kAddNorm) {
+                xb[k] = pro.b ? reinterpret_cast<const float4*>(pro.b)[idx] : make_float4(0, 0, 0, 0);
+                xw[k] = reinterpret_cast<const float4*>(pro.w)[idx];
+            }
         } else {
             xr[k] = x4[(active ? p : 0u) * 16 + k];
         }
@@ -460,6 +466,42 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_kernel(TaskTable tt, cons
         load(rowp, u[d]);
     }
     float xv[64];
+    if constexpr (XK == kSiluMul) {
+        // g / (1 + e^-g) * u, the expression of silu_mul_kernel
+        auto f = [](float g, float u) { return g / (1.0f + expf(-g)) * u; };
+#pragma unroll
+        for (int k = 0; k < XPT; ++k)
+            xr[k] = make_float4(f(xr[k].x, xb[k].x), f(xr[k].y, xb[k].y), f(xr[k].z, xb[k].z), f(xr[k].w, xb[k].w));
+    }
+    if constexpr (XK == kAddNorm) {
+        // v = a + b; sum of squares in double; inv = 1/sqrtf(float(ss/n) + eps);
+        // x = v * inv * w -- the arithmetic of rmsnorm_kernel
+        __shared__ double xred[NW];
+        double ss = 0.0;
+#pragma unroll
+        for (int k = 0; k < XPT; ++k) {
+            xr[k] = make_float4(xr[k].x + xb[k].x, xr[k].y + xb[k].y, xr[k].z + xb[k].z, xr[k].w + xb[k].w);
+            if (threadIdx.x + uint32_t(k) * NT < nx4) {
+                ss += double(xr[k].x) * double(xr[k].x);
+                ss += double(xr[k].y) * double(xr[k].y);
+                ss += double(xr[k].z) * double(xr[k].z);
+                ss += double(xr[k].w) * double(xr[k].w);
+                if (pro.r_out && blockIdx.x == 0)
+                    reinterpret_cast<float4*>(pro.r_out)[threadIdx.x + uint32_t(k) * NT] = xr[k];
+            }
+        }
+        ss = wave_sum(ss);
+        if (lane == 0) xred[wave] = ss;
+        __syncthreads();
+        double tot = 0.0;
+#pragma unroll
+        for (int i = 0; i < NW; ++i) tot += xred[i];
+        const float inv = 1.0f / sqrtf(float(tot / double(cols)) + pro.eps);
+#pragma unroll
+        for (int k = 0; k < XPT; ++k)
+            xr[k] = make_float4(xr[k].x * inv * xw[k].x, xr[k].y * inv * xw[k].y, xr[k].z * inv * xw[k].z,
+                                xr[k].w * inv * xw[k].w);
+    }
     if constexpr (XLDS) {
 #pragma unroll
         for (int k = 0; k < XPT; ++k) {  // out-of-range threads rewrite the last float4 with the same value
@@ -1110,8 +1152,9 @@ int wg_per_cu() {
     return v;
 }
 
-template <int FMT, int R, int S, int NW, int D>
-hipError_t launch_stream(TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream) {
+template <int FMT, int R, int S, int NW, int D, int XK = kXPlain>
+hipError_t launch_stream(TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream,
+                         const XPrologue& pro = XPrologue{}) {
     constexpr uint32_t RB = (NW / S) * R;
     constexpr int DW = FMT == kQ8_0 ? 17 : 9;
     uint32_t blocks = 0;
@@ -1125,14 +1168,14 @@ hipError_t launch_stream(TaskTable& tt, const float* x, uint32_t cols, hipStream
     if (lds > lds_limit()) return hipErrorInvalidConfiguration;
     static const int resident = [lds] {
         int n = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_stream_kernel<FMT, R, S, NW, D>, NW * 64, lds) !=
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_stream_kernel<FMT, R, S, NW, D, XK>, NW * 64, lds) !=
                 hipSuccess || n < 1)
             n = 1;
         return n;
     }();
     const uint32_t grid = std::min<uint32_t>(blocks, uint32_t(cu_count() * (NW == 16 ? 1 : resident)));
-    hipLaunchKernelGGL((gemv_stream_kernel<FMT, R, S, NW, D>), dim3(grid), dim3(NW * 64), lds, stream, tt, x, cols,
-                       blocks);
+    hipLaunchKernelGGL((gemv_stream_kernel<FMT, R, S, NW, D, XK>), dim3(grid), dim3(NW * 64), lds, stream, tt, x, cols,
+                       blocks, pro);
     return hipGetLastError();
 }
 // One workgroup of 16 waves per CU, one row block prefetched (D = 1): the
@@ -1364,6 +1407,41 @@ hipError_t launch_gemv(int fmt, const GemvTask* tasks, int count, const float* x
     if (R == 4) return launch_pairs<kQ4_0, 4>(tt, x, c, stream);
     if (R == 2) return launch_pairs<kQ4_0, 2>(tt, x, c, stream);
     return launch_pairs<kQ4_0, 1>(tt, x, c, stream);
+}
+
+
+namespace {
+template <int FMT, int XK>
+hipError_t launch_prologue_s(TaskTable& tt, uint32_t cols, const XPrologue& pro, hipStream_t stream) {
+    const uint32_t pairs = cols >> 6;
+    if (pairs <= 64) return launch_stream<FMT, 1, 1, 16, 1, XK>(tt, nullptr, cols, stream, pro);
+    if (pairs <= 128) return launch_stream<FMT, 1, 2, 16, 1, XK>(tt, nullptr, cols, stream, pro);
+    return launch_stream<FMT, 1, 4, 16, 1, XK>(tt, nullptr, cols, stream, pro);
+}
+}  // namespace
+
+hipError_t launch_gemv_prologue(int fmt, const GemvTask* tasks, int count, const XPrologue& pro, size_t cols,
+                                hipStream_t stream) {
+    if (count < 1 || count > kMaxTasks || !row_bytes(fmt, cols) || !pro.a) return hipErrorInvalidValue;
+    if ((fmt != kQ8_0 && fmt != kQ4_0) || cols % 256 || cols / 64 > 256) return hipErrorInvalidConfiguration;
+    auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    if (!a16(pro.a) || !a16(pro.b) || !a16(pro.w) || !a16(pro.r_out)) return hipErrorInvalidConfiguration;
+    if ((pro.kind == kSiluMul && !pro.b) || (pro.kind == kAddNorm && !pro.w) ||
+        (pro.kind != kSiluMul && pro.kind != kAddNorm))
+        return hipErrorInvalidValue;
+    TaskTable tt{};
+    tt.count = count;
+    for (int i = 0; i < count; ++i) {
+        if (!tasks[i].w || !tasks[i].y || !tasks[i].rows) return hipErrorInvalidValue;
+        if (!a16(tasks[i].w)) return hipErrorInvalidConfiguration;
+        tt.t[i] = tasks[i];
+    }
+    const uint32_t c = static_cast<uint32_t>(cols);
+    if (pro.kind == kSiluMul)
+        return fmt == kQ8_0 ? launch_prologue_s<kQ8_0, kSiluMul>(tt, c, pro, stream)
+                            : launch_prologue_s<kQ4_0, kSiluMul>(tt, c, pro, stream);
+    return fmt == kQ8_0 ? launch_prologue_s<kQ8_0, kAddNorm>(tt, c, pro, stream)
+                        : launch_prologue_s<kQ4_0, kAddNorm>(tt, c, pro, stream);
 }
 
 }  // namespace zq

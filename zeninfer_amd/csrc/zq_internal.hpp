@@ -24,6 +24,28 @@ size_t row_bytes(int fmt, size_t cols);
 hipError_t launch_gemv(int fmt, const GemvTask* tasks, int count, const float* x,
                        size_t cols, hipStream_t stream);
 
+// The producer of a decode GEMV's input folded into the GEMV itself (every
+// workgroup recomputes it while staging x):
+//   kSiluMul   x = silu(a) * b, elementwise as launch_silu_mul
+//   kAddNorm   v = a + b (b may be null), x = rmsnorm(v) * w as
+//              launch_add_rmsnorm; r_out (may be null) receives v, written by
+//              workgroup 0 only, so it must not alias a or b.
+struct XPrologue {
+    int kind;
+    const float* a;
+    const float* b;
+    const float* w;
+    float* r_out;
+    float eps;
+};
+constexpr int kXPlain = 0, kSiluMul = 1, kAddNorm = 2;
+// Q8_0 / Q4_0 only, on the streaming kernel's shapes (cols % 256 == 0,
+// cols <= 16384, 16-byte aligned operands); hipErrorInvalidConfiguration
+// when the shape or format is not covered, so the caller runs the unfused
+// kernels instead.
+hipError_t launch_gemv_prologue(int fmt, const GemvTask* tasks, int count, const XPrologue& pro, size_t cols,
+                                hipStream_t stream);
+
 // Per-32-element activation quantiser (int8 + fp32 scale per block).
 hipError_t launch_quantize_acts(const float* X, int8_t* xq, float* xs, size_t M, size_t K,
                                 hipStream_t stream);

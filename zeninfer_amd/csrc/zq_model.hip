@@ -90,6 +90,7 @@ struct zq_model {
 
     uint32_t cur_pos = 0;  // positions held in the cache
     bool use_graph = true;
+    bool fused = false;    // decode step with norms and SiLU folded into the GEMVs
     hipGraphExec_t decode_exec = nullptr;
     hipGraph_t decode_graph = nullptr;
 
@@ -324,10 +325,63 @@ hipError_t enqueue_head(zq_model& m, uint32_t row) {
     return zq::launch_argmax(m.logits, c.vocab, m.next_dev, m.argmax_part, m.stream);
 }
 
+// Decode step with every residual add + RMSNorm and the SiLU*up folded into
+// the GEMV that consumes it (zq::XPrologue): per layer QKV, attention, o,
+// gate|up, down.  The residual stream alternates between x and h (h is not
+// otherwise used on this path), so no workgroup's residual write races the
+// reads of another.
+hipError_t enqueue_decode_fused(zq_model& m) {
+    const auto& c = m.cfg;
+    const uint32_t E = c.embedding, QW = c.heads * c.head_dim, KW = c.kv_heads * c.head_dim, F = c.ffn;
+    float* r = m.x;
+    float* ralt = m.h;
+    const float* delta = nullptr;  // the pending residual add (down output)
+    for (uint32_t l = 0; l < c.layers; ++l) {
+        Layer& L = m.layers[l];
+        zq::GemvTask tq[3] = {{L.q.p, m.q, QW}, {L.k.p, m.k, KW}, {L.v.p, m.v, KW}};
+        const zq::XPrologue pq{zq::kAddNorm, r, delta, L.attn_norm, delta ? ralt : nullptr, c.rms_epsilon};
+        HIPCHK(zq::launch_gemv_prologue(L.q.fmt, tq, 3, pq, E, m.stream));
+        if (delta) std::swap(r, ralt);
+        HIPCHK(zq::launch_attention_decode(m.q, m.k, m.v, L.kc, L.vc, m.cos_tab, m.sin_tab, m.attn_part, m.att,
+                                           m.pos_dev, c.heads, c.kv_heads, c.head_dim, m.pairs, c.max_positions,
+                                           m.attn_scale, m.stream));
+        zq::GemvTask to = {L.o.p, m.tmp, E};
+        HIPCHK(zq::launch_gemv(L.o.fmt, &to, 1, m.att, QW, m.stream));
+        zq::GemvTask tg[2] = {{L.gate.p, m.gate, F}, {L.up.p, m.up, F}};
+        const zq::XPrologue pg{zq::kAddNorm, r, m.tmp, L.ffn_norm, ralt, c.rms_epsilon};
+        HIPCHK(zq::launch_gemv_prologue(L.gate.fmt, tg, 2, pg, E, m.stream));
+        std::swap(r, ralt);
+        zq::GemvTask td = {L.down.p, m.tmp, E};
+        const zq::XPrologue pd{zq::kSiluMul, m.gate, m.up, nullptr, nullptr, 0.0f};
+        HIPCHK(zq::launch_gemv_prologue(L.down.fmt, &td, 1, pd, F, m.stream));
+        delta = m.tmp;
+    }
+    zq::GemvTask th = {m.out.p, m.logits, c.vocab};
+    const zq::XPrologue ph{zq::kAddNorm, r, delta, m.out_norm, nullptr, c.rms_epsilon};
+    HIPCHK(zq::launch_gemv_prologue(m.out.fmt, &th, 1, ph, E, m.stream));
+    return zq::launch_argmax(m.logits, c.vocab, m.next_dev, m.argmax_part, m.stream);
+}
+
 hipError_t enqueue_decode(zq_model& m) {
     HIPCHK(zq::launch_embed(m.embd.fmt, m.embd.p, m.tokens_dev, m.cfg.vocab, m.x, m.cfg.embedding, 1, m.stream));
+    if (m.fused) return enqueue_decode_fused(m);
     HIPCHK(enqueue_layers(m, 1));
     return enqueue_head(m, 0);
+}
+
+// The fused decode covers Q8_0 / Q4_0 projections on the streaming GEMV's
+// shapes; anything else keeps the separate norm / activation kernels.
+// ZQ_MODEL_FUSED=0 disables it (A/B runs and the equivalence test).
+void choose_fused(zq_model& m) {
+    const char* e = std::getenv("ZQ_MODEL_FUSED");
+    const auto& c = m.cfg;
+    auto ok = [](int f) { return f == zq::kQ8_0 || f == zq::kQ4_0; };
+    bool f = !(e && e[0] == '0') && c.embedding % 256 == 0 && c.ffn % 256 == 0 && c.embedding <= 16384 &&
+             c.ffn <= 16384 && ok(m.out.fmt);
+    for (const Layer& L : m.layers)
+        f = f && ok(L.q.fmt) && L.k.fmt == L.q.fmt && L.v.fmt == L.q.fmt && ok(L.gate.fmt) && L.up.fmt == L.gate.fmt &&
+            ok(L.down.fmt) && ok(L.o.fmt);
+    m.fused = f;
 }
 
 int finish_outputs(zq_model& m, float* logits, uint32_t* next) {
@@ -512,6 +566,7 @@ int zq_model_load_gguf(const zq_gguf* g, uint32_t max_positions, zq_model_config
     }
     c.weight_format = m->layers.empty() ? m->out.fmt : m->layers[0].q.fmt;
     if (!alloc_runtime(*m, e)) { delete m; return fail(e, ZQ_ERR_OOM); }
+    choose_fused(*m);
     if (cfg_out) *cfg_out = c;
     *model = m;
     set_err(err, err_cap, "");
@@ -558,6 +613,7 @@ int zq_model_create_synthetic(const zq_model_config* cfg, uint64_t seed, zq_mode
     }
     if (hipStreamSynchronize(m->stream) != hipSuccess) { delete m; return ZQ_ERR_HIP; }
     if (!alloc_runtime(*m, e)) { delete m; set_err(err, err_cap, e); return ZQ_ERR_OOM; }
+    choose_fused(*m);
     *model = m;
     set_err(err, err_cap, "");
     return ZQ_OK;
