@@ -72,14 +72,6 @@ __device__ __forceinline__ constexpr bool use_nt() { return ZQ_GEMV_NT != 0; }
 #define ZQ_GEMV_STREAM_NT 1
 #endif
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ uint4 stream_load(const uint4* p) {
-    if constexpr (ZQ_GEMV_STREAM_NT != 0) {
-        const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
-        return make_uint4(v.x, v.y, v.z, v.w);
-    } else {
-        return *p;
-    }
-}
 
 // Diagnostic build only (-DZQ_GEMV_DIAG): wave 0 of each of the first 1024
 // workgroups of gemv_stream_kernel records the constant-rate clock at kernel
