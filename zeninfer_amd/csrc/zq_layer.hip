@@ -310,21 +310,22 @@ __global__ __launch_bounds__(kT) void attention_decode_kernel(
         if (sj == 0 && sp < n) sc[g][sp] = d * scale;
     }
     __syncthreads();
-    // ---- chunk softmax: one thread per head ----
+    // ---- chunk softmax: one wave per head, one lane per position ----
     float* outp = part + size_t(kh * G) * splits * (D + 2);
-    if (tid < int(G)) {
-        const uint32_t g = tid;
-        float m = -INFINITY;
-        for (uint32_t p = 0; p < n; ++p) m = fmaxf(m, sc[g][p]);
-        float l = 0.0f;
-        for (uint32_t p = 0; p < n; ++p) {
-            const float e = expf(sc[g][p] - m);
-            sc[g][p] = e;
-            l += e;
+    {
+        const int wv = tid >> 6, ln = tid & 63;
+        for (uint32_t g = wv; g < G; g += kT / 64) {
+            const float sv = uint32_t(ln) < n ? sc[g][ln] : -INFINITY;
+            const float m = wave_max(sv);
+            const float e = uint32_t(ln) < n ? expf(sv - m) : 0.0f;
+            if (uint32_t(ln) < n) sc[g][ln] = e;
+            const float l = wave_sum(e);
+            if (ln == 0) {
+                float* o = outp + (size_t(g) * splits + s) * (D + 2);
+                o[D] = m;
+                o[D + 1] = l;
+            }
         }
-        float* o = outp + (size_t(g) * splits + s) * (D + 2);
-        o[D] = m;
-        o[D + 1] = l;
     }
     __syncthreads();
     // ---- acc[g][d] = sum_p e[g][p] * v[p][d] ----
@@ -368,16 +369,19 @@ __global__ __launch_bounds__(kT) void attention_combine_kernel(const float* __re
     const float* ph = part + size_t(h) * splits * (D + 2);
     for (uint32_t i = threadIdx.x; i < ns * (D + 2); i += kT) ps[i] = ph[i];
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (threadIdx.x < 64) {  // wave 0: lanes stride over the chunks
+        const uint32_t ln = threadIdx.x;
         float M = -INFINITY;
-        for (uint32_t s = 0; s < ns; ++s) M = fmaxf(M, ps[s * (D + 2) + D]);
+        for (uint32_t s = ln; s < ns; s += 64) M = fmaxf(M, ps[s * (D + 2) + D]);
+        M = wave_max(M);
         double L = 0.0;
-        for (uint32_t s = 0; s < ns; ++s) {
+        for (uint32_t s = ln; s < ns; s += 64) {
             const float w = expf(ps[s * (D + 2) + D] - M);
             wgt[s] = w;
             L += double(ps[s * (D + 2) + D + 1]) * double(w);
         }
-        inv_l = 1.0f / float(L);
+        L = wave_sum(L);
+        if (ln == 0) inv_l = 1.0f / float(L);
     }
     __syncthreads();
     for (uint32_t d = threadIdx.x; d < D; d += kT) {
