@@ -39,6 +39,7 @@ traffic  HBM bytes per launch of the dominant kernel from two rocprofv3 --pmc
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
        python bench.py --summarize-trace kernel_trace.csv   (rocprofv3 helper)
        python bench.py --pmc-workload                       (short run for --pmc passes)
+       python bench.py --model-only                         (config 4 only, for profiling)
 """
 import argparse
 import json
@@ -286,12 +287,21 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--summarize-trace")
     ap.add_argument("--pmc-workload", action="store_true")
+    ap.add_argument("--model-only", action="store_true",
+                    help="run only the config-4 decoder leg and print its JSON (profiling helper)")
     args = ap.parse_args()
     if args.summarize_trace:
         summarize_trace(args.summarize_trace)
         return 0
     if args.pmc_workload:
         pmc_workload()
+        return 0
+    if args.model_only:
+        import torch
+        from zeninfer_amd import zq
+        torch.cuda.set_device(0)
+        zq.init()
+        print(json.dumps(model_config4()))
         return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this path has no multi-GPU leg in this build "

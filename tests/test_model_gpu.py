@@ -224,3 +224,32 @@ def test_fused_decode_equals_unfused(tiny_path, zq):
     for (ta, la), (tb, lb) in zip(*runs):
         assert ta == tb
         assert np.abs(la - lb).max() <= 1e-5 * np.abs(lb).max() + 1e-6
+
+
+@pytest.mark.parametrize("embedding,heads,kv_heads", [(512, 4, 2), (1024, 8, 1)])
+def test_prefill_attention_shapes_match_reference(tmp_path, zq, embedding, heads, kv_heads):
+    """head_dim 128 with 2 and 8 query heads per kv head, a 150-token prompt
+    (three 64-key tiles, a partial last query tile): fp32 prefill logits and
+    the following decode step within the fp32 bar of the reference."""
+    if not os.path.exists(REF_LIB):
+        pytest.skip("oracle/_ref not built")
+    from oracle.oracle import ReferenceModel
+    from zeninfer_amd.model import PREFILL_F32
+    shape = G.LlamaShape(embedding=embedding, layers=1, heads=heads, kv_heads=kv_heads, ffn=512, vocab=512,
+                         context=2048)
+    path = tmp_path / f"attn_{embedding}_{heads}_{kv_heads}.gguf"
+    G.synthetic_llama(path, shape, seed=5)
+    prompt = np.random.default_rng(9).integers(0, 512, size=150).tolist()
+    ref = ReferenceModel(path)
+    m = load(path, PREFILL_F32, max_positions=256)
+    nxt, lg = m.prefill(prompt)
+    lr = ref.prefill(prompt, capacity=256)
+    ok, err, scale = close_to(lg, lr, 1e-4)
+    print(f"E={embedding} H={heads} KV={kv_heads}: prefill max err {err:.3e} of {scale:.3f}")
+    assert ok and nxt == int(np.argmax(lr))
+    nxt2, lg2 = m.decode(nxt)
+    lr2 = ref.step(nxt, len(prompt))
+    ok, err, scale = close_to(lg2, lr2, 1e-4)
+    assert ok, err
+    m.close()
+    ref.close()
