@@ -83,8 +83,9 @@ def summarize_trace(path):
 
 def pmc_workload():
     """Few launches for rocprofv3 --pmc passes: a 256 MiB device copy (counter
-    calibration), the 4096x14336 Q8_0 down GEMV on 4 distinct matrices, and
-    the int8 GEMM at M=2048 on 3 distinct 14336x4096 matrices."""
+    calibration), the 4096x14336 Q8_0 down GEMV on 4 distinct matrices, the
+    int8 GEMM at M=2048 on 3 distinct 14336x4096 matrices and the Q4_K GEMV
+    14336x4096 on 3 distinct matrices."""
     import torch
     from zeninfer_amd import zq
     zq.init()
@@ -117,6 +118,18 @@ def pmc_workload():
     wsp = torch.empty(wsb, dtype=torch.uint8, device=dev)
     for w in wg:
         zq.gemm_dev(Q8, w, X, Y, M, N, K, zq.ACT_INT8, wsp, wsb)
+    torch.cuda.synchronize()
+    del wg
+    # Q4_K GEMV 14336x4096 on 3 distinct matrices (the K-quant streaming kernel)
+    wk = []
+    for i in range(3):
+        t = torch.empty(zq.weight_bytes(zq.Q4_K, FFN, HIDDEN), dtype=torch.uint8, device=dev)
+        zq.synth_weights_dev(zq.Q4_K, 70 + i, t, FFN, HIDDEN)
+        wk.append(t)
+    yk = torch.empty(FFN, device=dev)
+    torch.cuda.synchronize()
+    for t in wk:
+        zq.gemv_dev(zq.Q4_K, t, x[:HIDDEN], yk, FFN, HIDDEN)
     torch.cuda.synchronize()
 
 
