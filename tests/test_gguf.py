@@ -286,3 +286,18 @@ def test_kquant_writer_round_trip(q5):
     deq = o.dequantize(O.Q5_K if q5 else O.Q4_K, b, w.size).reshape(w.shape)
     step = 0.24 / (31 if q5 else 15)
     assert np.abs(deq - w).max() <= 0.5 * step * 1.15
+
+
+def test_q4_0_and_q6_k_writers_round_trip():
+    """The writer's Q4_0 and Q6_K packers read back by the oracle's
+    dequantiser: Q4_0 within one step (its range is [-8, 7] steps, so the
+    extreme of the other sign clamps by up to one step), Q6_K within half a
+    sub-block step."""
+    from oracle import oracle as O
+    o = O.Oracle()
+    rng = np.random.default_rng(22)
+    w = rng.uniform(-0.12, 0.12, size=(16, 768)).astype(np.float32)
+    b = np.frombuffer(G.quantize_q4_0(w), np.uint8)
+    assert np.abs(o.dequantize(O.Q4_0, b, w.size).reshape(w.shape) - w).max() <= 0.12 / 8 * 1.01
+    b = np.frombuffer(G.quantize_q6_k(w), np.uint8)
+    assert np.abs(o.dequantize(O.Q6_K, b, w.size).reshape(w.shape) - w).max() <= 0.5 * 0.12 / 31 * 1.15

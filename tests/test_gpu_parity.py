@@ -108,6 +108,8 @@ GEMV_SHAPES = [
     (O.Q6_K, 1000, 4096), (O.Q6_K, 7, 14336), (O.Q6_K, 3, 256),
     (O.Q4_K, 1000, 4096), (O.Q4_K, 4097, 4096), (O.Q4_K, 7, 14336), (O.Q4_K, 3, 256),
     (O.Q5_K, 1000, 4096), (O.Q5_K, 9, 14336), (O.Q5_K, 5, 11008), (O.Q5_K, 2, 768),
+    # widths past the streaming kernels' 16384 (fallback kernels)
+    (O.Q8_0, 17, 32768), (O.Q4_0, 9, 20480), (O.Q6_K, 5, 24576), (O.Q4_K, 9, 24576), (O.Q5_K, 3, 18432),
 ]
 
 

@@ -253,3 +253,39 @@ def test_prefill_attention_shapes_match_reference(tmp_path, zq, embedding, heads
     assert ok, err
     m.close()
     ref.close()
+
+
+@pytest.mark.parametrize("ptype,down,out", [(G.GGML_Q4_0, None, None), (G.GGML_Q4_K, G.GGML_Q6_K, G.GGML_Q6_K)])
+def test_other_formats_match_reference(tmp_path, zq, ptype, down, out):
+    """A Q4_0 model (fp32 prefill GEMM, the fused decode step's Q4_0
+    prologue kernels) and a mixed Q4_K / Q6_K model (ffn_down and output in
+    Q6_K, as llama.cpp's Q4_K_M files; the unfused decode): fp32-prefill and
+    decode logits within the fp32 bar of the reference, greedy generation
+    token-identical."""
+    if not os.path.exists(REF_LIB):
+        pytest.skip("oracle/_ref not built")
+    from oracle.oracle import ReferenceModel
+    from zeninfer_amd.model import PREFILL_F32
+    path = tmp_path / f"m_{ptype}_{down}.gguf"
+    G.synthetic_llama(path, SHAPE, seed=13, proj_type=ptype, down_type=down, out_type=out)
+    ref = ReferenceModel(path)
+    m = load(path, PREFILL_F32)
+    nxt, lg = m.prefill(PROMPT)
+    lr = ref.prefill(PROMPT, capacity=128)
+    ok, err, scale = close_to(lg, lr, 1e-4)
+    print(f"fmt {ptype}/{down}: prefill max err {err:.3e} of {scale:.3f}")
+    assert ok and nxt == int(np.argmax(lr))
+    tok = nxt
+    for step in range(4):
+        nxt, lg = m.decode(tok)
+        lr = ref.step(tok, len(PROMPT) + step)
+        ok, err, scale = close_to(lg, lr, 1e-4)
+        assert ok and nxt == int(np.argmax(lr)), (step, err)
+        tok = nxt
+    m.close()
+    m = load(path, PREFILL_F32)
+    ours, _, _ = m.generate(PROMPT, 16)
+    theirs, _, _ = ref.generate(PROMPT, 16)
+    assert ours == theirs
+    m.close()
+    ref.close()

@@ -104,6 +104,50 @@ def quantize_q8_0(w: np.ndarray) -> bytes:
     return out.tobytes()
 
 
+def quantize_q4_0(w: np.ndarray) -> bytes:
+    """Row-major fp32 [rows, cols] (cols % 32 == 0) to GGML Q4_0 blocks: fp16
+    d = max|v| / 8 with the sign of the extreme value (so it maps to -8),
+    nibble = clamp(round(v/d) + 8, 0, 15); byte j holds elements j (low
+    nibble) and j+16 (high nibble) (src/quant.cpp:391-397)."""
+    b = w.reshape(-1, 32).astype(np.float32)
+    idx = np.abs(b).argmax(axis=1)
+    ext = b[np.arange(b.shape[0]), idx]
+    d = (ext / -8.0).astype(np.float16)
+    d32 = d.astype(np.float32)
+    inv = np.where(d32 != 0, 1.0 / np.where(d32 != 0, d32, 1), 0.0)
+    n = np.clip(np.rint(b * inv[:, None]) + 8, 0, 15).astype(np.uint8)
+    out = np.empty((b.shape[0], 18), np.uint8)
+    out[:, 0:2] = d.view(np.uint8).reshape(-1, 2)
+    out[:, 2:] = n[:, :16] | (n[:, 16:] << 4)
+    return out.tobytes()
+
+
+def quantize_q6_k(w: np.ndarray) -> bytes:
+    """Row-major fp32 [rows, cols] (cols % 256 == 0) to GGML Q6_K super-blocks:
+    per 16 elements an int8 scale, per super-block fp16 d, element =
+    d*sc*(q-32) with q in 0..63 (src/quant.cpp:500-517 read in reverse)."""
+    g = w.reshape(-1, 16, 16).astype(np.float32)             # [sb, sub-block, 16]
+    amax = np.abs(g).max(axis=2)
+    sub = amax / 31.0                                        # per sub-block step
+    d = (sub.max(axis=1) / 127.0).astype(np.float16)
+    d32 = d.astype(np.float32)
+    sc = np.clip(np.rint(sub / np.where(d32 > 0, d32, 1)[:, None]), 1, 127).astype(np.int32)
+    step = d32[:, None] * sc.astype(np.float32)
+    q = np.clip(np.rint(g / np.where(step > 0, step, 1)[:, :, None]) + 32, 0, 63).astype(np.uint32).reshape(-1, 256)
+    nsb = q.shape[0]
+    out = np.zeros((nsb, 210), np.uint8)
+    for half in range(2):
+        for l in range(32):
+            e = half * 128 + l
+            q0, q1, q2, q3 = q[:, e], q[:, e + 32], q[:, e + 64], q[:, e + 96]
+            out[:, half * 64 + l] = (q0 & 15) | ((q2 & 15) << 4)
+            out[:, half * 64 + 32 + l] = (q1 & 15) | ((q3 & 15) << 4)
+            out[:, 128 + half * 32 + l] = (q0 >> 4) | ((q1 >> 4) << 2) | ((q2 >> 4) << 4) | ((q3 >> 4) << 6)
+    out[:, 192:208] = sc.astype(np.int8).view(np.uint8)
+    out[:, 208:210] = d.view(np.uint8).reshape(-1, 2)
+    return out.tobytes()
+
+
 def quantize_kquant(w: np.ndarray, q5: bool = False) -> bytes:
     """Row-major fp32 [rows, cols] (cols % 256 == 0) to GGML Q4_K / Q5_K
     super-blocks: per 32-element group a 6-bit scale and min, per super-block
@@ -165,10 +209,12 @@ class LlamaShape:
 
 
 def synthetic_llama(path, shape: LlamaShape, seed: int = 0x5EED0004, weight_scale: float = 0.12,
-                    name: str = "synthetic-llama-q8_0", proj_type: int = GGML_Q8_0) -> int:
-    """Write a random-init Llama-layout GGUF with Q8_0 (or, with proj_type,
-    Q4_K / Q5_K) projections and output, a Q8_0 token embedding and F32
-    norms.  Returns the file size in bytes."""
+                    name: str = "synthetic-llama-q8_0", proj_type: int = GGML_Q8_0, down_type: int = None,
+                    out_type: int = None) -> int:
+    """Write a random-init Llama-layout GGUF: projections of proj_type (Q8_0,
+    Q4_0, Q4_K, Q5_K or Q6_K; ffn_down and output may differ, as in
+    llama.cpp's mixed files), a Q8_0 token embedding and F32 norms.  Returns
+    the file size in bytes."""
     s = shape
     rng = np.random.default_rng(seed)
     hd = s.embedding // s.heads
@@ -188,10 +234,9 @@ def synthetic_llama(path, shape: LlamaShape, seed: int = 0x5EED0004, weight_scal
 
     def proj(name, rows, cols, ty=proj_type):
         m = rng.uniform(-weight_scale, weight_scale, size=(rows, cols)).astype(np.float32)
-        if ty == GGML_Q8_0:
-            w.add_tensor(name, [cols, rows], GGML_Q8_0, quantize_q8_0(m))
-        else:
-            w.add_tensor(name, [cols, rows], ty, quantize_kquant(m, ty == GGML_Q5_K))
+        enc = {GGML_Q8_0: quantize_q8_0, GGML_Q4_0: quantize_q4_0, GGML_Q6_K: quantize_q6_k,
+               GGML_Q4_K: lambda a: quantize_kquant(a, False), GGML_Q5_K: lambda a: quantize_kquant(a, True)}[ty]
+        w.add_tensor(name, [cols, rows], ty, enc(m))
 
     def norm(name, n):
         w.add_tensor(name, [n], GGML_F32, rng.uniform(0.85, 1.15, size=n).astype(np.float32).tobytes())
@@ -207,9 +252,9 @@ def synthetic_llama(path, shape: LlamaShape, seed: int = 0x5EED0004, weight_scal
         norm(p + "ffn_norm.weight", s.embedding)
         proj(p + "ffn_gate.weight", s.ffn, s.embedding)
         proj(p + "ffn_up.weight", s.ffn, s.embedding)
-        proj(p + "ffn_down.weight", s.embedding, s.ffn)
+        proj(p + "ffn_down.weight", s.embedding, s.ffn, down_type or proj_type)
     norm("output_norm.weight", s.embedding)
-    proj("output.weight", s.vocab, s.embedding)
+    proj("output.weight", s.vocab, s.embedding, out_type or proj_type)
     return w.write(path)
 
 
