@@ -366,26 +366,25 @@ __global__ __launch_bounds__(kThreads) void splitk_reduce_kernel(const float* __
 // Epilogue: per block one 2-block outer-product MFMA gives dx*dw for both
 // tiles in the accumulator layout, then one cvt + one fma per element.
 constexpr int QTH = 512;
-constexpr int QA_BYTES = BM * KB * 32;                 // 32768
-constexpr int QWROW = KB * 34;                         // 272 raw bytes of a weight row per stage
-constexpr int QWD = QWROW / 4;                         // 68 dwords
-// Weight row r starts at LDS dword r*QW_STRIDE + QW_SHIFT*(r/8).  With an odd
-// stride the MFMA B reads (32 rows, one dword each) fall on distinct banks:
-// measured zero LDS bank conflicts for the whole kernel at stride 69.
-#ifndef ZQ_W_STRIDE
-#define ZQ_W_STRIDE 69
-#define ZQ_W_SHIFT 0
-#endif
-constexpr int QW_STRIDE = ZQ_W_STRIDE, QW_SHIFT = ZQ_W_SHIFT;
-static_assert(QW_STRIDE >= QWD + QW_SHIFT * 15 || QW_SHIFT == 0, "rows must not overlap");
-constexpr int QW_DWORDS = (BN - 1) * QW_STRIDE + QW_SHIFT * ((BN - 1) / 8) + QWD + 1;  // +1: 5th dword read
-constexpr int QW_LOADS = (QW_DWORDS + 63) / 64;        // 64-lane dword loads per stage
-constexpr int QW_PER_WAVE = (QW_LOADS + QTH / 64 - 1) / (QTH / 64);
-constexpr int QW_BYTES = (QW_LOADS * 64 * 4 + 15) / 16 * 16;
-constexpr int QS_BYTES = KB * BM * 4;                  // 4096
-constexpr int QBUF = QA_BYTES + QW_BYTES + QS_BYTES;   // bytes per stage buffer
-static_assert(2 * QBUF <= 160 * 1024, "two stage buffers must fit the 160 KiB LDS");
-static_assert(QA_BYTES % 16 == 0 && QW_BYTES % 16 == 0, "LDS regions stay 16 B aligned");
+// Stage geometry for QKB blocks per K stage (8: 144 KB of LDS, one workgroup
+// per CU; 4: 72 KB, two).  Weight row r starts at LDS dword r * W_STRIDE, an
+// odd stride, so the MFMA B reads (32 rows, one dword each) fall on distinct
+// banks: measured zero LDS bank conflicts for the whole kernel at 69.
+template <int QKB>
+struct QStage {
+    static constexpr int A_BYTES = BM * QKB * 32;           // activation tile
+    static constexpr int UPR = QKB * 2;                     // 16 B units per activation row
+    static constexpr int WD = QKB * 34 / 4;                 // raw dwords of a weight row per stage
+    static constexpr int W_STRIDE = WD | 1;                 // 69 / 35
+    static constexpr int W_DWORDS = (BN - 1) * W_STRIDE + WD + 1;  // +1: the 5th dword read
+    static constexpr int W_LOADS = (W_DWORDS + 63) / 64;   // 64-lane dword loads per stage
+    static constexpr int W_PER_WAVE = (W_LOADS + QTH / 64 - 1) / (QTH / 64);
+    static constexpr int W_BYTES = (W_LOADS * 64 * 4 + 15) / 16 * 16;
+    static constexpr int S_BYTES = QKB * BM * 4;
+    static constexpr int BUF = A_BYTES + W_BYTES + S_BYTES;  // bytes per stage buffer
+    static_assert(2 * BUF <= 160 * 1024, "two stage buffers must fit the 160 KiB LDS");
+    static_assert(A_BYTES % 16 == 0 && W_BYTES % 16 == 0, "LDS regions stay 16 B aligned");
+};
 
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -393,12 +392,17 @@ typedef __attribute__((address_space(3))) void lds_void;
 // no swizzle, stride 0): offsets are plain byte offsets from the base.
 constexpr int kBufferWord3 = 0x00020000;
 
-template <bool DOTS>
-__global__ __launch_bounds__(QTH, 2) void gemm_q8_coalesced_kernel(
+// The kernel body, one instantiation per stage depth; the __global__
+// wrappers below carry the launch bounds (second argument: minimum waves per
+// SIMD -- 4 lets two 8-wave workgroups share a CU when 4-block stages leave
+// LDS for both).
+template <bool DOTS, int QKB>
+__device__ __forceinline__ void gemm_q8_coalesced_body(
     const uint8_t* __restrict__ W, const int8_t* __restrict__ XQ, const float* __restrict__ XS,
     float* __restrict__ Y, int32_t* __restrict__ dots, uint32_t M, uint32_t N, uint32_t K, uint32_t tiles_m,
     uint32_t tiles_n, uint32_t ksplit, uint32_t stages_per_split) {
-    __shared__ __align__(16) uint8_t lds[2 * QBUF];
+    using G = QStage<QKB>;
+    extern __shared__ __align__(16) uint8_t lds[];  // 2 * G::BUF bytes, sized at launch
 
     const uint32_t total_tiles = tiles_m * tiles_n;
     const uint32_t split = blockIdx.x / total_tiles;
@@ -407,8 +411,8 @@ __global__ __launch_bounds__(QTH, 2) void gemm_q8_coalesced_kernel(
     const uint32_t m0 = tm * BM, n0 = tn * BN;
     const uint32_t nb = K >> 5;
     const uint32_t rb = nb * 34;
-    const uint32_t kb_begin = split * stages_per_split * KB;
-    const uint32_t kb_end = min(nb, kb_begin + stages_per_split * KB);
+    const uint32_t kb_begin = split * stages_per_split * QKB;
+    const uint32_t kb_end = min(nb, kb_begin + stages_per_split * QKB);
     float* Yout = Y + (ksplit > 1 ? size_t(split) * M * N : 0);
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -419,8 +423,8 @@ __global__ __launch_bounds__(QTH, 2) void gemm_q8_coalesced_kernel(
     // activation row, weight row and scale row: per-lane 32-bit offsets
     // (computed once) plus the stage's scalar offset.  Rows past M or N are
     // clamped to the last one.
-    constexpr int A_LOADS = QA_BYTES / 1024 / (QTH / 64);   // 4 per wave
-    constexpr int S_LOADS = QS_BYTES / 256 / (QTH / 64);    // 2 per wave
+    constexpr int A_LOADS = G::A_BYTES / 1024 / (QTH / 64);   // 4 per wave
+    constexpr int S_LOADS = G::S_BYTES / 256 / (QTH / 64);    // 2 per wave
     const __amdgpu_buffer_rsrc_t a_rsrc =
         __builtin_amdgcn_make_buffer_rsrc((void*)(XQ + size_t(m0) * K), 0, -1, kBufferWord3);
     const __amdgpu_buffer_rsrc_t w_rsrc =
@@ -431,19 +435,18 @@ __global__ __launch_bounds__(QTH, 2) void gemm_q8_coalesced_kernel(
 #pragma unroll
     for (int i = 0; i < A_LOADS; ++i) {
         const int unit = (wave * A_LOADS + i) * 64 + lane;  // physical 16 B slot
-        const int row = unit >> 4, col = (unit & 15) ^ (row & 15);
+        const int row = unit / G::UPR, col = (unit % G::UPR) ^ (row % G::UPR);
         a_off[i] = (min(m0 + row, M - 1) - m0) * K + col * 16;
     }
     // Weight dword loads: LDS dword p of the region holds raw dword d of row r
-    // (p = r*QW_STRIDE + QW_SHIFT*(r/8) + d); gap dwords load a harmless dword.
-    uint32_t w_off[QW_PER_WAVE];
+    // (p = r*G::W_STRIDE + d); gap dwords load a harmless dword.
+    uint32_t w_off[G::W_PER_WAVE];
 #pragma unroll
-    for (int i = 0; i < QW_PER_WAVE; ++i) {
+    for (int i = 0; i < G::W_PER_WAVE; ++i) {
         const uint32_t p = uint32_t((wave + 8 * i) * 64 + lane);
-        uint32_t r = min(p / QW_STRIDE, uint32_t(BN - 1));
-        if (p < r * QW_STRIDE + QW_SHIFT * (r >> 3) && r > 0) --r;
-        uint32_t d = p - (r * QW_STRIDE + QW_SHIFT * (r >> 3));
-        if (d >= uint32_t(QWD)) d = 0;
+        uint32_t r = min(p / G::W_STRIDE, uint32_t(BN - 1));
+        uint32_t d = p - r * G::W_STRIDE;
+        if (d >= uint32_t(G::WD)) d = 0;
         w_off[i] = (min(n0 + r, N - 1) - n0) * rb + d * 4;
     }
     uint32_t s_off[S_LOADS];
@@ -453,21 +456,21 @@ __global__ __launch_bounds__(QTH, 2) void gemm_q8_coalesced_kernel(
         s_off[i] = ((min(m0 + uint32_t(idx & (BM - 1)), M - 1) - m0) * nb + (idx >> 7)) * 4;
     }
     auto stage_in = [&](uint32_t kb, int buf) {
-        uint8_t* base = lds + buf * QBUF;
+        uint8_t* base = lds + buf * G::BUF;
 #pragma unroll
         for (int i = 0; i < A_LOADS; ++i)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_void*)(base + (wave * A_LOADS + i) * 1024), 16,
                                                      a_off[i], kb * 32, 0, 0);
 #pragma unroll
-        for (int i = 0; i < QW_PER_WAVE; ++i)
-            if (wave + 8 * i < QW_LOADS)  // wave-uniform
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_void*)(base + QA_BYTES + (wave + 8 * i) * 256), 4,
+        for (int i = 0; i < G::W_PER_WAVE; ++i)
+            if (wave + 8 * i < G::W_LOADS)  // wave-uniform
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_void*)(base + G::A_BYTES + (wave + 8 * i) * 256), 4,
                                                          w_off[i], kb * 34, 0, 0);
         if constexpr (!DOTS) {
 #pragma unroll
             for (int i = 0; i < S_LOADS; ++i)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    s_rsrc, (lds_void*)(base + QA_BYTES + QW_BYTES + (wave * S_LOADS + i) * 256), 4, s_off[i], kb * 4,
+                    s_rsrc, (lds_void*)(base + G::A_BYTES + G::W_BYTES + (wave * S_LOADS + i) * 256), 4, s_off[i], kb * 4,
                     0, 0);
         }
     };
@@ -482,7 +485,7 @@ __global__ __launch_bounds__(QTH, 2) void gemm_q8_coalesced_kernel(
 #pragma unroll
     for (int v = 0; v < 32; ++v) szero[v] = 0.0f;
     const uint32_t nrow = wn * 32 + l32;  // this lane's weight row within the tile
-    const uint32_t wrow = nrow * QW_STRIDE + QW_SHIFT * (nrow >> 3);  // its first LDS dword
+    const uint32_t wrow = nrow * G::W_STRIDE;  // its first LDS dword
 
     // LDS operands of one block, read one step ahead of their MFMAs.
     struct Ops {
@@ -492,17 +495,17 @@ __global__ __launch_bounds__(QTH, 2) void gemm_q8_coalesced_kernel(
         float dx;
     };
     auto read_ops = [&](const uint8_t* base, int b, int odd, Ops& o) {
-        const uint32_t* Bw = reinterpret_cast<const uint32_t*>(base + QA_BYTES) + wrow;
+        const uint32_t* Bw = reinterpret_cast<const uint32_t*>(base + G::A_BYTES) + wrow;
         const int off = (b * 34 + 2 + lh * 16) >> 2;
 #pragma unroll
         for (int i = 0; i < 4 + (odd ? 0 : 1); ++i) o.t[i] = Bw[off + i];
         o.dwh = reinterpret_cast<const uint16_t*>(Bw)[b * 17];
         o.dx = DOTS ? 0.0f
-                    : reinterpret_cast<const float*>(base + QA_BYTES + QW_BYTES)[b * BM + wm * 64 + lh * 32 + l32];
+                    : reinterpret_cast<const float*>(base + G::A_BYTES + G::W_BYTES)[b * BM + wm * 64 + lh * 32 + l32];
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            const int row = wm * 64 + i * 32 + l32, col = (b * 2 + lh) ^ (row & 15);
-            o.a[i] = *reinterpret_cast<const v4i*>(base + row * 256 + col * 16);
+            const int row = wm * 64 + i * 32 + l32, col = (b * 2 + lh) ^ (row % G::UPR);
+            o.a[i] = *reinterpret_cast<const v4i*>(base + row * (QKB * 32) + col * 16);
         }
     };
     // In-flight results of one block: the two tiles' int32 dots and, from one
@@ -539,25 +542,25 @@ __global__ __launch_bounds__(QTH, 2) void gemm_q8_coalesced_kernel(
 #endif
     stage_in(kb_begin, 0);
     int buf = 0;
-    for (uint32_t kb = kb_begin; kb < kb_end; kb += KB, buf ^= 1) {
+    for (uint32_t kb = kb_begin; kb < kb_end; kb += QKB, buf ^= 1) {
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's direct loads of stage kb landed
         __syncthreads();                     // ... and everyone's; the other buffer is free again
 #if ZQ_GEMM_DIAG & 2
-        if (kb == kb_begin && kb + KB < kb_end) stage_in(kb + KB, buf ^ 1);
+        if (kb == kb_begin && kb + QKB < kb_end) stage_in(kb + QKB, buf ^ 1);
 #else
-        if (kb + KB < kb_end) stage_in(kb + KB, buf ^ 1);
+        if (kb + QKB < kb_end) stage_in(kb + QKB, buf ^ 1);
 #endif
-        const uint8_t* base = lds + buf * QBUF;
+        const uint8_t* base = lds + buf * G::BUF;
         // Waves sharing a SIMD start the stage at different block pairs, so
         // one wave's MFMAs overlap the other's VALU epilogue instead of both
         // running the same phase in lockstep after the barrier.
-        const int rot = (wave & 1) * (KB / 2);
+        const int rot = (wave & 1) * (QKB / 2);
         if constexpr (DOTS) {
 #pragma unroll 1
-            for (int it = 0; it < KB; it += 2) {
+            for (int it = 0; it < QKB; it += 2) {
 #pragma unroll
                 for (int bp = 0; bp < 2; ++bp) {
-                    const int b = ((it + rot) & (KB - 1)) + bp;
+                    const int b = ((it + rot) & (QKB - 1)) + bp;
                     Ops o;
                     Blk r;
                     read_ops(base, b, bp, o);
@@ -582,11 +585,11 @@ __global__ __launch_bounds__(QTH, 2) void gemm_q8_coalesced_kernel(
             read_ops(base, rot + 1, 1, oo);
             issue(oe, 0, p);
 #pragma unroll 1
-            for (int it = 0; it < KB - 2; it += 2) {
-                read_ops(base, (it + 2 + rot) & (KB - 1), 0, oe);
+            for (int it = 0; it < QKB - 2; it += 2) {
+                read_ops(base, (it + 2 + rot) & (QKB - 1), 0, oe);
                 issue(oo, 1, q);
                 retire(p);
-                read_ops(base, (it + 3 + rot) & (KB - 1), 1, oo);
+                read_ops(base, (it + 3 + rot) & (QKB - 1), 1, oo);
                 issue(oe, 0, p);
                 retire(q);
             }
@@ -617,6 +620,21 @@ __global__ __launch_bounds__(QTH, 2) void gemm_q8_coalesced_kernel(
                __builtin_amdgcn_s_getreg((4 << 0) | (0 << 6) | (31 << 11));                    // HW_ID
     }
 #endif
+}
+
+template <bool DOTS>
+__global__ __launch_bounds__(QTH, 2) void gemm_q8_coalesced_kernel(
+    const uint8_t* __restrict__ W, const int8_t* __restrict__ XQ, const float* __restrict__ XS,
+    float* __restrict__ Y, int32_t* __restrict__ dots, uint32_t M, uint32_t N, uint32_t K, uint32_t tiles_m,
+    uint32_t tiles_n, uint32_t ksplit, uint32_t stages_per_split) {
+    gemm_q8_coalesced_body<DOTS, 8>(W, XQ, XS, Y, dots, M, N, K, tiles_m, tiles_n, ksplit, stages_per_split);
+}
+template <bool DOTS>
+__global__ __launch_bounds__(QTH, 4) void gemm_q8_coalesced4_kernel(
+    const uint8_t* __restrict__ W, const int8_t* __restrict__ XQ, const float* __restrict__ XS,
+    float* __restrict__ Y, int32_t* __restrict__ dots, uint32_t M, uint32_t N, uint32_t K, uint32_t tiles_m,
+    uint32_t tiles_n, uint32_t ksplit, uint32_t stages_per_split) {
+    gemm_q8_coalesced_body<DOTS, 4>(W, XQ, XS, Y, dots, M, N, K, tiles_m, tiles_n, ksplit, stages_per_split);
 }
 
 // ------------------------------------------------------- fp32 GEMM -------
@@ -705,12 +723,12 @@ hipError_t launch_quantize_acts(const float* X, int8_t* xq, float* xs, size_t M,
 
 // Split factor so the grid reaches about two workgroups per CU (the LDS
 // budget allows two), keeping at least two K stages per split.
-static uint32_t choose_ksplit(uint32_t tiles, uint32_t nb) {
+static uint32_t choose_ksplit(uint32_t tiles, uint32_t nb, uint32_t kb = KB) {
     static const int forced = [] {
         const char* e = getenv("ZQ_GEMM_KSPLIT");
         return e ? atoi(e) : 0;
     }();
-    const uint32_t stages = (nb + KB - 1) / KB;
+    const uint32_t stages = (nb + kb - 1) / kb;
     uint32_t ks = forced > 0 ? uint32_t(forced) : (512 + tiles - 1) / tiles;
     ks = std::max(1u, std::min(ks, std::max(1u, stages / 2)));
     return ks;
@@ -718,8 +736,21 @@ static uint32_t choose_ksplit(uint32_t tiles, uint32_t nb) {
 
 size_t gemm_i8_partial_bytes(size_t M, size_t N, size_t K) {
     const uint32_t tiles = uint32_t(((M + BM - 1) / BM) * ((N + BN - 1) / BN));
-    const uint32_t ks = choose_ksplit(tiles, uint32_t(K / 32));
+    // sized for either stage depth of the direct-load kernel (4 or 8 blocks)
+    const uint32_t ks = std::max(choose_ksplit(tiles, uint32_t(K / 32), 8), choose_ksplit(tiles, uint32_t(K / 32), 4));
     return ks > 1 ? size_t(ks) * M * N * sizeof(float) : 0;
+}
+
+// Blocks per K stage of the direct-load kernel (ZQ_GEMM_KB = 4 or 8).  4
+// (72 KB of LDS, two workgroups = 16 waves per CU) measured faster at every
+// M than 8 (144 KB, one workgroup): 531 vs 472 TOPS at M = 2048.
+static int coalesced_kb() {
+    static const int v = [] {
+        const char* e = getenv("ZQ_GEMM_KB");
+        const int k = e ? atoi(e) : 0;
+        return k == 8 ? 8 : 4;
+    }();
+    return v;
 }
 
 static hipError_t launch_i8_common(int fmt, const uint8_t* w, const int8_t* xq, const float* xs, float* Y,
@@ -741,11 +772,16 @@ static hipError_t launch_i8_common(int fmt, const uint8_t* w, const int8_t* xq, 
     // first row: 129 activation rows and 129 weight rows must stay below 2 GiB.
     const bool offsets_fit = size_t(BM + 1) * K < (size_t(1) << 31) && size_t(BN + 1) * (K / 32 * 34) < (size_t(1) << 31);
     const bool coalesced = !legacy && fmt == kQ8_0 && K % 256 == 0 && offsets_fit;
+    const int qkb = coalesced_kb();
+    const uint32_t cstages = (nb + qkb - 1) / qkb;
     if (dots) {
         const dim3 grid(tiles_m * tiles_n);
-        if (coalesced)
-            hipLaunchKernelGGL((gemm_q8_coalesced_kernel<true>), grid, dim3(QTH), 0, stream, w, xq, xs, Y, dots,
-                               m, n, k, tiles_m, tiles_n, 1u, stages);
+        if (coalesced && qkb == 4)
+            hipLaunchKernelGGL((gemm_q8_coalesced4_kernel<true>), grid, dim3(QTH), 2 * QStage<4>::BUF, stream, w, xq, xs, Y, dots,
+                               m, n, k, tiles_m, tiles_n, 1u, cstages);
+        else if (coalesced)
+            hipLaunchKernelGGL((gemm_q8_coalesced_kernel<true>), grid, dim3(QTH), 2 * QStage<8>::BUF, stream, w, xq, xs, Y, dots,
+                               m, n, k, tiles_m, tiles_n, 1u, cstages);
         else if (fmt == kQ8_0)
             hipLaunchKernelGGL((gemm_i8_kernel<kQ8_0, true>), grid, dim3(kThreads), 0, stream, w, xq, xs, Y, dots, m, n,
                                k, tiles_m, tiles_n, 1u, stages);
@@ -755,14 +791,18 @@ static hipError_t launch_i8_common(int fmt, const uint8_t* w, const int8_t* xq, 
         return hipGetLastError();
     }
     if (!xs || !Y) return hipErrorInvalidValue;
-    uint32_t ks = choose_ksplit(tiles_m * tiles_n, nb);
+    const uint32_t st = coalesced ? cstages : stages;
+    uint32_t ks = choose_ksplit(tiles_m * tiles_n, nb, coalesced ? uint32_t(qkb) : uint32_t(KB));
     if (ks > 1 && !partial) ks = 1;
-    const uint32_t spw = (stages + ks - 1) / ks;
-    ks = (stages + spw - 1) / spw;  // no empty splits
+    const uint32_t spw = (st + ks - 1) / ks;
+    ks = (st + spw - 1) / spw;  // no empty splits
     float* out = ks > 1 ? partial : Y;
     const dim3 grid(tiles_m * tiles_n * ks);
-    if (coalesced)
-        hipLaunchKernelGGL((gemm_q8_coalesced_kernel<false>), grid, dim3(QTH), 0, stream, w, xq, xs, out, dots, m,
+    if (coalesced && qkb == 4)
+        hipLaunchKernelGGL((gemm_q8_coalesced4_kernel<false>), grid, dim3(QTH), 2 * QStage<4>::BUF, stream, w, xq, xs, out, dots, m,
+                           n, k, tiles_m, tiles_n, ks, spw);
+    else if (coalesced)
+        hipLaunchKernelGGL((gemm_q8_coalesced_kernel<false>), grid, dim3(QTH), 2 * QStage<8>::BUF, stream, w, xq, xs, out, dots, m,
                            n, k, tiles_m, tiles_n, ks, spw);
     else if (fmt == kQ8_0)
         hipLaunchKernelGGL((gemm_i8_kernel<kQ8_0, false>), grid, dim3(kThreads), 0, stream, w, xq, xs, out, dots, m, n,
