@@ -186,6 +186,50 @@ __device__ __forceinline__ float q4_pair_dot(const uint32_t (&q)[9], const float
     return fmaf(d1, s1, d0 * s0);
 }
 
+// Q4_0 pair dot on the mixed-precision FMA.  A nibble n (0..15) placed in a
+// 16-bit half is the binary16 denormal n * 2^-24, exactly; v_fma_mix_f32 takes
+// it straight from either half of a register, so two elements cost one mask
+// (0x000F000F over a shifted word) and two FMAs, and the products n*2^-24*x
+// and their sums are the cvt+fma ones scaled by 2^-24, exactly.  The offset
+// is applied once per block: sum (n-8)*x = 2^24 * sum n*x*2^-24 - 8 * sum x,
+// with sum x of the lane's two blocks precomputed (x is fixed per lane).
+__device__ __forceinline__ float mix_lo(uint32_t pair, float x, float acc) {
+    return fmaf(float(__builtin_bit_cast(_Float16, uint16_t(pair))), x, acc);
+}
+__device__ __forceinline__ float mix_hi(uint32_t pair, float x, float acc) {
+    return fmaf(float(__builtin_bit_cast(_Float16, uint16_t(pair >> 16))), x, acc);
+}
+__device__ __forceinline__ float q4_block_nx(const uint32_t (&u)[4], const float* xv) {
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t a02 = u[i] & 0x000F000Fu, a13 = (u[i] >> 8) & 0x000F000Fu;
+        const uint32_t b02 = (u[i] >> 4) & 0x000F000Fu, b13 = (u[i] >> 12) & 0x000F000Fu;
+        s = mix_lo(a02, xv[4 * i], s);
+        s = mix_lo(a13, xv[4 * i + 1], s);
+        s = mix_hi(a02, xv[4 * i + 2], s);
+        s = mix_hi(a13, xv[4 * i + 3], s);
+        s = mix_lo(b02, xv[16 + 4 * i], s);
+        s = mix_lo(b13, xv[16 + 4 * i + 1], s);
+        s = mix_hi(b02, xv[16 + 4 * i + 2], s);
+        s = mix_hi(b13, xv[16 + 4 * i + 3], s);
+    }
+    return s;
+}
+__device__ __forceinline__ float q4_pair_dot_mix(const uint32_t (&q)[9], const float (&xv)[64], float sx0, float sx1) {
+    uint32_t a[4], b[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        a[i] = __builtin_amdgcn_alignbyte(q[i + 1], q[i], 2);
+        b[i] = q[5 + i];
+    }
+    const float s0 = fmaf(q4_block_nx(a, xv), 16777216.0f, -8.0f * sx0);
+    const float s1 = fmaf(q4_block_nx(b, xv + 32), 16777216.0f, -8.0f * sx1);
+    const float d0 = half_bits_to_float(q[0]);
+    const float d1 = half_bits_to_float(q[4] >> 16);
+    return fmaf(d1, s1, d0 * s0);
+}
+
 // Pair-lane kernel for Q8_0 (DW=17) and Q4_0 (DW=9).
 template <int FMT, int R>
 __global__ __launch_bounds__(kThreads) void gemv_pairs_kernel(TaskTable tt, const float* __restrict__ x,
@@ -514,6 +558,14 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_kernel(TaskTable tt, cons
             xv[4 * i] = xr[i].x; xv[4 * i + 1] = xr[i].y; xv[4 * i + 2] = xr[i].z; xv[4 * i + 3] = xr[i].w;
         }
     }
+    float sx0 = 0.0f, sx1 = 0.0f;  // Q4_0: sum of x over the lane's two blocks
+    if constexpr (FMT == kQ4_0) {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            sx0 += xv[i];
+            sx1 += xv[32 + i];
+        }
+    }
     ZQ_DIAG_MARK(1);
     int parity = 0;
     [[maybe_unused]] int diag_it = 0;
@@ -540,7 +592,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_kernel(TaskTable tt, cons
 #pragma unroll
                     for (int j = 0; j < DW; ++j) q[j] = active ? buf[r * WBUF + DW * lane + j] : 0u;
                     if constexpr (FMT == kQ8_0) acc[r] = q8_pair_dot(q, xv);
-                    else acc[r] = q4_pair_dot(q, xv);
+                    else acc[r] = q4_pair_dot_mix(q, xv, sx0, sx1);
                     acc[r] = wave_sum(acc[r]);
                 }
                 const GemvTask& t = tt.t[ti];
@@ -704,6 +756,11 @@ __global__ __launch_bounds__(NW * 64) void gemv_q6k_stream_kernel(TaskTable tt, 
         locate(min(blk, total_blocks - 1), rowp, row0, ti);
         load(rowp, u);
     }
+    float sxg[2][4];  // sum of x per 4-element group of the lane's two units
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) sxg[kk][g] = (xv[kk][g][0] + xv[kk][g][1]) + (xv[kk][g][2] + xv[kk][g][3]);
     int parity = 0;
     while (blk < total_blocks) {
 #pragma unroll
@@ -742,19 +799,23 @@ __global__ __launch_bounds__(NW * 64) void gemv_q6k_stream_kernel(TaskTable tt, 
                 const uint32_t sc0 = lds_u32(base + 192 + h * 8);
                 const uint32_t sc1 = lds_u32(base + 196 + h * 8);
                 const uint32_t dbits = uint32_t(bbytes[base + 208]) | (uint32_t(bbytes[base + 209]) << 8);
-                const float d = half_bits_to_float(dbits) * 0.25f;
+                const float d = half_bits_to_float(dbits);
                 const uint32_t shsel = l0 >> 4;
                 float part = 0.0f;
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
-                    uint32_t lo = (g & 1) ? qlB : qlA;
-                    if (g >= 2) lo >>= 4;
-                    lo &= 0x0F0F0F0Fu;
-                    const uint32_t hi = ((qh >> (2 * g)) & 0x03030303u) << 4;
-                    const uint32_t v = ((lo | hi) ^ 0x20202020u) << 2;  // 4*(q-32) per byte
-                    float sum = 0.0f;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) sum = fmaf(sbyte(v, e), xv[k][g][e], sum);
+                    // the 6-bit u = q + 32 of elements (0,2) and (1,3) as binary16
+                    // denormals u * 2^-24 into v_fma_mix_f32; sum (u-32)*x =
+                    // 2^24 * sum u*x*2^-24 - 32 * sum x
+                    const uint32_t src = ((g & 1) ? qlB : qlA) >> (g >= 2 ? 4 : 0);
+                    const uint32_t p02 = (src & 0x000F000Fu) | (((qh >> (2 * g)) & 0x00030003u) << 4);
+                    const uint32_t p13 = ((src >> 8) & 0x000F000Fu) | (((qh >> (2 * g + 8)) & 0x00030003u) << 4);
+                    float t = 0.0f;
+                    t = mix_lo(p02, xv[k][g][0], t);
+                    t = mix_lo(p13, xv[k][g][1], t);
+                    t = mix_hi(p02, xv[k][g][2], t);
+                    t = mix_hi(p13, xv[k][g][3], t);
+                    const float sum = fmaf(t, 16777216.0f, -32.0f * sxg[k][g]);
                     const float sc = sbyte(g < 2 ? sc0 : sc1, (2 * g + shsel) & 3);
                     part = fmaf(d * sc, sum, part);
                 }
