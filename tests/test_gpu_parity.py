@@ -191,7 +191,9 @@ def test_device_synth_matches_host_generator(zq, orc):
 
 # ----------------------------------------------------------------- GEMM ---
 @pytest.mark.parametrize("fmt,m,n,k", [(O.Q8_0, 3, 300, 4096), (O.Q8_0, 130, 257, 1024), (O.Q8_0, 32, 128, 14336),
-                                       (O.Q8_0, 2, 64, 192), (O.Q4_0, 17, 200, 4096), (O.Q4_0, 129, 130, 256)])
+                                       (O.Q8_0, 2, 64, 192), (O.Q4_0, 17, 200, 4096), (O.Q4_0, 129, 130, 256),
+                                       # 32-token tiles: ragged M and N with a K split; M = 33 takes the 128-token tile
+                                       (O.Q8_0, 31, 1000, 8192), (O.Q8_0, 33, 260, 2048)])
 def test_gemm_int8(zq, orc, fmt, m, n, k):
     w = orc.gen_weights(fmt, 300 + n, n, k)
     X = orc.gen_normal(301 + m, m * k)
@@ -211,9 +213,9 @@ def test_gemm_f32(zq, orc, fmt, m, n, k):
     zq.release(w)
 
 
-def test_gemm_full_size_sampled(zq, orc):
-    # config 2 at M = 2048, N x K = 14336 x 4096, int8 activations, device path
-    m, n, k = 2048, 14336, 4096
+@pytest.mark.parametrize("m,n,k", [(2048, 14336, 4096), (32, 4096, 14336)])
+def test_gemm_full_size_sampled(zq, orc, m, n, k):
+    # config 2 at M = 2048 and M = 32, int8 activations, device path
     wd = torch.zeros(zq.weight_bytes(O.Q8_0, n, k), dtype=torch.uint8, device=DEV)
     zq.synth_weights_dev(O.Q8_0, 81, wd, n, k)
     X = orc.gen_normal(82, m * k)

@@ -27,6 +27,7 @@
 #include "zq_internal.hpp"
 
 #include <algorithm>
+#include <cmath>
 #include <cstdlib>
 
 namespace zq {
@@ -370,20 +371,23 @@ constexpr int QTH = 512;
 // per CU; 4: 72 KB, two).  Weight row r starts at LDS dword r * W_STRIDE, an
 // odd stride, so the MFMA B reads (32 rows, one dword each) fall on distinct
 // banks: measured zero LDS bank conflicts for the whole kernel at 69.
-template <int QKB>
+template <int QKB, int BMT = BM, int NW = QTH / 64>
 struct QStage {
-    static constexpr int A_BYTES = BM * QKB * 32;           // activation tile
+    static constexpr int A_BYTES = BMT * QKB * 32;          // activation tile
     static constexpr int UPR = QKB * 2;                     // 16 B units per activation row
     static constexpr int WD = QKB * 34 / 4;                 // raw dwords of a weight row per stage
     static constexpr int W_STRIDE = WD | 1;                 // 69 / 35
     static constexpr int W_DWORDS = (BN - 1) * W_STRIDE + WD + 1;  // +1: the 5th dword read
     static constexpr int W_LOADS = (W_DWORDS + 63) / 64;   // 64-lane dword loads per stage
-    static constexpr int W_PER_WAVE = (W_LOADS + QTH / 64 - 1) / (QTH / 64);
+    static constexpr int W_PER_WAVE = (W_LOADS + NW - 1) / NW;
     static constexpr int W_BYTES = (W_LOADS * 64 * 4 + 15) / 16 * 16;
-    static constexpr int S_BYTES = QKB * BM * 4;
+    static constexpr int S_BYTES = QKB * BMT * 4;
+    static constexpr int S_UNITS = S_BYTES / 256;           // 64-lane dword loads of scales per stage
+    static constexpr int S_PER_WAVE = (S_UNITS + NW - 1) / NW;
     static constexpr int BUF = A_BYTES + W_BYTES + S_BYTES;  // bytes per stage buffer
     static_assert(2 * BUF <= 160 * 1024, "two stage buffers must fit the 160 KiB LDS");
-    static_assert(A_BYTES % 16 == 0 && W_BYTES % 16 == 0, "LDS regions stay 16 B aligned");
+    static_assert(A_BYTES % (1024 * NW) == 0, "activation units split evenly over the waves");
+    static_assert(S_BYTES % 256 == 0 && A_BYTES % 16 == 0 && W_BYTES % 16 == 0, "LDS regions stay 16 B aligned");
 };
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -392,23 +396,28 @@ typedef __attribute__((address_space(3))) void lds_void;
 // no swizzle, stride 0): offsets are plain byte offsets from the base.
 constexpr int kBufferWord3 = 0x00020000;
 
-// The kernel body, one instantiation per stage depth; the __global__
-// wrappers below carry the launch bounds (second argument: minimum waves per
-// SIMD -- 4 lets two 8-wave workgroups share a CU when 4-block stages leave
-// LDS for both).
-template <bool DOTS, int QKB>
+// The kernel body, one instantiation per stage depth QKB and per tile height:
+// WM = 2 is the 128-token tile above (8 waves in 2 x 4, two 32x32 MFMA tiles
+// each); WM = 1 is a 32-token tile for small M (4 waves side by side, one
+// MFMA tile each), where the scale products of a pair of K blocks come from
+// one 2-block outer-product MFMA (block i = lane half i = K block 2j + i).
+// The __global__ wrappers below carry the launch bounds (second argument:
+// minimum waves per SIMD).
+template <bool DOTS, int QKB, int WM = 2>
 __device__ __forceinline__ void gemm_q8_coalesced_body(
     const uint8_t* __restrict__ W, const int8_t* __restrict__ XQ, const float* __restrict__ XS,
     float* __restrict__ Y, int32_t* __restrict__ dots, uint32_t M, uint32_t N, uint32_t K, uint32_t tiles_m,
     uint32_t tiles_n, uint32_t ksplit, uint32_t stages_per_split) {
-    using G = QStage<QKB>;
+    constexpr int BMT = WM == 2 ? BM : 32;  // tokens per tile
+    constexpr int NW = WM == 2 ? 8 : 4;     // waves per workgroup
+    using G = QStage<QKB, BMT, NW>;
     extern __shared__ __align__(16) uint8_t lds[];  // 2 * G::BUF bytes, sized at launch
 
     const uint32_t total_tiles = tiles_m * tiles_n;
     const uint32_t split = blockIdx.x / total_tiles;
     uint32_t tm, tn;
     tile_of(tiles_m, tiles_n, blockIdx.x % total_tiles, tm, tn);
-    const uint32_t m0 = tm * BM, n0 = tn * BN;
+    const uint32_t m0 = tm * BMT, n0 = tn * BN;
     const uint32_t nb = K >> 5;
     const uint32_t rb = nb * 34;
     const uint32_t kb_begin = split * stages_per_split * QKB;
@@ -416,15 +425,14 @@ __device__ __forceinline__ void gemm_q8_coalesced_body(
     float* Yout = Y + (ksplit > 1 ? size_t(split) * M * N : 0);
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 2, wn = wave & 3;
+    const int wm = WM == 2 ? wave >> 2 : 0, wn = wave & 3;
     const int l32 = lane & 31, lh = lane >> 5;
 
     // Direct loads go through buffer resources based at this tile's first
     // activation row, weight row and scale row: per-lane 32-bit offsets
     // (computed once) plus the stage's scalar offset.  Rows past M or N are
     // clamped to the last one.
-    constexpr int A_LOADS = G::A_BYTES / 1024 / (QTH / 64);   // 4 per wave
-    constexpr int S_LOADS = G::S_BYTES / 256 / (QTH / 64);    // 2 per wave
+    constexpr int A_LOADS = G::A_BYTES / 1024 / NW;
     const __amdgpu_buffer_rsrc_t a_rsrc =
         __builtin_amdgcn_make_buffer_rsrc((void*)(XQ + size_t(m0) * K), 0, -1, kBufferWord3);
     const __amdgpu_buffer_rsrc_t w_rsrc =
@@ -443,17 +451,17 @@ __device__ __forceinline__ void gemm_q8_coalesced_body(
     uint32_t w_off[G::W_PER_WAVE];
 #pragma unroll
     for (int i = 0; i < G::W_PER_WAVE; ++i) {
-        const uint32_t p = uint32_t((wave + 8 * i) * 64 + lane);
+        const uint32_t p = uint32_t((wave + NW * i) * 64 + lane);
         uint32_t r = min(p / G::W_STRIDE, uint32_t(BN - 1));
         uint32_t d = p - r * G::W_STRIDE;
         if (d >= uint32_t(G::WD)) d = 0;
         w_off[i] = (min(n0 + r, N - 1) - n0) * rb + d * 4;
     }
-    uint32_t s_off[S_LOADS];
+    uint32_t s_off[G::S_PER_WAVE];
 #pragma unroll
-    for (int i = 0; i < S_LOADS; ++i) {
-        const int idx = (wave * S_LOADS + i) * 64 + lane;  // = b * 128 + m
-        s_off[i] = ((min(m0 + uint32_t(idx & (BM - 1)), M - 1) - m0) * nb + (idx >> 7)) * 4;
+    for (int i = 0; i < G::S_PER_WAVE; ++i) {
+        const int idx = (wave * G::S_PER_WAVE + i) * 64 + lane;  // = b * BMT + m
+        s_off[i] = ((min(m0 + uint32_t(idx % BMT), M - 1) - m0) * nb + uint32_t(idx / BMT)) * 4;
     }
     auto stage_in = [&](uint32_t kb, int buf) {
         uint8_t* base = lds + buf * G::BUF;
@@ -463,21 +471,22 @@ __device__ __forceinline__ void gemm_q8_coalesced_body(
                                                      a_off[i], kb * 32, 0, 0);
 #pragma unroll
         for (int i = 0; i < G::W_PER_WAVE; ++i)
-            if (wave + 8 * i < G::W_LOADS)  // wave-uniform
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_void*)(base + G::A_BYTES + (wave + 8 * i) * 256), 4,
+            if (wave + NW * i < G::W_LOADS)  // wave-uniform
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_void*)(base + G::A_BYTES + (wave + NW * i) * 256), 4,
                                                          w_off[i], kb * 34, 0, 0);
         if constexpr (!DOTS) {
 #pragma unroll
-            for (int i = 0; i < S_LOADS; ++i)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    s_rsrc, (lds_void*)(base + G::A_BYTES + G::W_BYTES + (wave * S_LOADS + i) * 256), 4, s_off[i], kb * 4,
-                    0, 0);
+            for (int i = 0; i < G::S_PER_WAVE; ++i)
+                if (wave * G::S_PER_WAVE + i < G::S_UNITS)  // wave-uniform
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                        s_rsrc, (lds_void*)(base + G::A_BYTES + G::W_BYTES + (wave * G::S_PER_WAVE + i) * 256), 4,
+                        s_off[i], kb * 4, 0, 0);
         }
     };
 
-    v16f acc[2];
+    v16f acc[WM];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < WM; ++i)
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[i][v] = 0.0f;
     const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
@@ -489,7 +498,7 @@ __device__ __forceinline__ void gemm_q8_coalesced_body(
 
     // LDS operands of one block, read one step ahead of their MFMAs.
     struct Ops {
-        v4i a[2];
+        v4i a[WM];
         uint32_t t[5];  // raw weight dwords (4 used for odd blocks)
         uint32_t dwh;   // fp16 weight scale bits
         float dx;
@@ -499,40 +508,55 @@ __device__ __forceinline__ void gemm_q8_coalesced_body(
         const int off = (b * 34 + 2 + lh * 16) >> 2;
 #pragma unroll
         for (int i = 0; i < 4 + (odd ? 0 : 1); ++i) o.t[i] = Bw[off + i];
-        o.dwh = reinterpret_cast<const uint16_t*>(Bw)[b * 17];
-        o.dx = DOTS ? 0.0f
-                    : reinterpret_cast<const float*>(base + G::A_BYTES + G::W_BYTES)[b * BM + wm * 64 + lh * 32 + l32];
+        // WM = 2: scales of block b (lane half = tile); WM = 1: of block
+        // b - 1 + lh for the odd block of a pair (the even block needs none)
+        const int sb = WM == 2 ? b : b - 1 + lh;
+        o.dwh = WM == 2 || odd ? reinterpret_cast<const uint16_t*>(Bw)[sb * 17] : 0u;
+        o.dx = DOTS || (WM == 1 && !odd)
+                   ? 0.0f
+                   : reinterpret_cast<const float*>(base + G::A_BYTES + G::W_BYTES)[WM == 2 ? b * BMT + wm * 64 + lh * 32 + l32
+                                                                                         : sb * BMT + l32];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < WM; ++i) {
             const int row = wm * 64 + i * 32 + l32, col = (b * 2 + lh) ^ (row % G::UPR);
             o.a[i] = *reinterpret_cast<const v4i*>(base + row * (QKB * 32) + col * 16);
         }
     };
-    // In-flight results of one block: the two tiles' int32 dots and, from one
-    // 2-block outer-product MFMA (block i = lane half i: dx of tile i's rows
-    // times dw of the wave's columns), both tiles' dx*dw in the same layout.
+    // In-flight results of one block: the tiles' int32 dots and, from one
+    // 2-block outer-product MFMA, the dx*dw products in the same layout.  WM =
+    // 2: block i of the product = tile i of this K block.  WM = 1: issued with
+    // the odd block of a pair, block i = K block 2j + i of the single tile.
     struct Blk {
-        v16i c[2];
+        v16i c[WM];
         v32f s;
     };
     auto issue = [&](const Ops& o, int odd, Blk& r) {
+        if constexpr (!DOTS && WM == 1)  // first, so the even block's retire finds it done
+            if (odd) r.s = __builtin_amdgcn_mfma_f32_32x32x1f32(o.dx, half_bits_to_float(uint16_t(o.dwh)), szero, 0, 0, 0);
         v4i w;
 #pragma unroll
         for (int i = 0; i < 4; ++i) w[i] = odd ? int(o.t[i]) : int(__builtin_amdgcn_alignbyte(o.t[i + 1], o.t[i], 2));
 #pragma unroll
-        for (int i = 0; i < 2; ++i) r.c[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a[i], w, zero, 0, 0, 0);
-        if constexpr (!DOTS)
+        for (int i = 0; i < WM; ++i) r.c[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a[i], w, zero, 0, 0, 0);
+        if constexpr (!DOTS && WM == 2)
             r.s = __builtin_amdgcn_mfma_f32_32x32x1f32(o.dx, half_bits_to_float(uint16_t(o.dwh)), szero, 0, 0, 0);
     };
-    auto retire = [&](const Blk& r) {
+    // Accumulates block r; sc/half name its dx*dw products (WM = 1: the pair's
+    // odd block and this block's half of it; WM = 2: r itself).
+    auto retire = [&](const Blk& r, const Blk& sc, int half) {
 #if ZQ_GEMM_DIAG & 1
 #pragma unroll
-        for (int i = 0; i < 2; ++i) acc[i][0] = fmaf(float(r.c[i][0] ^ r.c[i][15]), r.s[16 * i] + r.s[16 * i + 15], acc[i][0]);
+        for (int i = 0; i < WM; ++i) acc[i][0] = fmaf(float(r.c[i][0] ^ r.c[i][15]), r.s[16 * i] + r.s[16 * i + 15], acc[i][0]);
 #else
+        if constexpr (WM == 2) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < 2; ++i)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) acc[i][v] = fmaf(float(r.c[i][v]), r.s[16 * i + v], acc[i][v]);
+                for (int v = 0; v < 16; ++v) acc[i][v] = fmaf(float(r.c[i][v]), r.s[16 * i + v], acc[i][v]);
+        } else {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[0][v] = fmaf(float(r.c[0][v]), sc.s[16 * half + v], acc[0][v]);
+        }
 #endif
     };
 
@@ -567,7 +591,7 @@ __device__ __forceinline__ void gemm_q8_coalesced_body(
                     issue(o, bp, r);
                     const uint32_t n = n0 + nrow;
 #pragma unroll
-                    for (int i = 0; i < 2; ++i)
+                    for (int i = 0; i < WM; ++i)
 #pragma unroll
                         for (int v = 0; v < 16; ++v) {
                             const uint32_t m = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
@@ -588,20 +612,20 @@ __device__ __forceinline__ void gemm_q8_coalesced_body(
             for (int it = 0; it < QKB - 2; it += 2) {
                 read_ops(base, (it + 2 + rot) & (QKB - 1), 0, oe);
                 issue(oo, 1, q);
-                retire(p);
+                retire(p, q, 0);
                 read_ops(base, (it + 3 + rot) & (QKB - 1), 1, oo);
                 issue(oe, 0, p);
-                retire(q);
+                retire(q, q, 1);
             }
             issue(oo, 1, q);
-            retire(p);
-            retire(q);
+            retire(p, q, 0);
+            retire(q, q, 1);
         }
     }
     if constexpr (DOTS) return;
     const uint32_t n = n0 + nrow;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < WM; ++i)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
             const uint32_t m = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
@@ -612,7 +636,7 @@ __device__ __forceinline__ void gemm_q8_coalesced_body(
     // of this workgroup, written past the end of Y
     __syncthreads();
     if (tid == 0) {
-        uint64_t* o = reinterpret_cast<uint64_t*>(Yout + size_t(M) * N) + 4 * blockIdx.x;  // caller over-allocates Y
+        uint64_t* o = reinterpret_cast<uint64_t*>(Y + size_t(ksplit) * M * N) + 4 * blockIdx.x;  // caller over-allocates Y (or the split-K workspace)
         o[0] = diag_t0;
         o[1] = __builtin_amdgcn_s_memrealtime();
         o[2] = __builtin_amdgcn_s_memtime() - diag_c0;
@@ -635,6 +659,15 @@ __global__ __launch_bounds__(QTH, 4) void gemm_q8_coalesced4_kernel(
     float* __restrict__ Y, int32_t* __restrict__ dots, uint32_t M, uint32_t N, uint32_t K, uint32_t tiles_m,
     uint32_t tiles_n, uint32_t ksplit, uint32_t stages_per_split) {
     gemm_q8_coalesced_body<DOTS, 4>(W, XQ, XS, Y, dots, M, N, K, tiles_m, tiles_n, ksplit, stages_per_split);
+}
+// 32-token tiles, 4 waves; 4-block stages (45 KB of LDS for both buffers) so
+// three workgroups share a CU.
+template <bool DOTS>
+__global__ __launch_bounds__(256, 3) void gemm_q8_small_kernel(
+    const uint8_t* __restrict__ W, const int8_t* __restrict__ XQ, const float* __restrict__ XS,
+    float* __restrict__ Y, int32_t* __restrict__ dots, uint32_t M, uint32_t N, uint32_t K, uint32_t tiles_m,
+    uint32_t tiles_n, uint32_t ksplit, uint32_t stages_per_split) {
+    gemm_q8_coalesced_body<DOTS, 4, 1>(W, XQ, XS, Y, dots, M, N, K, tiles_m, tiles_n, ksplit, stages_per_split);
 }
 
 // ------------------------------------------------------- fp32 GEMM -------
@@ -734,10 +767,47 @@ static uint32_t choose_ksplit(uint32_t tiles, uint32_t nb, uint32_t kb = KB) {
     return ks;
 }
 
+// Split factor of the 4-block direct-load kernels, from a cost model fitted
+// to their measured times over M = 32..2048 at 14336x4096 and 4096x14336:
+// one K stage of a tile takes `alone` us for a workgroup alone on its CU and
+// `shared` us x L when L workgroups share a CU (or queue for it) -- 2.5 and
+// 2.0 for the 128-token tile; a split factor ks > 1 adds the partial sums'
+// write and read (8 B per output per split at about 6 TB/s) and the reduce
+// launch (about 3 us).  Among equal costs the smaller split wins.
+struct StageCost {
+    double alone, shared;
+};
+constexpr StageCost kTileCost{2.5, 2.0};
+constexpr StageCost kSmallTileCost{1.0, 0.6};
+static uint32_t choose_ksplit_model(uint32_t tiles, uint32_t stages, size_t M, size_t N, StageCost c = kTileCost) {
+    static const int forced = [] {
+        const char* e = getenv("ZQ_GEMM_KSPLIT");
+        return e ? atoi(e) : 0;
+    }();
+    if (forced > 0) return std::max(1u, std::min(uint32_t(forced), stages));
+    const double cus = double(device_cu_count());
+    uint32_t best = 1;
+    double best_t = 1e300;
+    for (uint32_t ks = 1; ks <= std::min(stages, 32u); ++ks) {
+        const uint32_t spw = (stages + ks - 1) / ks;
+        if ((stages + spw - 1) / spw != ks) continue;  // would leave empty splits
+        const double L = std::ceil(double(tiles) * ks / cus);
+        double t = spw * (L <= 1.0 ? c.alone : c.shared * L);
+        if (ks > 1) t += double(ks) * double(M) * double(N) * 8.0 / 6.0e6 + 3.0;
+        if (t < best_t) best_t = t, best = ks;
+    }
+    return best;
+}
+
 size_t gemm_i8_partial_bytes(size_t M, size_t N, size_t K) {
     const uint32_t tiles = uint32_t(((M + BM - 1) / BM) * ((N + BN - 1) / BN));
-    // sized for either stage depth of the direct-load kernel (4 or 8 blocks)
-    const uint32_t ks = std::max(choose_ksplit(tiles, uint32_t(K / 32), 8), choose_ksplit(tiles, uint32_t(K / 32), 4));
+    const uint32_t nb = uint32_t(K / 32);
+    // sized for every kernel choice: either stage depth of the direct-load
+    // kernel (4 or 8 blocks) and the staged-conversion kernel
+    const uint32_t small_tiles = uint32_t(((M + 31) / 32) * ((N + BN - 1) / BN));
+    const uint32_t ks = std::max({choose_ksplit(tiles, nb, 8), choose_ksplit(tiles, nb, 4),
+                                  choose_ksplit_model(tiles, (nb + 3) / 4, M, N),
+                                  choose_ksplit_model(small_tiles, (nb + 3) / 4, M, N, kSmallTileCost)});
     return ks > 1 ? size_t(ks) * M * N * sizeof(float) : 0;
 }
 
@@ -749,6 +819,16 @@ static int coalesced_kb() {
         const char* e = getenv("ZQ_GEMM_KB");
         const int k = e ? atoi(e) : 0;
         return k == 8 ? 8 : 4;
+    }();
+    return v;
+}
+
+// Largest M that takes the 32-token tile (ZQ_GEMM_SMALL_M, default 32; 0
+// turns it off).
+static size_t small_m_limit() {
+    static const size_t v = [] {
+        const char* e = getenv("ZQ_GEMM_SMALL_M");
+        return e ? size_t(atoi(e)) : size_t(32);
     }();
     return v;
 }
@@ -774,6 +854,27 @@ static hipError_t launch_i8_common(int fmt, const uint8_t* w, const int8_t* xq, 
     const bool coalesced = !legacy && fmt == kQ8_0 && K % 256 == 0 && offsets_fit;
     const int qkb = coalesced_kb();
     const uint32_t cstages = (nb + qkb - 1) / qkb;
+    if (coalesced && M <= small_m_limit()) {
+        const uint32_t stm = uint32_t((M + 31) / 32), sst = (nb + 3) / 4;
+        constexpr size_t kSmallLds = 2 * QStage<4, 32, 4>::BUF;
+        if (dots) {
+            hipLaunchKernelGGL((gemm_q8_small_kernel<true>), dim3(stm * tiles_n), dim3(256), kSmallLds,
+                               stream, w, xq, xs, Y, dots, m, n, k, stm, tiles_n, 1u, sst);
+            return hipGetLastError();
+        }
+        if (!xs || !Y) return hipErrorInvalidValue;
+        uint32_t ks = partial ? choose_ksplit_model(stm * tiles_n, sst, M, N, kSmallTileCost) : 1u;
+        const uint32_t spw = (sst + ks - 1) / ks;
+        ks = (sst + spw - 1) / spw;
+        hipLaunchKernelGGL((gemm_q8_small_kernel<false>), dim3(stm * tiles_n * ks), dim3(256), kSmallLds,
+                           stream, w, xq, xs, ks > 1 ? partial : Y, dots, m, n, k, stm, tiles_n, ks, spw);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess || ks == 1) return e;
+        const size_t total = M * N;
+        hipLaunchKernelGGL(splitk_reduce_kernel, dim3(static_cast<uint32_t>((total + kThreads - 1) / kThreads)),
+                           dim3(kThreads), 0, stream, partial, Y, total, ks);
+        return hipGetLastError();
+    }
     if (dots) {
         const dim3 grid(tiles_m * tiles_n);
         if (coalesced && qkb == 4)
@@ -792,7 +893,8 @@ static hipError_t launch_i8_common(int fmt, const uint8_t* w, const int8_t* xq, 
     }
     if (!xs || !Y) return hipErrorInvalidValue;
     const uint32_t st = coalesced ? cstages : stages;
-    uint32_t ks = choose_ksplit(tiles_m * tiles_n, nb, coalesced ? uint32_t(qkb) : uint32_t(KB));
+    uint32_t ks = coalesced && qkb == 4 ? choose_ksplit_model(tiles_m * tiles_n, st, M, N)
+                                        : choose_ksplit(tiles_m * tiles_n, nb, coalesced ? uint32_t(qkb) : uint32_t(KB));
     if (ks > 1 && !partial) ks = 1;
     const uint32_t spw = (st + ks - 1) / ks;
     ks = (st + spw - 1) / spw;  // no empty splits

@@ -1384,6 +1384,8 @@ hipError_t launch_blocks(TaskTable& tt, const float* x, uint32_t cols, hipStream
 
 }  // namespace
 
+int device_cu_count() { return cu_count(); }
+
 hipError_t launch_gemv(int fmt, const GemvTask* tasks, int count, const float* x, size_t cols,
                        hipStream_t stream) {
     if (count < 1 || count > kMaxTasks || !x || !row_bytes(fmt, cols) || cols > (1u << 24))

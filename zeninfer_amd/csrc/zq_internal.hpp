@@ -54,6 +54,8 @@ hipError_t launch_quantize_acts(const float* X, int8_t* xq, float* xs, size_t M,
 // Y is token-major [M][N].  `partial` (gemm_i8_partial_bytes, may be 0) is
 // the split-K workspace; with partial == nullptr the GEMM runs unsplit.
 size_t gemm_i8_partial_bytes(size_t M, size_t N, size_t K);
+// Compute units of the current device (256 on MI355X; 256 if the query fails).
+int device_cu_count();
 hipError_t launch_gemm_i8(int fmt, const uint8_t* w, const int8_t* xq, const float* xs,
                           float* Y, float* partial, size_t M, size_t N, size_t K, hipStream_t stream);
 
