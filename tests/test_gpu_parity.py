@@ -74,7 +74,9 @@ def test_quantize_acts_bit_exact(zq, orc):
 
 
 @pytest.mark.parametrize("fmt,m,n,k", [(O.Q8_0, 5, 37, 256), (O.Q8_0, 130, 131, 192), (O.Q8_0, 1, 128, 4096),
-                                       (O.Q4_0, 7, 70, 320), (O.Q4_0, 129, 3, 128)])
+                                       (O.Q4_0, 7, 70, 320), (O.Q4_0, 129, 3, 128),
+                                       # direct-load kernels for Q4_0 (K % 256 == 0): 32- and 128-token tiles
+                                       (O.Q4_0, 9, 33, 1024), (O.Q4_0, 40, 70, 512)])
 def test_block_dots_bit_exact(zq, orc, fmt, m, n, k):
     w = orc.gen_weights(fmt, 3 + n, n, k)
     x = orc.gen_normal(4 + m, m * k)
@@ -193,7 +195,8 @@ def test_device_synth_matches_host_generator(zq, orc):
 @pytest.mark.parametrize("fmt,m,n,k", [(O.Q8_0, 3, 300, 4096), (O.Q8_0, 130, 257, 1024), (O.Q8_0, 32, 128, 14336),
                                        (O.Q8_0, 2, 64, 192), (O.Q4_0, 17, 200, 4096), (O.Q4_0, 129, 130, 256),
                                        # 32-token tiles: ragged M and N with a K split; M = 33 takes the 128-token tile
-                                       (O.Q8_0, 31, 1000, 8192), (O.Q8_0, 33, 260, 2048)])
+                                       (O.Q8_0, 31, 1000, 8192), (O.Q8_0, 33, 260, 2048),
+                                       (O.Q4_0, 31, 700, 8192), (O.Q4_0, 150, 300, 2048)])
 def test_gemm_int8(zq, orc, fmt, m, n, k):
     w = orc.gen_weights(fmt, 300 + n, n, k)
     X = orc.gen_normal(301 + m, m * k)

@@ -371,11 +371,11 @@ constexpr int QTH = 512;
 // per CU; 4: 72 KB, two).  Weight row r starts at LDS dword r * W_STRIDE, an
 // odd stride, so the MFMA B reads (32 rows, one dword each) fall on distinct
 // banks: measured zero LDS bank conflicts for the whole kernel at 69.
-template <int QKB, int BMT = BM, int NW = QTH / 64>
+template <int QKB, int BMT = BM, int NW = QTH / 64, int BB = 34>
 struct QStage {
     static constexpr int A_BYTES = BMT * QKB * 32;          // activation tile
     static constexpr int UPR = QKB * 2;                     // 16 B units per activation row
-    static constexpr int WD = QKB * 34 / 4;                 // raw dwords of a weight row per stage
+    static constexpr int WD = QKB * BB / 4;                 // raw dwords of a weight row per stage (BB = block bytes)
     static constexpr int W_STRIDE = WD | 1;                 // 69 / 35
     static constexpr int W_DWORDS = (BN - 1) * W_STRIDE + WD + 1;  // +1: the 5th dword read
     static constexpr int W_LOADS = (W_DWORDS + 63) / 64;   // 64-lane dword loads per stage
@@ -403,14 +403,16 @@ constexpr int kBufferWord3 = 0x00020000;
 // one 2-block outer-product MFMA (block i = lane half i = K block 2j + i).
 // The __global__ wrappers below carry the launch bounds (second argument:
 // minimum waves per SIMD).
-template <bool DOTS, int QKB, int WM = 2>
-__device__ __forceinline__ void gemm_q8_coalesced_body(
+template <int FMT, bool DOTS, int QKB, int WM = 2>
+__device__ __forceinline__ void gemm_i8_direct_body(
     const uint8_t* __restrict__ W, const int8_t* __restrict__ XQ, const float* __restrict__ XS,
     float* __restrict__ Y, int32_t* __restrict__ dots, uint32_t M, uint32_t N, uint32_t K, uint32_t tiles_m,
     uint32_t tiles_n, uint32_t ksplit, uint32_t stages_per_split) {
     constexpr int BMT = WM == 2 ? BM : 32;  // tokens per tile
     constexpr int NW = WM == 2 ? 8 : 4;     // waves per workgroup
-    using G = QStage<QKB, BMT, NW>;
+    constexpr int BB = FMT == kQ8_0 ? 34 : 18;  // block bytes: fp16 d + 32 int8 / 16 nibble bytes
+    static_assert(FMT == kQ8_0 || FMT == kQ4_0, "int8-activation formats only");
+    using G = QStage<QKB, BMT, NW, BB>;
     extern __shared__ __align__(16) uint8_t lds[];  // 2 * G::BUF bytes, sized at launch
 
     const uint32_t total_tiles = tiles_m * tiles_n;
@@ -419,7 +421,7 @@ __device__ __forceinline__ void gemm_q8_coalesced_body(
     tile_of(tiles_m, tiles_n, blockIdx.x % total_tiles, tm, tn);
     const uint32_t m0 = tm * BMT, n0 = tn * BN;
     const uint32_t nb = K >> 5;
-    const uint32_t rb = nb * 34;
+    const uint32_t rb = nb * BB;
     const uint32_t kb_begin = split * stages_per_split * QKB;
     const uint32_t kb_end = min(nb, kb_begin + stages_per_split * QKB);
     float* Yout = Y + (ksplit > 1 ? size_t(split) * M * N : 0);
@@ -473,7 +475,7 @@ __device__ __forceinline__ void gemm_q8_coalesced_body(
         for (int i = 0; i < G::W_PER_WAVE; ++i)
             if (wave + NW * i < G::W_LOADS)  // wave-uniform
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_void*)(base + G::A_BYTES + (wave + NW * i) * 256), 4,
-                                                         w_off[i], kb * 34, 0, 0);
+                                                         w_off[i], kb * BB, 0, 0);
         if constexpr (!DOTS) {
 #pragma unroll
             for (int i = 0; i < G::S_PER_WAVE; ++i)
@@ -505,13 +507,15 @@ __device__ __forceinline__ void gemm_q8_coalesced_body(
     };
     auto read_ops = [&](const uint8_t* base, int b, int odd, Ops& o) {
         const uint32_t* Bw = reinterpret_cast<const uint32_t*>(base + G::A_BYTES) + wrow;
-        const int off = (b * 34 + 2 + lh * 16) >> 2;
+        // Q8_0: lane half lh takes quant bytes lh*16..+15; Q4_0: both halves
+        // read the 16 nibble bytes (low nibbles = elements 0-15, high 16-31)
+        const int off = (b * BB + 2 + (FMT == kQ8_0 ? lh * 16 : 0)) >> 2;
 #pragma unroll
         for (int i = 0; i < 4 + (odd ? 0 : 1); ++i) o.t[i] = Bw[off + i];
         // WM = 2: scales of block b (lane half = tile); WM = 1: of block
         // b - 1 + lh for the odd block of a pair (the even block needs none)
         const int sb = WM == 2 ? b : b - 1 + lh;
-        o.dwh = WM == 2 || odd ? reinterpret_cast<const uint16_t*>(Bw)[sb * 17] : 0u;
+        o.dwh = WM == 2 || odd ? reinterpret_cast<const uint16_t*>(Bw)[sb * (BB / 2)] : 0u;
         o.dx = DOTS || (WM == 1 && !odd)
                    ? 0.0f
                    : reinterpret_cast<const float*>(base + G::A_BYTES + G::W_BYTES)[WM == 2 ? b * BMT + wm * 64 + lh * 32 + l32
@@ -536,6 +540,13 @@ __device__ __forceinline__ void gemm_q8_coalesced_body(
         v4i w;
 #pragma unroll
         for (int i = 0; i < 4; ++i) w[i] = odd ? int(o.t[i]) : int(__builtin_amdgcn_alignbyte(o.t[i + 1], o.t[i], 2));
+        if constexpr (FMT == kQ4_0) {
+            // nibble u of this lane half -> int8 u - 8, per byte without carries:
+            // u + 0x78 stays below 0x100, and flipping bit 7 subtracts 0x80
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                w[i] = int(((uint32_t(w[i]) >> (4 * lh)) & 0x0F0F0F0Fu) + 0x78787878u) ^ int(0x80808080u);
+        }
 #pragma unroll
         for (int i = 0; i < WM; ++i) r.c[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a[i], w, zero, 0, 0, 0);
         if constexpr (!DOTS && WM == 2)
@@ -646,28 +657,28 @@ __device__ __forceinline__ void gemm_q8_coalesced_body(
 #endif
 }
 
-template <bool DOTS>
-__global__ __launch_bounds__(QTH, 2) void gemm_q8_coalesced_kernel(
+template <int FMT, bool DOTS>
+__global__ __launch_bounds__(QTH, 2) void gemm_i8_direct8_kernel(
     const uint8_t* __restrict__ W, const int8_t* __restrict__ XQ, const float* __restrict__ XS,
     float* __restrict__ Y, int32_t* __restrict__ dots, uint32_t M, uint32_t N, uint32_t K, uint32_t tiles_m,
     uint32_t tiles_n, uint32_t ksplit, uint32_t stages_per_split) {
-    gemm_q8_coalesced_body<DOTS, 8>(W, XQ, XS, Y, dots, M, N, K, tiles_m, tiles_n, ksplit, stages_per_split);
+    gemm_i8_direct_body<FMT, DOTS, 8>(W, XQ, XS, Y, dots, M, N, K, tiles_m, tiles_n, ksplit, stages_per_split);
 }
-template <bool DOTS>
-__global__ __launch_bounds__(QTH, 4) void gemm_q8_coalesced4_kernel(
+template <int FMT, bool DOTS>
+__global__ __launch_bounds__(QTH, 4) void gemm_i8_direct4_kernel(
     const uint8_t* __restrict__ W, const int8_t* __restrict__ XQ, const float* __restrict__ XS,
     float* __restrict__ Y, int32_t* __restrict__ dots, uint32_t M, uint32_t N, uint32_t K, uint32_t tiles_m,
     uint32_t tiles_n, uint32_t ksplit, uint32_t stages_per_split) {
-    gemm_q8_coalesced_body<DOTS, 4>(W, XQ, XS, Y, dots, M, N, K, tiles_m, tiles_n, ksplit, stages_per_split);
+    gemm_i8_direct_body<FMT, DOTS, 4>(W, XQ, XS, Y, dots, M, N, K, tiles_m, tiles_n, ksplit, stages_per_split);
 }
 // 32-token tiles, 4 waves; 4-block stages (45 KB of LDS for both buffers) so
 // three workgroups share a CU.
-template <bool DOTS>
-__global__ __launch_bounds__(256, 3) void gemm_q8_small_kernel(
+template <int FMT, bool DOTS>
+__global__ __launch_bounds__(256, 3) void gemm_i8_small_kernel(
     const uint8_t* __restrict__ W, const int8_t* __restrict__ XQ, const float* __restrict__ XS,
     float* __restrict__ Y, int32_t* __restrict__ dots, uint32_t M, uint32_t N, uint32_t K, uint32_t tiles_m,
     uint32_t tiles_n, uint32_t ksplit, uint32_t stages_per_split) {
-    gemm_q8_coalesced_body<DOTS, 4, 1>(W, XQ, XS, Y, dots, M, N, K, tiles_m, tiles_n, ksplit, stages_per_split);
+    gemm_i8_direct_body<FMT, DOTS, 4, 1>(W, XQ, XS, Y, dots, M, N, K, tiles_m, tiles_n, ksplit, stages_per_split);
 }
 
 // ------------------------------------------------------- fp32 GEMM -------
@@ -833,57 +844,97 @@ static size_t small_m_limit() {
     return v;
 }
 
+// Reduces the K splits of `partial` into Y (fixed order) when ks > 1.
+static hipError_t finish_splits(hipError_t e, const float* partial, float* Y, size_t M, size_t N, uint32_t ks,
+                                hipStream_t stream) {
+    if (e != hipSuccess || ks <= 1) return e;
+    const size_t total = M * N;
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(static_cast<uint32_t>((total + kThreads - 1) / kThreads)),
+                       dim3(kThreads), 0, stream, partial, Y, total, ks);
+    return hipGetLastError();
+}
+
+// The direct-to-LDS kernels (K % 256 == 0): the 32-token tile for small M,
+// else the 128-token tile with 4-block (default) or 8-block stages.
+template <int FMT>
+static hipError_t launch_direct(const uint8_t* w, const int8_t* xq, const float* xs, float* Y, int32_t* dots,
+                                float* partial, size_t M, size_t N, size_t K, hipStream_t stream) {
+    constexpr int BB = FMT == kQ8_0 ? 34 : 18;
+    constexpr size_t kSmallLds = 2 * QStage<4, 32, 4, BB>::BUF;
+    constexpr size_t kLds4 = 2 * QStage<4, BM, QTH / 64, BB>::BUF;
+    constexpr size_t kLds8 = 2 * QStage<8, BM, QTH / 64, BB>::BUF;
+    const uint32_t m = uint32_t(M), n = uint32_t(N), k = uint32_t(K), nb = uint32_t(K / 32);
+    const uint32_t tiles_n = static_cast<uint32_t>((N + BN - 1) / BN);
+    if (M <= small_m_limit()) {
+        const uint32_t stm = uint32_t((M + 31) / 32), sst = (nb + 3) / 4;
+        if (dots) {
+            hipLaunchKernelGGL((gemm_i8_small_kernel<FMT, true>), dim3(stm * tiles_n), dim3(256), kSmallLds, stream, w, xq,
+                               xs, Y, dots, m, n, k, stm, tiles_n, 1u, sst);
+            return hipGetLastError();
+        }
+        uint32_t ks = partial ? choose_ksplit_model(stm * tiles_n, sst, M, N, kSmallTileCost) : 1u;
+        const uint32_t spw = (sst + ks - 1) / ks;
+        ks = (sst + spw - 1) / spw;  // no empty splits
+        hipLaunchKernelGGL((gemm_i8_small_kernel<FMT, false>), dim3(stm * tiles_n * ks), dim3(256), kSmallLds, stream, w,
+                           xq, xs, ks > 1 ? partial : Y, dots, m, n, k, stm, tiles_n, ks, spw);
+        return finish_splits(hipGetLastError(), partial, Y, M, N, ks, stream);
+    }
+    const uint32_t tiles_m = static_cast<uint32_t>((M + BM - 1) / BM);
+    const int qkb = coalesced_kb();
+    const uint32_t st = (nb + qkb - 1) / qkb;
+    if (dots) {
+        if (qkb == 4)
+            hipLaunchKernelGGL((gemm_i8_direct4_kernel<FMT, true>), dim3(tiles_m * tiles_n), dim3(QTH), kLds4, stream, w,
+                               xq, xs, Y, dots, m, n, k, tiles_m, tiles_n, 1u, st);
+        else
+            hipLaunchKernelGGL((gemm_i8_direct8_kernel<FMT, true>), dim3(tiles_m * tiles_n), dim3(QTH), kLds8, stream, w,
+                               xq, xs, Y, dots, m, n, k, tiles_m, tiles_n, 1u, st);
+        return hipGetLastError();
+    }
+    uint32_t ks = !partial ? 1u
+                  : qkb == 4 ? choose_ksplit_model(tiles_m * tiles_n, st, M, N)
+                             : choose_ksplit(tiles_m * tiles_n, nb, uint32_t(qkb));
+    const uint32_t spw = (st + ks - 1) / ks;
+    ks = (st + spw - 1) / spw;  // no empty splits
+    float* out = ks > 1 ? partial : Y;
+    const dim3 grid(tiles_m * tiles_n * ks);
+    if (qkb == 4)
+        hipLaunchKernelGGL((gemm_i8_direct4_kernel<FMT, false>), grid, dim3(QTH), kLds4, stream, w, xq, xs, out, dots, m,
+                           n, k, tiles_m, tiles_n, ks, spw);
+    else
+        hipLaunchKernelGGL((gemm_i8_direct8_kernel<FMT, false>), grid, dim3(QTH), kLds8, stream, w, xq, xs, out, dots, m,
+                           n, k, tiles_m, tiles_n, ks, spw);
+    return finish_splits(hipGetLastError(), partial, Y, M, N, ks, stream);
+}
+
 static hipError_t launch_i8_common(int fmt, const uint8_t* w, const int8_t* xq, const float* xs, float* Y,
                                    int32_t* dots, float* partial, size_t M, size_t N, size_t K, hipStream_t stream) {
     if (!w || !xq || !M || !N || !K || K % 64 || M > (1u << 24) || N > (1u << 24) || K > (1u << 24))
         return hipErrorInvalidValue;
     if (fmt != kQ8_0 && fmt != kQ4_0) return hipErrorInvalidValue;
     if ((reinterpret_cast<uintptr_t>(w) & 3u) || (reinterpret_cast<uintptr_t>(xq) & 15u)) return hipErrorInvalidValue;
+    if (!dots && (!xs || !Y)) return hipErrorInvalidValue;
+    static const bool legacy = [] {
+        const char* e = getenv("ZQ_GEMM_KERNEL");
+        return e && e[0] == 'l';
+    }();
+    // The direct-load kernels address a tile with 32-bit offsets from its
+    // first row: 129 activation rows and 129 weight rows must stay below 2 GiB.
+    const size_t rb = row_bytes(fmt, K);
+    const bool offsets_fit = size_t(BM + 1) * K < (size_t(1) << 31) && size_t(BN + 1) * rb < (size_t(1) << 31);
+    if (!legacy && K % 256 == 0 && offsets_fit)
+        return fmt == kQ8_0 ? launch_direct<kQ8_0>(w, xq, xs, Y, dots, partial, M, N, K, stream)
+                            : launch_direct<kQ4_0>(w, xq, xs, Y, dots, partial, M, N, K, stream);
+
+    // Staged-conversion kernel (any K % 64 == 0).
     const uint32_t tiles_m = static_cast<uint32_t>((M + BM - 1) / BM);
     const uint32_t tiles_n = static_cast<uint32_t>((N + BN - 1) / BN);
     const uint32_t nb = uint32_t(K / 32);
     const uint32_t stages = (nb + KB - 1) / KB;
     const uint32_t m = uint32_t(M), n = uint32_t(N), k = uint32_t(K);
-    static const bool legacy = [] {
-        const char* e = getenv("ZQ_GEMM_KERNEL");
-        return e && e[0] == 'l';
-    }();
-    // The direct-load kernel addresses a tile with 32-bit offsets from its
-    // first row: 129 activation rows and 129 weight rows must stay below 2 GiB.
-    const bool offsets_fit = size_t(BM + 1) * K < (size_t(1) << 31) && size_t(BN + 1) * (K / 32 * 34) < (size_t(1) << 31);
-    const bool coalesced = !legacy && fmt == kQ8_0 && K % 256 == 0 && offsets_fit;
-    const int qkb = coalesced_kb();
-    const uint32_t cstages = (nb + qkb - 1) / qkb;
-    if (coalesced && M <= small_m_limit()) {
-        const uint32_t stm = uint32_t((M + 31) / 32), sst = (nb + 3) / 4;
-        constexpr size_t kSmallLds = 2 * QStage<4, 32, 4>::BUF;
-        if (dots) {
-            hipLaunchKernelGGL((gemm_q8_small_kernel<true>), dim3(stm * tiles_n), dim3(256), kSmallLds,
-                               stream, w, xq, xs, Y, dots, m, n, k, stm, tiles_n, 1u, sst);
-            return hipGetLastError();
-        }
-        if (!xs || !Y) return hipErrorInvalidValue;
-        uint32_t ks = partial ? choose_ksplit_model(stm * tiles_n, sst, M, N, kSmallTileCost) : 1u;
-        const uint32_t spw = (sst + ks - 1) / ks;
-        ks = (sst + spw - 1) / spw;
-        hipLaunchKernelGGL((gemm_q8_small_kernel<false>), dim3(stm * tiles_n * ks), dim3(256), kSmallLds,
-                           stream, w, xq, xs, ks > 1 ? partial : Y, dots, m, n, k, stm, tiles_n, ks, spw);
-        hipError_t e = hipGetLastError();
-        if (e != hipSuccess || ks == 1) return e;
-        const size_t total = M * N;
-        hipLaunchKernelGGL(splitk_reduce_kernel, dim3(static_cast<uint32_t>((total + kThreads - 1) / kThreads)),
-                           dim3(kThreads), 0, stream, partial, Y, total, ks);
-        return hipGetLastError();
-    }
     if (dots) {
         const dim3 grid(tiles_m * tiles_n);
-        if (coalesced && qkb == 4)
-            hipLaunchKernelGGL((gemm_q8_coalesced4_kernel<true>), grid, dim3(QTH), 2 * QStage<4>::BUF, stream, w, xq, xs, Y, dots,
-                               m, n, k, tiles_m, tiles_n, 1u, cstages);
-        else if (coalesced)
-            hipLaunchKernelGGL((gemm_q8_coalesced_kernel<true>), grid, dim3(QTH), 2 * QStage<8>::BUF, stream, w, xq, xs, Y, dots,
-                               m, n, k, tiles_m, tiles_n, 1u, cstages);
-        else if (fmt == kQ8_0)
+        if (fmt == kQ8_0)
             hipLaunchKernelGGL((gemm_i8_kernel<kQ8_0, true>), grid, dim3(kThreads), 0, stream, w, xq, xs, Y, dots, m, n,
                                k, tiles_m, tiles_n, 1u, stages);
         else
@@ -891,33 +942,18 @@ static hipError_t launch_i8_common(int fmt, const uint8_t* w, const int8_t* xq, 
                                k, tiles_m, tiles_n, 1u, stages);
         return hipGetLastError();
     }
-    if (!xs || !Y) return hipErrorInvalidValue;
-    const uint32_t st = coalesced ? cstages : stages;
-    uint32_t ks = coalesced && qkb == 4 ? choose_ksplit_model(tiles_m * tiles_n, st, M, N)
-                                        : choose_ksplit(tiles_m * tiles_n, nb, coalesced ? uint32_t(qkb) : uint32_t(KB));
-    if (ks > 1 && !partial) ks = 1;
-    const uint32_t spw = (st + ks - 1) / ks;
-    ks = (st + spw - 1) / spw;  // no empty splits
+    uint32_t ks = partial ? choose_ksplit(tiles_m * tiles_n, nb, uint32_t(KB)) : 1u;
+    const uint32_t spw = (stages + ks - 1) / ks;
+    ks = (stages + spw - 1) / spw;  // no empty splits
     float* out = ks > 1 ? partial : Y;
     const dim3 grid(tiles_m * tiles_n * ks);
-    if (coalesced && qkb == 4)
-        hipLaunchKernelGGL((gemm_q8_coalesced4_kernel<false>), grid, dim3(QTH), 2 * QStage<4>::BUF, stream, w, xq, xs, out, dots, m,
-                           n, k, tiles_m, tiles_n, ks, spw);
-    else if (coalesced)
-        hipLaunchKernelGGL((gemm_q8_coalesced_kernel<false>), grid, dim3(QTH), 2 * QStage<8>::BUF, stream, w, xq, xs, out, dots, m,
-                           n, k, tiles_m, tiles_n, ks, spw);
-    else if (fmt == kQ8_0)
+    if (fmt == kQ8_0)
         hipLaunchKernelGGL((gemm_i8_kernel<kQ8_0, false>), grid, dim3(kThreads), 0, stream, w, xq, xs, out, dots, m, n,
                            k, tiles_m, tiles_n, ks, spw);
     else
         hipLaunchKernelGGL((gemm_i8_kernel<kQ4_0, false>), grid, dim3(kThreads), 0, stream, w, xq, xs, out, dots, m, n,
                            k, tiles_m, tiles_n, ks, spw);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess || ks == 1) return e;
-    const size_t total = M * N;
-    const dim3 rgrid(static_cast<uint32_t>((total + kThreads - 1) / kThreads));
-    hipLaunchKernelGGL(splitk_reduce_kernel, rgrid, dim3(kThreads), 0, stream, partial, Y, total, ks);
-    return hipGetLastError();
+    return finish_splits(hipGetLastError(), partial, Y, M, N, ks, stream);
 }
 
 hipError_t launch_gemm_i8(int fmt, const uint8_t* w, const int8_t* xq, const float* xs, float* Y, float* partial,
