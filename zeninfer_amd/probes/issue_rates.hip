@@ -39,8 +39,8 @@ __global__ void mix(float* out, unsigned long long* cyc, int seed) {
     v16f cf[4] = {};
     v32f c2 = {};
     const float x0 = threadIdx.x, x1 = x0 + 1, x3 = x0 + 3, y = seed * 0.5f;
-    float acc[16];
-    for (int i = 0; i < 16; ++i) acc[i] = i * x0;
+    float acc[16], acc2[16];
+    for (int i = 0; i < 16; ++i) acc[i] = i * x0, acc2[i] = i * x1;
     __syncthreads();
     const unsigned long long t0 = __builtin_amdgcn_s_memtime();
     for (int it = 0; it < ITERS; ++it) {
@@ -74,6 +74,31 @@ __global__ void mix(float* out, unsigned long long* cyc, int seed) {
 #pragma unroll
                     for (int q = 0; q < 16; ++q) acc[q] = fmaf(acc[q], y, x3);
             }
+        } else if constexpr (KIND == 8 || KIND == 9) {
+            // the int8 GEMM's per-block unit for a wave's two 32x32 tiles: two
+            // int8 MFMAs, one 2-block dx*dw MFMA, then cvt + fma on all 32
+            // results.  8: the epilogue consumes this block's results; 9: it
+            // consumes the previous block's (one-block software pipeline).
+            const v16i zero = {};
+            const v32f szero = {};
+            v16i n0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, a, zero, 0, 0, 0);
+            v16i n1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a + it, a, zero, 0, 0, 0);
+            v32f ns = __builtin_amdgcn_mfma_f32_32x32x1f32(x0 + it, x1, szero, 0, 0, 0);
+            if constexpr (KIND == 8) {
+                ci[0] = n0;
+                ci[1] = n1;
+                c2 = ns;
+            }
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                acc[v] = fmaf(float(ci[0][v]), c2[v], acc[v]);
+                acc2[v] = fmaf(float(ci[1][v]), c2[16 + v], acc2[v]);
+            }
+            if constexpr (KIND == 9) {
+                ci[0] = n0;
+                ci[1] = n1;
+                c2 = ns;
+            }
         } else if constexpr (KIND == 7) {  // fp32 2-block MFMA + 16 independent fma
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -87,7 +112,7 @@ __global__ void mix(float* out, unsigned long long* cyc, int seed) {
     for (int j = 0; j < 4; ++j)
         for (int v = 0; v < 16; ++v) s += float(ci[j][v]) + cf[j][v];
     for (int v = 0; v < 32; ++v) s += c2[v];
-    for (int i = 0; i < 16; ++i) s += acc[i];
+    for (int i = 0; i < 16; ++i) s += acc[i] + acc2[i];
     out[blockIdx.x * blockDim.x + threadIdx.x] = s;
     __syncthreads();
     const unsigned long long t1 = __builtin_amdgcn_s_memtime();
@@ -132,6 +157,8 @@ int main() {
         run<5>("i8 MFMA + 16 fma (per MFMA)", w, 4, cus);
         run<6>("i8 MFMA + 48 fma (per MFMA)", w, 4, cus);
         run<7>("f32 2b MFMA + 16 fma (per MFMA)", w, 4, cus);
+        run<8>("GEMM block unit, dependent (per unit)", w, 1, cus);
+        run<9>("GEMM block unit, pipelined (per unit)", w, 1, cus);
     }
     return 0;
 }
