@@ -194,8 +194,9 @@ def test_device_synth_matches_host_generator(zq, orc):
 # ----------------------------------------------------------------- GEMM ---
 @pytest.mark.parametrize("fmt,m,n,k", [(O.Q8_0, 3, 300, 4096), (O.Q8_0, 130, 257, 1024), (O.Q8_0, 32, 128, 14336),
                                        (O.Q8_0, 2, 64, 192), (O.Q4_0, 17, 200, 4096), (O.Q4_0, 129, 130, 256),
-                                       # 32-token tiles: ragged M and N with a K split; M = 33 takes the 128-token tile
-                                       (O.Q8_0, 31, 1000, 8192), (O.Q8_0, 33, 260, 2048),
+                                       # 32-token tiles (M <= 64): ragged M and N, a K split, two token
+                                       # tiles; M = 65 takes the 128-token tile
+                                       (O.Q8_0, 31, 1000, 8192), (O.Q8_0, 33, 260, 2048), (O.Q8_0, 65, 260, 2048),
                                        (O.Q4_0, 31, 700, 8192), (O.Q4_0, 150, 300, 2048)])
 def test_gemm_int8(zq, orc, fmt, m, n, k):
     w = orc.gen_weights(fmt, 300 + n, n, k)

@@ -375,6 +375,12 @@ template <int QKB, int BMT = BM, int NW = QTH / 64, int BB = 34>
 struct QStage {
     static constexpr int A_BYTES = BMT * QKB * 32;          // activation tile
     static constexpr int UPR = QKB * 2;                     // 16 B units per activation row
+    // XOR swizzle of a row's 16 B units, so the 16 rows that a half-wave's
+    // ds_read_b128 touches fall on distinct 16 B bank groups: with 256 B rows
+    // (8-block stages) row % 16; with 128 B rows two rows share a 256 B bank
+    // line, so the swizzle takes (row / 2) % 8.
+    __device__ static int swz(int row) { return UPR == 16 ? row % 16 : (row >> 1) & 7; }
+    static_assert(UPR == 8 || UPR == 16, "4- or 8-block stages");
     static constexpr int WD = QKB * BB / 4;                 // raw dwords of a weight row per stage (BB = block bytes)
     static constexpr int W_STRIDE = WD | 1;                 // 69 / 35
     static constexpr int W_DWORDS = (BN - 1) * W_STRIDE + WD + 1;  // +1: the 5th dword read
@@ -445,7 +451,7 @@ __device__ __forceinline__ void gemm_i8_direct_body(
 #pragma unroll
     for (int i = 0; i < A_LOADS; ++i) {
         const int unit = (wave * A_LOADS + i) * 64 + lane;  // physical 16 B slot
-        const int row = unit / G::UPR, col = (unit % G::UPR) ^ (row % G::UPR);
+        const int row = unit / G::UPR, col = (unit % G::UPR) ^ G::swz(row);
         a_off[i] = (min(m0 + row, M - 1) - m0) * K + col * 16;
     }
     // Weight dword loads: LDS dword p of the region holds raw dword d of row r
@@ -522,7 +528,7 @@ __device__ __forceinline__ void gemm_i8_direct_body(
                                                                                          : sb * BMT + l32];
 #pragma unroll
         for (int i = 0; i < WM; ++i) {
-            const int row = wm * 64 + i * 32 + l32, col = (b * 2 + lh) ^ (row % G::UPR);
+            const int row = wm * 64 + i * 32 + l32, col = (b * 2 + lh) ^ G::swz(row);
             o.a[i] = *reinterpret_cast<const v4i*>(base + row * (QKB * 32) + col * 16);
         }
     };
@@ -834,12 +840,14 @@ static int coalesced_kb() {
     return v;
 }
 
-// Largest M that takes the 32-token tile (ZQ_GEMM_SMALL_M, default 32; 0
-// turns it off).
+// Largest M that takes the 32-token tile (ZQ_GEMM_SMALL_M, default 64; 0
+// turns it off).  Measured crossover at 14336x4096 and 4096x14336: the
+// 32-token tile is faster at M = 48 and 64 (36-39 vs 41-43 us), slower from
+// M = 96 (46-49 vs 45-46 us), where its token tiles re-read each weight panel.
 static size_t small_m_limit() {
     static const size_t v = [] {
         const char* e = getenv("ZQ_GEMM_SMALL_M");
-        return e ? size_t(atoi(e)) : size_t(32);
+        return e ? size_t(atoi(e)) : size_t(64);
     }();
     return v;
 }
