@@ -215,8 +215,12 @@ int enqueue_gemm(int fmt, const uint8_t* w, const float* X, float* Y, size_t tok
         *dispatches += pbytes ? 3 : 2;
         return ZQ_OK;
     }
-    if (zq::launch_gemm_f32(fmt, w, X, Y, tokens, rows, cols, s) != hipSuccess) return ZQ_ERR_HIP;
-    *dispatches += 1;
+    // fp32 activations: the workspace, when large enough, holds split-K
+    // partial sums; without it the GEMM runs unsplit
+    const size_t pbytes = zq::gemm_f32_partial_bytes(tokens, rows, cols);
+    float* part = pbytes && ws && ws_bytes >= pbytes ? static_cast<float*>(ws) : nullptr;
+    if (zq::launch_gemm_f32(fmt, w, X, Y, part, tokens, rows, cols, s) != hipSuccess) return ZQ_ERR_HIP;
+    *dispatches += part ? 2 : 1;
     return ZQ_OK;
 }
 
@@ -551,7 +555,7 @@ int zq_hip_gemv_dev(int fmt, const void* weights, const float* x, float* y, size
 
 size_t zq_hip_gemm_workspace_bytes(int fmt, size_t tokens, size_t rows, size_t cols, int act_mode) {
     if (!valid_fmt(fmt) || !zq::row_bytes(fmt, cols) || !tokens || !rows) return 0;
-    if (resolve_act(fmt, act_mode) != ZQ_ACT_INT8) return 0;
+    if (resolve_act(fmt, act_mode) != ZQ_ACT_INT8) return zq::gemm_f32_partial_bytes(tokens, rows, cols);
     return align_up(tokens * cols, 256) + align_up(tokens * (cols / 32) * sizeof(float), 256) +
            zq::gemm_i8_partial_bytes(tokens, rows, cols);
 }

@@ -691,15 +691,24 @@ __global__ __launch_bounds__(256, 3) void gemm_i8_small_kernel(
 constexpr int FK = 32;          // K elements per fp32 stage
 constexpr int FROW = FK + 4;    // LDS floats per row (pad)
 
+// Split K (ksplit > 1): workgroup blockIdx.x / tiles covers stages
+// [split * stages_per_split, ...) of FK elements and writes its partial sums
+// to Y + split * M * N; splitk_reduce_kernel adds them in split order.
 template <int FMT>
 __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(const uint8_t* __restrict__ W, const float* __restrict__ X,
                                                             float* __restrict__ Y, uint32_t M, uint32_t N, uint32_t K,
-                                                            uint32_t tiles_m, uint32_t tiles_n) {
+                                                            uint32_t tiles_m, uint32_t tiles_n, uint32_t ksplit,
+                                                            uint32_t stages_per_split) {
     __shared__ __align__(16) float As[BM * FROW];
     __shared__ __align__(16) float Bs[BN * FROW];
+    const uint32_t total_tiles = tiles_m * tiles_n;
+    const uint32_t split = blockIdx.x / total_tiles;
     uint32_t tm, tn;
-    tile_of(tiles_m, tiles_n, blockIdx.x, tm, tn);
+    tile_of(tiles_m, tiles_n, blockIdx.x % total_tiles, tm, tn);
     const uint32_t m0 = tm * BM, n0 = tn * BN;
+    const uint32_t k_begin = split * stages_per_split * FK;
+    const uint32_t k_end = min(K, k_begin + stages_per_split * FK);
+    float* Yout = Y + (ksplit > 1 ? size_t(split) * M * N : 0);
     const size_t rb = row_bytes_dev(FMT, K);
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -717,7 +726,7 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(const uint8_t* __res
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-    for (uint32_t k0 = 0; k0 < K; k0 += FK) {
+    for (uint32_t k0 = k_begin; k0 < k_end; k0 += FK) {
         __syncthreads();
         {
             const float4* s = reinterpret_cast<const float4*>(a_src + k0 + ld_half * 16);
@@ -754,7 +763,7 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(const uint8_t* __res
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const uint32_t m = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
-                if (m < M && n < N) Y[size_t(m) * N + n] = acc[i][j][v];
+                if (m < M && n < N) Yout[size_t(m) * N + n] = acc[i][j][v];
             }
         }
 }
@@ -975,39 +984,58 @@ hipError_t launch_block_dots(int fmt, const uint8_t* w, const int8_t* xq, int32_
     return launch_i8_common(fmt, w, xq, nullptr, nullptr, out, nullptr, M, N, K, stream);
 }
 
-hipError_t launch_gemm_f32(int fmt, const uint8_t* w, const float* X, float* Y, size_t M, size_t N, size_t K,
-                           hipStream_t stream) {
+// Split factor of the fp32-activation GEMM: enough workgroups for two per CU
+// (ZQ_GEMMF_KSPLIT forces one), at least 16 K stages per split.
+static uint32_t choose_ksplit_f32(uint32_t tiles, uint32_t stages) {
+    static const int forced = [] {
+        const char* e = getenv("ZQ_GEMMF_KSPLIT");
+        return e ? atoi(e) : 0;
+    }();
+    if (forced > 0) return std::max(1u, std::min(uint32_t(forced), stages));
+    const uint32_t want = (2u * uint32_t(device_cu_count()) + tiles - 1) / tiles;
+    return std::max(1u, std::min(want, std::max(1u, stages / 16)));
+}
+
+size_t gemm_f32_partial_bytes(size_t M, size_t N, size_t K) {
+    const uint32_t tiles = uint32_t(((M + BM - 1) / BM) * ((N + BN - 1) / BN));
+    const uint32_t ks = choose_ksplit_f32(tiles, uint32_t((K + FK - 1) / FK));
+    return ks > 1 ? size_t(ks) * M * N * sizeof(float) : 0;
+}
+
+hipError_t launch_gemm_f32(int fmt, const uint8_t* w, const float* X, float* Y, float* partial, size_t M, size_t N,
+                           size_t K, hipStream_t stream) {
     if (!w || !X || !Y || !M || !N || !row_bytes(fmt, K) || M > (1u << 24) || N > (1u << 24) || K > (1u << 24))
         return hipErrorInvalidValue;
     if ((reinterpret_cast<uintptr_t>(w) & 1u) || (reinterpret_cast<uintptr_t>(X) & 15u)) return hipErrorInvalidValue;
     if ((fmt == kQ4_K || fmt == kQ5_K) && (reinterpret_cast<uintptr_t>(w) & 3u)) return hipErrorInvalidValue;
     const uint32_t tiles_m = static_cast<uint32_t>((M + BM - 1) / BM);
     const uint32_t tiles_n = static_cast<uint32_t>((N + BN - 1) / BN);
-    const dim3 grid(tiles_m * tiles_n);
+    const uint32_t stages = uint32_t((K + FK - 1) / FK);
+    uint32_t ks = partial ? choose_ksplit_f32(tiles_m * tiles_n, stages) : 1u;
+    const uint32_t spw = (stages + ks - 1) / ks;
+    ks = (stages + spw - 1) / spw;  // no empty splits
+    float* out = ks > 1 ? partial : Y;
+    const dim3 grid(tiles_m * tiles_n * ks);
+    const uint32_t m = uint32_t(M), n = uint32_t(N), k = uint32_t(K);
     switch (fmt) {
     case kQ8_0:
-        hipLaunchKernelGGL(gemm_f32_kernel<kQ8_0>, grid, dim3(kThreads), 0, stream, w, X, Y, uint32_t(M), uint32_t(N),
-                           uint32_t(K), tiles_m, tiles_n);
+        hipLaunchKernelGGL(gemm_f32_kernel<kQ8_0>, grid, dim3(kThreads), 0, stream, w, X, out, m, n, k, tiles_m, tiles_n, ks, spw);
         break;
     case kQ4_0:
-        hipLaunchKernelGGL(gemm_f32_kernel<kQ4_0>, grid, dim3(kThreads), 0, stream, w, X, Y, uint32_t(M), uint32_t(N),
-                           uint32_t(K), tiles_m, tiles_n);
+        hipLaunchKernelGGL(gemm_f32_kernel<kQ4_0>, grid, dim3(kThreads), 0, stream, w, X, out, m, n, k, tiles_m, tiles_n, ks, spw);
         break;
     case kQ6_K:
-        hipLaunchKernelGGL(gemm_f32_kernel<kQ6_K>, grid, dim3(kThreads), 0, stream, w, X, Y, uint32_t(M), uint32_t(N),
-                           uint32_t(K), tiles_m, tiles_n);
+        hipLaunchKernelGGL(gemm_f32_kernel<kQ6_K>, grid, dim3(kThreads), 0, stream, w, X, out, m, n, k, tiles_m, tiles_n, ks, spw);
         break;
     case kQ4_K:
-        hipLaunchKernelGGL(gemm_f32_kernel<kQ4_K>, grid, dim3(kThreads), 0, stream, w, X, Y, uint32_t(M), uint32_t(N),
-                           uint32_t(K), tiles_m, tiles_n);
+        hipLaunchKernelGGL(gemm_f32_kernel<kQ4_K>, grid, dim3(kThreads), 0, stream, w, X, out, m, n, k, tiles_m, tiles_n, ks, spw);
         break;
     case kQ5_K:
-        hipLaunchKernelGGL(gemm_f32_kernel<kQ5_K>, grid, dim3(kThreads), 0, stream, w, X, Y, uint32_t(M), uint32_t(N),
-                           uint32_t(K), tiles_m, tiles_n);
+        hipLaunchKernelGGL(gemm_f32_kernel<kQ5_K>, grid, dim3(kThreads), 0, stream, w, X, out, m, n, k, tiles_m, tiles_n, ks, spw);
         break;
     default: return hipErrorInvalidValue;
     }
-    return hipGetLastError();
+    return finish_splits(hipGetLastError(), partial, Y, M, N, ks, stream);
 }
 
 }  // namespace zq

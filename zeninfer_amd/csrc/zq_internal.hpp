@@ -59,8 +59,11 @@ int device_cu_count();
 hipError_t launch_gemm_i8(int fmt, const uint8_t* w, const int8_t* xq, const float* xs,
                           float* Y, float* partial, size_t M, size_t N, size_t K, hipStream_t stream);
 
-// Prefill GEMM on fp32 activations (the reference CPU arithmetic).
-hipError_t launch_gemm_f32(int fmt, const uint8_t* w, const float* X, float* Y, size_t M,
+// Prefill GEMM on fp32 activations (the reference CPU arithmetic).  `partial`
+// (gemm_f32_partial_bytes, may be null) is the split-K workspace; with
+// partial == nullptr the GEMM runs unsplit.
+size_t gemm_f32_partial_bytes(size_t M, size_t N, size_t K);
+hipError_t launch_gemm_f32(int fmt, const uint8_t* w, const float* X, float* Y, float* partial, size_t M,
                            size_t N, size_t K, hipStream_t stream);
 
 // Bit-exact tier helpers.

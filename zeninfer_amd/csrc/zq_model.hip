@@ -151,7 +151,8 @@ bool alloc_runtime(zq_model& m, std::string& e) {
     size_t partial = 0;
     for (uint32_t M = 1; M <= kPrefillChunk; ++M)
         for (auto nk : {std::pair<size_t, size_t>{QW, E}, {KW, E}, {E, QW}, {F, E}, {E, F}})
-            partial = std::max(partial, zq::gemm_i8_partial_bytes(M, nk.first, nk.second));
+            partial = std::max({partial, zq::gemm_i8_partial_bytes(M, nk.first, nk.second),
+                                zq::gemm_f32_partial_bytes(M, nk.first, nk.second)});
     const size_t xq_bytes = align_up(T * widest, kAlign), xs_bytes = align_up(T * widest / 32 * 4, kAlign);
     const size_t attn_bytes = align_up(zq::attention_decode_partial_floats(c.heads, c.head_dim, c.max_positions) * 4, kAlign);
     const size_t arg_bytes = align_up(zq::argmax_partial_bytes(), kAlign);
@@ -224,7 +225,7 @@ bool init_common(zq_model& m, std::string& e) {
 // into xq/xs when `quantized` (int8 mode).
 hipError_t project(zq_model& m, const Weight& w, const float* X, float* Y, uint32_t M, bool quantized) {
     if (quantized) return zq::launch_gemm_i8(w.fmt, w.p, m.xq, m.xs, Y, m.partial, M, w.rows, w.cols, m.stream);
-    return zq::launch_gemm_f32(w.fmt, w.p, X, Y, M, w.rows, w.cols, m.stream);
+    return zq::launch_gemm_f32(w.fmt, w.p, X, Y, m.partial, M, w.rows, w.cols, m.stream);
 }
 
 bool int8_ok(int fmt) { return fmt == zq::kQ8_0 || fmt == zq::kQ4_0; }
