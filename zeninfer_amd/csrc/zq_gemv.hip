@@ -699,9 +699,14 @@ __global__ __launch_bounds__(kThreads) void gemv_q6k_kernel(TaskTable tt, const 
 // chunks-per-row waves covers a row, wave s owning chunk s, so each lane's x
 // values (two 16-element units: 32 floats) stay in VGPRs for the whole
 // kernel.  Each chunk is fetched with lane-contiguous dwordx4 loads into a
-// per-wave LDS buffer; lane L then decodes units L and L+64 of the chunk
-// (super-block u/16, half (u/8)%2, l-quad 4*(u%8)) from LDS.  Fields of odd
-// super-blocks sit at 2 mod 4 and are assembled with v_alignbyte.
+// per-wave LDS buffer; lane L then decodes its two 16-element units (one
+// quarter of one half of super-block 2*(L/16) + k, a single sub-block scale)
+// from LDS.  Fields of odd super-blocks sit at 2 mod 4 and are assembled
+// with v_alignbyte.  ZQ_Q6K_DIAG (diagnostic builds only): 1 drops the
+// decode, 2 also the LDS staging.
+#ifndef ZQ_Q6K_DIAG
+#define ZQ_Q6K_DIAG 0
+#endif
 template <int R, int S, int NW>
 __global__ __launch_bounds__(NW * 64) void gemv_q6k_stream_kernel(TaskTable tt, const float* __restrict__ x,
                                                                  uint32_t cols, uint32_t total_blocks) {
@@ -717,16 +722,23 @@ __global__ __launch_bounds__(NW * 64) void gemv_q6k_stream_kernel(TaskTable tt, 
     const int team = wave / S, slice = wave % S;
     uint32_t* wbuf = lds + wave * (R * BUFW);
 
-    // x for this lane's two units, kept in registers; loaded before any weights
-    float xv[2][4][4];
+    // A lane's unit k (two per lane) is 16 consecutive elements of one
+    // quarter, so one sub-block scale covers it: super-block 2*(lane/16) + k
+    // of the chunk, half h, quarter q, l0 = 0 or 16 from lane % 16.  One LDS
+    // read instruction thus touches super-blocks {0,2,4,6} (k = 0, all 4-byte
+    // aligned) or {1,3,5,7} (k = 1, all at 2 mod 4), whose dword starts fall
+    // in four distinct residues mod 4: no bank conflicts.  x of both units
+    // is kept in registers, loaded before any weights.
+    float xv[2][16];
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
-        const uint32_t uu = lane + 64 * k;
-        const uint32_t sb = slice * 8 + (uu >> 4), h = (uu >> 3) & 1u, l0 = (uu & 7u) * 4u;
+        const uint32_t sb = slice * 8 + ((uint32_t(lane) >> 4) << 1) + k, h = (lane >> 3) & 1u, q = (lane >> 1) & 3u,
+                       l0 = (lane & 1u) * 16u;
+        const float4* xp = reinterpret_cast<const float4*>(x + sb * 256 + h * 128 + q * 32 + l0);
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const float4 v = *reinterpret_cast<const float4*>(x + sb * 256 + h * 128 + g * 32 + l0);
-            xv[k][g][0] = v.x; xv[k][g][1] = v.y; xv[k][g][2] = v.z; xv[k][g][3] = v.w;
+        for (int i = 0; i < 4; ++i) {
+            const float4 v = xp[i];
+            xv[k][4 * i] = v.x; xv[k][4 * i + 1] = v.y; xv[k][4 * i + 2] = v.z; xv[k][4 * i + 3] = v.w;
         }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -756,18 +768,27 @@ __global__ __launch_bounds__(NW * 64) void gemv_q6k_stream_kernel(TaskTable tt, 
         locate(min(blk, total_blocks - 1), rowp, row0, ti);
         load(rowp, u);
     }
-    float sxg[2][4];  // sum of x per 4-element group of the lane's two units
+    float nsx[2];  // -32 * sum of x over each of the lane's two units
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
+    for (int kk = 0; kk < 2; ++kk) {
+        float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
-        for (int g = 0; g < 4; ++g) sxg[kk][g] = (xv[kk][g][0] + xv[kk][g][1]) + (xv[kk][g][2] + xv[kk][g][3]);
+        for (int i = 0; i < 16; i += 2) a0 += xv[kk][i], a1 += xv[kk][i + 1];
+        nsx[kk] = -32.0f * (a0 + a1);
+    }
     int parity = 0;
     while (blk < total_blocks) {
+#if ZQ_Q6K_DIAG == 2  // diagnostic builds only: no LDS staging, no decode
+        uint32_t dg = 0;
+#pragma unroll
+        for (int r = 0; r < R; ++r) dg ^= u[r][0].x ^ u[r][0].w ^ u[r][1].y;
+#else
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             reinterpret_cast<uint4*>(wbuf + r * BUFW)[lane] = u[r][0];
             if (lane + 64 < int(CUNITS)) reinterpret_cast<uint4*>(wbuf + r * BUFW)[lane + 64] = u[r][1];
         }
+#endif
         const uint32_t nblk = blk + gridDim.x;
         const uint32_t row0c = row0;
         const int tic = ti;
@@ -777,52 +798,72 @@ __global__ __launch_bounds__(NW * 64) void gemv_q6k_stream_kernel(TaskTable tt, 
             load(rowp, u);
         }
         float acc[R];
+#if ZQ_Q6K_DIAG == 2
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = wave_sum(__uint_as_float((dg + r) & 0x3FFFFFFFu));
+#else
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const uint32_t* buf = wbuf + r * BUFW;
             const uint8_t* bbytes = reinterpret_cast<const uint8_t*>(buf);
-            auto lds_u32 = [&](uint32_t off) -> uint32_t {  // 32 bits at a 2-byte aligned chunk offset
-                const uint32_t a = off & ~3u;
-                const uint32_t lo = buf[a >> 2];
-                if ((off & 3u) == 0) return lo;
-                return __builtin_amdgcn_alignbyte(buf[(a >> 2) + 1], lo, 2);
+            // 16 bytes at a chunk offset that is 4-byte aligned (even
+            // super-blocks) or at 2 mod 4 (odd: five dword reads, four
+            // v_alignbyte)
+            auto lds16 = [&](uint32_t off, bool odd, uint32_t (&o)[4]) {
+                const uint32_t* w = buf + (off >> 2);
+                if (!odd) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) o[i] = w[i];
+                } else {
+                    uint32_t t5[5];
+#pragma unroll
+                    for (int i = 0; i < 5; ++i) t5[i] = w[i];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) o[i] = __builtin_amdgcn_alignbyte(t5[i + 1], t5[i], 2);
+                }
             };
             float a = 0.0f;
 #pragma unroll
             for (int k = 0; k < 2; ++k) {
-                const uint32_t uu = lane + 64 * k;
-                const uint32_t sbl = uu >> 4, h = (uu >> 3) & 1u, l0 = (uu & 7u) * 4u;
+                const uint32_t sbl = ((uint32_t(lane) >> 4) << 1) + k, h = (lane >> 3) & 1u, q = (lane >> 1) & 3u,
+                               l0 = (lane & 1u) * 16u;
                 const uint32_t base = sbl * 210;
-                const uint32_t qlA = lds_u32(base + h * 64 + l0);
-                const uint32_t qlB = lds_u32(base + h * 64 + 32 + l0);
-                const uint32_t qh = lds_u32(base + 128 + h * 32 + l0);
-                const uint32_t sc0 = lds_u32(base + 192 + h * 8);
-                const uint32_t sc1 = lds_u32(base + 196 + h * 8);
-                const uint32_t dbits = uint32_t(bbytes[base + 208]) | (uint32_t(bbytes[base + 209]) << 8);
-                const float d = half_bits_to_float(dbits);
-                const uint32_t shsel = l0 >> 4;
-                float part = 0.0f;
+                uint32_t ql[4], qh[4];
+                lds16(base + h * 64 + (q & 1u) * 32 + l0, k == 1, ql);  // low nibbles (q < 2) or high (q >= 2)
+                lds16(base + 128 + h * 32 + l0, k == 1, qh);            // 2-bit fields, quarter q at bit 2q
+                const float sc = float(int8_t(bbytes[base + 192 + h * 8 + q * 2 + (l0 >> 4)]));
+                const float d = half_bits_to_float(reinterpret_cast<const uint16_t*>(bbytes)[(base + 208) >> 1]);
+                // rotations that bring quarter q's nibble to bits 0-3 and its
+                // 2-bit field to bits 4-5 of every byte (bits rotated in from
+                // neighbouring bytes land outside the masks)
+                const uint32_t nrot = (q >> 1) * 4, hrot = (2 * q + 28) & 31u;
+                float t0 = 0.0f, t1 = 0.0f;
+#if ZQ_Q6K_DIAG != 1
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    // the 6-bit u = q + 32 of elements (0,2) and (1,3) as binary16
-                    // denormals u * 2^-24 into v_fma_mix_f32; sum (u-32)*x =
-                    // 2^24 * sum u*x*2^-24 - 32 * sum x
-                    const uint32_t src = ((g & 1) ? qlB : qlA) >> (g >= 2 ? 4 : 0);
-                    const uint32_t p02 = (src & 0x000F000Fu) | (((qh >> (2 * g)) & 0x00030003u) << 4);
-                    const uint32_t p13 = ((src >> 8) & 0x000F000Fu) | (((qh >> (2 * g + 8)) & 0x00030003u) << 4);
-                    float t = 0.0f;
-                    t = mix_lo(p02, xv[k][g][0], t);
-                    t = mix_lo(p13, xv[k][g][1], t);
-                    t = mix_hi(p02, xv[k][g][2], t);
-                    t = mix_hi(p13, xv[k][g][3], t);
-                    const float sum = fmaf(t, 16777216.0f, -32.0f * sxg[k][g]);
-                    const float sc = sbyte(g < 2 ? sc0 : sc1, (2 * g + shsel) & 3);
-                    part = fmaf(d * sc, sum, part);
+                for (int j = 0; j < 4; ++j) {
+                    // the four 6-bit codes u = q + 32 of elements 4j..4j+3, one per
+                    // byte, spread into binary16 halves: u * 2^-24 as denormals
+                    // into v_fma_mix_f32; sum (u-32)*x = 2^24 * sum u*x*2^-24 - 32 * sum x
+                    const uint32_t lo4 = __builtin_amdgcn_alignbit(ql[j], ql[j], nrot);
+                    const uint32_t hi2 = __builtin_amdgcn_alignbit(qh[j], qh[j], hrot) & 0x30303030u;
+                    const uint32_t codes = (lo4 & 0x0F0F0F0Fu) | hi2;
+                    const uint32_t p02 = codes & 0x00FF00FFu;
+                    const uint32_t p13 = __builtin_amdgcn_perm(0u, codes, 0x0c030c01u);  // bytes 1, 3 -> halves
+                    t0 = mix_lo(p02, xv[k][4 * j], t0);
+                    t1 = mix_lo(p13, xv[k][4 * j + 1], t1);
+                    t0 = mix_hi(p02, xv[k][4 * j + 2], t0);
+                    t1 = mix_hi(p13, xv[k][4 * j + 3], t1);
                 }
-                a += part;
+#endif
+#if ZQ_Q6K_DIAG == 1  // diagnostic builds only: decode removed, LDS reads kept
+                a += __uint_as_float((ql[0] ^ ql[1] ^ ql[2] ^ ql[3] ^ qh[0] ^ qh[1] ^ qh[2] ^ qh[3]) & 0x3FFFFFFFu) + sc + d;
+#else
+                a = fmaf(d * sc, fmaf(t0 + t1, 16777216.0f, nsx[k]), a);
+#endif
             }
             acc[r] = wave_sum(a);
         }
+#endif
         const GemvTask& t = tt.t[tic];
         if constexpr (S == 1) {
 #pragma unroll
@@ -1289,7 +1330,7 @@ hipError_t launch_q6k(TaskTable& tt, const float* x, uint32_t cols, hipStream_t 
     return hipGetLastError();
 }
 template <int R, int S, int NW>
-hipError_t launch_q6k_stream(TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream) {
+hipError_t launch_q6k_stream(TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream, uint32_t wg_per_cu = 1) {
     constexpr uint32_t TEAMS = NW / S;
     uint32_t blocks = 0;
     for (int i = 0; i < tt.count; ++i) {
@@ -1297,28 +1338,31 @@ hipError_t launch_q6k_stream(TaskTable& tt, const float* x, uint32_t cols, hipSt
         blocks += (tt.t[i].rows + TEAMS * R - 1) / (TEAMS * R);
     }
     tt.group_start[tt.count] = blocks;
-    const uint32_t grid = std::min<uint32_t>(blocks, uint32_t(cu_count()));
+    const uint32_t grid = std::min<uint32_t>(blocks, uint32_t(cu_count()) * wg_per_cu);
     const size_t lds = size_t(NW) * R * (8 * 210 / 4 + 4) * 4;
     hipLaunchKernelGGL((gemv_q6k_stream_kernel<R, S, NW>), dim3(grid), dim3(NW * 64), lds, stream, tt, x, cols, blocks);
     return hipGetLastError();
 }
-// chunks per row -> (S, waves per workgroup)
+// chunks per row -> (S, waves per workgroup); two workgroups per CU.  Two
+// 8-wave workgroups measured faster than one 16-wave one (the per-step
+// slice reduction then synchronises 8 waves, not 16), and 2 rows per step
+// faster than 1 or 4: 14336x4096 19.6 -> 17.0 us, lm_head 96.6 -> 89.5 us.
 template <int R>
 hipError_t launch_q6k_stream_s(TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream) {
     switch ((cols >> 8) / 8) {
-    case 1: return launch_q6k_stream<R, 1, 16>(tt, x, cols, stream);
-    case 2: return launch_q6k_stream<R, 2, 16>(tt, x, cols, stream);
-    case 3: return launch_q6k_stream<R, 3, 15>(tt, x, cols, stream);
-    case 4: return launch_q6k_stream<R, 4, 16>(tt, x, cols, stream);
-    case 5: return launch_q6k_stream<R, 5, 15>(tt, x, cols, stream);
-    case 6: return launch_q6k_stream<R, 6, 12>(tt, x, cols, stream);
-    case 7: return launch_q6k_stream<R, 7, 14>(tt, x, cols, stream);
-    case 8: return launch_q6k_stream<R, 8, 16>(tt, x, cols, stream);
+    case 1: return launch_q6k_stream<R, 1, 8>(tt, x, cols, stream, 2);
+    case 2: return launch_q6k_stream<R, 2, 8>(tt, x, cols, stream, 2);
+    case 3: return launch_q6k_stream<R, 3, 6>(tt, x, cols, stream, 2);
+    case 4: return launch_q6k_stream<R, 4, 8>(tt, x, cols, stream, 2);
+    case 5: return launch_q6k_stream<R, 5, 5>(tt, x, cols, stream, 2);
+    case 6: return launch_q6k_stream<R, 6, 6>(tt, x, cols, stream, 2);
+    case 7: return launch_q6k_stream<R, 7, 7>(tt, x, cols, stream, 2);
+    case 8: return launch_q6k_stream<R, 8, 8>(tt, x, cols, stream, 2);
     default: return hipErrorInvalidConfiguration;
     }
 }
 hipError_t launch_q6k_stream_any(TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream, uint32_t total_rows) {
-    return total_rows >= 4096 ? launch_q6k_stream_s<4>(tt, x, cols, stream) : launch_q6k_stream_s<1>(tt, x, cols, stream);
+    return total_rows >= 4096 ? launch_q6k_stream_s<2>(tt, x, cols, stream) : launch_q6k_stream_s<1>(tt, x, cols, stream);
 }
 
 template <int FMT, int R, int S, int NW>
