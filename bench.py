@@ -30,6 +30,9 @@ cpu_baseline the reference's own AVX2 ComputePool path (compiled from the
          reference sources into oracle/_ref) on this host's cores (up to 16
          threads, the box's CPU share), on four layers' projections (0.93 GB);
          falls back to the C oracle if the reference build is absent.
+         cpu_baseline_reference_policy repeats it (shorter) with the
+         reference's own decode worker count, min(physical cores, 8);
+         cpu_host gives nproc, usable CPUs, physical cores and the CPU model.
 
 traffic  HBM bytes per launch of the dominant kernel from two rocprofv3 --pmc
          passes (FETCH_SIZE, WRITE_SIZE) over `bench.py --pmc-workload`, each
@@ -143,9 +146,34 @@ def measured_traffic():
         return None
 
 
-def cpu_baseline(seconds=10.0, layers=4):
+def cpu_host():
+    """nproc, usable CPUs, physical cores and the CPU model of this host."""
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count() or 1
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        import psutil
+        physical = psutil.cpu_count(logical=False) or usable
+    except Exception:
+        physical = usable
+    return {"nproc": os.cpu_count(), "usable_cpus": usable, "physical_cores": physical, "model": model}
+
+
+def cpu_baseline(seconds=10.0, layers=4, workers=None):
     """Reference CPU path (oracle/_ref) on `layers` layers' seven Q8_0
-    projections each (~0.93 GB, more than a server CPU's last-level cache)."""
+    projections each (~0.93 GB, more than a server CPU's last-level cache).
+    `workers` defaults to all usable host CPUs up to 16 (the pool caps at 32,
+    compute_pool.cpp:87)."""
     from oracle import oracle as O
     o = O.Oracle()
     kind = "reference"
@@ -159,7 +187,8 @@ def cpu_baseline(seconds=10.0, layers=4):
     ws = [o.gen_weights(O.Q8_0, 0xC0 + i, rr, cc) for i, (rr, cc) in enumerate(shapes)]
     xs = {c: o.gen_normal(0xC1 + c, c) for c in (HIDDEN, FFN)}
     nbytes = sum(gemv_bytes(o.row_bytes(O.Q8_0, c), rr, c) for rr, c in shapes)
-    workers = max(1, min(16, os.cpu_count() or 1, 32))
+    if workers is None:
+        workers = max(1, min(16, cpu_host()["usable_cpus"], 32))
 
     def one_pass():
         for w, (rr, cc) in zip(ws, shapes):
@@ -453,10 +482,17 @@ def main():
     # ---- config 4: the device-resident decoder, prefill 512 + 128 greedy tokens
     model4 = model_config4()
 
-    cpu = None
+    cpu = cpu_policy = host = None
     if not args.no_cpu:
         try:
-            cpu = cpu_baseline()
+            cpu = cpu_baseline(seconds=8.0)
+            host = cpu_host()
+            # the reference's own decode policy: min(physical cores, 8) workers
+            # (execution_planner.cpp:22-28), a shorter sample
+            pw = max(1, min(host["physical_cores"], host["usable_cpus"], 8))
+            pol = cpu_baseline(seconds=4.0, workers=pw)
+            cpu_policy = {"value": pol["value"], "unit": pol["unit"], "cores": pol["cores"], "kind": pol["kind"],
+                          "policy": "decode: min(physical cores, 8) workers (execution_planner.cpp:22-28)"}
         except Exception as e:  # reported, never fatal to the GPU measurement
             cpu = {"error": str(e)}
 
@@ -487,6 +523,8 @@ def main():
         "formats_config3": formats,
         "model_config4": model4,
         "cpu_baseline": cpu,
+        "cpu_baseline_reference_policy": cpu_policy,
+        "cpu_host": host,
     }
     print(json.dumps(out))
     return 0
