@@ -326,3 +326,37 @@ def test_ffn_gemv(zq, orc):
     # projection (the GEMV bar relative to the magnitude that is summed)
     mag = np.abs(dd) @ np.abs(act)
     assert np.all(np.abs(y - want) <= 1e-4 + 1e-5 * mag), np.max(np.abs(y - want) / (1e-4 + 1e-5 * mag))
+
+
+# ----------------------------------------------------- random-shape sweeps ---
+# Seeded shapes that land on every kernel choice: the 32-token and 128-token
+# int8 tiles (M <= 64 / M > 64), K % 256 (direct-to-LDS) or not (staged),
+# split factors from the cost models, ragged M and N; GEMV widths on and off
+# the streaming kernels for every format.
+_RNG = np.random.default_rng(20261202)
+_GEMM_SHAPES = [(int(f), int(_RNG.integers(1, 200)), int(_RNG.integers(1, 700)), int(k))
+                for f, k in zip(_RNG.choice([O.Q8_0, O.Q4_0], 12), _RNG.choice([256, 512, 768, 1024, 2304, 4096, 320], 12))]
+_GEMV_SHAPES = [(int(f), int(_RNG.integers(1, 5000)), int(c))
+                for f, c in zip(_RNG.choice([O.Q8_0, O.Q4_0, O.Q6_K, O.Q4_K, O.Q5_K], 15),
+                                _RNG.choice([256, 2048, 4096, 6144, 12288], 15))]
+# the staged int8 kernel (K % 256 != 0) and the Q6_K / K-quant two-rows-per-step path
+_GEMM_SHAPES += [(O.Q8_0, 70, 300, 320), (O.Q4_0, 40, 129, 192)]
+_GEMV_SHAPES += [(O.Q6_K, 4500, 4096), (O.Q5_K, 4099, 6144)]
+
+
+@pytest.mark.parametrize("fmt,m,n,k", _GEMM_SHAPES)
+def test_gemm_int8_random_shapes(zq, orc, fmt, m, n, k):
+    w = orc.gen_weights(fmt, 500 + n, n, k)
+    X = orc.gen_normal(501 + m, m * k)
+    got = zq.gemm(fmt, w, X, m, n, k, zq.ACT_INT8)
+    assert_close(got, orc.gemm_i8(fmt, w, X, m, n, k), f"gemm_i8 fmt={fmt} {m}x{n}x{k}")
+    zq.release(w)
+
+
+@pytest.mark.parametrize("fmt,rows,cols", _GEMV_SHAPES)
+def test_gemv_random_shapes(zq, orc, fmt, rows, cols):
+    w = orc.gen_weights(fmt, 600 + rows, rows, cols)
+    x = orc.gen_normal(601 + cols, cols)
+    got = zq.gemv(fmt, w, x, rows, cols)
+    assert_close(got, orc.gemv_f32(fmt, w, x, rows, cols), f"gemv fmt={fmt} {rows}x{cols}")
+    zq.release(w)
