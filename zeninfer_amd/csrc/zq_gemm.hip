@@ -16,13 +16,20 @@
 //    are dequantised exactly into LDS (the reference's dequantize values) and
 //    multiplied with v_mfma_f32_32x32x2_f32 in fp32.
 //
-// Tiling: a 256-thread workgroup computes a 128 (tokens) x 128 (weight rows)
-// tile with 4 waves in 2x2, each wave 2x2 MFMA tiles of 32x32.  Weight rows
-// are read in their native GGML layout and converted while being staged into
-// LDS (one conversion per weight element per workgroup, amortised over 128
-// tokens).  Workgroup ids are remapped so that the workgroups a given XCD
-// receives (ids congruent mod 8) walk the token tiles of one weight panel
-// before moving on, keeping that panel in the XCD's L2.
+// Kernels (int8 mode):
+//  * gemm_i8_direct4_kernel / gemm_i8_direct8_kernel (K % 256 == 0, M > 64):
+//    128 (tokens) x 128 (weight rows) tiles, 8 waves of 64x32; activations,
+//    raw weight blocks and scales stream straight from HBM into LDS
+//    (buffer_load ... lds), double-buffered by 4 (or 8) K blocks; the B
+//    operand is assembled per lane from the raw Q8_0 / Q4_0 blocks;
+//  * gemm_i8_small_kernel (K % 256 == 0, M <= 64): the same body with
+//    32-token tiles, 4 waves;
+//  * gemm_i8_kernel (any K % 64 == 0): 4 waves of 2x2 MFMA tiles, weights
+//    converted while staged through registers into LDS.
+// Small grids split K; the partial sums are reduced in a fixed order.
+// Workgroup ids are remapped so that the workgroups a given XCD receives
+// (ids congruent mod 8) walk the token tiles of one weight panel before
+// moving on, keeping that panel in the XCD's L2.
 #include "zq_device.hpp"
 #include "zq_internal.hpp"
 
