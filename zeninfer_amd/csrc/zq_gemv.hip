@@ -29,10 +29,14 @@
 // values and their two sums stay in VGPRs, so per row the lane needs only
 // sum(q*x) per group: w*x summed = (d*sc)*sum(q*x) - (dmin*m)*sum(x).
 //
-// Q6_K: one lane owns a 16-element unit (half h, l-quad l0) of a super-block:
-// 3 data dwords (ql low/high streams and qh), 4 int8 sub-scales and d.  The
-// four 4-element groups are decoded byte-parallel: q = lo4 | hi2 << 4, then
-// ((q ^ 0x20) << 2) is 4*(q-32) as a signed byte.
+// Q6_K, fallback kernel: one lane owns a 16-element unit (half h, l-quad l0)
+// of a super-block: 3 data dwords (ql low/high streams and qh), 4 int8
+// sub-scales and d.  The four 4-element groups are decoded byte-parallel:
+// q = lo4 | hi2 << 4, then ((q ^ 0x20) << 2) is 4*(q-32) as a signed byte.
+// The streaming Q6_K kernel (cols % 2048 == 0) instead gives each lane 16
+// consecutive elements of one quarter (one sub-block scale), builds the
+// 6-bit codes four per dword and feeds them as binary16 denormals to
+// v_fma_mix_f32; see gemv_q6k_stream_kernel.
 #include "zq_device.hpp"
 #include "zq_internal.hpp"
 
