@@ -110,6 +110,9 @@ GEMV_SHAPES = [
     (O.Q6_K, 1000, 4096), (O.Q6_K, 7, 14336), (O.Q6_K, 3, 256),
     (O.Q4_K, 1000, 4096), (O.Q4_K, 4097, 4096), (O.Q4_K, 7, 14336), (O.Q4_K, 3, 256),
     (O.Q5_K, 1000, 4096), (O.Q5_K, 9, 14336), (O.Q5_K, 5, 11008), (O.Q5_K, 2, 768),
+    # every slice count of the Q6_K / K-quant streaming kernels (2048 columns per slice)
+    (O.Q6_K, 33, 8192), (O.Q6_K, 9, 10240), (O.Q6_K, 4100, 16384),
+    (O.Q4_K, 33, 8192), (O.Q5_K, 9, 10240), (O.Q4_K, 17, 16384),
     # widths past the streaming kernels' 16384 (fallback kernels)
     (O.Q8_0, 17, 32768), (O.Q4_0, 9, 20480), (O.Q6_K, 5, 24576), (O.Q4_K, 9, 24576), (O.Q5_K, 3, 18432),
 ]
