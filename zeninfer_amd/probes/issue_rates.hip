@@ -34,6 +34,10 @@ template <int KIND>
 __global__ void mix(float* out, unsigned long long* cyc, int seed) {
     extern __shared__ float reserve[];
     if (seed == 12345) reserve[threadIdx.x] = 1.0f;  // never true; keeps the reservation live
+    float* lds_pool = reserve;  // 64 KiB of the reservation, filled below for KIND 10
+    if constexpr (KIND == 10) {
+        for (int i = threadIdx.x; i < 16384; i += blockDim.x) lds_pool[i] = float(i & 127);
+    }
     v4i a = {seed, seed + 1, seed + 2, int(threadIdx.x)};
     v16i ci[4] = {};
     v16f cf[4] = {};
@@ -73,6 +77,30 @@ __global__ void mix(float* out, unsigned long long* cyc, int seed) {
                 for (int r = 0; r < (KIND == 5 ? 1 : 3); ++r)
 #pragma unroll
                     for (int q = 0; q < 16; ++q) acc[q] = fmaf(acc[q], y, x3);
+            }
+        } else if constexpr (KIND == 10) {
+            // the unit of KIND 8 with its operands read from LDS as the GEMM
+            // does per block: two ds_read_b128 (A of both tiles), five dwords
+            // of raw weights (B, with four v_alignbyte), a u16 weight scale and
+            // an activation scale
+            const v16i zero = {};
+            const v32f szero = {};
+            const int base = (int(threadIdx.x) * 5 + it * 64) & 0x3FFF;
+            const v4i a0 = *reinterpret_cast<const v4i*>(&lds_pool[(base & ~3) + 0]);
+            const v4i a1 = *reinterpret_cast<const v4i*>(&lds_pool[(base & ~3) + 4096]);
+            unsigned t5[5];
+            for (int i = 0; i < 5; ++i) t5[i] = reinterpret_cast<const unsigned*>(lds_pool)[(base + 8192 + i) & 0x3FFF];
+            const unsigned dwh = reinterpret_cast<const unsigned short*>(lds_pool)[base & 0x7FFF];
+            const float dx = lds_pool[(base + 12288) & 0x3FFF];
+            v4i w;
+            for (int i = 0; i < 4; ++i) w[i] = int(__builtin_amdgcn_alignbyte(t5[i + 1], t5[i], 2));
+            v16i n0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, w, zero, 0, 0, 0);
+            v16i n1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, w, zero, 0, 0, 0);
+            v32f ns = __builtin_amdgcn_mfma_f32_32x32x1f32(dx, float(dwh), szero, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                acc[v] = fmaf(float(n0[v]), ns[v], acc[v]);
+                acc2[v] = fmaf(float(n1[v]), ns[16 + v], acc2[v]);
             }
         } else if constexpr (KIND == 8 || KIND == 9) {
             // the int8 GEMM's per-block unit for a wave's two 32x32 tiles: two
@@ -159,6 +187,7 @@ int main() {
         run<7>("f32 2b MFMA + 16 fma (per MFMA)", w, 4, cus);
         run<8>("GEMM block unit, dependent (per unit)", w, 1, cus);
         run<9>("GEMM block unit, pipelined (per unit)", w, 1, cus);
+        run<10>("GEMM block unit + its LDS reads", w, 1, cus);
     }
     return 0;
 }
