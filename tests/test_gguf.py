@@ -273,6 +273,29 @@ def test_differential_structured_mutations(ref):
     assert n_ok > 100 and n_err > 100  # both outcomes exercised
 
 
+def test_differential_every_truncation(ref):
+    """Every prefix of a small, metadata-rich image (all value types, nested
+    arrays, a tensor directory and payloads): same verdict and description as
+    the reference, never a crash."""
+    w = G.GGUFWriter()
+    w.add_meta("general.architecture", G.STRING, "llama")
+    w.add_meta("llama.embedding_length", G.U32, 32)
+    w.add_meta("general.alignment", G.U32, 32)
+    w.add_meta("general.i16", G.I16, -7)
+    w.add_meta("general.u64", G.U64, 2 ** 40)
+    w.add_meta("general.f64", G.F64, -2.25)
+    w.add_meta("general.flag", G.BOOL, 0)
+    w.add_meta("tokenizer.ggml.tokens", G.ARRAY, (G.STRING, ["x", "yy", ""]))
+    w.add_meta("general.nested", G.ARRAY, (G.ARRAY, [(G.I32, [1, -2]), (G.F32, [0.5])]))
+    w.add_tensor("t0", [32, 2], G.GGML_Q8_0, bytes(range(68)))
+    w.add_tensor("t1", [32], G.GGML_F32, bytes(128))
+    img = w.to_bytes()
+    assert ref_describe(ref, img) == our_describe(img)
+    for n in range(len(img)):
+        r, o = ref_describe(ref, img[:n]), our_describe(img[:n])
+        assert r == o, (n, r[:200], o[:200])
+
+
 @pytest.mark.parametrize("q5", [False, True])
 def test_kquant_writer_round_trip(q5):
     """The writer's K-quant packer (the inverse of k_scale_min) read back by
