@@ -87,8 +87,8 @@ def summarize_trace(path):
 def pmc_workload():
     """Few launches for rocprofv3 --pmc passes: a 256 MiB device copy (counter
     calibration), the 4096x14336 Q8_0 down GEMV on 4 distinct matrices, the
-    int8 GEMM at M=2048 on 3 distinct 14336x4096 matrices and the Q4_K GEMV
-    14336x4096 on 3 distinct matrices."""
+    int8 GEMM at M=2048 on 3 distinct 14336x4096 matrices, and the Q4_K and Q6_K
+    GEMVs 14336x4096 on 3 distinct matrices each."""
     import torch
     from zeninfer_amd import zq
     zq.init()
@@ -133,6 +133,17 @@ def pmc_workload():
     torch.cuda.synchronize()
     for t in wk:
         zq.gemv_dev(zq.Q4_K, t, x[:HIDDEN], yk, FFN, HIDDEN)
+    torch.cuda.synchronize()
+    del wk
+    # Q6_K GEMV 14336x4096 on 3 distinct matrices (the Q6_K streaming kernel)
+    w6 = []
+    for i in range(3):
+        t = torch.empty(zq.weight_bytes(zq.Q6_K, FFN, HIDDEN), dtype=torch.uint8, device=dev)
+        zq.synth_weights_dev(zq.Q6_K, 80 + i, t, FFN, HIDDEN)
+        w6.append(t)
+    torch.cuda.synchronize()
+    for t in w6:
+        zq.gemv_dev(zq.Q6_K, t, x[:HIDDEN], yk, FFN, HIDDEN)
     torch.cuda.synchronize()
 
 
