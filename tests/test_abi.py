@@ -85,3 +85,24 @@ def test_opt_in_semantics(monkeypatch):
     assert L.zq_hip_opted_in() == 0
     monkeypatch.setenv("ZEN_HIP", "1")
     assert L.zq_hip_opted_in() == 1
+
+
+def test_device_wrappers_reject_short_buffers():
+    """The Python device-pointer wrappers refuse a tensor shorter than the
+    call's sizes (the kernels would run past its end) before any library call."""
+    import torch
+    from zeninfer_amd import zq
+    wb = zq.weight_bytes(zq.Q8_0, 64, 256)
+    w = torch.empty(wb, dtype=torch.uint8)
+    with pytest.raises(ValueError, match="gemm_dev X"):
+        zq.gemm_dev(zq.Q8_0, w, torch.empty(3 * 256 - 1), torch.empty(3 * 64), 3, 64, 256)
+    with pytest.raises(ValueError, match="gemm_dev weights"):
+        zq.gemm_dev(zq.Q8_0, w[:-1], torch.empty(3 * 256), torch.empty(3 * 64), 3, 64, 256)
+    with pytest.raises(ValueError, match="gemv_dev y"):
+        zq.gemv_dev(zq.Q8_0, w, torch.empty(256), torch.empty(63), 64, 256)
+    with pytest.raises(ValueError, match="gemv_batch_dev weights"):
+        zq.gemv_batch_dev(zq.Q8_0, torch.empty(256), [(w, torch.empty(64), 64), (w, torch.empty(65), 65)], 256)
+    with pytest.raises(ValueError, match="quantize_acts_dev xs"):
+        zq.quantize_acts_dev(torch.empty(2 * 256), torch.empty(512, dtype=torch.int8), torch.empty(15), 2, 256)
+    with pytest.raises(ValueError, match="contiguous"):
+        zq.synth_normal_dev(1, torch.empty(8, 8).t(), 64)

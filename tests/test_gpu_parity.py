@@ -58,12 +58,13 @@ def test_dequantize_bit_exact(zq, orc, fmt, rows, cols):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
-def test_quantize_acts_bit_exact(zq, orc):
-    m, k = 37, 4096
+@pytest.mark.parametrize("m,k", [(37, 4096), (3, 96)])  # the second leaves most of the last workgroup idle
+def test_quantize_acts_bit_exact(zq, orc, m, k):
     x = orc.gen_normal(7, m * k)
     x[:32] = [127, 2.5, -2.5, 0.5, -0.5, 1.5, -1.5, 126.5] + [0.0] * 24   # exact ties
     x[32:64] = 0.0                                                          # amax == 0
     x[64:96] = np.float32(1e-30)
+    x[m * k - 32:m * k - 24] = [-300.0, 1.0, 2.0, 3.0, 4.0, 5.0, 6.0, 7.0]  # amax in the block's first lane
     xd = to_dev(x)
     xq = torch.empty(m * k, dtype=torch.int8, device=DEV)
     xs = torch.empty(m * k // 32, dtype=torch.float32, device=DEV)

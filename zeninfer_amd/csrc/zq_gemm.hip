@@ -56,48 +56,44 @@ constexpr int KB = 8;               // 32-element blocks per K stage
 constexpr int ROWB = KB * 32 + 16;  // LDS bytes per tile row (16 B pad)
 
 // ------------------------------------------------- activation quantiser ---
-// One thread per 32-element block.  Bit-exact with kernels/avx2.cpp:502-524.
+// Bit-exact with kernels/avx2.cpp:502-524.
 __device__ __forceinline__ int round_half_away(float v) {
     const float t = truncf(v);
     const float f = v - t;  // exact for |v| < 2^23
     return static_cast<int>(t) + (f >= 0.5f ? 1 : (f <= -0.5f ? -1 : 0));
 }
 
+// Eight lanes per block, four elements each (a coalesced float4 load and a
+// 4-byte store per lane); the block's amax is the max over its eight lanes
+// (DPP, exact), so d, 1/d and every quant equal the one-thread-per-block form.
 __global__ __launch_bounds__(kThreads) void quantize_acts_kernel(const float* __restrict__ X, int8_t* __restrict__ xq,
                                                                  float* __restrict__ xs, size_t nblocks) {
-    const size_t b = size_t(blockIdx.x) * kThreads + threadIdx.x;
-    if (b >= nblocks) return;
-    const float4* src = reinterpret_cast<const float4*>(X + b * 32);
-    float v[32];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const float4 t = src[i];
-        v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
-    }
+    const size_t g = size_t(blockIdx.x) * kThreads + threadIdx.x;  // lane's 4-element group
+    const size_t b = g >> 3;
+    const bool live = b < nblocks;
+    const float4 t = live ? reinterpret_cast<const float4*>(X)[g] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const float v[4] = {t.x, t.y, t.z, t.w};
     float amax = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) {
+    for (int i = 0; i < 4; ++i) {
         const float a = fabsf(v[i]);
         amax = a > amax ? a : amax;
     }
+    amax = fmaxf(amax, dpp_f<kDppXor1>(amax));  // |x| >= 0, so fmaxf is the same max
+    amax = fmaxf(amax, dpp_f<kDppXor2>(amax));
+    amax = fmaxf(amax, dpp_f<kDppHalfMirror>(amax));
+    if (!live) return;
     const float d = amax > 0.0f ? amax / 127.0f : 0.0f;
     const float inv = d > 0.0f ? 1.0f / d : 0.0f;
-    xs[b] = d;
-    uint32_t packed[8];
+    if ((g & 7) == 0) xs[b] = d;
+    uint32_t w = 0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        uint32_t w = 0;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            float t = v[4 * i + k] * inv;
-            t = t > 127.0f ? 127.0f : (t < -127.0f ? -127.0f : t);
-            w |= (uint32_t(round_half_away(t)) & 0xffu) << (8 * k);
-        }
-        packed[i] = w;
+    for (int k = 0; k < 4; ++k) {
+        float q = v[k] * inv;
+        q = q > 127.0f ? 127.0f : (q < -127.0f ? -127.0f : q);
+        w |= (uint32_t(round_half_away(q)) & 0xffu) << (8 * k);
     }
-    uint4* dst = reinterpret_cast<uint4*>(xq + b * 32);
-    dst[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
-    dst[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
+    reinterpret_cast<uint32_t*>(xq)[g] = w;
 }
 
 // ------------------------------------------------------- tile mapping ---
@@ -346,13 +342,28 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_i8_kernel(const uint8_t* __r
         }
 }
 
+// Y = sum of the ksplit partial planes in split order; four outputs a thread
+// (float4) when n % 4 == 0 and both buffers are 16-byte aligned, else one.
+template <bool VEC4>
 __global__ __launch_bounds__(kThreads) void splitk_reduce_kernel(const float* __restrict__ part, float* __restrict__ Y,
                                                                  size_t n, uint32_t ksplit) {
     const size_t i = size_t(blockIdx.x) * kThreads + threadIdx.x;
-    if (i >= n) return;
-    float acc = part[i];
-    for (uint32_t s = 1; s < ksplit; ++s) acc += part[size_t(s) * n + i];
-    Y[i] = acc;
+    if constexpr (VEC4) {
+        const size_t n4 = n / 4;
+        if (i >= n4) return;
+        const float4* p = reinterpret_cast<const float4*>(part);
+        float4 acc = p[i];
+        for (uint32_t s = 1; s < ksplit; ++s) {
+            const float4 t = p[size_t(s) * n4 + i];
+            acc.x += t.x; acc.y += t.y; acc.z += t.z; acc.w += t.w;
+        }
+        reinterpret_cast<float4*>(Y)[i] = acc;
+    } else {
+        if (i >= n) return;
+        float acc = part[i];
+        for (uint32_t s = 1; s < ksplit; ++s) acc += part[size_t(s) * n + i];
+        Y[i] = acc;
+    }
 }
 
 // Q8_0 int8 GEMM with direct-to-LDS staging (K % 256 == 0, 16 B aligned
@@ -781,7 +792,7 @@ hipError_t launch_quantize_acts(const float* X, int8_t* xq, float* xs, size_t M,
     if (!X || !xq || !xs || !M || !K || K % 32) return hipErrorInvalidValue;
     if ((reinterpret_cast<uintptr_t>(X) & 15u) || (reinterpret_cast<uintptr_t>(xq) & 15u)) return hipErrorInvalidValue;
     const size_t nblocks = M * (K / 32);
-    const size_t grid = (nblocks + kThreads - 1) / kThreads;
+    const size_t grid = (nblocks * 8 + kThreads - 1) / kThreads;
     hipLaunchKernelGGL(quantize_acts_kernel, dim3(static_cast<uint32_t>(grid)), dim3(kThreads), 0, stream, X, xq, xs,
                        nblocks);
     return hipGetLastError();
@@ -873,8 +884,14 @@ static hipError_t finish_splits(hipError_t e, const float* partial, float* Y, si
                                 hipStream_t stream) {
     if (e != hipSuccess || ks <= 1) return e;
     const size_t total = M * N;
-    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(static_cast<uint32_t>((total + kThreads - 1) / kThreads)),
-                       dim3(kThreads), 0, stream, partial, Y, total, ks);
+    const bool vec4 = total % 4 == 0 && !(reinterpret_cast<uintptr_t>(partial) & 15u) &&
+                      !(reinterpret_cast<uintptr_t>(Y) & 15u);
+    if (vec4)
+        hipLaunchKernelGGL(splitk_reduce_kernel<true>, dim3(static_cast<uint32_t>((total / 4 + kThreads - 1) / kThreads)),
+                           dim3(kThreads), 0, stream, partial, Y, total, ks);
+    else
+        hipLaunchKernelGGL(splitk_reduce_kernel<false>, dim3(static_cast<uint32_t>((total + kThreads - 1) / kThreads)),
+                           dim3(kThreads), 0, stream, partial, Y, total, ks);
     return hipGetLastError();
 }
 

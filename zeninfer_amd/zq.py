@@ -172,6 +172,20 @@ def _dptr(t):
     return t.data_ptr()
 
 
+def _need(t, nbytes, what):
+    """A torch tensor passed as a device buffer must be contiguous and hold at
+    least nbytes: the kernels index it from the sizes alone, so a short buffer
+    would be read or written past its end.  Raw addresses are the caller's
+    responsibility."""
+    if t is None or isinstance(t, int):
+        return
+    if not t.is_contiguous():
+        raise ValueError(f"{what}: tensor must be contiguous")
+    have = t.numel() * t.element_size()
+    if have < nbytes:
+        raise ValueError(f"{what}: buffer holds {have} bytes, the call needs {nbytes}")
+
+
 def _stream(stream):
     if stream is None:
         return None
@@ -258,12 +272,19 @@ def release_all():
 
 # ---- device-pointer API (torch tensors or raw addresses) ------------------
 def gemv_dev(fmt, w, x, y, rows, cols, stream=None):
+    _need(w, weight_bytes(fmt, rows, cols), "gemv_dev weights")
+    _need(x, 4 * cols, "gemv_dev x")
+    _need(y, 4 * rows, "gemv_dev y")
     return check(lib().zq_hip_gemv_dev(fmt, _dptr(w), _dptr(x), _dptr(y), rows, cols, _stream(stream)),
                  "zq_hip_gemv_dev")
 
 
 def gemv_batch_dev(fmt, x, tasks, cols, stream=None):
     """tasks: list of (weights, y, rows)."""
+    _need(x, 4 * cols, "gemv_batch_dev x")
+    for w, y, r in tasks:
+        _need(w, weight_bytes(fmt, r, cols), "gemv_batch_dev weights")
+        _need(y, 4 * r, "gemv_batch_dev y")
     arr = (GemvTask * len(tasks))(*[GemvTask(_dptr(w), _dptr(y), r) for w, y, r in tasks])
     return check(lib().zq_hip_gemv_batch_dev(fmt, _dptr(x), arr, len(tasks), cols, _stream(stream)),
                  "zq_hip_gemv_batch_dev")
@@ -274,29 +295,43 @@ def gemm_workspace_bytes(fmt, tokens, rows, cols, act=ACT_DEFAULT):
 
 
 def gemm_dev(fmt, w, X, Y, tokens, rows, cols, act=ACT_DEFAULT, workspace=None, workspace_bytes=0, stream=None):
+    _need(w, weight_bytes(fmt, rows, cols), "gemm_dev weights")
+    _need(X, 4 * tokens * cols, "gemm_dev X")
+    _need(Y, 4 * tokens * rows, "gemm_dev Y")
+    _need(workspace, workspace_bytes, "gemm_dev workspace")
     return check(lib().zq_hip_gemm_dev(fmt, _dptr(w), _dptr(X), _dptr(Y), tokens, rows, cols, act,
                                        _dptr(workspace), workspace_bytes, _stream(stream)), "zq_hip_gemm_dev")
 
 
 def quantize_acts_dev(X, xq, xs, tokens, cols, stream=None):
+    _need(X, 4 * tokens * cols, "quantize_acts_dev X")
+    _need(xq, tokens * cols, "quantize_acts_dev xq")
+    _need(xs, 4 * tokens * (cols // 32), "quantize_acts_dev xs")
     return check(lib().zq_hip_quantize_acts_dev(_dptr(X), _dptr(xq), _dptr(xs), tokens, cols, _stream(stream)),
                  "zq_hip_quantize_acts_dev")
 
 
 def block_dots_dev(fmt, w, xq, out, tokens, rows, cols, stream=None):
+    _need(w, weight_bytes(fmt, rows, cols), "block_dots_dev weights")
+    _need(xq, tokens * cols, "block_dots_dev xq")
+    _need(out, 4 * tokens * rows * (cols // 32), "block_dots_dev out")
     return check(lib().zq_hip_block_dots_dev(fmt, _dptr(w), _dptr(xq), _dptr(out), tokens, rows, cols,
                                              _stream(stream)), "zq_hip_block_dots_dev")
 
 
 def dequantize_dev(fmt, w, out, rows, cols, stream=None):
+    _need(w, weight_bytes(fmt, rows, cols), "dequantize_dev weights")
+    _need(out, 4 * rows * cols, "dequantize_dev out")
     return check(lib().zq_hip_dequantize_dev(fmt, _dptr(w), _dptr(out), rows, cols, _stream(stream)),
                  "zq_hip_dequantize_dev")
 
 
 def synth_weights_dev(fmt, seed, w, rows, cols, stream=None):
+    _need(w, weight_bytes(fmt, rows, cols), "synth_weights_dev weights")
     return check(lib().zq_hip_synth_weights_dev(fmt, seed, _dptr(w), rows, cols, _stream(stream)),
                  "zq_hip_synth_weights_dev")
 
 
 def synth_normal_dev(seed, out, n, stream=None):
+    _need(out, 4 * n, "synth_normal_dev out")
     return check(lib().zq_hip_synth_normal_dev(seed, _dptr(out), n, _stream(stream)), "zq_hip_synth_normal_dev")
