@@ -87,11 +87,28 @@ def test_opt_in_semantics(monkeypatch):
     assert L.zq_hip_opted_in() == 1
 
 
-def test_device_wrappers_reject_short_buffers():
-    """The Python device-pointer wrappers refuse a tensor shorter than the
-    call's sizes (the kernels would run past its end) before any library call."""
+def test_device_wrappers_reject_host_tensors():
+    """A host tensor handed to a device entry point is refused before any
+    library call: its address would reach a kernel and fault the GPU."""
     import torch
     from zeninfer_amd import zq
+    wb = zq.weight_bytes(zq.Q8_0, 64, 256)
+    with pytest.raises(ValueError, match="gemv_dev weights: tensor must be on the GPU"):
+        zq.gemv_dev(zq.Q8_0, torch.empty(wb, dtype=torch.uint8), torch.empty(256), torch.empty(64), 64, 256)
+    with pytest.raises(ValueError, match="synth_normal_dev out: tensor must be on the GPU"):
+        zq.synth_normal_dev(1, torch.empty(64), 64)
+    with pytest.raises(ValueError, match="gemm_dev workspace: tensor must be on the GPU"):
+        zq.gemm_dev(zq.Q8_0, 1 << 20, 2 << 20, 3 << 20, 3, 64, 256, zq.ACT_INT8, torch.empty(16), 64)
+
+
+def test_device_wrappers_reject_short_buffers(monkeypatch):
+    """The Python device-pointer wrappers refuse a tensor shorter than the
+    call's sizes (the kernels would run past its end) before any library call.
+    Host tensors stand in for device ones here (the device check is bypassed:
+    no GPU on the CPU runner)."""
+    import torch
+    from zeninfer_amd import zq
+    monkeypatch.setattr(zq, "_check_device", lambda t, what: None)
     wb = zq.weight_bytes(zq.Q8_0, 64, 256)
     w = torch.empty(wb, dtype=torch.uint8)
     with pytest.raises(ValueError, match="gemm_dev X"):

@@ -17,10 +17,10 @@
 //    multiplied with v_mfma_f32_32x32x2_f32 in fp32.
 //
 // Kernels (int8 mode):
-//  * gemm_i8_direct4_kernel / gemm_i8_direct8_kernel (K % 256 == 0, M > 64):
+//  * gemm_i8_direct4_kernel (K % 256 == 0, M > 64):
 //    128 (tokens) x 128 (weight rows) tiles, 8 waves of 64x32; activations,
 //    raw weight blocks and scales stream straight from HBM into LDS
-//    (buffer_load ... lds), double-buffered by 4 (or 8) K blocks; the B
+//    (buffer_load ... lds), double-buffered by 4 K blocks; the B
 //    operand is assembled per lane from the raw Q8_0 / Q4_0 blocks;
 //  * gemm_i8_small_kernel (K % 256 == 0, M <= 64): the same body with
 //    32-token tiles, 4 waves;
@@ -48,10 +48,6 @@ typedef float v32f __attribute__((ext_vector_type(32)));
 constexpr int kThreads = 256;
 constexpr int BM = 128;             // tokens per tile
 constexpr int BN = 128;             // weight rows per tile
-#ifndef ZQ_GEMM_DIAG
-#define ZQ_GEMM_DIAG 0  // diagnostic builds only: bit 0 thins the epilogue, bit 1 drops the K streaming,
-                        // bit 2 records per-workgroup timestamps past the end of Y
-#endif
 constexpr int KB = 8;               // 32-element blocks per K stage
 constexpr int ROWB = KB * 32 + 16;  // LDS bytes per tile row (16 B pad)
 
@@ -579,10 +575,6 @@ __device__ __forceinline__ void gemm_i8_direct_body(
     // Accumulates block r; sc/half name its dx*dw products (WM = 1: the pair's
     // odd block and this block's half of it; WM = 2: r itself).
     auto retire = [&](const Blk& r, const Blk& sc, int half) {
-#if ZQ_GEMM_DIAG & 1
-#pragma unroll
-        for (int i = 0; i < WM; ++i) acc[i][0] = fmaf(float(r.c[i][0] ^ r.c[i][15]), r.s[16 * i] + r.s[16 * i + 15], acc[i][0]);
-#else
         if constexpr (WM == 2) {
 #pragma unroll
             for (int i = 0; i < 2; ++i)
@@ -592,23 +584,15 @@ __device__ __forceinline__ void gemm_i8_direct_body(
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[0][v] = fmaf(float(r.c[0][v]), sc.s[16 * half + v], acc[0][v]);
         }
-#endif
     };
 
     if (kb_begin >= kb_end) return;
-#if ZQ_GEMM_DIAG & 4
-    const uint64_t diag_c0 = __builtin_amdgcn_s_memtime(), diag_t0 = __builtin_amdgcn_s_memrealtime();
-#endif
     stage_in(kb_begin, 0);
     int buf = 0;
     for (uint32_t kb = kb_begin; kb < kb_end; kb += QKB, buf ^= 1) {
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's direct loads of stage kb landed
         __syncthreads();                     // ... and everyone's; the other buffer is free again
-#if ZQ_GEMM_DIAG & 2
-        if (kb == kb_begin && kb + QKB < kb_end) stage_in(kb + QKB, buf ^ 1);
-#else
         if (kb + QKB < kb_end) stage_in(kb + QKB, buf ^ 1);
-#endif
         const uint8_t* base = lds + buf * G::BUF;
         // Waves sharing a SIMD start the stage at different block pairs, so
         // one wave's MFMAs overlap the other's VALU epilogue instead of both
@@ -666,28 +650,8 @@ __device__ __forceinline__ void gemm_i8_direct_body(
             const uint32_t m = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
             if (m < M && n < N) Yout[size_t(m) * N + n] = acc[i][v];
         }
-#if ZQ_GEMM_DIAG & 4
-    // diagnostic builds only: start/end ticks, shader cycles and hardware ids
-    // of this workgroup, written past the end of Y
-    __syncthreads();
-    if (tid == 0) {
-        uint64_t* o = reinterpret_cast<uint64_t*>(Y + size_t(ksplit) * M * N) + 4 * blockIdx.x;  // caller over-allocates Y (or the split-K workspace)
-        o[0] = diag_t0;
-        o[1] = __builtin_amdgcn_s_memrealtime();
-        o[2] = __builtin_amdgcn_s_memtime() - diag_c0;
-        o[3] = (uint64_t(__builtin_amdgcn_s_getreg((23 << 0) | (0 << 6) | (31 << 11))) << 32) |  // XCC_ID
-               __builtin_amdgcn_s_getreg((4 << 0) | (0 << 6) | (31 << 11));                    // HW_ID
-    }
-#endif
 }
 
-template <int FMT, bool DOTS>
-__global__ __launch_bounds__(QTH, 2) void gemm_i8_direct8_kernel(
-    const uint8_t* __restrict__ W, const int8_t* __restrict__ XQ, const float* __restrict__ XS,
-    float* __restrict__ Y, int32_t* __restrict__ dots, uint32_t M, uint32_t N, uint32_t K, uint32_t tiles_m,
-    uint32_t tiles_n, uint32_t ksplit, uint32_t stages_per_split) {
-    gemm_i8_direct_body<FMT, DOTS, 8>(W, XQ, XS, Y, dots, M, N, K, tiles_m, tiles_n, ksplit, stages_per_split);
-}
 template <int FMT, bool DOTS>
 __global__ __launch_bounds__(QTH, 4) void gemm_i8_direct4_kernel(
     const uint8_t* __restrict__ W, const int8_t* __restrict__ XQ, const float* __restrict__ XS,
@@ -798,17 +762,13 @@ hipError_t launch_quantize_acts(const float* X, int8_t* xq, float* xs, size_t M,
     return hipGetLastError();
 }
 
-// Split factor so the grid reaches about two workgroups per CU (the LDS
-// budget allows two), keeping at least two K stages per split.
-static uint32_t choose_ksplit(uint32_t tiles, uint32_t nb, uint32_t kb = KB) {
-    static const int forced = [] {
-        const char* e = getenv("ZQ_GEMM_KSPLIT");
-        return e ? atoi(e) : 0;
-    }();
-    const uint32_t stages = (nb + kb - 1) / kb;
-    uint32_t ks = forced > 0 ? uint32_t(forced) : (512 + tiles - 1) / tiles;
-    ks = std::max(1u, std::min(ks, std::max(1u, stages / 2)));
-    return ks;
+// Split factor of the staged-conversion kernel: the grid reaches about two
+// workgroups per CU (the LDS budget allows two), keeping at least two K
+// stages per split.
+static uint32_t choose_ksplit(uint32_t tiles, uint32_t nb) {
+    const uint32_t stages = (nb + KB - 1) / KB;
+    const uint32_t ks = (512 + tiles - 1) / tiles;
+    return std::max(1u, std::min(ks, std::max(1u, stages / 2)));
 }
 
 // Split factor of the 4-block direct-load kernels, from a cost model fitted
@@ -824,11 +784,6 @@ struct StageCost {
 constexpr StageCost kTileCost{2.5, 2.0};
 constexpr StageCost kSmallTileCost{1.0, 0.6};
 static uint32_t choose_ksplit_model(uint32_t tiles, uint32_t stages, size_t M, size_t N, StageCost c = kTileCost) {
-    static const int forced = [] {
-        const char* e = getenv("ZQ_GEMM_KSPLIT");
-        return e ? atoi(e) : 0;
-    }();
-    if (forced > 0) return std::max(1u, std::min(uint32_t(forced), stages));
     const double cus = double(device_cu_count());
     uint32_t best = 1;
     double best_t = 1e300;
@@ -846,38 +801,20 @@ static uint32_t choose_ksplit_model(uint32_t tiles, uint32_t stages, size_t M, s
 size_t gemm_i8_partial_bytes(size_t M, size_t N, size_t K) {
     const uint32_t tiles = uint32_t(((M + BM - 1) / BM) * ((N + BN - 1) / BN));
     const uint32_t nb = uint32_t(K / 32);
-    // sized for every kernel choice: either stage depth of the direct-load
-    // kernel (4 or 8 blocks) and the staged-conversion kernel
+    // sized for every kernel choice: the direct-load kernels (128- and
+    // 32-token tiles) and the staged-conversion kernel
     const uint32_t small_tiles = uint32_t(((M + 31) / 32) * ((N + BN - 1) / BN));
-    const uint32_t ks = std::max({choose_ksplit(tiles, nb, 8), choose_ksplit(tiles, nb, 4),
+    const uint32_t ks = std::max({choose_ksplit(tiles, nb),
                                   choose_ksplit_model(tiles, (nb + 3) / 4, M, N),
                                   choose_ksplit_model(small_tiles, (nb + 3) / 4, M, N, kSmallTileCost)});
     return ks > 1 ? size_t(ks) * M * N * sizeof(float) : 0;
 }
 
-// Blocks per K stage of the direct-load kernel (ZQ_GEMM_KB = 4 or 8).  4
-// (72 KB of LDS, two workgroups = 16 waves per CU) measured faster at every
-// M than 8 (144 KB, one workgroup): 531 vs 472 TOPS at M = 2048.
-static int coalesced_kb() {
-    static const int v = [] {
-        const char* e = getenv("ZQ_GEMM_KB");
-        const int k = e ? atoi(e) : 0;
-        return k == 8 ? 8 : 4;
-    }();
-    return v;
-}
-
-// Largest M that takes the 32-token tile (ZQ_GEMM_SMALL_M, default 64; 0
-// turns it off).  Measured crossover at 14336x4096 and 4096x14336: the
-// 32-token tile is faster at M = 48 and 64 (36-39 vs 41-43 us), slower from
-// M = 96 (46-49 vs 45-46 us), where its token tiles re-read each weight panel.
-static size_t small_m_limit() {
-    static const size_t v = [] {
-        const char* e = getenv("ZQ_GEMM_SMALL_M");
-        return e ? size_t(atoi(e)) : size_t(64);
-    }();
-    return v;
-}
+// Largest M that takes the 32-token tile.  Measured crossover at 14336x4096
+// and 4096x14336: the 32-token tile is faster at M = 48 and 64 (36-39 vs
+// 41-43 us), slower from M = 96 (46-49 vs 45-46 us), where its token tiles
+// re-read each weight panel.
+constexpr size_t kSmallMLimit = 64;
 
 // Reduces the K splits of `partial` into Y (fixed order) when ks > 1.
 static hipError_t finish_splits(hipError_t e, const float* partial, float* Y, size_t M, size_t N, uint32_t ks,
@@ -903,10 +840,9 @@ static hipError_t launch_direct(const uint8_t* w, const int8_t* xq, const float*
     constexpr int BB = FMT == kQ8_0 ? 34 : 18;
     constexpr size_t kSmallLds = 2 * QStage<4, 32, 4, BB>::BUF;
     constexpr size_t kLds4 = 2 * QStage<4, BM, QTH / 64, BB>::BUF;
-    constexpr size_t kLds8 = 2 * QStage<8, BM, QTH / 64, BB>::BUF;
     const uint32_t m = uint32_t(M), n = uint32_t(N), k = uint32_t(K), nb = uint32_t(K / 32);
     const uint32_t tiles_n = static_cast<uint32_t>((N + BN - 1) / BN);
-    if (M <= small_m_limit()) {
+    if (M <= kSmallMLimit) {
         const uint32_t stm = uint32_t((M + 31) / 32), sst = (nb + 3) / 4;
         if (dots) {
             hipLaunchKernelGGL((gemm_i8_small_kernel<FMT, true>), dim3(stm * tiles_n), dim3(256), kSmallLds, stream, w, xq,
@@ -921,30 +857,18 @@ static hipError_t launch_direct(const uint8_t* w, const int8_t* xq, const float*
         return finish_splits(hipGetLastError(), partial, Y, M, N, ks, stream);
     }
     const uint32_t tiles_m = static_cast<uint32_t>((M + BM - 1) / BM);
-    const int qkb = coalesced_kb();
-    const uint32_t st = (nb + qkb - 1) / qkb;
+    const uint32_t st = (nb + 3) / 4;
     if (dots) {
-        if (qkb == 4)
-            hipLaunchKernelGGL((gemm_i8_direct4_kernel<FMT, true>), dim3(tiles_m * tiles_n), dim3(QTH), kLds4, stream, w,
-                               xq, xs, Y, dots, m, n, k, tiles_m, tiles_n, 1u, st);
-        else
-            hipLaunchKernelGGL((gemm_i8_direct8_kernel<FMT, true>), dim3(tiles_m * tiles_n), dim3(QTH), kLds8, stream, w,
-                               xq, xs, Y, dots, m, n, k, tiles_m, tiles_n, 1u, st);
+        hipLaunchKernelGGL((gemm_i8_direct4_kernel<FMT, true>), dim3(tiles_m * tiles_n), dim3(QTH), kLds4, stream, w, xq,
+                           xs, Y, dots, m, n, k, tiles_m, tiles_n, 1u, st);
         return hipGetLastError();
     }
-    uint32_t ks = !partial ? 1u
-                  : qkb == 4 ? choose_ksplit_model(tiles_m * tiles_n, st, M, N)
-                             : choose_ksplit(tiles_m * tiles_n, nb, uint32_t(qkb));
+    uint32_t ks = partial ? choose_ksplit_model(tiles_m * tiles_n, st, M, N) : 1u;
     const uint32_t spw = (st + ks - 1) / ks;
     ks = (st + spw - 1) / spw;  // no empty splits
     float* out = ks > 1 ? partial : Y;
-    const dim3 grid(tiles_m * tiles_n * ks);
-    if (qkb == 4)
-        hipLaunchKernelGGL((gemm_i8_direct4_kernel<FMT, false>), grid, dim3(QTH), kLds4, stream, w, xq, xs, out, dots, m,
-                           n, k, tiles_m, tiles_n, ks, spw);
-    else
-        hipLaunchKernelGGL((gemm_i8_direct8_kernel<FMT, false>), grid, dim3(QTH), kLds8, stream, w, xq, xs, out, dots, m,
-                           n, k, tiles_m, tiles_n, ks, spw);
+    hipLaunchKernelGGL((gemm_i8_direct4_kernel<FMT, false>), dim3(tiles_m * tiles_n * ks), dim3(QTH), kLds4, stream, w,
+                       xq, xs, out, dots, m, n, k, tiles_m, tiles_n, ks, spw);
     return finish_splits(hipGetLastError(), partial, Y, M, N, ks, stream);
 }
 
@@ -955,15 +879,11 @@ static hipError_t launch_i8_common(int fmt, const uint8_t* w, const int8_t* xq, 
     if (fmt != kQ8_0 && fmt != kQ4_0) return hipErrorInvalidValue;
     if ((reinterpret_cast<uintptr_t>(w) & 3u) || (reinterpret_cast<uintptr_t>(xq) & 15u)) return hipErrorInvalidValue;
     if (!dots && (!xs || !Y)) return hipErrorInvalidValue;
-    static const bool legacy = [] {
-        const char* e = getenv("ZQ_GEMM_KERNEL");
-        return e && e[0] == 'l';
-    }();
     // The direct-load kernels address a tile with 32-bit offsets from its
     // first row: 129 activation rows and 129 weight rows must stay below 2 GiB.
     const size_t rb = row_bytes(fmt, K);
     const bool offsets_fit = size_t(BM + 1) * K < (size_t(1) << 31) && size_t(BN + 1) * rb < (size_t(1) << 31);
-    if (!legacy && K % 256 == 0 && offsets_fit)
+    if (K % 256 == 0 && offsets_fit)
         return fmt == kQ8_0 ? launch_direct<kQ8_0>(w, xq, xs, Y, dots, partial, M, N, K, stream)
                             : launch_direct<kQ4_0>(w, xq, xs, Y, dots, partial, M, N, K, stream);
 
@@ -983,7 +903,7 @@ static hipError_t launch_i8_common(int fmt, const uint8_t* w, const int8_t* xq, 
                                k, tiles_m, tiles_n, 1u, stages);
         return hipGetLastError();
     }
-    uint32_t ks = partial ? choose_ksplit(tiles_m * tiles_n, nb, uint32_t(KB)) : 1u;
+    uint32_t ks = partial ? choose_ksplit(tiles_m * tiles_n, nb) : 1u;
     const uint32_t spw = (stages + ks - 1) / ks;
     ks = (stages + spw - 1) / spw;  // no empty splits
     float* out = ks > 1 ? partial : Y;
@@ -1008,14 +928,9 @@ hipError_t launch_block_dots(int fmt, const uint8_t* w, const int8_t* xq, int32_
     return launch_i8_common(fmt, w, xq, nullptr, nullptr, out, nullptr, M, N, K, stream);
 }
 
-// Split factor of the fp32-activation GEMM: enough workgroups for two per CU
-// (ZQ_GEMMF_KSPLIT forces one), at least 16 K stages per split.
+// Split factor of the fp32-activation GEMM: enough workgroups for two per CU,
+// at least 16 K stages per split.
 static uint32_t choose_ksplit_f32(uint32_t tiles, uint32_t stages) {
-    static const int forced = [] {
-        const char* e = getenv("ZQ_GEMMF_KSPLIT");
-        return e ? atoi(e) : 0;
-    }();
-    if (forced > 0) return std::max(1u, std::min(uint32_t(forced), stages));
     const uint32_t want = (2u * uint32_t(device_cu_count()) + tiles - 1) / tiles;
     return std::max(1u, std::min(want, std::max(1u, stages / 16)));
 }

@@ -77,23 +77,6 @@ __device__ __forceinline__ constexpr bool use_nt() { return ZQ_GEMV_NT != 0; }
 #endif
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
-// Diagnostic build only (-DZQ_GEMV_DIAG): wave 0 of each of the first 1024
-// workgroups of gemv_stream_kernel records the constant-rate clock at kernel
-// entry, once x is in registers, at the top of each of its first 14 row
-// blocks and at exit; zq_gemv_diag_read copies the table out.
-#ifdef ZQ_GEMV_DIAG
-__device__ uint64_t g_gemv_diag[1024][20];
-#define ZQ_DIAG_MARK(k)                                                       \
-    do {                                                                      \
-        const int zq_diag_k = (k);                                            \
-        if (threadIdx.x == 0 && blockIdx.x < 1024 && zq_diag_k < 20)          \
-            g_gemv_diag[blockIdx.x][zq_diag_k] = __builtin_amdgcn_s_memrealtime(); \
-    } while (0)
-#else
-#define ZQ_DIAG_MARK(k) \
-    do {                \
-    } while (0)
-#endif
 
 // 16 B load through a raw buffer resource covering `bytes` from a
 // wave-uniform base: lanes past the end read 0 and generate no memory
@@ -430,7 +413,6 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_kernel(TaskTable tt, cons
     constexpr int XPT = XLDS ? (S * 1024 + NT - 1) / NT : 16;  // float4 of x per thread (cols <= S * 4096)
     extern __shared__ uint32_t lds[];        // [waves][R][WBUF]; the padded x is staged over it first
     __shared__ float red[2][NW][R];
-    ZQ_DIAG_MARK(0);
     const uint32_t pairs = cols >> 6;
     const uint32_t W = min(64u, (((pairs + S - 1) / S) + 3u) & ~3u);
     const uint32_t rb = pairs * DW * 4;
@@ -570,16 +552,13 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_kernel(TaskTable tt, cons
             sx1 += xv[32 + i];
         }
     }
-    ZQ_DIAG_MARK(1);
     int parity = 0;
-    [[maybe_unused]] int diag_it = 0;
     // one row block from ring slot d (a compile-time index, so the slot's
     // registers are never addressed dynamically)
     auto step = [&](auto dc) {
         constexpr int d = decltype(dc)::value;
         {
             {
-                ZQ_DIAG_MARK(2 + min(diag_it++, 16));
                 stash(u[d]);
                 const uint32_t row0 = row0s[d];
                 const int ti = tis[d];
@@ -627,7 +606,6 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_kernel(TaskTable tt, cons
         if constexpr (D > 1) if (blk < total_blocks) step(std::integral_constant<int, 1>{});
         if constexpr (D > 2) if (blk < total_blocks) step(std::integral_constant<int, 2>{});
     }
-    ZQ_DIAG_MARK(19);
 }
 
 // ---------------------------------------------------------------- Q6_K ---
@@ -706,11 +684,7 @@ __global__ __launch_bounds__(kThreads) void gemv_q6k_kernel(TaskTable tt, const 
 // per-wave LDS buffer; lane L then decodes its two 16-element units (one
 // quarter of one half of super-block 2*(L/16) + k, a single sub-block scale)
 // from LDS.  Fields of odd super-blocks sit at 2 mod 4 and are assembled
-// with v_alignbyte.  ZQ_Q6K_DIAG (diagnostic builds only): 1 drops the
-// decode, 2 also the LDS staging.
-#ifndef ZQ_Q6K_DIAG
-#define ZQ_Q6K_DIAG 0
-#endif
+// with v_alignbyte.
 template <int R, int S, int NW>
 __global__ __launch_bounds__(NW * 64) void gemv_q6k_stream_kernel(TaskTable tt, const float* __restrict__ x,
                                                                  uint32_t cols, uint32_t total_blocks) {
@@ -782,17 +756,11 @@ __global__ __launch_bounds__(NW * 64) void gemv_q6k_stream_kernel(TaskTable tt, 
     }
     int parity = 0;
     while (blk < total_blocks) {
-#if ZQ_Q6K_DIAG == 2  // diagnostic builds only: no LDS staging, no decode
-        uint32_t dg = 0;
-#pragma unroll
-        for (int r = 0; r < R; ++r) dg ^= u[r][0].x ^ u[r][0].w ^ u[r][1].y;
-#else
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             reinterpret_cast<uint4*>(wbuf + r * BUFW)[lane] = u[r][0];
             if (lane + 64 < int(CUNITS)) reinterpret_cast<uint4*>(wbuf + r * BUFW)[lane + 64] = u[r][1];
         }
-#endif
         const uint32_t nblk = blk + gridDim.x;
         const uint32_t row0c = row0;
         const int tic = ti;
@@ -802,10 +770,6 @@ __global__ __launch_bounds__(NW * 64) void gemv_q6k_stream_kernel(TaskTable tt, 
             load(rowp, u);
         }
         float acc[R];
-#if ZQ_Q6K_DIAG == 2
-#pragma unroll
-        for (int r = 0; r < R; ++r) acc[r] = wave_sum(__uint_as_float((dg + r) & 0x3FFFFFFFu));
-#else
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const uint32_t* buf = wbuf + r * BUFW;
@@ -842,7 +806,6 @@ __global__ __launch_bounds__(NW * 64) void gemv_q6k_stream_kernel(TaskTable tt, 
                 // neighbouring bytes land outside the masks)
                 const uint32_t nrot = (q >> 1) * 4, hrot = (2 * q + 28) & 31u;
                 float t0 = 0.0f, t1 = 0.0f;
-#if ZQ_Q6K_DIAG != 1
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     // the four 6-bit codes u = q + 32 of elements 4j..4j+3, one per
@@ -858,16 +821,10 @@ __global__ __launch_bounds__(NW * 64) void gemv_q6k_stream_kernel(TaskTable tt, 
                     t0 = mix_hi(p02, xv[k][4 * j + 2], t0);
                     t1 = mix_hi(p13, xv[k][4 * j + 3], t1);
                 }
-#endif
-#if ZQ_Q6K_DIAG == 1  // diagnostic builds only: decode removed, LDS reads kept
-                a += __uint_as_float((ql[0] ^ ql[1] ^ ql[2] ^ ql[3] ^ qh[0] ^ qh[1] ^ qh[2] ^ qh[3]) & 0x3FFFFFFFu) + sc + d;
-#else
                 a = fmaf(d * sc, fmaf(t0 + t1, 16777216.0f, nsx[k]), a);
-#endif
             }
             acc[r] = wave_sum(a);
         }
-#endif
         const GemvTask& t = tt.t[tic];
         if constexpr (S == 1) {
 #pragma unroll
@@ -989,7 +946,6 @@ __global__ __launch_bounds__(NW * 64) void gemv_kquant_stream_kernel(TaskTable t
     constexpr int TEAMS = NW / S;
     extern __shared__ uint4 klds[];           // [waves][R][CUNITS]
     __shared__ float red[2][NW][R];
-    ZQ_DIAG_MARK(0);
     const uint32_t nsb = cols >> 8;
     const uint32_t rb = nsb * BB;
     const int lane = threadIdx.x & 63;
@@ -1063,11 +1019,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_kquant_stream_kernel(TaskTable t
     const uint32_t sbl = uint32_t(lane >> 3), c = uint32_t(lane & 7), j2 = c >> 1, l0 = (c & 1u) * 16;
     const uint32_t hidx = sbl * (BB / 16), qidx = (sbl * BB + QOFF + j2 * 32 + l0) / 16,
                    bidx = (sbl * BB + 16 + l0) / 16;
-    ZQ_DIAG_MARK(1);
-    [[maybe_unused]] int diag_it = 0;
     int parity = 0;
     while (blk < total_blocks) {
-        ZQ_DIAG_MARK(2 + min(diag_it++, 16));
         stash(v);
         const uint32_t nblk = blk + gridDim.x;
         const uint32_t row0c = row0;
@@ -1083,11 +1036,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kquant_stream_kernel(TaskTable t
             const uint4* rb4 = buf + r * CUNITS;
             const uint4 h = rb4[hidx], q = rb4[qidx];
             const uint4 bq = FMT == kQ5_K ? rb4[bidx] : make_uint4(0, 0, 0, 0);
-#ifdef ZQ_GEMV_DIAG_NOCOMPUTE
-            acc[r] = active ? __uint_as_float((h.x ^ q.y ^ bq.z) & 0x3fffffffu) * xl[0] : 0.0f;
-#else
             acc[r] = active ? kquant_dot<FMT>(h, q, bq, xl, xh, sxl, sxh, j2) : 0.0f;
-#endif
             acc[r] = wave_sum(acc[r]);
         }
         const GemvTask& t = tt.t[tic];
@@ -1111,7 +1060,6 @@ __global__ __launch_bounds__(NW * 64) void gemv_kquant_stream_kernel(TaskTable t
         }
         blk = nblk;
     }
-    ZQ_DIAG_MARK(19);
 }
 
 // Generic K-quant GEMV: any cols % 256 == 0 with dword-aligned rows; one wave
@@ -1241,14 +1189,8 @@ int cu_count() {
     }();
     return n;
 }
-int wg_per_cu() {
-    static const int v = [] {
-        const char* e = getenv("ZQ_GEMV_WG_PER_CU");
-        const int k = e ? atoi(e) : 0;
-        return (k >= 1 && k <= 64) ? k : 4;
-    }();
-    return v;
-}
+// Workgroups per CU of the x-in-registers kernel.
+constexpr int kXregWgPerCu = 4;
 
 template <int FMT, int R, int S, int NW, int D, int XK = kXPlain>
 hipError_t launch_stream(TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream,
@@ -1301,7 +1243,7 @@ hipError_t launch_xreg(TaskTable& tt, const float* x, uint32_t cols, hipStream_t
         blocks += (tt.t[i].rows + RB - 1) / RB;
     }
     tt.group_start[tt.count] = blocks;
-    const uint32_t grid = std::min<uint32_t>(blocks, uint32_t(cu_count() * wg_per_cu()));
+    const uint32_t grid = std::min<uint32_t>(blocks, uint32_t(cu_count() * kXregWgPerCu));
     const size_t lds = S == 1 ? size_t(cols >> 6) * kPadStride * sizeof(float) : 0;
     hipLaunchKernelGGL((gemv_xreg_kernel<FMT, R, S>), dim3(grid), dim3(kThreads), lds, stream, tt, x, cols, blocks);
     return hipGetLastError();
@@ -1475,11 +1417,7 @@ hipError_t launch_gemv(int fmt, const GemvTask* tasks, int count, const float* x
         if (reinterpret_cast<uintptr_t>(x) & 15u) return hipErrorInvalidValue;
         bool w16 = true;
         for (int i = 0; i < count; ++i) w16 = w16 && (reinterpret_cast<uintptr_t>(tasks[i].w) & 15u) == 0;
-        static const bool q6_legacy = [] {
-            const char* e = getenv("ZQ_GEMV_KERNEL");
-            return e && e[0] == 'l';
-        }();
-        if (!q6_legacy && w16 && c % 2048 == 0 && c / 2048 <= 8) {
+        if (w16 && c % 2048 == 0 && c / 2048 <= 8) {
             const hipError_t e = launch_q6k_stream_any(tt, x, c, stream, total_rows);
             if (e != hipErrorInvalidConfiguration) return e;
         }
@@ -1490,18 +1428,14 @@ hipError_t launch_gemv(int fmt, const GemvTask* tasks, int count, const float* x
         if (R == 2) return launch_q6k<2>(tt, x, c, stream);
         return launch_q6k<1>(tt, x, c, stream);
     }
-    static const int kernel_choice = [] {  // 's' stream (default), 'x' xreg, 'l' legacy
-        const char* e = getenv("ZQ_GEMV_KERNEL");
-        return e ? int(e[0]) : int('s');
-    }();
     const bool x16 = (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
     bool w16 = true;
     for (int i = 0; i < count; ++i) w16 = w16 && (reinterpret_cast<uintptr_t>(tasks[i].w) & 15u) == 0;
-    if (kernel_choice == 's' && w16 && x16 && c % 256 == 0 && c / 64 <= 256) {
+    if (w16 && x16 && c % 256 == 0 && c / 64 <= 256) {
         const int Rx = xreg_rows(total_rows);
         return fmt == kQ8_0 ? launch_stream_any<kQ8_0>(Rx, tt, x, c, stream) : launch_stream_any<kQ4_0>(Rx, tt, x, c, stream);
     }
-    if (kernel_choice != 'l' && aligned && x16 && c % 64 == 0 && c / 64 <= 256) {
+    if (aligned && x16 && c % 64 == 0 && c / 64 <= 256) {
         const int Rx = xreg_rows(total_rows);
         return fmt == kQ8_0 ? launch_xreg_any<kQ8_0>(Rx, tt, x, c, stream) : launch_xreg_any<kQ4_0>(Rx, tt, x, c, stream);
     }
@@ -1553,9 +1487,3 @@ hipError_t launch_gemv_prologue(int fmt, const GemvTask* tasks, int count, const
 }
 
 }  // namespace zq
-
-#ifdef ZQ_GEMV_DIAG
-extern "C" int zq_gemv_diag_read(uint64_t* out) {
-    return hipMemcpyFromSymbol(out, HIP_SYMBOL(zq::g_gemv_diag), sizeof(zq::g_gemv_diag)) == hipSuccess ? 0 : -4;
-}
-#endif

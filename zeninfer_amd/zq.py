@@ -172,13 +172,30 @@ def _dptr(t):
     return t.data_ptr()
 
 
+def _device_index():
+    """Device the library runs on: ZEN_HIP_DEVICE, default 0 (as zq_hip_init)."""
+    try:
+        return int(os.environ.get("ZEN_HIP_DEVICE", "0"))
+    except ValueError:
+        return 0
+
+
+def _check_device(t, what):
+    if not getattr(t, "is_cuda", False):
+        raise ValueError(f"{what}: tensor must be on the GPU, got device {getattr(t, 'device', '?')}")
+    if t.device.index is not None and t.device.index != _device_index():
+        raise ValueError(f"{what}: tensor is on {t.device}, the library runs on cuda:{_device_index()}")
+
+
 def _need(t, nbytes, what):
-    """A torch tensor passed as a device buffer must be contiguous and hold at
-    least nbytes: the kernels index it from the sizes alone, so a short buffer
-    would be read or written past its end.  Raw addresses are the caller's
-    responsibility."""
+    """A torch tensor passed as a device buffer must live on the library's GPU,
+    be contiguous and hold at least nbytes: the kernels index it from the sizes
+    alone, so a short buffer would be read or written past its end, and the
+    address of a host tensor handed to a kernel faults the GPU.  Raw addresses
+    are the caller's responsibility."""
     if t is None or isinstance(t, int):
         return
+    _check_device(t, what)
     if not t.is_contiguous():
         raise ValueError(f"{what}: tensor must be contiguous")
     have = t.numel() * t.element_size()
