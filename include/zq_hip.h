@@ -86,19 +86,38 @@ typedef struct zq_hip_stats {
     uint64_t evictions;
     uint64_t declined;        /* calls answered ZQ_DECLINED              */
     uint64_t errors;
-    uint64_t upload_us;
+    uint64_t upload_us;       /* weight copies to the device             */
     uint64_t transfer_us;     /* activation H2D + output D2H, host clock */
     uint64_t wait_us;         /* stream synchronisation                  */
+    uint64_t fallbacks;       /* host calls after init that returned non-OK (the caller
+                                 ran its CPU route), Stats::fallbacks         */
+    uint64_t alloc_us;        /* device/pinned allocation, Stats::alloc_us    */
+    uint64_t launch_us;       /* kernel enqueue, Stats::launch_us             */
+    uint64_t readback_us;     /* output D2H + copy out, Stats::readback_us    */
+    uint64_t gpu_us;          /* event-timed kernels of host calls; only with
+                                 ZEN_HIP_TRACE=1 (hip_backend.hip:889-891)    */
 } zq_hip_stats;
 
 /* One projection of a batched GEMV.  Replaces zen::hip::GemvTask
- * (include/zen/hip_backend.h:62-71); all tasks share x and cols. */
+ * (include/zen/hip_backend.h:62-71) without its `columns` field: every task
+ * of a batch shares x, so cols is one argument of the batch call (the
+ * reference's quant::gemv_batch also takes a single `columns`,
+ * include/zen/quant.h:71-74). */
 typedef struct zq_gemv_task {
     const uint8_t* weights;  /* host pointer (zq_hip_gemv_batch) or device pointer (_dev) */
     float* y;
     size_t rows;
 } zq_gemv_task;
 #define ZQ_MAX_BATCH 8       /* zen::hip::kMaxBatch (include/zen/hip_backend.h:72) */
+
+/* One projection of a batched GEMM: all tasks share X, tokens and cols.
+ * Replaces one (weights[i], outputs[i], rows[i]) triple of quant::gemm_batch
+ * (include/zen/quant.h:77-84). */
+typedef struct zq_gemm_task {
+    const uint8_t* weights;  /* host pointer (zq_hip_gemm_batch) or device pointer (_dev) */
+    float* Y;                /* [tokens x rows], token-major */
+    size_t rows;
+} zq_gemm_task;
 
 /* ---- lifecycle (include/zen/hip_backend.h:46-50) -------------------------- */
 /* 1 when ZEN_BACKEND is hip|rocm|amd or ZEN_HIP=1 (hip_backend.hip:266-282). */
@@ -136,11 +155,34 @@ int zq_hip_gemv_batch(int fmt, const float* x, const zq_gemv_task* tasks, size_t
  * quant::gemm (src/quant.cpp:1656-1659). */
 int zq_hip_gemm(int fmt, const uint8_t* weights, const float* X, float* Y, size_t tokens, size_t rows,
                 size_t cols, int act_mode);
+/* Several GEMMs sharing X (prefill Q|K|V, gate|up), one submission; with
+ * int8 activations X is quantised once for all tasks.  Replaces
+ * quant::gemm_batch (include/zen/quant.h:77-84, src/quant.cpp:1521-1554),
+ * whose GPU route is the D3D12 gemm_q8_0_batch. */
+int zq_hip_gemm_batch(int fmt, const float* X, const zq_gemm_task* tasks, size_t count, size_t tokens, size_t cols,
+                      int act_mode);
 /* gate|up -> SiLU(gate)*up -> down with the FFN activation kept on the
  * device.  Replaces zen::hip::gemv_q8_0_ffn (include/zen/hip_backend.h:80-82),
  * called from quant::ffn_gemv (src/quant.cpp:1566-1571). */
 int zq_hip_ffn_gemv(int fmt, const uint8_t* gate, const uint8_t* up, const uint8_t* down, const float* x,
                     float* y, size_t ffn_rows, size_t cols, size_t out_rows);
+/* y[r] = rmsnorm(x[r]) * weight for rows of cols floats: sum of squares in
+ * double, inv = 1/sqrtf(float(ss/cols) + eps), y = x*inv*w -- the reference
+ * CPU rms_norm (src/adapters/dense_transformer_runtime.cpp:117-124).
+ * Replaces zen::hip::rms_norm (include/zen/hip_backend.h:77-78,
+ * src/backends/hip/hip_backend.hip:990-1001). */
+int zq_hip_rms_norm(const float* x, const float* weight, float* y, size_t rows, size_t cols, float eps);
+/* The FFN half of a decoder layer in one submission, every intermediate on
+ * the device:  t0 = Wo.attn_out; h1 = t0 + x; h2 = rmsnorm(h1)*norm_weight;
+ * f = silu(Wg.h2) * (Wu.h2); out = h1 + Wd.f.  Wo is [hidden x attn_width],
+ * Wg/Wu [ffn_rows x hidden], Wd [hidden x ffn_rows], all of format fmt
+ * (other mixes are declined to the caller's separate operations).  out may
+ * alias x.  Replaces quant::ffn_residual_fused (include/zen/quant.h:97-106,
+ * src/quant.cpp:1580-1612), whose GPU route is the D3D12 one
+ * (include/zen/d3d12_backend.h:352-364). */
+int zq_hip_ffn_residual_fused(int fmt, const uint8_t* attn_output, const uint8_t* gate, const uint8_t* up,
+                              const uint8_t* down, const float* norm_weight, const float* x, const float* attn_out,
+                              float* out, size_t hidden, size_t attn_width, size_t ffn_rows, float eps);
 /* Drops the device copy of one weight tensor (the D3D12 slot's
  * release_q8_0_weights, include/zen/d3d12_backend.h:87-91). */
 int zq_hip_release(const uint8_t* weights);
@@ -159,6 +201,22 @@ int zq_hip_gemv_batch_dev(int fmt, const float* x, const zq_gemv_task* tasks, si
 size_t zq_hip_gemm_workspace_bytes(int fmt, size_t tokens, size_t rows, size_t cols, int act_mode);
 int zq_hip_gemm_dev(int fmt, const void* weights, const float* X, float* Y, size_t tokens, size_t rows,
                     size_t cols, int act_mode, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Batched GEMM on the device; workspace as zq_hip_gemm_batch_workspace_bytes
+ * (the shared int8 activations and the largest task's split-K partials). */
+size_t zq_hip_gemm_batch_workspace_bytes(int fmt, const zq_gemm_task* tasks, size_t count, size_t tokens, size_t cols,
+                                         int act_mode);
+int zq_hip_gemm_batch_dev(int fmt, const float* X, const zq_gemm_task* tasks, size_t count, size_t tokens, size_t cols,
+                          int act_mode, void* workspace, size_t workspace_bytes, void* stream);
+int zq_hip_rms_norm_dev(const float* x, const float* weight, float* y, size_t rows, size_t cols, float eps,
+                        void* stream);
+/* zq_hip_ffn_residual_fused on device pointers; workspace holds
+ * zq_hip_ffn_residual_workspace_bytes(hidden, ffn_rows) bytes. */
+size_t zq_hip_ffn_residual_workspace_bytes(size_t hidden, size_t ffn_rows);
+int zq_hip_ffn_residual_fused_dev(int fmt, const void* attn_output, const void* gate, const void* up, const void* down,
+                                  const float* norm_weight, const float* x, const float* attn_out, float* out,
+                                  size_t hidden, size_t attn_width, size_t ffn_rows, float eps, void* workspace,
+                                  size_t workspace_bytes, void* stream);
 
 /* ---- bit-exact tier hooks (device pointers, asynchronous) ---------------- */
 /* Per-32 activation quantiser, kernels/avx2.cpp:502-524: xq[tokens*cols],

@@ -71,6 +71,26 @@ int zq_model_decode(zq_model* model, uint32_t token, float* logits, uint32_t* ne
  * tokens, stopping after EOS.  Wall times of the two phases in ms. */
 int zq_model_generate(zq_model* model, const uint32_t* prompt, size_t n, uint32_t max_new, uint32_t* out,
                       size_t* n_out, double* prefill_ms, double* decode_ms);
+/* Device address, shape and GGML type of one resident weight, so a caller can
+ * run its own projections on it (zq_hip_*_dev) or check it: which is one of
+ * ZQ_W_Q..ZQ_W_DOWN with layer < layers, or ZQ_W_EMBED / ZQ_W_OUTPUT with
+ * layer == ZQ_MODEL_GLOBAL.  The tensor names of dense_transformer_runtime.cpp
+ * (blk.N.attn_q.weight ... token_embd.weight, output.weight).
+ * A synthetic model's weights are zq_hip_synth_weights_dev of seeds seed+0
+ * (token_embd), seed+1 (output), then seed+2+7*layer+i for q, k, v, o, gate,
+ * up, down. */
+#define ZQ_MODEL_GLOBAL 0xFFFFFFFFu
+#define ZQ_W_EMBED 0
+#define ZQ_W_OUTPUT 1
+#define ZQ_W_Q 2
+#define ZQ_W_K 3
+#define ZQ_W_V 4
+#define ZQ_W_O 5
+#define ZQ_W_GATE 6
+#define ZQ_W_UP 7
+#define ZQ_W_DOWN 8
+int zq_model_weight(const zq_model* model, uint32_t layer, int which, const void** dev, uint32_t* rows,
+                    uint32_t* cols, int* fmt);
 /* Device bytes held: weights, KV cache, activations. */
 int zq_model_memory(zq_model* model, uint64_t* weight_bytes, uint64_t* cache_bytes, uint64_t* activation_bytes);
 

@@ -201,7 +201,9 @@ def test_device_synth_matches_host_generator(zq, orc):
                                        # 32-token tiles (M <= 64): ragged M and N, a K split, two token
                                        # tiles; M = 65 takes the 128-token tile
                                        (O.Q8_0, 31, 1000, 8192), (O.Q8_0, 33, 260, 2048), (O.Q8_0, 65, 260, 2048),
-                                       (O.Q4_0, 31, 700, 8192), (O.Q4_0, 150, 300, 2048)])
+                                       (O.Q4_0, 31, 700, 8192), (O.Q4_0, 150, 300, 2048),
+                                       # always split K, with an odd output count (scalar split-K reduce)
+                                       (O.Q8_0, 3, 301, 14336)])
 def test_gemm_int8(zq, orc, fmt, m, n, k):
     w = orc.gen_weights(fmt, 300 + n, n, k)
     X = orc.gen_normal(301 + m, m * k)
@@ -212,7 +214,8 @@ def test_gemm_int8(zq, orc, fmt, m, n, k):
 
 @pytest.mark.parametrize("fmt,m,n,k", [(O.Q8_0, 5, 300, 4096), (O.Q8_0, 130, 129, 1024), (O.Q4_0, 9, 150, 4096),
                                        (O.Q6_K, 17, 200, 4096), (O.Q6_K, 129, 33, 512), (O.Q8_0, 3, 40, 96),
-                                       (O.Q4_K, 17, 200, 4096), (O.Q5_K, 129, 33, 512), (O.Q4_K, 1, 70, 768)])
+                                       (O.Q4_K, 17, 200, 4096), (O.Q5_K, 129, 33, 512), (O.Q4_K, 1, 70, 768),
+                                       (O.Q8_0, 3, 301, 14336)])
 def test_gemm_f32(zq, orc, fmt, m, n, k):
     w = orc.gen_weights(fmt, 400 + n, n, k)
     X = orc.gen_normal(401 + m, m * k)
@@ -221,26 +224,54 @@ def test_gemm_f32(zq, orc, fmt, m, n, k):
     zq.release(w)
 
 
-@pytest.mark.parametrize("m,n,k", [(2048, 14336, 4096), (32, 4096, 14336)])
-def test_gemm_full_size_sampled(zq, orc, m, n, k):
-    # config 2 at M = 2048 and M = 32, int8 activations, device path
-    wd = torch.zeros(zq.weight_bytes(O.Q8_0, n, k), dtype=torch.uint8, device=DEV)
-    zq.synth_weights_dev(O.Q8_0, 81, wd, n, k)
-    X = orc.gen_normal(82, m * k)
+# The BASELINE configs' own GEMM workloads at full size: config 2 (Q8_0, int8
+# activations, M = 32 / 128 / 512 / 2048 on both FFN shapes) and config 3
+# (Q4_0 int8 and Q6_K fp32 at M = 512).  Rows and tokens are independent, so
+# sampled (token, row) outputs are checked against the oracle.
+_FULL_GEMM = [(O.Q8_0, 1, 2048, 14336, 4096), (O.Q8_0, 1, 32, 4096, 14336),
+              (O.Q8_0, 1, 128, 14336, 4096), (O.Q8_0, 1, 128, 4096, 14336),
+              (O.Q8_0, 1, 512, 14336, 4096), (O.Q8_0, 1, 512, 4096, 14336),
+              (O.Q4_0, 1, 512, 14336, 4096), (O.Q4_0, 1, 512, 4096, 14336),
+              (O.Q6_K, 2, 512, 14336, 4096), (O.Q6_K, 2, 512, 4096, 14336)]
+
+
+@pytest.mark.parametrize("fmt,act,m,n,k", _FULL_GEMM)
+def test_gemm_full_size_sampled(zq, orc, fmt, act, m, n, k):
+    wd = torch.zeros(zq.weight_bytes(fmt, n, k), dtype=torch.uint8, device=DEV)
+    zq.synth_weights_dev(fmt, 81 + m + n, wd, n, k)
+    X = orc.gen_normal(82 + m, m * k)
     Y = torch.empty(m * n, device=DEV)
-    ws_bytes = zq.gemm_workspace_bytes(O.Q8_0, m, n, k, zq.ACT_INT8)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=DEV)
-    zq.gemm_dev(O.Q8_0, wd, to_dev(X), Y, m, n, k, zq.ACT_INT8, ws, ws_bytes)
+    ws_bytes = zq.gemm_workspace_bytes(fmt, m, n, k, act)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=DEV)
+    zq.gemm_dev(fmt, wd, to_dev(X), Y, m, n, k, act, ws, ws_bytes)
     Yh = Y.cpu().numpy().reshape(m, n)
-    rb = zq.row_bytes(O.Q8_0, k)
-    rng = np.random.default_rng(83)
+    assert np.all(np.isfinite(Yh))
+    rb = zq.row_bytes(fmt, k)
+    rng = np.random.default_rng(83 + m)
     rows = np.sort(rng.choice(n, 24, replace=False))
     toks = np.sort(rng.choice(m, 6, replace=False))
     w_all = wd[: n * rb].cpu().numpy()
     sub = np.concatenate([w_all[r * rb:(r + 1) * rb] for r in rows])
     Xs = X.reshape(m, k)[toks].reshape(-1)
-    want = orc.gemm_i8(O.Q8_0, sub, Xs, len(toks), len(rows), k).reshape(len(toks), len(rows))
-    assert_close(Yh[np.ix_(toks, rows)].reshape(-1), want.reshape(-1), "full-size gemm_i8")
+    ref = orc.gemm_i8 if act == zq.ACT_INT8 else orc.gemm_f32
+    want = ref(fmt, sub, Xs, len(toks), len(rows), k).reshape(len(toks), len(rows))
+    assert_close(Yh[np.ix_(toks, rows)].reshape(-1), want.reshape(-1), f"full-size gemm fmt={fmt} M={m} {n}x{k}")
+
+
+def test_lm_head_full_size_sampled_rows(zq, orc):
+    # config 1 lm_head: 128256 x 4096 Q8_0 (558 MB), sampled rows incl. the last
+    rows, cols, seed = 128256, 4096, 75
+    wd = torch.zeros(zq.weight_bytes(O.Q8_0, rows, cols), dtype=torch.uint8, device=DEV)
+    zq.synth_weights_dev(O.Q8_0, seed, wd, rows, cols)
+    x = orc.gen_normal(seed, cols)
+    y = torch.empty(rows, device=DEV)
+    zq.gemv_dev(O.Q8_0, wd, to_dev(x), y, rows, cols)
+    yh = y.cpu().numpy()
+    assert np.all(np.isfinite(yh))
+    rb = zq.row_bytes(O.Q8_0, cols)
+    pick = np.unique(np.concatenate([np.random.default_rng(seed).choice(rows, 64, replace=False), [0, rows - 1]]))
+    sub = np.concatenate([wd[r * rb:(r + 1) * rb].cpu().numpy() for r in pick])
+    assert_close(yh[pick], orc.gemv_f32(O.Q8_0, sub, x, len(pick), cols), "lm_head gemv")
 
 
 @pytest.mark.parametrize("fmt", [O.Q6_K, O.Q4_K, O.Q5_K])

@@ -12,6 +12,7 @@
 // every resident tensor is evicted first.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <chrono>
 #include <cstdio>
 #include <cstdlib>
@@ -52,6 +53,10 @@ struct Backend {
     size_t dev_scratch_bytes = 0;
     void* host_pinned = nullptr;
     size_t host_pinned_bytes = 0;
+    // ZEN_HIP_TRACE=1: events around each host call's kernels feed gpu_us
+    // (hip_backend.hip:549-565, 889-891)
+    bool trace = false;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
 };
 
 Backend& B() {
@@ -107,6 +112,9 @@ int init_locked(Backend& b) {
         b.failed = true;
         return ZQ_ERR_NO_DEVICE;
     }
+    const char* tr = std::getenv("ZEN_HIP_TRACE");
+    b.trace = tr && tr[0] == '1';
+    if (b.trace && (hipEventCreate(&b.ev0) != hipSuccess || hipEventCreate(&b.ev1) != hipSuccess)) b.trace = false;
     b.budget = static_cast<size_t>(static_cast<double>(p.totalGlobalMem) * 0.8);
     if (const char* me = std::getenv("ZEN_HIP_MIN_ELEMENTS")) b.min_elements = std::strtoull(me, nullptr, 10);
     b.initialised = true;
@@ -138,12 +146,14 @@ int ensure_resident(Backend& b, int fmt, const uint8_t* w, size_t rows, size_t c
     const size_t bytes = payload + ZQ_WEIGHT_TAIL_PAD;
     if (bytes > b.budget) return ZQ_DECLINED;
     if (b.stats.resident_bytes + bytes > b.budget) free_resident(b);
-    const auto t0 = Clock::now();
+    auto t0 = Clock::now();
     uint8_t* dev = nullptr;
     if (hipMalloc(&dev, bytes) != hipSuccess) {
         free_resident(b);
         if (hipMalloc(&dev, bytes) != hipSuccess) return ZQ_ERR_OOM;
     }
+    b.stats.alloc_us += us_since(t0);
+    t0 = Clock::now();
     if (hipMemcpy(dev, w, payload, hipMemcpyHostToDevice) != hipSuccess ||
         hipMemset(dev + payload, 0, ZQ_WEIGHT_TAIL_PAD) != hipSuccess) {
         (void)hipFree(dev);
@@ -160,6 +170,12 @@ int ensure_resident(Backend& b, int fmt, const uint8_t* w, size_t rows, size_t c
 }
 
 int ensure_scratch(Backend& b, size_t dev_bytes, size_t host_bytes) {
+    const auto t0 = Clock::now();
+    struct Tally {
+        Backend& b;
+        Clock::time_point t0;
+        ~Tally() { b.stats.alloc_us += us_since(t0); }
+    } tally{b, t0};
     if (dev_bytes > b.dev_scratch_bytes) {
         if (b.dev_scratch) (void)hipFree(b.dev_scratch);
         b.dev_scratch = nullptr;
@@ -224,6 +240,177 @@ int enqueue_gemm(int fmt, const uint8_t* w, const float* X, float* Y, size_t tok
     return ZQ_OK;
 }
 
+// Workspace of a batched GEMM: the shared int8 activations and scales (int8
+// mode), then room for the largest task's split-K partial sums (reused task
+// after task on the one stream).
+size_t batch_workspace_bytes(int fmt, const size_t* rows, size_t count, size_t tokens, size_t cols, int act) {
+    size_t part = 0;
+    for (size_t i = 0; i < count; ++i)
+        part = std::max(part, act == ZQ_ACT_INT8 ? zq::gemm_i8_partial_bytes(tokens, rows[i], cols)
+                                                 : zq::gemm_f32_partial_bytes(tokens, rows[i], cols));
+    if (act != ZQ_ACT_INT8) return part;
+    return align_up(tokens * cols, 256) + align_up(tokens * (cols / 32) * sizeof(float), 256) + part;
+}
+
+// Enqueue the GEMMs of tasks sharing X: with int8 activations X is quantised
+// once (the reference batches exactly this sharing, src/quant.cpp:1521-1554).
+int enqueue_gemm_batch(int fmt, const uint8_t* const* w, float* const* Y, const size_t* rows, size_t count,
+                       const float* X, size_t tokens, size_t cols, int act, void* ws, size_t ws_bytes, hipStream_t s,
+                       uint64_t* dispatches) {
+    if (ws_bytes < batch_workspace_bytes(fmt, rows, count, tokens, cols, act)) return ZQ_ERR_ARG;
+    if (act == ZQ_ACT_INT8) {
+        if (!ws) return ZQ_ERR_ARG;
+        const size_t qbytes = align_up(tokens * cols, 256);
+        const size_t sbytes = align_up(tokens * (cols / 32) * sizeof(float), 256);
+        int8_t* xq = static_cast<int8_t*>(ws);
+        float* xs = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + qbytes);
+        float* part = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + qbytes + sbytes);
+        if (zq::launch_quantize_acts(X, xq, xs, tokens, cols, s) != hipSuccess) return ZQ_ERR_HIP;
+        ++*dispatches;
+        for (size_t i = 0; i < count; ++i) {
+            const size_t pb = zq::gemm_i8_partial_bytes(tokens, rows[i], cols);
+            if (zq::launch_gemm_i8(fmt, w[i], xq, xs, Y[i], pb ? part : nullptr, tokens, rows[i], cols, s) != hipSuccess)
+                return ZQ_ERR_HIP;
+            *dispatches += pb ? 2 : 1;
+        }
+        return ZQ_OK;
+    }
+    for (size_t i = 0; i < count; ++i) {
+        const size_t pb = zq::gemm_f32_partial_bytes(tokens, rows[i], cols);
+        float* part = pb && ws ? static_cast<float*>(ws) : nullptr;
+        if (zq::launch_gemm_f32(fmt, w[i], X, Y[i], part, tokens, rows[i], cols, s) != hipSuccess) return ZQ_ERR_HIP;
+        *dispatches += part ? 2 : 1;
+    }
+    return ZQ_OK;
+}
+
+bool ffn_residual_args_ok(int fmt, const void* wo, const void* wg, const void* wu, const void* wd, const float* norm_w,
+                          const float* x, const float* attn_out, const float* out, size_t hidden, size_t attn_width,
+                          size_t ffn_rows) {
+    return wo && wg && wu && wd && norm_w && x && attn_out && out && hidden && attn_width && ffn_rows &&
+           valid_fmt(fmt) && zq::row_bytes(fmt, attn_width) && zq::row_bytes(fmt, hidden) &&
+           zq::row_bytes(fmt, ffn_rows) && hidden <= (1u << 24) && attn_width <= (1u << 24) && ffn_rows <= (1u << 24);
+}
+
+// The FFN half of a decoder layer, every intermediate on the device
+// (d3d12_backend.h:352-364):
+//   t0 = Wo . attn_out;  h1 = t0 + x;  h2 = rmsnorm(h1) * norm_w;
+//   g = Wg . h2;  u = Wu . h2;  f = silu(g) * u;  d = Wd . f;  out = h1 + d.
+// Q8_0 / Q4_0 on the streaming shapes fold the add + norm into the gate|up
+// GEMV and silu * up into the down GEMV; other formats run them as kernels
+// of their own.  x is read before out is written, so out may alias x.
+int enqueue_ffn_residual(int fmt, const uint8_t* wo, const uint8_t* wg, const uint8_t* wu, const uint8_t* wd,
+                         const float* norm_w, const float* x, const float* attn_out, float* out, size_t hidden,
+                         size_t attn_width, size_t ffn_rows, float eps, void* ws, size_t ws_bytes, hipStream_t s,
+                         uint64_t* dispatches);
+
+}  // namespace
+
+extern "C" size_t zq_hip_ffn_residual_workspace_bytes(size_t hidden, size_t ffn_rows) {
+    if (!hidden || !ffn_rows) return 0;
+    return 3 * align_up(hidden * sizeof(float), 256) + 2 * align_up(ffn_rows * sizeof(float), 256);
+}
+
+namespace {
+int enqueue_ffn_residual(int fmt, const uint8_t* wo, const uint8_t* wg, const uint8_t* wu, const uint8_t* wd,
+                         const float* norm_w, const float* x, const float* attn_out, float* out, size_t hidden,
+                         size_t attn_width, size_t ffn_rows, float eps, void* ws, size_t ws_bytes, hipStream_t s,
+                         uint64_t* dispatches) {
+    if (!ws || ws_bytes < zq_hip_ffn_residual_workspace_bytes(hidden, ffn_rows)) return ZQ_ERR_ARG;
+    const size_t hb = align_up(hidden * sizeof(float), 256), fb = align_up(ffn_rows * sizeof(float), 256);
+    uint8_t* base = static_cast<uint8_t*>(ws);
+    float* t0 = reinterpret_cast<float*>(base);
+    float* h1 = reinterpret_cast<float*>(base + hb);
+    float* d = reinterpret_cast<float*>(base + 2 * hb);
+    float* g = reinterpret_cast<float*>(base + 3 * hb);
+    float* u = reinterpret_cast<float*>(base + 3 * hb + fb);
+    const uint32_t H = uint32_t(hidden), F = uint32_t(ffn_rows);
+    zq::GemvTask to{wo, t0, H};
+    if (zq::launch_gemv(fmt, &to, 1, attn_out, attn_width, s) != hipSuccess) return ZQ_ERR_HIP;
+    zq::GemvTask gu[2] = {{wg, g, F}, {wu, u, F}};
+    const zq::XPrologue norm{zq::kAddNorm, t0, x, norm_w, h1, eps};
+    hipError_t e = zq::launch_gemv_prologue(fmt, gu, 2, norm, hidden, s);
+    if (e == hipErrorInvalidConfiguration) {
+        // unfused: h1 = t0 + x, h2 = rmsnorm(h1) * w (into d), gate|up of h2
+        if (zq::launch_add_to(t0, x, h1, hidden, s) != hipSuccess ||
+            zq::launch_rmsnorm(h1, norm_w, d, 1, H, eps, s) != hipSuccess ||
+            zq::launch_gemv(fmt, gu, 2, d, hidden, s) != hipSuccess)
+            return ZQ_ERR_HIP;
+        *dispatches += 3;
+    } else if (e != hipSuccess) {
+        return ZQ_ERR_HIP;
+    } else {
+        ++*dispatches;
+    }
+    zq::GemvTask dn{wd, d, H};
+    const zq::XPrologue act{zq::kSiluMul, g, u, nullptr, nullptr, 0.0f};
+    e = zq::launch_gemv_prologue(fmt, &dn, 1, act, ffn_rows, s);
+    if (e == hipErrorInvalidConfiguration) {
+        if (zq::launch_silu_mul(g, u, g, ffn_rows, s) != hipSuccess || zq::launch_gemv(fmt, &dn, 1, g, ffn_rows, s) != hipSuccess)
+            return ZQ_ERR_HIP;
+        *dispatches += 2;
+    } else if (e != hipSuccess) {
+        return ZQ_ERR_HIP;
+    } else {
+        ++*dispatches;
+    }
+    if (zq::launch_add_to(h1, d, out, hidden, s) != hipSuccess) return ZQ_ERR_HIP;
+    *dispatches += 2;
+    return ZQ_OK;
+}
+
+// Accounting of one synchronous host-pointer call, as zen::hip keeps it
+// (hip_backend.hip:549-565, 597-607): inputs staged through pinned memory
+// (transfer_us), kernel enqueue (launch_us), the stream wait (wait_us; the
+// kernels' event time in gpu_us when tracing), then the read-back
+// (readback_us, also counted in transfer_us).
+struct HostCall {
+    Backend& b;
+    Clock::time_point t_launch{};
+    explicit HostCall(Backend& bb) : b(bb) {}
+    int put(void* dev, const void* src, size_t bytes) {
+        const auto t0 = Clock::now();
+        std::memcpy(b.host_pinned, src, bytes);
+        const hipError_t e = hipMemcpyAsync(dev, b.host_pinned, bytes, hipMemcpyHostToDevice, b.stream);
+        // the staging buffer is reused by the next put: wait for this copy
+        const hipError_t w = e == hipSuccess ? hipStreamSynchronize(b.stream) : e;
+        b.stats.transfer_us += us_since(t0);
+        return w == hipSuccess ? ZQ_OK : fail_hip(b);
+    }
+    void begin() {
+        t_launch = Clock::now();
+        if (b.trace) (void)hipEventRecord(b.ev0, b.stream);
+    }
+    void launched(uint64_t n) {
+        b.stats.dispatches += n;
+        b.stats.launch_us += us_since(t_launch);
+    }
+    int end() {
+        if (b.trace) (void)hipEventRecord(b.ev1, b.stream);
+        const auto t0 = Clock::now();
+        if (hipStreamSynchronize(b.stream) != hipSuccess) return fail_hip(b);
+        b.stats.wait_us += us_since(t0);
+        if (b.trace) {
+            float ms = 0.0f;
+            if (hipEventElapsedTime(&ms, b.ev0, b.ev1) == hipSuccess && ms > 0.0f)
+                b.stats.gpu_us += static_cast<uint64_t>(ms * 1000.0f);
+        }
+        ++b.stats.submits;
+        return ZQ_OK;
+    }
+    int get(void* dst, const void* dev, size_t bytes) {
+        const auto t0 = Clock::now();
+        if (hipMemcpyAsync(b.host_pinned, dev, bytes, hipMemcpyDeviceToHost, b.stream) != hipSuccess ||
+            hipStreamSynchronize(b.stream) != hipSuccess)
+            return fail_hip(b);
+        std::memcpy(dst, b.host_pinned, bytes);
+        const uint64_t us = us_since(t0);
+        b.stats.readback_us += us;
+        b.stats.transfer_us += us;
+        return ZQ_OK;
+    }
+};
+
 }  // namespace
 
 namespace zq {
@@ -253,8 +440,12 @@ void zq_hip_shutdown(void) {
         free_resident(b);
         if (b.dev_scratch) (void)hipFree(b.dev_scratch);
         if (b.host_pinned) (void)hipHostFree(b.host_pinned);
+        if (b.ev0) (void)hipEventDestroy(b.ev0);
+        if (b.ev1) (void)hipEventDestroy(b.ev1);
         (void)hipStreamDestroy(b.stream);
     }
+    b.ev0 = b.ev1 = nullptr;
+    b.trace = false;
     b.dev_scratch = nullptr;
     b.dev_scratch_bytes = 0;
     b.host_pinned = nullptr;
@@ -318,6 +509,227 @@ size_t zq_hip_set_min_elements(size_t elements) {
     return prev;
 }
 
+}  // extern "C"
+
+// Host-pointer calls.  Each public entry point takes the mutex, runs its
+// *_locked body and counts a non-OK result after a successful init as a
+// fallback (the caller runs its CPU route), as zen::hip does
+// (hip_backend.hip:940-1015).
+namespace {
+
+int counted(Backend& b, int st) {
+    if (st != ZQ_OK && b.initialised) ++b.stats.fallbacks;
+    return st;
+}
+
+int gemv_batch_locked(Backend& b, int fmt, const float* x, const zq_gemv_task* tasks, size_t count, size_t cols,
+                      size_t total_rows) {
+    int st = init_locked(b);
+    if (st != ZQ_OK) return st;
+    if (total_rows * cols < b.min_elements) {
+        ++b.stats.declined;
+        return ZQ_DECLINED;
+    }
+    zq::GemvTask dt[zq::kMaxTasks];
+    for (int pass = 0; pass < 2; ++pass)  // a later upload may evict an earlier one: resolve twice
+        for (size_t i = 0; i < count; ++i) {
+            const uint8_t* dw = nullptr;
+            st = ensure_resident(b, fmt, tasks[i].weights, tasks[i].rows, cols, &dw);
+            if (st == ZQ_DECLINED) ++b.stats.declined;
+            if (st != ZQ_OK) return st;
+            dt[i] = zq::GemvTask{dw, nullptr, static_cast<uint32_t>(tasks[i].rows)};
+        }
+    const size_t xbytes = align_up(cols * sizeof(float), 256);
+    const size_t ybytes = total_rows * sizeof(float);
+    st = ensure_scratch(b, xbytes + ybytes, std::max(xbytes, ybytes));
+    if (st != ZQ_OK) return st;
+    float* dx = static_cast<float*>(b.dev_scratch);
+    float* dy = reinterpret_cast<float*>(static_cast<uint8_t*>(b.dev_scratch) + xbytes);
+    size_t off = 0;
+    for (size_t i = 0; i < count; ++i) {
+        dt[i].y = dy + off;
+        off += tasks[i].rows;
+    }
+    HostCall c(b);
+    if ((st = c.put(dx, x, cols * sizeof(float))) != ZQ_OK) return st;
+    c.begin();
+    if (zq::launch_gemv(fmt, dt, static_cast<int>(count), dx, cols, b.stream) != hipSuccess) return fail_hip(b);
+    c.launched(1);
+    if ((st = c.end()) != ZQ_OK) return st;
+    off = 0;
+    for (size_t i = 0; i < count; ++i) {
+        if ((st = c.get(tasks[i].y, dy + off, tasks[i].rows * sizeof(float))) != ZQ_OK) return st;
+        off += tasks[i].rows;
+    }
+    if (count > 1) ++b.stats.batches;
+    return ZQ_OK;
+}
+
+int gemm_batch_locked(Backend& b, int fmt, const float* X, const zq_gemm_task* tasks, size_t count, size_t tokens,
+                      size_t cols, int act, size_t total_rows) {
+    int st = init_locked(b);
+    if (st != ZQ_OK) return st;
+    st = gemm_supported(fmt, cols, act);
+    if (st == ZQ_DECLINED) ++b.stats.declined;
+    if (st != ZQ_OK) return st;
+    if (tokens * total_rows * cols < b.min_elements) {
+        ++b.stats.declined;
+        return ZQ_DECLINED;
+    }
+    const uint8_t* dw[ZQ_MAX_BATCH];
+    size_t rows[ZQ_MAX_BATCH];
+    for (int pass = 0; pass < 2; ++pass)
+        for (size_t i = 0; i < count; ++i) {
+            st = ensure_resident(b, fmt, tasks[i].weights, tasks[i].rows, cols, &dw[i]);
+            if (st == ZQ_DECLINED) ++b.stats.declined;
+            if (st != ZQ_OK) return st;
+            rows[i] = tasks[i].rows;
+        }
+    const size_t xbytes = align_up(tokens * cols * sizeof(float), 256);
+    size_t ybytes = 0, ymax = 0;
+    for (size_t i = 0; i < count; ++i) {
+        ybytes += align_up(tokens * rows[i] * sizeof(float), 256);
+        ymax = std::max(ymax, tokens * rows[i] * sizeof(float));
+    }
+    const size_t wsbytes = batch_workspace_bytes(fmt, rows, count, tokens, cols, act);
+    st = ensure_scratch(b, xbytes + ybytes + wsbytes, std::max(xbytes, ymax));
+    if (st != ZQ_OK) return st;
+    uint8_t* base = static_cast<uint8_t*>(b.dev_scratch);
+    float* dx = reinterpret_cast<float*>(base);
+    float* dy[ZQ_MAX_BATCH];
+    size_t off = xbytes;
+    for (size_t i = 0; i < count; ++i) {
+        dy[i] = reinterpret_cast<float*>(base + off);
+        off += align_up(tokens * rows[i] * sizeof(float), 256);
+    }
+    void* ws = wsbytes ? base + off : nullptr;
+    HostCall c(b);
+    if ((st = c.put(dx, X, tokens * cols * sizeof(float))) != ZQ_OK) return st;
+    c.begin();
+    uint64_t n = 0;
+    st = enqueue_gemm_batch(fmt, dw, dy, rows, count, dx, tokens, cols, act, ws, wsbytes, b.stream, &n);
+    if (st != ZQ_OK) {
+        ++b.stats.errors;
+        return st;
+    }
+    c.launched(n);
+    if ((st = c.end()) != ZQ_OK) return st;
+    for (size_t i = 0; i < count; ++i)
+        if ((st = c.get(tasks[i].Y, dy[i], tokens * rows[i] * sizeof(float))) != ZQ_OK) return st;
+    if (count > 1) ++b.stats.batches;
+    return ZQ_OK;
+}
+
+int ffn_gemv_locked(Backend& b, int fmt, const uint8_t* gate, const uint8_t* up, const uint8_t* down, const float* x,
+                    float* y, size_t ffn_rows, size_t cols, size_t out_rows) {
+    int st = init_locked(b);
+    if (st != ZQ_OK) return st;
+    if ((2 * ffn_rows * cols + out_rows * ffn_rows) < b.min_elements) {
+        ++b.stats.declined;
+        return ZQ_DECLINED;
+    }
+    const uint8_t *dg = nullptr, *du = nullptr, *dd = nullptr;
+    for (int pass = 0; pass < 2; ++pass)
+        if ((st = ensure_resident(b, fmt, gate, ffn_rows, cols, &dg)) != ZQ_OK ||
+            (st = ensure_resident(b, fmt, up, ffn_rows, cols, &du)) != ZQ_OK ||
+            (st = ensure_resident(b, fmt, down, out_rows, ffn_rows, &dd)) != ZQ_OK) {
+            if (st == ZQ_DECLINED) ++b.stats.declined;
+            return st;
+        }
+    const size_t xbytes = align_up(cols * sizeof(float), 256);
+    const size_t hbytes = align_up(ffn_rows * sizeof(float), 256);
+    const size_t ybytes = align_up(out_rows * sizeof(float), 256);
+    st = ensure_scratch(b, xbytes + 3 * hbytes + ybytes, std::max(xbytes, ybytes));
+    if (st != ZQ_OK) return st;
+    uint8_t* base = static_cast<uint8_t*>(b.dev_scratch);
+    float* dx = reinterpret_cast<float*>(base);
+    float* dgate = reinterpret_cast<float*>(base + xbytes);
+    float* dup = reinterpret_cast<float*>(base + xbytes + hbytes);
+    float* dact = reinterpret_cast<float*>(base + xbytes + 2 * hbytes);
+    float* dy = reinterpret_cast<float*>(base + xbytes + 3 * hbytes);
+    HostCall c(b);
+    if ((st = c.put(dx, x, cols * sizeof(float))) != ZQ_OK) return st;
+    c.begin();
+    zq::GemvTask gu[2] = {{dg, dgate, static_cast<uint32_t>(ffn_rows)}, {du, dup, static_cast<uint32_t>(ffn_rows)}};
+    if (zq::launch_gemv(fmt, gu, 2, dx, cols, b.stream) != hipSuccess) return fail_hip(b);
+    if (zq::launch_silu_mul(dgate, dup, dact, ffn_rows, b.stream) != hipSuccess) return fail_hip(b);
+    zq::GemvTask dn{dd, dy, static_cast<uint32_t>(out_rows)};
+    if (zq::launch_gemv(fmt, &dn, 1, dact, ffn_rows, b.stream) != hipSuccess) return fail_hip(b);
+    c.launched(3);
+    if ((st = c.end()) != ZQ_OK) return st;
+    return c.get(y, dy, out_rows * sizeof(float));
+}
+
+int rms_norm_locked(Backend& b, const float* x, const float* w, float* y, size_t rows, size_t cols, float eps) {
+    int st = init_locked(b);
+    if (st != ZQ_OK) return st;
+    const size_t xbytes = align_up(rows * cols * sizeof(float), 256);
+    const size_t wbytes = align_up(cols * sizeof(float), 256);
+    st = ensure_scratch(b, 2 * xbytes + wbytes, xbytes);
+    if (st != ZQ_OK) return st;
+    uint8_t* base = static_cast<uint8_t*>(b.dev_scratch);
+    float* dx = reinterpret_cast<float*>(base);
+    float* dw = reinterpret_cast<float*>(base + xbytes);
+    float* dy = reinterpret_cast<float*>(base + xbytes + wbytes);
+    HostCall c(b);
+    if ((st = c.put(dx, x, rows * cols * sizeof(float))) != ZQ_OK) return st;
+    if ((st = c.put(dw, w, cols * sizeof(float))) != ZQ_OK) return st;
+    c.begin();
+    if (zq::launch_rmsnorm(dx, dw, dy, uint32_t(rows), uint32_t(cols), eps, b.stream) != hipSuccess) return fail_hip(b);
+    c.launched(1);
+    if ((st = c.end()) != ZQ_OK) return st;
+    return c.get(y, dy, rows * cols * sizeof(float));
+}
+
+int ffn_residual_locked(Backend& b, int fmt, const uint8_t* wo, const uint8_t* wg, const uint8_t* wu, const uint8_t* wd,
+                        const float* norm_w, const float* x, const float* attn_out, float* out, size_t hidden,
+                        size_t attn_width, size_t ffn_rows, float eps) {
+    int st = init_locked(b);
+    if (st != ZQ_OK) return st;
+    if ((hidden * attn_width + 3 * ffn_rows * hidden) < b.min_elements) {
+        ++b.stats.declined;
+        return ZQ_DECLINED;
+    }
+    const uint8_t *dwo = nullptr, *dwg = nullptr, *dwu = nullptr, *dwd = nullptr;
+    for (int pass = 0; pass < 2; ++pass)
+        if ((st = ensure_resident(b, fmt, wo, hidden, attn_width, &dwo)) != ZQ_OK ||
+            (st = ensure_resident(b, fmt, wg, ffn_rows, hidden, &dwg)) != ZQ_OK ||
+            (st = ensure_resident(b, fmt, wu, ffn_rows, hidden, &dwu)) != ZQ_OK ||
+            (st = ensure_resident(b, fmt, wd, hidden, ffn_rows, &dwd)) != ZQ_OK) {
+            if (st == ZQ_DECLINED) ++b.stats.declined;
+            return st;
+        }
+    const size_t hb = align_up(hidden * sizeof(float), 256), ab = align_up(attn_width * sizeof(float), 256);
+    const size_t wsb = zq_hip_ffn_residual_workspace_bytes(hidden, ffn_rows);
+    st = ensure_scratch(b, 3 * hb + ab + wsb, std::max(hb, ab));
+    if (st != ZQ_OK) return st;
+    uint8_t* base = static_cast<uint8_t*>(b.dev_scratch);
+    float* dx = reinterpret_cast<float*>(base);
+    float* dn = reinterpret_cast<float*>(base + hb);
+    float* dout = reinterpret_cast<float*>(base + 2 * hb);
+    float* da = reinterpret_cast<float*>(base + 3 * hb);
+    void* ws = base + 3 * hb + ab;
+    HostCall c(b);
+    if ((st = c.put(dx, x, hidden * sizeof(float))) != ZQ_OK || (st = c.put(dn, norm_w, hidden * sizeof(float))) != ZQ_OK ||
+        (st = c.put(da, attn_out, attn_width * sizeof(float))) != ZQ_OK)
+        return st;
+    c.begin();
+    uint64_t n = 0;
+    st = enqueue_ffn_residual(fmt, dwo, dwg, dwu, dwd, dn, dx, da, dout, hidden, attn_width, ffn_rows, eps, ws, wsb,
+                              b.stream, &n);
+    if (st != ZQ_OK) {
+        ++b.stats.errors;
+        return st;
+    }
+    c.launched(n);
+    if ((st = c.end()) != ZQ_OK) return st;
+    return c.get(out, dout, hidden * sizeof(float));
+}
+
+}  // namespace
+
+extern "C" {
+
 int zq_hip_gemv_batch(int fmt, const float* x, const zq_gemv_task* tasks, size_t count, size_t cols) {
     if (!x || !tasks || count < 1 || count > ZQ_MAX_BATCH || !valid_fmt(fmt) || !zq::row_bytes(fmt, cols))
         return ZQ_ERR_ARG;
@@ -329,56 +741,11 @@ int zq_hip_gemv_batch(int fmt, const float* x, const zq_gemv_task* tasks, size_t
     Backend& b = B();
     std::lock_guard<std::mutex> lock(b.mu);
     try {
-        int st = init_locked(b);
-        if (st != ZQ_OK) return st;
-        if (total_rows * cols < b.min_elements) {
-            ++b.stats.declined;
-            return ZQ_DECLINED;
-        }
-        zq::GemvTask dt[zq::kMaxTasks];
-        for (size_t i = 0; i < count; ++i) {
-            const uint8_t* dw = nullptr;
-            st = ensure_resident(b, fmt, tasks[i].weights, tasks[i].rows, cols, &dw);
-            if (st == ZQ_DECLINED) ++b.stats.declined;
-            if (st != ZQ_OK) return st;
-            dt[i] = zq::GemvTask{dw, nullptr, static_cast<uint32_t>(tasks[i].rows)};
-        }
-        const size_t xbytes = align_up(cols * sizeof(float), 256);
-        const size_t ybytes = total_rows * sizeof(float);
-        st = ensure_scratch(b, xbytes + ybytes, xbytes + ybytes);
-        if (st != ZQ_OK) return st;
-        float* dx = static_cast<float*>(b.dev_scratch);
-        float* dy = reinterpret_cast<float*>(static_cast<uint8_t*>(b.dev_scratch) + xbytes);
-        float* hx = static_cast<float*>(b.host_pinned);
-        float* hy = reinterpret_cast<float*>(static_cast<uint8_t*>(b.host_pinned) + xbytes);
-        size_t off = 0;
-        for (size_t i = 0; i < count; ++i) {
-            dt[i].y = dy + off;
-            off += tasks[i].rows;
-        }
-        auto t0 = Clock::now();
-        std::memcpy(hx, x, cols * sizeof(float));
-        if (hipMemcpyAsync(dx, hx, cols * sizeof(float), hipMemcpyHostToDevice, b.stream) != hipSuccess)
-            return fail_hip(b);
-        if (zq::launch_gemv(fmt, dt, static_cast<int>(count), dx, cols, b.stream) != hipSuccess) return fail_hip(b);
-        ++b.stats.dispatches;
-        if (hipMemcpyAsync(hy, dy, ybytes, hipMemcpyDeviceToHost, b.stream) != hipSuccess) return fail_hip(b);
-        const auto t1 = Clock::now();
-        if (hipStreamSynchronize(b.stream) != hipSuccess) return fail_hip(b);
-        b.stats.wait_us += us_since(t1);
-        off = 0;
-        for (size_t i = 0; i < count; ++i) {
-            std::memcpy(tasks[i].y, hy + off, tasks[i].rows * sizeof(float));
-            off += tasks[i].rows;
-        }
-        b.stats.transfer_us += us_since(t0);
-        ++b.stats.submits;
-        if (count > 1) ++b.stats.batches;
-        return ZQ_OK;
+        return counted(b, gemv_batch_locked(b, fmt, x, tasks, count, cols, total_rows));
     } catch (const std::bad_alloc&) {
-        return ZQ_ERR_OOM;
+        return counted(b, ZQ_ERR_OOM);
     } catch (...) {
-        return ZQ_ERR_HIP;
+        return counted(b, ZQ_ERR_HIP);
     }
 }
 
@@ -388,62 +755,33 @@ int zq_hip_gemv(int fmt, const uint8_t* weights, const float* x, float* y, size_
     return zq_hip_gemv_batch(fmt, x, &t, 1, cols);
 }
 
-int zq_hip_gemm(int fmt, const uint8_t* weights, const float* X, float* Y, size_t tokens, size_t rows, size_t cols,
-                int act_mode) {
-    if (!weights || !X || !Y || !tokens || !rows || !valid_fmt(fmt) || !zq::row_bytes(fmt, cols) ||
-        tokens > (1u << 24) || rows > (1u << 24))
+int zq_hip_gemm_batch(int fmt, const float* X, const zq_gemm_task* tasks, size_t count, size_t tokens, size_t cols,
+                      int act_mode) {
+    if (!X || !tasks || count < 1 || count > ZQ_MAX_BATCH || !tokens || !valid_fmt(fmt) ||
+        !zq::row_bytes(fmt, cols) || tokens > (1u << 24))
         return ZQ_ERR_ARG;
+    size_t total_rows = 0;
+    for (size_t i = 0; i < count; ++i) {
+        if (!tasks[i].weights || !tasks[i].Y || !tasks[i].rows || tasks[i].rows > (1u << 24)) return ZQ_ERR_ARG;
+        total_rows += tasks[i].rows;
+    }
     const int act = resolve_act(fmt, act_mode);
     Backend& b = B();
     std::lock_guard<std::mutex> lock(b.mu);
     try {
-        int st = init_locked(b);
-        if (st != ZQ_OK) return st;
-        st = gemm_supported(fmt, cols, act);
-        if (st == ZQ_DECLINED) ++b.stats.declined;
-        if (st != ZQ_OK) return st;
-        if (tokens * rows * cols < b.min_elements) {
-            ++b.stats.declined;
-            return ZQ_DECLINED;
-        }
-        const uint8_t* dw = nullptr;
-        st = ensure_resident(b, fmt, weights, rows, cols, &dw);
-        if (st == ZQ_DECLINED) ++b.stats.declined;
-        if (st != ZQ_OK) return st;
-        const size_t xbytes = align_up(tokens * cols * sizeof(float), 256);
-        const size_t ybytes = align_up(tokens * rows * sizeof(float), 256);
-        const size_t wsbytes = zq_hip_gemm_workspace_bytes(fmt, tokens, rows, cols, act);
-        st = ensure_scratch(b, xbytes + ybytes + wsbytes, xbytes + ybytes);
-        if (st != ZQ_OK) return st;
-        uint8_t* base = static_cast<uint8_t*>(b.dev_scratch);
-        float* dx = reinterpret_cast<float*>(base);
-        float* dy = reinterpret_cast<float*>(base + xbytes);
-        void* ws = wsbytes ? base + xbytes + ybytes : nullptr;
-        float* hx = static_cast<float*>(b.host_pinned);
-        float* hy = reinterpret_cast<float*>(static_cast<uint8_t*>(b.host_pinned) + xbytes);
-        auto t0 = Clock::now();
-        std::memcpy(hx, X, tokens * cols * sizeof(float));
-        if (hipMemcpyAsync(dx, hx, tokens * cols * sizeof(float), hipMemcpyHostToDevice, b.stream) != hipSuccess)
-            return fail_hip(b);
-        st = enqueue_gemm(fmt, dw, dx, dy, tokens, rows, cols, act, ws, wsbytes, b.stream, &b.stats.dispatches);
-        if (st != ZQ_OK) {
-            ++b.stats.errors;
-            return st;
-        }
-        if (hipMemcpyAsync(hy, dy, tokens * rows * sizeof(float), hipMemcpyDeviceToHost, b.stream) != hipSuccess)
-            return fail_hip(b);
-        const auto t1 = Clock::now();
-        if (hipStreamSynchronize(b.stream) != hipSuccess) return fail_hip(b);
-        b.stats.wait_us += us_since(t1);
-        std::memcpy(Y, hy, tokens * rows * sizeof(float));
-        b.stats.transfer_us += us_since(t0);
-        ++b.stats.submits;
-        return ZQ_OK;
+        return counted(b, gemm_batch_locked(b, fmt, X, tasks, count, tokens, cols, act, total_rows));
     } catch (const std::bad_alloc&) {
-        return ZQ_ERR_OOM;
+        return counted(b, ZQ_ERR_OOM);
     } catch (...) {
-        return ZQ_ERR_HIP;
+        return counted(b, ZQ_ERR_HIP);
     }
+}
+
+int zq_hip_gemm(int fmt, const uint8_t* weights, const float* X, float* Y, size_t tokens, size_t rows, size_t cols,
+                int act_mode) {
+    if (!weights || !Y || !rows) return ZQ_ERR_ARG;
+    const zq_gemm_task t{weights, Y, rows};
+    return zq_hip_gemm_batch(fmt, X, &t, 1, tokens, cols, act_mode);
 }
 
 int zq_hip_ffn_gemv(int fmt, const uint8_t* gate, const uint8_t* up, const uint8_t* down, const float* x, float* y,
@@ -455,59 +793,42 @@ int zq_hip_ffn_gemv(int fmt, const uint8_t* gate, const uint8_t* up, const uint8
     Backend& b = B();
     std::lock_guard<std::mutex> lock(b.mu);
     try {
-        int st = init_locked(b);
-        if (st != ZQ_OK) return st;
-        if ((2 * ffn_rows * cols + out_rows * ffn_rows) < b.min_elements) {
-            ++b.stats.declined;
-            return ZQ_DECLINED;
-        }
-        const uint8_t *dg = nullptr, *du = nullptr, *dd = nullptr;
-        if ((st = ensure_resident(b, fmt, gate, ffn_rows, cols, &dg)) != ZQ_OK ||
-            (st = ensure_resident(b, fmt, up, ffn_rows, cols, &du)) != ZQ_OK ||
-            (st = ensure_resident(b, fmt, down, out_rows, ffn_rows, &dd)) != ZQ_OK) {
-            if (st == ZQ_DECLINED) ++b.stats.declined;
-            return st;
-        }
-        // a second upload may have evicted the first: re-resolve all three
-        if ((st = ensure_resident(b, fmt, gate, ffn_rows, cols, &dg)) != ZQ_OK ||
-            (st = ensure_resident(b, fmt, up, ffn_rows, cols, &du)) != ZQ_OK)
-            return st;
-        const size_t xbytes = align_up(cols * sizeof(float), 256);
-        const size_t hbytes = align_up(ffn_rows * sizeof(float), 256);
-        const size_t ybytes = align_up(out_rows * sizeof(float), 256);
-        st = ensure_scratch(b, xbytes + 3 * hbytes + ybytes, xbytes + ybytes);
-        if (st != ZQ_OK) return st;
-        uint8_t* base = static_cast<uint8_t*>(b.dev_scratch);
-        float* dx = reinterpret_cast<float*>(base);
-        float* dgate = reinterpret_cast<float*>(base + xbytes);
-        float* dup = reinterpret_cast<float*>(base + xbytes + hbytes);
-        float* dact = reinterpret_cast<float*>(base + xbytes + 2 * hbytes);
-        float* dy = reinterpret_cast<float*>(base + xbytes + 3 * hbytes);
-        float* hx = static_cast<float*>(b.host_pinned);
-        float* hy = reinterpret_cast<float*>(static_cast<uint8_t*>(b.host_pinned) + xbytes);
-        auto t0 = Clock::now();
-        std::memcpy(hx, x, cols * sizeof(float));
-        if (hipMemcpyAsync(dx, hx, cols * sizeof(float), hipMemcpyHostToDevice, b.stream) != hipSuccess)
-            return fail_hip(b);
-        zq::GemvTask gu[2] = {{dg, dgate, static_cast<uint32_t>(ffn_rows)}, {du, dup, static_cast<uint32_t>(ffn_rows)}};
-        if (zq::launch_gemv(fmt, gu, 2, dx, cols, b.stream) != hipSuccess) return fail_hip(b);
-        if (zq::launch_silu_mul(dgate, dup, dact, ffn_rows, b.stream) != hipSuccess) return fail_hip(b);
-        zq::GemvTask dn{dd, dy, static_cast<uint32_t>(out_rows)};
-        if (zq::launch_gemv(fmt, &dn, 1, dact, ffn_rows, b.stream) != hipSuccess) return fail_hip(b);
-        b.stats.dispatches += 3;
-        if (hipMemcpyAsync(hy, dy, out_rows * sizeof(float), hipMemcpyDeviceToHost, b.stream) != hipSuccess)
-            return fail_hip(b);
-        const auto t1 = Clock::now();
-        if (hipStreamSynchronize(b.stream) != hipSuccess) return fail_hip(b);
-        b.stats.wait_us += us_since(t1);
-        std::memcpy(y, hy, out_rows * sizeof(float));
-        b.stats.transfer_us += us_since(t0);
-        ++b.stats.submits;
-        return ZQ_OK;
+        return counted(b, ffn_gemv_locked(b, fmt, gate, up, down, x, y, ffn_rows, cols, out_rows));
     } catch (const std::bad_alloc&) {
-        return ZQ_ERR_OOM;
+        return counted(b, ZQ_ERR_OOM);
     } catch (...) {
-        return ZQ_ERR_HIP;
+        return counted(b, ZQ_ERR_HIP);
+    }
+}
+
+int zq_hip_rms_norm(const float* x, const float* weight, float* y, size_t rows, size_t cols, float eps) {
+    if (!x || !weight || !y || !rows || !cols || rows > (1u << 24) || cols > (1u << 24)) return ZQ_ERR_ARG;
+    Backend& b = B();
+    std::lock_guard<std::mutex> lock(b.mu);
+    try {
+        return counted(b, rms_norm_locked(b, x, weight, y, rows, cols, eps));
+    } catch (const std::bad_alloc&) {
+        return counted(b, ZQ_ERR_OOM);
+    } catch (...) {
+        return counted(b, ZQ_ERR_HIP);
+    }
+}
+
+int zq_hip_ffn_residual_fused(int fmt, const uint8_t* attn_output, const uint8_t* gate, const uint8_t* up,
+                              const uint8_t* down, const float* norm_weight, const float* x, const float* attn_out,
+                              float* out, size_t hidden, size_t attn_width, size_t ffn_rows, float eps) {
+    if (!ffn_residual_args_ok(fmt, attn_output, gate, up, down, norm_weight, x, attn_out, out, hidden, attn_width,
+                              ffn_rows))
+        return ZQ_ERR_ARG;
+    Backend& b = B();
+    std::lock_guard<std::mutex> lock(b.mu);
+    try {
+        return counted(b, ffn_residual_locked(b, fmt, attn_output, gate, up, down, norm_weight, x, attn_out, out,
+                                              hidden, attn_width, ffn_rows, eps));
+    } catch (const std::bad_alloc&) {
+        return counted(b, ZQ_ERR_OOM);
+    } catch (...) {
+        return counted(b, ZQ_ERR_HIP);
     }
 }
 
@@ -571,6 +892,62 @@ int zq_hip_gemm_dev(int fmt, const void* weights, const float* X, float* Y, size
     uint64_t d = 0;
     return enqueue_gemm(fmt, static_cast<const uint8_t*>(weights), X, Y, tokens, rows, cols, act, workspace,
                         workspace_bytes, static_cast<hipStream_t>(stream), &d);
+}
+
+size_t zq_hip_gemm_batch_workspace_bytes(int fmt, const zq_gemm_task* tasks, size_t count, size_t tokens, size_t cols,
+                                         int act_mode) {
+    if (!tasks || count < 1 || count > ZQ_MAX_BATCH || !valid_fmt(fmt) || !zq::row_bytes(fmt, cols) || !tokens) return 0;
+    size_t rows[ZQ_MAX_BATCH];
+    for (size_t i = 0; i < count; ++i) {
+        if (!tasks[i].rows) return 0;
+        rows[i] = tasks[i].rows;
+    }
+    return batch_workspace_bytes(fmt, rows, count, tokens, cols, resolve_act(fmt, act_mode));
+}
+
+int zq_hip_gemm_batch_dev(int fmt, const float* X, const zq_gemm_task* tasks, size_t count, size_t tokens, size_t cols,
+                          int act_mode, void* workspace, size_t workspace_bytes, void* stream) {
+    if (!X || !tasks || count < 1 || count > ZQ_MAX_BATCH || !tokens || !valid_fmt(fmt) ||
+        !zq::row_bytes(fmt, cols) || tokens > (1u << 24))
+        return ZQ_ERR_ARG;
+    const uint8_t* w[ZQ_MAX_BATCH];
+    float* Y[ZQ_MAX_BATCH];
+    size_t rows[ZQ_MAX_BATCH];
+    for (size_t i = 0; i < count; ++i) {
+        if (!tasks[i].weights || !tasks[i].Y || !tasks[i].rows || tasks[i].rows > (1u << 24)) return ZQ_ERR_ARG;
+        w[i] = tasks[i].weights;
+        Y[i] = tasks[i].Y;
+        rows[i] = tasks[i].rows;
+    }
+    const int act = resolve_act(fmt, act_mode);
+    const int st = gemm_supported(fmt, cols, act);
+    if (st != ZQ_OK) return st;
+    uint64_t d = 0;
+    return enqueue_gemm_batch(fmt, w, Y, rows, count, X, tokens, cols, act, workspace, workspace_bytes,
+                              static_cast<hipStream_t>(stream), &d);
+}
+
+int zq_hip_rms_norm_dev(const float* x, const float* weight, float* y, size_t rows, size_t cols, float eps,
+                        void* stream) {
+    if (!x || !weight || !y || !rows || !cols || rows > (1u << 24) || cols > (1u << 24)) return ZQ_ERR_ARG;
+    return zq::launch_rmsnorm(x, weight, y, uint32_t(rows), uint32_t(cols), eps, static_cast<hipStream_t>(stream)) ==
+                   hipSuccess
+               ? ZQ_OK
+               : ZQ_ERR_HIP;
+}
+
+int zq_hip_ffn_residual_fused_dev(int fmt, const void* attn_output, const void* gate, const void* up, const void* down,
+                                  const float* norm_weight, const float* x, const float* attn_out, float* out,
+                                  size_t hidden, size_t attn_width, size_t ffn_rows, float eps, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+    if (!ffn_residual_args_ok(fmt, attn_output, gate, up, down, norm_weight, x, attn_out, out, hidden, attn_width,
+                              ffn_rows))
+        return ZQ_ERR_ARG;
+    uint64_t d = 0;
+    return enqueue_ffn_residual(fmt, static_cast<const uint8_t*>(attn_output), static_cast<const uint8_t*>(gate),
+                                static_cast<const uint8_t*>(up), static_cast<const uint8_t*>(down), norm_weight, x,
+                                attn_out, out, hidden, attn_width, ffn_rows, eps, workspace, workspace_bytes,
+                                static_cast<hipStream_t>(stream), &d);
 }
 
 int zq_hip_quantize_acts_dev(const float* X, int8_t* xq, float* xs, size_t tokens, size_t cols, void* stream) {

@@ -102,6 +102,8 @@ hipError_t launch_attention_decode(const float* q, const float* knew, const floa
                                    const uint32_t* pos, uint32_t H, uint32_t KH, uint32_t D, uint32_t pairs,
                                    uint32_t max_pos, float scale, hipStream_t stream);
 hipError_t launch_add(float* x, const float* y, size_t n, hipStream_t stream);
+// out = x + y elementwise (out may alias x)
+hipError_t launch_add_to(const float* x, const float* y, float* out, size_t n, hipStream_t stream);
 // x += r, then y = rmsnorm(x) * w (rows of n)
 hipError_t launch_add_rmsnorm(float* x, const float* r, const float* w, float* y, uint32_t rows, uint32_t n, float eps,
                               hipStream_t stream);

@@ -533,9 +533,10 @@ __global__ __launch_bounds__(kT) void attention_combine_kernel(const float* __re
     }
 }
 
-__global__ __launch_bounds__(kT) void add_kernel(float* __restrict__ x, const float* __restrict__ y, size_t n) {
+// out = x + y (out may be x)
+__global__ __launch_bounds__(kT) void add_kernel(const float* x, const float* __restrict__ y, float* out, size_t n) {
     const size_t i = size_t(blockIdx.x) * kT + threadIdx.x;
-    if (i < n) x[i] += y[i];
+    if (i < n) out[i] = x[i] + y[i];
 }
 
 // Greedy id: the lowest index among the finite maxima.  Stage 1: kArgBlocks
@@ -687,11 +688,13 @@ hipError_t launch_attention_decode(const float* q, const float* knew, const floa
     return hipGetLastError();
 }
 
-hipError_t launch_add(float* x, const float* y, size_t n, hipStream_t stream) {
-    if (!x || !y || !n) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(add_kernel, dim3(uint32_t((n + kT - 1) / kT)), dim3(kT), 0, stream, x, y, n);
+hipError_t launch_add_to(const float* x, const float* y, float* out, size_t n, hipStream_t stream) {
+    if (!x || !y || !out || !n) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(add_kernel, dim3(uint32_t((n + kT - 1) / kT)), dim3(kT), 0, stream, x, y, out, n);
     return hipGetLastError();
 }
+
+hipError_t launch_add(float* x, const float* y, size_t n, hipStream_t stream) { return launch_add_to(x, y, x, n, stream); }
 
 size_t argmax_partial_bytes() { return size_t(kArgBlocks) * 8; }
 

@@ -622,6 +622,26 @@ int zq_model_create_synthetic(const zq_model_config* cfg, uint64_t seed, zq_mode
 
 void zq_model_free(zq_model* m) { delete m; }
 
+int zq_model_weight(const zq_model* m, uint32_t layer, int which, const void** dev, uint32_t* rows, uint32_t* cols,
+                    int* fmt) {
+    if (!m || !dev) return ZQ_ERR_ARG;
+    const Weight* w = nullptr;
+    if (layer == ZQ_MODEL_GLOBAL) {
+        if (which == ZQ_W_EMBED) w = &m->embd;
+        else if (which == ZQ_W_OUTPUT) w = &m->out;
+    } else if (layer < m->layers.size() && which >= ZQ_W_Q && which <= ZQ_W_DOWN) {
+        const Layer& L = m->layers[layer];
+        const Weight* t[7] = {&L.q, &L.k, &L.v, &L.o, &L.gate, &L.up, &L.down};
+        w = t[which - ZQ_W_Q];
+    }
+    if (!w || !w->p) return ZQ_ERR_ARG;
+    *dev = w->p;
+    if (rows) *rows = w->rows;
+    if (cols) *cols = w->cols;
+    if (fmt) *fmt = w->fmt;
+    return ZQ_OK;
+}
+
 int zq_model_set_prefill_mode(zq_model* m, int mode) {
     if (!m || (mode != ZQ_PREFILL_INT8 && mode != ZQ_PREFILL_F32)) return ZQ_ERR_ARG;
     m->prefill_mode = mode;

@@ -13,6 +13,8 @@ import numpy as np
 from . import zq
 
 PREFILL_INT8, PREFILL_F32 = 0, 1
+GLOBAL = 0xFFFFFFFF
+W_EMBED, W_OUTPUT, W_Q, W_K, W_V, W_O, W_GATE, W_UP, W_DOWN = range(9)
 
 
 class ModelError(RuntimeError):
@@ -88,6 +90,13 @@ class Model:
                                            out.ctypes.data_as(ctypes.c_void_p), ctypes.byref(n), ctypes.byref(pm),
                                            ctypes.byref(dm)), "generate")
         return out[:n.value].tolist(), pm.value, dm.value
+
+    def weight(self, layer, which):
+        """(device address, rows, cols, GGML type) of one resident weight."""
+        p, r, c, f = ctypes.c_void_p(), ctypes.c_uint32(), ctypes.c_uint32(), ctypes.c_int()
+        zq.check(self._L.zq_model_weight(self._h, layer, which, ctypes.byref(p), ctypes.byref(r), ctypes.byref(c),
+                                         ctypes.byref(f)), "weight")
+        return p.value, r.value, c.value, f.value
 
     def memory(self):
         w, c, a = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_uint64()

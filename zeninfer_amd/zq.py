@@ -17,6 +17,7 @@ FORMATS = {"Q4_0": Q4_0, "Q8_0": Q8_0, "Q4_K": Q4_K, "Q5_K": Q5_K, "Q6_K": Q6_K}
 BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210)}
 ACT_DEFAULT, ACT_INT8, ACT_F32 = 0, 1, 2
 OK, DECLINED = 0, 1
+ERR_ARG, ERR_NO_DEVICE, ERR_OOM, ERR_HIP = -1, -2, -3, -4
 WEIGHT_TAIL_PAD = 64
 MAX_BATCH = 8
 
@@ -39,11 +40,16 @@ class Info(ctypes.Structure):
 class Stats(ctypes.Structure):
     _fields_ = [(n, ctypes.c_uint64) for n in (
         "dispatches", "submits", "batches", "uploads", "upload_bytes", "resident_bytes", "resident_tensors",
-        "evictions", "declined", "errors", "upload_us", "transfer_us", "wait_us")]
+        "evictions", "declined", "errors", "upload_us", "transfer_us", "wait_us", "fallbacks", "alloc_us",
+        "launch_us", "readback_us", "gpu_us")]
 
 
 class GemvTask(ctypes.Structure):
     _fields_ = [("weights", _P), ("y", _P), ("rows", _S)]
+
+
+class GemmTask(ctypes.Structure):
+    _fields_ = [("weights", _P), ("Y", _P), ("rows", _S)]
 
 
 # Every symbol include/zq_hip.h declares, with (restype, argtypes).
@@ -63,6 +69,17 @@ SIGNATURES = {
     "zq_hip_gemv_batch": (ctypes.c_int, [ctypes.c_int, _P, ctypes.POINTER(GemvTask), _S, _S]),
     "zq_hip_gemm": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _S, _S, _S, ctypes.c_int]),
     "zq_hip_ffn_gemv": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _P, _P, _S, _S, _S]),
+    "zq_hip_gemm_batch": (ctypes.c_int, [ctypes.c_int, _P, ctypes.POINTER(GemmTask), _S, _S, _S, ctypes.c_int]),
+    "zq_hip_rms_norm": (ctypes.c_int, [_P, _P, _P, _S, _S, ctypes.c_float]),
+    "zq_hip_ffn_residual_fused": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _P, _P, _P, _P, _P, _S, _S, _S,
+                                                 ctypes.c_float]),
+    "zq_hip_gemm_batch_workspace_bytes": (_S, [ctypes.c_int, ctypes.POINTER(GemmTask), _S, _S, _S, ctypes.c_int]),
+    "zq_hip_gemm_batch_dev": (ctypes.c_int, [ctypes.c_int, _P, ctypes.POINTER(GemmTask), _S, _S, _S, ctypes.c_int,
+                                             _P, _S, _P]),
+    "zq_hip_rms_norm_dev": (ctypes.c_int, [_P, _P, _P, _S, _S, ctypes.c_float, _P]),
+    "zq_hip_ffn_residual_workspace_bytes": (_S, [_S, _S]),
+    "zq_hip_ffn_residual_fused_dev": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _P, _P, _P, _P, _P, _S, _S, _S,
+                                                     ctypes.c_float, _P, _S, _P]),
     "zq_hip_release": (ctypes.c_int, [_P]),
     "zq_hip_release_all": (ctypes.c_int, []),
     "zq_hip_gemv_dev": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _S, _S, _P]),
@@ -117,6 +134,9 @@ MODEL_SIGNATURES = {
     "zq_model_create_synthetic": (ctypes.c_int, [ctypes.POINTER(ModelConfig), ctypes.c_uint64, ctypes.POINTER(_P),
                                                  ctypes.c_char_p, _S]),
     "zq_model_free": (None, [_P]),
+    "zq_model_weight": (ctypes.c_int, [_P, ctypes.c_uint32, ctypes.c_int, ctypes.POINTER(_P),
+                                       ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_uint32),
+                                       ctypes.POINTER(ctypes.c_int)]),
     "zq_model_set_prefill_mode": (ctypes.c_int, [_P, ctypes.c_int]),
     "zq_model_prefill": (ctypes.c_int, [_P, _P, _S, _P, ctypes.POINTER(ctypes.c_uint32)]),
     "zq_model_decode": (ctypes.c_int, [_P, ctypes.c_uint32, _P, ctypes.POINTER(ctypes.c_uint32)]),
@@ -279,6 +299,34 @@ def ffn_gemv(fmt, gate, up, down, x, ffn_rows, cols, out_rows):
     return y
 
 
+def gemm_batch(fmt, ws, X, tokens, rows, cols, act=ACT_DEFAULT):
+    """Y_i = X . W_i^T for every weight of ws (shared X), one submission."""
+    X = np.ascontiguousarray(X, dtype=np.float32)
+    Ys = [np.empty(tokens * r, np.float32) for r in rows]
+    tasks = (GemmTask * len(ws))(*[GemmTask(w.ctypes.data, Y.ctypes.data, r) for w, Y, r in zip(ws, Ys, rows)])
+    check(lib().zq_hip_gemm_batch(fmt, _np_ptr(X), tasks, len(ws), tokens, cols, act), "zq_hip_gemm_batch")
+    return Ys
+
+
+def rms_norm(x, w, rows, cols, eps):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    y = np.empty(rows * cols, np.float32)
+    check(lib().zq_hip_rms_norm(_np_ptr(x), _np_ptr(w), _np_ptr(y), rows, cols, eps), "zq_hip_rms_norm")
+    return y
+
+
+def ffn_residual_fused(fmt, wo, wg, wu, wd, norm_w, x, attn_out, hidden, attn_width, ffn_rows, eps):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    a = np.ascontiguousarray(attn_out, dtype=np.float32)
+    nw = np.ascontiguousarray(norm_w, dtype=np.float32)
+    out = np.empty(hidden, np.float32)
+    check(lib().zq_hip_ffn_residual_fused(fmt, _np_ptr(wo), _np_ptr(wg), _np_ptr(wu), _np_ptr(wd), _np_ptr(nw),
+                                          _np_ptr(x), _np_ptr(a), _np_ptr(out), hidden, attn_width, ffn_rows, eps),
+          "zq_hip_ffn_residual_fused")
+    return out
+
+
 def release(w):
     return lib().zq_hip_release(_np_ptr(w))
 
@@ -318,6 +366,56 @@ def gemm_dev(fmt, w, X, Y, tokens, rows, cols, act=ACT_DEFAULT, workspace=None, 
     _need(workspace, workspace_bytes, "gemm_dev workspace")
     return check(lib().zq_hip_gemm_dev(fmt, _dptr(w), _dptr(X), _dptr(Y), tokens, rows, cols, act,
                                        _dptr(workspace), workspace_bytes, _stream(stream)), "zq_hip_gemm_dev")
+
+
+def _gemm_tasks(tasks):
+    return (GemmTask * len(tasks))(*[GemmTask(_dptr(w), _dptr(Y), r) for w, Y, r in tasks])
+
+
+def gemm_batch_workspace_bytes(fmt, rows, tokens, cols, act=ACT_DEFAULT):
+    arr = (GemmTask * len(rows))(*[GemmTask(None, None, r) for r in rows])
+    return lib().zq_hip_gemm_batch_workspace_bytes(fmt, arr, len(rows), tokens, cols, act)
+
+
+def gemm_batch_dev(fmt, X, tasks, tokens, cols, act=ACT_DEFAULT, workspace=None, workspace_bytes=0, stream=None):
+    """tasks: list of (weights, Y, rows)."""
+    _need(X, 4 * tokens * cols, "gemm_batch_dev X")
+    for w, Y, r in tasks:
+        _need(w, weight_bytes(fmt, r, cols), "gemm_batch_dev weights")
+        _need(Y, 4 * tokens * r, "gemm_batch_dev Y")
+    _need(workspace, workspace_bytes, "gemm_batch_dev workspace")
+    return check(lib().zq_hip_gemm_batch_dev(fmt, _dptr(X), _gemm_tasks(tasks), len(tasks), tokens, cols, act,
+                                             _dptr(workspace), workspace_bytes, _stream(stream)),
+                 "zq_hip_gemm_batch_dev")
+
+
+def rms_norm_dev(x, w, y, rows, cols, eps, stream=None):
+    _need(x, 4 * rows * cols, "rms_norm_dev x")
+    _need(w, 4 * cols, "rms_norm_dev weight")
+    _need(y, 4 * rows * cols, "rms_norm_dev y")
+    return check(lib().zq_hip_rms_norm_dev(_dptr(x), _dptr(w), _dptr(y), rows, cols, eps, _stream(stream)),
+                 "zq_hip_rms_norm_dev")
+
+
+def ffn_residual_workspace_bytes(hidden, ffn_rows):
+    return lib().zq_hip_ffn_residual_workspace_bytes(hidden, ffn_rows)
+
+
+def ffn_residual_fused_dev(fmt, wo, wg, wu, wd, norm_w, x, attn_out, out, hidden, attn_width, ffn_rows, eps,
+                           workspace, workspace_bytes, stream=None):
+    _need(wo, weight_bytes(fmt, hidden, attn_width), "ffn_residual_fused_dev attn_output")
+    for w, what in ((wg, "gate"), (wu, "up")):
+        _need(w, weight_bytes(fmt, ffn_rows, hidden), f"ffn_residual_fused_dev {what}")
+    _need(wd, weight_bytes(fmt, hidden, ffn_rows), "ffn_residual_fused_dev down")
+    _need(norm_w, 4 * hidden, "ffn_residual_fused_dev norm_weight")
+    _need(x, 4 * hidden, "ffn_residual_fused_dev x")
+    _need(attn_out, 4 * attn_width, "ffn_residual_fused_dev attn_out")
+    _need(out, 4 * hidden, "ffn_residual_fused_dev out")
+    _need(workspace, workspace_bytes, "ffn_residual_fused_dev workspace")
+    return check(lib().zq_hip_ffn_residual_fused_dev(fmt, _dptr(wo), _dptr(wg), _dptr(wu), _dptr(wd), _dptr(norm_w),
+                                                     _dptr(x), _dptr(attn_out), _dptr(out), hidden, attn_width,
+                                                     ffn_rows, eps, _dptr(workspace), workspace_bytes,
+                                                     _stream(stream)), "zq_hip_ffn_residual_fused_dev")
 
 
 def quantize_acts_dev(X, xq, xs, tokens, cols, stream=None):
