@@ -42,6 +42,7 @@ extern "C" {
 #define ZQ_ERR_NO_DEVICE (-2)  /* no usable gfx950 device / init failed                    */
 #define ZQ_ERR_OOM (-3)        /* device or host allocation failed                         */
 #define ZQ_ERR_HIP (-4)        /* a HIP runtime call or kernel launch failed               */
+#define ZQ_ERR_TOO_LARGE (-5)  /* the call needs more than the fixed no-allocation scratch */
 
 /* ---- weight formats: GGML type ids (src/gguf.cpp:370-393) ---------------- */
 #define ZQ_FMT_Q4_0 2   /* 32 el / 18 B: fp16 d + 16 B nibbles   (src/quant.cpp:253)  */
@@ -217,6 +218,21 @@ int zq_hip_ffn_residual_fused_dev(int fmt, const void* attn_output, const void* 
                                   const float* norm_weight, const float* x, const float* attn_out, float* out,
                                   size_t hidden, size_t attn_width, size_t ffn_rows, float eps, void* workspace,
                                   size_t workspace_bytes, void* stream);
+
+/* zq_hip_gemm_dev without a workspace and without any allocation: the
+ * quantised activations, scales and split-K partials live in a fixed
+ * file-scope device array (zq_hip_noalloc_scratch_bytes(), 64 MiB) that each
+ * GPU holds for the life of the process.  No counterpart in the reference: it
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Calls whose
+ * workspace (zq_hip_gemm_workspace_bytes) exceeds the scratch return
+ * ZQ_ERR_TOO_LARGE before any launch or memory operation.  Every call on a GPU shares
+ * that GPU's scratch: calls that overlap on one GPU (two streams, two
+ * threads) race; calls in one stream are ordered and safe.  Nothing in the
+ * scratch needs to start at zero (each call writes what it reads). */
+size_t zq_hip_noalloc_scratch_bytes(void);
+int zq_hip_gemm_dev_noalloc(int fmt, const void* weights, const float* X, float* Y, size_t tokens, size_t rows,
+                            size_t cols, int act_mode, void* stream);
 
 /* ---- bit-exact tier hooks (device pointers, asynchronous) ---------------- */
 /* Per-32 activation quantiser, kernels/avx2.cpp:502-524: xq[tokens*cols],

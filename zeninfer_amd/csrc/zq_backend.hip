@@ -24,6 +24,14 @@
 #include "../../include/zq_hip.h"
 #include "zq_internal.hpp"
 
+// Fixed device scratch of zq_hip_gemm_dev_noalloc: the int8 activations,
+// their scales and the split-K partial sums of one GEMM, for callers that
+// cannot allocate.  Every GPU the library runs on holds its own copy until
+// the process ends.  Host code never uses the array's name as an address:
+// its device address is looked up per device (scratch_ptr) and passed on.
+constexpr size_t kNoAllocScratchBytes = size_t(64) << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
 namespace {
 
 using Clock = std::chrono::steady_clock;
@@ -62,6 +70,24 @@ struct Backend {
 Backend& B() {
     static Backend b;
     return b;
+}
+
+// Device address of `scratch` on the current device, looked up once per
+// device with that device current (each GPU holds its own copy).
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+void* scratch_ptr() {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return nullptr;
+        g_scratch_ptr[dev] = p;
+    }
+    return g_scratch_ptr[dev];
 }
 
 int fail_hip(Backend& b) {
@@ -115,6 +141,10 @@ int init_locked(Backend& b) {
     const char* tr = std::getenv("ZEN_HIP_TRACE");
     b.trace = tr && tr[0] == '1';
     if (b.trace && (hipEventCreate(&b.ev0) != hipSuccess || hipEventCreate(&b.ev1) != hipSuccess)) b.trace = false;
+    if (!scratch_ptr()) {  // the no-allocation GEMM's scratch on this device
+        b.failed = true;
+        return ZQ_ERR_NO_DEVICE;
+    }
     b.budget = static_cast<size_t>(static_cast<double>(p.totalGlobalMem) * 0.8);
     if (const char* me = std::getenv("ZEN_HIP_MIN_ELEMENTS")) b.min_elements = std::strtoull(me, nullptr, 10);
     b.initialised = true;
@@ -490,6 +520,7 @@ const char* zq_hip_status_string(int status) {
     case ZQ_ERR_NO_DEVICE: return "no usable gfx950 device";
     case ZQ_ERR_OOM: return "out of memory";
     case ZQ_ERR_HIP: return "HIP runtime error";
+    case ZQ_ERR_TOO_LARGE: return "request exceeds the fixed no-allocation scratch (zq_hip_noalloc_scratch_bytes)";
     default: return "unknown status";
     }
 }
@@ -892,6 +923,25 @@ int zq_hip_gemm_dev(int fmt, const void* weights, const float* X, float* Y, size
     uint64_t d = 0;
     return enqueue_gemm(fmt, static_cast<const uint8_t*>(weights), X, Y, tokens, rows, cols, act, workspace,
                         workspace_bytes, static_cast<hipStream_t>(stream), &d);
+}
+
+size_t zq_hip_noalloc_scratch_bytes(void) { return kNoAllocScratchBytes; }
+
+int zq_hip_gemm_dev_noalloc(int fmt, const void* weights, const float* X, float* Y, size_t tokens, size_t rows,
+                            size_t cols, int act_mode, void* stream) {
+    if (!weights || !X || !Y || !tokens || !rows || !valid_fmt(fmt) || !zq::row_bytes(fmt, cols) ||
+        tokens > (1u << 24) || rows > (1u << 24))
+        return ZQ_ERR_ARG;
+    const int act = resolve_act(fmt, act_mode);
+    int st = gemm_supported(fmt, cols, act);
+    if (st != ZQ_OK) return st;
+    const size_t need = zq_hip_gemm_workspace_bytes(fmt, tokens, rows, cols, act);
+    if (need > kNoAllocScratchBytes) return ZQ_ERR_TOO_LARGE;  // before any launch or copy
+    void* ws = scratch_ptr();
+    if (!ws) return ZQ_ERR_HIP;
+    uint64_t d = 0;
+    return enqueue_gemm(fmt, static_cast<const uint8_t*>(weights), X, Y, tokens, rows, cols, act, ws,
+                        kNoAllocScratchBytes, static_cast<hipStream_t>(stream), &d);
 }
 
 size_t zq_hip_gemm_batch_workspace_bytes(int fmt, const zq_gemm_task* tasks, size_t count, size_t tokens, size_t cols,

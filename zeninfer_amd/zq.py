@@ -17,7 +17,7 @@ FORMATS = {"Q4_0": Q4_0, "Q8_0": Q8_0, "Q4_K": Q4_K, "Q5_K": Q5_K, "Q6_K": Q6_K}
 BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210)}
 ACT_DEFAULT, ACT_INT8, ACT_F32 = 0, 1, 2
 OK, DECLINED = 0, 1
-ERR_ARG, ERR_NO_DEVICE, ERR_OOM, ERR_HIP = -1, -2, -3, -4
+ERR_ARG, ERR_NO_DEVICE, ERR_OOM, ERR_HIP, ERR_TOO_LARGE = -1, -2, -3, -4, -5
 WEIGHT_TAIL_PAD = 64
 MAX_BATCH = 8
 
@@ -86,6 +86,8 @@ SIGNATURES = {
     "zq_hip_gemv_batch_dev": (ctypes.c_int, [ctypes.c_int, _P, ctypes.POINTER(GemvTask), _S, _S, _P]),
     "zq_hip_gemm_workspace_bytes": (_S, [ctypes.c_int, _S, _S, _S, ctypes.c_int]),
     "zq_hip_gemm_dev": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _S, _S, _S, ctypes.c_int, _P, _S, _P]),
+    "zq_hip_noalloc_scratch_bytes": (_S, []),
+    "zq_hip_gemm_dev_noalloc": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _S, _S, _S, ctypes.c_int, _P]),
     "zq_hip_quantize_acts_dev": (ctypes.c_int, [_P, _P, _P, _S, _S, _P]),
     "zq_hip_block_dots_dev": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _S, _S, _S, _P]),
     "zq_hip_dequantize_dev": (ctypes.c_int, [ctypes.c_int, _P, _P, _S, _S, _P]),
@@ -416,6 +418,20 @@ def ffn_residual_fused_dev(fmt, wo, wg, wu, wd, norm_w, x, attn_out, out, hidden
                                                      _dptr(x), _dptr(attn_out), _dptr(out), hidden, attn_width,
                                                      ffn_rows, eps, _dptr(workspace), workspace_bytes,
                                                      _stream(stream)), "zq_hip_ffn_residual_fused_dev")
+
+
+def noalloc_scratch_bytes():
+    return lib().zq_hip_noalloc_scratch_bytes()
+
+
+def gemm_dev_noalloc(fmt, w, X, Y, tokens, rows, cols, act=ACT_DEFAULT, stream=None):
+    """zq_hip_gemm_dev with the library's fixed device scratch: no workspace,
+    no allocation (ERR_TOO_LARGE beyond noalloc_scratch_bytes())."""
+    _need(w, weight_bytes(fmt, rows, cols), "gemm_dev_noalloc weights")
+    _need(X, 4 * tokens * cols, "gemm_dev_noalloc X")
+    _need(Y, 4 * tokens * rows, "gemm_dev_noalloc Y")
+    return check(lib().zq_hip_gemm_dev_noalloc(fmt, _dptr(w), _dptr(X), _dptr(Y), tokens, rows, cols, act,
+                                               _stream(stream)), "zq_hip_gemm_dev_noalloc")
 
 
 def quantize_acts_dev(X, xq, xs, tokens, cols, stream=None):
