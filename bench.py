@@ -223,6 +223,66 @@ def cpu_baseline(seconds=10.0, layers=4, workers=None):
                          if r is not None else "scalar C oracle")}
 
 
+def prefill_workers(host):
+    """The reference's prefill worker count: max(policy workers,
+    min(logical CPUs, 32)) (execution_planner.cpp:16-29), the policy being
+    min(logical, physical) CPUs when memory is abundant
+    (resource_governor.cpp:52-56); logical CPUs are the usable ones (the
+    governor reads the cgroup quota, resource_governor.cpp:40-42)."""
+    logical = host["usable_cpus"]
+    policy = max(1, min(logical, host["physical_cores"]))
+    return max(policy, min(logical, 32))
+
+
+def cpu_gemm_baseline(host, reps=3):
+    """The reference's own quant::gemm / quant::gemv (oracle/_ref: AVX2 +
+    ComputePool, its K-blocked fp32 route from tokens*K >= 131072,
+    src/quant.cpp:1188-1192) on this host at the prefill worker count:
+    BASELINE config 2 (Q8_0, M = 32..2048 on both FFN shapes) and config 3
+    (Q4_0 and Q6_K: GEMV and M = 512 GEMM on both shapes).  Median of `reps`
+    runs after one warm-up.  The reference CPU GEMM computes with fp32
+    activations (there is no int8-activation CPU GEMM)."""
+    from oracle import oracle as O
+    r = O.Reference()
+    if not r.has_avx2():
+        raise RuntimeError("no AVX2 on this host")
+    o = O.Oracle()
+    workers = prefill_workers(host)
+    out = {"workers": workers, "policy": "prefill: max(policy, min(logical CPUs, 32)) (execution_planner.cpp:16-29)",
+           "kind": "reference", "config2_q8_0_gemm": {}, "config3": {}}
+
+    def med(fn):
+        fn()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return statistics.median(ts)
+
+    for (N, K) in ((FFN, HIDDEN), (HIDDEN, FFN)):
+        w = o.gen_weights(O.Q8_0, 0x5EED0002, N, K)
+        for M in (32, 128, 512, 2048):
+            X = o.gen_normal(0x5EED0012 + M, M * K)
+            sec = med(lambda: r.gemm(O.Q8_0, w, X, M, N, K, workers))
+            out["config2_q8_0_gemm"][f"M={M} N={N} K={K}"] = {"ms": round(sec * 1e3, 2),
+                                                               "TOPS": round(2.0 * M * N * K / sec / 1e12, 3)}
+        del w
+    for fname, fmt in (("Q4_0", O.Q4_0), ("Q6_K", O.Q6_K)):
+        res = {}
+        for shape, N, K in (("gate/up 14336x4096", FFN, HIDDEN), ("down 4096x14336", HIDDEN, FFN)):
+            w = o.gen_weights(fmt, 0x5EED0003, N, K)
+            x = o.gen_normal(0x5EED0013, K)
+            X = o.gen_normal(0x5EED0014, 512 * K)
+            g = med(lambda: r.gemv(fmt, w, x, N, K, workers))
+            m = med(lambda: r.gemm(fmt, w, X, 512, N, K, workers))
+            res[shape] = {"gemv_ms": round(g * 1e3, 3), "gemv_GB_s": round(gemv_bytes(o.row_bytes(fmt, K), N, K) / g / 1e9, 1),
+                          "gemm_M512_ms": round(m * 1e3, 2), "gemm_M512_TOPS": round(2.0 * 512 * N * K / m / 1e12, 3)}
+            del w
+        out["config3"][fname] = res
+    return out
+
+
 def timed_launches_on(torch, launch, n, skip):
     """Average time per launch of n back-to-back launches (after `skip`
     untimed ones), bracketed by HIP events on the launch stream; a spin
@@ -486,6 +546,18 @@ def main():
                       "TOPS_gemm": round(ops / (k_ms * 1e-3) / 1e12, 1),
                       "frac_int8_peak": round(ops / (k_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4)}
 
+    # ---- the int8 peak from measurement (MFMA rate x CUs x sclk) -----------
+    sclk_mhz, cyc_per_mfma, int8_peak_meas = zq.mfma_peak()
+    # the GEMM's own arithmetic floor: per 32x32 output tile and 32-element K
+    # block (65536 int8 ops) one int8 MFMA (32 cycles), half of a 2-block
+    # scale MFMA (32 cycles) and 16 cvt + 16 fma VALU at 2.2 cycles each
+    # (measured issue rates; MFMA and VALU do not overlap on one SIMD)
+    floor_cycles = 32.0 + 32.0 + 32 * 2.2
+    valu_floor_tops = info["compute_units"] * 4 * 65536.0 / floor_cycles * sclk_mhz * 1e6 / 1e12
+    for g in gemm.values():
+        g["frac_measured_int8_peak"] = round(g["TOPS_per_call"] / int8_peak_meas, 4)
+        g["frac_epilogue_floor"] = round(g["TOPS_per_call"] / valu_floor_tops, 4)
+
     # ---- config 3 formats + config 2 M sweep ----------------------------------
     formats = format_sweep(torch, zq, dev)
     print(f"[bench] formats {json.dumps(formats)}", file=sys.stderr, flush=True)
@@ -493,7 +565,7 @@ def main():
     # ---- config 4: the device-resident decoder, prefill 512 + 128 greedy tokens
     model4 = model_config4()
 
-    cpu = cpu_policy = host = None
+    cpu = cpu_policy = host = cpu_gemm = None
     if not args.no_cpu:
         try:
             cpu = cpu_baseline(seconds=8.0)
@@ -506,6 +578,10 @@ def main():
                           "policy": "decode: min(physical cores, 8) workers (execution_planner.cpp:22-28)"}
         except Exception as e:  # reported, never fatal to the GPU measurement
             cpu = {"error": str(e)}
+        try:
+            cpu_gemm = cpu_gemm_baseline(host or cpu_host())
+        except Exception as e:
+            cpu_gemm = {"error": str(e)}
 
     out = {
         "metric": "Q8_0 decode GEMV GB/s (% HBM peak); prefill GEMM int8 TOPS (% MFMA peak)",
@@ -530,11 +606,19 @@ def main():
                      "avg_launch_us": round(down_ms * 1e3, 2), "algorithmic_bytes_per_launch": down_bytes},
         "per_shape_gemv": per_shape,
         "secondary": {"metric": "prefill GEMM int8 TOPS (% MFMA peak), config 2 at M=2048",
-                      "prefill_gemm_int8_M2048": gemm, "int8_peak_tops": INT8_PEAK_TOPS},
+                      "prefill_gemm_int8_M2048": gemm, "int8_peak_tops": INT8_PEAK_TOPS,
+                      "int8_peak_measured": {"tops": round(int8_peak_meas, 1), "sclk_mhz": round(sclk_mhz, 1),
+                                             "cycles_per_mfma_i32_32x32x32_i8": round(cyc_per_mfma, 2),
+                                             "derivation": "CUs x 4 SIMDs x 65536 ops / cycles per MFMA x measured sclk"},
+                      "roofline_epilogue_floor": {"tops": round(valu_floor_tops, 1),
+                                                  "cycles_per_tile_block": floor_cycles,
+                                                  "derivation": "int8 MFMA 32 + half a 2-block scale MFMA 32 + "
+                                                                "(16 cvt + 16 fma) x 2.2 cycles per 32x32x32 tile-block"}},
         "formats_config3": formats,
         "model_config4": model4,
         "cpu_baseline": cpu,
         "cpu_baseline_reference_policy": cpu_policy,
+        "cpu_baseline_gemm_and_config3": cpu_gemm,
         "cpu_host": host,
     }
     print(json.dumps(out))

@@ -304,6 +304,14 @@ int zq_hip_block_dots_dev(int fmt, const void* weights, const int8_t* xq, int32_
 /* Dequantised weights, row-major fp32 (src/quant.cpp:391-416, 500-517). */
 int zq_hip_dequantize_dev(int fmt, const void* weights, float* out, size_t rows, size_t cols, void* stream);
 
+/* ---- measurement helper --------------------------------------------------- */
+/* The int8 MFMA peak of this device from measurement: every CU runs
+ * v_mfma_i32_32x32x32_i8 back to back on all four SIMDs; sclk is the shader
+ * clock measured against the 100 MHz constant clock during that run, and
+ * int8_tops = CUs x 4 SIMDs x 65536 ops / cycles_per_mfma x sclk.  No
+ * counterpart in the reference (roofline reporting). */
+int zq_hip_mfma_peak(double* sclk_mhz, double* cycles_per_mfma, double* int8_tops);
+
 /* ---- synthetic inputs on the device (bench workloads) -------------------- */
 int zq_hip_synth_weights_dev(int fmt, uint64_t seed, void* weights, size_t rows, size_t cols, void* stream);
 int zq_hip_synth_normal_dev(uint64_t seed, float* out, size_t n, void* stream);

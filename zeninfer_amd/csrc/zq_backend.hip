@@ -1026,6 +1026,37 @@ int zq_hip_dequantize_dev(int fmt, const void* weights, float* out, size_t rows,
                : ZQ_ERR_HIP;
 }
 
+int zq_hip_mfma_peak(double* sclk_mhz, double* cycles_per_mfma, double* int8_tops) {
+    if (!sclk_mhz || !cycles_per_mfma || !int8_tops) return ZQ_ERR_ARG;
+    Backend& b = B();
+    std::lock_guard<std::mutex> lock(b.mu);
+    int st = init_locked(b);
+    if (st != ZQ_OK) return st;
+    const uint32_t wgs = uint32_t(b.info.compute_units), iters = 20000;
+    uint64_t* d = nullptr;
+    if (hipMalloc(&d, size_t(wgs) * 4 * sizeof(uint64_t)) != hipSuccess) return ZQ_ERR_OOM;
+    std::vector<uint64_t> h(size_t(wgs) * 4);
+    const bool ok = zq::launch_mfma_probe(d, wgs, iters / 10, b.stream) == hipSuccess &&  // warm-up (clock ramp)
+                    zq::launch_mfma_probe(d, wgs, iters, b.stream) == hipSuccess &&
+                    hipStreamSynchronize(b.stream) == hipSuccess &&
+                    hipMemcpy(h.data(), d, h.size() * sizeof(uint64_t), hipMemcpyDeviceToHost) == hipSuccess;
+    (void)hipFree(d);
+    if (!ok) return fail_hip(b);
+    double cyc = 0.0, ticks = 0.0;
+    for (uint32_t i = 0; i < wgs; ++i) {
+        cyc += double(h[4 * i]);
+        ticks += double(h[4 * i + 1]);
+    }
+    cyc /= wgs;
+    ticks /= wgs;
+    if (ticks <= 0.0 || cyc <= 0.0) return ZQ_ERR_HIP;
+    *sclk_mhz = cyc / ticks * 100.0;  // s_memrealtime counts at 100 MHz
+    *cycles_per_mfma = cyc / (4.0 * iters);
+    // 32x32x32 MACs = 65536 ops per MFMA, one MFMA pipe per SIMD, 4 SIMDs per CU
+    *int8_tops = double(wgs) * 4.0 * 65536.0 / *cycles_per_mfma * (*sclk_mhz * 1e6) / 1e12;
+    return ZQ_OK;
+}
+
 int zq_hip_synth_weights_dev(int fmt, uint64_t seed, void* weights, size_t rows, size_t cols, void* stream) {
     if (!weights || !rows || !valid_fmt(fmt) || !zq::row_bytes(fmt, cols)) return ZQ_ERR_ARG;
     return zq::launch_synth_weights(fmt, seed, static_cast<uint8_t*>(weights), rows, cols,

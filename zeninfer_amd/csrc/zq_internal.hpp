@@ -116,6 +116,10 @@ hipError_t launch_dequantize(int fmt, const uint8_t* w, float* out, size_t rows,
 hipError_t launch_block_dots(int fmt, const uint8_t* w, const int8_t* xq, int32_t* out,
                              size_t M, size_t N, size_t K, hipStream_t stream);
 
+// Int8 MFMA rate probe (one 4-wave workgroup per CU): out[4*wg] shader
+// cycles and out[4*wg+1] 100 MHz ticks of iters x 4 MFMAs per wave.
+hipError_t launch_mfma_probe(uint64_t* out, uint32_t wgs, uint32_t iters, hipStream_t stream);
+
 // Synthetic inputs generated on the device (bench workloads).
 hipError_t launch_synth_weights(int fmt, uint64_t seed, uint8_t* w, size_t rows, size_t cols,
                                 hipStream_t stream);

@@ -118,6 +118,44 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const float* __restr
 
 }  // namespace
 
+namespace {
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+typedef int v16i_t __attribute__((ext_vector_type(16)));
+// Int8 MFMA rate probe: every wave of every CU issues `iters` x 4
+// independent v_mfma_i32_32x32x32_i8; wave 0 of each workgroup records the
+// shader-clock counter (s_memtime) and the 100 MHz constant clock
+// (s_memrealtime) around the loop.  out[4*wg] = shader cycles, [4*wg+1] =
+// 100 MHz ticks, [4*wg+2] = a sink of the results (so the loop is kept).
+__global__ __launch_bounds__(256) void mfma_probe_kernel(uint64_t* out, uint32_t iters, int seed) {
+    v4i_t a = {seed, seed + 1, seed + 2, int(threadIdx.x)};
+    v16i_t c[4] = {};
+    __syncthreads();
+    const uint64_t t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+    for (uint32_t it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) c[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, a, c[j], 0, 0, 0);
+    }
+    int sink = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) sink ^= c[j][v];
+    __syncthreads();
+    const uint64_t t1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+    if (threadIdx.x == 0) {
+        out[4 * blockIdx.x] = t1 - t0;
+        out[4 * blockIdx.x + 1] = r1 - r0;
+    }
+    if (sink == 0x7FFFFFFF) out[4 * blockIdx.x + 2] = uint64_t(sink);
+}
+}  // namespace
+
+hipError_t launch_mfma_probe(uint64_t* out, uint32_t wgs, uint32_t iters, hipStream_t stream) {
+    if (!out || !wgs || !iters) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(mfma_probe_kernel, dim3(wgs), dim3(256), 0, stream, out, iters, 3);
+    return hipGetLastError();
+}
+
 hipError_t launch_silu_mul(const float* gate, const float* up, float* out, size_t n, hipStream_t stream) {
     if (!gate || !up || !out || !n) return hipErrorInvalidValue;
     const dim3 grid(static_cast<uint32_t>((n + kThreads - 1) / kThreads));

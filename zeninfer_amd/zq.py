@@ -107,6 +107,7 @@ SIGNATURES = {
     "zq_hip_quantize_acts_dev": (ctypes.c_int, [_P, _P, _P, _S, _S, _P]),
     "zq_hip_block_dots_dev": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _S, _S, _S, _P]),
     "zq_hip_dequantize_dev": (ctypes.c_int, [ctypes.c_int, _P, _P, _S, _S, _P]),
+    "zq_hip_mfma_peak": (ctypes.c_int, [ctypes.POINTER(ctypes.c_double)] * 3),
     "zq_hip_synth_weights_dev": (ctypes.c_int, [ctypes.c_int, ctypes.c_uint64, _P, _S, _S, _P]),
     "zq_hip_synth_normal_dev": (ctypes.c_int, [ctypes.c_uint64, _P, _S, _P]),
 }
@@ -524,6 +525,13 @@ def dequantize_dev(fmt, w, out, rows, cols, stream=None):
     _need(out, 4 * rows * cols, "dequantize_dev out")
     return check(lib().zq_hip_dequantize_dev(fmt, _dptr(w), _dptr(out), rows, cols, _stream(stream)),
                  "zq_hip_dequantize_dev")
+
+
+def mfma_peak():
+    """(sclk MHz, cycles per int8 MFMA, int8 TOPS peak) measured on the device."""
+    a, b, c = ctypes.c_double(), ctypes.c_double(), ctypes.c_double()
+    check(lib().zq_hip_mfma_peak(ctypes.byref(a), ctypes.byref(b), ctypes.byref(c)), "zq_hip_mfma_peak")
+    return a.value, b.value, c.value
 
 
 def synth_weights_dev(fmt, seed, w, rows, cols, stream=None):
