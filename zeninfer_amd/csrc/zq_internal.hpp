@@ -140,8 +140,10 @@ hipError_t launch_rope_kv(float* q, const float* k, const float* v, float* kc, f
 hipError_t launch_attention(const float* q, const float* kc, const float* vc, float* out, const uint32_t* pos0,
                             uint32_t T, uint32_t H, uint32_t KH, uint32_t D, uint32_t max_pos, float scale,
                             hipStream_t stream);
-// Decode attention split over 32-position chunks (+ combine); `part` holds
-// attention_decode_partial_floats(H, D, max_pos) floats.
+// Decode attention split over 32-position chunks, the last chunk of each kv
+// head merging; `part` holds attention_decode_partial_floats(H, D, max_pos)
+// floats and must be zero when first used (its tail holds arrival counters
+// that the kernel leaves at zero).
 size_t attention_decode_partial_floats(uint32_t H, uint32_t D, uint32_t max_pos);
 // RoPE (adjacent pairs) of q and the new key, the KV append at *pos and the
 // attention of the one query token, fused.

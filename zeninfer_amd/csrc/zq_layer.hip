@@ -350,35 +350,88 @@ __global__ __launch_bounds__(kT) void attention_prefill_kernel(const float* __re
 // and value to the caches and uses them from LDS.  All global loads of a
 // workgroup are issued up front, so its cost is about one memory latency.
 // Per query head it writes the chunk's max score m, l = sum exp(score - m)
-// and acc[d] = sum exp(score - m) * v[d]; attention_combine_kernel merges the
-// chunks, out = sum_s exp(m_s - M) acc_s / sum_s exp(m_s - M) l_s, equal to
-// the single-pass softmax of the reference up to rounding.
+// and acc[d] = sum exp(score - m) * v[d].  The last chunk workgroup of a kv
+// head to finish (an agent-scope arrival counter per kv head) merges the
+// chunks of its G heads, out = sum_s exp(m_s - M) acc_s / sum_s exp(m_s - M)
+// l_s, equal to the single-pass softmax of the reference up to rounding.
+// Partials are written with agent-scope stores and read back with
+// agent-scope loads (coherent across XCDs without cache write-back or
+// invalidation); a chunk workgroup waits for its own partial stores
+// (s_waitcnt) before it arrives.  The merging workgroup resets the counter,
+// so the kernel needs no clearing between steps (HIP-graph replays).
 constexpr int kAttnChunk = 32;
 constexpr int kAttnMaxG = 8;
+constexpr int kAttnMaxSplits = 1024;  // positions <= 32768
 
+__device__ __forceinline__ void coherent_store_f(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// A float written by another workgroup in this launch: a load with the
+// device-scope cache policy (SC1), so it comes from the device-coherent level
+// and not from a stale line of this XCD's L2.  Not an atomic, so the compiler
+// may issue many of them before waiting.
+__device__ __forceinline__ float coherent_load_f(const float* base, uint32_t n, uint32_t i) {
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, int(n * 4), 0x00020000);
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, i * 4, 0, 0x10));
+}
+
+// out[g][d] of the G query heads of one kv head from their ns chunk partials
+// (part: [g][splits][D + 2]), by one workgroup: per head, wave g's lanes
+// stride over the chunks for the max M and L = sum l_s exp(m_s - M) (in
+// double), then out = sum_s acc_s[d] exp(m_s - M) / L with the chunks summed
+// in order.
 template <int D>
+__device__ void merge_chunks(const float* part, float* out, uint32_t G, uint32_t ns, uint32_t splits) {
+    __shared__ float wgt[kAttnMaxG][kAttnMaxSplits];
+    __shared__ float inv_l[kAttnMaxG];
+    const int wv = threadIdx.x >> 6, ln = threadIdx.x & 63;
+    const uint32_t n = G * splits * (D + 2);
+    for (uint32_t g = wv; g < G; g += kT / 64) {
+        const uint32_t base = g * splits * (D + 2);
+        float M = -INFINITY;
+        for (uint32_t s = ln; s < ns; s += 64) M = fmaxf(M, coherent_load_f(part, n, base + s * (D + 2) + D));
+        M = wave_max(M);
+        double L = 0.0;
+        for (uint32_t s = ln; s < ns; s += 64) {
+            const float w = expf(coherent_load_f(part, n, base + s * (D + 2) + D) - M);
+            wgt[g][s] = w;
+            L += double(coherent_load_f(part, n, base + s * (D + 2) + D + 1)) * double(w);
+        }
+        L = wave_sum(L);
+        if (ln == 0) inv_l[g] = 1.0f / float(L);
+    }
+    __syncthreads();
+    for (uint32_t e = threadIdx.x; e < G * D; e += kT) {
+        const uint32_t g = e / D, d = e % D, base = g * splits * (D + 2) + d;
+        float acc = 0.0f;
+#pragma unroll 8
+        for (uint32_t s = 0; s < ns; ++s) acc = fmaf(coherent_load_f(part, n, base + s * (D + 2)), wgt[g][s], acc);
+        out[size_t(g) * D + d] = acc * inv_l[g];
+    }
+}
+
+template <int D, int G>
 __global__ __launch_bounds__(kT) void attention_decode_kernel(
     const float* __restrict__ q, const float* __restrict__ knew, const float* __restrict__ vnew, float* __restrict__ kc,
     float* __restrict__ vc, const float* __restrict__ cos_tab, const float* __restrict__ sin_tab,
-    float* __restrict__ part, const uint32_t* __restrict__ pos_ptr, uint32_t H, uint32_t KH, uint32_t pairs,
-    float scale, uint32_t splits) {
+    float* __restrict__ part, float* __restrict__ out, const uint32_t* __restrict__ pos_ptr, uint32_t H, uint32_t KH,
+    uint32_t pairs, float scale, uint32_t splits) {
     constexpr int C = kAttnChunk;
     constexpr int LPP = kT / C;       // lanes per position in the score phase (8)
     constexpr int DPL = D / LPP;      // key elements per lane (16 for D = 128)
     constexpr int HALVES = kT / D;    // position groups in the value phase
     constexpr int VPT = C / HALVES;   // value rows per thread
-    constexpr int QPT = kAttnMaxG * D / kT;
-    __shared__ float qs[kAttnMaxG][D];
+    constexpr int QPT = (G * D + kT - 1) / kT;
+    __shared__ float qs[G][D];
     __shared__ float kn[D], vn[D];
-    __shared__ float sc[kAttnMaxG][C];
-    __shared__ float red[kAttnMaxG][kT];
+    __shared__ __align__(16) float sc[C][G];  // position-major: the G weights of a position are adjacent
+    __shared__ float red[G][kT];
     const uint32_t kh = blockIdx.x, s = blockIdx.y;
     const uint32_t pos = *pos_ptr;
     const uint32_t p0 = s * C;
     if (p0 > pos) return;  // chunk past the current position: nothing to contribute
     const uint32_t n = min(uint32_t(C), pos + 1 - p0);
     const bool owns_new = pos < p0 + C;
-    const uint32_t G = H / KH;
     const uint32_t KW = KH * D;
     const int tid = threadIdx.x;
 
@@ -414,6 +467,17 @@ __global__ __launch_bounds__(kT) void attention_decode_kernel(
     }
     const float* cs = cos_tab + size_t(pos) * pairs;
     const float* sn = sin_tab + size_t(pos) * pairs;
+    // the rotation factors come in with the other loads, not after them
+    constexpr int QP = (G * D / 2 + kT - 1) / kT;  // q pairs per thread
+    float cq[QP], sq[QP];
+#pragma unroll
+    for (int k = 0; k < QP; ++k) {
+        const uint32_t j = tid + k * kT, i = j % (pairs ? pairs : 1u);
+        cq[k] = j < G * pairs ? cs[i] : 0.0f;
+        sq[k] = j < G * pairs ? sn[i] : 0.0f;
+    }
+    const float ck = owns_new && uint32_t(tid) < pairs ? cs[tid] : 0.0f;
+    const float sk = owns_new && uint32_t(tid) < pairs ? sn[tid] : 0.0f;
 
     // ---- RoPE (adjacent pairs) on q and the new key, in LDS ----
 #pragma unroll
@@ -423,14 +487,18 @@ __global__ __launch_bounds__(kT) void attention_decode_kernel(
     }
     if (owns_new && tid < D) { kn[tid] = knr; vn[tid] = vnr; }
     __syncthreads();
-    for (uint32_t j = tid; j < G * pairs; j += kT) {
-        const uint32_t g = j / pairs, i = j - g * pairs;
-        const float a = qs[g][2 * i], b = qs[g][2 * i + 1], c = cs[i], sv = sn[i];
-        qs[g][2 * i] = a * c - b * sv;
-        qs[g][2 * i + 1] = a * sv + b * c;
+#pragma unroll
+    for (int k = 0; k < QP; ++k) {
+        const uint32_t j = tid + k * kT;
+        if (j < G * pairs) {
+            const uint32_t g = j / pairs, i = j - g * pairs;
+            const float a = qs[g][2 * i], b = qs[g][2 * i + 1], c = cq[k], sv = sq[k];
+            qs[g][2 * i] = a * c - b * sv;
+            qs[g][2 * i + 1] = a * sv + b * c;
+        }
     }
-    if (owns_new && tid < pairs) {
-        const float a = kn[2 * tid], b = kn[2 * tid + 1], c = cs[tid], sv = sn[tid];
+    if (owns_new && uint32_t(tid) < pairs) {
+        const float a = kn[2 * tid], b = kn[2 * tid + 1], c = ck, sv = sk;
         kn[2 * tid] = a * c - b * sv;
         kn[2 * tid + 1] = a * sv + b * c;
     }
@@ -444,93 +512,85 @@ __global__ __launch_bounds__(kT) void attention_decode_kernel(
 #pragma unroll
         for (int i = 0; i < DPL; ++i) kv[i] = kn[sj * DPL + i];
     }
-    for (uint32_t g = 0; g < G; ++g) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
         float d = 0.0f;
 #pragma unroll
         for (int i = 0; i < DPL; ++i) d = fmaf(qs[g][sj * DPL + i], kv[i], d);
         d = group_sum<LPP>(d);
-        if (sj == 0 && sp < n) sc[g][sp] = d * scale;
+        if (sj == 0 && sp < n) sc[sp][g] = d * scale;
     }
     __syncthreads();
     // ---- chunk softmax: one wave per head, one lane per position ----
     float* outp = part + size_t(kh * G) * splits * (D + 2);
     {
         const int wv = tid >> 6, ln = tid & 63;
-        for (uint32_t g = wv; g < G; g += kT / 64) {
-            const float sv = uint32_t(ln) < n ? sc[g][ln] : -INFINITY;
+        for (int g = wv; g < G; g += kT / 64) {
+            const float sv = uint32_t(ln) < n ? sc[ln][g] : -INFINITY;
             const float m = wave_max(sv);
             const float e = uint32_t(ln) < n ? expf(sv - m) : 0.0f;
-            if (uint32_t(ln) < n) sc[g][ln] = e;
+            if (ln < C) sc[ln][g] = e;  // zero past the chunk's last position
             const float l = wave_sum(e);
             if (ln == 0) {
                 float* o = outp + (size_t(g) * splits + s) * (D + 2);
-                o[D] = m;
-                o[D + 1] = l;
+                coherent_store_f(o + D, m);
+                coherent_store_f(o + D + 1, l);
             }
         }
     }
     __syncthreads();
-    // ---- acc[g][d] = sum_p e[g][p] * v[p][d] ----
-    float acc[kAttnMaxG];
+    // ---- acc[g][d] = sum_p e[g][p] * v[p][d]; past the last position e = 0
+    // and v is selected to 0 (the row read there may be an unwritten one) ----
+    float acc[G];
 #pragma unroll
-    for (int g = 0; g < kAttnMaxG; ++g) acc[g] = 0.0f;
+    for (int g = 0; g < G; ++g) acc[g] = 0.0f;
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
         const uint32_t p = vh + i * HALVES;
-        if (p < n) {
-            const float v = p0 + p == pos ? vn[vd] : vv[i];
+        const float v = p0 + p == pos ? vn[vd] : (p < n ? vv[i] : 0.0f);
+        float e[G];
+        if constexpr (G % 4 == 0) {
 #pragma unroll
-            for (int g = 0; g < kAttnMaxG; ++g)
-                if (g < int(G)) acc[g] = fmaf(sc[g][p], v, acc[g]);
+            for (int g4 = 0; g4 < G; g4 += 4) {
+                const float4 w = *reinterpret_cast<const float4*>(&sc[p][g4]);
+                e[g4] = w.x; e[g4 + 1] = w.y; e[g4 + 2] = w.z; e[g4 + 3] = w.w;
+            }
+        } else {
+#pragma unroll
+            for (int g = 0; g < G; ++g) e[g] = sc[p][g];
         }
+#pragma unroll
+        for (int g = 0; g < G; ++g) acc[g] = fmaf(e[g], v, acc[g]);
     }
     if (HALVES > 1) {
-        for (uint32_t g = 0; g < G; ++g) red[g][tid] = acc[g];
+#pragma unroll
+        for (int g = 0; g < G; ++g) red[g][tid] = acc[g];
         __syncthreads();
         if (vh == 0)
-            for (uint32_t g = 0; g < G; ++g) {
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
                 float t = 0.0f;
                 for (int k = 0; k < HALVES; ++k) t += red[g][vd + k * D];
-                outp[(size_t(g) * splits + s) * (D + 2) + vd] = t;
+                coherent_store_f(outp + (size_t(g) * splits + s) * (D + 2) + vd, t);
             }
     } else {
-        for (uint32_t g = 0; g < G; ++g) outp[(size_t(g) * splits + s) * (D + 2) + vd] = acc[g];
+#pragma unroll
+        for (int g = 0; g < G; ++g) coherent_store_f(outp + (size_t(g) * splits + s) * (D + 2) + vd, acc[g]);
     }
-}
-
-// out[h][d] from the chunk partials of head h: one workgroup per head, all
-// partials read into LDS in one pass.
-__global__ __launch_bounds__(kT) void attention_combine_kernel(const float* __restrict__ part, float* __restrict__ out,
-                                                               const uint32_t* __restrict__ pos_ptr, uint32_t D,
-                                                               uint32_t splits) {
-    extern __shared__ float ps[];  // ns * (D + 2)
-    __shared__ float wgt[1024];
-    __shared__ float inv_l;
-    const uint32_t h = blockIdx.x;
-    const uint32_t ns = *pos_ptr / kAttnChunk + 1;
-    const float* ph = part + size_t(h) * splits * (D + 2);
-    for (uint32_t i = threadIdx.x; i < ns * (D + 2); i += kT) ps[i] = ph[i];
+    // ---- arrival; the last chunk of this kv head merges ----
+    __shared__ uint32_t last;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // this thread's partial stores completed
     __syncthreads();
-    if (threadIdx.x < 64) {  // wave 0: lanes stride over the chunks
-        const uint32_t ln = threadIdx.x;
-        float M = -INFINITY;
-        for (uint32_t s = ln; s < ns; s += 64) M = fmaxf(M, ps[s * (D + 2) + D]);
-        M = wave_max(M);
-        double L = 0.0;
-        for (uint32_t s = ln; s < ns; s += 64) {
-            const float w = expf(ps[s * (D + 2) + D] - M);
-            wgt[s] = w;
-            L += double(ps[s * (D + 2) + D + 1]) * double(w);
-        }
-        L = wave_sum(L);
-        if (ln == 0) inv_l = 1.0f / float(L);
+    const uint32_t ns = pos / C + 1;
+    uint32_t* cnt = reinterpret_cast<uint32_t*>(part + size_t(H) * splits * (D + 2)) + kh;
+    if (tid == 0) {
+        const uint32_t old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = old + 1 == ns ? 1u : 0u;
+        if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // all ns have arrived
     }
     __syncthreads();
-    for (uint32_t d = threadIdx.x; d < D; d += kT) {
-        float acc = 0.0f;
-        for (uint32_t s = 0; s < ns; ++s) acc = fmaf(ps[s * (D + 2) + d], wgt[s], acc);
-        out[size_t(h) * D + d] = acc * inv_l;
-    }
+    if (!last) return;
+    merge_chunks<D>(outp, out + size_t(kh * G) * D, G, ns, splits);
 }
 
 // out = x + y (out may be x)
@@ -657,7 +717,7 @@ hipError_t launch_attention(const float* q, const float* kc, const float* vc, fl
 
 size_t attention_decode_partial_floats(uint32_t H, uint32_t D, uint32_t max_pos) {
     const uint32_t splits = (max_pos + kAttnChunk - 1) / kAttnChunk;
-    return size_t(H) * splits * (D + 2);
+    return size_t(H) * splits * (D + 2) + H;  // + one arrival counter per kv head (<= H), zero at rest
 }
 
 hipError_t launch_attention_decode(const float* q, const float* knew, const float* vnew, float* kc, float* vc,
@@ -668,23 +728,28 @@ hipError_t launch_attention_decode(const float* q, const float* knew, const floa
         H / KH > uint32_t(kAttnMaxG) || !max_pos || !pairs || pairs > D / 2)
         return hipErrorInvalidValue;
     const uint32_t splits = (max_pos + kAttnChunk - 1) / kAttnChunk;
-    if (splits > 1024 || size_t(splits) * (D + 2) * 4 > 64 * 1024) return hipErrorInvalidValue;
+    if (splits > uint32_t(kAttnMaxSplits)) return hipErrorInvalidValue;
     const dim3 grid(KH, splits);
-#define ZQ_ATTN(DD)                                                                                                   \
-    hipLaunchKernelGGL(attention_decode_kernel<DD>, grid, dim3(kT), 0, stream, q, knew, vnew, kc, vc, cos_tab, sin_tab, \
-                       part, pos, H, KH, pairs, scale, splits)
+    const uint32_t G = H / KH;
+#define ZQ_ATTN(DD, GG)                                                                                                \
+    hipLaunchKernelGGL((attention_decode_kernel<DD, GG>), grid, dim3(kT), 0, stream, q, knew, vnew, kc, vc, cos_tab,  \
+                       sin_tab, part, out, pos, H, KH, pairs, scale, splits)
+#define ZQ_ATTN_G(DD)                      \
+    switch (G) {                           \
+    case 1: ZQ_ATTN(DD, 1); break;         \
+    case 2: ZQ_ATTN(DD, 2); break;         \
+    case 4: ZQ_ATTN(DD, 4); break;         \
+    case 8: ZQ_ATTN(DD, 8); break;         \
+    default: return hipErrorInvalidValue;  \
+    }
     switch (D) {
-    case 64: ZQ_ATTN(64); break;
-    case 128: ZQ_ATTN(128); break;
-    case 256: ZQ_ATTN(256); break;
+    case 64: ZQ_ATTN_G(64); break;
+    case 128: ZQ_ATTN_G(128); break;
+    case 256: ZQ_ATTN_G(256); break;
     default: return hipErrorInvalidValue;
     }
+#undef ZQ_ATTN_G
 #undef ZQ_ATTN
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    // the partials of the chunks up to the current position go through LDS
-    hipLaunchKernelGGL(attention_combine_kernel, dim3(H), dim3(kT), size_t(splits) * (D + 2) * 4, stream, part, out,
-                       pos, D, splits);
     return hipGetLastError();
 }
 

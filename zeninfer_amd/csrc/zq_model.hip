@@ -166,6 +166,7 @@ bool alloc_runtime(zq_model& m, std::string& e) {
     m.xs = reinterpret_cast<float*>(p); p += xs_bytes;
     m.partial = partial ? reinterpret_cast<float*>(p) : nullptr; p += align_up(partial, kAlign);
     m.attn_part = reinterpret_cast<float*>(p); p += attn_bytes;
+    if (hipMemset(m.attn_part, 0, attn_bytes) != hipSuccess) { e = "device memset failed (attention counters)"; return false; }
     m.argmax_part = p; p += arg_bytes;
     m.pos_dev = reinterpret_cast<uint32_t*>(p); p += kAlign;
     m.next_dev = reinterpret_cast<uint32_t*>(p); p += kAlign;
