@@ -509,6 +509,13 @@ def main():
     down_ms = timed_launches(lambda i: zq.gemv_dev(Q8, layers[i % LAYERS]["down"], x_f, y_d, HIDDEN, FFN),
                              4 * LAYERS, LAYERS)
     down_gbs = down_bytes / (down_ms * 1e-3) / 1e9
+    # the practical ceiling of one launch that reads the same weight bytes: a
+    # plain non-temporal streaming read (no compute) of each down matrix,
+    # timed the same way (zq_hip_read_probe_dev)
+    sink = torch.empty(zq.read_probe_sink_bytes(), dtype=torch.uint8, device=dev)
+    wbytes = HIDDEN * rbf
+    read_ms = timed_launches(lambda i: zq.read_probe_dev(layers[i % LAYERS]["down"], wbytes, sink), 4 * LAYERS, LAYERS)
+    read_gbs = wbytes / (read_ms * 1e-3) / 1e9
 
     # per-shape GB/s (informational), same method
     per_shape = {}
@@ -603,7 +610,12 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(down_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(down_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "kernel": "gemv_stream_kernel<Q8_0> (4 column slices x 16 waves) at 4096x14336, the down projection",
-                     "avg_launch_us": round(down_ms * 1e3, 2), "algorithmic_bytes_per_launch": down_bytes},
+                     "avg_launch_us": round(down_ms * 1e3, 2), "algorithmic_bytes_per_launch": down_bytes,
+                     "read_ceiling": {"us": round(read_ms * 1e3, 2), "GB/s": round(read_gbs, 1),
+                                      "frac": round(read_gbs / HBM_PEAK_GBS, 4),
+                                      "what": "plain streaming read of the same weight bytes, one launch each, "
+                                              "same timing (zq_hip_read_probe_dev)"},
+                     "frac_of_read_ceiling": round(down_gbs / read_gbs, 4)},
         "per_shape_gemv": per_shape,
         "secondary": {"metric": "prefill GEMM int8 TOPS (% MFMA peak), config 2 at M=2048",
                       "prefill_gemm_int8_M2048": gemm, "int8_peak_tops": INT8_PEAK_TOPS,

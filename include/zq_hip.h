@@ -311,6 +311,15 @@ int zq_hip_dequantize_dev(int fmt, const void* weights, float* out, size_t rows,
  * int8_tops = CUs x 4 SIMDs x 65536 ops / cycles_per_mfma x sclk.  No
  * counterpart in the reference (roofline reporting). */
 int zq_hip_mfma_peak(double* sclk_mhz, double* cycles_per_mfma, double* int8_tops);
+/* The streaming-read yardstick of the GEMV rooflines: enqueues one kernel
+ * that reads `bytes` of device memory at `buf` (16 B aligned, a multiple of
+ * 16) once, with the GEMVs' non-temporal 16-byte loads and nothing else, on
+ * `stream`.  `sink` is device memory of zq_hip_read_probe_sink_bytes()
+ * bytes.  Timed by the caller (events around back-to-back launches), it is
+ * the practical ceiling of one launch that must read those bytes.  No
+ * counterpart in the reference (roofline reporting). */
+int zq_hip_read_probe_dev(const void* buf, size_t bytes, void* sink, void* stream);
+size_t zq_hip_read_probe_sink_bytes(void);
 
 /* ---- synthetic inputs on the device (bench workloads) -------------------- */
 int zq_hip_synth_weights_dev(int fmt, uint64_t seed, void* weights, size_t rows, size_t cols, void* stream);

@@ -153,3 +153,17 @@ def test_stats_fallbacks_and_timers(zq, orc):
         zq.gemm(O.Q6_K, w6, orc.gen_normal(753, 2 * 256), 2, 8, 256, zq.ACT_INT8)
     assert zq.stats()["fallbacks"] == 1
     zq.release_all()
+
+
+# ------------------------------------------------------- measurement probe ---
+def test_read_probe(zq):
+    """The streaming-read yardstick runs on a device buffer, stores nothing
+    for real data, and refuses sizes its 16-byte loads cannot cover."""
+    buf = torch.ones(1 << 22, dtype=torch.uint8, device=DEV)
+    sink = torch.zeros(zq.read_probe_sink_bytes(), dtype=torch.uint8, device=DEV)
+    zq.read_probe_dev(buf, buf.numel(), sink)
+    torch.cuda.synchronize()
+    assert int(sink.sum()) == 0
+    with pytest.raises(zq.ZQError) as e:
+        zq.read_probe_dev(buf, 1000, sink)  # not a multiple of 16
+    assert e.value.status == zq.ERR_ARG

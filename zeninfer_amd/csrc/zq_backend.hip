@@ -1026,6 +1026,15 @@ int zq_hip_dequantize_dev(int fmt, const void* weights, float* out, size_t rows,
                : ZQ_ERR_HIP;
 }
 
+int zq_hip_read_probe_dev(const void* buf, size_t bytes, void* sink, void* stream) {
+    if (!buf || !sink || !bytes || bytes % 16 || (reinterpret_cast<uintptr_t>(buf) & 15u)) return ZQ_ERR_ARG;
+    return zq::launch_read_probe(buf, bytes, static_cast<uint32_t*>(sink), static_cast<hipStream_t>(stream)) ==
+                   hipSuccess
+               ? ZQ_OK
+               : ZQ_ERR_HIP;
+}
+size_t zq_hip_read_probe_sink_bytes(void) { return zq::read_probe_sink_bytes(); }
+
 int zq_hip_mfma_peak(double* sclk_mhz, double* cycles_per_mfma, double* int8_tops) {
     if (!sclk_mhz || !cycles_per_mfma || !int8_tops) return ZQ_ERR_ARG;
     Backend& b = B();

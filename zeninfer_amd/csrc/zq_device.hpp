@@ -207,4 +207,20 @@ __device__ __forceinline__ float wave_max(float v) {
     return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
 }
 
+// Cross-workgroup hand-off inside one launch (workgroups run on 8 XCDs with
+// private L2s): the producer writes with agent-scope stores (through to the
+// device-coherent level) and waits for them (s_waitcnt) before it signals;
+// the consumer reads with the device-scope cache policy (SC1), from the
+// device-coherent level and not from a stale line of its own L2.  No L2
+// write-back or invalidate is needed.
+__device__ __forceinline__ void coherent_store_f(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Element i of the n floats at `base`, written by another workgroup of this
+// launch.  Not an atomic, so the compiler may issue many before waiting.
+__device__ __forceinline__ float coherent_load_f(const float* base, uint32_t n, uint32_t i) {
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, int(n * 4), 0x00020000);
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, i * 4, 0, 0x10));
+}
+
 }  // namespace zq

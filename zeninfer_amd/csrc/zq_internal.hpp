@@ -119,6 +119,10 @@ hipError_t launch_block_dots(int fmt, const uint8_t* w, const int8_t* xq, int32_
 // Int8 MFMA rate probe (one 4-wave workgroup per CU): out[4*wg] shader
 // cycles and out[4*wg+1] 100 MHz ticks of iters x 4 MFMAs per wave.
 hipError_t launch_mfma_probe(uint64_t* out, uint32_t wgs, uint32_t iters, hipStream_t stream);
+// Streaming read of `bytes` (16 B aligned, multiple of 16); `sink` holds
+// read_probe_sink_bytes().
+hipError_t launch_read_probe(const void* buf, size_t bytes, uint32_t* sink, hipStream_t stream);
+size_t read_probe_sink_bytes();
 
 // Synthetic inputs generated on the device (bench workloads).
 hipError_t launch_synth_weights(int fmt, uint64_t seed, uint8_t* w, size_t rows, size_t cols,

@@ -363,17 +363,6 @@ constexpr int kAttnChunk = 32;
 constexpr int kAttnMaxG = 8;
 constexpr int kAttnMaxSplits = 1024;  // positions <= 32768
 
-__device__ __forceinline__ void coherent_store_f(float* p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// A float written by another workgroup in this launch: a load with the
-// device-scope cache policy (SC1), so it comes from the device-coherent level
-// and not from a stale line of this XCD's L2.  Not an atomic, so the compiler
-// may issue many of them before waiting.
-__device__ __forceinline__ float coherent_load_f(const float* base, uint32_t n, uint32_t i) {
-    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, int(n * 4), 0x00020000);
-    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, i * 4, 0, 0x10));
-}
 
 // out[g][d] of the G query heads of one kv head from their ns chunk partials
 // (part: [g][splits][D + 2]), by one workgroup: per head, wave g's lanes

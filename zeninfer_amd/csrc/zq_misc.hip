@@ -150,6 +150,35 @@ __global__ __launch_bounds__(256) void mfma_probe_kernel(uint64_t* out, uint32_t
 }
 }  // namespace
 
+// Plain streaming read, the yardstick of the GEMV rooflines: `bytes` (a
+// multiple of 16) read once with non-temporal 16-byte loads, each workgroup
+// a contiguous share, two loads per thread in flight per step; the xor of
+// everything is stored only if it equals a value no input produces here,
+// so the loads cannot be dropped.
+constexpr uint32_t kReadProbeWgs = 4096;
+typedef uint32_t u32x4_probe_t __attribute__((ext_vector_type(4)));
+__global__ __launch_bounds__(kThreads) void read_probe_kernel(const u32x4_probe_t* __restrict__ w, size_t n16,
+                                                              uint32_t* sink) {
+    const size_t per = (n16 + gridDim.x - 1) / gridDim.x;
+    const size_t b = size_t(blockIdx.x) * per, e = min(b + per, n16);
+    uint32_t acc = 0;
+    for (size_t i = b + threadIdx.x; i < e; i += 2 * kThreads) {
+        const size_t j = i + kThreads;
+        const u32x4_probe_t v0 = __builtin_nontemporal_load(&w[i]);
+        const u32x4_probe_t v1 = j < e ? __builtin_nontemporal_load(&w[j]) : u32x4_probe_t{0, 0, 0, 0};
+        acc ^= v0.x ^ v0.y ^ v0.z ^ v0.w ^ v1.x ^ v1.y ^ v1.z ^ v1.w;
+    }
+    if (acc == 0x9E3779B9u) sink[blockIdx.x] = acc;
+}
+
+hipError_t launch_read_probe(const void* buf, size_t bytes, uint32_t* sink, hipStream_t stream) {
+    if (!buf || !sink || !bytes || bytes % 16 || (reinterpret_cast<uintptr_t>(buf) & 15u)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(read_probe_kernel, dim3(kReadProbeWgs), dim3(kThreads), 0, stream, static_cast<const u32x4_probe_t*>(buf),
+                       bytes / 16, sink);
+    return hipGetLastError();
+}
+size_t read_probe_sink_bytes() { return size_t(kReadProbeWgs) * sizeof(uint32_t); }
+
 hipError_t launch_mfma_probe(uint64_t* out, uint32_t wgs, uint32_t iters, hipStream_t stream) {
     if (!out || !wgs || !iters) return hipErrorInvalidValue;
     hipLaunchKernelGGL(mfma_probe_kernel, dim3(wgs), dim3(256), 0, stream, out, iters, 3);

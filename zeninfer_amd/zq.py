@@ -108,6 +108,8 @@ SIGNATURES = {
     "zq_hip_block_dots_dev": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _S, _S, _S, _P]),
     "zq_hip_dequantize_dev": (ctypes.c_int, [ctypes.c_int, _P, _P, _S, _S, _P]),
     "zq_hip_mfma_peak": (ctypes.c_int, [ctypes.POINTER(ctypes.c_double)] * 3),
+    "zq_hip_read_probe_dev": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p]),
+    "zq_hip_read_probe_sink_bytes": (ctypes.c_size_t, []),
     "zq_hip_synth_weights_dev": (ctypes.c_int, [ctypes.c_int, ctypes.c_uint64, _P, _S, _S, _P]),
     "zq_hip_synth_normal_dev": (ctypes.c_int, [ctypes.c_uint64, _P, _S, _P]),
 }
@@ -532,6 +534,17 @@ def mfma_peak():
     a, b, c = ctypes.c_double(), ctypes.c_double(), ctypes.c_double()
     check(lib().zq_hip_mfma_peak(ctypes.byref(a), ctypes.byref(b), ctypes.byref(c)), "zq_hip_mfma_peak")
     return a.value, b.value, c.value
+
+
+def read_probe_sink_bytes():
+    return lib().zq_hip_read_probe_sink_bytes()
+
+
+def read_probe_dev(buf, nbytes, sink, stream=None):
+    """Enqueue one streaming read of nbytes of device memory (the GEMV roofline's yardstick)."""
+    _need(buf, nbytes, "read_probe_dev buffer")
+    _need(sink, read_probe_sink_bytes(), "read_probe_dev sink")
+    return check(lib().zq_hip_read_probe_dev(_dptr(buf), nbytes, _dptr(sink), _stream(stream)), "zq_hip_read_probe_dev")
 
 
 def synth_weights_dev(fmt, seed, w, rows, cols, stream=None):
