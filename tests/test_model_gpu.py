@@ -226,11 +226,15 @@ def test_fused_decode_equals_unfused(tiny_path, zq):
         assert np.abs(la - lb).max() <= 1e-5 * np.abs(lb).max() + 1e-6
 
 
-@pytest.mark.parametrize("embedding,heads,kv_heads", [(512, 4, 2), (1024, 8, 1)])
+@pytest.mark.parametrize("embedding,heads,kv_heads", [(512, 4, 2), (1024, 8, 1), (768, 3, 1), (896, 14, 2)])
 def test_prefill_attention_shapes_match_reference(tmp_path, zq, embedding, heads, kv_heads):
     """head_dim 128 with 2 and 8 query heads per kv head, a 150-token prompt
     (three 64-key tiles, a partial last query tile): fp32 prefill logits and
-    the following decode step within the fp32 bar of the reference."""
+    the following decode step within the fp32 bar of the reference.  Also
+    head_dim 256 with 3 query heads per kv head and head_dim 64 with 7: the
+    prefill falls back to the one-workgroup-per-row kernel (the MFMA kernel
+    takes head_dim 64/128 with G dividing 64) and the decode kernel runs
+    its G = 3 and G = 7 instances."""
     if not os.path.exists(REF_LIB):
         pytest.skip("oracle/_ref not built")
     from oracle.oracle import ReferenceModel

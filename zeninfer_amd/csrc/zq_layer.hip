@@ -681,11 +681,7 @@ hipError_t launch_attention(const float* q, const float* kc, const float* vc, fl
     if (!q || !kc || !vc || !out || !pos0 || !T || !H || !KH || H % KH || D % 64 || D > 256 || !max_pos)
         return hipErrorInvalidValue;
     const uint32_t G = H / KH;
-    static const bool legacy = [] {
-        const char* e = getenv("ZQ_ATTN_PREFILL");
-        return e && e[0] == 'l';
-    }();
-    if (!legacy && kFRows % G == 0 && (D == 64 || D == 128)) {
+    if (kFRows % G == 0 && (D == 64 || D == 128)) {
         const uint32_t TQ = kFRows / G;
         const dim3 grid(KH, (T + TQ - 1) / TQ);
         const size_t lds = (size_t(kFRows) * (D + 1) + size_t(kFKeys) * (D + 1) + size_t(kFKeys) * D +
@@ -727,7 +723,11 @@ hipError_t launch_attention_decode(const float* q, const float* knew, const floa
     switch (G) {                           \
     case 1: ZQ_ATTN(DD, 1); break;         \
     case 2: ZQ_ATTN(DD, 2); break;         \
+    case 3: ZQ_ATTN(DD, 3); break;         \
     case 4: ZQ_ATTN(DD, 4); break;         \
+    case 5: ZQ_ATTN(DD, 5); break;         \
+    case 6: ZQ_ATTN(DD, 6); break;         \
+    case 7: ZQ_ATTN(DD, 7); break;         \
     case 8: ZQ_ATTN(DD, 8); break;         \
     default: return hipErrorInvalidValue;  \
     }

@@ -210,7 +210,7 @@ bool init_common(zq_model& m, std::string& e) {
         return false;
     }
     if (c.heads % c.kv_heads) { e = "heads must be a multiple of kv_heads"; return false; }
-    if (c.head_dim % 64 || c.head_dim > 256) { e = "head_dim must be a multiple of 64, at most 256"; return false; }
+    if (c.head_dim != 64 && c.head_dim != 128 && c.head_dim != 256) { e = "head_dim must be 64, 128 or 256"; return false; }
     if (c.rope_dim == 0 || c.rope_dim > c.head_dim || c.rope_dim % 2) { e = "Invalid rotary dimension"; return false; }
     if (size_t(c.max_positions) * 4 > 96 * 1024) { e = "max_positions above 24576"; return false; }
     if (c.embedding % 32 || c.ffn % 32 || (size_t(c.heads) * c.head_dim) % 32) { e = "dimensions must divide into 32-blocks"; return false; }
