@@ -234,13 +234,22 @@ __global__ __launch_bounds__(kT) void attention_prefill_kernel(const float* __re
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l32 = lane & 31, lh = lane >> 5;
 
-    for (uint32_t i = tid; i < uint32_t(kFRows) * D / 4; i += kT) {
-        const uint32_t r = (4 * i) / D, d = (4 * i) % D;
-        const uint32_t g = r / TQ, t = r % TQ;
-        float4 v = make_float4(0, 0, 0, 0);
-        if (t0 + t < T) v = *reinterpret_cast<const float4*>(q + (size_t(t0 + t) * H + kh * G + g) * D + d);
-        float* dst = qs + r * QP + d;
-        dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;
+    {
+        constexpr int QL = kFRows * D / 4 / kT;  // float4 of Q per thread, all loaded before any is stored
+        float4 qv[QL];
+#pragma unroll
+        for (int j = 0; j < QL; ++j) {
+            const uint32_t i = tid + j * kT, r = (4 * i) / D, d = (4 * i) % D;
+            const uint32_t g = r / TQ, t = r % TQ;
+            qv[j] = t0 + t < T ? *reinterpret_cast<const float4*>(q + (size_t(t0 + t) * H + kh * G + g) * D + d)
+                               : make_float4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < QL; ++j) {
+            const uint32_t i = tid + j * kT, r = (4 * i) / D, d = (4 * i) % D;
+            float* dst = qs + r * QP + d;
+            dst[0] = qv[j].x; dst[1] = qv[j].y; dst[2] = qv[j].z; dst[3] = qv[j].w;
+        }
     }
     if (tid < kFRows) {
         row_m[tid] = -INFINITY;
@@ -253,20 +262,33 @@ __global__ __launch_bounds__(kT) void attention_prefill_kernel(const float* __re
 #pragma unroll
         for (int v = 0; v < 16; ++v) o[n][v] = 0.0f;
     const uint32_t nkeys = pos0 + min(t0 + TQ, T);  // keys any row of the tile sees
+    // K/V tiles go global -> registers -> LDS; the registers of tile k0 + 64
+    // are loaded while tile k0 is computed, so a tile's loads (one round trip
+    // for all of them) overlap the previous tile's MFMAs.
+    constexpr int KVL = kFKeys * D / 4 / kT;  // float4 of K (and of V) per thread per tile
+    float4 kr4[KVL], vr4[KVL];
+    auto load_tile = [&](uint32_t k0) {
+#pragma unroll
+        for (int j = 0; j < KVL; ++j) {
+            const uint32_t i = tid + j * kT, kr = (4 * i) / D, d = (4 * i) % D;
+            const uint32_t key = min(k0 + kr, nkeys - 1);  // past the last key: a valid row, masked in S
+            kr4[j] = *reinterpret_cast<const float4*>(kc + size_t(key) * KW + size_t(kh) * D + d);
+            vr4[j] = *reinterpret_cast<const float4*>(vc + size_t(key) * KW + size_t(kh) * D + d);
+        }
+    };
+    load_tile(0);
     for (uint32_t k0 = 0; k0 < nkeys; k0 += kFKeys) {
         __syncthreads();  // the previous tile's readers are done
-        for (uint32_t i = tid; i < uint32_t(kFKeys) * D / 4; i += kT) {
-            const uint32_t kr = (4 * i) / D, d = (4 * i) % D;
-            const uint32_t key = k0 + kr;
-            float4 kv = make_float4(0, 0, 0, 0), vv = make_float4(0, 0, 0, 0);
-            if (key < nkeys) {
-                kv = *reinterpret_cast<const float4*>(kc + size_t(key) * KW + size_t(kh) * D + d);
-                vv = *reinterpret_cast<const float4*>(vc + size_t(key) * KW + size_t(kh) * D + d);
-            }
+#pragma unroll
+        for (int j = 0; j < KVL; ++j) {
+            const uint32_t i = tid + j * kT, kr = (4 * i) / D, d = (4 * i) % D;
+            const bool live = k0 + kr < nkeys;  // zero K/V past the last key (as before: S is masked there)
+            const float4 kv = live ? kr4[j] : make_float4(0, 0, 0, 0), vv = live ? vr4[j] : make_float4(0, 0, 0, 0);
             float* kd = ks + kr * QP + d;
             kd[0] = kv.x; kd[1] = kv.y; kd[2] = kv.z; kd[3] = kv.w;
             *reinterpret_cast<float4*>(vs + kr * D + d) = vv;
         }
+        if (k0 + kFKeys < nkeys) load_tile(k0 + kFKeys);
         __syncthreads();
         {   // S tile of this wave: rows 32*(wave>>1), keys 32*(wave&1)
             v16f_t sacc;
