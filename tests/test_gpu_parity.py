@@ -76,8 +76,10 @@ def test_quantize_acts_bit_exact(zq, orc, m, k):
 
 @pytest.mark.parametrize("fmt,m,n,k", [(O.Q8_0, 5, 37, 256), (O.Q8_0, 130, 131, 192), (O.Q8_0, 1, 128, 4096),
                                        (O.Q4_0, 7, 70, 320), (O.Q4_0, 129, 3, 128),
-                                       # direct-load kernels for Q4_0 (K % 256 == 0): 32- and 128-token tiles
-                                       (O.Q4_0, 9, 33, 1024), (O.Q4_0, 40, 70, 512)])
+                                       # M <= 64 with K % 512 == 0: the skinny kernel (ragged M and N, two
+                                       # token tiles); K % 512 != 0: the 32-token kernel; M > 64: 128-token tiles
+                                       (O.Q4_0, 9, 33, 1024), (O.Q4_0, 40, 70, 512), (O.Q8_0, 33, 45, 1024),
+                                       (O.Q8_0, 17, 100, 768), (O.Q4_0, 70, 40, 512)])
 def test_block_dots_bit_exact(zq, orc, fmt, m, n, k):
     w = orc.gen_weights(fmt, 3 + n, n, k)
     x = orc.gen_normal(4 + m, m * k)
@@ -198,9 +200,11 @@ def test_device_synth_matches_host_generator(zq, orc):
 # ----------------------------------------------------------------- GEMM ---
 @pytest.mark.parametrize("fmt,m,n,k", [(O.Q8_0, 3, 300, 4096), (O.Q8_0, 130, 257, 1024), (O.Q8_0, 32, 128, 14336),
                                        (O.Q8_0, 2, 64, 192), (O.Q4_0, 17, 200, 4096), (O.Q4_0, 129, 130, 256),
-                                       # 32-token tiles (M <= 64): ragged M and N, a K split, two token
-                                       # tiles; M = 65 takes the 128-token tile
+                                       # M <= 64: the skinny kernel (K % 512 == 0: ragged M and N, a K split,
+                                       # two token tiles) or the 32-token kernel (K = 768, 1280); M = 65
+                                       # takes the 128-token tile
                                        (O.Q8_0, 31, 1000, 8192), (O.Q8_0, 33, 260, 2048), (O.Q8_0, 65, 260, 2048),
+                                       (O.Q8_0, 17, 100, 768), (O.Q4_0, 40, 90, 1280), (O.Q8_0, 64, 4096, 512),
                                        (O.Q4_0, 31, 700, 8192), (O.Q4_0, 150, 300, 2048),
                                        # always split K, with an odd output count (scalar split-K reduce)
                                        (O.Q8_0, 3, 301, 14336)])

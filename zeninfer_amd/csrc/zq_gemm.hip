@@ -669,6 +669,214 @@ __global__ __launch_bounds__(256, 3) void gemm_i8_small_kernel(
     gemm_i8_direct_body<FMT, DOTS, 4, 1>(W, XQ, XS, Y, dots, M, N, K, tiles_m, tiles_n, ksplit, stages_per_split);
 }
 
+// Skinny int8 GEMM for M <= 64 (Q8_0 / Q4_0, K % 512 == 0): a 32-token x
+// 32-row tile per workgroup, K stages of 16 blocks, and the workgroup's 4
+// waves sharing the tile, each taking 4 of a stage's 16 blocks (the same
+// 32x32x32 int8 MFMA and 2-block scale MFMA per block pair as the 32-token
+// kernel above); the 4 partial tiles are summed through LDS in wave order at
+// the end.  Why: at small M the weights are the traffic, and a stage now
+// reads 32 rows x 16 blocks (544 B contiguous per Q8_0 row) instead of 128
+// rows x 4 blocks (136 B): measured, the longer row segments alone bring a
+// 32-token GEMM from 27.5 to 23.5 us at 14336x4096 (HBM serves short
+// scattered segments at a lower rate).  With N / 32 tiles a 14336-row matrix
+// needs no K split.
+constexpr int SKB = 16;                        // blocks per K stage
+constexpr int SK_ROWS = 32;                    // weight rows per tile
+template <int BB>
+struct SkinnyStage {
+    static constexpr int A_BYTES = 32 * SKB * 32;                // 32 tokens x 16 blocks x 32 int8
+    static constexpr int UPR = SKB * 2;                          // 16 B units per activation row
+    static constexpr int WD = SKB * BB / 4;                      // raw dwords of a weight row per stage
+    static constexpr int W_STRIDE = WD | 1;                      // odd: conflict-free B reads
+    static constexpr int W_DWORDS = (SK_ROWS - 1) * W_STRIDE + WD + 1;  // +1: the 5th dword read
+    static constexpr int W_LOADS = (W_DWORDS + 63) / 64;
+    static constexpr int W_PER_WAVE = (W_LOADS + 3) / 4;
+    static constexpr int W_BYTES = (W_LOADS * 256 + 15) / 16 * 16;
+    static constexpr int S_BYTES = SKB * 32 * 4;
+    static constexpr int S_UNITS = S_BYTES / 256;
+    static constexpr int S_PER_WAVE = (S_UNITS + 3) / 4;
+    static constexpr int BUF = A_BYTES + W_BYTES + S_BYTES;
+    static_assert(2 * BUF <= 80 * 1024, "two workgroups per CU");
+    static_assert(A_BYTES % 4096 == 0 && S_UNITS % 4 == 0, "loads split evenly over the 4 waves");
+    // row r's 16 B units XOR-swizzled by r % 16: the 16 rows a quarter-wave's
+    // ds_read_b128 touches fall on distinct 16 B bank groups
+    __device__ static int swz(int row) { return row & 15; }
+};
+
+// (a __device__ body under a __global__ wrapper: a __global__ template with
+// dynamic LDS declared inside left its host launch stub undefined)
+// DOTS = true: the bit-exact test mode of the other int8 kernels -- every
+// per-block int32 MFMA result goes to dots[(m*N + n)*nb + b] instead.
+template <int FMT, bool DOTS>
+__device__ __forceinline__ void gemm_i8_skinny_body(
+    const uint8_t* __restrict__ W, const int8_t* __restrict__ XQ, const float* __restrict__ XS,
+    float* __restrict__ Y, int32_t* __restrict__ dots, uint32_t M, uint32_t N, uint32_t K, uint32_t tiles_m,
+    uint32_t tiles_n, uint32_t ksplit, uint32_t stages_per_split) {
+    constexpr int BB = FMT == kQ8_0 ? 34 : 18;
+    static_assert(FMT == kQ8_0 || FMT == kQ4_0, "int8-activation formats only");
+    using G = SkinnyStage<BB>;
+    extern __shared__ __align__(16) uint8_t lds[];  // 2 * G::BUF bytes
+    const uint32_t total_tiles = tiles_m * tiles_n;
+    const uint32_t split = blockIdx.x / total_tiles;
+    uint32_t tm, tn;
+    tile_of(tiles_m, tiles_n, blockIdx.x % total_tiles, tm, tn);
+    const uint32_t m0 = tm * 32, n0 = tn * SK_ROWS;
+    const uint32_t nb = K >> 5, rb = nb * BB;
+    const uint32_t kb_begin = split * stages_per_split * SKB;
+    const uint32_t kb_end = min(nb, kb_begin + stages_per_split * SKB);
+    float* Yout = Y + (ksplit > 1 ? size_t(split) * M * N : 0);
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l32 = lane & 31, lh = lane >> 5;
+
+    constexpr int A_LOADS = G::A_BYTES / 1024 / 4;
+    const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)(XQ + size_t(m0) * K), 0, -1, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t w_rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)(W + size_t(n0) * rb), 0, -1, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t s_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(DOTS ? reinterpret_cast<const float*>(XQ) : XS + size_t(m0) * nb), 0, -1, kBufferWord3);
+    uint32_t a_off[A_LOADS];
+#pragma unroll
+    for (int i = 0; i < A_LOADS; ++i) {
+        const int unit = (wave * A_LOADS + i) * 64 + lane;
+        const int row = unit / G::UPR, col = (unit % G::UPR) ^ G::swz(row);
+        a_off[i] = (min(m0 + row, M - 1) - m0) * K + col * 16;
+    }
+    uint32_t w_off[G::W_PER_WAVE];
+#pragma unroll
+    for (int i = 0; i < G::W_PER_WAVE; ++i) {
+        const uint32_t p = uint32_t((wave + 4 * i) * 64 + lane);
+        const uint32_t r = min(p / G::W_STRIDE, uint32_t(SK_ROWS - 1));
+        uint32_t d = p - r * G::W_STRIDE;
+        if (d >= uint32_t(G::WD)) d = 0;
+        w_off[i] = (min(n0 + r, N - 1) - n0) * rb + d * 4;
+    }
+    uint32_t s_off[G::S_PER_WAVE];
+#pragma unroll
+    for (int i = 0; i < G::S_PER_WAVE; ++i) {
+        const int idx = (wave * G::S_PER_WAVE + i) * 64 + lane;  // = b * 32 + m
+        s_off[i] = ((min(m0 + uint32_t(idx % 32), M - 1) - m0) * nb + uint32_t(idx / 32)) * 4;
+    }
+    auto stage_in = [&](uint32_t kb, int buf) {
+        uint8_t* base = lds + buf * G::BUF;
+#pragma unroll
+        for (int i = 0; i < A_LOADS; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_void*)(base + (wave * A_LOADS + i) * 1024), 16,
+                                                     a_off[i], kb * 32, 0, 0);
+#pragma unroll
+        for (int i = 0; i < G::W_PER_WAVE; ++i)
+            if (wave + 4 * i < G::W_LOADS)  // wave-uniform
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_void*)(base + G::A_BYTES + (wave + 4 * i) * 256), 4,
+                                                         w_off[i], kb * BB, 0, 0);
+        if constexpr (!DOTS) {
+#pragma unroll
+            for (int i = 0; i < G::S_PER_WAVE; ++i)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    s_rsrc, (lds_void*)(base + G::A_BYTES + G::W_BYTES + (wave * G::S_PER_WAVE + i) * 256), 4, s_off[i],
+                    kb * 4, 0, 0);
+        }
+    };
+
+    v16f acc;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
+    const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    v32f szero;
+#pragma unroll
+    for (int v = 0; v < 32; ++v) szero[v] = 0.0f;
+    const uint32_t wrow = uint32_t(l32) * G::W_STRIDE;  // this lane's weight row (n0 + l32), first LDS dword
+
+    // one block pair (2j, 2j+1) of this wave's quarter: operands, the two
+    // int8 MFMAs and one 2-block scale MFMA (block i of it = lane half i =
+    // K block 2j + i), then cvt + fma per output element and block
+    auto pair = [&](const uint8_t* base, int b0, uint32_t kb) {
+        const uint32_t* Bw = reinterpret_cast<const uint32_t*>(base + G::A_BYTES) + wrow;
+        v4i a[2], w[2];
+        uint32_t t[2][5];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int b = b0 + h;
+            const int off = (b * BB + 2 + (FMT == kQ8_0 ? lh * 16 : 0)) >> 2;
+#pragma unroll
+            for (int i = 0; i < 4 + (h ? 0 : 1); ++i) t[h][i] = Bw[off + i];
+            const int col = (b * 2 + lh) ^ G::swz(l32);
+            a[h] = *reinterpret_cast<const v4i*>(base + l32 * (SKB * 32) + col * 16);
+        }
+        const int sb = b0 + lh;  // scales of this lane half's block
+        v32f sc = szero;
+        if constexpr (!DOTS) {
+            const uint32_t dwh = reinterpret_cast<const uint16_t*>(Bw)[sb * (BB / 2)];
+            const float dx = reinterpret_cast<const float*>(base + G::A_BYTES + G::W_BYTES)[sb * 32 + l32];
+            sc = __builtin_amdgcn_mfma_f32_32x32x1f32(dx, half_bits_to_float(uint16_t(dwh)), szero, 0, 0, 0);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                w[h][i] = h ? int(t[h][i]) : int(__builtin_amdgcn_alignbyte(t[h][i + 1], t[h][i], 2));
+            if constexpr (FMT == kQ4_0) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    w[h][i] = int(((uint32_t(w[h][i]) >> (4 * lh)) & 0x0F0F0F0Fu) + 0x78787878u) ^ int(0x80808080u);
+            }
+        }
+        const v16i c0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[0], w[0], zero, 0, 0, 0);
+        const v16i c1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[1], w[1], zero, 0, 0, 0);
+        if constexpr (DOTS) {
+            const uint32_t n = n0 + l32;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const uint32_t m = m0 + 8 * (v >> 2) + 4 * lh + (v & 3);
+                if (m < M && n < N) {
+                    dots[(size_t(m) * N + n) * nb + kb + b0] = c0[v];
+                    dots[(size_t(m) * N + n) * nb + kb + b0 + 1] = c1[v];
+                }
+            }
+            return;
+        }
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[v] = fmaf(float(c0[v]), sc[v], acc[v]);
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[v] = fmaf(float(c1[v]), sc[16 + v], acc[v]);
+    };
+
+    if (kb_begin < kb_end) {
+        stage_in(kb_begin, 0);
+        int buf = 0;
+        for (uint32_t kb = kb_begin; kb < kb_end; kb += SKB, buf ^= 1) {
+            __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's direct loads of stage kb landed
+            __syncthreads();                     // ... and everyone's; the other buffer is free again
+            if (kb + SKB < kb_end) stage_in(kb + SKB, buf ^ 1);
+            const uint8_t* base = lds + buf * G::BUF;
+            pair(base, 4 * wave, kb);
+            pair(base, 4 * wave + 2, kb);
+        }
+    }
+    if constexpr (DOTS) return;
+    // the four waves' partial tiles, summed in wave order
+    __syncthreads();
+    float* red = reinterpret_cast<float*>(lds);  // [wave][16][64]
+#pragma unroll
+    for (int v = 0; v < 16; ++v) red[(wave * 16 + v) * 64 + lane] = acc[v];
+    __syncthreads();
+    if (wave == 0) {
+        const uint32_t n = n0 + l32;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            float t = red[v * 64 + lane];
+#pragma unroll
+            for (int w = 1; w < 4; ++w) t += red[(w * 16 + v) * 64 + lane];
+            const uint32_t m = m0 + 8 * (v >> 2) + 4 * lh + (v & 3);
+            if (m < M && n < N) Yout[size_t(m) * N + n] = t;
+        }
+    }
+}
+template <int FMT, bool DOTS>
+__global__ __launch_bounds__(256, 2) void gemm_i8_skinny_kernel(
+    const uint8_t* __restrict__ W, const int8_t* __restrict__ XQ, const float* __restrict__ XS,
+    float* __restrict__ Y, int32_t* __restrict__ dots, uint32_t M, uint32_t N, uint32_t K, uint32_t tiles_m,
+    uint32_t tiles_n, uint32_t ksplit, uint32_t stages_per_split) {
+    gemm_i8_skinny_body<FMT, DOTS>(W, XQ, XS, Y, dots, M, N, K, tiles_m, tiles_n, ksplit, stages_per_split);
+}
+
 // ------------------------------------------------------- fp32 GEMM -------
 constexpr int FK = 32;          // K elements per fp32 stage
 constexpr int FROW = FK + 4;    // LDS floats per row (pad)
@@ -798,15 +1006,25 @@ static uint32_t choose_ksplit_model(uint32_t tiles, uint32_t stages, size_t M, s
     return best;
 }
 
+// Split factor of the skinny kernel: as many splits as keep the whole grid
+// resident at once (two workgroups per CU, its LDS budget), at least 2 K
+// stages per split.  A grid past one round measured slower than fewer splits.
+static uint32_t choose_ksplit_skinny(uint32_t tiles, uint32_t stages) {
+    const uint32_t fit = std::max(1u, 2u * uint32_t(device_cu_count()) / tiles);
+    return std::max(1u, std::min(fit, std::max(1u, stages / 2)));
+}
+
 size_t gemm_i8_partial_bytes(size_t M, size_t N, size_t K) {
     const uint32_t tiles = uint32_t(((M + BM - 1) / BM) * ((N + BN - 1) / BN));
     const uint32_t nb = uint32_t(K / 32);
     // sized for every kernel choice: the direct-load kernels (128- and
     // 32-token tiles) and the staged-conversion kernel
     const uint32_t small_tiles = uint32_t(((M + 31) / 32) * ((N + BN - 1) / BN));
+    const uint32_t skinny_tiles = uint32_t(((M + 31) / 32) * ((N + SK_ROWS - 1) / SK_ROWS));
     const uint32_t ks = std::max({choose_ksplit(tiles, nb),
                                   choose_ksplit_model(tiles, (nb + 3) / 4, M, N),
-                                  choose_ksplit_model(small_tiles, (nb + 3) / 4, M, N, kSmallTileCost)});
+                                  choose_ksplit_model(small_tiles, (nb + 3) / 4, M, N, kSmallTileCost),
+                                  choose_ksplit_skinny(skinny_tiles, (nb + SKB - 1) / SKB)});
     return ks > 1 ? size_t(ks) * M * N * sizeof(float) : 0;
 }
 
@@ -842,6 +1060,21 @@ static hipError_t launch_direct(const uint8_t* w, const int8_t* xq, const float*
     constexpr size_t kLds4 = 2 * QStage<4, BM, QTH / 64, BB>::BUF;
     const uint32_t m = uint32_t(M), n = uint32_t(N), k = uint32_t(K), nb = uint32_t(K / 32);
     const uint32_t tiles_n = static_cast<uint32_t>((N + BN - 1) / BN);
+    if (M <= kSmallMLimit && K % (SKB * 32) == 0) {
+        const uint32_t stm = uint32_t((M + 31) / 32), stn = uint32_t((N + SK_ROWS - 1) / SK_ROWS), sst = nb / SKB;
+        constexpr size_t lds = 2 * SkinnyStage<BB>::BUF;
+        if (dots) {
+            hipLaunchKernelGGL((gemm_i8_skinny_kernel<FMT, true>), dim3(stm * stn), dim3(256), lds, stream, w, xq, xs, Y,
+                               dots, m, n, k, stm, stn, 1u, sst);
+            return hipGetLastError();
+        }
+        uint32_t ks = partial ? choose_ksplit_skinny(stm * stn, sst) : 1u;
+        const uint32_t spw = (sst + ks - 1) / ks;
+        ks = (sst + spw - 1) / spw;  // no empty splits
+        hipLaunchKernelGGL((gemm_i8_skinny_kernel<FMT, false>), dim3(stm * stn * ks), dim3(256), lds, stream, w, xq, xs,
+                           ks > 1 ? partial : Y, dots, m, n, k, stm, stn, ks, spw);
+        return finish_splits(hipGetLastError(), partial, Y, M, N, ks, stream);
+    }
     if (M <= kSmallMLimit) {
         const uint32_t stm = uint32_t((M + 31) / 32), sst = (nb + 3) / 4;
         if (dots) {
