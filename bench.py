@@ -524,11 +524,18 @@ def main():
                                      ("down 4096x14336", "down", HIDDEN, FFN, x_f)):
         yb = torch.empty(rows, device=dev)
         ms = timed_launches(lambda i: zq.gemv_dev(Q8, layers[i % LAYERS][key], x, yb, rows, cols), 2 * LAYERS, LAYERS)
+        # the same weight bytes read by the plain streaming-read probe, same timing
+        wb = rows * zq.row_bytes(Q8, cols)
+        rms = timed_launches(lambda i: zq.read_probe_dev(layers[i % LAYERS][key], wb, sink), 2 * LAYERS, LAYERS)
         per_shape[name] = {"us": round(ms * 1e3, 2),
-                           "GB/s": round(gemv_bytes(zq.row_bytes(Q8, cols), rows, cols) / (ms * 1e-3) / 1e9, 1)}
+                           "GB/s": round(gemv_bytes(zq.row_bytes(Q8, cols), rows, cols) / (ms * 1e-3) / 1e9, 1),
+                           "read_ceiling_us": round(rms * 1e3, 2), "frac_of_read_ceiling": round(rms / ms, 4)}
     ms = timed_launches(lambda i: zq.gemv_dev(Q8, lm_head, x_h, y_lm, VOCAB, HIDDEN), 8, 1)
+    rms = timed_launches(lambda i: zq.read_probe_dev(lm_head, VOCAB * rbh, sink), 8, 1)
     per_shape["lm_head 128256x4096"] = {"us": round(ms * 1e3, 2),
-                                        "GB/s": round(gemv_bytes(rbh, VOCAB, HIDDEN) / (ms * 1e-3) / 1e9, 1)}
+                                        "GB/s": round(gemv_bytes(rbh, VOCAB, HIDDEN) / (ms * 1e-3) / 1e9, 1),
+                                        "read_ceiling_us": round(rms * 1e3, 2),
+                                        "frac_of_read_ceiling": round(rms / ms, 4)}
 
     # ---- secondary: int8 prefill GEMM at M = 2048 (config 2) ---------------
     M = 2048
