@@ -226,6 +226,35 @@ def test_fused_decode_equals_unfused(tiny_path, zq):
         assert np.abs(la - lb).max() <= 1e-5 * np.abs(lb).max() + 1e-6
 
 
+@pytest.mark.parametrize("ptype", [G.GGML_Q8_0, G.GGML_Q4_0])
+def test_fused_prefill_quantiser_equals_unfused(tmp_path, zq, ptype):
+    """Int8 prefill with the activations quantised inside the RMSNorm and
+    SiLU*up kernels against the separate quantiser launches
+    (ZQ_MODEL_FUSED=0): the same per-block arithmetic on the same fp32
+    values, so the prefill logits are bit-identical, for a 16-token and a
+    150-token prompt."""
+    from zeninfer_amd.model import PREFILL_INT8
+    path = tmp_path / f"fq_{ptype}.gguf"
+    G.synthetic_llama(path, SHAPE, seed=23, proj_type=ptype)
+    long_prompt = [int(t) for t in np.random.default_rng(5).integers(0, SHAPE.vocab, 150)]
+    outs = []
+    for fused in ("1", "0"):
+        os.environ["ZQ_MODEL_FUSED"] = fused
+        try:
+            m = load(path, PREFILL_INT8, max_positions=256)
+        finally:
+            os.environ.pop("ZQ_MODEL_FUSED", None)
+        res = []
+        for prompt in (PROMPT, long_prompt):
+            nxt, lg = m.prefill(prompt)
+            res.append((nxt, lg.copy()))
+        outs.append(res)
+        m.close()
+    for (ta, la), (tb, lb) in zip(*outs):
+        assert ta == tb
+        assert np.array_equal(la, lb)
+
+
 @pytest.mark.parametrize("embedding,heads,kv_heads", [(512, 4, 2), (1024, 8, 1), (768, 3, 1), (896, 14, 2)])
 def test_prefill_attention_shapes_match_reference(tmp_path, zq, embedding, heads, kv_heads):
     """head_dim 128 with 2 and 8 query heads per kv head, a 150-token prompt

@@ -444,10 +444,6 @@ struct HostCall {
 
 }  // namespace
 
-namespace zq {
-hipError_t launch_silu_mul(const float* gate, const float* up, float* out, size_t n, hipStream_t stream);
-}
-
 extern "C" {
 
 int zq_hip_opted_in(void) { return env_opted_in() ? 1 : 0; }

@@ -207,6 +207,34 @@ __device__ __forceinline__ float wave_max(float v) {
     return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
 }
 
+// Round half away from zero (the reference quantiser's lround), exact for
+// |v| < 2^23.
+__device__ __forceinline__ int round_half_away(float v) {
+    const float t = truncf(v);
+    const float f = v - t;  // exact for |v| < 2^23
+    return static_cast<int>(t) + (f >= 0.5f ? 1 : (f <= -0.5f ? -1 : 0));
+}
+// The per-32 activation quantiser (kernels/avx2.cpp:502-524) with one element
+// per lane: the 32 consecutive lanes of a half-wave hold one block.  The
+// block's amax is the max over its lanes (exact in any order), then d =
+// amax/127, inv = 1/d, q = round_half_away(clamp(v * inv, +-127)) -- the
+// arithmetic of quantize_acts_kernel, so the bytes and scales are equal.
+// Every lane of the wave must call it (the max crosses lanes).
+__device__ __forceinline__ void quantize_lane_block32(float v, int8_t* q_out, float* d_out) {
+    float amax = fabsf(v);
+    amax = fmaxf(amax, __shfl_xor(amax, 1));
+    amax = fmaxf(amax, __shfl_xor(amax, 2));
+    amax = fmaxf(amax, __shfl_xor(amax, 4));
+    amax = fmaxf(amax, __shfl_xor(amax, 8));
+    amax = fmaxf(amax, __shfl_xor(amax, 16));
+    const float d = amax > 0.0f ? amax / 127.0f : 0.0f;
+    const float inv = d > 0.0f ? 1.0f / d : 0.0f;
+    if ((threadIdx.x & 31u) == 0) *d_out = d;
+    float q = v * inv;
+    q = q > 127.0f ? 127.0f : (q < -127.0f ? -127.0f : q);
+    *q_out = int8_t(round_half_away(q));
+}
+
 // Cross-workgroup hand-off inside one launch (workgroups run on 8 XCDs with
 // private L2s): the producer writes with agent-scope stores (through to the
 // device-coherent level) and waits for them (s_waitcnt) before it signals;

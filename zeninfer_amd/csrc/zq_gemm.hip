@@ -53,11 +53,6 @@ constexpr int ROWB = KB * 32 + 16;  // LDS bytes per tile row (16 B pad)
 
 // ------------------------------------------------- activation quantiser ---
 // Bit-exact with kernels/avx2.cpp:502-524.
-__device__ __forceinline__ int round_half_away(float v) {
-    const float t = truncf(v);
-    const float f = v - t;  // exact for |v| < 2^23
-    return static_cast<int>(t) + (f >= 0.5f ? 1 : (f <= -0.5f ? -1 : 0));
-}
 
 // Eight lanes per block, four elements each (a coalesced float4 load and a
 // 4-byte store per lane); the block's amax is the max over its eight lanes

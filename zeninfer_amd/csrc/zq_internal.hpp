@@ -136,8 +136,10 @@ namespace zq {
 // read from device memory, so a captured decode step replays unchanged.
 hipError_t launch_embed(int fmt, const void* table, const uint32_t* tokens, uint32_t vocab, float* x, uint32_t E,
                         uint32_t T, hipStream_t stream);
+// xq/xs (optional, n % 32 == 0): y's int8 activations and scales as
+// launch_quantize_acts would write them, for the int8 GEMMs that read y.
 hipError_t launch_rmsnorm(const float* x, const float* w, float* y, uint32_t rows, uint32_t n, float eps,
-                          hipStream_t stream);
+                          hipStream_t stream, int8_t* xq = nullptr, float* xs = nullptr);
 hipError_t launch_rope_kv(float* q, const float* k, const float* v, float* kc, float* vc, const float* cos_tab,
                           const float* sin_tab, const uint32_t* pos0, uint32_t T, uint32_t H, uint32_t KH, uint32_t D,
                           uint32_t pairs, bool adjacent, hipStream_t stream);
@@ -160,9 +162,10 @@ hipError_t launch_add(float* x, const float* y, size_t n, hipStream_t stream);
 hipError_t launch_add_to(const float* x, const float* y, float* out, size_t n, hipStream_t stream);
 // x += r, then y = rmsnorm(x) * w (rows of n)
 hipError_t launch_add_rmsnorm(float* x, const float* r, const float* w, float* y, uint32_t rows, uint32_t n, float eps,
-                              hipStream_t stream);
+                              hipStream_t stream, int8_t* xq = nullptr, float* xs = nullptr);
 // Greedy id over n values; `partial` holds argmax_partial_bytes().
 size_t argmax_partial_bytes();
 hipError_t launch_argmax(const float* x, uint32_t n, uint32_t* out, void* partial, hipStream_t stream);
-hipError_t launch_silu_mul(const float* gate, const float* up, float* out, size_t n, hipStream_t stream);
+hipError_t launch_silu_mul(const float* gate, const float* up, float* out, size_t n, hipStream_t stream,
+                           int8_t* xq = nullptr, float* xs = nullptr);
 }  // namespace zq

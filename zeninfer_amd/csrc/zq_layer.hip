@@ -81,7 +81,7 @@ constexpr int kNormT = 1024;
 template <bool ADD>
 __global__ __launch_bounds__(kNormT) void rmsnorm_kernel(float* __restrict__ x, const float* __restrict__ r,
                                                          const float* __restrict__ w, float* __restrict__ y, uint32_t n,
-                                                         float eps) {
+                                                         float eps, int8_t* __restrict__ xq, float* __restrict__ xs) {
     __shared__ double red[kNormT / 64];
     float* xr = x + size_t(blockIdx.x) * n;
     float* yr = y + size_t(blockIdx.x) * n;
@@ -97,6 +97,16 @@ __global__ __launch_bounds__(kNormT) void rmsnorm_kernel(float* __restrict__ x, 
     }
     ss = block_sum_d(ss, red);
     const float inv = 1.0f / sqrtf(float(ss / double(n)) + eps);
+    if (xq) {  // also the int8 activations of y for the GEMMs that read it (n % 32 == 0: whole blocks per half-wave)
+        int8_t* qr = xq + size_t(blockIdx.x) * n;
+        float* sr = xs + size_t(blockIdx.x) * (n / 32);
+        for (uint32_t i = threadIdx.x; i < n; i += kNormT) {
+            const float v = xr[i] * inv * w[i];
+            yr[i] = v;
+            quantize_lane_block32(v, qr + i, sr + i / 32);
+        }
+        return;
+    }
     for (uint32_t i = threadIdx.x; i < n; i += kNormT) yr[i] = xr[i] * inv * w[i];
 }
 
@@ -672,17 +682,17 @@ hipError_t launch_embed(int fmt, const void* table, const uint32_t* tokens, uint
 }
 
 hipError_t launch_rmsnorm(const float* x, const float* w, float* y, uint32_t rows, uint32_t n, float eps,
-                          hipStream_t stream) {
-    if (!x || !w || !y || !rows || !n) return hipErrorInvalidValue;
+                          hipStream_t stream, int8_t* xq, float* xs) {
+    if (!x || !w || !y || !rows || !n || (xq && (!xs || n % 32))) return hipErrorInvalidValue;
     hipLaunchKernelGGL(rmsnorm_kernel<false>, dim3(rows), dim3(kNormT), 0, stream, const_cast<float*>(x), nullptr, w, y,
-                       n, eps);
+                       n, eps, xq, xs);
     return hipGetLastError();
 }
 
 hipError_t launch_add_rmsnorm(float* x, const float* r, const float* w, float* y, uint32_t rows, uint32_t n, float eps,
-                              hipStream_t stream) {
-    if (!x || !r || !w || !y || !rows || !n) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(rmsnorm_kernel<true>, dim3(rows), dim3(kNormT), 0, stream, x, r, w, y, n, eps);
+                              hipStream_t stream, int8_t* xq, float* xs) {
+    if (!x || !r || !w || !y || !rows || !n || (xq && (!xs || n % 32))) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rmsnorm_kernel<true>, dim3(rows), dim3(kNormT), 0, stream, x, r, w, y, n, eps, xq, xs);
     return hipGetLastError();
 }
 

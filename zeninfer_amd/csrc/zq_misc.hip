@@ -107,9 +107,20 @@ __global__ __launch_bounds__(kThreads) void synth_normal_kernel(uint64_t seed, f
 
 // SiLU(gate) * up, the FFN activation between gate|up and down
 // (g / (1 + e^-g)) * u.
+// With xq: also the int8 activations of o for the GEMM that reads it
+// (n % 32 == 0, so each 32-lane half-wave is one whole block, live or not).
 __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const float* __restrict__ g, const float* __restrict__ u,
-                                                            float* __restrict__ o, size_t n) {
+                                                            float* __restrict__ o, size_t n, int8_t* __restrict__ xq,
+                                                            float* __restrict__ xs) {
     const size_t i = size_t(blockIdx.x) * kThreads + threadIdx.x;
+    if (xq) {
+        if (i >= n) return;
+        const float gv = g[i];
+        const float v = gv / (1.0f + expf(-gv)) * u[i];
+        o[i] = v;
+        quantize_lane_block32(v, xq + i, xs + i / 32);
+        return;
+    }
     if (i < n) {
         const float gv = g[i];
         o[i] = gv / (1.0f + expf(-gv)) * u[i];
@@ -185,10 +196,11 @@ hipError_t launch_mfma_probe(uint64_t* out, uint32_t wgs, uint32_t iters, hipStr
     return hipGetLastError();
 }
 
-hipError_t launch_silu_mul(const float* gate, const float* up, float* out, size_t n, hipStream_t stream) {
-    if (!gate || !up || !out || !n) return hipErrorInvalidValue;
+hipError_t launch_silu_mul(const float* gate, const float* up, float* out, size_t n, hipStream_t stream, int8_t* xq,
+                           float* xs) {
+    if (!gate || !up || !out || !n || (xq && (!xs || n % 32))) return hipErrorInvalidValue;
     const dim3 grid(static_cast<uint32_t>((n + kThreads - 1) / kThreads));
-    hipLaunchKernelGGL(silu_mul_kernel, grid, dim3(kThreads), 0, stream, gate, up, out, n);
+    hipLaunchKernelGGL(silu_mul_kernel, grid, dim3(kThreads), 0, stream, gate, up, out, n, xq, xs);
     return hipGetLastError();
 }
 

@@ -91,6 +91,7 @@ struct zq_model {
     uint32_t cur_pos = 0;  // positions held in the cache
     bool use_graph = true;
     bool fused = false;    // decode step with norms and SiLU folded into the GEMVs
+    bool fuse_quant = true;  // prefill norms / SiLU*up also write the int8 activations
     hipGraphExec_t decode_exec = nullptr;
     hipGraph_t decode_graph = nullptr;
 
@@ -231,11 +232,18 @@ hipError_t project(zq_model& m, const Weight& w, const float* X, float* Y, uint3
 
 bool int8_ok(int fmt) { return fmt == zq::kQ8_0 || fmt == zq::kQ4_0; }
 
+// Whether the projections ws read their input as int8 activations (prefill
+// in ZQ_PREFILL_INT8 mode, formats with an int8 GEMM).
+bool int8_inputs(const zq_model& m, std::initializer_list<const Weight*> ws) {
+    bool q = m.prefill_mode == ZQ_PREFILL_INT8;
+    for (const Weight* w : ws) q = q && int8_ok(w->fmt);
+    return q;
+}
+
 // Quantise X[M][K] once for every projection that reads it in int8 mode.
 hipError_t quantize_for(zq_model& m, std::initializer_list<const Weight*> ws, const float* X, uint32_t M, uint32_t K,
                         bool& quantized) {
-    quantized = m.prefill_mode == ZQ_PREFILL_INT8;
-    for (const Weight* w : ws) quantized = quantized && int8_ok(w->fmt);
+    quantized = int8_inputs(m, ws);
     if (!quantized) return hipSuccess;
     return zq::launch_quantize_acts(X, m.xq, m.xs, M, K, m.stream);
 }
@@ -253,7 +261,16 @@ hipError_t quantize_for(zq_model& m, std::initializer_list<const Weight*> ws, co
 hipError_t enqueue_layers(zq_model& m, uint32_t T) {
     const auto& c = m.cfg;
     const uint32_t E = c.embedding, QW = c.heads * c.head_dim, KW = c.kv_heads * c.head_dim, F = c.ffn;
-    HIPCHK(zq::launch_rmsnorm(m.x, m.layers[0].attn_norm, m.h, T, E, c.rms_epsilon, m.stream));
+    // In prefill the RMSNorm and SiLU*up kernels also write the int8
+    // activations of their output when the projections that read it take
+    // them (the quantiser's own arithmetic, one launch fewer per GEMM group).
+    auto qin = [&](std::initializer_list<const Weight*> ws) { return T > 1 && m.fuse_quant && int8_inputs(m, ws); };
+    {
+        const Layer& L0 = m.layers[0];
+        const bool q0 = qin({&L0.q, &L0.k, &L0.v});
+        HIPCHK(zq::launch_rmsnorm(m.x, L0.attn_norm, m.h, T, E, c.rms_epsilon, m.stream, q0 ? m.xq : nullptr,
+                                  q0 ? m.xs : nullptr));
+    }
     for (uint32_t l = 0; l < c.layers; ++l) {
         Layer& L = m.layers[l];
         if (T == 1) {
@@ -267,8 +284,8 @@ hipError_t enqueue_layers(zq_model& m, uint32_t T) {
                 HIPCHK(zq::launch_gemv(L.v.fmt, &t[2], 1, m.h, E, m.stream));
             }
         } else {
-            bool qz;
-            HIPCHK(quantize_for(m, {&L.q, &L.k, &L.v}, m.h, T, E, qz));
+            bool qz = qin({&L.q, &L.k, &L.v});  // h's int8 activations came with its norm
+            if (!qz) HIPCHK(quantize_for(m, {&L.q, &L.k, &L.v}, m.h, T, E, qz));
             HIPCHK(project(m, L.q, m.h, m.q, T, qz));
             HIPCHK(project(m, L.k, m.h, m.k, T, qz));
             HIPCHK(project(m, L.v, m.h, m.v, T, qz));
@@ -288,7 +305,9 @@ hipError_t enqueue_layers(zq_model& m, uint32_t T) {
             HIPCHK(quantize_for(m, {&L.o}, m.att, T, QW, qz));
             HIPCHK(project(m, L.o, m.att, m.tmp, T, qz));
         }
-        HIPCHK(zq::launch_add_rmsnorm(m.x, m.tmp, L.ffn_norm, m.h, T, E, c.rms_epsilon, m.stream));
+        const bool qgu = qin({&L.gate, &L.up});
+        HIPCHK(zq::launch_add_rmsnorm(m.x, m.tmp, L.ffn_norm, m.h, T, E, c.rms_epsilon, m.stream, qgu ? m.xq : nullptr,
+                                      qgu ? m.xs : nullptr));
         if (T == 1) {
             zq::GemvTask t[2] = {{L.gate.p, m.gate, F}, {L.up.p, m.up, F}};
             if (L.gate.fmt == L.up.fmt) {
@@ -298,22 +317,26 @@ hipError_t enqueue_layers(zq_model& m, uint32_t T) {
                 HIPCHK(zq::launch_gemv(L.up.fmt, &t[1], 1, m.h, E, m.stream));
             }
         } else {
-            bool qz;
-            HIPCHK(quantize_for(m, {&L.gate, &L.up}, m.h, T, E, qz));
+            bool qz = qgu;
+            if (!qz) HIPCHK(quantize_for(m, {&L.gate, &L.up}, m.h, T, E, qz));
             HIPCHK(project(m, L.gate, m.h, m.gate, T, qz));
             HIPCHK(project(m, L.up, m.h, m.up, T, qz));
         }
-        HIPCHK(zq::launch_silu_mul(m.gate, m.up, m.act, size_t(T) * F, m.stream));
+        const bool qd = qin({&L.down});
+        HIPCHK(zq::launch_silu_mul(m.gate, m.up, m.act, size_t(T) * F, m.stream, qd ? m.xq : nullptr,
+                                   qd ? m.xs : nullptr));
         if (T == 1) {
             zq::GemvTask t = {L.down.p, m.tmp, E};
             HIPCHK(zq::launch_gemv(L.down.fmt, &t, 1, m.act, F, m.stream));
         } else {
-            bool qz;
-            HIPCHK(quantize_for(m, {&L.down}, m.act, T, F, qz));
+            bool qz = qd;
+            if (!qz) HIPCHK(quantize_for(m, {&L.down}, m.act, T, F, qz));
             HIPCHK(project(m, L.down, m.act, m.tmp, T, qz));
         }
         const float* next_norm = l + 1 < c.layers ? m.layers[l + 1].attn_norm : m.out_norm;
-        HIPCHK(zq::launch_add_rmsnorm(m.x, m.tmp, next_norm, m.h, T, E, c.rms_epsilon, m.stream));
+        const bool qn = l + 1 < c.layers && qin({&m.layers[l + 1].q, &m.layers[l + 1].k, &m.layers[l + 1].v});
+        HIPCHK(zq::launch_add_rmsnorm(m.x, m.tmp, next_norm, m.h, T, E, c.rms_epsilon, m.stream, qn ? m.xq : nullptr,
+                                      qn ? m.xs : nullptr));
     }
     return hipSuccess;
 }
@@ -384,6 +407,7 @@ void choose_fused(zq_model& m) {
         f = f && ok(L.q.fmt) && L.k.fmt == L.q.fmt && L.v.fmt == L.q.fmt && ok(L.gate.fmt) && L.up.fmt == L.gate.fmt &&
             ok(L.down.fmt) && ok(L.o.fmt);
     m.fused = f;
+    m.fuse_quant = !(e && e[0] == '0');
 }
 
 int finish_outputs(zq_model& m, float* logits, uint32_t* next) {
