@@ -397,37 +397,82 @@ constexpr int kAttnMaxSplits = 1024;  // positions <= 32768
 
 
 // out[g][d] of the G query heads of one kv head from their ns chunk partials
-// (part: [g][splits][D + 2]), by one workgroup: per head, wave g's lanes
-// stride over the chunks for the max M and L = sum l_s exp(m_s - M) (in
-// double), then out = sum_s acc_s[d] exp(m_s - M) / L with the chunks summed
-// in order.
-template <int D>
-__device__ void merge_chunks(const float* part, float* out, uint32_t G, uint32_t ns, uint32_t splits) {
-    __shared__ float wgt[kAttnMaxG][kAttnMaxSplits];
-    __shared__ float inv_l[kAttnMaxG];
-    const int wv = threadIdx.x >> 6, ln = threadIdx.x & 63;
+// (part: [g][splits][D + 2]), by one workgroup, in batches of NB chunks.  All
+// loads of a batch (every thread's acc values and the batch's (m, l) pairs)
+// are issued together, so a batch costs one memory round trip.  Per head a
+// group of NB lanes takes the batch's max, the weights w_s = exp(m_s - M)
+// against the running max M and L = sum l_s w_s (in double); the running
+// acc and L are rescaled by exp(M_old - M) when the max grows.  With ns <= NB
+// (positions < 32 * NB) that is out = (sum_s acc_s[d] w_s, in chunk order) / L.
+template <int D, int G>
+__device__ void merge_chunks(const float* part, float* out, uint32_t ns, uint32_t splits) {
+    constexpr int E = (G * D + kT - 1) / kT;     // output elements per thread
+    constexpr int NB = E <= 2 ? 32 : (E <= 4 ? 16 : 8);  // chunks per batch: E * NB <= 64 loads per thread
+    static_assert(G * NB <= kT && (64 % NB) == 0, "one lane per (head, chunk) of a batch, groups inside a wave");
+    __shared__ float wgt[G][NB];
+    __shared__ float rs[G];
+    __shared__ float Ms[G];
+    __shared__ double Ls[G];
     const uint32_t n = G * splits * (D + 2);
-    for (uint32_t g = wv; g < G; g += kT / 64) {
-        const uint32_t base = g * splits * (D + 2);
-        float M = -INFINITY;
-        for (uint32_t s = ln; s < ns; s += 64) M = fmaxf(M, coherent_load_f(part, n, base + s * (D + 2) + D));
-        M = wave_max(M);
-        double L = 0.0;
-        for (uint32_t s = ln; s < ns; s += 64) {
-            const float w = expf(coherent_load_f(part, n, base + s * (D + 2) + D) - M);
-            wgt[g][s] = w;
-            L += double(coherent_load_f(part, n, base + s * (D + 2) + D + 1)) * double(w);
-        }
-        L = wave_sum(L);
-        if (ln == 0) inv_l[g] = 1.0f / float(L);
+    const int tid = threadIdx.x;
+    const bool wt = tid < G * NB;
+    const uint32_t wg = tid / NB, wj = tid % NB;
+    if (tid < G) {
+        Ms[tid] = -INFINITY;
+        Ls[tid] = 0.0;
     }
-    __syncthreads();
-    for (uint32_t e = threadIdx.x; e < G * D; e += kT) {
-        const uint32_t g = e / D, d = e % D, base = g * splits * (D + 2) + d;
-        float acc = 0.0f;
-#pragma unroll 8
-        for (uint32_t s = 0; s < ns; ++s) acc = fmaf(coherent_load_f(part, n, base + s * (D + 2)), wgt[g][s], acc);
-        out[size_t(g) * D + d] = acc * inv_l[g];
+    float acc[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) acc[e] = 0.0f;
+    for (uint32_t b0 = 0; b0 < ns; b0 += NB) {
+        const uint32_t nb = min(ns - b0, uint32_t(NB));
+        float a[E][NB];
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const uint32_t el = tid + e * kT, g = el / D, d = el % D;
+#pragma unroll
+            for (int j = 0; j < NB; ++j)
+                a[e][j] = el < G * D && uint32_t(j) < nb ? coherent_load_f(part, n, (g * splits + b0 + j) * (D + 2) + d)
+                                                         : 0.0f;
+        }
+        float mj = -INFINITY, lj = 0.0f;
+        if (wt && wj < nb) {
+            const uint32_t o = (wg * splits + b0 + wj) * (D + 2) + D;
+            mj = coherent_load_f(part, n, o);
+            lj = coherent_load_f(part, n, o + 1);
+        }
+        __syncthreads();  // Ms / Ls of the previous batch written; its wgt reads done
+        if (wt) {
+            float mb = mj;
+#pragma unroll
+            for (int o = NB / 2; o > 0; o >>= 1) mb = fmaxf(mb, __shfl_xor(mb, o));
+            const float mo = Ms[wg], mn = fmaxf(mo, mb);
+            const float w = wj < nb ? expf(mj - mn) : 0.0f;
+            double ls = double(lj) * double(w);
+#pragma unroll
+            for (int o = NB / 2; o > 0; o >>= 1) ls += __shfl_xor(ls, o);
+            wgt[wg][wj] = w;
+            if (wj == 0) {  // the group's lanes have read Ms[wg] (one wave, in order)
+                const float r = expf(mo - mn);  // 0 for the first batch (mo = -inf)
+                rs[wg] = r;
+                Ms[wg] = mn;
+                Ls[wg] = Ls[wg] * double(r) + ls;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const uint32_t el = tid + e * kT, g = min(el / D, uint32_t(G - 1));
+            float t = 0.0f;
+#pragma unroll
+            for (int j = 0; j < NB; ++j) t = fmaf(a[e][j], wgt[g][j], t);
+            acc[e] = acc[e] * rs[g] + t;
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const uint32_t el = tid + e * kT;
+        if (el < G * D) out[el] = acc[e] * (1.0f / float(Ls[el / D]));
     }
 }
 
@@ -611,7 +656,7 @@ __global__ __launch_bounds__(kT) void attention_decode_kernel(
     }
     __syncthreads();
     if (!last) return;
-    merge_chunks<D>(outp, out + size_t(kh * G) * D, G, ns, splits);
+    merge_chunks<D, G>(outp, out + size_t(kh * G) * D, ns, splits);
 }
 
 // out = x + y (out may be x)
