@@ -140,9 +140,14 @@ hipError_t launch_embed(int fmt, const void* table, const uint32_t* tokens, uint
 // launch_quantize_acts would write them, for the int8 GEMMs that read y.
 hipError_t launch_rmsnorm(const float* x, const float* w, float* y, uint32_t rows, uint32_t n, float eps,
                           hipStream_t stream, int8_t* xq = nullptr, float* xs = nullptr);
+// q is rotated in place ([T][H*D]), and k, v ([T][KH*D]) go to the caches.
+// With ld != 0 the inputs are rows of one [T][ld] buffer (the fused Q|K|V
+// projection's output): q_in, k and v point at its q, k and v columns, and
+// the rotated q is written to q ([T][H*D]).
 hipError_t launch_rope_kv(float* q, const float* k, const float* v, float* kc, float* vc, const float* cos_tab,
                           const float* sin_tab, const uint32_t* pos0, uint32_t T, uint32_t H, uint32_t KH, uint32_t D,
-                          uint32_t pairs, bool adjacent, hipStream_t stream);
+                          uint32_t pairs, bool adjacent, hipStream_t stream, uint32_t ld = 0,
+                          const float* q_in = nullptr);
 hipError_t launch_attention(const float* q, const float* kc, const float* vc, float* out, const uint32_t* pos0,
                             uint32_t T, uint32_t H, uint32_t KH, uint32_t D, uint32_t max_pos, float scale,
                             hipStream_t stream);

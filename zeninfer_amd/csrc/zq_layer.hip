@@ -114,29 +114,38 @@ __global__ __launch_bounds__(kNormT) void rmsnorm_kernel(float* __restrict__ x, 
 // position pos0 + t.  One workgroup per token.  `pairs` rotated pairs per head:
 // adjacent (x[2i], x[2i+1]) or half-split (x[i], x[i+pairs]); dimensions past
 // 2*pairs are left as they are (rope(), :317-328 of the reference runtime).
-__global__ __launch_bounds__(kT) void rope_kv_kernel(float* __restrict__ q, const float* __restrict__ k,
+__global__ __launch_bounds__(kT) void rope_kv_kernel(const float* q, float* q_out, const float* __restrict__ k,
                                                      const float* __restrict__ v, float* __restrict__ kc,
                                                      float* __restrict__ vc, const float* __restrict__ cos_tab,
                                                      const float* __restrict__ sin_tab, const uint32_t* __restrict__ pos0,
-                                                     uint32_t H, uint32_t KH, uint32_t D, uint32_t pairs, int adjacent) {
+                                                     uint32_t H, uint32_t KH, uint32_t D, uint32_t pairs, int adjacent,
+                                                     uint32_t ldq, uint32_t ldkv) {
     const uint32_t t = blockIdx.x;
     const uint32_t pos = *pos0 + t;
     const float* cs = cos_tab + size_t(pos) * pairs;
     const float* sn = sin_tab + size_t(pos) * pairs;
-    float* qt = q + size_t(t) * H * D;
-    const float* kt = k + size_t(t) * KH * D;
-    const float* vt = v + size_t(t) * KH * D;
+    const float* qt = q + size_t(t) * ldq;
+    float* qo = q_out + size_t(t) * H * D;
+    const float* kt = k + size_t(t) * ldkv;
+    const float* vt = v + size_t(t) * ldkv;
     float* kd = kc + size_t(pos) * KH * D;
     float* vd = vc + size_t(pos) * KH * D;
-    // q in place: one thread per rotated pair
+    // q (in place, or into q_out): one thread per rotated pair; elements past
+    // the rotated ones are copied when q_out is another buffer
     for (uint32_t j = threadIdx.x; j < H * pairs; j += kT) {
         const uint32_t h = j / pairs, i = j - h * pairs;
-        float* vh = qt + size_t(h) * D;
+        const float* vh = qt + size_t(h) * D;
+        float* oh = qo + size_t(h) * D;
         const uint32_t ia = adjacent ? 2 * i : i, ib = adjacent ? 2 * i + 1 : i + pairs;
         const float a = vh[ia], b = vh[ib], c = cs[i], s = sn[i];
-        vh[ia] = a * c - b * s;
-        vh[ib] = a * s + b * c;
+        oh[ia] = a * c - b * s;
+        oh[ib] = a * s + b * c;
     }
+    if (q_out != q && 2 * pairs < D)
+        for (uint32_t j = threadIdx.x; j < H * (D - 2 * pairs); j += kT) {
+            const uint32_t h = j / (D - 2 * pairs), d = 2 * pairs + (j - h * (D - 2 * pairs));
+            qo[size_t(h) * D + d] = qt[size_t(h) * D + d];
+        }
     // k into the cache: one thread per element, from the unrotated input
     for (uint32_t j = threadIdx.x; j < KH * D; j += kT) {
         const uint32_t h = j / D, d = j - h * D;
@@ -743,12 +752,13 @@ hipError_t launch_add_rmsnorm(float* x, const float* r, const float* w, float* y
 
 hipError_t launch_rope_kv(float* q, const float* k, const float* v, float* kc, float* vc, const float* cos_tab,
                           const float* sin_tab, const uint32_t* pos0, uint32_t T, uint32_t H, uint32_t KH, uint32_t D,
-                          uint32_t pairs, bool adjacent, hipStream_t stream) {
+                          uint32_t pairs, bool adjacent, hipStream_t stream, uint32_t ld, const float* q_in) {
     if (!q || !k || !v || !kc || !vc || !cos_tab || !sin_tab || !pos0 || !T || !H || !KH || !D || !pairs ||
-        pairs > D / 2 || H % KH)
+        pairs > D / 2 || H % KH || (ld && ld < (H + 2 * KH) * D) || (q_in && !ld))
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(rope_kv_kernel, dim3(T), dim3(kT), 0, stream, q, k, v, kc, vc, cos_tab, sin_tab, pos0, H, KH, D,
-                       pairs, adjacent ? 1 : 0);
+    const float* qi = q_in ? q_in : q;
+    hipLaunchKernelGGL(rope_kv_kernel, dim3(T), dim3(kT), 0, stream, qi, q, k, v, kc, vc, cos_tab, sin_tab, pos0, H, KH,
+                       D, pairs, adjacent ? 1 : 0, ld ? ld : H * D, ld ? ld : KH * D);
     return hipGetLastError();
 }
 

@@ -86,6 +86,7 @@ struct zq_model {
     float* xs = nullptr;
     float* partial = nullptr;
     float* attn_part = nullptr;  // decode attention chunk partials
+    float* qkv = nullptr;        // prefill output of the fused Q|K|V projection, [T][QW + 2 KW]
     void* argmax_part = nullptr;
 
     uint32_t cur_pos = 0;  // positions held in the cache
@@ -145,13 +146,14 @@ bool alloc_runtime(zq_model& m, std::string& e) {
     const size_t widest = std::max({E, QW, F});
     struct B { float** p; size_t n; };
     const B bufs[] = {{&m.x, T * E}, {&m.h, T * E}, {&m.q, T * QW}, {&m.k, T * KW}, {&m.v, T * KW}, {&m.att, T * QW},
-                      {&m.tmp, T * E}, {&m.gate, T * F}, {&m.up, T * F}, {&m.act, T * F}, {&m.logits, c.vocab}};
+                      {&m.tmp, T * E}, {&m.gate, T * F}, {&m.up, T * F}, {&m.act, T * F}, {&m.logits, c.vocab},
+                      {&m.qkv, T * (QW + 2 * KW)}};
     size_t total = 0;
     for (const B& b : bufs) total += align_up(b.n * 4, kAlign);
     // int8 activations + scales + split-K partials for the widest projection
     size_t partial = 0;
     for (uint32_t M = 1; M <= kPrefillChunk; ++M)
-        for (auto nk : {std::pair<size_t, size_t>{QW, E}, {KW, E}, {E, QW}, {F, E}, {E, F}})
+        for (auto nk : {std::pair<size_t, size_t>{QW, E}, {KW, E}, {QW + 2 * KW, E}, {E, QW}, {F, E}, {E, F}})
             partial = std::max({partial, zq::gemm_i8_partial_bytes(M, nk.first, nk.second),
                                 zq::gemm_f32_partial_bytes(M, nk.first, nk.second)});
     const size_t xq_bytes = align_up(T * widest, kAlign), xs_bytes = align_up(T * widest / 32 * 4, kAlign);
@@ -232,6 +234,16 @@ hipError_t project(zq_model& m, const Weight& w, const float* X, float* Y, uint3
 
 bool int8_ok(int fmt) { return fmt == zq::kQ8_0 || fmt == zq::kQ4_0; }
 
+// q, k and v of one type stored back to back: one [QW + 2 KW] x E weight.
+bool qkv_packed(const Layer& L, Weight& qkv) {
+    const size_t rb = zq::row_bytes(L.q.fmt, L.q.cols);
+    if (L.k.fmt != L.q.fmt || L.v.fmt != L.q.fmt || L.k.cols != L.q.cols || L.v.cols != L.q.cols ||
+        L.k.p != L.q.p + size_t(L.q.rows) * rb || L.v.p != L.k.p + size_t(L.k.rows) * rb)
+        return false;
+    qkv = Weight{L.q.p, L.q.fmt, L.q.rows + L.k.rows + L.v.rows, L.q.cols};
+    return true;
+}
+
 // Whether the projections ws read their input as int8 activations (prefill
 // in ZQ_PREFILL_INT8 mode, formats with an int8 GEMM).
 bool int8_inputs(const zq_model& m, std::initializer_list<const Weight*> ws) {
@@ -286,9 +298,14 @@ hipError_t enqueue_layers(zq_model& m, uint32_t T) {
         } else {
             bool qz = qin({&L.q, &L.k, &L.v});  // h's int8 activations came with its norm
             if (!qz) HIPCHK(quantize_for(m, {&L.q, &L.k, &L.v}, m.h, T, E, qz));
-            HIPCHK(project(m, L.q, m.h, m.q, T, qz));
-            HIPCHK(project(m, L.k, m.h, m.k, T, qz));
-            HIPCHK(project(m, L.v, m.h, m.v, T, qz));
+            Weight qkv;
+            if (qkv_packed(L, qkv)) {
+                HIPCHK(project(m, qkv, m.h, m.qkv, T, qz));
+            } else {
+                HIPCHK(project(m, L.q, m.h, m.q, T, qz));
+                HIPCHK(project(m, L.k, m.h, m.k, T, qz));
+                HIPCHK(project(m, L.v, m.h, m.v, T, qz));
+            }
         }
         if (T == 1) {
             HIPCHK(zq::launch_attention_decode(m.q, m.k, m.v, L.kc, L.vc, m.cos_tab, m.sin_tab, m.attn_part, m.att,
@@ -297,8 +314,14 @@ hipError_t enqueue_layers(zq_model& m, uint32_t T) {
             zq::GemvTask t = {L.o.p, m.tmp, E};
             HIPCHK(zq::launch_gemv(L.o.fmt, &t, 1, m.att, QW, m.stream));
         } else {
-            HIPCHK(zq::launch_rope_kv(m.q, m.k, m.v, L.kc, L.vc, m.cos_tab, m.sin_tab, m.pos_dev, T, c.heads,
-                                      c.kv_heads, c.head_dim, m.pairs, true, m.stream));
+            Weight qkv;
+            if (qkv_packed(L, qkv))
+                HIPCHK(zq::launch_rope_kv(m.q, m.qkv + QW, m.qkv + QW + KW, L.kc, L.vc, m.cos_tab, m.sin_tab, m.pos_dev,
+                                          T, c.heads, c.kv_heads, c.head_dim, m.pairs, true, m.stream, QW + 2 * KW,
+                                          m.qkv));
+            else
+                HIPCHK(zq::launch_rope_kv(m.q, m.k, m.v, L.kc, L.vc, m.cos_tab, m.sin_tab, m.pos_dev, T, c.heads,
+                                          c.kv_heads, c.head_dim, m.pairs, true, m.stream));
             HIPCHK(zq::launch_attention(m.q, L.kc, L.vc, m.att, m.pos_dev, T, c.heads, c.kv_heads, c.head_dim,
                                         c.max_positions, m.attn_scale, m.stream));
             bool qz;
@@ -532,7 +555,7 @@ int zq_model_load_gguf(const zq_gguf* g, uint32_t max_positions, zq_model_config
     const uint32_t E = c.embedding, QW = c.heads * c.head_dim, KW = c.kv_heads * c.head_dim, F = c.ffn;
 
     // collect every tensor with its expected shape
-    struct Need { std::string name; uint32_t rows, cols; Weight* w; const float** f32; };
+    struct Need { std::string name; uint32_t rows, cols; Weight* w; const float** f32; bool qkv_head = false; };
     std::vector<Need> needs;
     needs.push_back({"token_embd.weight", c.vocab, E, &m->embd, nullptr});
     needs.push_back({tied ? "token_embd.weight" : "output.weight", c.vocab, E, &m->out, nullptr});
@@ -542,7 +565,7 @@ int zq_model_load_gguf(const zq_gguf* g, uint32_t max_positions, zq_model_config
         Layer& L = m->layers[l];
         needs.push_back({p + "attn_norm.weight", 1, E, nullptr, &L.attn_norm});
         needs.push_back({p + "ffn_norm.weight", 1, E, nullptr, &L.ffn_norm});
-        needs.push_back({p + "attn_q.weight", QW, E, &L.q, nullptr});
+        needs.push_back({p + "attn_q.weight", QW, E, &L.q, nullptr, true});
         needs.push_back({p + "attn_k.weight", KW, E, &L.k, nullptr});
         needs.push_back({p + "attn_v.weight", KW, E, &L.v, nullptr});
         needs.push_back({p + "attn_output.weight", E, QW, &L.o, nullptr});
@@ -551,6 +574,7 @@ int zq_model_load_gguf(const zq_gguf* g, uint32_t max_positions, zq_model_config
         needs.push_back({p + "ffn_down.weight", E, F, &L.down, nullptr});
     }
     std::vector<zq_gguf_tensor> ts(needs.size());
+    std::vector<size_t> advance(needs.size());
     size_t arena = 0;
     for (size_t i = 0; i < needs.size(); ++i) {
         const Need& n = needs[i];
@@ -573,8 +597,17 @@ int zq_model_load_gguf(const zq_gguf* g, uint32_t max_positions, zq_model_config
                 return fail("output projection must be Q8_0, Q4_0, Q4_K, Q5_K or Q6_K", ZQ_DECLINED);
             }
         }
-        arena += align_up(size_t(t.byte_size) + ZQ_WEIGHT_TAIL_PAD, kAlign);
+        advance[i] = align_up(size_t(t.byte_size) + ZQ_WEIGHT_TAIL_PAD, kAlign);
     }
+    // A layer's q, k and v of one type sit back to back (no padding between
+    // them), so prefill runs them as one [QW + 2 KW] x E projection.
+    for (size_t i = 0; i + 2 < needs.size(); ++i)
+        if (needs[i].qkv_head && ts[i + 1].ggml_type == ts[i].ggml_type && ts[i + 2].ggml_type == ts[i].ggml_type &&
+            ts[i].byte_size % 16 == 0 && ts[i + 1].byte_size % 16 == 0) {
+            advance[i] = size_t(ts[i].byte_size);
+            advance[i + 1] = size_t(ts[i + 1].byte_size);
+        }
+    for (size_t a : advance) arena += a;
     void* base;
     if (!dev_alloc(*m, &base, arena)) { delete m; return fail("device allocation failed (weights)", ZQ_ERR_OOM); }
     m->weight_bytes = arena;
@@ -588,7 +621,7 @@ int zq_model_load_gguf(const zq_gguf* g, uint32_t max_positions, zq_model_config
         const Need& n = needs[i];
         if (n.w) *n.w = Weight{p, int(t.ggml_type), n.rows, n.cols};
         if (n.f32) *n.f32 = reinterpret_cast<const float*>(p);
-        p += align_up(size_t(t.byte_size) + ZQ_WEIGHT_TAIL_PAD, kAlign);
+        p += advance[i];
     }
     c.weight_format = m->layers.empty() ? m->out.fmt : m->layers[0].q.fmt;
     if (!alloc_runtime(*m, e)) { delete m; return fail(e, ZQ_ERR_OOM); }
@@ -613,14 +646,20 @@ int zq_model_create_synthetic(const zq_model_config* cfg, uint64_t seed, zq_mode
     std::string e;
     if (!init_common(*m, e)) { delete m; set_err(err, err_cap, e); return ZQ_ERR_NO_DEVICE; }
     const uint32_t E = c.embedding, QW = c.heads * c.head_dim, KW = c.kv_heads * c.head_dim, F = c.ffn;
-    struct W { Weight* w; uint32_t rows, cols; };
+    // q and k are followed by k and v without padding (one Q|K|V weight)
+    struct W { Weight* w; uint32_t rows, cols; bool packed = false; };
     std::vector<W> ws = {{&m->embd, c.vocab, E}, {&m->out, c.vocab, E}};
     for (auto& L : m->layers)
-        for (auto x : {W{&L.q, QW, E}, W{&L.k, KW, E}, W{&L.v, KW, E}, W{&L.o, E, QW}, W{&L.gate, F, E},
+        for (auto x : {W{&L.q, QW, E, true}, W{&L.k, KW, E, true}, W{&L.v, KW, E}, W{&L.o, E, QW}, W{&L.gate, F, E},
                        W{&L.up, F, E}, W{&L.down, E, F}})
             ws.push_back(x);
+    auto advance = [](const W& w) {
+        return w.packed && (size_t(w.rows) * zq::row_bytes(zq::kQ8_0, w.cols)) % 16 == 0
+                   ? size_t(w.rows) * zq::row_bytes(zq::kQ8_0, w.cols)
+                   : align_up(zq_weight_bytes(zq::kQ8_0, w.rows, w.cols), kAlign);
+    };
     size_t arena = align_up(size_t(E) * 4, kAlign);  // one shared unit norm vector
-    for (const W& w : ws) arena += align_up(zq_weight_bytes(zq::kQ8_0, w.rows, w.cols), kAlign);
+    for (const W& w : ws) arena += advance(w);
     void* base;
     if (!dev_alloc(*m, &base, arena)) { delete m; set_err(err, err_cap, "device allocation failed (weights)"); return ZQ_ERR_OOM; }
     m->weight_bytes = arena;
@@ -635,7 +674,7 @@ int zq_model_create_synthetic(const zq_model_config* cfg, uint64_t seed, zq_mode
     for (const W& w : ws) {
         *w.w = Weight{p, zq::kQ8_0, w.rows, w.cols};
         if (zq::launch_synth_weights(zq::kQ8_0, s++, p, w.rows, w.cols, m->stream) != hipSuccess) { delete m; return ZQ_ERR_HIP; }
-        p += align_up(zq_weight_bytes(zq::kQ8_0, w.rows, w.cols), kAlign);
+        p += advance(w);
     }
     if (hipStreamSynchronize(m->stream) != hipSuccess) { delete m; return ZQ_ERR_HIP; }
     if (!alloc_runtime(*m, e)) { delete m; set_err(err, err_cap, e); return ZQ_ERR_OOM; }
