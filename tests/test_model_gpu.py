@@ -105,11 +105,15 @@ def test_f32_generate_matches_reference(tiny_path, reference, zq):
     m.close()
 
 
-def test_int8_prefill_close_to_reference(tiny_path, reference, zq):
+@pytest.mark.parametrize("plen", [16, 120])
+def test_int8_prefill_close_to_reference(tiny_path, reference, zq, plen):
+    """16 tokens run the skinny int8 GEMM; 120 the 128-token tile, with q|k|v
+    as one projection."""
     from zeninfer_amd.model import PREFILL_INT8
+    prompt = PROMPT if plen == 16 else [int(t) for t in np.random.default_rng(9).integers(0, SHAPE.vocab, plen)]
     m = load(tiny_path, PREFILL_INT8)
-    nxt, lg = m.prefill(PROMPT)
-    lr = reference.prefill(PROMPT, capacity=128)
+    nxt, lg = m.prefill(prompt)
+    lr = reference.prefill(prompt, capacity=128)
     ok, err, scale = close_to(lg, lr, 5e-2)
     corr = float(np.corrcoef(lg, lr)[0, 1])
     print(f"int8 prefill: max err {err:.3e} of {scale:.3f}, correlation {corr:.6f}")
