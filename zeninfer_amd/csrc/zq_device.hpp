@@ -235,6 +235,28 @@ __device__ __forceinline__ void quantize_lane_block32(float v, int8_t* q_out, fl
     *q_out = int8_t(round_half_away(q));
 }
 
+// The same quantiser with four consecutive elements per lane: the 8
+// consecutive lanes of an aligned group hold one block, q_out receives the
+// lane's 4 bytes (4-byte aligned).  Every lane of the wave must call it.
+__device__ __forceinline__ void quantize_lane4_block32(float4 v, int8_t* q_out, float* d_out) {
+    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    amax = fmaxf(amax, __shfl_xor(amax, 1));
+    amax = fmaxf(amax, __shfl_xor(amax, 2));
+    amax = fmaxf(amax, __shfl_xor(amax, 4));
+    const float d = amax > 0.0f ? amax / 127.0f : 0.0f;
+    const float inv = d > 0.0f ? 1.0f / d : 0.0f;
+    if ((threadIdx.x & 7u) == 0) *d_out = d;
+    const float e[4] = {v.x, v.y, v.z, v.w};
+    uint32_t w = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        float q = e[k] * inv;
+        q = q > 127.0f ? 127.0f : (q < -127.0f ? -127.0f : q);
+        w |= (uint32_t(round_half_away(q)) & 0xffu) << (8 * k);
+    }
+    *reinterpret_cast<uint32_t*>(q_out) = w;
+}
+
 // Cross-workgroup hand-off inside one launch (workgroups run on 8 XCDs with
 // private L2s): the producer writes with agent-scope stores (through to the
 // device-coherent level) and waits for them (s_waitcnt) before it signals;

@@ -110,6 +110,60 @@ __global__ __launch_bounds__(kNormT) void rmsnorm_kernel(float* __restrict__ x, 
     for (uint32_t i = threadIdx.x; i < n; i += kNormT) yr[i] = xr[i] * inv * w[i];
 }
 
+// rmsnorm_kernel for n % 4 == 0, n <= 4 * kNormV * kNormT, 16-byte aligned
+// rows: every load of a row (x, r, w) is issued up front as float4, the row
+// stays in registers across the reduction, so the row costs one memory
+// round trip.  Same arithmetic per element (the double sum of squares in
+// another order).
+constexpr int kNormV = 4;
+template <bool ADD>
+__global__ __launch_bounds__(kNormT) void rmsnorm4_kernel(float* __restrict__ x, const float* __restrict__ r,
+                                                          const float* __restrict__ w, float* __restrict__ y, uint32_t n,
+                                                          float eps, int8_t* __restrict__ xq, float* __restrict__ xs) {
+    __shared__ double red[kNormT / 64];
+    const uint32_t n4 = n / 4;
+    float4* xr = reinterpret_cast<float4*>(x + size_t(blockIdx.x) * n);
+    float4* yr = reinterpret_cast<float4*>(y + size_t(blockIdx.x) * n);
+    const float4* rr = ADD ? reinterpret_cast<const float4*>(r + size_t(blockIdx.x) * n) : nullptr;
+    const float4* w4 = reinterpret_cast<const float4*>(w);
+    float4 v[kNormV], b[ADD ? kNormV : 1], wv[kNormV];
+#pragma unroll
+    for (int j = 0; j < kNormV; ++j) {
+        const uint32_t i = threadIdx.x + j * kNormT;
+        const bool live = i < n4;
+        v[j] = live ? xr[i] : make_float4(0, 0, 0, 0);
+        if constexpr (ADD) b[j] = live ? rr[i] : make_float4(0, 0, 0, 0);
+        wv[j] = live ? w4[i] : make_float4(0, 0, 0, 0);
+    }
+    double ss = 0.0;
+#pragma unroll
+    for (int j = 0; j < kNormV; ++j) {
+        const uint32_t i = threadIdx.x + j * kNormT;
+        if constexpr (ADD) {
+            v[j] = make_float4(v[j].x + b[j].x, v[j].y + b[j].y, v[j].z + b[j].z, v[j].w + b[j].w);
+            if (i < n4) xr[i] = v[j];
+        }
+        ss += double(v[j].x) * double(v[j].x);
+        ss += double(v[j].y) * double(v[j].y);
+        ss += double(v[j].z) * double(v[j].z);
+        ss += double(v[j].w) * double(v[j].w);
+    }
+    ss = block_sum_d(ss, red);
+    const float inv = 1.0f / sqrtf(float(ss / double(n)) + eps);
+    int8_t* qr = xq ? xq + size_t(blockIdx.x) * n : nullptr;
+    float* sr = xq ? xs + size_t(blockIdx.x) * (n / 32) : nullptr;
+#pragma unroll
+    for (int j = 0; j < kNormV; ++j) {
+        const uint32_t i = threadIdx.x + j * kNormT;
+        if (j * kNormT >= n4) break;  // uniform: no element of this round is live
+        const float4 o = make_float4(v[j].x * inv * wv[j].x, v[j].y * inv * wv[j].y, v[j].z * inv * wv[j].z,
+                                     v[j].w * inv * wv[j].w);
+        if (i < n4) yr[i] = o;
+        // n % 32 == 0 with xq: a round's live lanes are whole 8-lane blocks
+        if (qr && i < n4) quantize_lane4_block32(o, qr + 4 * i, sr + i / 8);
+    }
+}
+
 // RoPE on q (in place) and k, then k and v appended to the caches at
 // position pos0 + t.  One workgroup per token.  `pairs` rotated pairs per head:
 // adjacent (x[2i], x[2i+1]) or half-split (x[i], x[i+pairs]); dimensions past
@@ -735,18 +789,31 @@ hipError_t launch_embed(int fmt, const void* table, const uint32_t* tokens, uint
     return hipGetLastError();
 }
 
+static bool norm4_ok(const void* x, const void* r, const void* w, const void* y, const void* xq, uint32_t n) {
+    auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    return n % 4 == 0 && n <= uint32_t(4 * kNormV * kNormT) && a16(x) && a16(r) && a16(w) && a16(y) &&
+           (reinterpret_cast<uintptr_t>(xq) & 3u) == 0;
+}
+
 hipError_t launch_rmsnorm(const float* x, const float* w, float* y, uint32_t rows, uint32_t n, float eps,
                           hipStream_t stream, int8_t* xq, float* xs) {
     if (!x || !w || !y || !rows || !n || (xq && (!xs || n % 32))) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(rmsnorm_kernel<false>, dim3(rows), dim3(kNormT), 0, stream, const_cast<float*>(x), nullptr, w, y,
-                       n, eps, xq, xs);
+    if (norm4_ok(x, nullptr, w, y, xq, n))
+        hipLaunchKernelGGL(rmsnorm4_kernel<false>, dim3(rows), dim3(kNormT), 0, stream, const_cast<float*>(x), nullptr, w,
+                           y, n, eps, xq, xs);
+    else
+        hipLaunchKernelGGL(rmsnorm_kernel<false>, dim3(rows), dim3(kNormT), 0, stream, const_cast<float*>(x), nullptr, w,
+                           y, n, eps, xq, xs);
     return hipGetLastError();
 }
 
 hipError_t launch_add_rmsnorm(float* x, const float* r, const float* w, float* y, uint32_t rows, uint32_t n, float eps,
                               hipStream_t stream, int8_t* xq, float* xs) {
     if (!x || !r || !w || !y || !rows || !n || (xq && (!xs || n % 32))) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(rmsnorm_kernel<true>, dim3(rows), dim3(kNormT), 0, stream, x, r, w, y, n, eps, xq, xs);
+    if (norm4_ok(x, r, w, y, xq, n))
+        hipLaunchKernelGGL(rmsnorm4_kernel<true>, dim3(rows), dim3(kNormT), 0, stream, x, r, w, y, n, eps, xq, xs);
+    else
+        hipLaunchKernelGGL(rmsnorm_kernel<true>, dim3(rows), dim3(kNormT), 0, stream, x, r, w, y, n, eps, xq, xs);
     return hipGetLastError();
 }
 

@@ -127,6 +127,20 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const float* __restr
     }
 }
 
+// The same for n % 4 == 0 and 16-byte aligned operands, four elements per
+// lane (float4 loads and stores; 8 lanes per quantiser block).
+__global__ __launch_bounds__(kThreads) void silu_mul4_kernel(const float4* __restrict__ g, const float4* __restrict__ u,
+                                                             float4* __restrict__ o, size_t n4, int8_t* __restrict__ xq,
+                                                             float* __restrict__ xs) {
+    const size_t i = size_t(blockIdx.x) * kThreads + threadIdx.x;
+    if (i >= n4) return;  // n % 32 == 0 with xq: whole 8-lane blocks leave together
+    const float4 a = g[i], b = u[i];
+    auto f = [](float gv, float uv) { return gv / (1.0f + expf(-gv)) * uv; };
+    const float4 v = make_float4(f(a.x, b.x), f(a.y, b.y), f(a.z, b.z), f(a.w, b.w));
+    o[i] = v;
+    if (xq) quantize_lane4_block32(v, xq + 4 * i, xs + i / 8);
+}
+
 }  // namespace
 
 namespace {
@@ -199,6 +213,14 @@ hipError_t launch_mfma_probe(uint64_t* out, uint32_t wgs, uint32_t iters, hipStr
 hipError_t launch_silu_mul(const float* gate, const float* up, float* out, size_t n, hipStream_t stream, int8_t* xq,
                            float* xs) {
     if (!gate || !up || !out || !n || (xq && (!xs || n % 32))) return hipErrorInvalidValue;
+    auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    if (n % 4 == 0 && a16(gate) && a16(up) && a16(out) && (reinterpret_cast<uintptr_t>(xq) & 3u) == 0) {
+        const size_t n4 = n / 4;
+        hipLaunchKernelGGL(silu_mul4_kernel, dim3(static_cast<uint32_t>((n4 + kThreads - 1) / kThreads)), dim3(kThreads),
+                           0, stream, reinterpret_cast<const float4*>(gate), reinterpret_cast<const float4*>(up),
+                           reinterpret_cast<float4*>(out), n4, xq, xs);
+        return hipGetLastError();
+    }
     const dim3 grid(static_cast<uint32_t>((n + kThreads - 1) / kThreads));
     hipLaunchKernelGGL(silu_mul_kernel, grid, dim3(kThreads), 0, stream, gate, up, out, n, xq, xs);
     return hipGetLastError();
