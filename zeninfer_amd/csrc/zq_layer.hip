@@ -817,6 +817,66 @@ hipError_t launch_add_rmsnorm(float* x, const float* r, const float* w, float* y
     return hipGetLastError();
 }
 
+// rope_kv_kernel with adjacent pairs, float4 accesses (a float4 is two whole
+// pairs: 2 * pairs % 4 == 0) and every load of a token issued up front: q
+// (H * D <= 4 * kRopeQV * kT) and k, v (KH * D <= 4 * kRopeKV * kT).  The
+// same expressions per element.
+constexpr int kRopeQV = 8, kRopeKV = 2;
+__global__ __launch_bounds__(kT) void rope_kv4_kernel(const float* q, float* q_out, const float* __restrict__ k,
+                                                      const float* __restrict__ v, float* __restrict__ kc,
+                                                      float* __restrict__ vc, const float* __restrict__ cos_tab,
+                                                      const float* __restrict__ sin_tab,
+                                                      const uint32_t* __restrict__ pos0, uint32_t H, uint32_t KH,
+                                                      uint32_t D, uint32_t pairs, uint32_t ldq, uint32_t ldkv) {
+    const uint32_t t = blockIdx.x;
+    const uint32_t pos = *pos0 + t;
+    const float* cs = cos_tab + size_t(pos) * pairs;
+    const float* sn = sin_tab + size_t(pos) * pairs;
+    const float4* qt = reinterpret_cast<const float4*>(q + size_t(t) * ldq);
+    float4* qo = reinterpret_cast<float4*>(q_out + size_t(t) * H * D);
+    const float4* kt = reinterpret_cast<const float4*>(k + size_t(t) * ldkv);
+    const float4* vt = reinterpret_cast<const float4*>(v + size_t(t) * ldkv);
+    float4* kd = reinterpret_cast<float4*>(kc + size_t(pos) * KH * D);
+    float4* vd = reinterpret_cast<float4*>(vc + size_t(pos) * KH * D);
+    const uint32_t nq = H * D / 4, nk = KH * D / 4, D4 = D / 4, rot4 = pairs / 2;  // float4s rotated per head
+    float4 qv[kRopeQV], kv[kRopeKV], vv[kRopeKV];
+    float4 qc[kRopeQV], kcs[kRopeKV];  // (cos i, cos i+1, sin i, sin i+1)
+    auto factors = [&](uint32_t d4) {
+        const float2 c = *reinterpret_cast<const float2*>(cs + 2 * d4);
+        const float2 s = *reinterpret_cast<const float2*>(sn + 2 * d4);
+        return make_float4(c.x, c.y, s.x, s.y);
+    };
+#pragma unroll
+    for (int j = 0; j < kRopeQV; ++j) {
+        const uint32_t i = threadIdx.x + j * kT, d4 = i % D4;
+        qv[j] = i < nq ? qt[i] : make_float4(0, 0, 0, 0);
+        qc[j] = i < nq && d4 < rot4 ? factors(d4) : make_float4(1, 1, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < kRopeKV; ++j) {
+        const uint32_t i = threadIdx.x + j * kT, d4 = i % D4;
+        kv[j] = i < nk ? kt[i] : make_float4(0, 0, 0, 0);
+        vv[j] = i < nk ? vt[i] : make_float4(0, 0, 0, 0);
+        kcs[j] = i < nk && d4 < rot4 ? factors(d4) : make_float4(1, 1, 0, 0);
+    }
+    auto rot = [](float4 x, float4 f) {  // pairs (x, y) and (z, w)
+        return make_float4(x.x * f.x - x.y * f.z, x.x * f.z + x.y * f.x, x.z * f.y - x.w * f.w, x.z * f.w + x.w * f.y);
+    };
+#pragma unroll
+    for (int j = 0; j < kRopeQV; ++j) {
+        const uint32_t i = threadIdx.x + j * kT;
+        if (i < nq) qo[i] = i % D4 < rot4 ? rot(qv[j], qc[j]) : qv[j];
+    }
+#pragma unroll
+    for (int j = 0; j < kRopeKV; ++j) {
+        const uint32_t i = threadIdx.x + j * kT;
+        if (i < nk) {
+            kd[i] = i % D4 < rot4 ? rot(kv[j], kcs[j]) : kv[j];
+            vd[i] = vv[j];
+        }
+    }
+}
+
 hipError_t launch_rope_kv(float* q, const float* k, const float* v, float* kc, float* vc, const float* cos_tab,
                           const float* sin_tab, const uint32_t* pos0, uint32_t T, uint32_t H, uint32_t KH, uint32_t D,
                           uint32_t pairs, bool adjacent, hipStream_t stream, uint32_t ld, const float* q_in) {
@@ -824,6 +884,15 @@ hipError_t launch_rope_kv(float* q, const float* k, const float* v, float* kc, f
         pairs > D / 2 || H % KH || (ld && ld < (H + 2 * KH) * D) || (q_in && !ld))
         return hipErrorInvalidValue;
     const float* qi = q_in ? q_in : q;
+    const uint32_t ldq = ld ? ld : H * D, ldkv = ld ? ld : KH * D;
+    auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    if (adjacent && pairs % 2 == 0 && D % 4 == 0 && ldq % 4 == 0 && ldkv % 4 == 0 && H * D <= 4u * kRopeQV * kT &&
+        KH * D <= 4u * kRopeKV * kT && a16(qi) && a16(q) && a16(k) && a16(v) && a16(kc) && a16(vc) && a16(cos_tab) &&
+        a16(sin_tab)) {
+        hipLaunchKernelGGL(rope_kv4_kernel, dim3(T), dim3(kT), 0, stream, qi, q, k, v, kc, vc, cos_tab, sin_tab, pos0, H,
+                           KH, D, pairs, ldq, ldkv);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(rope_kv_kernel, dim3(T), dim3(kT), 0, stream, qi, q, k, v, kc, vc, cos_tab, sin_tab, pos0, H, KH,
                        D, pairs, adjacent ? 1 : 0, ld ? ld : H * D, ld ? ld : KH * D);
     return hipGetLastError();
