@@ -437,6 +437,308 @@ __global__ __launch_bounds__(kT) void attention_prefill_kernel(const float* __re
     }
 }
 
+// The same attention with the products on the f16 MFMA
+// (v_mfma_f32_32x32x16_f16, 16x the fp32 MFMA rate) at fp32-level accuracy,
+// computed transposed so the softmax stays in registers:
+//  * every operand x is scaled by a power of two 2^e (exact) so max |x| lies
+//    in [2^14, 2^15) -- per query row, per K tile, per V tile, and P (in
+//    [0, 1]) by 2^14 -- then split into h = f16(x) and l = f16(x - h) (x - h
+//    is exact in fp32); a product is h_a h_b + h_a l_b + l_a h_b (the dropped
+//    l_a l_b is below 2^-22 of the operands' maxima), accumulated in fp32, and
+//    the scales come off exactly;
+//  * S^T = K Q^T: a lane holds 16 scores of its query, so the row max and
+//    sum need one cross-half exchange, and P^T is the B operand of
+//    O^T = V^T P^T straight from the lane's registers (the MFMA's k slots
+//    take the keys in the order the S^T accumulator holds them; V^T is read
+//    in that order, two 4-key runs per operand);
+//  * wave w takes query rows 32 (w & 1) .. + 31 of the tile and keys
+//    32 (w >> 1) .. + 31 of every 64-key tile, with its own running max, sum
+//    and O; the two waves of a row set merge at the end.
+// K is staged row-major and V transposed ([column][key], 8 keys of one
+// column per lane load group), both as f16 pairs; two barriers per key tile.
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_attn_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float pow2f(int e) { return __int_as_float((e + 127) << 23); }
+// exponent e with max |x| * 2^e in [2^14, 2^15); 0 for max 0
+__device__ __forceinline__ int split_exp(float amax) {
+    if (!(amax > 0.0f)) return 0;
+    return min(max(15 - __builtin_amdgcn_frexp_expf(amax), -100), 100);
+}
+// element i of h and l: h = f16(x), l = f16(x - h)
+template <class V>
+__device__ __forceinline__ void split_h(float x, V& h, V& l, int i) {
+    const _Float16 a = _Float16(x);
+    h[i] = a;
+    l[i] = _Float16(x - float(a));
+}
+constexpr int kFHP(int D) { return D + 8; }  // halves per padded K (and Q staging) row
+constexpr int kFKP = kFKeys + 8;             // halves per padded V^T row
+constexpr size_t attention_prefill_t_lds(int D) {
+    return size_t(2) * kFKeys * kFHP(D) * 2 + size_t(2) * D * kFKP * 2;
+}
+
+template <int D>
+__global__ __launch_bounds__(kT) void attention_prefill_t_kernel(const float* __restrict__ q, const float* __restrict__ kc,
+                                                                 const float* __restrict__ vc, float* __restrict__ out,
+                                                                 const uint32_t* __restrict__ pos0_ptr, uint32_t T,
+                                                                 uint32_t H, uint32_t KH, float scale) {
+    constexpr int HP = kFHP(D), KP = kFKP;
+    constexpr int NT = D / 32;  // 32-row O^T tiles (head-dim blocks)
+    constexpr int KS = D / 16;  // k-steps of S^T
+    constexpr int RL = D / 4;   // lanes per row in the float4 row layout (16 or 32)
+    extern __shared__ __align__(16) uint8_t fsm_raw[];
+    _Float16* khi = reinterpret_cast<_Float16*>(fsm_raw);  // [64][HP]
+    _Float16* klo = khi + kFKeys * HP;
+    _Float16* vth = klo + kFKeys * HP;                      // [D][KP]
+    _Float16* vtl = vth + D * KP;
+    float* mrg = reinterpret_cast<float*>(fsm_raw);         // end-of-kernel merge, over K and V
+    static_assert(size_t(2) * 64 * (NT * 16 + 2) * 4 <= attention_prefill_t_lds(D), "merge area fits");
+    __shared__ float inv_q[kFRows], kred[kT / 64], vred[kT / 64];
+    const uint32_t G = H / KH, TQ = kFRows / G;
+    const uint32_t kh = blockIdx.x, t0 = blockIdx.y * TQ;
+    const uint32_t pos0 = *pos0_ptr;
+    const uint32_t KW = KH * D;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l32 = lane & 31, lh = lane >> 5;
+    const int qh = wave & 1, kh2 = wave >> 1;
+    const uint32_t qrow = 32 * qh + l32;  // this lane's query row of the tile
+    const uint32_t qt = qrow % TQ;        // its token offset
+
+    // ---- Q: per-row scale, split, staged over the K area, operands into registers ----
+    {
+        _Float16* qhi = khi;
+        _Float16* qlo = klo;
+        constexpr int QL = kFRows * D / 4 / kT;
+        float4 qv[QL];
+#pragma unroll
+        for (int j = 0; j < QL; ++j) {
+            const uint32_t i = tid + j * kT, r = (4 * i) / D, d = (4 * i) % D;
+            const uint32_t g = r / TQ, t = r % TQ;
+            qv[j] = t0 + t < T ? *reinterpret_cast<const float4*>(q + (size_t(t0 + t) * H + kh * G + g) * D + d)
+                               : make_float4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < QL; ++j) {
+            const uint32_t i = tid + j * kT, r = (4 * i) / D, d = (4 * i) % D;
+            float m = fmaxf(fmaxf(fabsf(qv[j].x), fabsf(qv[j].y)), fmaxf(fabsf(qv[j].z), fabsf(qv[j].w)));
+#pragma unroll
+            for (int o = RL / 2; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+            const int e = split_exp(m);
+            const float f = pow2f(e);
+            if (d == 0) inv_q[r] = pow2f(-e);
+            h4_t h, l;
+            split_h(qv[j].x * f, h, l, 0);
+            split_h(qv[j].y * f, h, l, 1);
+            split_h(qv[j].z * f, h, l, 2);
+            split_h(qv[j].w * f, h, l, 3);
+            *reinterpret_cast<h4_t*>(qhi + r * HP + d) = h;
+            *reinterpret_cast<h4_t*>(qlo + r * HP + d) = l;
+        }
+    }
+    __syncthreads();
+    h8_t bqh[KS], bql[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        bqh[ks] = *reinterpret_cast<const h8_t*>(khi + qrow * HP + ks * 16 + 8 * lh);
+        bql[ks] = *reinterpret_cast<const h8_t*>(klo + qrow * HP + ks * 16 + 8 * lh);
+    }
+    const float iq2 = inv_q[qrow];
+
+    v16f_t o[NT];
+#pragma unroll
+    for (int n = 0; n < NT; ++n)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) o[n][v] = 0.0f;
+    float m_run = -INFINITY, l_run = 0.0f, fv_prev = 1.0f;
+
+    const uint32_t nkeys = pos0 + min(t0 + TQ, T);  // keys any row of the tile sees
+    constexpr int KVL = kFKeys * D / 4 / kT;
+    constexpr int VG = kFKeys * D / kT / 8;  // 8-key groups per thread
+    constexpr int VGS = kT / D;              // threads per column
+    constexpr int KRJ = kT * 4 / D;          // K rows per float4 round
+    const uint32_t vcol = tid % D, vgi = tid / D;
+    const uint32_t koff = ((tid * 4 / D) * KW + (tid * 4) % D) * 4;  // byte offsets within a tile
+    const uint32_t voff = (vgi * 8 * KW + vcol) * 4;
+    float4 kr4[KVL];
+    float vr[VG][8];
+    // Buffer loads bounded to the tile's live rows: rows past the last key
+    // read 0 (no request), so no address clamps and no zeroing.
+    auto load_tile = [&](uint32_t k0) {
+        const uint32_t rows = min(nkeys - k0, uint32_t(kFKeys));
+        const int bytes = int(((rows - 1) * KW + D) * 4);
+        const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(kc + size_t(k0) * KW + size_t(kh) * D), 0, bytes, 0x00020000);
+        const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(vc + size_t(k0) * KW + size_t(kh) * D), 0, bytes, 0x00020000);
+#pragma unroll
+        for (int j = 0; j < KVL; ++j) {
+            const u32x4_attn_t t = __builtin_amdgcn_raw_buffer_load_b128(krs, koff + uint32_t(j * KRJ) * KW * 4, 0, 0);
+            kr4[j] = make_float4(__uint_as_float(t.x), __uint_as_float(t.y), __uint_as_float(t.z), __uint_as_float(t.w));
+        }
+#pragma unroll
+        for (int g = 0; g < VG; ++g)
+#pragma unroll
+            for (int c = 0; c < 8; ++c)
+                vr[g][c] = __uint_as_float(
+                    __builtin_amdgcn_raw_buffer_load_b32(vrs, voff + uint32_t(g * VGS * 8 + c) * KW * 4, 0, 0));
+    };
+    load_tile(0);
+    for (uint32_t k0 = 0; k0 < nkeys; k0 += kFKeys) {
+        // the K and V tiles' maxima, for their scales
+        float vm = 0.0f, km = 0.0f;
+#pragma unroll
+        for (int g = 0; g < VG; ++g)
+#pragma unroll
+            for (int c = 0; c < 8; ++c) vm = fmaxf(vm, fabsf(vr[g][c]));
+#pragma unroll
+        for (int j = 0; j < KVL; ++j)
+            km = fmaxf(km, fmaxf(fmaxf(fabsf(kr4[j].x), fabsf(kr4[j].y)), fmaxf(fabsf(kr4[j].z), fabsf(kr4[j].w))));
+        vm = wave_max(vm);
+        km = wave_max(km);
+        if (lane == 0) {
+            vred[wave] = vm;
+            kred[wave] = km;
+        }
+        __syncthreads();  // the previous tile's readers are done (and the Q operands read); maxima complete
+        float vmax = vred[0], kmax = kred[0];
+#pragma unroll
+        for (int w = 1; w < kT / 64; ++w) {
+            vmax = fmaxf(vmax, vred[w]);
+            kmax = fmaxf(kmax, kred[w]);
+        }
+        const int ev = split_exp(vmax), ek = split_exp(kmax);
+        const float fv = pow2f(ev), f = pow2f(ek), ik = pow2f(-ek);
+#pragma unroll
+        for (int j = 0; j < KVL; ++j) {
+            const uint32_t i = tid + j * kT, kr = (4 * i) / D, d = (4 * i) % D;
+            const float4 kv = kr4[j];
+            h4_t h, l;
+            split_h(kv.x * f, h, l, 0);
+            split_h(kv.y * f, h, l, 1);
+            split_h(kv.z * f, h, l, 2);
+            split_h(kv.w * f, h, l, 3);
+            *reinterpret_cast<h4_t*>(khi + kr * HP + d) = h;
+            *reinterpret_cast<h4_t*>(klo + kr * HP + d) = l;
+        }
+#pragma unroll
+        for (int g = 0; g < VG; ++g) {
+            h8_t h, l;
+#pragma unroll
+            for (int c = 0; c < 8; ++c) split_h(vr[g][c] * fv, h, l, c);
+            const uint32_t kb = (g * VGS + vgi) * 8;
+            *reinterpret_cast<h8_t*>(vth + vcol * KP + kb) = h;
+            *reinterpret_cast<h8_t*>(vtl + vcol * KP + kb) = l;
+        }
+        if (k0 + kFKeys < nkeys) load_tile(k0 + kFKeys);
+        __syncthreads();
+        // ---- S^T for keys 32*kh2 .. + 31 and this wave's 32 queries ----
+        v16f_t sacc;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) sacc[v] = 0.0f;
+        {
+            const int krow = 32 * kh2 + l32;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const h8_t ah = *reinterpret_cast<const h8_t*>(khi + krow * HP + ks * 16 + 8 * lh);
+                const h8_t al = *reinterpret_cast<const h8_t*>(klo + krow * HP + ks * 16 + 8 * lh);
+                sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bqh[ks], sacc, 0, 0, 0);
+                sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bql[ks], sacc, 0, 0, 0);
+                sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bqh[ks], sacc, 0, 0, 0);
+            }
+        }
+        // ---- online softmax of this lane's query over the wave's 32 keys ----
+        float sv[16];
+        float mx = -INFINITY;
+        const uint32_t lim = pos0 + t0 + qt;  // last key this query sees
+        const bool qok = t0 + qt < T;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const uint32_t kk = 32 * kh2 + 8 * (v >> 2) + 4 * lh + (v & 3);
+            const bool ok = qok && k0 + kk <= lim;
+            sv[v] = ok ? sacc[v] * (ik * iq2) * scale : -INFINITY;
+            mx = fmaxf(mx, sv[v]);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float m_new = fmaxf(m_run, mx);
+        float sum = 0.0f;
+        h8_t ph[2], pl[2];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const float pv = m_new == -INFINITY ? 0.0f : expf(sv[v] - m_new);
+            sum += pv;
+            split_h(pv * 16384.0f, ph[v >> 3], pl[v >> 3], v & 7);
+        }
+        sum += __shfl_xor(sum, 32);
+        const float alpha = m_run == -INFINITY ? 0.0f : expf(m_run - m_new);
+        l_run = l_run * alpha + sum;
+        m_run = m_new;
+        // O^T is kept in units of this tile's V scale: rescale by alpha and the scale change
+        const float ro = alpha * (fv / fv_prev);
+        fv_prev = fv;
+#pragma unroll
+        for (int n = 0; n < NT; ++n)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) o[n][v] *= ro;
+        // ---- O^T += V^T P^T: k slot j of step st is key 32*kh2 + kk(8 st + j) ----
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            const int kb = 32 * kh2 + 16 * st + 4 * lh;
+#pragma unroll
+            for (int n = 0; n < NT; ++n) {
+                const int vrow = 32 * n + l32;
+                h8_t ah, al;
+                const h4_t a0 = *reinterpret_cast<const h4_t*>(vth + vrow * KP + kb);
+                const h4_t a1 = *reinterpret_cast<const h4_t*>(vth + vrow * KP + kb + 8);
+                const h4_t b0 = *reinterpret_cast<const h4_t*>(vtl + vrow * KP + kb);
+                const h4_t b1 = *reinterpret_cast<const h4_t*>(vtl + vrow * KP + kb + 8);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    ah[j] = a0[j]; ah[j + 4] = a1[j];
+                    al[j] = b0[j]; al[j + 4] = b1[j];
+                }
+                o[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, ph[st], o[n], 0, 0, 0);
+                o[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, pl[st], o[n], 0, 0, 0);
+                o[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, ph[st], o[n], 0, 0, 0);
+            }
+        }
+    }
+    // ---- merge the two key halves of each query row set; O / (2^14 fv) / l ----
+    __syncthreads();  // every wave is done with K and V
+    float* mp = mrg + size_t(qh) * 64 * (NT * 16 + 2);
+    if (kh2 == 1) {
+#pragma unroll
+        for (int n = 0; n < NT; ++n)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) mp[(n * 16 + v) * 64 + lane] = o[n][v];
+        mp[(NT * 16) * 64 + lane] = m_run;
+        mp[(NT * 16 + 1) * 64 + lane] = l_run;
+    }
+    __syncthreads();
+    if (kh2 == 1 || t0 + qt >= T) return;
+    {
+        const float m1 = mp[(NT * 16) * 64 + lane], l1 = mp[(NT * 16 + 1) * 64 + lane];
+        const float M = fmaxf(m_run, m1);
+        const float a0 = m_run == -INFINITY ? 0.0f : expf(m_run - M);
+        const float a1 = m1 == -INFINITY ? 0.0f : expf(m1 - M);
+        const float L = l_run * a0 + l1 * a1;
+        const float inv = pow2f(-14) / fv_prev / L;
+        const uint32_t g = qrow / TQ;
+        float* orow = out + (size_t(t0 + qt) * H + kh * G + g) * D;
+#pragma unroll
+        for (int n = 0; n < NT; ++n)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float4 r;
+                r.x = (o[n][4 * j] * a0 + mp[(n * 16 + 4 * j) * 64 + lane] * a1) * inv;
+                r.y = (o[n][4 * j + 1] * a0 + mp[(n * 16 + 4 * j + 1) * 64 + lane] * a1) * inv;
+                r.z = (o[n][4 * j + 2] * a0 + mp[(n * 16 + 4 * j + 2) * 64 + lane] * a1) * inv;
+                r.w = (o[n][4 * j + 3] * a0 + mp[(n * 16 + 4 * j + 3) * 64 + lane] * a1) * inv;
+                *reinterpret_cast<float4*>(orow + 32 * n + 8 * j + 4 * lh) = r;
+            }
+    }
+}
+
 // Decode attention (one query token at position pos) with RoPE and the KV
 // append fused in, split over positions: workgroup (kh, s) covers positions
 // [s*C, s*C + C) of kv head kh for the G query heads that share it, reading
@@ -907,14 +1209,12 @@ hipError_t launch_attention(const float* q, const float* kc, const float* vc, fl
     if (kFRows % G == 0 && (D == 64 || D == 128)) {
         const uint32_t TQ = kFRows / G;
         const dim3 grid(KH, (T + TQ - 1) / TQ);
-        const size_t lds = (size_t(kFRows) * (D + 1) + size_t(kFKeys) * (D + 1) + size_t(kFKeys) * D +
-                            size_t(kFRows) * (kFKeys + 1)) * sizeof(float);
         if (D == 64)
-            hipLaunchKernelGGL(attention_prefill_kernel<64>, grid, dim3(kT), lds, stream, q, kc, vc, out, pos0, T, H, KH,
-                               scale);
+            hipLaunchKernelGGL(attention_prefill_t_kernel<64>, grid, dim3(kT), attention_prefill_t_lds(64), stream, q, kc,
+                               vc, out, pos0, T, H, KH, scale);
         else
-            hipLaunchKernelGGL(attention_prefill_kernel<128>, grid, dim3(kT), lds, stream, q, kc, vc, out, pos0, T, H,
-                               KH, scale);
+            hipLaunchKernelGGL(attention_prefill_t_kernel<128>, grid, dim3(kT), attention_prefill_t_lds(128), stream, q,
+                               kc, vc, out, pos0, T, H, KH, scale);
         return hipGetLastError();
     }
     const size_t lds = size_t(max_pos) * sizeof(float);
