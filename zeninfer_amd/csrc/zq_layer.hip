@@ -278,166 +278,13 @@ __global__ __launch_bounds__(kT) void attention_kernel(const float* __restrict__
 // Causal GQA prefill attention, tiled: workgroup (kh, i) takes a tile of 64
 // rows = (query head g of kv head kh, token t) pairs, t in [i*TQ, i*TQ + TQ)
 // with TQ = 64 / G, so the G heads that share a K/V row read it once.  Key
-// tiles of 64 positions stream through LDS; S = Q K^T and O += P V run on the
-// fp32 MFMA (v_mfma_f32_32x32x2f32, each wave one 32x32 tile of S and D/64
-// tiles of O), with an online softmax (running max m, sum l, rescale of O by
-// exp(m_old - m_new)) between them.  The result equals the reference's
-// softmax(q.k * scale) . v up to fp32 summation order.
+// tiles of 64 positions stream through LDS, with an online softmax (running
+// max m, sum l, rescale of O by exp(m_old - m_new)).  The result equals the
+// reference's softmax(q.k * scale) . v to fp32-level accuracy.
 typedef float v16f_t __attribute__((ext_vector_type(16)));
 constexpr int kFRows = 64, kFKeys = 64;
 
-template <int D>
-__global__ __launch_bounds__(kT) void attention_prefill_kernel(const float* __restrict__ q, const float* __restrict__ kc,
-                                                               const float* __restrict__ vc, float* __restrict__ out,
-                                                               const uint32_t* __restrict__ pos0_ptr, uint32_t T,
-                                                               uint32_t H, uint32_t KH, float scale) {
-    constexpr int QP = D + 1;       // padded rows: conflict-free column reads
-    constexpr int SP = kFKeys + 1;
-    constexpr int NTW = D / 64;     // 32-wide O tiles per wave
-    extern __shared__ float fsm[];
-    float* qs = fsm;                          // [64][D+1]
-    float* ks = qs + kFRows * QP;             // [64][D+1]
-    float* vs = ks + kFKeys * QP;             // [64][D]
-    float* ss = vs + kFKeys * D;              // [64][65]
-    __shared__ float row_m[kFRows], row_l[kFRows], row_a[kFRows];
-    const uint32_t G = H / KH, TQ = kFRows / G;
-    const uint32_t kh = blockIdx.x, t0 = blockIdx.y * TQ;
-    const uint32_t pos0 = *pos0_ptr;
-    const uint32_t KW = KH * D;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int l32 = lane & 31, lh = lane >> 5;
-
-    {
-        constexpr int QL = kFRows * D / 4 / kT;  // float4 of Q per thread, all loaded before any is stored
-        float4 qv[QL];
-#pragma unroll
-        for (int j = 0; j < QL; ++j) {
-            const uint32_t i = tid + j * kT, r = (4 * i) / D, d = (4 * i) % D;
-            const uint32_t g = r / TQ, t = r % TQ;
-            qv[j] = t0 + t < T ? *reinterpret_cast<const float4*>(q + (size_t(t0 + t) * H + kh * G + g) * D + d)
-                               : make_float4(0, 0, 0, 0);
-        }
-#pragma unroll
-        for (int j = 0; j < QL; ++j) {
-            const uint32_t i = tid + j * kT, r = (4 * i) / D, d = (4 * i) % D;
-            float* dst = qs + r * QP + d;
-            dst[0] = qv[j].x; dst[1] = qv[j].y; dst[2] = qv[j].z; dst[3] = qv[j].w;
-        }
-    }
-    if (tid < kFRows) {
-        row_m[tid] = -INFINITY;
-        row_l[tid] = 0.0f;
-    }
-    const uint32_t mt = wave >> 1, ntb = (wave & 1) * NTW;
-    v16f_t o[NTW];
-#pragma unroll
-    for (int n = 0; n < NTW; ++n)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) o[n][v] = 0.0f;
-    const uint32_t nkeys = pos0 + min(t0 + TQ, T);  // keys any row of the tile sees
-    // K/V tiles go global -> registers -> LDS; the registers of tile k0 + 64
-    // are loaded while tile k0 is computed, so a tile's loads (one round trip
-    // for all of them) overlap the previous tile's MFMAs.
-    constexpr int KVL = kFKeys * D / 4 / kT;  // float4 of K (and of V) per thread per tile
-    float4 kr4[KVL], vr4[KVL];
-    auto load_tile = [&](uint32_t k0) {
-#pragma unroll
-        for (int j = 0; j < KVL; ++j) {
-            const uint32_t i = tid + j * kT, kr = (4 * i) / D, d = (4 * i) % D;
-            const uint32_t key = min(k0 + kr, nkeys - 1);  // past the last key: a valid row, masked in S
-            kr4[j] = *reinterpret_cast<const float4*>(kc + size_t(key) * KW + size_t(kh) * D + d);
-            vr4[j] = *reinterpret_cast<const float4*>(vc + size_t(key) * KW + size_t(kh) * D + d);
-        }
-    };
-    load_tile(0);
-    for (uint32_t k0 = 0; k0 < nkeys; k0 += kFKeys) {
-        __syncthreads();  // the previous tile's readers are done
-#pragma unroll
-        for (int j = 0; j < KVL; ++j) {
-            const uint32_t i = tid + j * kT, kr = (4 * i) / D, d = (4 * i) % D;
-            const bool live = k0 + kr < nkeys;  // zero K/V past the last key (as before: S is masked there)
-            const float4 kv = live ? kr4[j] : make_float4(0, 0, 0, 0), vv = live ? vr4[j] : make_float4(0, 0, 0, 0);
-            float* kd = ks + kr * QP + d;
-            kd[0] = kv.x; kd[1] = kv.y; kd[2] = kv.z; kd[3] = kv.w;
-            *reinterpret_cast<float4*>(vs + kr * D + d) = vv;
-        }
-        if (k0 + kFKeys < nkeys) load_tile(k0 + kFKeys);
-        __syncthreads();
-        {   // S tile of this wave: rows 32*(wave>>1), keys 32*(wave&1)
-            v16f_t sacc;
-#pragma unroll
-            for (int v = 0; v < 16; ++v) sacc[v] = 0.0f;
-            const float* qa = qs + (32 * (wave >> 1) + l32) * QP + lh;
-            const float* kb = ks + (32 * (wave & 1) + l32) * QP + lh;
-#pragma unroll 8
-            for (int kk = 0; kk < D; kk += 2) sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(qa[kk], kb[kk], sacc, 0, 0, 0);
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const uint32_t r = 32 * (wave >> 1) + 8 * (v >> 2) + 4 * lh + (v & 3);
-                const uint32_t c = 32 * (wave & 1) + l32;
-                const uint32_t t = r % TQ;
-                const bool ok = t0 + t < T && k0 + c <= pos0 + t0 + t;
-                ss[r * SP + c] = ok ? sacc[v] * scale : -INFINITY;
-            }
-        }
-        __syncthreads();
-        {   // online softmax: the 4 lanes of a quad share a row, 16 keys each
-            const uint32_t r = tid >> 2, part = tid & 3;
-            float* sr = ss + r * SP + part * 16;
-            float mx = -INFINITY;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sr[i]);
-            mx = fmaxf(mx, dpp_f<kDppXor1>(mx));
-            mx = fmaxf(mx, dpp_f<kDppXor2>(mx));
-            const float m_old = row_m[r];
-            const float m_new = fmaxf(m_old, mx);
-            float sum = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const float p = m_new == -INFINITY ? 0.0f : expf(sr[i] - m_new);
-                sr[i] = p;
-                sum += p;
-            }
-            sum = group_sum<4>(sum);
-            if (part == 0) {
-                const float alpha = m_old == -INFINITY ? 0.0f : expf(m_old - m_new);
-                row_a[r] = alpha;
-                row_m[r] = m_new;
-                row_l[r] = row_l[r] * alpha + sum;
-            }
-        }
-        __syncthreads();
-        {   // O = O * alpha + P V
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const float a = row_a[32 * mt + 8 * (v >> 2) + 4 * lh + (v & 3)];
-#pragma unroll
-                for (int n = 0; n < NTW; ++n) o[n][v] *= a;
-            }
-            const float* pa = ss + (32 * mt + l32) * SP + lh;
-            const float* vb = vs + lh * D + 32 * ntb + l32;
-#pragma unroll 4
-            for (int kk = 0; kk < kFKeys; kk += 2) {
-                const float a = pa[kk];
-#pragma unroll
-                for (int n = 0; n < NTW; ++n) o[n] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, vb[kk * D + 32 * n], o[n], 0, 0, 0);
-            }
-        }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int v = 0; v < 16; ++v) {
-        const uint32_t r = 32 * mt + 8 * (v >> 2) + 4 * lh + (v & 3);
-        const uint32_t g = r / TQ, t = r % TQ;
-        if (t0 + t >= T) continue;
-        const float inv = 1.0f / row_l[r];
-        float* orow = out + (size_t(t0 + t) * H + kh * G + g) * D + 32 * ntb + l32;
-#pragma unroll
-        for (int n = 0; n < NTW; ++n) orow[32 * n] = o[n][v] * inv;
-    }
-}
-
-// The same attention with the products on the f16 MFMA
+// The products run on the f16 MFMA
 // (v_mfma_f32_32x32x16_f16, 16x the fp32 MFMA rate) at fp32-level accuracy,
 // computed transposed so the softmax stays in registers:
 //  * every operand x is scaled by a power of two 2^e (exact) so max |x| lies
