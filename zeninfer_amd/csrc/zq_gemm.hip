@@ -377,9 +377,11 @@ __global__ __launch_bounds__(kThreads) void splitk_reduce_kernel(const float* __
 // tiles in the accumulator layout, then one cvt + one fma per element.
 constexpr int QTH = 512;
 // Stage geometry for QKB blocks per K stage (8: 144 KB of LDS, one workgroup
-// per CU; 4: 72 KB, two).  Weight row r starts at LDS dword r * W_STRIDE, an
-// odd stride, so the MFMA B reads (32 rows, one dword each) fall on distinct
-// banks: measured zero LDS bank conflicts for the whole kernel at 69.
+// per CU; 4: 72 KB, two).  Weight row r starts at LDS dword r * W_STRIDE, the
+// row's stage bytes rounded up to whole 16 B units, so each weight load moves
+// 16 B per lane.  (An odd stride, 69 / 35 dwords, made the B reads conflict-free
+// but needed 4 B loads, 4x the load instructions; the 16 B form measured 4-7%
+// faster at M = 512 and 2048 despite 2-way B-read conflicts.)
 template <int QKB, int BMT = BM, int NW = QTH / 64, int BB = 34>
 struct QStage {
     static constexpr int A_BYTES = BMT * QKB * 32;          // activation tile
@@ -391,11 +393,11 @@ struct QStage {
     __device__ static int swz(int row) { return UPR == 16 ? row % 16 : (row >> 1) & 7; }
     static_assert(UPR == 8 || UPR == 16, "4- or 8-block stages");
     static constexpr int WD = QKB * BB / 4;                 // raw dwords of a weight row per stage (BB = block bytes)
-    static constexpr int W_STRIDE = WD | 1;                 // 69 / 35
-    static constexpr int W_DWORDS = (BN - 1) * W_STRIDE + WD + 1;  // +1: the 5th dword read
-    static constexpr int W_LOADS = (W_DWORDS + 63) / 64;   // 64-lane dword loads per stage
+    static constexpr int W_STRIDE = (WD + 4) & ~3;          // 36 / 20: whole 16 B units per row
+    static constexpr int W_UNITS = BN * W_STRIDE / 4;
+    static constexpr int W_LOADS = (W_UNITS + 63) / 64;     // 64-lane 16 B loads per stage
     static constexpr int W_PER_WAVE = (W_LOADS + NW - 1) / NW;
-    static constexpr int W_BYTES = (W_LOADS * 64 * 4 + 15) / 16 * 16;
+    static constexpr int W_BYTES = W_LOADS * 64 * 16;
     static constexpr int S_BYTES = QKB * BMT * 4;
     static constexpr int S_UNITS = S_BYTES / 256;           // 64-lane dword loads of scales per stage
     static constexpr int S_PER_WAVE = (S_UNITS + NW - 1) / NW;
@@ -463,15 +465,16 @@ __device__ __forceinline__ void gemm_i8_direct_body(
         const int row = unit / G::UPR, col = (unit % G::UPR) ^ G::swz(row);
         a_off[i] = (min(m0 + row, M - 1) - m0) * K + col * 16;
     }
-    // Weight dword loads: LDS dword p of the region holds raw dword d of row r
-    // (p = r*G::W_STRIDE + d); gap dwords load a harmless dword.
+    // Weight loads in 16 B units: LDS dword p of the region holds raw dword d
+    // of row r (p = r*G::W_STRIDE + d); a row's last unit runs 2 dwords past its
+    // stage bytes into the row's next bytes (the matrix's tail pad after the
+    // last row), unused.
     uint32_t w_off[G::W_PER_WAVE];
 #pragma unroll
     for (int i = 0; i < G::W_PER_WAVE; ++i) {
-        const uint32_t p = uint32_t((wave + NW * i) * 64 + lane);
-        uint32_t r = min(p / G::W_STRIDE, uint32_t(BN - 1));
-        uint32_t d = p - r * G::W_STRIDE;
-        if (d >= uint32_t(G::WD)) d = 0;
+        const uint32_t u = uint32_t((wave + NW * i) * 64 + lane);
+        const uint32_t r = min(4 * u / G::W_STRIDE, uint32_t(BN - 1));
+        const uint32_t d = 4 * u - r * G::W_STRIDE;
         w_off[i] = (min(n0 + r, N - 1) - n0) * rb + d * 4;
     }
     uint32_t s_off[G::S_PER_WAVE];
@@ -489,7 +492,7 @@ __device__ __forceinline__ void gemm_i8_direct_body(
 #pragma unroll
         for (int i = 0; i < G::W_PER_WAVE; ++i)
             if (wave + NW * i < G::W_LOADS)  // wave-uniform
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_void*)(base + G::A_BYTES + (wave + NW * i) * 256), 4,
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_void*)(base + G::A_BYTES + (wave + NW * i) * 1024), 16,
                                                          w_off[i], kb * BB, 0, 0);
         if constexpr (!DOTS) {
 #pragma unroll
