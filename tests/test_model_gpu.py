@@ -259,6 +259,39 @@ def test_fused_prefill_quantiser_equals_unfused(tmp_path, zq, ptype):
         assert np.array_equal(la, lb)
 
 
+@pytest.mark.parametrize("rope_dim", [64, 32])
+def test_partial_rope_matches_reference(tmp_path, zq, rope_dim):
+    """rope.dimension_count below the head dim (128): only the first rope_dim
+    dimensions of q and k rotate, the rest pass through (the reference's
+    rope()).  150-token fp32 prefill and 4 decode steps within the fp32 bar,
+    through the float4 RoPE kernel (rope_dim / 2 even) and the decode kernel's
+    fused RoPE."""
+    if not os.path.exists(REF_LIB):
+        pytest.skip("oracle/_ref not built")
+    from oracle.oracle import ReferenceModel
+    from zeninfer_amd.model import PREFILL_F32
+    shape = G.LlamaShape(embedding=512, layers=1, heads=4, kv_heads=2, ffn=512, vocab=512, context=2048,
+                         rope_dim=rope_dim)
+    path = tmp_path / f"rope_{rope_dim}.gguf"
+    G.synthetic_llama(path, shape, seed=31)
+    prompt = [int(t) for t in np.random.default_rng(rope_dim).integers(0, shape.vocab, 150)]
+    ref = ReferenceModel(path)
+    m = load(path, PREFILL_F32, max_positions=256)
+    nxt, lg = m.prefill(prompt)
+    lr = ref.prefill(prompt, capacity=256)
+    ok, err, scale = close_to(lg, lr, 1e-4)
+    assert ok and nxt == int(np.argmax(lr)), err
+    tok = nxt
+    for step in range(4):
+        nxt, lg = m.decode(tok)
+        lr = ref.step(tok, len(prompt) + step)
+        ok, err, scale = close_to(lg, lr, 1e-4)
+        assert ok and nxt == int(np.argmax(lr)), (step, err)
+        tok = nxt
+    m.close()
+    ref.close()
+
+
 @pytest.mark.parametrize("embedding,heads,kv_heads", [(512, 4, 2), (1024, 8, 1), (768, 3, 1), (896, 14, 2)])
 def test_prefill_attention_shapes_match_reference(tmp_path, zq, embedding, heads, kv_heads):
     """head_dim 128 with 2 and 8 query heads per kv head, a 150-token prompt

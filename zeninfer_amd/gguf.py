@@ -206,6 +206,7 @@ class LlamaShape:
     context: int = 8192
     rope_theta: float = 500000.0
     rms_eps: float = 1e-5
+    rope_dim: int = 0  # rotated dimensions per head (0: the whole head)
 
 
 def synthetic_llama(path, shape: LlamaShape, seed: int = 0x5EED0004, weight_scale: float = 0.12,
@@ -225,7 +226,7 @@ def synthetic_llama(path, shape: LlamaShape, seed: int = 0x5EED0004, weight_scal
         ("llama.embedding_length", U32, s.embedding), ("llama.block_count", U32, s.layers),
         ("llama.attention.head_count", U32, s.heads), ("llama.attention.head_count_kv", U32, s.kv_heads),
         ("llama.feed_forward_length", U32, s.ffn), ("llama.context_length", U32, s.context),
-        ("llama.rope.dimension_count", U32, hd), ("llama.rope.freq_base", F32, s.rope_theta),
+        ("llama.rope.dimension_count", U32, s.rope_dim or hd), ("llama.rope.freq_base", F32, s.rope_theta),
         ("llama.attention.layer_norm_rms_epsilon", F32, s.rms_eps),
         ("tokenizer.ggml.model", STRING, "llama"), ("tokenizer.ggml.tokens", ARRAY, (STRING, tokens)),
         ("tokenizer.ggml.bos_token_id", U32, 1), ("tokenizer.ggml.eos_token_id", U32, 2),
