@@ -309,8 +309,8 @@ typedef uint32_t u32x4_attn_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float pow2f(int e) { return __int_as_float((e + 127) << 23); }
 // exponent e with max |x| * 2^e in [2^14, 2^15); 0 for max 0.  Clamped to
 // [-40, 40]: a change of the V scale between tiles multiplies the running O by
-// at most 2^80, which stays finite; values outside 2^-25 .. 2^55 lose precision
-// instead of overflowing.
+// at most 2^80, which stays finite.  Operands whose maximum lies below 2^-26
+// lose precision (f16 subnormals); above 2^56 they would overflow f16.
 __device__ __forceinline__ int split_exp(float amax) {
     if (!(amax > 0.0f)) return 0;
     return min(max(15 - __builtin_amdgcn_frexp_expf(amax), -40), 40);
