@@ -262,12 +262,13 @@ int enqueue_gemm(int fmt, const uint8_t* w, const float* X, float* Y, size_t tok
         *dispatches += pbytes ? 3 : 2;
         return ZQ_OK;
     }
-    // fp32 activations: the workspace, when large enough, holds split-K
-    // partial sums; without it the GEMM runs unsplit
-    const size_t pbytes = zq::gemm_f32_partial_bytes(tokens, rows, cols);
-    float* part = pbytes && ws && ws_bytes >= pbytes ? static_cast<float*>(ws) : nullptr;
-    if (zq::launch_gemm_f32(fmt, w, X, Y, part, tokens, rows, cols, s) != hipSuccess) return ZQ_ERR_HIP;
-    *dispatches += part ? 2 : 1;
+    // fp32 activations: the workspace, when large enough, holds the split
+    // activations (Q6_K) and split-K partial sums; with less the GEMM runs
+    // with what fits
+    uint32_t n = 0;
+    if (zq::launch_gemm_f32(fmt, w, X, Y, ws, ws ? ws_bytes : 0, tokens, rows, cols, s, &n) != hipSuccess)
+        return ZQ_ERR_HIP;
+    *dispatches += n;
     return ZQ_OK;
 }
 
@@ -278,7 +279,7 @@ size_t batch_workspace_bytes(int fmt, const size_t* rows, size_t count, size_t t
     size_t part = 0;
     for (size_t i = 0; i < count; ++i)
         part = std::max(part, act == ZQ_ACT_INT8 ? zq::gemm_i8_partial_bytes(tokens, rows[i], cols)
-                                                 : zq::gemm_f32_partial_bytes(tokens, rows[i], cols));
+                                                 : zq::gemm_f32_workspace_bytes(fmt, tokens, rows[i], cols));
     if (act != ZQ_ACT_INT8) return part;
     return align_up(tokens * cols, 256) + align_up(tokens * (cols / 32) * sizeof(float), 256) + part;
 }
@@ -307,10 +308,10 @@ int enqueue_gemm_batch(int fmt, const uint8_t* const* w, float* const* Y, const 
         return ZQ_OK;
     }
     for (size_t i = 0; i < count; ++i) {
-        const size_t pb = zq::gemm_f32_partial_bytes(tokens, rows[i], cols);
-        float* part = pb && ws ? static_cast<float*>(ws) : nullptr;
-        if (zq::launch_gemm_f32(fmt, w[i], X, Y[i], part, tokens, rows[i], cols, s) != hipSuccess) return ZQ_ERR_HIP;
-        *dispatches += part ? 2 : 1;
+        uint32_t n = 0;
+        if (zq::launch_gemm_f32(fmt, w[i], X, Y[i], ws, ws ? ws_bytes : 0, tokens, rows[i], cols, s, &n) != hipSuccess)
+            return ZQ_ERR_HIP;
+        *dispatches += n;
     }
     return ZQ_OK;
 }
@@ -904,7 +905,7 @@ int zq_hip_gemv_dev(int fmt, const void* weights, const float* x, float* y, size
 
 size_t zq_hip_gemm_workspace_bytes(int fmt, size_t tokens, size_t rows, size_t cols, int act_mode) {
     if (!valid_fmt(fmt) || !zq::row_bytes(fmt, cols) || !tokens || !rows) return 0;
-    if (resolve_act(fmt, act_mode) != ZQ_ACT_INT8) return zq::gemm_f32_partial_bytes(tokens, rows, cols);
+    if (resolve_act(fmt, act_mode) != ZQ_ACT_INT8) return zq::gemm_f32_workspace_bytes(fmt, tokens, rows, cols);
     return align_up(tokens * cols, 256) + align_up(tokens * (cols / 32) * sizeof(float), 256) +
            zq::gemm_i8_partial_bytes(tokens, rows, cols);
 }

@@ -144,6 +144,29 @@ __device__ __forceinline__ void dequant32(const uint8_t* row, uint32_t k0, float
     }
 }
 
+// Split-f16 operands for the f16 MFMA at fp32-level accuracy (prefill
+// attention, the Q6_K fp32-activation GEMM): a value x, scaled by a power of
+// two so its block's maximum lies in [2^14, 2^15), is carried as
+// h = f16(x) and l = f16(x - h) (x - h is exact in fp32).
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_attn_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float pow2f(int e) { return __int_as_float((e + 127) << 23); }
+// exponent e with max |x| * 2^e in [2^14, 2^15); 0 for max 0.  Clamped to
+// [-40, 40]: a change of scale between tiles multiplies a running accumulator
+// by at most 2^80, which stays finite.  Operands whose maximum lies below 2^-26
+// lose precision (f16 subnormals); above 2^56 they would overflow f16.
+__device__ __forceinline__ int split_exp(float amax) {
+    if (!(amax > 0.0f)) return 0;
+    return min(max(15 - __builtin_amdgcn_frexp_expf(amax), -40), 40);
+}
+// element i of h and l: h = f16(x), l = f16(x - h)
+template <class V>
+__device__ __forceinline__ void split_h(float x, V& h, V& l, int i) {
+    const _Float16 a = _Float16(x);
+    h[i] = a;
+    l[i] = _Float16(x - float(a));
+}
 // Cross-lane reductions on DPP (quad_perm, row_half_mirror, row_mirror move
 // data between lanes of a 16-lane row inside the VALU, a few cycles each)
 // plus v_readlane for the four rows; ds_bpermute (what __shfl_xor lowers

@@ -956,6 +956,220 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(const uint8_t* __res
         }
 }
 
+// ------------------------------------------------ Q6_K on the f16 MFMA ---
+// The fp32-activation Q6_K GEMM with its products on v_mfma_f32_32x32x16_f16
+// (16x the fp32 MFMA rate) at fp32-level accuracy:
+//  * each activation row is scaled by a power of two (split_rows_kernel) and
+//    carried as f16 hi + lo;
+//  * each weight is the integer sc * q of its 16-element group (|sc*q| <=
+//    4096), carried as h = f16(sc*q) and l = sc*q - h (nonzero only past
+//    2048), both exact;
+//  * a product is Xh*Wh + Xl*Wh + Xh*Wl, accumulated in fp32 over a
+//    super-block (256 K), then scaled by the super-block's d and added to
+//    the output; the row scale comes off at the end.
+// Against the reference's (d*sc)*q times x in fp32 the difference is
+// rounding order plus the dropped Xl*Wl (below 2^-22 of the row maximum).
+// A workgroup barrier that orders LDS only: unlike __syncthreads it does not
+// wait for the wave's outstanding global loads (a prefetch stays in flight).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+constexpr int HK = 32;          // K elements per stage
+constexpr int HROW = HK + 8;    // halves per LDS row (pad: 16 B)
+
+__global__ __launch_bounds__(kThreads) void split_rows_kernel(const float* __restrict__ X, _Float16* __restrict__ xh,
+                                                              _Float16* __restrict__ xl, float* __restrict__ inv,
+                                                              uint32_t K) {
+    __shared__ float red[kThreads / 64];
+    const float4* r = reinterpret_cast<const float4*>(X + size_t(blockIdx.x) * K);
+    const uint32_t K4 = K / 4;
+    float m = 0.0f;
+    for (uint32_t i = threadIdx.x; i < K4; i += kThreads) {
+        const float4 v = r[i];
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+    m = wave_max(m);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = red[0];
+#pragma unroll
+    for (int w = 1; w < kThreads / 64; ++w) m = fmaxf(m, red[w]);
+    const int e = split_exp(m);
+    const float f = pow2f(e);
+    if (threadIdx.x == 0) inv[blockIdx.x] = pow2f(-e);
+    h4_t* oh = reinterpret_cast<h4_t*>(xh + size_t(blockIdx.x) * K);
+    h4_t* ol = reinterpret_cast<h4_t*>(xl + size_t(blockIdx.x) * K);
+    for (uint32_t i = threadIdx.x; i < K4; i += kThreads) {
+        const float4 v = r[i];
+        h4_t h, l;
+        split_h(v.x * f, h, l, 0);
+        split_h(v.y * f, h, l, 1);
+        split_h(v.z * f, h, l, 2);
+        split_h(v.w * f, h, l, 3);
+        oh[i] = h;
+        ol[i] = l;
+    }
+}
+
+// Split K as in gemm_f32_kernel; stages_per_split is a multiple of the 8
+// stages of a super-block.
+__global__ __launch_bounds__(kThreads) void gemm_q6k_h_kernel(const uint8_t* __restrict__ W, const _Float16* __restrict__ XH,
+                                                              const _Float16* __restrict__ XL,
+                                                              const float* __restrict__ xinv, float* __restrict__ Y,
+                                                              uint32_t M, uint32_t N, uint32_t K, uint32_t tiles_m,
+                                                              uint32_t tiles_n, uint32_t ksplit,
+                                                              uint32_t stages_per_split) {
+    __shared__ __align__(16) _Float16 Ah[BM * HROW];
+    __shared__ __align__(16) _Float16 Al[BM * HROW];
+    __shared__ __align__(16) _Float16 Bh[BN * HROW];
+    __shared__ __align__(16) _Float16 Bl[BN * HROW];
+    const uint32_t total_tiles = tiles_m * tiles_n;
+    const uint32_t split = blockIdx.x / total_tiles;
+    uint32_t tm, tn;
+    tile_of(tiles_m, tiles_n, blockIdx.x % total_tiles, tm, tn);
+    const uint32_t m0 = tm * BM, n0 = tn * BN;
+    const uint32_t k_begin = split * stages_per_split * HK;
+    const uint32_t k_end = min(K, k_begin + stages_per_split * HK);
+    float* Yout = Y + (ksplit > 1 ? size_t(split) * M * N : 0);
+    const size_t rb = row_bytes_dev(kQ6_K, K);
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int l32 = lane & 31, lh = lane >> 5;
+    const uint32_t ld_row = tid >> 1, ld_half = tid & 1;  // loader: row, 16-element half of the stage
+    const _Float16* ah_src = XH + size_t(min(m0 + ld_row, M - 1)) * K + ld_half * 16;
+    const _Float16* al_src = XL + size_t(min(m0 + ld_row, M - 1)) * K + ld_half * 16;
+    const uint8_t* b_src = W + size_t(min(n0 + ld_row, N - 1)) * rb;
+    const uint8_t* d_src[2];  // this lane's two output columns
+#pragma unroll
+    for (int j = 0; j < 2; ++j) d_src[j] = W + size_t(min(n0 + wn * 64 + j * 32 + l32, N - 1)) * rb + 208;
+
+    v16f acc[2][2], part[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = part[i][j][v] = 0.0f;
+    float dj[2] = {0.0f, 0.0f};
+
+    // Raw stage data of this thread: 16 activations (hi, lo), the 16 weights'
+    // low-nibble and high-bit words and their group's scale.  The next stage's
+    // are loaded while the current one is converted and multiplied.
+    struct Raw {
+        uint4 xa0, xa1, xb0, xb1;
+        uint32_t lw[4], hw[4];
+        int sc;
+        uint32_t dbits[2];  // d of the super-block, this lane's two output columns
+    };
+    auto load_raw = [&](uint32_t k0, Raw& r) {
+        r.xa0 = *reinterpret_cast<const uint4*>(ah_src + k0);
+        r.xa1 = *reinterpret_cast<const uint4*>(ah_src + k0 + 8);
+        r.xb0 = *reinterpret_cast<const uint4*>(al_src + k0);
+        r.xb1 = *reinterpret_cast<const uint4*>(al_src + k0 + 8);
+        const uint8_t* p = b_src + size_t(k0 >> 8) * 210;
+        const uint32_t in_sb = k0 & 255u;
+        const uint32_t h = in_sb >> 7, grp = (in_sb >> 5) & 3u;
+        r.sc = int(reinterpret_cast<const int8_t*>(p + 192)[h * 8 + grp * 2 + ld_half]);
+        const uint8_t* lo = p + h * 64 + (grp & 1u) * 32 + ld_half * 16;
+        const uint8_t* hi = p + 128 + h * 32 + ld_half * 16;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            r.lw[i] = load_u32_a2(lo + 4 * i);
+            r.hw[i] = load_u32_a2(hi + 4 * i);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) r.dbits[j] = *reinterpret_cast<const uint16_t*>(d_src[j] + size_t(k0 >> 8) * 210);
+    };
+    Raw cur, nxt;
+    if (k_begin < k_end) load_raw(k_begin, cur);
+    for (uint32_t k0 = k_begin; k0 < k_end; k0 += HK) {
+        // unconditional (the last stage reloads itself), so the wait for the
+        // current stage's data counts the prefetch statically
+        load_raw(min(k0 + HK, k_end - HK), nxt);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) dj[j] = half_bits_to_float(cur.dbits[j]);
+        const uint4 xa0 = cur.xa0, xa1 = cur.xa1, xb0 = cur.xb0, xb1 = cur.xb1;
+        h8_t wh0, wl0, wh1, wl1;
+        {
+            const uint32_t grp = ((k0 & 255u) >> 5) & 3u;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t lw = cur.lw[i], hw = cur.hw[i];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    uint32_t l = (lw >> (8 * k)) & 0xffu;
+                    if (grp >= 2) l >>= 4;
+                    const uint32_t hb = ((hw >> (8 * k)) >> (2 * grp)) & 3u;
+                    const float v = float(cur.sc * (int((l & 15u) | (hb << 4)) - 32));  // exact integer
+                    const int e = 4 * i + k;
+                    if (e < 8) split_h(v, wh0, wl0, e);
+                    else split_h(v, wh1, wl1, e - 8);
+                }
+            }
+        }
+        lds_barrier();  // the previous stage's readers are done (the prefetch stays in flight)
+        *reinterpret_cast<uint4*>(Ah + ld_row * HROW + ld_half * 16) = xa0;
+        *reinterpret_cast<uint4*>(Ah + ld_row * HROW + ld_half * 16 + 8) = xa1;
+        *reinterpret_cast<uint4*>(Al + ld_row * HROW + ld_half * 16) = xb0;
+        *reinterpret_cast<uint4*>(Al + ld_row * HROW + ld_half * 16 + 8) = xb1;
+        *reinterpret_cast<h8_t*>(Bh + ld_row * HROW + ld_half * 16) = wh0;
+        *reinterpret_cast<h8_t*>(Bh + ld_row * HROW + ld_half * 16 + 8) = wh1;
+        *reinterpret_cast<h8_t*>(Bl + ld_row * HROW + ld_half * 16) = wl0;
+        *reinterpret_cast<h8_t*>(Bl + ld_row * HROW + ld_half * 16 + 8) = wl1;
+        lds_barrier();
+#pragma unroll
+        for (int ks = 0; ks < HK / 16; ++ks) {
+            h8_t ah[2], al[2], bh[2], bl[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int r = (wm * 64 + i * 32 + l32) * HROW + ks * 16 + 8 * lh;
+                ah[i] = *reinterpret_cast<const h8_t*>(Ah + r);
+                al[i] = *reinterpret_cast<const h8_t*>(Al + r);
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int r = (wn * 64 + j * 32 + l32) * HROW + ks * 16 + 8 * lh;
+                bh[j] = *reinterpret_cast<const h8_t*>(Bh + r);
+                bl[j] = *reinterpret_cast<const h8_t*>(Bl + r);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bh[j], part[i][j], 0, 0, 0);
+                    part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], bh[j], part[i][j], 0, 0, 0);
+                    part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bl[j], part[i][j], 0, 0, 0);
+                }
+        }
+        if (((k0 + HK) & 255u) == 0 || k0 + HK >= k_end) {  // end of a super-block: scale by its d
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) {
+                        acc[i][j][v] = fmaf(part[i][j][v], dj[j], acc[i][j][v]);
+                        part[i][j][v] = 0.0f;
+                    }
+        }
+        cur = nxt;
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const uint32_t n = n0 + wn * 64 + j * 32 + l32;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const uint32_t m = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+                if (m < M && n < N) Yout[size_t(m) * N + n] = acc[i][j][v] * xinv[m];
+            }
+        }
+}
+
 }  // namespace
 
 hipError_t launch_quantize_acts(const float* X, int8_t* xq, float* xs, size_t M, size_t K, hipStream_t stream) {
@@ -1172,8 +1386,18 @@ size_t gemm_f32_partial_bytes(size_t M, size_t N, size_t K) {
     return ks > 1 ? size_t(ks) * M * N * sizeof(float) : 0;
 }
 
-hipError_t launch_gemm_f32(int fmt, const uint8_t* w, const float* X, float* Y, float* partial, size_t M, size_t N,
-                           size_t K, hipStream_t stream) {
+// Q6_K on the f16 MFMA: the split activations (hi and lo halves, [M][K] each)
+// and the row scales come first in the workspace.
+static size_t q6k_split_bytes(size_t M, size_t K) {
+    return (M * K * 2 * sizeof(_Float16) + M * sizeof(float) + 255) / 256 * 256;
+}
+
+size_t gemm_f32_workspace_bytes(int fmt, size_t M, size_t N, size_t K) {
+    return (fmt == kQ6_K && K % 256 == 0 ? q6k_split_bytes(M, K) : 0) + gemm_f32_partial_bytes(M, N, K);
+}
+
+hipError_t launch_gemm_f32(int fmt, const uint8_t* w, const float* X, float* Y, void* ws, size_t ws_bytes, size_t M,
+                           size_t N, size_t K, hipStream_t stream, uint32_t* launches) {
     if (!w || !X || !Y || !M || !N || !row_bytes(fmt, K) || M > (1u << 24) || N > (1u << 24) || K > (1u << 24))
         return hipErrorInvalidValue;
     if ((reinterpret_cast<uintptr_t>(w) & 1u) || (reinterpret_cast<uintptr_t>(X) & 15u)) return hipErrorInvalidValue;
@@ -1181,12 +1405,29 @@ hipError_t launch_gemm_f32(int fmt, const uint8_t* w, const float* X, float* Y, 
     const uint32_t tiles_m = static_cast<uint32_t>((M + BM - 1) / BM);
     const uint32_t tiles_n = static_cast<uint32_t>((N + BN - 1) / BN);
     const uint32_t stages = uint32_t((K + FK - 1) / FK);
+    const uint32_t m = uint32_t(M), n = uint32_t(N), k = uint32_t(K);
+    const size_t pbytes = gemm_f32_partial_bytes(M, N, K);
+    if (fmt == kQ6_K && K % 256 == 0 && ws && ws_bytes >= q6k_split_bytes(M, K)) {
+        _Float16* xh = static_cast<_Float16*>(ws);
+        _Float16* xl = xh + M * K;
+        float* inv = reinterpret_cast<float*>(xl + M * K);
+        const size_t sb = q6k_split_bytes(M, K);
+        float* partial = ws_bytes >= sb + pbytes && pbytes ? reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + sb) : nullptr;
+        uint32_t ks = partial ? choose_ksplit_f32(tiles_m * tiles_n, stages) : 1u;
+        const uint32_t spw = ((stages + ks - 1) / ks + 7) / 8 * 8;  // whole super-blocks per split
+        ks = (stages + spw - 1) / spw;
+        hipLaunchKernelGGL(split_rows_kernel, dim3(m), dim3(kThreads), 0, stream, X, xh, xl, inv, k);
+        hipLaunchKernelGGL(gemm_q6k_h_kernel, dim3(tiles_m * tiles_n * ks), dim3(kThreads), 0, stream, w, xh, xl, inv,
+                           ks > 1 ? partial : Y, m, n, k, tiles_m, tiles_n, ks, spw);
+        if (launches) *launches = ks > 1 ? 3 : 2;
+        return finish_splits(hipGetLastError(), partial, Y, M, N, ks, stream);
+    }
+    float* partial = ws && pbytes && ws_bytes >= pbytes ? static_cast<float*>(ws) : nullptr;
     uint32_t ks = partial ? choose_ksplit_f32(tiles_m * tiles_n, stages) : 1u;
     const uint32_t spw = (stages + ks - 1) / ks;
     ks = (stages + spw - 1) / spw;  // no empty splits
     float* out = ks > 1 ? partial : Y;
     const dim3 grid(tiles_m * tiles_n * ks);
-    const uint32_t m = uint32_t(M), n = uint32_t(N), k = uint32_t(K);
     switch (fmt) {
     case kQ8_0:
         hipLaunchKernelGGL(gemm_f32_kernel<kQ8_0>, grid, dim3(kThreads), 0, stream, w, X, out, m, n, k, tiles_m, tiles_n, ks, spw);
@@ -1205,6 +1446,7 @@ hipError_t launch_gemm_f32(int fmt, const uint8_t* w, const float* X, float* Y, 
         break;
     default: return hipErrorInvalidValue;
     }
+    if (launches) *launches = ks > 1 ? 2 : 1;
     return finish_splits(hipGetLastError(), partial, Y, M, N, ks, stream);
 }
 

@@ -103,12 +103,15 @@ int device_cu_count();
 hipError_t launch_gemm_i8(int fmt, const uint8_t* w, const int8_t* xq, const float* xs,
                           float* Y, float* partial, size_t M, size_t N, size_t K, hipStream_t stream);
 
-// Prefill GEMM on fp32 activations (the reference CPU arithmetic).  `partial`
-// (gemm_f32_partial_bytes, may be null) is the split-K workspace; with
-// partial == nullptr the GEMM runs unsplit.
+// Prefill GEMM on fp32 activations (the reference CPU arithmetic).  `ws`
+// (ws_bytes, may be null) is the workspace: gemm_f32_workspace_bytes() lets
+// Q6_K run on the f16 MFMA (split activations) and any format split K; with
+// less the GEMM runs with what fits (fp32 MFMA, unsplit).  `launches`
+// (optional) receives the number of kernels enqueued.
 size_t gemm_f32_partial_bytes(size_t M, size_t N, size_t K);
-hipError_t launch_gemm_f32(int fmt, const uint8_t* w, const float* X, float* Y, float* partial, size_t M,
-                           size_t N, size_t K, hipStream_t stream);
+size_t gemm_f32_workspace_bytes(int fmt, size_t M, size_t N, size_t K);
+hipError_t launch_gemm_f32(int fmt, const uint8_t* w, const float* X, float* Y, void* ws, size_t ws_bytes, size_t M,
+                           size_t N, size_t K, hipStream_t stream, uint32_t* launches = nullptr);
 
 // Bit-exact tier helpers.
 hipError_t launch_dequantize(int fmt, const uint8_t* w, float* out, size_t rows, size_t cols,

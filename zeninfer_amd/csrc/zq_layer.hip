@@ -303,25 +303,6 @@ constexpr int kFRows = 64, kFKeys = 64;
 //    and O; the two waves of a row set merge at the end.
 // K is staged row-major and V transposed ([column][key], 8 keys of one
 // column per lane load group), both as f16 pairs; two barriers per key tile.
-typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
-typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4_attn_t __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ float pow2f(int e) { return __int_as_float((e + 127) << 23); }
-// exponent e with max |x| * 2^e in [2^14, 2^15); 0 for max 0.  Clamped to
-// [-40, 40]: a change of the V scale between tiles multiplies the running O by
-// at most 2^80, which stays finite.  Operands whose maximum lies below 2^-26
-// lose precision (f16 subnormals); above 2^56 they would overflow f16.
-__device__ __forceinline__ int split_exp(float amax) {
-    if (!(amax > 0.0f)) return 0;
-    return min(max(15 - __builtin_amdgcn_frexp_expf(amax), -40), 40);
-}
-// element i of h and l: h = f16(x), l = f16(x - h)
-template <class V>
-__device__ __forceinline__ void split_h(float x, V& h, V& l, int i) {
-    const _Float16 a = _Float16(x);
-    h[i] = a;
-    l[i] = _Float16(x - float(a));
-}
 constexpr int kFHP(int D) { return D + 8; }  // halves per padded K (and Q staging) row
 constexpr int kFKP = kFKeys + 8;             // halves per padded V^T row
 constexpr size_t attention_prefill_t_lds(int D) {

@@ -85,6 +85,7 @@ struct zq_model {
     int8_t* xq = nullptr;
     float* xs = nullptr;
     float* partial = nullptr;
+    size_t partial_bytes = 0;  // its size (GEMM split-K partials, split Q6_K activations)
     float* attn_part = nullptr;  // decode attention chunk partials
     float* qkv = nullptr;        // prefill output of the fused Q|K|V projection, [T][QW + 2 KW]
     void* argmax_part = nullptr;
@@ -155,7 +156,7 @@ bool alloc_runtime(zq_model& m, std::string& e) {
     for (uint32_t M = 1; M <= kPrefillChunk; ++M)
         for (auto nk : {std::pair<size_t, size_t>{QW, E}, {KW, E}, {QW + 2 * KW, E}, {E, QW}, {F, E}, {E, F}})
             partial = std::max({partial, zq::gemm_i8_partial_bytes(M, nk.first, nk.second),
-                                zq::gemm_f32_partial_bytes(M, nk.first, nk.second)});
+                                zq::gemm_f32_workspace_bytes(zq::kQ6_K, M, nk.first, nk.second)});
     const size_t xq_bytes = align_up(T * widest, kAlign), xs_bytes = align_up(T * widest / 32 * 4, kAlign);
     const size_t attn_bytes = align_up(zq::attention_decode_partial_floats(c.heads, c.head_dim, c.max_positions) * 4, kAlign);
     const size_t arg_bytes = align_up(zq::argmax_partial_bytes(), kAlign);
@@ -168,6 +169,7 @@ bool alloc_runtime(zq_model& m, std::string& e) {
     m.xq = reinterpret_cast<int8_t*>(p); p += xq_bytes;
     m.xs = reinterpret_cast<float*>(p); p += xs_bytes;
     m.partial = partial ? reinterpret_cast<float*>(p) : nullptr; p += align_up(partial, kAlign);
+    m.partial_bytes = partial;
     m.attn_part = reinterpret_cast<float*>(p); p += attn_bytes;
     if (hipMemset(m.attn_part, 0, attn_bytes) != hipSuccess) { e = "device memset failed (attention counters)"; return false; }
     m.argmax_part = p; p += arg_bytes;
@@ -229,7 +231,7 @@ bool init_common(zq_model& m, std::string& e) {
 // into xq/xs when `quantized` (int8 mode).
 hipError_t project(zq_model& m, const Weight& w, const float* X, float* Y, uint32_t M, bool quantized) {
     if (quantized) return zq::launch_gemm_i8(w.fmt, w.p, m.xq, m.xs, Y, m.partial, M, w.rows, w.cols, m.stream);
-    return zq::launch_gemm_f32(w.fmt, w.p, X, Y, m.partial, M, w.rows, w.cols, m.stream);
+    return zq::launch_gemm_f32(w.fmt, w.p, X, Y, m.partial, m.partial_bytes, M, w.rows, w.cols, m.stream);
 }
 
 bool int8_ok(int fmt) { return fmt == zq::kQ8_0 || fmt == zq::kQ4_0; }
