@@ -197,8 +197,10 @@ int zq_hip_gemv_batch_dev(int fmt, const float* x, const zq_gemv_task* tasks, si
                           void* stream);
 /* Workspace (device bytes) a zq_hip_gemm_dev call needs: int8 activations,
  * their scales and, for small grids, split-K partial sums (ZQ_ACT_INT8);
- * split-K partial sums for small grids, else 0 (ZQ_ACT_F32: a smaller or
- * null workspace runs the fp32 GEMM unsplit). */
+ * with fp32 activations, Q6_K's split activations (f16 hi + lo, row scales;
+ * they let it run on the f16 MFMA) and split-K partial sums for small grids,
+ * else 0 (a smaller or null workspace runs with what fits: the fp32 MFMA,
+ * unsplit). */
 size_t zq_hip_gemm_workspace_bytes(int fmt, size_t tokens, size_t rows, size_t cols, int act_mode);
 int zq_hip_gemm_dev(int fmt, const void* weights, const float* X, float* Y, size_t tokens, size_t rows,
                     size_t cols, int act_mode, void* workspace, size_t workspace_bytes, void* stream);

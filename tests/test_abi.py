@@ -65,10 +65,15 @@ def test_argument_errors_without_device():
     assert ws >= 4 * 4096 + 4 * 128 * 4 and ws % 4 == 0
     assert L.zq_hip_gemm_workspace_bytes(zq.Q8_0, 2048, 14336, 4096, zq.ACT_INT8) == 2048 * 4096 + 2048 * 128 * 4
     # fp32 activations: split-K partial sums (whole fp32 [M][N] planes) for small grids only
-    for fmt, act in ((zq.Q8_0, zq.ACT_F32), (zq.Q6_K, zq.ACT_DEFAULT)):
-        ws = L.zq_hip_gemm_workspace_bytes(fmt, 4, 4096, 4096, act)
-        assert ws > 0 and ws % (4 * 4096 * 4) == 0
-        assert L.zq_hip_gemm_workspace_bytes(fmt, 2048, 14336, 4096, act) == 0
+    ws = L.zq_hip_gemm_workspace_bytes(zq.Q8_0, 4, 4096, 4096, zq.ACT_F32)
+    assert ws > 0 and ws % (4 * 4096 * 4) == 0
+    assert L.zq_hip_gemm_workspace_bytes(zq.Q8_0, 2048, 14336, 4096, zq.ACT_F32) == 0
+    # Q6_K also holds its split activations: f16 hi + lo [M][K] and the row
+    # scales, 256-byte aligned, ahead of the partial sums
+    split = lambda m, k: (m * k * 4 + m * 4 + 255) // 256 * 256
+    ws = L.zq_hip_gemm_workspace_bytes(zq.Q6_K, 4, 4096, 4096, zq.ACT_DEFAULT)
+    assert ws > split(4, 4096) and (ws - split(4, 4096)) % (4 * 4096 * 4) == 0
+    assert L.zq_hip_gemm_workspace_bytes(zq.Q6_K, 2048, 14336, 4096, zq.ACT_DEFAULT) == split(2048, 4096)
 
 
 def test_opt_in_semantics(monkeypatch):
