@@ -59,6 +59,7 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 INT8_PEAK_TOPS = 5000.0        # MI355X dense int8 MFMA (POP/s x 1000)
 FP32_PEAK_TFLOPS = 157.3       # MI355X dense fp32 MFMA
+F16_PEAK_TFLOPS = 2500.0       # MI355X dense fp16 / bf16 MFMA
 
 HIDDEN, FFN, KV, VOCAB, LAYERS = 4096, 14336, 1024, 128256, 32
 
@@ -333,9 +334,17 @@ def format_sweep(torch, zq, dev):
             ms = timed_launches_on(torch, lambda i: zq.gemm_dev(fmt, ws[i % nrep], X[: 512 * K], Y, 512, N, K, act,
                                                                 wsp, wsb), 2 * nrep, 2)
             tops = 2.0 * 512 * N * K / (ms * 1e-3) / 1e12
+            # the MFMA each path runs on: int8; Q6_K's split-f16 products (three
+            # f16 MFMA products per multiply-add); the fp32 MFMA otherwise
+            if act == zq.ACT_INT8:
+                peak, mfma = INT8_PEAK_TOPS, "int8"
+            elif fmt == zq.Q6_K:
+                peak, mfma = F16_PEAK_TFLOPS / 3.0, "f16 x3 (split operands)"
+            else:
+                peak, mfma = FP32_PEAK_TFLOPS, "fp32"
             entry.update({"gemm_M512_ms": round(ms, 4), "gemm_M512_TOPS": round(tops, 1),
-                          "gemm_act": "int8" if act == zq.ACT_INT8 else "f32",
-                          "gemm_frac_peak": round(tops / (INT8_PEAK_TOPS if act == zq.ACT_INT8 else FP32_PEAK_TFLOPS), 4)})
+                          "gemm_act": "int8" if act == zq.ACT_INT8 else "f32", "gemm_mfma": mfma,
+                          "gemm_frac_peak": round(tops / peak, 4)})
             res[shape] = entry
             del ws
             torch.cuda.empty_cache()

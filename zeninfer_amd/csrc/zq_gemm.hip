@@ -1015,7 +1015,7 @@ __global__ __launch_bounds__(kThreads) void split_rows_kernel(const float* __res
 
 // Split K as in gemm_f32_kernel; stages_per_split is a multiple of the 8
 // stages of a super-block.
-__global__ __launch_bounds__(kThreads) void gemm_q6k_h_kernel(const uint8_t* __restrict__ W, const _Float16* __restrict__ XH,
+__global__ __launch_bounds__(kThreads, 2) void gemm_q6k_h_kernel(const uint8_t* __restrict__ W, const _Float16* __restrict__ XH,
                                                               const _Float16* __restrict__ XL,
                                                               const float* __restrict__ xinv, float* __restrict__ Y,
                                                               uint32_t M, uint32_t N, uint32_t K, uint32_t tiles_m,
