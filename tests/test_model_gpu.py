@@ -168,7 +168,7 @@ def test_synthetic_model_runs(zq):
     m.close()
 
 
-@pytest.mark.parametrize("ptype", [G.GGML_Q4_K, G.GGML_Q5_K])
+@pytest.mark.parametrize("ptype", [G.GGML_Q4_K, G.GGML_Q5_K, G.GGML_Q6_K])
 def test_kquant_model_matches_reference(tmp_path, zq, ptype):
     """A Q4_K / Q5_K llama (projections and output K-quants, Q8_0 embedding):
     prefill and decode logits of the device model within the fp32 bar of the
