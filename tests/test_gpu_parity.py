@@ -230,13 +230,15 @@ def test_gemm_f32(zq, orc, fmt, m, n, k):
 
 # The BASELINE configs' own GEMM workloads at full size: config 2 (Q8_0, int8
 # activations, M = 32 / 128 / 512 / 2048 on both FFN shapes) and config 3
-# (Q4_0 int8 and Q6_K fp32 at M = 512).  Rows and tokens are independent, so
+# (Q4_0 int8 and Q6_K fp32 at M = 512), plus the Q4_K / Q5_K fp32 path at
+# M = 512.  Rows and tokens are independent, so
 # sampled (token, row) outputs are checked against the oracle.
 _FULL_GEMM = [(O.Q8_0, 1, 2048, 14336, 4096), (O.Q8_0, 1, 32, 4096, 14336),
               (O.Q8_0, 1, 128, 14336, 4096), (O.Q8_0, 1, 128, 4096, 14336),
               (O.Q8_0, 1, 512, 14336, 4096), (O.Q8_0, 1, 512, 4096, 14336),
               (O.Q4_0, 1, 512, 14336, 4096), (O.Q4_0, 1, 512, 4096, 14336),
-              (O.Q6_K, 2, 512, 14336, 4096), (O.Q6_K, 2, 512, 4096, 14336)]
+              (O.Q6_K, 2, 512, 14336, 4096), (O.Q6_K, 2, 512, 4096, 14336),
+              (O.Q4_K, 2, 512, 14336, 4096), (O.Q4_K, 2, 512, 4096, 14336), (O.Q5_K, 2, 512, 4096, 14336)]
 
 
 @pytest.mark.parametrize("fmt,act,m,n,k", _FULL_GEMM)

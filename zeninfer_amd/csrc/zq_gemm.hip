@@ -34,6 +34,7 @@
 #include "zq_internal.hpp"
 
 #include <algorithm>
+#include <type_traits>
 #include <cmath>
 #include <cstdlib>
 
@@ -956,19 +957,25 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(const uint8_t* __res
         }
 }
 
-// ------------------------------------------------ Q6_K on the f16 MFMA ---
-// The fp32-activation Q6_K GEMM with its products on v_mfma_f32_32x32x16_f16
-// (16x the fp32 MFMA rate) at fp32-level accuracy:
+// ------------------------------------------- K-quants on the f16 MFMA ---
+// The fp32-activation GEMM of the super-block formats (Q6_K, Q4_K, Q5_K)
+// with its products on v_mfma_f32_32x32x16_f16 (16x the fp32 MFMA rate) at
+// fp32-level accuracy:
 //  * each activation row is scaled by a power of two (split_rows_kernel) and
-//    carried as f16 hi + lo;
-//  * each weight is the integer sc * q of its 16-element group (|sc*q| <=
-//    4096), carried as h = f16(sc*q) and l = sc*q - h (nonzero only past
-//    2048), both exact;
-//  * a product is Xh*Wh + Xl*Wh + Xh*Wl, accumulated in fp32 over a
-//    super-block (256 K), then scaled by the super-block's d and added to
-//    the output; the row scale comes off at the end.
-// Against the reference's (d*sc)*q times x in fp32 the difference is
-// rounding order plus the dropped Xl*Wl (below 2^-22 of the row maximum).
+//    carried as f16 hi + lo; for Q4_K / Q5_K also the sum of each 32-element
+//    group (scaled by 2^-5, hi + lo);
+//  * each weight is the integer sc*q of its group (Q6_K: 16 elements,
+//    sc int8, q - 32 in -32..31, |sc*q| <= 4096, carried as h = f16(sc*q) and
+//    l = sc*q - h, nonzero only past 2048; Q4_K / Q5_K: 32 elements, sc
+//    6-bit, q 0..15 / 0..31, |sc*q| <= 1953, one exact f16);
+//  * a product is Xh*Wh + Xl*Wh (+ Xh*Wl for Q6_K), accumulated in fp32 over
+//    a super-block (256 K), then scaled by the super-block's d; Q4_K / Q5_K
+//    subtract dmin * sum_j m_j * sum(x in group j), whose inner sum is one
+//    more MFMA pair (group sums against the 8 mins); the row scale comes
+//    off at the end.
+// Against the reference's dequantise-then-fp32 arithmetic the difference is
+// rounding order plus the dropped lo*lo products (below 2^-22 of the row
+// maximum).
 // A workgroup barrier that orders LDS only: unlike __syncthreads it does not
 // wait for the wave's outstanding global loads (a prefetch stays in flight).
 __device__ __forceinline__ void lds_barrier() {
@@ -979,8 +986,11 @@ __device__ __forceinline__ void lds_barrier() {
 constexpr int HK = 32;          // K elements per stage
 constexpr int HROW = HK + 8;    // halves per LDS row (pad: 16 B)
 
+// One workgroup per row.  xsh / xsl (optional): the row's 32-element group
+// sums of the scaled values, times 2^-5, as f16 hi + lo ([M][K / 32]).
 __global__ __launch_bounds__(kThreads) void split_rows_kernel(const float* __restrict__ X, _Float16* __restrict__ xh,
                                                               _Float16* __restrict__ xl, float* __restrict__ inv,
+                                                              _Float16* __restrict__ xsh, _Float16* __restrict__ xsl,
                                                               uint32_t K) {
     __shared__ float red[kThreads / 64];
     const float4* r = reinterpret_cast<const float4*>(X + size_t(blockIdx.x) * K);
@@ -1001,30 +1011,54 @@ __global__ __launch_bounds__(kThreads) void split_rows_kernel(const float* __res
     if (threadIdx.x == 0) inv[blockIdx.x] = pow2f(-e);
     h4_t* oh = reinterpret_cast<h4_t*>(xh + size_t(blockIdx.x) * K);
     h4_t* ol = reinterpret_cast<h4_t*>(xl + size_t(blockIdx.x) * K);
-    for (uint32_t i = threadIdx.x; i < K4; i += kThreads) {
-        const float4 v = r[i];
-        h4_t h, l;
-        split_h(v.x * f, h, l, 0);
-        split_h(v.y * f, h, l, 1);
-        split_h(v.z * f, h, l, 2);
-        split_h(v.w * f, h, l, 3);
-        oh[i] = h;
-        ol[i] = l;
+    for (uint32_t i0 = 0; i0 < K4; i0 += kThreads) {  // K % 1024 == 0 is not assumed: whole 8-lane groups
+        const uint32_t i = i0 + threadIdx.x;
+        const bool live = i < K4;
+        const float4 v = live ? r[i] : make_float4(0, 0, 0, 0);
+        const float4 sv = make_float4(v.x * f, v.y * f, v.z * f, v.w * f);
+        if (live) {
+            h4_t h, l;
+            split_h(sv.x, h, l, 0);
+            split_h(sv.y, h, l, 1);
+            split_h(sv.z, h, l, 2);
+            split_h(sv.w, h, l, 3);
+            oh[i] = h;
+            ol[i] = l;
+        }
+        if (xsh) {  // 8 consecutive lanes hold one 32-element group (K % 32 == 0)
+            float t = (sv.x + sv.y) + (sv.z + sv.w);
+            t += __shfl_xor(t, 1);
+            t += __shfl_xor(t, 2);
+            t += __shfl_xor(t, 4);
+            if (live && (i & 7u) == 0) {
+                const float ts = t * 0.03125f;  // |t| <= 2^20: into the f16 range
+                const _Float16 th = _Float16(ts);
+                xsh[size_t(blockIdx.x) * (K / 32) + i / 8] = th;
+                xsl[size_t(blockIdx.x) * (K / 32) + i / 8] = _Float16(ts - float(th));
+            }
+        }
     }
 }
 
 // Split K as in gemm_f32_kernel; stages_per_split is a multiple of the 8
 // stages of a super-block.
-__global__ __launch_bounds__(kThreads, 2) void gemm_q6k_h_kernel(const uint8_t* __restrict__ W, const _Float16* __restrict__ XH,
-                                                              const _Float16* __restrict__ XL,
-                                                              const float* __restrict__ xinv, float* __restrict__ Y,
-                                                              uint32_t M, uint32_t N, uint32_t K, uint32_t tiles_m,
-                                                              uint32_t tiles_n, uint32_t ksplit,
-                                                              uint32_t stages_per_split) {
+template <int FMT>
+__global__ __launch_bounds__(kThreads, 2) void gemm_kq_h_kernel(const uint8_t* __restrict__ W,
+                                                                 const _Float16* __restrict__ XH,
+                                                                 const _Float16* __restrict__ XL,
+                                                                 const float* __restrict__ xinv,
+                                                                 const _Float16* __restrict__ XSH,
+                                                                 const _Float16* __restrict__ XSL, float* __restrict__ Y,
+                                                                 uint32_t M, uint32_t N, uint32_t K, uint32_t tiles_m,
+                                                                 uint32_t tiles_n, uint32_t ksplit,
+                                                                 uint32_t stages_per_split) {
+    static_assert(FMT == kQ6_K || FMT == kQ4_K || FMT == kQ5_K, "super-block formats");
+    constexpr bool Q6 = FMT == kQ6_K;
+    constexpr uint32_t BB = FMT == kQ6_K ? 210 : (FMT == kQ5_K ? 176 : 144);
     __shared__ __align__(16) _Float16 Ah[BM * HROW];
     __shared__ __align__(16) _Float16 Al[BM * HROW];
     __shared__ __align__(16) _Float16 Bh[BN * HROW];
-    __shared__ __align__(16) _Float16 Bl[BN * HROW];
+    __shared__ __align__(16) _Float16 Bl[Q6 ? BN * HROW : 8];
     const uint32_t total_tiles = tiles_m * tiles_n;
     const uint32_t split = blockIdx.x / total_tiles;
     uint32_t tm, tn;
@@ -1033,7 +1067,8 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q6k_h_kernel(const uint8_t* 
     const uint32_t k_begin = split * stages_per_split * HK;
     const uint32_t k_end = min(K, k_begin + stages_per_split * HK);
     float* Yout = Y + (ksplit > 1 ? size_t(split) * M * N : 0);
-    const size_t rb = row_bytes_dev(kQ6_K, K);
+    const size_t rb = row_bytes_dev(FMT, K);
+    const uint32_t ng = K / 32;  // 32-element groups per row
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
@@ -1042,9 +1077,10 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q6k_h_kernel(const uint8_t* 
     const _Float16* ah_src = XH + size_t(min(m0 + ld_row, M - 1)) * K + ld_half * 16;
     const _Float16* al_src = XL + size_t(min(m0 + ld_row, M - 1)) * K + ld_half * 16;
     const uint8_t* b_src = W + size_t(min(n0 + ld_row, N - 1)) * rb;
-    const uint8_t* d_src[2];  // this lane's two output columns
+    const uint8_t* c_src[2];  // this lane's two output columns (weight rows)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) d_src[j] = W + size_t(min(n0 + wn * 64 + j * 32 + l32, N - 1)) * rb + 208;
+    for (int j = 0; j < 2; ++j) c_src[j] = W + size_t(min(n0 + wn * 64 + j * 32 + l32, N - 1)) * rb;
+    const uint32_t xrow[2] = {min(m0 + wm * 64 + l32, M - 1), min(m0 + wm * 64 + 32 + l32, M - 1)};
 
     v16f acc[2][2], part[2][2];
 #pragma unroll
@@ -1053,35 +1089,69 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q6k_h_kernel(const uint8_t* 
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = part[i][j][v] = 0.0f;
-    float dj[2] = {0.0f, 0.0f};
 
-    // Raw stage data of this thread: 16 activations (hi, lo), the 16 weights'
-    // low-nibble and high-bit words and their group's scale.  The next stage's
-    // are loaded while the current one is converted and multiplied.
-    struct Raw {
+    // Raw stage data of this thread: 16 activations (hi, lo) and the words of
+    // its 16 weights; of this lane's output columns the super-block's d (and
+    // dmin, the packed scale bytes, and its rows' group sums for Q4_K / Q5_K).
+    // The next stage's are loaded while the current one is converted and
+    // multiplied.
+    struct RawQ6 {
         uint4 xa0, xa1, xb0, xb1;
-        uint32_t lw[4], hw[4];
+        uint32_t qw[4], hw[4];
         int sc;
-        uint32_t dbits[2];  // d of the super-block, this lane's two output columns
+        uint32_t dbits[2];
     };
+    struct RawK : RawQ6 {
+        uint32_t sbytes[2][3];
+        uint4 xs[2][2];
+    };
+    using Raw = std::conditional_t<Q6, RawQ6, RawK>;
     auto load_raw = [&](uint32_t k0, Raw& r) {
         r.xa0 = *reinterpret_cast<const uint4*>(ah_src + k0);
         r.xa1 = *reinterpret_cast<const uint4*>(ah_src + k0 + 8);
         r.xb0 = *reinterpret_cast<const uint4*>(al_src + k0);
         r.xb1 = *reinterpret_cast<const uint4*>(al_src + k0 + 8);
-        const uint8_t* p = b_src + size_t(k0 >> 8) * 210;
+        const uint8_t* p = b_src + size_t(k0 >> 8) * BB;
         const uint32_t in_sb = k0 & 255u;
-        const uint32_t h = in_sb >> 7, grp = (in_sb >> 5) & 3u;
-        r.sc = int(reinterpret_cast<const int8_t*>(p + 192)[h * 8 + grp * 2 + ld_half]);
-        const uint8_t* lo = p + h * 64 + (grp & 1u) * 32 + ld_half * 16;
-        const uint8_t* hi = p + 128 + h * 32 + ld_half * 16;
+        if constexpr (Q6) {
+            const uint32_t h = in_sb >> 7, grp = (in_sb >> 5) & 3u;
+            r.sc = int(reinterpret_cast<const int8_t*>(p + 192)[h * 8 + grp * 2 + ld_half]);
+            const uint8_t* lo = p + h * 64 + (grp & 1u) * 32 + ld_half * 16;
+            const uint8_t* hi = p + 128 + h * 32 + ld_half * 16;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            r.lw[i] = load_u32_a2(lo + 4 * i);
-            r.hw[i] = load_u32_a2(hi + 4 * i);
+            for (int i = 0; i < 4; ++i) {
+                r.qw[i] = load_u32_a2(lo + 4 * i);
+                r.hw[i] = load_u32_a2(hi + 4 * i);
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j) r.dbits[j] = *reinterpret_cast<const uint16_t*>(c_src[j] + size_t(k0 >> 8) * BB + 208);
+        } else {
+            const uint32_t g = in_sb >> 5;
+            uint32_t sc, mn;
+            kquant_scale_min(p + 4, g, sc, mn);
+            r.sc = int(sc);
+            const uint32_t* qs = reinterpret_cast<const uint32_t*>(p + (FMT == kQ5_K ? 48 : 16) + (g >> 1) * 32 + ld_half * 16);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) r.qw[i] = qs[i];
+            if constexpr (FMT == kQ5_K) {
+                const uint32_t* qh = reinterpret_cast<const uint32_t*>(p + 16 + ld_half * 16);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) r.hw[i] = qh[i];
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const uint8_t* c = c_src[j] + size_t(k0 >> 8) * BB;
+                r.dbits[j] = *reinterpret_cast<const uint32_t*>(c);  // d | dmin << 16
+#pragma unroll
+                for (int t = 0; t < 3; ++t) r.sbytes[j][t] = reinterpret_cast<const uint32_t*>(c + 4)[t];
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {  // the 8 group sums of the super-block, lanes of the first half only
+                const size_t o = size_t(xrow[i]) * ng + (k0 >> 5 & ~7u);
+                r.xs[i][0] = lh == 0 ? *reinterpret_cast<const uint4*>(XSH + o) : make_uint4(0, 0, 0, 0);
+                r.xs[i][1] = lh == 0 ? *reinterpret_cast<const uint4*>(XSL + o) : make_uint4(0, 0, 0, 0);
+            }
         }
-#pragma unroll
-        for (int j = 0; j < 2; ++j) r.dbits[j] = *reinterpret_cast<const uint16_t*>(d_src[j] + size_t(k0 >> 8) * 210);
     };
     Raw cur, nxt;
     if (k_begin < k_end) load_raw(k_begin, cur);
@@ -1089,24 +1159,42 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q6k_h_kernel(const uint8_t* 
         // unconditional (the last stage reloads itself), so the wait for the
         // current stage's data counts the prefetch statically
         load_raw(min(k0 + HK, k_end - HK), nxt);
+        float dj[2], mj[2];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) dj[j] = half_bits_to_float(cur.dbits[j]);
+        for (int j = 0; j < 2; ++j) {
+            dj[j] = half_bits_to_float(cur.dbits[j] & 0xffffu);
+            mj[j] = -32.0f * half_bits_to_float(cur.dbits[j] >> 16);  // the group sums carry 2^-5
+        }
         const uint4 xa0 = cur.xa0, xa1 = cur.xa1, xb0 = cur.xb0, xb1 = cur.xb1;
         h8_t wh0, wl0, wh1, wl1;
         {
-            const uint32_t grp = ((k0 & 255u) >> 5) & 3u;
+            const uint32_t in_sb = k0 & 255u;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const uint32_t lw = cur.lw[i], hw = cur.hw[i];
+                const uint32_t qw = cur.qw[i];
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
-                    uint32_t l = (lw >> (8 * k)) & 0xffu;
-                    if (grp >= 2) l >>= 4;
-                    const uint32_t hb = ((hw >> (8 * k)) >> (2 * grp)) & 3u;
-                    const float v = float(cur.sc * (int((l & 15u) | (hb << 4)) - 32));  // exact integer
+                    int q;
+                    if constexpr (Q6) {
+                        const uint32_t grp = (in_sb >> 5) & 3u;
+                        uint32_t l = (qw >> (8 * k)) & 0xffu;
+                        if (grp >= 2) l >>= 4;
+                        const uint32_t hb = ((cur.hw[i] >> (8 * k)) >> (2 * grp)) & 3u;
+                        q = int((l & 15u) | (hb << 4)) - 32;
+                    } else {
+                        const uint32_t g = in_sb >> 5;
+                        q = int((qw >> (8 * k + 4 * (g & 1u))) & 15u);
+                        if constexpr (FMT == kQ5_K) q |= int(((cur.hw[i] >> (8 * k + g)) & 1u) << 4);
+                    }
+                    const float v = float(cur.sc * q);  // exact integer
                     const int e = 4 * i + k;
-                    if (e < 8) split_h(v, wh0, wl0, e);
-                    else split_h(v, wh1, wl1, e - 8);
+                    if constexpr (Q6) {
+                        if (e < 8) split_h(v, wh0, wl0, e);
+                        else split_h(v, wh1, wl1, e - 8);
+                    } else {
+                        if (e < 8) wh0[e] = _Float16(v);
+                        else wh1[e - 8] = _Float16(v);
+                    }
                 }
             }
         }
@@ -1117,8 +1205,10 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q6k_h_kernel(const uint8_t* 
         *reinterpret_cast<uint4*>(Al + ld_row * HROW + ld_half * 16 + 8) = xb1;
         *reinterpret_cast<h8_t*>(Bh + ld_row * HROW + ld_half * 16) = wh0;
         *reinterpret_cast<h8_t*>(Bh + ld_row * HROW + ld_half * 16 + 8) = wh1;
-        *reinterpret_cast<h8_t*>(Bl + ld_row * HROW + ld_half * 16) = wl0;
-        *reinterpret_cast<h8_t*>(Bl + ld_row * HROW + ld_half * 16 + 8) = wl1;
+        if constexpr (Q6) {
+            *reinterpret_cast<h8_t*>(Bl + ld_row * HROW + ld_half * 16) = wl0;
+            *reinterpret_cast<h8_t*>(Bl + ld_row * HROW + ld_half * 16 + 8) = wl1;
+        }
         lds_barrier();
 #pragma unroll
         for (int ks = 0; ks < HK / 16; ++ks) {
@@ -1133,7 +1223,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q6k_h_kernel(const uint8_t* 
             for (int j = 0; j < 2; ++j) {
                 const int r = (wn * 64 + j * 32 + l32) * HROW + ks * 16 + 8 * lh;
                 bh[j] = *reinterpret_cast<const h8_t*>(Bh + r);
-                bl[j] = *reinterpret_cast<const h8_t*>(Bl + r);
+                if constexpr (Q6) bl[j] = *reinterpret_cast<const h8_t*>(Bl + r);
             }
 #pragma unroll
             for (int i = 0; i < 2; ++i)
@@ -1141,19 +1231,46 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q6k_h_kernel(const uint8_t* 
                 for (int j = 0; j < 2; ++j) {
                     part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bh[j], part[i][j], 0, 0, 0);
                     part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], bh[j], part[i][j], 0, 0, 0);
-                    part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bl[j], part[i][j], 0, 0, 0);
+                    if constexpr (Q6) part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bl[j], part[i][j], 0, 0, 0);
                 }
         }
-        if (((k0 + HK) & 255u) == 0 || k0 + HK >= k_end) {  // end of a super-block: scale by its d
+        if (((k0 + HK) & 255u) == 0 || k0 + HK >= k_end) {  // end of a super-block
+            h8_t bmin[2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                if constexpr (!Q6) {  // the 8 mins of the column's super-block (k slots 0..7; 8..15 zero)
+                    uint8_t sb[12];
+#pragma unroll
+                    for (int t = 0; t < 12; ++t) sb[t] = uint8_t(cur.sbytes[j][t >> 2] >> (8 * (t & 3)));
+#pragma unroll
+                    for (int g = 0; g < 8; ++g) {
+                        uint32_t sc, mn;
+                        kquant_scale_min(sb, uint32_t(g), sc, mn);
+                        bmin[j][g] = lh == 0 ? _Float16(float(mn)) : _Float16(0.0f);
+                    }
+                }
+            }
 #pragma unroll
             for (int i = 0; i < 2; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
+                for (int j = 0; j < 2; ++j) {
+                    v16f cm;
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) cm[v] = 0.0f;
+                    if constexpr (!Q6) {
+                        const h8_t xsh = __builtin_bit_cast(h8_t, cur.xs[i][0]);
+                        const h8_t xsl = __builtin_bit_cast(h8_t, cur.xs[i][1]);
+                        cm = __builtin_amdgcn_mfma_f32_32x32x16_f16(xsh, bmin[j], cm, 0, 0, 0);
+                        cm = __builtin_amdgcn_mfma_f32_32x32x16_f16(xsl, bmin[j], cm, 0, 0, 0);
+                    }
 #pragma unroll
                     for (int v = 0; v < 16; ++v) {
-                        acc[i][j][v] = fmaf(part[i][j][v], dj[j], acc[i][j][v]);
+                        float t = fmaf(part[i][j][v], dj[j], acc[i][j][v]);
+                        if constexpr (!Q6) t = fmaf(cm[v], mj[j], t);
+                        acc[i][j][v] = t;
                         part[i][j][v] = 0.0f;
                     }
+                }
         }
         cur = nxt;
     }
@@ -1386,14 +1503,18 @@ size_t gemm_f32_partial_bytes(size_t M, size_t N, size_t K) {
     return ks > 1 ? size_t(ks) * M * N * sizeof(float) : 0;
 }
 
-// Q6_K on the f16 MFMA: the split activations (hi and lo halves, [M][K] each)
-// and the row scales come first in the workspace.
-static size_t q6k_split_bytes(size_t M, size_t K) {
-    return (M * K * 2 * sizeof(_Float16) + M * sizeof(float) + 255) / 256 * 256;
+// The super-block formats on the f16 MFMA: the split activations (hi and lo
+// halves, [M][K] each), the row scales and (Q4_K / Q5_K) the split group sums
+// ([M][K / 32] each) come first in the workspace, 256-byte aligned sections.
+static bool kq_f16(int fmt, size_t K) { return (fmt == kQ6_K || fmt == kQ4_K || fmt == kQ5_K) && K % 256 == 0; }
+static size_t a256(size_t v) { return (v + 255) / 256 * 256; }
+static size_t kq_split_bytes(int fmt, size_t M, size_t K) {
+    const size_t base = a256(M * K * 2 * sizeof(_Float16) + M * sizeof(float));
+    return fmt == kQ6_K ? base : base + 2 * a256(M * (K / 32) * sizeof(_Float16));
 }
 
 size_t gemm_f32_workspace_bytes(int fmt, size_t M, size_t N, size_t K) {
-    return (fmt == kQ6_K && K % 256 == 0 ? q6k_split_bytes(M, K) : 0) + gemm_f32_partial_bytes(M, N, K);
+    return (kq_f16(fmt, K) ? kq_split_bytes(fmt, M, K) : 0) + gemm_f32_partial_bytes(M, N, K);
 }
 
 hipError_t launch_gemm_f32(int fmt, const uint8_t* w, const float* X, float* Y, void* ws, size_t ws_bytes, size_t M,
@@ -1407,18 +1528,31 @@ hipError_t launch_gemm_f32(int fmt, const uint8_t* w, const float* X, float* Y, 
     const uint32_t stages = uint32_t((K + FK - 1) / FK);
     const uint32_t m = uint32_t(M), n = uint32_t(N), k = uint32_t(K);
     const size_t pbytes = gemm_f32_partial_bytes(M, N, K);
-    if (fmt == kQ6_K && K % 256 == 0 && ws && ws_bytes >= q6k_split_bytes(M, K)) {
-        _Float16* xh = static_cast<_Float16*>(ws);
+    if (kq_f16(fmt, K) && ws && ws_bytes >= kq_split_bytes(fmt, M, K) && !(reinterpret_cast<uintptr_t>(ws) & 255u)) {
+        uint8_t* b = static_cast<uint8_t*>(ws);
+        _Float16* xh = reinterpret_cast<_Float16*>(b);
         _Float16* xl = xh + M * K;
         float* inv = reinterpret_cast<float*>(xl + M * K);
-        const size_t sb = q6k_split_bytes(M, K);
-        float* partial = ws_bytes >= sb + pbytes && pbytes ? reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + sb) : nullptr;
+        const size_t base = a256(M * K * 2 * sizeof(_Float16) + M * sizeof(float));
+        _Float16* xsh = fmt == kQ6_K ? nullptr : reinterpret_cast<_Float16*>(b + base);
+        _Float16* xsl = fmt == kQ6_K ? nullptr : reinterpret_cast<_Float16*>(b + base + a256(M * (K / 32) * 2));
+        const size_t sb = kq_split_bytes(fmt, M, K);
+        float* partial = ws_bytes >= sb + pbytes && pbytes ? reinterpret_cast<float*>(b + sb) : nullptr;
         uint32_t ks = partial ? choose_ksplit_f32(tiles_m * tiles_n, stages) : 1u;
         const uint32_t spw = ((stages + ks - 1) / ks + 7) / 8 * 8;  // whole super-blocks per split
         ks = (stages + spw - 1) / spw;
-        hipLaunchKernelGGL(split_rows_kernel, dim3(m), dim3(kThreads), 0, stream, X, xh, xl, inv, k);
-        hipLaunchKernelGGL(gemm_q6k_h_kernel, dim3(tiles_m * tiles_n * ks), dim3(kThreads), 0, stream, w, xh, xl, inv,
-                           ks > 1 ? partial : Y, m, n, k, tiles_m, tiles_n, ks, spw);
+        float* out = ks > 1 ? partial : Y;
+        const dim3 grid(tiles_m * tiles_n * ks);
+        hipLaunchKernelGGL(split_rows_kernel, dim3(m), dim3(kThreads), 0, stream, X, xh, xl, inv, xsh, xsl, k);
+        if (fmt == kQ6_K)
+            hipLaunchKernelGGL(gemm_kq_h_kernel<kQ6_K>, grid, dim3(kThreads), 0, stream, w, xh, xl, inv, xsh, xsl, out, m, n,
+                               k, tiles_m, tiles_n, ks, spw);
+        else if (fmt == kQ4_K)
+            hipLaunchKernelGGL(gemm_kq_h_kernel<kQ4_K>, grid, dim3(kThreads), 0, stream, w, xh, xl, inv, xsh, xsl, out, m, n,
+                               k, tiles_m, tiles_n, ks, spw);
+        else
+            hipLaunchKernelGGL(gemm_kq_h_kernel<kQ5_K>, grid, dim3(kThreads), 0, stream, w, xh, xl, inv, xsh, xsl, out, m, n,
+                               k, tiles_m, tiles_n, ks, spw);
         if (launches) *launches = ks > 1 ? 3 : 2;
         return finish_splits(hipGetLastError(), partial, Y, M, N, ks, stream);
     }

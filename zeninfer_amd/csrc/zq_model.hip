@@ -156,7 +156,7 @@ bool alloc_runtime(zq_model& m, std::string& e) {
     for (uint32_t M = 1; M <= kPrefillChunk; ++M)
         for (auto nk : {std::pair<size_t, size_t>{QW, E}, {KW, E}, {QW + 2 * KW, E}, {E, QW}, {F, E}, {E, F}})
             partial = std::max({partial, zq::gemm_i8_partial_bytes(M, nk.first, nk.second),
-                                zq::gemm_f32_workspace_bytes(zq::kQ6_K, M, nk.first, nk.second)});
+                                zq::gemm_f32_workspace_bytes(zq::kQ4_K, M, nk.first, nk.second)});
     const size_t xq_bytes = align_up(T * widest, kAlign), xs_bytes = align_up(T * widest / 32 * 4, kAlign);
     const size_t attn_bytes = align_up(zq::attention_decode_partial_floats(c.heads, c.head_dim, c.max_positions) * 4, kAlign);
     const size_t arg_bytes = align_up(zq::argmax_partial_bytes(), kAlign);
