@@ -1059,6 +1059,11 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kq_h_kernel(const uint8_t* _
     __shared__ __align__(16) _Float16 Al[BM * HROW];
     __shared__ __align__(16) _Float16 Bh[BN * HROW];
     __shared__ __align__(16) _Float16 Bl[Q6 ? BN * HROW : 8];
+    // Q4_K / Q5_K: per super-block, slot g holds group g's activation sums
+    // (hi, lo) of each tile row and its min m_g of each weight row
+    __shared__ __align__(16) _Float16 Gsh[Q6 ? 8 : BM * 8];
+    __shared__ __align__(16) _Float16 Gsl[Q6 ? 8 : BM * 8];
+    __shared__ __align__(16) _Float16 Bmin[Q6 ? 8 : BN * 8];
     const uint32_t total_tiles = tiles_m * tiles_n;
     const uint32_t split = blockIdx.x / total_tiles;
     uint32_t tm, tn;
@@ -1080,7 +1085,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kq_h_kernel(const uint8_t* _
     const uint8_t* c_src[2];  // this lane's two output columns (weight rows)
 #pragma unroll
     for (int j = 0; j < 2; ++j) c_src[j] = W + size_t(min(n0 + wn * 64 + j * 32 + l32, N - 1)) * rb;
-    const uint32_t xrow[2] = {min(m0 + wm * 64 + l32, M - 1), min(m0 + wm * 64 + 32 + l32, M - 1)};
+    const _Float16* gs_src = (ld_half ? XSL : XSH) + size_t(min(m0 + ld_row, M - 1)) * ng;
 
     v16f acc[2][2], part[2][2];
 #pragma unroll
@@ -1092,7 +1097,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kq_h_kernel(const uint8_t* _
 
     // Raw stage data of this thread: 16 activations (hi, lo) and the words of
     // its 16 weights; of this lane's output columns the super-block's d (and
-    // dmin, the packed scale bytes, and its rows' group sums for Q4_K / Q5_K).
+    // dmin for Q4_K / Q5_K, with the loader rows' group min and group sum).
     // The next stage's are loaded while the current one is converted and
     // multiplied.
     struct RawQ6 {
@@ -1102,8 +1107,8 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kq_h_kernel(const uint8_t* _
         uint32_t dbits[2];
     };
     struct RawK : RawQ6 {
-        uint32_t sbytes[2][3];
-        uint4 xs[2][2];
+        uint32_t mn;       // weight row ld_row: the stage group's min
+        uint32_t gs;       // activation row ld_row: the group's sum, hi (ld_half 0) or lo (1), f16 bits
     };
     using Raw = std::conditional_t<Q6, RawQ6, RawK>;
     auto load_raw = [&](uint32_t k0, Raw& r) {
@@ -1130,6 +1135,8 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kq_h_kernel(const uint8_t* _
             uint32_t sc, mn;
             kquant_scale_min(p + 4, g, sc, mn);
             r.sc = int(sc);
+            r.mn = mn;
+            r.gs = *reinterpret_cast<const uint16_t*>(gs_src + (k0 >> 5));
             const uint32_t* qs = reinterpret_cast<const uint32_t*>(p + (FMT == kQ5_K ? 48 : 16) + (g >> 1) * 32 + ld_half * 16);
 #pragma unroll
             for (int i = 0; i < 4; ++i) r.qw[i] = qs[i];
@@ -1139,18 +1146,8 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kq_h_kernel(const uint8_t* _
                 for (int i = 0; i < 4; ++i) r.hw[i] = qh[i];
             }
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const uint8_t* c = c_src[j] + size_t(k0 >> 8) * BB;
-                r.dbits[j] = *reinterpret_cast<const uint32_t*>(c);  // d | dmin << 16
-#pragma unroll
-                for (int t = 0; t < 3; ++t) r.sbytes[j][t] = reinterpret_cast<const uint32_t*>(c + 4)[t];
-            }
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {  // the 8 group sums of the super-block, lanes of the first half only
-                const size_t o = size_t(xrow[i]) * ng + (k0 >> 5 & ~7u);
-                r.xs[i][0] = lh == 0 ? *reinterpret_cast<const uint4*>(XSH + o) : make_uint4(0, 0, 0, 0);
-                r.xs[i][1] = lh == 0 ? *reinterpret_cast<const uint4*>(XSL + o) : make_uint4(0, 0, 0, 0);
-            }
+            for (int j = 0; j < 2; ++j)
+                r.dbits[j] = *reinterpret_cast<const uint32_t*>(c_src[j] + size_t(k0 >> 8) * BB);  // d | dmin << 16
         }
     };
     Raw cur, nxt;
@@ -1208,6 +1205,10 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kq_h_kernel(const uint8_t* _
         if constexpr (Q6) {
             *reinterpret_cast<h8_t*>(Bl + ld_row * HROW + ld_half * 16) = wl0;
             *reinterpret_cast<h8_t*>(Bl + ld_row * HROW + ld_half * 16 + 8) = wl1;
+        } else {
+            const uint32_t g = (k0 >> 5) & 7u;
+            (ld_half ? Gsl : Gsh)[ld_row * 8 + g] = __builtin_bit_cast(_Float16, uint16_t(cur.gs));
+            if (ld_half == 0) Bmin[ld_row * 8 + g] = _Float16(float(cur.mn));
         }
         lds_barrier();
 #pragma unroll
@@ -1235,19 +1236,20 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kq_h_kernel(const uint8_t* _
                 }
         }
         if (((k0 + HK) & 255u) == 0 || k0 + HK >= k_end) {  // end of a super-block
-            h8_t bmin[2];
+            // Q4_K / Q5_K: the super-block's 8 group sums and mins in k slots
+            // 0..7 (the upper lane half, k slots 8..15, multiplies zeros)
+            h8_t bmin[2], gsh[2], gsl[2];
+            if constexpr (!Q6) {
+                const h8_t zero = {};
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                if constexpr (!Q6) {  // the 8 mins of the column's super-block (k slots 0..7; 8..15 zero)
-                    uint8_t sb[12];
+                for (int j = 0; j < 2; ++j) {
+                    const h8_t t = *reinterpret_cast<const h8_t*>(Bmin + (wn * 64 + j * 32 + l32) * 8);
+                    bmin[j] = lh == 0 ? t : zero;
+                }
 #pragma unroll
-                    for (int t = 0; t < 12; ++t) sb[t] = uint8_t(cur.sbytes[j][t >> 2] >> (8 * (t & 3)));
-#pragma unroll
-                    for (int g = 0; g < 8; ++g) {
-                        uint32_t sc, mn;
-                        kquant_scale_min(sb, uint32_t(g), sc, mn);
-                        bmin[j][g] = lh == 0 ? _Float16(float(mn)) : _Float16(0.0f);
-                    }
+                for (int i = 0; i < 2; ++i) {
+                    gsh[i] = *reinterpret_cast<const h8_t*>(Gsh + (wm * 64 + i * 32 + l32) * 8);
+                    gsl[i] = *reinterpret_cast<const h8_t*>(Gsl + (wm * 64 + i * 32 + l32) * 8);
                 }
             }
 #pragma unroll
@@ -1258,10 +1260,8 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kq_h_kernel(const uint8_t* _
 #pragma unroll
                     for (int v = 0; v < 16; ++v) cm[v] = 0.0f;
                     if constexpr (!Q6) {
-                        const h8_t xsh = __builtin_bit_cast(h8_t, cur.xs[i][0]);
-                        const h8_t xsl = __builtin_bit_cast(h8_t, cur.xs[i][1]);
-                        cm = __builtin_amdgcn_mfma_f32_32x32x16_f16(xsh, bmin[j], cm, 0, 0, 0);
-                        cm = __builtin_amdgcn_mfma_f32_32x32x16_f16(xsl, bmin[j], cm, 0, 0, 0);
+                        cm = __builtin_amdgcn_mfma_f32_32x32x16_f16(gsh[i], bmin[j], cm, 0, 0, 0);
+                        cm = __builtin_amdgcn_mfma_f32_32x32x16_f16(gsl[i], bmin[j], cm, 0, 0, 0);
                     }
 #pragma unroll
                     for (int v = 0; v < 16; ++v) {
