@@ -334,15 +334,13 @@ def format_sweep(torch, zq, dev):
             ms = timed_launches_on(torch, lambda i: zq.gemm_dev(fmt, ws[i % nrep], X[: 512 * K], Y, 512, N, K, act,
                                                                 wsp, wsb), 2 * nrep, 2)
             tops = 2.0 * 512 * N * K / (ms * 1e-3) / 1e12
-            # the MFMA each path runs on: int8; Q6_K's split-f16 products (three
-            # f16 MFMA products per multiply-add: both operands split); Q4_K /
-            # Q5_K (two: split activations, exact f16 weights); fp32 otherwise
+            # the MFMA each path runs on: int8; the super-block formats' split-f16
+            # products (three f16 MFMA products per multiply-add: both operands
+            # split); fp32 otherwise
             if act == zq.ACT_INT8:
                 peak, mfma = INT8_PEAK_TOPS, "int8"
-            elif fmt == zq.Q6_K:
+            elif fmt in (zq.Q6_K, zq.Q4_K, zq.Q5_K):
                 peak, mfma = F16_PEAK_TFLOPS / 3.0, "f16 x3 (split operands)"
-            elif fmt in (zq.Q4_K, zq.Q5_K):
-                peak, mfma = F16_PEAK_TFLOPS / 2.0, "f16 x2 (split activations)"
             else:
                 peak, mfma = FP32_PEAK_TFLOPS, "fp32"
             entry.update({"gemm_M512_ms": round(ms, 4), "gemm_M512_TOPS": round(tops, 1),

@@ -198,9 +198,8 @@ int zq_hip_gemv_batch_dev(int fmt, const float* x, const zq_gemv_task* tasks, si
 /* Workspace (device bytes) a zq_hip_gemm_dev call needs: int8 activations,
  * their scales and, for small grids, split-K partial sums (ZQ_ACT_INT8);
  * with fp32 activations, the super-block formats' split activations (Q6_K,
- * Q4_K, Q5_K: f16 hi + lo and row scales, plus each row's 32-element group
- * sums for Q4_K / Q5_K; they let the GEMM run on the f16 MFMA) and split-K
- * partial sums for small grids,
+ * Q4_K, Q5_K: f16 hi + lo and row scales; they let the GEMM run on the f16
+ * MFMA) and split-K partial sums for small grids,
  * else 0 (a smaller or null workspace runs with what fits: the fp32 MFMA,
  * unsplit). */
 size_t zq_hip_gemm_workspace_bytes(int fmt, size_t tokens, size_t rows, size_t cols, int act_mode);

@@ -74,13 +74,10 @@ def test_argument_errors_without_device():
     ws = L.zq_hip_gemm_workspace_bytes(zq.Q6_K, 4, 4096, 4096, zq.ACT_DEFAULT)
     assert ws > split(4, 4096) and (ws - split(4, 4096)) % (4 * 4096 * 4) == 0
     assert L.zq_hip_gemm_workspace_bytes(zq.Q6_K, 2048, 14336, 4096, zq.ACT_DEFAULT) == split(2048, 4096)
-    # Q4_K / Q5_K add the 32-element group sums of each row, f16 hi + lo, each
-    # plane 256-byte aligned
-    gsum = lambda m, k: 2 * ((m * (k // 32) * 2 + 255) // 256 * 256)
-    for fmt in (zq.Q4_K, zq.Q5_K):
+    for fmt in (zq.Q4_K, zq.Q5_K):  # the same split activations as Q6_K
         ws = L.zq_hip_gemm_workspace_bytes(fmt, 4, 4096, 4096, zq.ACT_DEFAULT)
-        assert ws > split(4, 4096) + gsum(4, 4096) and (ws - split(4, 4096) - gsum(4, 4096)) % (4 * 4096 * 4) == 0
-        assert L.zq_hip_gemm_workspace_bytes(fmt, 2048, 14336, 4096, zq.ACT_DEFAULT) == split(2048, 4096) + gsum(2048, 4096)
+        assert ws > split(4, 4096) and (ws - split(4, 4096)) % (4 * 4096 * 4) == 0
+        assert L.zq_hip_gemm_workspace_bytes(fmt, 2048, 14336, 4096, zq.ACT_DEFAULT) == split(2048, 4096)
 
 
 def test_opt_in_semantics(monkeypatch):

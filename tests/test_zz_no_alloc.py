@@ -37,7 +37,7 @@ def _run_pair(zq, orc, fmt, act, m, n, k, seed):
     (O.Q4_0, 1, (2048, 1024, 4096), (70, 300, 320)),      # large M, then the staged kernel
     (O.Q8_0, 2, (64, 2048, 4096), (5, 300, 4096)),        # fp32 activations (split-K partials in scratch)
     (O.Q6_K, 2, (129, 512, 2048), (1, 70, 768)),
-    (O.Q4_K, 2, (129, 512, 2048), (1, 70, 768)),      # split activations + group sums in scratch
+    (O.Q4_K, 2, (129, 512, 2048), (1, 70, 768)),      # split activations in scratch
     (O.Q5_K, 2, (300, 256, 4096), (17, 40, 512)),
 ])
 def test_noalloc_matches_workspace_entry_point(zq, orc, fmt, act, big, small):

@@ -962,20 +962,16 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(const uint8_t* __res
 // with its products on v_mfma_f32_32x32x16_f16 (16x the fp32 MFMA rate) at
 // fp32-level accuracy:
 //  * each activation row is scaled by a power of two (split_rows_kernel) and
-//    carried as f16 hi + lo; for Q4_K / Q5_K also the sum of each 32-element
-//    group (scaled by 2^-5, hi + lo);
-//  * each weight is the integer sc*q of its group (Q6_K: 16 elements,
-//    sc int8, q - 32 in -32..31, |sc*q| <= 4096, carried as h = f16(sc*q) and
-//    l = sc*q - h, nonzero only past 2048; Q4_K / Q5_K: 32 elements, sc
-//    6-bit, q 0..15 / 0..31, |sc*q| <= 1953, one exact f16);
-//  * a product is Xh*Wh + Xl*Wh (+ Xh*Wl for Q6_K), accumulated in fp32 over
-//    a super-block (256 K), then scaled by the super-block's d; Q4_K / Q5_K
-//    subtract dmin * sum_j m_j * sum(x in group j), whose inner sum is one
-//    more MFMA pair (group sums against the 8 mins); the row scale comes
-//    off at the end.
+//    carried as f16 hi + lo;
+//  * each weight is dequantised as the reference does (Q6_K d*sc*(q-32),
+//    Q4_K / Q5_K d*sc*q - dmin*m, one fp32 rounding), scaled by a power of
+//    two per weight row (so the row's largest possible value lies below
+//    2^15) and carried as h = f16(w) and l = f16(w - h);
+//  * a product is Xh*Wh + Xl*Wh + Xh*Wl, accumulated in fp32 per super-block
+//    and the super-blocks summed; the row scales come off at the end.
 // Against the reference's dequantise-then-fp32 arithmetic the difference is
-// rounding order plus the dropped lo*lo products (below 2^-22 of the row
-// maximum).
+// rounding order, the 22-bit operand splits and the dropped lo*lo products
+// (all below 2^-21 of each operand).
 // A workgroup barrier that orders LDS only: unlike __syncthreads it does not
 // wait for the wave's outstanding global loads (a prefetch stays in flight).
 __device__ __forceinline__ void lds_barrier() {
@@ -983,14 +979,13 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
-constexpr int HK = 32;          // K elements per stage
-constexpr int HROW = HK + 8;    // halves per LDS row (pad: 16 B)
+#ifndef ZQ_KQ_HKS
+#define ZQ_KQ_HKS 32
+#endif
 
-// One workgroup per row.  xsh / xsl (optional): the row's 32-element group
-// sums of the scaled values, times 2^-5, as f16 hi + lo ([M][K / 32]).
+// One workgroup per row.
 __global__ __launch_bounds__(kThreads) void split_rows_kernel(const float* __restrict__ X, _Float16* __restrict__ xh,
                                                               _Float16* __restrict__ xl, float* __restrict__ inv,
-                                                              _Float16* __restrict__ xsh, _Float16* __restrict__ xsl,
                                                               uint32_t K) {
     __shared__ float red[kThreads / 64];
     const float4* r = reinterpret_cast<const float4*>(X + size_t(blockIdx.x) * K);
@@ -1011,82 +1006,86 @@ __global__ __launch_bounds__(kThreads) void split_rows_kernel(const float* __res
     if (threadIdx.x == 0) inv[blockIdx.x] = pow2f(-e);
     h4_t* oh = reinterpret_cast<h4_t*>(xh + size_t(blockIdx.x) * K);
     h4_t* ol = reinterpret_cast<h4_t*>(xl + size_t(blockIdx.x) * K);
-    for (uint32_t i0 = 0; i0 < K4; i0 += kThreads) {  // K % 1024 == 0 is not assumed: whole 8-lane groups
-        const uint32_t i = i0 + threadIdx.x;
-        const bool live = i < K4;
-        const float4 v = live ? r[i] : make_float4(0, 0, 0, 0);
-        const float4 sv = make_float4(v.x * f, v.y * f, v.z * f, v.w * f);
-        if (live) {
-            h4_t h, l;
-            split_h(sv.x, h, l, 0);
-            split_h(sv.y, h, l, 1);
-            split_h(sv.z, h, l, 2);
-            split_h(sv.w, h, l, 3);
-            oh[i] = h;
-            ol[i] = l;
-        }
-        if (xsh) {  // 8 consecutive lanes hold one 32-element group (K % 32 == 0)
-            float t = (sv.x + sv.y) + (sv.z + sv.w);
-            t += __shfl_xor(t, 1);
-            t += __shfl_xor(t, 2);
-            t += __shfl_xor(t, 4);
-            if (live && (i & 7u) == 0) {
-                const float ts = t * 0.03125f;  // |t| <= 2^20: into the f16 range
-                const _Float16 th = _Float16(ts);
-                xsh[size_t(blockIdx.x) * (K / 32) + i / 8] = th;
-                xsl[size_t(blockIdx.x) * (K / 32) + i / 8] = _Float16(ts - float(th));
-            }
-        }
+    for (uint32_t i = threadIdx.x; i < K4; i += kThreads) {
+        const float4 v = r[i];
+        h4_t h, l;
+        split_h(v.x * f, h, l, 0);
+        split_h(v.y * f, h, l, 1);
+        split_h(v.z * f, h, l, 2);
+        split_h(v.w * f, h, l, 3);
+        oh[i] = h;
+        ol[i] = l;
     }
 }
 
-// Split K as in gemm_f32_kernel; stages_per_split is a multiple of the 8
-// stages of a super-block.
-template <int FMT>
+// Split K as in gemm_f32_kernel; stages_per_split is a multiple of the
+// stages of a super-block.  HKS: K elements per stage (32 or 64).
+template <int FMT, int HKS>
 __global__ __launch_bounds__(kThreads, 2) void gemm_kq_h_kernel(const uint8_t* __restrict__ W,
                                                                  const _Float16* __restrict__ XH,
                                                                  const _Float16* __restrict__ XL,
-                                                                 const float* __restrict__ xinv,
-                                                                 const _Float16* __restrict__ XSH,
-                                                                 const _Float16* __restrict__ XSL, float* __restrict__ Y,
+                                                                 const float* __restrict__ xinv, float* __restrict__ Y,
                                                                  uint32_t M, uint32_t N, uint32_t K, uint32_t tiles_m,
                                                                  uint32_t tiles_n, uint32_t ksplit,
                                                                  uint32_t stages_per_split) {
     static_assert(FMT == kQ6_K || FMT == kQ4_K || FMT == kQ5_K, "super-block formats");
+    static_assert(HKS == 32 || HKS == 64, "stage depth");
     constexpr bool Q6 = FMT == kQ6_K;
     constexpr uint32_t BB = FMT == kQ6_K ? 210 : (FMT == kQ5_K ? 176 : 144);
-    __shared__ __align__(16) _Float16 Ah[BM * HROW];
-    __shared__ __align__(16) _Float16 Al[BM * HROW];
-    __shared__ __align__(16) _Float16 Bh[BN * HROW];
-    __shared__ __align__(16) _Float16 Bl[Q6 ? BN * HROW : 8];
-    // Q4_K / Q5_K: per super-block, slot g holds group g's activation sums
-    // (hi, lo) of each tile row and its min m_g of each weight row
-    __shared__ __align__(16) _Float16 Gsh[Q6 ? 8 : BM * 8];
-    __shared__ __align__(16) _Float16 Gsl[Q6 ? 8 : BM * 8];
-    __shared__ __align__(16) _Float16 Bmin[Q6 ? 8 : BN * 8];
+    constexpr int HR = HKS + 8;      // halves per LDS row (pad: 16 B)
+    constexpr int EPT = HKS / 2;     // elements per loader thread per stage
+    constexpr int XU = EPT / 8;      // 16-byte units of activations per thread, each of hi and lo
+    constexpr int QWN = EPT / 4;     // words of codes per thread (one byte per element)
+    __shared__ __align__(16) _Float16 Ah[BM * HR];
+    __shared__ __align__(16) _Float16 Al[BM * HR];
+    __shared__ __align__(16) _Float16 Bh[BN * HR];
+    __shared__ __align__(16) _Float16 Bl[BN * HR];
+    __shared__ float binv[BN];
     const uint32_t total_tiles = tiles_m * tiles_n;
     const uint32_t split = blockIdx.x / total_tiles;
     uint32_t tm, tn;
     tile_of(tiles_m, tiles_n, blockIdx.x % total_tiles, tm, tn);
     const uint32_t m0 = tm * BM, n0 = tn * BN;
-    const uint32_t k_begin = split * stages_per_split * HK;
-    const uint32_t k_end = min(K, k_begin + stages_per_split * HK);
+    const uint32_t k_begin = split * stages_per_split * HKS;
+    const uint32_t k_end = min(K, k_begin + stages_per_split * HKS);
     float* Yout = Y + (ksplit > 1 ? size_t(split) * M * N : 0);
     const size_t rb = row_bytes_dev(FMT, K);
-    const uint32_t ng = K / 32;  // 32-element groups per row
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int l32 = lane & 31, lh = lane >> 5;
-    const uint32_t ld_row = tid >> 1, ld_half = tid & 1;  // loader: row, 16-element half of the stage
-    const _Float16* ah_src = XH + size_t(min(m0 + ld_row, M - 1)) * K + ld_half * 16;
-    const _Float16* al_src = XL + size_t(min(m0 + ld_row, M - 1)) * K + ld_half * 16;
+    const uint32_t ld_row = tid >> 1, ld_half = tid & 1;  // loader: row, half of the stage
+    const _Float16* ah_src = XH + size_t(min(m0 + ld_row, M - 1)) * K + ld_half * EPT;
+    const _Float16* al_src = XL + size_t(min(m0 + ld_row, M - 1)) * K + ld_half * EPT;
     const uint8_t* b_src = W + size_t(min(n0 + ld_row, N - 1)) * rb;
-    const uint8_t* c_src[2];  // this lane's two output columns (weight rows)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) c_src[j] = W + size_t(min(n0 + wn * 64 + j * 32 + l32, N - 1)) * rb;
-    const _Float16* gs_src = (ld_half ? XSL : XSH) + size_t(min(m0 + ld_row, M - 1)) * ng;
 
+    // The loader row's scale 2^e: its dequantised weights over this split's
+    // super-blocks, times 2^e, lie below 2^15 in magnitude (a bound from d,
+    // dmin and the largest code and scale), so each is h + l in f16 with
+    // normal h.  The two threads of a row scan alternate super-blocks.
+    float wscale;
+    {
+        float bound = 0.0f;
+        for (uint32_t sb = k_begin / 256 + ld_half; sb < (k_end + 255) / 256; sb += 2) {
+            const uint8_t* p = b_src + size_t(sb) * BB;
+            if constexpr (Q6) {
+                bound = fmaxf(bound, fabsf(half_bits_to_float(*reinterpret_cast<const uint16_t*>(p + 208))) * 4096.0f);
+            } else {
+                const uint32_t dd = *reinterpret_cast<const uint32_t*>(p);
+                const float dmax = FMT == kQ5_K ? 1953.0f : 945.0f;  // 63 x 31, 63 x 15
+                bound = fmaxf(bound, fmaf(fabsf(half_bits_to_float(dd & 0xffffu)), dmax,
+                                          fabsf(half_bits_to_float(dd >> 16)) * 63.0f));
+            }
+        }
+        bound = fmaxf(bound, __shfl_xor(bound, 1));
+        const int e = split_exp(bound);
+        wscale = pow2f(e);
+        if (ld_half == 0) binv[ld_row] = pow2f(-e);
+    }
+
+    // part: the current super-block's products; acc: the sum of the
+    // super-blocks' (a two-level sum, so rounding grows with the number of
+    // super-blocks rather than of MFMA steps)
     v16f acc[2][2], part[2][2];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -1095,136 +1094,148 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kq_h_kernel(const uint8_t* _
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = part[i][j][v] = 0.0f;
 
-    // Raw stage data of this thread: 16 activations (hi, lo) and the words of
-    // its 16 weights; of this lane's output columns the super-block's d (and
-    // dmin for Q4_K / Q5_K, with the loader rows' group min and group sum).
-    // The next stage's are loaded while the current one is converted and
-    // multiplied.
-    struct RawQ6 {
-        uint4 xa0, xa1, xb0, xb1;
-        uint32_t qw[4], hw[4];
-        int sc;
-        uint32_t dbits[2];
+    // Raw stage data of this thread: EPT activations (hi, lo), the words of
+    // its EPT weight codes, their group scales and the super-block's d (and
+    // dmin).  The next stage's are loaded while the current one is converted
+    // and multiplied.  The thread's codes are one 32-element line of the
+    // super-block (a Q6_K quarter of a half, a Q4_K / Q5_K group): for HKS =
+    // 32 its half, for HKS = 64 line ld_half of the stage's two.
+    struct Raw {
+        u32x4_attn_t xa[XU], xb[XU];
+        uint32_t qw[QWN], hw[Q6 || FMT == kQ5_K ? QWN : 1];
+        uint32_t sc;   // Q6_K: the int8 scales of the thread's 16-element groups; else the 12 scale bytes' words
+        uint32_t sc1, sc2;
+        uint32_t dd;   // d (| dmin << 16)
     };
-    struct RawK : RawQ6 {
-        uint32_t mn;       // weight row ld_row: the stage group's min
-        uint32_t gs;       // activation row ld_row: the group's sum, hi (ld_half 0) or lo (1), f16 bits
-    };
-    using Raw = std::conditional_t<Q6, RawQ6, RawK>;
-    auto load_raw = [&](uint32_t k0, Raw& r) {
-        r.xa0 = *reinterpret_cast<const uint4*>(ah_src + k0);
-        r.xa1 = *reinterpret_cast<const uint4*>(ah_src + k0 + 8);
-        r.xb0 = *reinterpret_cast<const uint4*>(al_src + k0);
-        r.xb1 = *reinterpret_cast<const uint4*>(al_src + k0 + 8);
-        const uint8_t* p = b_src + size_t(k0 >> 8) * BB;
+    auto line_of = [&](uint32_t k0, uint32_t& line, uint32_t& ls) {
         const uint32_t in_sb = k0 & 255u;
-        if constexpr (Q6) {
-            const uint32_t h = in_sb >> 7, grp = (in_sb >> 5) & 3u;
-            r.sc = int(reinterpret_cast<const int8_t*>(p + 192)[h * 8 + grp * 2 + ld_half]);
-            const uint8_t* lo = p + h * 64 + (grp & 1u) * 32 + ld_half * 16;
-            const uint8_t* hi = p + 128 + h * 32 + ld_half * 16;
+        line = (in_sb >> 5) + (HKS == 64 ? ld_half : 0u);
+        ls = HKS == 64 ? 0u : ld_half * 16u;
+    };
+    auto load_raw = [&](uint32_t k0, Raw& r) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+        for (int u = 0; u < XU; ++u) {
+            r.xa[u] = *reinterpret_cast<const u32x4_attn_t*>(ah_src + k0 + 8 * u);
+            r.xb[u] = *reinterpret_cast<const u32x4_attn_t*>(al_src + k0 + 8 * u);
+        }
+        const uint8_t* p = b_src + size_t(k0 >> 8) * BB;
+        uint32_t line, ls;
+        line_of(k0, line, ls);
+        if constexpr (Q6) {
+            const uint32_t h = line >> 2, q4 = line & 3u;
+            const uint8_t* lo = p + h * 64 + (q4 & 1u) * 32 + ls;
+            const uint8_t* hi = p + 128 + h * 32 + ls;
+#pragma unroll
+            for (int i = 0; i < QWN; ++i) {
                 r.qw[i] = load_u32_a2(lo + 4 * i);
                 r.hw[i] = load_u32_a2(hi + 4 * i);
             }
-#pragma unroll
-            for (int j = 0; j < 2; ++j) r.dbits[j] = *reinterpret_cast<const uint16_t*>(c_src[j] + size_t(k0 >> 8) * BB + 208);
+            const uint8_t* s = p + 192 + h * 8 + q4 * 2 + (ls >> 4);
+            r.sc = HKS == 64 ? uint32_t(*reinterpret_cast<const uint16_t*>(s)) : uint32_t(*s);
+            r.dd = *reinterpret_cast<const uint16_t*>(p + 208);
+            r.sc1 = r.sc2 = 0;
         } else {
-            const uint32_t g = in_sb >> 5;
-            uint32_t sc, mn;
-            kquant_scale_min(p + 4, g, sc, mn);
-            r.sc = int(sc);
-            r.mn = mn;
-            r.gs = *reinterpret_cast<const uint16_t*>(gs_src + (k0 >> 5));
-            const uint32_t* qs = reinterpret_cast<const uint32_t*>(p + (FMT == kQ5_K ? 48 : 16) + (g >> 1) * 32 + ld_half * 16);
+            const uint32_t* qs =
+                reinterpret_cast<const uint32_t*>(p + (FMT == kQ5_K ? 48 : 16) + (line >> 1) * 32 + ls);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) r.qw[i] = qs[i];
+            for (int i = 0; i < QWN; ++i) r.qw[i] = qs[i];
             if constexpr (FMT == kQ5_K) {
-                const uint32_t* qh = reinterpret_cast<const uint32_t*>(p + 16 + ld_half * 16);
+                const uint32_t* qh = reinterpret_cast<const uint32_t*>(p + 16 + ls);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) r.hw[i] = qh[i];
+                for (int i = 0; i < QWN; ++i) r.hw[i] = qh[i];
             }
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-                r.dbits[j] = *reinterpret_cast<const uint32_t*>(c_src[j] + size_t(k0 >> 8) * BB);  // d | dmin << 16
+            const uint32_t* w = reinterpret_cast<const uint32_t*>(p);
+            r.dd = w[0];
+            r.sc = w[1];
+            r.sc1 = w[2];
+            r.sc2 = w[3];
         }
     };
-    Raw cur, nxt;
-    if (k_begin < k_end) load_raw(k_begin, cur);
-    for (uint32_t k0 = k_begin; k0 < k_end; k0 += HK) {
+    // one stage from `cur`, prefetching the next into `nxt` (two named
+    // records used alternately: no copy between them)
+    auto stage = [&](uint32_t k0, Raw& cur, Raw& nxt) {
         // unconditional (the last stage reloads itself), so the wait for the
         // current stage's data counts the prefetch statically
-        load_raw(min(k0 + HK, k_end - HK), nxt);
-        float dj[2], mj[2];
+        load_raw(min(k0 + HKS, k_end - HKS), nxt);
+        u32x4_attn_t xa[XU], xb[XU];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            dj[j] = half_bits_to_float(cur.dbits[j] & 0xffffu);
-            mj[j] = -32.0f * half_bits_to_float(cur.dbits[j] >> 16);  // the group sums carry 2^-5
+        for (int u = 0; u < XU; ++u) {
+            xa[u] = cur.xa[u];
+            xb[u] = cur.xb[u];
         }
-        const uint4 xa0 = cur.xa0, xa1 = cur.xa1, xb0 = cur.xb0, xb1 = cur.xb1;
-        h8_t wh0, wl0, wh1, wl1;
+        h8_t wh[EPT / 8], wl[EPT / 8];
         {
-            const uint32_t in_sb = k0 & 255u;
+            uint32_t line, ls;
+            line_of(k0, line, ls);
+            // per 16-element group: value = a * code - b (exact in fp32), times 2^e
+            float a[EPT / 16], b[EPT / 16];
+            if constexpr (Q6) {
+                const float ds = half_bits_to_float(cur.dd & 0xffffu) * wscale;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+                for (int g = 0; g < EPT / 16; ++g) {
+                    a[g] = ds * float(int(int8_t(uint8_t(cur.sc >> (8 * g)))));
+                    b[g] = 32.0f * a[g];
+                }
+            } else {
+                // scale / min of group `line` (src/quant.cpp:133-141) from the
+                // words of scale bytes 0-3, 4-7, 8-11
+                const uint32_t sh = 8 * (line & 3u);
+                const uint32_t sa = cur.sc >> sh, sbb = cur.sc1 >> sh, scc = cur.sc2 >> sh;
+                const uint32_t sc = line < 4 ? sa & 63u : (scc & 15u) | ((sa >> 2) & 0x30u);
+                const uint32_t mn = line < 4 ? sbb & 63u : ((scc >> 4) & 15u) | ((sbb >> 2) & 0x30u);
+                const float d = half_bits_to_float(cur.dd & 0xffffu) * wscale;
+                const float dm = half_bits_to_float(cur.dd >> 16) * wscale;
+#pragma unroll
+                for (int g = 0; g < EPT / 16; ++g) {
+                    a[g] = d * float(sc);
+                    b[g] = dm * float(mn);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < QWN; ++i) {
                 const uint32_t qw = cur.qw[i];
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
-                    int q;
+                    uint32_t q;
                     if constexpr (Q6) {
-                        const uint32_t grp = (in_sb >> 5) & 3u;
+                        const uint32_t q4 = line & 3u;
                         uint32_t l = (qw >> (8 * k)) & 0xffu;
-                        if (grp >= 2) l >>= 4;
-                        const uint32_t hb = ((cur.hw[i] >> (8 * k)) >> (2 * grp)) & 3u;
-                        q = int((l & 15u) | (hb << 4)) - 32;
+                        if (q4 >= 2) l >>= 4;
+                        const uint32_t hb = ((cur.hw[i] >> (8 * k)) >> (2 * q4)) & 3u;
+                        q = (l & 15u) | (hb << 4);
                     } else {
-                        const uint32_t g = in_sb >> 5;
-                        q = int((qw >> (8 * k + 4 * (g & 1u))) & 15u);
-                        if constexpr (FMT == kQ5_K) q |= int(((cur.hw[i] >> (8 * k + g)) & 1u) << 4);
+                        q = (qw >> (8 * k + 4 * (line & 1u))) & 15u;
+                        if constexpr (FMT == kQ5_K) q |= ((cur.hw[i] >> (8 * k + line)) & 1u) << 4;
                     }
-                    const float v = float(cur.sc * q);  // exact integer
                     const int e = 4 * i + k;
-                    if constexpr (Q6) {
-                        if (e < 8) split_h(v, wh0, wl0, e);
-                        else split_h(v, wh1, wl1, e - 8);
-                    } else {
-                        if (e < 8) wh0[e] = _Float16(v);
-                        else wh1[e - 8] = _Float16(v);
-                    }
+                    const float v = fmaf(a[e / 16], float(q), -b[e / 16]);
+                    split_h(v, wh[e / 8], wl[e / 8], e % 8);
                 }
             }
         }
         lds_barrier();  // the previous stage's readers are done (the prefetch stays in flight)
-        *reinterpret_cast<uint4*>(Ah + ld_row * HROW + ld_half * 16) = xa0;
-        *reinterpret_cast<uint4*>(Ah + ld_row * HROW + ld_half * 16 + 8) = xa1;
-        *reinterpret_cast<uint4*>(Al + ld_row * HROW + ld_half * 16) = xb0;
-        *reinterpret_cast<uint4*>(Al + ld_row * HROW + ld_half * 16 + 8) = xb1;
-        *reinterpret_cast<h8_t*>(Bh + ld_row * HROW + ld_half * 16) = wh0;
-        *reinterpret_cast<h8_t*>(Bh + ld_row * HROW + ld_half * 16 + 8) = wh1;
-        if constexpr (Q6) {
-            *reinterpret_cast<h8_t*>(Bl + ld_row * HROW + ld_half * 16) = wl0;
-            *reinterpret_cast<h8_t*>(Bl + ld_row * HROW + ld_half * 16 + 8) = wl1;
-        } else {
-            const uint32_t g = (k0 >> 5) & 7u;
-            (ld_half ? Gsl : Gsh)[ld_row * 8 + g] = __builtin_bit_cast(_Float16, uint16_t(cur.gs));
-            if (ld_half == 0) Bmin[ld_row * 8 + g] = _Float16(float(cur.mn));
+#pragma unroll
+        for (int u = 0; u < XU; ++u) {
+            *reinterpret_cast<u32x4_attn_t*>(Ah + ld_row * HR + ld_half * EPT + 8 * u) = xa[u];
+            *reinterpret_cast<u32x4_attn_t*>(Al + ld_row * HR + ld_half * EPT + 8 * u) = xb[u];
+            *reinterpret_cast<h8_t*>(Bh + ld_row * HR + ld_half * EPT + 8 * u) = wh[u];
+            *reinterpret_cast<h8_t*>(Bl + ld_row * HR + ld_half * EPT + 8 * u) = wl[u];
         }
         lds_barrier();
 #pragma unroll
-        for (int ks = 0; ks < HK / 16; ++ks) {
+        for (int ks = 0; ks < HKS / 16; ++ks) {
             h8_t ah[2], al[2], bh[2], bl[2];
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
-                const int r = (wm * 64 + i * 32 + l32) * HROW + ks * 16 + 8 * lh;
+                const int r = (wm * 64 + i * 32 + l32) * HR + ks * 16 + 8 * lh;
                 ah[i] = *reinterpret_cast<const h8_t*>(Ah + r);
                 al[i] = *reinterpret_cast<const h8_t*>(Al + r);
             }
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-                const int r = (wn * 64 + j * 32 + l32) * HROW + ks * 16 + 8 * lh;
+                const int r = (wn * 64 + j * 32 + l32) * HR + ks * 16 + 8 * lh;
                 bh[j] = *reinterpret_cast<const h8_t*>(Bh + r);
-                if constexpr (Q6) bl[j] = *reinterpret_cast<const h8_t*>(Bl + r);
+                bl[j] = *reinterpret_cast<const h8_t*>(Bl + r);
             }
 #pragma unroll
             for (int i = 0; i < 2; ++i)
@@ -1232,57 +1243,40 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kq_h_kernel(const uint8_t* _
                 for (int j = 0; j < 2; ++j) {
                     part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bh[j], part[i][j], 0, 0, 0);
                     part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], bh[j], part[i][j], 0, 0, 0);
-                    if constexpr (Q6) part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bl[j], part[i][j], 0, 0, 0);
+                    part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bl[j], part[i][j], 0, 0, 0);
                 }
         }
-        if (((k0 + HK) & 255u) == 0 || k0 + HK >= k_end) {  // end of a super-block
-            // Q4_K / Q5_K: the super-block's 8 group sums and mins in k slots
-            // 0..7 (the upper lane half, k slots 8..15, multiplies zeros)
-            h8_t bmin[2], gsh[2], gsl[2];
-            if constexpr (!Q6) {
-                const h8_t zero = {};
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const h8_t t = *reinterpret_cast<const h8_t*>(Bmin + (wn * 64 + j * 32 + l32) * 8);
-                    bmin[j] = lh == 0 ? t : zero;
-                }
-#pragma unroll
-                for (int i = 0; i < 2; ++i) {
-                    gsh[i] = *reinterpret_cast<const h8_t*>(Gsh + (wm * 64 + i * 32 + l32) * 8);
-                    gsl[i] = *reinterpret_cast<const h8_t*>(Gsl + (wm * 64 + i * 32 + l32) * 8);
-                }
-            }
+        if (((k0 + HKS) & 255u) == 0) {  // end of a super-block
 #pragma unroll
             for (int i = 0; i < 2; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    v16f cm;
-#pragma unroll
-                    for (int v = 0; v < 16; ++v) cm[v] = 0.0f;
-                    if constexpr (!Q6) {
-                        cm = __builtin_amdgcn_mfma_f32_32x32x16_f16(gsh[i], bmin[j], cm, 0, 0, 0);
-                        cm = __builtin_amdgcn_mfma_f32_32x32x16_f16(gsl[i], bmin[j], cm, 0, 0, 0);
-                    }
+                for (int j = 0; j < 2; ++j)
 #pragma unroll
                     for (int v = 0; v < 16; ++v) {
-                        float t = fmaf(part[i][j][v], dj[j], acc[i][j][v]);
-                        if constexpr (!Q6) t = fmaf(cm[v], mj[j], t);
-                        acc[i][j][v] = t;
+                        acc[i][j][v] += part[i][j][v];
                         part[i][j][v] = 0.0f;
                     }
-                }
         }
-        cur = nxt;
+    };
+    Raw r0, r1;
+    if (k_begin < k_end) load_raw(k_begin, r0);
+    // a split holds whole super-blocks: an even number of stages
+    for (uint32_t k0 = k_begin; k0 < k_end; k0 += 2 * HKS) {
+        stage(k0, r0, r1);
+        stage(k0 + HKS, r1, r0);
     }
+    lds_barrier();  // binv
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            const uint32_t n = n0 + wn * 64 + j * 32 + l32;
+            const uint32_t nl = wn * 64 + j * 32 + l32;
+            const uint32_t n = n0 + nl;
+            const float bs = binv[nl];
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const uint32_t m = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
-                if (m < M && n < N) Yout[size_t(m) * N + n] = acc[i][j][v] * xinv[m];
+                if (m < M && n < N) Yout[size_t(m) * N + n] = acc[i][j][v] * xinv[m] * bs;
             }
         }
 }
@@ -1508,10 +1502,7 @@ size_t gemm_f32_partial_bytes(size_t M, size_t N, size_t K) {
 // ([M][K / 32] each) come first in the workspace, 256-byte aligned sections.
 static bool kq_f16(int fmt, size_t K) { return (fmt == kQ6_K || fmt == kQ4_K || fmt == kQ5_K) && K % 256 == 0; }
 static size_t a256(size_t v) { return (v + 255) / 256 * 256; }
-static size_t kq_split_bytes(int fmt, size_t M, size_t K) {
-    const size_t base = a256(M * K * 2 * sizeof(_Float16) + M * sizeof(float));
-    return fmt == kQ6_K ? base : base + 2 * a256(M * (K / 32) * sizeof(_Float16));
-}
+static size_t kq_split_bytes(int, size_t M, size_t K) { return a256(M * K * 2 * sizeof(_Float16) + M * sizeof(float)); }
 
 size_t gemm_f32_workspace_bytes(int fmt, size_t M, size_t N, size_t K) {
     return (kq_f16(fmt, K) ? kq_split_bytes(fmt, M, K) : 0) + gemm_f32_partial_bytes(M, N, K);
@@ -1533,25 +1524,24 @@ hipError_t launch_gemm_f32(int fmt, const uint8_t* w, const float* X, float* Y, 
         _Float16* xh = reinterpret_cast<_Float16*>(b);
         _Float16* xl = xh + M * K;
         float* inv = reinterpret_cast<float*>(xl + M * K);
-        const size_t base = a256(M * K * 2 * sizeof(_Float16) + M * sizeof(float));
-        _Float16* xsh = fmt == kQ6_K ? nullptr : reinterpret_cast<_Float16*>(b + base);
-        _Float16* xsl = fmt == kQ6_K ? nullptr : reinterpret_cast<_Float16*>(b + base + a256(M * (K / 32) * 2));
         const size_t sb = kq_split_bytes(fmt, M, K);
         float* partial = ws_bytes >= sb + pbytes && pbytes ? reinterpret_cast<float*>(b + sb) : nullptr;
         uint32_t ks = partial ? choose_ksplit_f32(tiles_m * tiles_n, stages) : 1u;
-        const uint32_t spw = ((stages + ks - 1) / ks + 7) / 8 * 8;  // whole super-blocks per split
-        ks = (stages + spw - 1) / spw;
+        constexpr uint32_t HKS = ZQ_KQ_HKS, SPB = 256 / HKS;  // stages per super-block
+        const uint32_t hstages = k / HKS;
+        const uint32_t spw = ((hstages + ks - 1) / ks + SPB - 1) / SPB * SPB;  // whole super-blocks per split
+        ks = (hstages + spw - 1) / spw;
         float* out = ks > 1 ? partial : Y;
         const dim3 grid(tiles_m * tiles_n * ks);
-        hipLaunchKernelGGL(split_rows_kernel, dim3(m), dim3(kThreads), 0, stream, X, xh, xl, inv, xsh, xsl, k);
+        hipLaunchKernelGGL(split_rows_kernel, dim3(m), dim3(kThreads), 0, stream, X, xh, xl, inv, k);
         if (fmt == kQ6_K)
-            hipLaunchKernelGGL(gemm_kq_h_kernel<kQ6_K>, grid, dim3(kThreads), 0, stream, w, xh, xl, inv, xsh, xsl, out, m, n,
+            hipLaunchKernelGGL((gemm_kq_h_kernel<kQ6_K, HKS>), grid, dim3(kThreads), 0, stream, w, xh, xl, inv, out, m, n,
                                k, tiles_m, tiles_n, ks, spw);
         else if (fmt == kQ4_K)
-            hipLaunchKernelGGL(gemm_kq_h_kernel<kQ4_K>, grid, dim3(kThreads), 0, stream, w, xh, xl, inv, xsh, xsl, out, m, n,
+            hipLaunchKernelGGL((gemm_kq_h_kernel<kQ4_K, HKS>), grid, dim3(kThreads), 0, stream, w, xh, xl, inv, out, m, n,
                                k, tiles_m, tiles_n, ks, spw);
         else
-            hipLaunchKernelGGL(gemm_kq_h_kernel<kQ5_K>, grid, dim3(kThreads), 0, stream, w, xh, xl, inv, xsh, xsl, out, m, n,
+            hipLaunchKernelGGL((gemm_kq_h_kernel<kQ5_K, HKS>), grid, dim3(kThreads), 0, stream, w, xh, xl, inv, out, m, n,
                                k, tiles_m, tiles_n, ks, spw);
         if (launches) *launches = ks > 1 ? 3 : 2;
         return finish_splits(hipGetLastError(), partial, Y, M, N, ks, stream);
