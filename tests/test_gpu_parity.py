@@ -228,6 +228,38 @@ def test_gemm_f32(zq, orc, fmt, m, n, k):
     zq.release(w)
 
 
+@pytest.mark.parametrize("fmt", [O.Q6_K, O.Q4_K, O.Q5_K])
+def test_superblock_gemm_mixed_scales(zq, orc, fmt):
+    """Super-blocks of one weight row whose d (and dmin) lie 1 to 1e5 times below
+    the row's largest, and an all-zero row, through the f16-MFMA GEMM (explicit
+    workspace): it scales each weight row by one power of two taken from its
+    largest super-block, so the small super-blocks carry fewer bits in their low
+    halves and must still meet the fp32 bar against the reference arithmetic."""
+    m, n, k = 37, 70, 2048
+    w = orc.gen_weights(fmt, 4242, n, k).copy()
+    bb = {O.Q6_K: 210, O.Q4_K: 144, O.Q5_K: 176}[fmt]
+    doff = 208 if fmt == O.Q6_K else 0
+    nsb = k // 256
+    rb = nsb * bb
+    factors = [1.0, 1e-3, 0.3, 1e-5, 1.0, 3e-4, 0.1, 1e-2]
+    for r in range(n):
+        for sb in range(nsb):
+            o = r * rb + sb * bb + doff
+            for f_off in ((0,) if fmt == O.Q6_K else (0, 2)):  # d, and dmin for Q4_K / Q5_K
+                h = w[o + f_off:o + f_off + 2].view(np.float16)
+                v = np.float16(np.clip(np.float32(h[0]) * factors[(sb + r) % len(factors)], -60000, 60000))
+                w[o + f_off:o + f_off + 2] = np.frombuffer(v.tobytes(), np.uint8)
+    w[5 * rb:6 * rb] = 0  # an all-zero row
+    X = orc.gen_normal(4243, m * k)
+    Y = torch.empty(m * n, device=DEV)
+    wsb = zq.gemm_workspace_bytes(fmt, m, n, k, zq.ACT_F32)
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=DEV)
+    zq.gemm_dev(fmt, dev_weights(zq, fmt, w, n, k), to_dev(X), Y, m, n, k, zq.ACT_F32, ws, wsb)
+    got = Y.cpu().numpy()
+    assert np.all(got.reshape(m, n)[:, 5] == 0)
+    assert_close(got, orc.gemm_f32(fmt, w, X, m, n, k), f"mixed-scale gemm fmt={fmt}")
+
+
 # The BASELINE configs' own GEMM workloads at full size: config 2 (Q8_0, int8
 # activations, M = 32 / 128 / 512 / 2048 on both FFN shapes) and config 3
 # (Q4_0 int8 and Q6_K fp32 at M = 512), plus the Q4_K / Q5_K fp32 path at
