@@ -1498,8 +1498,8 @@ size_t gemm_f32_partial_bytes(size_t M, size_t N, size_t K) {
 }
 
 // The super-block formats on the f16 MFMA: the split activations (hi and lo
-// halves, [M][K] each), the row scales and (Q4_K / Q5_K) the split group sums
-// ([M][K / 32] each) come first in the workspace, 256-byte aligned sections.
+// halves, [M][K] each) and the row scales come first in the workspace, the
+// section rounded up to 256 bytes.
 static bool kq_f16(int fmt, size_t K) { return (fmt == kQ6_K || fmt == kQ4_K || fmt == kQ5_K) && K % 256 == 0; }
 static size_t a256(size_t v) { return (v + 255) / 256 * 256; }
 static size_t kq_split_bytes(int, size_t M, size_t K) { return a256(M * K * 2 * sizeof(_Float16) + M * sizeof(float)); }
