@@ -263,8 +263,8 @@ int enqueue_gemm(int fmt, const uint8_t* w, const float* X, float* Y, size_t tok
         return ZQ_OK;
     }
     // fp32 activations: the workspace, when large enough, holds the split
-    // activations (Q6_K) and split-K partial sums; with less the GEMM runs
-    // with what fits
+    // activations (Q6_K, Q4_K, Q5_K) and split-K partial sums; with less the
+    // GEMM runs with what fits
     uint32_t n = 0;
     if (zq::launch_gemm_f32(fmt, w, X, Y, ws, ws ? ws_bytes : 0, tokens, rows, cols, s, &n) != hipSuccess)
         return ZQ_ERR_HIP;
