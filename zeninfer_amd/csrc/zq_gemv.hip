@@ -35,8 +35,9 @@
 // q = lo4 | hi2 << 4, then ((q ^ 0x20) << 2) is 4*(q-32) as a signed byte.
 // The streaming Q6_K kernel (cols % 2048 == 0) instead gives each lane 16
 // consecutive elements of one quarter (one sub-block scale), builds the
-// 6-bit codes four per dword and feeds them as binary16 denormals to
-// v_fma_mix_f32; see gemv_q6k_stream_kernel.
+// 6-bit codes four per dword and converts each with one v_cvt_f32_ubyteN,
+// the code offset applied once per unit through a precomputed sum of x; see
+// gemv_q6k_stream_kernel.
 #include "zq_device.hpp"
 #include "zq_internal.hpp"
 #include "zq_pairs.hpp"
@@ -680,19 +681,21 @@ __global__ __launch_bounds__(NW * 64) void gemv_q6k_stream_kernel(TaskTable tt, 
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     // the four 6-bit codes u = q + 32 of elements 4j..4j+3, one per
-                    // byte, spread into binary16 halves: u * 2^-24 as denormals
-                    // into v_fma_mix_f32; sum (u-32)*x = 2^24 * sum u*x*2^-24 - 32 * sum x
+                    // byte; sum (u-32)*x = sum u*x - 32 * sum x
                     const uint32_t lo4 = __builtin_amdgcn_alignbit(ql[j], ql[j], nrot);
                     const uint32_t hi2 = __builtin_amdgcn_alignbit(qh[j], qh[j], hrot) & 0x30303030u;
-                    const uint32_t codes = (lo4 & 0x0F0F0F0Fu) | hi2;
-                    const uint32_t p02 = codes & 0x00FF00FFu;
-                    const uint32_t p13 = __builtin_amdgcn_perm(0u, codes, 0x0c030c01u);  // bytes 1, 3 -> halves
-                    t0 = mix_lo(p02, xv[k][4 * j], t0);
-                    t1 = mix_lo(p13, xv[k][4 * j + 1], t1);
-                    t0 = mix_hi(p02, xv[k][4 * j + 2], t0);
-                    t1 = mix_hi(p13, xv[k][4 * j + 3], t1);
+                    uint32_t codes = (lo4 & 0x0F0F0F0Fu) | hi2;
+                    // opaque to the combiner, so each byte converts with one
+                    // v_cvt_f32_ubyteN (one instruction per code, like Q8_0's SDWA
+                    // conversion; v_fma_mix_f32 on the codes as binary16
+                    // denormals issued more slowly)
+                    asm volatile("" : "+v"(codes));
+                    t0 = fmaf(float(codes & 0xffu), xv[k][4 * j], t0);
+                    t1 = fmaf(float((codes >> 8) & 0xffu), xv[k][4 * j + 1], t1);
+                    t0 = fmaf(float((codes >> 16) & 0xffu), xv[k][4 * j + 2], t0);
+                    t1 = fmaf(float(codes >> 24), xv[k][4 * j + 3], t1);
                 }
-                a = fmaf(d * sc, fmaf(t0 + t1, 16777216.0f, nsx[k]), a);
+                a = fmaf(d * sc, (t0 + t1) + nsx[k], a);
             }
             acc[r] = wave_sum(a);
         }
