@@ -84,7 +84,7 @@ __global__ __launch_bounds__(kNormT) void rmsnorm_kernel(float* __restrict__ x, 
                                                          float eps, int8_t* __restrict__ xq, float* __restrict__ xs) {
     __shared__ double red[kNormT / 64];
     float* xr = x + size_t(blockIdx.x) * n;
-    float* yr = y + size_t(blockIdx.x) * n;
+    float* yr = y ? y + size_t(blockIdx.x) * n : nullptr;  // null with xq: only the int8 form is wanted
     const float* rr = ADD ? r + size_t(blockIdx.x) * n : nullptr;
     double ss = 0.0;
     for (uint32_t i = threadIdx.x; i < n; i += kNormT) {
@@ -102,7 +102,7 @@ __global__ __launch_bounds__(kNormT) void rmsnorm_kernel(float* __restrict__ x, 
         float* sr = xs + size_t(blockIdx.x) * (n / 32);
         for (uint32_t i = threadIdx.x; i < n; i += kNormT) {
             const float v = xr[i] * inv * w[i];
-            yr[i] = v;
+            if (yr) yr[i] = v;
             quantize_lane_block32(v, qr + i, sr + i / 32);
         }
         return;
@@ -123,7 +123,7 @@ __global__ __launch_bounds__(kNormT) void rmsnorm4_kernel(float* __restrict__ x,
     __shared__ double red[kNormT / 64];
     const uint32_t n4 = n / 4;
     float4* xr = reinterpret_cast<float4*>(x + size_t(blockIdx.x) * n);
-    float4* yr = reinterpret_cast<float4*>(y + size_t(blockIdx.x) * n);
+    float4* yr = y ? reinterpret_cast<float4*>(y + size_t(blockIdx.x) * n) : nullptr;  // null with xq
     const float4* rr = ADD ? reinterpret_cast<const float4*>(r + size_t(blockIdx.x) * n) : nullptr;
     const float4* w4 = reinterpret_cast<const float4*>(w);
     float4 v[kNormV], b[ADD ? kNormV : 1], wv[kNormV];
@@ -158,7 +158,7 @@ __global__ __launch_bounds__(kNormT) void rmsnorm4_kernel(float* __restrict__ x,
         if (j * kNormT >= n4) break;  // uniform: no element of this round is live
         const float4 o = make_float4(v[j].x * inv * wv[j].x, v[j].y * inv * wv[j].y, v[j].z * inv * wv[j].z,
                                      v[j].w * inv * wv[j].w);
-        if (i < n4) yr[i] = o;
+        if (yr && i < n4) yr[i] = o;
         // n % 32 == 0 with xq: a round's live lanes are whole 8-lane blocks
         if (qr && i < n4) quantize_lane4_block32(o, qr + 4 * i, sr + i / 8);
     }
@@ -930,7 +930,7 @@ static bool norm4_ok(const void* x, const void* r, const void* w, const void* y,
 
 hipError_t launch_rmsnorm(const float* x, const float* w, float* y, uint32_t rows, uint32_t n, float eps,
                           hipStream_t stream, int8_t* xq, float* xs) {
-    if (!x || !w || !y || !rows || !n || (xq && (!xs || n % 32))) return hipErrorInvalidValue;
+    if (!x || !w || (!y && !xq) || !rows || !n || (xq && (!xs || n % 32))) return hipErrorInvalidValue;
     if (norm4_ok(x, nullptr, w, y, xq, n))
         hipLaunchKernelGGL(rmsnorm4_kernel<false>, dim3(rows), dim3(kNormT), 0, stream, const_cast<float*>(x), nullptr, w,
                            y, n, eps, xq, xs);
@@ -942,7 +942,7 @@ hipError_t launch_rmsnorm(const float* x, const float* w, float* y, uint32_t row
 
 hipError_t launch_add_rmsnorm(float* x, const float* r, const float* w, float* y, uint32_t rows, uint32_t n, float eps,
                               hipStream_t stream, int8_t* xq, float* xs) {
-    if (!x || !r || !w || !y || !rows || !n || (xq && (!xs || n % 32))) return hipErrorInvalidValue;
+    if (!x || !r || !w || (!y && !xq) || !rows || !n || (xq && (!xs || n % 32))) return hipErrorInvalidValue;
     if (norm4_ok(x, r, w, y, xq, n))
         hipLaunchKernelGGL(rmsnorm4_kernel<true>, dim3(rows), dim3(kNormT), 0, stream, x, r, w, y, n, eps, xq, xs);
     else

@@ -117,7 +117,7 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const float* __restr
         if (i >= n) return;
         const float gv = g[i];
         const float v = gv / (1.0f + expf(-gv)) * u[i];
-        o[i] = v;
+        if (o) o[i] = v;  // null with xq: only the int8 form is wanted
         quantize_lane_block32(v, xq + i, xs + i / 32);
         return;
     }
@@ -137,7 +137,7 @@ __global__ __launch_bounds__(kThreads) void silu_mul4_kernel(const float4* __res
     const float4 a = g[i], b = u[i];
     auto f = [](float gv, float uv) { return gv / (1.0f + expf(-gv)) * uv; };
     const float4 v = make_float4(f(a.x, b.x), f(a.y, b.y), f(a.z, b.z), f(a.w, b.w));
-    o[i] = v;
+    if (o) o[i] = v;  // null with xq: only the int8 form is wanted
     if (xq) quantize_lane4_block32(v, xq + 4 * i, xs + i / 8);
 }
 
@@ -212,7 +212,7 @@ hipError_t launch_mfma_probe(uint64_t* out, uint32_t wgs, uint32_t iters, hipStr
 
 hipError_t launch_silu_mul(const float* gate, const float* up, float* out, size_t n, hipStream_t stream, int8_t* xq,
                            float* xs) {
-    if (!gate || !up || !out || !n || (xq && (!xs || n % 32))) return hipErrorInvalidValue;
+    if (!gate || !up || (!out && !xq) || !n || (xq && (!xs || n % 32))) return hipErrorInvalidValue;
     auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
     if (n % 4 == 0 && a16(gate) && a16(up) && a16(out) && (reinterpret_cast<uintptr_t>(xq) & 3u) == 0) {
         const size_t n4 = n / 4;

@@ -275,15 +275,16 @@ hipError_t quantize_for(zq_model& m, std::initializer_list<const Weight*> ws, co
 hipError_t enqueue_layers(zq_model& m, uint32_t T) {
     const auto& c = m.cfg;
     const uint32_t E = c.embedding, QW = c.heads * c.head_dim, KW = c.kv_heads * c.head_dim, F = c.ffn;
-    // In prefill the RMSNorm and SiLU*up kernels also write the int8
-    // activations of their output when the projections that read it take
-    // them (the quantiser's own arithmetic, one launch fewer per GEMM group).
+    // In prefill the RMSNorm and SiLU*up kernels write the int8 activations
+    // of their output when the projections that read it take them (the
+    // quantiser's own arithmetic, one launch fewer per GEMM group), and then
+    // skip the fp32 output, which nothing reads.
     auto qin = [&](std::initializer_list<const Weight*> ws) { return T > 1 && m.fuse_quant && int8_inputs(m, ws); };
     {
         const Layer& L0 = m.layers[0];
         const bool q0 = qin({&L0.q, &L0.k, &L0.v});
-        HIPCHK(zq::launch_rmsnorm(m.x, L0.attn_norm, m.h, T, E, c.rms_epsilon, m.stream, q0 ? m.xq : nullptr,
-                                  q0 ? m.xs : nullptr));
+        HIPCHK(zq::launch_rmsnorm(m.x, L0.attn_norm, q0 ? nullptr : m.h, T, E, c.rms_epsilon, m.stream,
+                                  q0 ? m.xq : nullptr, q0 ? m.xs : nullptr));
     }
     for (uint32_t l = 0; l < c.layers; ++l) {
         Layer& L = m.layers[l];
@@ -331,8 +332,8 @@ hipError_t enqueue_layers(zq_model& m, uint32_t T) {
             HIPCHK(project(m, L.o, m.att, m.tmp, T, qz));
         }
         const bool qgu = qin({&L.gate, &L.up});
-        HIPCHK(zq::launch_add_rmsnorm(m.x, m.tmp, L.ffn_norm, m.h, T, E, c.rms_epsilon, m.stream, qgu ? m.xq : nullptr,
-                                      qgu ? m.xs : nullptr));
+        HIPCHK(zq::launch_add_rmsnorm(m.x, m.tmp, L.ffn_norm, qgu ? nullptr : m.h, T, E, c.rms_epsilon, m.stream,
+                                      qgu ? m.xq : nullptr, qgu ? m.xs : nullptr));
         if (T == 1) {
             zq::GemvTask t[2] = {{L.gate.p, m.gate, F}, {L.up.p, m.up, F}};
             if (L.gate.fmt == L.up.fmt) {
@@ -348,8 +349,8 @@ hipError_t enqueue_layers(zq_model& m, uint32_t T) {
             HIPCHK(project(m, L.up, m.h, m.up, T, qz));
         }
         const bool qd = qin({&L.down});
-        HIPCHK(zq::launch_silu_mul(m.gate, m.up, m.act, size_t(T) * F, m.stream, qd ? m.xq : nullptr,
-                                   qd ? m.xs : nullptr));
+        HIPCHK(zq::launch_silu_mul(m.gate, m.up, qd ? nullptr : m.act, size_t(T) * F, m.stream,
+                                   qd ? m.xq : nullptr, qd ? m.xs : nullptr));
         if (T == 1) {
             zq::GemvTask t = {L.down.p, m.tmp, E};
             HIPCHK(zq::launch_gemv(L.down.fmt, &t, 1, m.act, F, m.stream));
@@ -360,8 +361,8 @@ hipError_t enqueue_layers(zq_model& m, uint32_t T) {
         }
         const float* next_norm = l + 1 < c.layers ? m.layers[l + 1].attn_norm : m.out_norm;
         const bool qn = l + 1 < c.layers && qin({&m.layers[l + 1].q, &m.layers[l + 1].k, &m.layers[l + 1].v});
-        HIPCHK(zq::launch_add_rmsnorm(m.x, m.tmp, next_norm, m.h, T, E, c.rms_epsilon, m.stream, qn ? m.xq : nullptr,
-                                      qn ? m.xs : nullptr));
+        HIPCHK(zq::launch_add_rmsnorm(m.x, m.tmp, next_norm, qn ? nullptr : m.h, T, E, c.rms_epsilon, m.stream,
+                                      qn ? m.xq : nullptr, qn ? m.xs : nullptr));
     }
     return hipSuccess;
 }
