@@ -1358,9 +1358,13 @@ size_t gemm_i8_partial_bytes(size_t M, size_t N, size_t K) {
 constexpr size_t kSmallMLimit = 64;
 
 // Reduces the K splits of `partial` into Y (fixed order) when ks > 1.
+// deferred (optional): receives the split count instead of the reduction
+// being enqueued; with more than one split the partial planes are left for
+// the caller to sum (in split order, as splitk_reduce_kernel does).
 static hipError_t finish_splits(hipError_t e, const float* partial, float* Y, size_t M, size_t N, uint32_t ks,
-                                hipStream_t stream) {
-    if (e != hipSuccess || ks <= 1) return e;
+                                hipStream_t stream, uint32_t* deferred = nullptr) {
+    if (deferred) *deferred = ks;
+    if (e != hipSuccess || ks <= 1 || deferred) return e;
     const size_t total = M * N;
     const bool vec4 = total % 4 == 0 && !(reinterpret_cast<uintptr_t>(partial) & 15u) &&
                       !(reinterpret_cast<uintptr_t>(Y) & 15u);
@@ -1377,7 +1381,8 @@ static hipError_t finish_splits(hipError_t e, const float* partial, float* Y, si
 // else the 128-token tile with 4-block (default) or 8-block stages.
 template <int FMT>
 static hipError_t launch_direct(const uint8_t* w, const int8_t* xq, const float* xs, float* Y, int32_t* dots,
-                                float* partial, size_t M, size_t N, size_t K, hipStream_t stream) {
+                                float* partial, size_t M, size_t N, size_t K, hipStream_t stream,
+                                uint32_t* deferred = nullptr) {
     constexpr int BB = FMT == kQ8_0 ? 34 : 18;
     constexpr size_t kSmallLds = 2 * QStage<4, 32, 4, BB>::BUF;
     constexpr size_t kLds4 = 2 * QStage<4, BM, QTH / 64, BB>::BUF;
@@ -1396,7 +1401,7 @@ static hipError_t launch_direct(const uint8_t* w, const int8_t* xq, const float*
         ks = (sst + spw - 1) / spw;  // no empty splits
         hipLaunchKernelGGL((gemm_i8_skinny_kernel<FMT, false>), dim3(stm * stn * ks), dim3(256), lds, stream, w, xq, xs,
                            ks > 1 ? partial : Y, dots, m, n, k, stm, stn, ks, spw);
-        return finish_splits(hipGetLastError(), partial, Y, M, N, ks, stream);
+        return finish_splits(hipGetLastError(), partial, Y, M, N, ks, stream, deferred);
     }
     if (M <= kSmallMLimit) {
         const uint32_t stm = uint32_t((M + 31) / 32), sst = (nb + 3) / 4;
@@ -1410,7 +1415,7 @@ static hipError_t launch_direct(const uint8_t* w, const int8_t* xq, const float*
         ks = (sst + spw - 1) / spw;  // no empty splits
         hipLaunchKernelGGL((gemm_i8_small_kernel<FMT, false>), dim3(stm * tiles_n * ks), dim3(256), kSmallLds, stream, w,
                            xq, xs, ks > 1 ? partial : Y, dots, m, n, k, stm, tiles_n, ks, spw);
-        return finish_splits(hipGetLastError(), partial, Y, M, N, ks, stream);
+        return finish_splits(hipGetLastError(), partial, Y, M, N, ks, stream, deferred);
     }
     const uint32_t tiles_m = static_cast<uint32_t>((M + BM - 1) / BM);
     const uint32_t st = (nb + 3) / 4;
@@ -1425,11 +1430,12 @@ static hipError_t launch_direct(const uint8_t* w, const int8_t* xq, const float*
     float* out = ks > 1 ? partial : Y;
     hipLaunchKernelGGL((gemm_i8_direct4_kernel<FMT, false>), dim3(tiles_m * tiles_n * ks), dim3(QTH), kLds4, stream, w,
                        xq, xs, out, dots, m, n, k, tiles_m, tiles_n, ks, spw);
-    return finish_splits(hipGetLastError(), partial, Y, M, N, ks, stream);
+    return finish_splits(hipGetLastError(), partial, Y, M, N, ks, stream, deferred);
 }
 
 static hipError_t launch_i8_common(int fmt, const uint8_t* w, const int8_t* xq, const float* xs, float* Y,
-                                   int32_t* dots, float* partial, size_t M, size_t N, size_t K, hipStream_t stream) {
+                                   int32_t* dots, float* partial, size_t M, size_t N, size_t K, hipStream_t stream,
+                                   uint32_t* deferred = nullptr) {
     if (!w || !xq || !M || !N || !K || K % 64 || M > (1u << 24) || N > (1u << 24) || K > (1u << 24))
         return hipErrorInvalidValue;
     if (fmt != kQ8_0 && fmt != kQ4_0) return hipErrorInvalidValue;
@@ -1440,8 +1446,8 @@ static hipError_t launch_i8_common(int fmt, const uint8_t* w, const int8_t* xq, 
     const size_t rb = row_bytes(fmt, K);
     const bool offsets_fit = size_t(BM + 1) * K < (size_t(1) << 31) && size_t(BN + 1) * rb < (size_t(1) << 31);
     if (K % 256 == 0 && offsets_fit)
-        return fmt == kQ8_0 ? launch_direct<kQ8_0>(w, xq, xs, Y, dots, partial, M, N, K, stream)
-                            : launch_direct<kQ4_0>(w, xq, xs, Y, dots, partial, M, N, K, stream);
+        return fmt == kQ8_0 ? launch_direct<kQ8_0>(w, xq, xs, Y, dots, partial, M, N, K, stream, deferred)
+                            : launch_direct<kQ4_0>(w, xq, xs, Y, dots, partial, M, N, K, stream, deferred);
 
     // Staged-conversion kernel (any K % 64 == 0).
     const uint32_t tiles_m = static_cast<uint32_t>((M + BM - 1) / BM);
@@ -1470,12 +1476,12 @@ static hipError_t launch_i8_common(int fmt, const uint8_t* w, const int8_t* xq, 
     else
         hipLaunchKernelGGL((gemm_i8_kernel<kQ4_0, false>), grid, dim3(kThreads), 0, stream, w, xq, xs, out, dots, m, n,
                            k, tiles_m, tiles_n, ks, spw);
-    return finish_splits(hipGetLastError(), partial, Y, M, N, ks, stream);
+    return finish_splits(hipGetLastError(), partial, Y, M, N, ks, stream, deferred);
 }
 
 hipError_t launch_gemm_i8(int fmt, const uint8_t* w, const int8_t* xq, const float* xs, float* Y, float* partial,
-                          size_t M, size_t N, size_t K, hipStream_t stream) {
-    return launch_i8_common(fmt, w, xq, xs, Y, nullptr, partial, M, N, K, stream);
+                          size_t M, size_t N, size_t K, hipStream_t stream, uint32_t* splits) {
+    return launch_i8_common(fmt, w, xq, xs, Y, nullptr, partial, M, N, K, stream, splits);
 }
 
 hipError_t launch_block_dots(int fmt, const uint8_t* w, const int8_t* xq, int32_t* out, size_t M, size_t N, size_t K,

@@ -100,8 +100,12 @@ hipError_t launch_quantize_acts(const float* X, int8_t* xq, float* xs, size_t M,
 size_t gemm_i8_partial_bytes(size_t M, size_t N, size_t K);
 // Compute units of the current device (256 on MI355X; 256 if the query fails).
 int device_cu_count();
+// splits (optional): the split-K reduction is left to the caller, which gets
+// the split count; with more than one, Y is untouched and the partial planes
+// (partial + s * M * N, s < splits) are to be summed in split order.
 hipError_t launch_gemm_i8(int fmt, const uint8_t* w, const int8_t* xq, const float* xs,
-                          float* Y, float* partial, size_t M, size_t N, size_t K, hipStream_t stream);
+                          float* Y, float* partial, size_t M, size_t N, size_t K, hipStream_t stream,
+                          uint32_t* splits = nullptr);
 
 // Prefill GEMM on fp32 activations (the reference CPU arithmetic).  `ws`
 // (ws_bytes, may be null) is the workspace: gemm_f32_workspace_bytes() lets
@@ -168,9 +172,10 @@ hipError_t launch_attention_decode(const float* q, const float* knew, const floa
 hipError_t launch_add(float* x, const float* y, size_t n, hipStream_t stream);
 // out = x + y elementwise (out may alias x)
 hipError_t launch_add_to(const float* x, const float* y, float* out, size_t n, hipStream_t stream);
-// x += r, then y = rmsnorm(x) * w (rows of n)
+// x += r, then y = rmsnorm(x) * w (rows of n).  rsplit > 1: r is that many
+// [rows][n] planes (a GEMM's split-K partials), summed in split order first.
 hipError_t launch_add_rmsnorm(float* x, const float* r, const float* w, float* y, uint32_t rows, uint32_t n, float eps,
-                              hipStream_t stream, int8_t* xq = nullptr, float* xs = nullptr);
+                              hipStream_t stream, int8_t* xq = nullptr, float* xs = nullptr, uint32_t rsplit = 1);
 // Greedy id over n values; `partial` holds argmax_partial_bytes().
 size_t argmax_partial_bytes();
 hipError_t launch_argmax(const float* x, uint32_t n, uint32_t* out, void* partial, hipStream_t stream);

@@ -81,7 +81,8 @@ constexpr int kNormT = 1024;
 template <bool ADD>
 __global__ __launch_bounds__(kNormT) void rmsnorm_kernel(float* __restrict__ x, const float* __restrict__ r,
                                                          const float* __restrict__ w, float* __restrict__ y, uint32_t n,
-                                                         float eps, int8_t* __restrict__ xq, float* __restrict__ xs) {
+                                                         float eps, int8_t* __restrict__ xq, float* __restrict__ xs,
+                                                         uint32_t rsplit) {
     __shared__ double red[kNormT / 64];
     float* xr = x + size_t(blockIdx.x) * n;
     float* yr = y ? y + size_t(blockIdx.x) * n : nullptr;  // null with xq: only the int8 form is wanted
@@ -90,7 +91,9 @@ __global__ __launch_bounds__(kNormT) void rmsnorm_kernel(float* __restrict__ x, 
     for (uint32_t i = threadIdx.x; i < n; i += kNormT) {
         float v = xr[i];
         if constexpr (ADD) {
-            v += rr[i];
+            float t = rr[i];  // r's planes summed in split order (splitk_reduce_kernel's)
+            for (uint32_t s = 1; s < rsplit; ++s) t += rr[size_t(s) * gridDim.x * n + i];
+            v += t;
             xr[i] = v;
         }
         ss += double(v) * double(v);
@@ -119,7 +122,8 @@ constexpr int kNormV = 4;
 template <bool ADD>
 __global__ __launch_bounds__(kNormT) void rmsnorm4_kernel(float* __restrict__ x, const float* __restrict__ r,
                                                           const float* __restrict__ w, float* __restrict__ y, uint32_t n,
-                                                          float eps, int8_t* __restrict__ xq, float* __restrict__ xs) {
+                                                          float eps, int8_t* __restrict__ xq, float* __restrict__ xs,
+                                                          uint32_t rsplit) {
     __shared__ double red[kNormT / 64];
     const uint32_t n4 = n / 4;
     float4* xr = reinterpret_cast<float4*>(x + size_t(blockIdx.x) * n);
@@ -133,6 +137,11 @@ __global__ __launch_bounds__(kNormT) void rmsnorm4_kernel(float* __restrict__ x,
         const bool live = i < n4;
         v[j] = live ? xr[i] : make_float4(0, 0, 0, 0);
         if constexpr (ADD) b[j] = live ? rr[i] : make_float4(0, 0, 0, 0);
+        if constexpr (ADD)  // r's further planes, summed in split order (splitk_reduce_kernel's)
+            for (uint32_t s = 1; s < rsplit; ++s) {
+                const float4 t = live ? rr[size_t(s) * gridDim.x * n4 + i] : make_float4(0, 0, 0, 0);
+                b[j] = make_float4(b[j].x + t.x, b[j].y + t.y, b[j].z + t.z, b[j].w + t.w);
+            }
         wv[j] = live ? w4[i] : make_float4(0, 0, 0, 0);
     }
     double ss = 0.0;
@@ -933,20 +942,21 @@ hipError_t launch_rmsnorm(const float* x, const float* w, float* y, uint32_t row
     if (!x || !w || (!y && !xq) || !rows || !n || (xq && (!xs || n % 32))) return hipErrorInvalidValue;
     if (norm4_ok(x, nullptr, w, y, xq, n))
         hipLaunchKernelGGL(rmsnorm4_kernel<false>, dim3(rows), dim3(kNormT), 0, stream, const_cast<float*>(x), nullptr, w,
-                           y, n, eps, xq, xs);
+                           y, n, eps, xq, xs, 1u);
     else
         hipLaunchKernelGGL(rmsnorm_kernel<false>, dim3(rows), dim3(kNormT), 0, stream, const_cast<float*>(x), nullptr, w,
-                           y, n, eps, xq, xs);
+                           y, n, eps, xq, xs, 1u);
     return hipGetLastError();
 }
 
 hipError_t launch_add_rmsnorm(float* x, const float* r, const float* w, float* y, uint32_t rows, uint32_t n, float eps,
-                              hipStream_t stream, int8_t* xq, float* xs) {
+                              hipStream_t stream, int8_t* xq, float* xs, uint32_t rsplit) {
+    if (rsplit < 1) return hipErrorInvalidValue;
     if (!x || !r || !w || (!y && !xq) || !rows || !n || (xq && (!xs || n % 32))) return hipErrorInvalidValue;
     if (norm4_ok(x, r, w, y, xq, n))
-        hipLaunchKernelGGL(rmsnorm4_kernel<true>, dim3(rows), dim3(kNormT), 0, stream, x, r, w, y, n, eps, xq, xs);
+        hipLaunchKernelGGL(rmsnorm4_kernel<true>, dim3(rows), dim3(kNormT), 0, stream, x, r, w, y, n, eps, xq, xs, rsplit);
     else
-        hipLaunchKernelGGL(rmsnorm_kernel<true>, dim3(rows), dim3(kNormT), 0, stream, x, r, w, y, n, eps, xq, xs);
+        hipLaunchKernelGGL(rmsnorm_kernel<true>, dim3(rows), dim3(kNormT), 0, stream, x, r, w, y, n, eps, xq, xs, rsplit);
     return hipGetLastError();
 }
 

@@ -229,8 +229,14 @@ bool init_common(zq_model& m, std::string& e) {
 
 // y[M][N] = X[M][K] . W^T through the GEMM (prefill) -- X already quantised
 // into xq/xs when `quantized` (int8 mode).
-hipError_t project(zq_model& m, const Weight& w, const float* X, float* Y, uint32_t M, bool quantized) {
-    if (quantized) return zq::launch_gemm_i8(w.fmt, w.p, m.xq, m.xs, Y, m.partial, M, w.rows, w.cols, m.stream);
+// splits (optional, int8 activations only): the split-K reduction is left to
+// the reader of Y, which sums the *splits planes at m.partial (Y is not
+// written when *splits > 1).
+hipError_t project(zq_model& m, const Weight& w, const float* X, float* Y, uint32_t M, bool quantized,
+                   uint32_t* splits = nullptr) {
+    if (splits) *splits = 1;
+    if (quantized)
+        return zq::launch_gemm_i8(w.fmt, w.p, m.xq, m.xs, Y, m.partial, M, w.rows, w.cols, m.stream, splits);
     return zq::launch_gemm_f32(w.fmt, w.p, X, Y, m.partial, m.partial_bytes, M, w.rows, w.cols, m.stream);
 }
 
@@ -288,6 +294,7 @@ hipError_t enqueue_layers(zq_model& m, uint32_t T) {
     }
     for (uint32_t l = 0; l < c.layers; ++l) {
         Layer& L = m.layers[l];
+        uint32_t o_splits = 1, d_splits = 1;  // split-K planes of the o / down outputs left to the norms
         if (T == 1) {
             // decode: the three projections share x -> one batched GEMV per format
             zq::GemvTask t[3] = {{L.q.p, m.q, QW}, {L.k.p, m.k, KW}, {L.v.p, m.v, KW}};
@@ -329,11 +336,12 @@ hipError_t enqueue_layers(zq_model& m, uint32_t T) {
                                         c.max_positions, m.attn_scale, m.stream));
             bool qz;
             HIPCHK(quantize_for(m, {&L.o}, m.att, T, QW, qz));
-            HIPCHK(project(m, L.o, m.att, m.tmp, T, qz));
+            HIPCHK(project(m, L.o, m.att, m.tmp, T, qz, &o_splits));
         }
+        // the o projection's split-K partials, if any, are summed by the norm
         const bool qgu = qin({&L.gate, &L.up});
-        HIPCHK(zq::launch_add_rmsnorm(m.x, m.tmp, L.ffn_norm, qgu ? nullptr : m.h, T, E, c.rms_epsilon, m.stream,
-                                      qgu ? m.xq : nullptr, qgu ? m.xs : nullptr));
+        HIPCHK(zq::launch_add_rmsnorm(m.x, o_splits > 1 ? m.partial : m.tmp, L.ffn_norm, qgu ? nullptr : m.h, T, E,
+                                      c.rms_epsilon, m.stream, qgu ? m.xq : nullptr, qgu ? m.xs : nullptr, o_splits));
         if (T == 1) {
             zq::GemvTask t[2] = {{L.gate.p, m.gate, F}, {L.up.p, m.up, F}};
             if (L.gate.fmt == L.up.fmt) {
@@ -357,12 +365,12 @@ hipError_t enqueue_layers(zq_model& m, uint32_t T) {
         } else {
             bool qz = qd;
             if (!qz) HIPCHK(quantize_for(m, {&L.down}, m.act, T, F, qz));
-            HIPCHK(project(m, L.down, m.act, m.tmp, T, qz));
+            HIPCHK(project(m, L.down, m.act, m.tmp, T, qz, &d_splits));
         }
         const float* next_norm = l + 1 < c.layers ? m.layers[l + 1].attn_norm : m.out_norm;
         const bool qn = l + 1 < c.layers && qin({&m.layers[l + 1].q, &m.layers[l + 1].k, &m.layers[l + 1].v});
-        HIPCHK(zq::launch_add_rmsnorm(m.x, m.tmp, next_norm, qn ? nullptr : m.h, T, E, c.rms_epsilon, m.stream,
-                                      qn ? m.xq : nullptr, qn ? m.xs : nullptr));
+        HIPCHK(zq::launch_add_rmsnorm(m.x, d_splits > 1 ? m.partial : m.tmp, next_norm, qn ? nullptr : m.h, T, E,
+                                      c.rms_epsilon, m.stream, qn ? m.xq : nullptr, qn ? m.xs : nullptr, d_splits));
     }
     return hipSuccess;
 }
