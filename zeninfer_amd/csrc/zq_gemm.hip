@@ -1479,6 +1479,11 @@ static hipError_t launch_i8_common(int fmt, const uint8_t* w, const int8_t* xq, 
     return finish_splits(hipGetLastError(), partial, Y, M, N, ks, stream, deferred);
 }
 
+hipError_t launch_splitk_reduce(const float* partial, float* Y, size_t M, size_t N, uint32_t splits, hipStream_t stream) {
+    if (!partial || !Y || !splits) return hipErrorInvalidValue;
+    return finish_splits(hipSuccess, partial, Y, M, N, splits, stream);
+}
+
 hipError_t launch_gemm_i8(int fmt, const uint8_t* w, const int8_t* xq, const float* xs, float* Y, float* partial,
                           size_t M, size_t N, size_t K, hipStream_t stream, uint32_t* splits) {
     return launch_i8_common(fmt, w, xq, xs, Y, nullptr, partial, M, N, K, stream, splits);

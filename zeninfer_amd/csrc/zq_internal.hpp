@@ -106,6 +106,9 @@ int device_cu_count();
 hipError_t launch_gemm_i8(int fmt, const uint8_t* w, const int8_t* xq, const float* xs,
                           float* Y, float* partial, size_t M, size_t N, size_t K, hipStream_t stream,
                           uint32_t* splits = nullptr);
+// Y[M][N] = the sum of `splits` partial planes in split order (the reduction
+// launch_gemm_i8 leaves to its caller when asked to).
+hipError_t launch_splitk_reduce(const float* partial, float* Y, size_t M, size_t N, uint32_t splits, hipStream_t stream);
 
 // Prefill GEMM on fp32 activations (the reference CPU arithmetic).  `ws`
 // (ws_bytes, may be null) is the workspace: gemm_f32_workspace_bytes() lets
@@ -154,7 +157,7 @@ hipError_t launch_rmsnorm(const float* x, const float* w, float* y, uint32_t row
 hipError_t launch_rope_kv(float* q, const float* k, const float* v, float* kc, float* vc, const float* cos_tab,
                           const float* sin_tab, const uint32_t* pos0, uint32_t T, uint32_t H, uint32_t KH, uint32_t D,
                           uint32_t pairs, bool adjacent, hipStream_t stream, uint32_t ld = 0,
-                          const float* q_in = nullptr);
+                          const float* q_in = nullptr, uint32_t splits = 1, float* reduce_to = nullptr);
 hipError_t launch_attention(const float* q, const float* kc, const float* vc, float* out, const uint32_t* pos0,
                             uint32_t T, uint32_t H, uint32_t KH, uint32_t D, uint32_t max_pos, float scale,
                             hipStream_t stream);

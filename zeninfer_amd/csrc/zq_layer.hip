@@ -970,7 +970,8 @@ __global__ __launch_bounds__(kT) void rope_kv4_kernel(const float* q, float* q_o
                                                       float* __restrict__ vc, const float* __restrict__ cos_tab,
                                                       const float* __restrict__ sin_tab,
                                                       const uint32_t* __restrict__ pos0, uint32_t H, uint32_t KH,
-                                                      uint32_t D, uint32_t pairs, uint32_t ldq, uint32_t ldkv) {
+                                                      uint32_t D, uint32_t pairs, uint32_t ldq, uint32_t ldkv,
+                                                      uint32_t splits, size_t plane4) {
     const uint32_t t = blockIdx.x;
     const uint32_t pos = *pos0 + t;
     const float* cs = cos_tab + size_t(pos) * pairs;
@@ -989,6 +990,7 @@ __global__ __launch_bounds__(kT) void rope_kv4_kernel(const float* q, float* q_o
         const float2 s = *reinterpret_cast<const float2*>(sn + 2 * d4);
         return make_float4(c.x, c.y, s.x, s.y);
     };
+    auto add4 = [](float4 a, float4 b) { return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w); };
 #pragma unroll
     for (int j = 0; j < kRopeQV; ++j) {
         const uint32_t i = threadIdx.x + j * kT, d4 = i % D4;
@@ -1001,6 +1003,23 @@ __global__ __launch_bounds__(kT) void rope_kv4_kernel(const float* q, float* q_o
         kv[j] = i < nk ? kt[i] : make_float4(0, 0, 0, 0);
         vv[j] = i < nk ? vt[i] : make_float4(0, 0, 0, 0);
         kcs[j] = i < nk && d4 < rot4 ? factors(d4) : make_float4(1, 1, 0, 0);
+    }
+    // splits > 1: q, k, v are a GEMM's split-K partial planes (plane4 float4s
+    // apart), summed here in split order (splitk_reduce_kernel's)
+    for (uint32_t s = 1; s < splits; ++s) {
+#pragma unroll
+        for (int j = 0; j < kRopeQV; ++j) {
+            const uint32_t i = threadIdx.x + j * kT;
+            if (i < nq) qv[j] = add4(qv[j], qt[s * plane4 + i]);
+        }
+#pragma unroll
+        for (int j = 0; j < kRopeKV; ++j) {
+            const uint32_t i = threadIdx.x + j * kT;
+            if (i < nk) {
+                kv[j] = add4(kv[j], kt[s * plane4 + i]);
+                vv[j] = add4(vv[j], vt[s * plane4 + i]);
+            }
+        }
     }
     auto rot = [](float4 x, float4 f) {  // pairs (x, y) and (z, w)
         return make_float4(x.x * f.x - x.y * f.z, x.x * f.z + x.y * f.x, x.z * f.y - x.w * f.w, x.z * f.w + x.w * f.y);
@@ -1022,9 +1041,11 @@ __global__ __launch_bounds__(kT) void rope_kv4_kernel(const float* q, float* q_o
 
 hipError_t launch_rope_kv(float* q, const float* k, const float* v, float* kc, float* vc, const float* cos_tab,
                           const float* sin_tab, const uint32_t* pos0, uint32_t T, uint32_t H, uint32_t KH, uint32_t D,
-                          uint32_t pairs, bool adjacent, hipStream_t stream, uint32_t ld, const float* q_in) {
+                          uint32_t pairs, bool adjacent, hipStream_t stream, uint32_t ld, const float* q_in,
+                          uint32_t splits, float* reduce_to) {
     if (!q || !k || !v || !kc || !vc || !cos_tab || !sin_tab || !pos0 || !T || !H || !KH || !D || !pairs ||
-        pairs > D / 2 || H % KH || (ld && ld < (H + 2 * KH) * D) || (q_in && !ld))
+        pairs > D / 2 || H % KH || (ld && ld < (H + 2 * KH) * D) || (q_in && !ld) || !splits ||
+        (splits > 1 && (!q_in || !reduce_to)))
         return hipErrorInvalidValue;
     const float* qi = q_in ? q_in : q;
     const uint32_t ldq = ld ? ld : H * D, ldkv = ld ? ld : KH * D;
@@ -1033,8 +1054,15 @@ hipError_t launch_rope_kv(float* q, const float* k, const float* v, float* kc, f
         KH * D <= 4u * kRopeKV * kT && a16(qi) && a16(q) && a16(k) && a16(v) && a16(kc) && a16(vc) && a16(cos_tab) &&
         a16(sin_tab)) {
         hipLaunchKernelGGL(rope_kv4_kernel, dim3(T), dim3(kT), 0, stream, qi, q, k, v, kc, vc, cos_tab, sin_tab, pos0, H,
-                           KH, D, pairs, ldq, ldkv);
+                           KH, D, pairs, ldq, ldkv, splits, size_t(T) * ld / 4);
         return hipGetLastError();
+    }
+    if (splits > 1) {  // the partial planes reduced into reduce_to first (q_in's layout), then as one plane
+        const hipError_t e = launch_splitk_reduce(q_in, reduce_to, T, ld, splits, stream);
+        if (e != hipSuccess) return e;
+        k = reduce_to + (k - q_in);
+        v = reduce_to + (v - q_in);
+        qi = reduce_to;
     }
     hipLaunchKernelGGL(rope_kv_kernel, dim3(T), dim3(kT), 0, stream, qi, q, k, v, kc, vc, cos_tab, sin_tab, pos0, H, KH,
                        D, pairs, adjacent ? 1 : 0, ld ? ld : H * D, ld ? ld : KH * D);

@@ -294,7 +294,9 @@ hipError_t enqueue_layers(zq_model& m, uint32_t T) {
     }
     for (uint32_t l = 0; l < c.layers; ++l) {
         Layer& L = m.layers[l];
-        uint32_t o_splits = 1, d_splits = 1;  // split-K planes of the o / down outputs left to the norms
+        // split-K planes of the qkv / o / down GEMM outputs left to their readers
+        // (the RoPE + KV-append kernel, the norms)
+        uint32_t qkv_splits = 1, o_splits = 1, d_splits = 1;
         if (T == 1) {
             // decode: the three projections share x -> one batched GEMV per format
             zq::GemvTask t[3] = {{L.q.p, m.q, QW}, {L.k.p, m.k, KW}, {L.v.p, m.v, KW}};
@@ -310,7 +312,7 @@ hipError_t enqueue_layers(zq_model& m, uint32_t T) {
             if (!qz) HIPCHK(quantize_for(m, {&L.q, &L.k, &L.v}, m.h, T, E, qz));
             Weight qkv;
             if (qkv_packed(L, qkv)) {
-                HIPCHK(project(m, qkv, m.h, m.qkv, T, qz));
+                HIPCHK(project(m, qkv, m.h, m.qkv, T, qz, &qkv_splits));
             } else {
                 HIPCHK(project(m, L.q, m.h, m.q, T, qz));
                 HIPCHK(project(m, L.k, m.h, m.k, T, qz));
@@ -325,10 +327,12 @@ hipError_t enqueue_layers(zq_model& m, uint32_t T) {
             HIPCHK(zq::launch_gemv(L.o.fmt, &t, 1, m.att, QW, m.stream));
         } else {
             Weight qkv;
-            if (qkv_packed(L, qkv))
-                HIPCHK(zq::launch_rope_kv(m.q, m.qkv + QW, m.qkv + QW + KW, L.kc, L.vc, m.cos_tab, m.sin_tab, m.pos_dev,
-                                          T, c.heads, c.kv_heads, c.head_dim, m.pairs, true, m.stream, QW + 2 * KW,
-                                          m.qkv));
+            if (qkv_packed(L, qkv)) {
+                const float* base = qkv_splits > 1 ? m.partial : m.qkv;
+                HIPCHK(zq::launch_rope_kv(m.q, base + QW, base + QW + KW, L.kc, L.vc, m.cos_tab, m.sin_tab, m.pos_dev, T,
+                                          c.heads, c.kv_heads, c.head_dim, m.pairs, true, m.stream, QW + 2 * KW, base,
+                                          qkv_splits, m.qkv));
+            }
             else
                 HIPCHK(zq::launch_rope_kv(m.q, m.k, m.v, L.kc, L.vc, m.cos_tab, m.sin_tab, m.pos_dev, T, c.heads,
                                           c.kv_heads, c.head_dim, m.pairs, true, m.stream));
