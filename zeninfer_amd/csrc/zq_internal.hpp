@@ -158,9 +158,12 @@ hipError_t launch_rope_kv(float* q, const float* k, const float* v, float* kc, f
                           const float* sin_tab, const uint32_t* pos0, uint32_t T, uint32_t H, uint32_t KH, uint32_t D,
                           uint32_t pairs, bool adjacent, hipStream_t stream, uint32_t ld = 0,
                           const float* q_in = nullptr, uint32_t splits = 1, float* reduce_to = nullptr);
+// xq / xs (optional, with `quantized`): the output's int8 activations and
+// block scales instead of out, when the kernel taken supports it (*quantized
+// then true; else out is written as usual).
 hipError_t launch_attention(const float* q, const float* kc, const float* vc, float* out, const uint32_t* pos0,
                             uint32_t T, uint32_t H, uint32_t KH, uint32_t D, uint32_t max_pos, float scale,
-                            hipStream_t stream);
+                            hipStream_t stream, int8_t* xq = nullptr, float* xs = nullptr, bool* quantized = nullptr);
 // Decode attention split over 32-position chunks, the last chunk of each kv
 // head merging; `part` holds attention_decode_partial_floats(H, D, max_pos)
 // floats and must be zero when first used (its tail holds arrival counters

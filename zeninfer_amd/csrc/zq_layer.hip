@@ -322,7 +322,8 @@ template <int D>
 __global__ __launch_bounds__(kT) void attention_prefill_t_kernel(const float* __restrict__ q, const float* __restrict__ kc,
                                                                  const float* __restrict__ vc, float* __restrict__ out,
                                                                  const uint32_t* __restrict__ pos0_ptr, uint32_t T,
-                                                                 uint32_t H, uint32_t KH, float scale) {
+                                                                 uint32_t H, uint32_t KH, float scale,
+                                                                 int8_t* __restrict__ xq, float* __restrict__ xs) {
     constexpr int HP = kFHP(D), KP = kFKP;
     constexpr int NT = D / 32;  // 32-row O^T tiles (head-dim blocks)
     constexpr int KS = D / 16;  // k-steps of S^T
@@ -564,18 +565,47 @@ __global__ __launch_bounds__(kT) void attention_prefill_t_kernel(const float* __
         const float L = l_run * a0 + l1 * a1;
         const float inv = pow2f(-14) / fv_prev / L;
         const uint32_t g = qrow / TQ;
-        float* orow = out + (size_t(t0 + qt) * H + kh * G + g) * D;
+        const size_t row_off = (size_t(t0 + qt) * H + kh * G + g) * D;
+        float* orow = out + row_off;
 #pragma unroll
-        for (int n = 0; n < NT; ++n)
+        for (int n = 0; n < NT; ++n) {
+            float4 r[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                float4 r;
-                r.x = (o[n][4 * j] * a0 + mp[(n * 16 + 4 * j) * 64 + lane] * a1) * inv;
-                r.y = (o[n][4 * j + 1] * a0 + mp[(n * 16 + 4 * j + 1) * 64 + lane] * a1) * inv;
-                r.z = (o[n][4 * j + 2] * a0 + mp[(n * 16 + 4 * j + 2) * 64 + lane] * a1) * inv;
-                r.w = (o[n][4 * j + 3] * a0 + mp[(n * 16 + 4 * j + 3) * 64 + lane] * a1) * inv;
-                *reinterpret_cast<float4*>(orow + 32 * n + 8 * j + 4 * lh) = r;
+                r[j].x = (o[n][4 * j] * a0 + mp[(n * 16 + 4 * j) * 64 + lane] * a1) * inv;
+                r[j].y = (o[n][4 * j + 1] * a0 + mp[(n * 16 + 4 * j + 1) * 64 + lane] * a1) * inv;
+                r[j].z = (o[n][4 * j + 2] * a0 + mp[(n * 16 + 4 * j + 2) * 64 + lane] * a1) * inv;
+                r[j].w = (o[n][4 * j + 3] * a0 + mp[(n * 16 + 4 * j + 3) * 64 + lane] * a1) * inv;
             }
+            if (!xq) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) *reinterpret_cast<float4*>(orow + 32 * n + 8 * j + 4 * lh) = r[j];
+                continue;
+            }
+            // only the int8 form for the o GEMM: the 32-element block 32n..32n+31
+            // of this row is split over this lane (4 * lh + 8j + 0..3) and its
+            // partner lane ^ 32; the quantiser's arithmetic (quantize_acts_kernel)
+            float amax = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                amax = fmaxf(amax, fmaxf(fmaxf(fabsf(r[j].x), fabsf(r[j].y)), fmaxf(fabsf(r[j].z), fabsf(r[j].w))));
+            amax = fmaxf(amax, __shfl_xor(amax, 32));
+            const float d = amax > 0.0f ? amax / 127.0f : 0.0f;
+            const float id = d > 0.0f ? 1.0f / d : 0.0f;
+            if (lh == 0) xs[(row_off >> 5) + n] = d;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float e[4] = {r[j].x, r[j].y, r[j].z, r[j].w};
+                uint32_t w = 0;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    float qv = e[k] * id;
+                    qv = qv > 127.0f ? 127.0f : (qv < -127.0f ? -127.0f : qv);
+                    w |= (uint32_t(round_half_away(qv)) & 0xffu) << (8 * k);
+                }
+                *reinterpret_cast<uint32_t*>(xq + row_off + 32 * n + 8 * j + 4 * lh) = w;
+            }
+        }
     }
 }
 
@@ -1071,8 +1101,10 @@ hipError_t launch_rope_kv(float* q, const float* k, const float* v, float* kc, f
 
 hipError_t launch_attention(const float* q, const float* kc, const float* vc, float* out, const uint32_t* pos0,
                             uint32_t T, uint32_t H, uint32_t KH, uint32_t D, uint32_t max_pos, float scale,
-                            hipStream_t stream) {
-    if (!q || !kc || !vc || !out || !pos0 || !T || !H || !KH || H % KH || D % 64 || D > 256 || !max_pos)
+                            hipStream_t stream, int8_t* xq, float* xs, bool* quantized) {
+    if (quantized) *quantized = false;
+    if (!q || !kc || !vc || !out || !pos0 || !T || !H || !KH || H % KH || D % 64 || D > 256 || !max_pos ||
+        (xq && (!xs || !quantized)))
         return hipErrorInvalidValue;
     const uint32_t G = H / KH;
     if (kFRows % G == 0 && (D == 64 || D == 128)) {
@@ -1080,10 +1112,11 @@ hipError_t launch_attention(const float* q, const float* kc, const float* vc, fl
         const dim3 grid(KH, (T + TQ - 1) / TQ);
         if (D == 64)
             hipLaunchKernelGGL(attention_prefill_t_kernel<64>, grid, dim3(kT), attention_prefill_t_lds(64), stream, q, kc,
-                               vc, out, pos0, T, H, KH, scale);
+                               vc, out, pos0, T, H, KH, scale, xq, xs);
         else
             hipLaunchKernelGGL(attention_prefill_t_kernel<128>, grid, dim3(kT), attention_prefill_t_lds(128), stream, q,
-                               kc, vc, out, pos0, T, H, KH, scale);
+                               kc, vc, out, pos0, T, H, KH, scale, xq, xs);
+        if (quantized) *quantized = xq != nullptr;
         return hipGetLastError();
     }
     const size_t lds = size_t(max_pos) * sizeof(float);

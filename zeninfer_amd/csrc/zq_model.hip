@@ -336,10 +336,13 @@ hipError_t enqueue_layers(zq_model& m, uint32_t T) {
             else
                 HIPCHK(zq::launch_rope_kv(m.q, m.k, m.v, L.kc, L.vc, m.cos_tab, m.sin_tab, m.pos_dev, T, c.heads,
                                           c.kv_heads, c.head_dim, m.pairs, true, m.stream));
+            // with int8 o inputs the attention kernel writes them itself when it can
+            const bool qo = qin({&L.o});
+            bool qz = false;
             HIPCHK(zq::launch_attention(m.q, L.kc, L.vc, m.att, m.pos_dev, T, c.heads, c.kv_heads, c.head_dim,
-                                        c.max_positions, m.attn_scale, m.stream));
-            bool qz;
-            HIPCHK(quantize_for(m, {&L.o}, m.att, T, QW, qz));
+                                        c.max_positions, m.attn_scale, m.stream, qo ? m.xq : nullptr,
+                                        qo ? m.xs : nullptr, &qz));
+            if (!qz) HIPCHK(quantize_for(m, {&L.o}, m.att, T, QW, qz));
             HIPCHK(project(m, L.o, m.att, m.tmp, T, qz, &o_splits));
         }
         // the o projection's split-K partials, if any, are summed by the norm
