@@ -91,6 +91,36 @@ int zq_model_generate(zq_model* model, const uint32_t* prompt, size_t n, uint32_
 #define ZQ_W_DOWN 8
 int zq_model_weight(const zq_model* model, uint32_t layer, int which, const void** dev, uint32_t* rows,
                     uint32_t* cols, int* fmt);
+/* Test hook (no counterpart in the reference, whose runtime keeps no device
+ * intermediates): record the inputs and outputs of one decoder layer's
+ * int8-activation prefill projections, so a checker can recompute them.
+ * While set (dev != NULL), each prefill clears the records, and every int8
+ * GEMM of decoder layer `layer` copies into dev, after its launch, the
+ * int8 activations [m][k], their fp32 block scales [m][k/32] and its
+ * output planes [splits][m][n] (split-K partial sums; the layer's readers
+ * add them in plane order).  A projection whose copies would pass cap is
+ * not recorded and zq_model_tap_records returns ZQ_ERR_TOO_LARGE.
+ * dev == NULL turns the hook off.  Prefill only; decode is never recorded. */
+#define ZQ_TAP_QKV 0  /* the packed q|k|v weight (n = q + k + v rows) */
+#define ZQ_TAP_Q 1
+#define ZQ_TAP_K 2
+#define ZQ_TAP_V 3
+#define ZQ_TAP_O 4
+#define ZQ_TAP_GATE 5
+#define ZQ_TAP_UP 6
+#define ZQ_TAP_DOWN 7
+typedef struct zq_model_tap_record {
+    int proj;           /* ZQ_TAP_* */
+    int fmt;            /* GGML type of the weight */
+    const void* w;      /* device address of its rows */
+    uint32_t m, n, k;   /* tokens, weight rows, columns */
+    uint32_t splits;    /* output planes */
+    uint64_t xq_off, xs_off, y_off; /* byte offsets into dev */
+} zq_model_tap_record;
+int zq_model_set_tap(zq_model* model, uint32_t layer, void* dev, size_t cap);
+/* The records of the last prefill (at most cap of them; *n = how many). */
+int zq_model_tap_records(const zq_model* model, zq_model_tap_record* out, size_t cap, size_t* n);
+
 /* Device bytes held: weights, KV cache, activations. */
 int zq_model_memory(zq_model* model, uint64_t* weight_bytes, uint64_t* cache_bytes, uint64_t* activation_bytes);
 

@@ -63,6 +63,8 @@ class Oracle:
         L.zqo_gemm_f32.argtypes = [ctypes.c_int, _P, _P, _P, _S, _S, _S]
         L.zqo_gemm_i8.restype = ctypes.c_int
         L.zqo_gemm_i8.argtypes = [ctypes.c_int, _P, _P, _P, _S, _S, _S]
+        L.zqo_gemm_i8_prequant.restype = ctypes.c_int
+        L.zqo_gemm_i8_prequant.argtypes = [ctypes.c_int, _P, _P, _P, _P, _S, _S, _S]
         L.zqo_gemm_f64.restype = ctypes.c_int
         L.zqo_gemm_f64.argtypes = [ctypes.c_int, _P, _P, _P, _P, _S, _S, _S]
         self.L = L
@@ -140,6 +142,16 @@ class Oracle:
         X = np.ascontiguousarray(X, dtype=np.float32)
         if not self.L.zqo_gemm_i8(fmt, _ptr(w), _ptr(X), _ptr(Y), m, n, k):
             raise ValueError("gemm_i8 declined")
+        return Y
+
+    def gemm_i8_prequant(self, fmt, w, xq, xs, m, n, k):
+        """gemm_i8 on activations already quantised (int8 [m][k], scales [m][k/32])."""
+        Y = np.empty(m * n, np.float32)
+        xq = np.ascontiguousarray(xq, dtype=np.int8)
+        xs = np.ascontiguousarray(xs, dtype=np.float32)
+        assert xq.size == m * k and xs.size == m * (k // 32)
+        if not self.L.zqo_gemm_i8_prequant(fmt, _ptr(w), _ptr(xq), _ptr(xs), _ptr(Y), m, n, k):
+            raise ValueError("gemm_i8_prequant declined")
         return Y
 
     def gemm_f64(self, fmt, w, X, m, n, k):

@@ -596,17 +596,16 @@ int zqo_gemm_f32(int fmt, const uint8_t* w, const float* X, float* Y, size_t m, 
  * then hsum_ps256.  Q4_0 / Q6_K have no int8 route in the reference; here
  * acc = fma(d_w*d_x, float(block_dot), acc) per block, with block_dot from
  * zqo_block_dots (Q6_K: d_w is the super-block d; the int8 sub-scales are
- * inside the integer dot). */
-int zqo_gemm_i8(int fmt, const uint8_t* w, const float* X, float* Y, size_t m, size_t n, size_t k) {
+ * inside the integer dot).  xq / xs are already-quantised activations
+ * (zqo_quantize_acts's layout: int8 [m][k], fp32 [m][k/32]). */
+int zqo_gemm_i8_prequant(int fmt, const uint8_t* w, const int8_t* xq, const float* xs, float* Y, size_t m, size_t n,
+                         size_t k) {
     size_t rb = zqo_row_bytes(fmt, k); if (!rb || k % 32 || fmt == ZQO_Q4_K || fmt == ZQO_Q5_K) return 0;
     size_t nb = k / 32;
-    int8_t* xq = (int8_t*)malloc(m * k); float* xs = (float*)malloc(sizeof(float) * m * nb);
     int32_t* dots = NULL;
-    if (!xq || !xs) { free(xq); free(xs); return 0; }
-    zqo_quantize_acts(X, m, k, xq, xs);
     if (fmt != ZQO_Q8_0) {
         dots = (int32_t*)malloc(sizeof(int32_t) * m * n * nb);
-        if (!dots || !zqo_block_dots(fmt, w, xq, m, n, k, dots)) { free(xq); free(xs); free(dots); return 0; }
+        if (!dots || !zqo_block_dots(fmt, w, xq, m, n, k, dots)) { free(dots); return 0; }
     }
     for (size_t t = 0; t < m; ++t)
         for (size_t r = 0; r < n; ++r) {
@@ -635,6 +634,17 @@ int zqo_gemm_i8(int fmt, const uint8_t* w, const float* X, float* Y, size_t m, s
                 Y[t * n + r] = acc;
             }
         }
-    free(xq); free(xs); free(dots);
+    free(dots);
     return 1;
+}
+
+/* The same from fp32 activations: zqo_quantize_acts, then the above. */
+int zqo_gemm_i8(int fmt, const uint8_t* w, const float* X, float* Y, size_t m, size_t n, size_t k) {
+    size_t rb = zqo_row_bytes(fmt, k); if (!rb || k % 32 || fmt == ZQO_Q4_K || fmt == ZQO_Q5_K) return 0;
+    int8_t* xq = (int8_t*)malloc(m * k); float* xs = (float*)malloc(sizeof(float) * m * (k / 32));
+    if (!xq || !xs) { free(xq); free(xs); return 0; }
+    zqo_quantize_acts(X, m, k, xq, xs);
+    int ok = zqo_gemm_i8_prequant(fmt, w, xq, xs, Y, m, n, k);
+    free(xq); free(xs);
+    return ok;
 }

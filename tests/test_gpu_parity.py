@@ -168,20 +168,25 @@ def test_gemv_batch_qkv(zq, orc):
     assert zq.stats()["batches"] == before + 1
 
 
-def test_gemv_full_size_sampled_rows(zq, orc):
-    # config 1 gate/up (14336 x 4096) and down (4096 x 14336) at full size,
-    # weights generated on the device; sampled rows checked against the oracle
+@pytest.mark.parametrize("fmt", [O.Q8_0, O.Q4_0, O.Q6_K])
+def test_gemv_full_size_sampled_rows(zq, orc, fmt):
+    # config 1 gate/up (14336 x 4096) and down (4096 x 14336) at full size for
+    # Q8_0, and the config-3 Q4_0 / Q6_K GEMVs at the same full row counts;
+    # weights generated on the device, sampled rows (with the first and last)
+    # checked against the oracle
     for rows, cols, seed in ((14336, 4096, 71), (4096, 14336, 72)):
-        wd = torch.zeros(zq.weight_bytes(O.Q8_0, rows, cols), dtype=torch.uint8, device=DEV)
-        zq.synth_weights_dev(O.Q8_0, seed, wd, rows, cols)
+        wd = torch.zeros(zq.weight_bytes(fmt, rows, cols), dtype=torch.uint8, device=DEV)
+        zq.synth_weights_dev(fmt, seed, wd, rows, cols)
         x = orc.gen_normal(seed, cols)
         y = torch.empty(rows, device=DEV)
-        zq.gemv_dev(O.Q8_0, wd, to_dev(x), y, rows, cols)
-        w_all = wd[: rows * zq.row_bytes(O.Q8_0, cols)].cpu().numpy()
-        rb = zq.row_bytes(O.Q8_0, cols)
-        pick = np.sort(np.random.default_rng(seed).choice(rows, 48, replace=False))
+        zq.gemv_dev(fmt, wd, to_dev(x), y, rows, cols)
+        rb = zq.row_bytes(fmt, cols)
+        w_all = wd[: rows * rb].cpu().numpy()
+        pick = np.unique(np.concatenate([np.random.default_rng(seed).choice(rows, 64, replace=False), [0, rows - 1]]))
         sub = np.concatenate([w_all[r * rb:(r + 1) * rb] for r in pick])
-        assert_close(y.cpu().numpy()[pick], orc.gemv_f32(O.Q8_0, sub, x, len(pick), cols), "full-size gemv")
+        yh = y.cpu().numpy()
+        assert np.all(np.isfinite(yh))
+        assert_close(yh[pick], orc.gemv_f32(fmt, sub, x, len(pick), cols), f"full-size gemv fmt={fmt} {rows}x{cols}")
 
 
 def test_device_synth_matches_host_generator(zq, orc):
@@ -263,9 +268,12 @@ def test_superblock_gemm_mixed_scales(zq, orc, fmt):
 # The BASELINE configs' own GEMM workloads at full size: config 2 (Q8_0, int8
 # activations, M = 32 / 128 / 512 / 2048 on both FFN shapes) and config 3
 # (Q4_0 int8 and Q6_K fp32 at M = 512), plus the Q4_K / Q5_K fp32 path at
-# M = 512.  Rows and tokens are independent, so
+# M = 512.  Every M of the sweep runs on both shapes (M = 32 takes the skinny
+# kernel, 448 row tiles at 14336 rows; M = 2048 at K = 14336 the 128-token
+# tile over 448 K blocks).  Rows and tokens are independent, so
 # sampled (token, row) outputs are checked against the oracle.
-_FULL_GEMM = [(O.Q8_0, 1, 2048, 14336, 4096), (O.Q8_0, 1, 32, 4096, 14336),
+_FULL_GEMM = [(O.Q8_0, 1, 2048, 14336, 4096), (O.Q8_0, 1, 2048, 4096, 14336),
+              (O.Q8_0, 1, 32, 14336, 4096), (O.Q8_0, 1, 32, 4096, 14336),
               (O.Q8_0, 1, 128, 14336, 4096), (O.Q8_0, 1, 128, 4096, 14336),
               (O.Q8_0, 1, 512, 14336, 4096), (O.Q8_0, 1, 512, 4096, 14336),
               (O.Q4_0, 1, 512, 14336, 4096), (O.Q4_0, 1, 512, 4096, 14336),

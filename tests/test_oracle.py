@@ -372,6 +372,17 @@ def test_int8_gemm_against_double_of_quantised(orc):
     assert_close(orc.gemm_i8(fmt, w, X, m, rows, cols), want, "gemm_i8 vs double")
 
 
+@pytest.mark.parametrize("fmt", [O.Q8_0, O.Q4_0, O.Q6_K])
+def test_int8_gemm_prequant_is_the_int8_gemm_after_quantisation(orc, fmt):
+    # gemm_i8 = quantize_acts then gemm_i8_prequant; the Q8_0 gemm_i8 is pinned
+    # bit-exact to the reference's int8 route by the golden vectors above
+    rows, cols, m = 9, 2048, 4
+    w = orc.gen_weights(fmt, 43, rows, cols)
+    X = orc.gen_normal(44, m * cols)
+    xq, xs = orc.quantize_acts(X, m, cols)
+    assert np.array_equal(orc.gemm_i8_prequant(fmt, w, xq, xs, m, rows, cols), orc.gemm_i8(fmt, w, X, m, rows, cols))
+
+
 def test_generators_are_counter_based(orc):
     # draw i of a stream is the (i+1)-th output of sequential SplitMix64
     state, seq = 12345, []

@@ -97,6 +97,13 @@ struct zq_model {
     hipGraphExec_t decode_exec = nullptr;
     hipGraph_t decode_graph = nullptr;
 
+    // zq_model_set_tap: one layer's int8 prefill projections copied to tap_dev
+    uint32_t tap_layer = 0;
+    uint8_t* tap_dev = nullptr;
+    size_t tap_cap = 0, tap_used = 0;
+    bool tap_overflow = false;
+    std::vector<zq_model_tap_record> tap_recs;
+
     ~zq_model() {
         if (stream) (void)hipStreamSynchronize(stream);
         if (decode_exec) (void)hipGraphExecDestroy(decode_exec);
@@ -274,6 +281,27 @@ hipError_t quantize_for(zq_model& m, std::initializer_list<const Weight*> ws, co
         if (e_ != hipSuccess) return e_;       \
     } while (0)
 
+// zq_model_set_tap: after an int8 projection of the tapped layer, copy its
+// activations, scales and output planes (m.partial when split) to the tap
+// buffer, in stream order.
+hipError_t tap(zq_model& m, uint32_t layer, int proj, const Weight& w, uint32_t M, bool quantized, const float* Y,
+               uint32_t splits) {
+    if (!m.tap_dev || layer != m.tap_layer || !quantized) return hipSuccess;
+    const size_t xq = size_t(M) * w.cols, xs = size_t(M) * (w.cols / 32) * 4;
+    const size_t y = size_t(splits) * M * w.rows * 4;
+    const size_t o0 = align_up(m.tap_used, kAlign), o1 = align_up(o0 + xq, kAlign), o2 = align_up(o1 + xs, kAlign);
+    if (o2 + y > m.tap_cap) {
+        m.tap_overflow = true;
+        return hipSuccess;
+    }
+    HIPCHK(hipMemcpyAsync(m.tap_dev + o0, m.xq, xq, hipMemcpyDeviceToDevice, m.stream));
+    HIPCHK(hipMemcpyAsync(m.tap_dev + o1, m.xs, xs, hipMemcpyDeviceToDevice, m.stream));
+    HIPCHK(hipMemcpyAsync(m.tap_dev + o2, splits > 1 ? m.partial : Y, y, hipMemcpyDeviceToDevice, m.stream));
+    m.tap_used = o2 + y;
+    m.tap_recs.push_back(zq_model_tap_record{proj, w.fmt, w.p, M, w.rows, w.cols, splits, o0, o1, o2});
+    return hipSuccess;
+}
+
 // Decoder layers over T tokens at positions pos0 .. pos0+T-1 (pos0 in device
 // memory).  On entry x holds the embeddings; on exit x is the residual stream
 // and h = rmsnorm(x) * output_norm, every residual add fused into the norm
@@ -313,10 +341,14 @@ hipError_t enqueue_layers(zq_model& m, uint32_t T) {
             Weight qkv;
             if (qkv_packed(L, qkv)) {
                 HIPCHK(project(m, qkv, m.h, m.qkv, T, qz, &qkv_splits));
+                HIPCHK(tap(m, l, ZQ_TAP_QKV, qkv, T, qz, m.qkv, qkv_splits));
             } else {
                 HIPCHK(project(m, L.q, m.h, m.q, T, qz));
+                HIPCHK(tap(m, l, ZQ_TAP_Q, L.q, T, qz, m.q, 1));
                 HIPCHK(project(m, L.k, m.h, m.k, T, qz));
+                HIPCHK(tap(m, l, ZQ_TAP_K, L.k, T, qz, m.k, 1));
                 HIPCHK(project(m, L.v, m.h, m.v, T, qz));
+                HIPCHK(tap(m, l, ZQ_TAP_V, L.v, T, qz, m.v, 1));
             }
         }
         if (T == 1) {
@@ -344,6 +376,7 @@ hipError_t enqueue_layers(zq_model& m, uint32_t T) {
                                         qo ? m.xs : nullptr, &qz));
             if (!qz) HIPCHK(quantize_for(m, {&L.o}, m.att, T, QW, qz));
             HIPCHK(project(m, L.o, m.att, m.tmp, T, qz, &o_splits));
+            HIPCHK(tap(m, l, ZQ_TAP_O, L.o, T, qz, m.tmp, o_splits));
         }
         // the o projection's split-K partials, if any, are summed by the norm
         const bool qgu = qin({&L.gate, &L.up});
@@ -361,7 +394,9 @@ hipError_t enqueue_layers(zq_model& m, uint32_t T) {
             bool qz = qgu;
             if (!qz) HIPCHK(quantize_for(m, {&L.gate, &L.up}, m.h, T, E, qz));
             HIPCHK(project(m, L.gate, m.h, m.gate, T, qz));
+            HIPCHK(tap(m, l, ZQ_TAP_GATE, L.gate, T, qz, m.gate, 1));
             HIPCHK(project(m, L.up, m.h, m.up, T, qz));
+            HIPCHK(tap(m, l, ZQ_TAP_UP, L.up, T, qz, m.up, 1));
         }
         const bool qd = qin({&L.down});
         HIPCHK(zq::launch_silu_mul(m.gate, m.up, qd ? nullptr : m.act, size_t(T) * F, m.stream,
@@ -373,6 +408,7 @@ hipError_t enqueue_layers(zq_model& m, uint32_t T) {
             bool qz = qd;
             if (!qz) HIPCHK(quantize_for(m, {&L.down}, m.act, T, F, qz));
             HIPCHK(project(m, L.down, m.act, m.tmp, T, qz, &d_splits));
+            HIPCHK(tap(m, l, ZQ_TAP_DOWN, L.down, T, qz, m.tmp, d_splits));
         }
         const float* next_norm = l + 1 < c.layers ? m.layers[l + 1].attn_norm : m.out_norm;
         const bool qn = l + 1 < c.layers && qin({&m.layers[l + 1].q, &m.layers[l + 1].k, &m.layers[l + 1].v});
@@ -465,6 +501,9 @@ int prefill(zq_model& m, const uint32_t* tokens, size_t n, float* logits, uint32
     for (size_t i = 0; i < n; ++i)
         if (tokens[i] >= m.cfg.vocab) return ZQ_ERR_ARG;
     m.cur_pos = 0;
+    m.tap_used = 0;
+    m.tap_overflow = false;
+    m.tap_recs.clear();
     for (size_t s = 0; s < n; s += kPrefillChunk) {
         const uint32_t T = uint32_t(std::min<size_t>(kPrefillChunk, n - s));
         m.host_small[0] = uint32_t(s);
@@ -762,6 +801,25 @@ int zq_model_generate(zq_model* m, const uint32_t* prompt, size_t n, uint32_t ma
     if (prefill_ms) *prefill_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
     if (decode_ms) *decode_ms = std::chrono::duration<double, std::milli>(t2 - t1).count();
     return ZQ_OK;
+}
+
+int zq_model_set_tap(zq_model* m, uint32_t layer, void* dev, size_t cap) {
+    if (!m || (dev && layer >= m->layers.size())) return ZQ_ERR_ARG;
+    m->tap_layer = layer;
+    m->tap_dev = static_cast<uint8_t*>(dev);
+    m->tap_cap = dev ? cap : 0;
+    m->tap_used = 0;
+    m->tap_overflow = false;
+    m->tap_recs.clear();
+    return ZQ_OK;
+}
+
+int zq_model_tap_records(const zq_model* m, zq_model_tap_record* out, size_t cap, size_t* n) {
+    if (!m || !n || (cap && !out)) return ZQ_ERR_ARG;
+    const size_t c = std::min(cap, m->tap_recs.size());
+    std::copy(m->tap_recs.begin(), m->tap_recs.begin() + c, out);
+    *n = c;
+    return m->tap_overflow ? ZQ_ERR_TOO_LARGE : ZQ_OK;
 }
 
 int zq_model_memory(zq_model* m, uint64_t* weight_bytes, uint64_t* cache_bytes, uint64_t* activation_bytes) {

@@ -15,6 +15,7 @@ from . import zq
 PREFILL_INT8, PREFILL_F32 = 0, 1
 GLOBAL = 0xFFFFFFFF
 W_EMBED, W_OUTPUT, W_Q, W_K, W_V, W_O, W_GATE, W_UP, W_DOWN = range(9)
+TAP_QKV, TAP_Q, TAP_K, TAP_V, TAP_O, TAP_GATE, TAP_UP, TAP_DOWN = range(8)
 
 
 class ModelError(RuntimeError):
@@ -97,6 +98,19 @@ class Model:
         zq.check(self._L.zq_model_weight(self._h, layer, which, ctypes.byref(p), ctypes.byref(r), ctypes.byref(c),
                                          ctypes.byref(f)), "weight")
         return p.value, r.value, c.value, f.value
+
+    def set_tap(self, layer, dev_ptr, cap):
+        """Record one layer's int8 prefill projections into a device buffer
+        (zq_model_set_tap); dev_ptr 0 turns it off."""
+        zq.check(self._L.zq_model_set_tap(self._h, layer, dev_ptr or None, cap), "set_tap")
+
+    def tap_records(self):
+        """The last prefill's tap records (zq_model_tap_records); raises
+        ZQError(TOO_LARGE) when the buffer could not hold every projection."""
+        recs = (zq.TapRecord * 16)()
+        n = ctypes.c_size_t()
+        zq.check(self._L.zq_model_tap_records(self._h, recs, 16, ctypes.byref(n)), "tap_records")
+        return [recs[i] for i in range(n.value)]
 
     def memory(self):
         w, c, a = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_uint64()

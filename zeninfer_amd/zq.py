@@ -148,6 +148,13 @@ class ModelConfig(ctypes.Structure):
         ("weight_format", ctypes.c_int)]
 
 
+class TapRecord(ctypes.Structure):
+    """zq_model_tap_record (include/zq_model.h)."""
+    _fields_ = [("proj", ctypes.c_int), ("fmt", ctypes.c_int), ("w", ctypes.c_void_p), ("m", ctypes.c_uint32),
+                ("n", ctypes.c_uint32), ("k", ctypes.c_uint32), ("splits", ctypes.c_uint32),
+                ("xq_off", ctypes.c_uint64), ("xs_off", ctypes.c_uint64), ("y_off", ctypes.c_uint64)]
+
+
 # Every symbol include/zq_model.h declares.
 MODEL_SIGNATURES = {
     "zq_model_load_gguf": (ctypes.c_int, [_P, ctypes.c_uint32, ctypes.POINTER(ModelConfig), ctypes.POINTER(_P),
@@ -165,6 +172,8 @@ MODEL_SIGNATURES = {
                                          ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]),
     "zq_model_memory": (ctypes.c_int, [_P, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64),
                                        ctypes.POINTER(ctypes.c_uint64)]),
+    "zq_model_set_tap": (ctypes.c_int, [_P, ctypes.c_uint32, _P, _S]),
+    "zq_model_tap_records": (ctypes.c_int, [_P, ctypes.POINTER(TapRecord), _S, ctypes.POINTER(_S)]),
 }
 
 _lib = None
