@@ -237,65 +237,6 @@ size_t zq_hip_noalloc_scratch_bytes(void);
 int zq_hip_gemm_dev_noalloc(int fmt, const void* weights, const float* X, float* Y, size_t tokens, size_t rows,
                             size_t cols, int act_mode, void* stream);
 
-/* ---- chained decode projections (device pointers) ----------------------- */
-/* A decode step's projections as ONE persistent launch: each stage is a
- * gemv_batch (up to ZQ_MAX_BATCH device weights sharing x and cols) whose x
- * is a plain vector or is computed while it is staged:
- *   ZQ_X_PLAIN     x = a
- *   ZQ_X_ADD_NORM  v = a + b (b may be NULL), x = rmsnorm(v) * w with the
- *                  arithmetic of zq_hip_rms_norm; r_out (may be NULL, must
- *                  not alias a or b) receives v
- * and whose outputs are each task's rows (ZQ_Y_STORE) or, for exactly two
- * tasks of equal rows (gate, up), f = silu(gate.x) * (up.x) into the first
- * task's y (ZQ_Y_SILU_PAIR; the second task's y is unused and may be NULL).
- * A stage with wait = j >= 0 reads its x only after stage j (< its own index)
- * has completed, so x may be the output of an earlier stage in the same
- * launch; wait = -1 means x exists before the launch.  Each workgroup keeps
- * the weight loads of its next row blocks (of this or later stages) in
- * flight while it waits, so the HBM stream does not drain between
- * projections.  Plain stages equal zq_hip_gemv_batch_dev bit for bit.
- * Q8_0 / Q4_0, cols % 256 == 0, cols <= 14336 (4608 with ZQ_X_ADD_NORM), at
- * most 64 row blocks of 8 rows per CU per stage (about 131000 rows at
- * cols <= 4096), 16-byte aligned weights and vectors; other stages are
- * ZQ_DECLINED at create time (ZQ_X_SILU_MUL included: use ZQ_Y_SILU_PAIR on
- * the producing stage).
- * The reference's one-submission decode is the D3D12 layer_decode_pipeline
- * (include/zen/d3d12_backend.h:316-327); the HIP slot has none. */
-#define ZQ_X_PLAIN 0
-#define ZQ_X_SILU_MUL 1
-#define ZQ_X_ADD_NORM 2
-#define ZQ_Y_STORE 0
-#define ZQ_Y_SILU_PAIR 1
-typedef struct zq_chain_stage {
-    const zq_gemv_task* tasks; /* device weights and outputs */
-    size_t count;
-    size_t cols;
-    int kind;
-    const float* a;
-    const float* b;
-    const float* w;
-    float* r_out;
-    float eps;
-    int wait;
-    int epilogue;
-} zq_chain_stage;
-typedef struct zq_chain zq_chain;
-/* Validates and uploads the program (allocates its device memory). */
-int zq_hip_chain_create(int fmt, const zq_chain_stage* stages, size_t count, zq_chain** out);
-/* Enqueues one launch of the whole program on `stream`; allocates nothing
- * and records no memset, so it may be captured in a HIP graph. */
-int zq_hip_chain_launch(zq_chain* chain, void* stream);
-/* Synchronises the chain's last stream and reports whether a launch gave up
- * a bounded wait (*timed_out = 1: outputs invalid; call zq_hip_chain_reset). */
-int zq_hip_chain_check(zq_chain* chain, int* timed_out);
-/* Bound of each wait, in polls (default 1048576, about a second): past it the launch
- * gives up (zq_hip_chain_check reports it).  Tests use a tiny bound to force
- * that path from the host. */
-int zq_hip_chain_set_spin_limit(zq_chain* chain, uint32_t polls);
-/* Clears the chain's counters and status with a kernel on `stream`. */
-int zq_hip_chain_reset(zq_chain* chain, void* stream);
-void zq_hip_chain_destroy(zq_chain* chain);
-
 /* ---- bit-exact tier hooks (device pointers, asynchronous) ---------------- */
 /* Per-32 activation quantiser, kernels/avx2.cpp:502-524: xq[tokens*cols],
  * xs[tokens*cols/32]. */

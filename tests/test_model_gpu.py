@@ -230,17 +230,24 @@ def test_fused_decode_equals_unfused(tiny_path, zq):
         assert np.abs(la - lb).max() <= 1e-5 * np.abs(lb).max() + 1e-6
 
 
-@pytest.mark.parametrize("ptype", [G.GGML_Q8_0, G.GGML_Q4_0])
-def test_fused_prefill_quantiser_equals_unfused(tmp_path, zq, ptype):
+@pytest.mark.parametrize("ptype,rope_dim", [(G.GGML_Q8_0, 0), (G.GGML_Q4_0, 0), (G.GGML_Q8_0, 62)])
+def test_fused_prefill_quantiser_equals_unfused(tmp_path, zq, ptype, rope_dim):
     """Int8 prefill with the activations quantised inside the RMSNorm and
-    SiLU*up kernels against the separate quantiser launches
-    (ZQ_MODEL_FUSED=0): the same per-block arithmetic on the same fp32
-    values, so the prefill logits are bit-identical, for a 16-token and a
-    150-token prompt."""
+    SiLU*up kernels, and the GEMMs' split-K partial sums left to their readers
+    (the RoPE + KV-append kernel and the add+RMSNorms sum the planes), against
+    ZQ_MODEL_FUSED=0: separate quantiser launches and the GEMMs' own split-K
+    reduction.  The same per-block arithmetic on the same fp32 values, and the
+    planes summed in the same order, so the prefill logits are bit-identical,
+    for a 16-token and a 150-token prompt.  rope_dim 62 (31 rotary pairs, odd)
+    takes the scalar RoPE kernel, which reduces the q|k|v planes itself before
+    rotating; the tap records show that the split-K paths were taken."""
     from zeninfer_amd.model import PREFILL_INT8
-    path = tmp_path / f"fq_{ptype}.gguf"
-    G.synthetic_llama(path, SHAPE, seed=23, proj_type=ptype)
-    long_prompt = [int(t) for t in np.random.default_rng(5).integers(0, SHAPE.vocab, 150)]
+    import torch
+    shape = SHAPE if not rope_dim else G.LlamaShape(embedding=512, layers=2, heads=4, kv_heads=2, ffn=512, vocab=512,
+                                                    context=2048, rope_dim=rope_dim)
+    path = tmp_path / f"fq_{ptype}_{rope_dim}.gguf"
+    G.synthetic_llama(path, shape, seed=23, proj_type=ptype)
+    long_prompt = [int(t) for t in np.random.default_rng(5).integers(0, shape.vocab, 150)]
     outs = []
     for fused in ("1", "0"):
         os.environ["ZQ_MODEL_FUSED"] = fused
@@ -248,15 +255,21 @@ def test_fused_prefill_quantiser_equals_unfused(tmp_path, zq, ptype):
             m = load(path, PREFILL_INT8, max_positions=256)
         finally:
             os.environ.pop("ZQ_MODEL_FUSED", None)
+        buf = torch.empty(64 << 20, dtype=torch.uint8, device="cuda:0")
+        m.set_tap(0, buf.data_ptr(), buf.numel())
         res = []
         for prompt in (PROMPT, long_prompt):
             nxt, lg = m.prefill(prompt)
-            res.append((nxt, lg.copy()))
+            splits = {r.proj: r.splits for r in m.tap_records()}
+            res.append((nxt, lg.copy(), splits))
+        m.set_tap(0, 0, 0)
         outs.append(res)
         m.close()
-    for (ta, la), (tb, lb) in zip(*outs):
+    for (ta, la, sa), (tb, lb, sb) in zip(*outs):
         assert ta == tb
         assert np.array_equal(la, lb)
+        assert all(v == 1 for v in sb.values()), sb  # unfused: the GEMMs reduced their planes
+    assert any(v > 1 for v in outs[0][1][2].values()), outs[0][1][2]  # fused: some reader summed planes
 
 
 @pytest.mark.parametrize("rope_dim", [64, 32])

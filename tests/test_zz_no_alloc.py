@@ -49,6 +49,13 @@ def test_noalloc_matches_workspace_entry_point(zq, orc, fmt, act, big, small):
 def test_noalloc_refuses_beyond_scratch(zq):
     m, n, k = 8192, 4096, 14336  # 117 MB of int8 activations + scales
     assert zq.gemm_workspace_bytes(O.Q8_0, m, n, k, zq.ACT_INT8) > zq.noalloc_scratch_bytes()
-    st = zq.lib().zq_hip_gemm_dev_noalloc(O.Q8_0, 1 << 20, 2 << 20, 3 << 20, m, n, k, zq.ACT_INT8, None)
+    # real operands of the full sizes (zeros), so a regression of the size
+    # check would run a valid GEMM rather than touch unmapped memory
+    w = torch.zeros(zq.weight_bytes(O.Q8_0, n, k), dtype=torch.uint8, device=DEV)
+    X = torch.zeros(m * k, device=DEV)
+    Y = torch.full((m * n,), float("nan"), device=DEV)
+    st = zq.lib().zq_hip_gemm_dev_noalloc(O.Q8_0, w.data_ptr(), X.data_ptr(), Y.data_ptr(), m, n, k, zq.ACT_INT8, None)
+    torch.cuda.synchronize()
     assert st == zq.ERR_TOO_LARGE
     assert "scratch" in zq.status_string(st)
+    assert torch.isnan(Y).all(), "a refused call wrote its output"

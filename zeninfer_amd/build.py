@@ -13,7 +13,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 SRC = os.path.join(HERE, "csrc")
 LIB_DIR = os.path.join(HERE, "lib")
 LIB = os.path.join(LIB_DIR, "libzq_hip.so")
-SOURCES = ["zq_backend.hip", "zq_gemv.hip", "zq_gemm.hip", "zq_misc.hip", "zq_gguf.cpp", "zq_layer.hip", "zq_model.hip", "zq_chain.hip"]
+SOURCES = ["zq_backend.hip", "zq_gemv.hip", "zq_gemm.hip", "zq_misc.hip", "zq_gguf.cpp", "zq_layer.hip", "zq_model.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 FLAGS = [

@@ -1076,110 +1076,4 @@ int zq_hip_synth_normal_dev(uint64_t seed, float* out, size_t n, void* stream) {
     return zq::launch_synth_normal(seed, out, n, static_cast<hipStream_t>(stream)) == hipSuccess ? ZQ_OK : ZQ_ERR_HIP;
 }
 
-// ------------------------------------------------------------------ chain --
-}  // extern "C"
-
-struct zq_chain {
-    int fmt = 0;
-    uint32_t nstages = 0;
-    zq::ChainStage* prog = nullptr;  // device
-    uint32_t* counters = nullptr;    // device: nstages counters, then the status word
-    hipStream_t last = nullptr;
-    uint32_t spin_limit = 1u << 20;  // polls (an agent-scope load + s_sleep each): ~1 s
-};
-
-extern "C" {
-
-int zq_hip_chain_create(int fmt, const zq_chain_stage* stages, size_t count, zq_chain** out) {
-    if (!stages || !count || count > (1u << 20) || !out) return ZQ_ERR_ARG;
-    *out = nullptr;
-    if (fmt != ZQ_FMT_Q8_0 && fmt != ZQ_FMT_Q4_0) return ZQ_DECLINED;
-    if (!zq::chain_grid(fmt)) return ZQ_DECLINED;
-    try {
-        std::vector<zq::ChainStage> prog(count);
-        for (size_t i = 0; i < count; ++i) {
-            const zq_chain_stage& in = stages[i];
-            if (!in.tasks || in.count < 1 || in.count > ZQ_MAX_BATCH || in.cols > (1u << 24)) return ZQ_ERR_ARG;
-            zq::ChainStage& st = prog[i];
-            st = zq::ChainStage{};
-            st.count = int32_t(in.count);
-            for (size_t k = 0; k < in.count; ++k) {
-                if (in.tasks[k].rows > (1u << 30)) return ZQ_ERR_ARG;
-                st.t[k] = zq::GemvTask{in.tasks[k].weights, in.tasks[k].y, uint32_t(in.tasks[k].rows)};
-            }
-            st.cols = uint32_t(in.cols);
-            st.kind = in.kind;
-            st.a = in.a;
-            st.b = in.b;
-            st.w = in.w;
-            st.r_out = in.r_out;
-            st.eps = in.eps;
-            st.wait = in.wait;
-            st.epi = in.epilogue;
-            const hipError_t e = zq::chain_stage_prepare(fmt, st, uint32_t(i));
-            if (e == hipErrorInvalidConfiguration) return ZQ_DECLINED;
-            if (e != hipSuccess) return ZQ_ERR_ARG;
-        }
-        auto* c = new zq_chain;
-        c->fmt = fmt;
-        c->nstages = uint32_t(count);
-        if (hipMalloc(&c->prog, count * sizeof(zq::ChainStage)) != hipSuccess ||
-            hipMalloc(&c->counters, (count + 1) * sizeof(uint32_t)) != hipSuccess) {
-            zq_hip_chain_destroy(c);
-            return ZQ_ERR_OOM;
-        }
-        if (hipMemcpy(c->prog, prog.data(), count * sizeof(zq::ChainStage), hipMemcpyHostToDevice) != hipSuccess ||
-            hipMemset(c->counters, 0, (count + 1) * sizeof(uint32_t)) != hipSuccess ||
-            hipDeviceSynchronize() != hipSuccess) {
-            zq_hip_chain_destroy(c);
-            return ZQ_ERR_HIP;
-        }
-        *out = c;
-        return ZQ_OK;
-    } catch (const std::bad_alloc&) {
-        return ZQ_ERR_OOM;
-    }
-}
-
-int zq_hip_chain_launch(zq_chain* c, void* stream) {
-    if (!c) return ZQ_ERR_ARG;
-    c->last = static_cast<hipStream_t>(stream);
-    return zq::launch_gemv_chain(c->fmt, c->prog, c->nstages, c->counters, c->counters + c->nstages, c->spin_limit,
-                                 c->last) == hipSuccess
-               ? ZQ_OK
-               : ZQ_ERR_HIP;
-}
-
-int zq_hip_chain_check(zq_chain* c, int* timed_out) {
-    if (!c || !timed_out) return ZQ_ERR_ARG;
-    uint32_t st = 0;
-    if (hipStreamSynchronize(c->last) != hipSuccess ||
-        hipMemcpy(&st, c->counters + c->nstages, sizeof st, hipMemcpyDeviceToHost) != hipSuccess)
-        return ZQ_ERR_HIP;
-    *timed_out = st != 0 ? 1 : 0;
-    return ZQ_OK;
-}
-
-int zq_hip_chain_set_spin_limit(zq_chain* c, uint32_t polls) {
-    if (!c) return ZQ_ERR_ARG;
-    c->spin_limit = polls;
-    return ZQ_OK;
-}
-
-int zq_hip_chain_reset(zq_chain* c, void* stream) {
-    if (!c) return ZQ_ERR_ARG;
-    return zq::launch_chain_reset(c->counters, c->nstages, c->counters + c->nstages, static_cast<hipStream_t>(stream)) ==
-                   hipSuccess
-               ? ZQ_OK
-               : ZQ_ERR_HIP;
-}
-
-void zq_hip_chain_destroy(zq_chain* c) {
-    if (!c) return;
-    if (c->prog || c->counters) (void)hipDeviceSynchronize();
-    if (c->prog) (void)hipFree(c->prog);
-    if (c->counters) (void)hipFree(c->counters);
-    delete c;
-}
-
 }  // extern "C"

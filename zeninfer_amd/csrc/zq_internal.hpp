@@ -46,50 +46,6 @@ constexpr int kXPlain = 0, kSiluMul = 1, kAddNorm = 2;
 hipError_t launch_gemv_prologue(int fmt, const GemvTask* tasks, int count, const XPrologue& pro, size_t cols,
                                 hipStream_t stream);
 
-// One stage of a chained decode GEMV (zq_chain.hip): a gemv_batch whose x
-// is a plain vector (kind kXPlain: x = a) or the add+RMSNorm of a, b with
-// weight w (kind kAddNorm, as XPrologue); `wait` is an earlier stage that
-// must complete before x is read (-1: x exists before the launch).  With
-// epi == kEpiSiluPair the stage holds exactly two projections of equal rows
-// (gate, up) and stores f = silu(gate.x) * (up.x) into t[0].y (the SiLU*up of
-// silu_mul_kernel); otherwise every task's rows are stored.  S, group_start
-// and total_blocks are derived by chain_stage_prepare.  Lives in device
-// memory.
-constexpr int kEpiStore = 0, kEpiSiluPair = 1;
-struct ChainStage {
-    GemvTask t[kMaxTasks];
-    uint32_t group_start[kMaxTasks + 1];
-    int32_t count;
-    uint32_t cols;
-    uint32_t S;             // column slices per row (1, 2 or 4)
-    uint32_t total_blocks;  // row blocks (8 / S rows; 4 / S of each of gate and up for kEpiSiluPair)
-    int32_t kind;
-    int32_t epi;
-    const float* a;
-    const float* b;
-    const float* w;
-    float* r_out;
-    float eps;
-    int32_t wait;
-};
-// Validates a stage for format fmt (Q8_0 / Q4_0, cols % 256 == 0,
-// cols <= 14336 (4608 with the add+RMSNorm prologue), kind kXPlain or
-// kAddNorm, at most 64 row blocks per workgroup, 16-byte aligned operands,
-// earlier `wait`) and fills its derived fields; hipErrorInvalidValue /
-// hipErrorInvalidConfiguration when not covered.
-hipError_t chain_stage_prepare(int fmt, ChainStage& st, uint32_t index);
-// Grid of a chain launch (one 16-wave workgroup per CU), 0 if it cannot be
-// resident all at once.
-uint32_t chain_grid(int fmt);
-size_t chain_lds_bytes(int fmt);
-// One launch running every stage of prog (device memory, nstages entries);
-// counters (nstages, zero before the first launch; the kernel leaves them
-// zero) and status (status[0] = 1 after a bounded wait gave up).
-hipError_t launch_gemv_chain(int fmt, const ChainStage* prog, uint32_t nstages, uint32_t* counters, uint32_t* status,
-                             uint32_t spin_limit, hipStream_t stream);
-// Zeroes counters and status with a kernel (capturable; no memset nodes).
-hipError_t launch_chain_reset(uint32_t* counters, uint32_t nstages, uint32_t* status, hipStream_t stream);
-
 // Per-32-element activation quantiser (int8 + fp32 scale per block).
 hipError_t launch_quantize_acts(const float* X, int8_t* xq, float* xs, size_t M, size_t K,
                                 hipStream_t stream);

@@ -242,6 +242,7 @@ bool init_common(zq_model& m, std::string& e) {
 hipError_t project(zq_model& m, const Weight& w, const float* X, float* Y, uint32_t M, bool quantized,
                    uint32_t* splits = nullptr) {
     if (splits) *splits = 1;
+    if (!m.fuse_quant) splits = nullptr;  // ZQ_MODEL_FUSED=0: the GEMM reduces its own split-K planes
     if (quantized)
         return zq::launch_gemm_i8(w.fmt, w.p, m.xq, m.xs, Y, m.partial, M, w.rows, w.cols, m.stream, splits);
     return zq::launch_gemm_f32(w.fmt, w.p, X, Y, m.partial, m.partial_bytes, M, w.rows, w.cols, m.stream);
@@ -473,7 +474,9 @@ hipError_t enqueue_decode(zq_model& m) {
 
 // The fused decode covers Q8_0 / Q4_0 projections on the streaming GEMV's
 // shapes; anything else keeps the separate norm / activation kernels.
-// ZQ_MODEL_FUSED=0 disables it (A/B runs and the equivalence test).
+// ZQ_MODEL_FUSED=0 disables it and, in prefill, the quantisers folded into
+// the norm / SiLU kernels and the split-K sums left to the GEMMs' readers
+// (A/B runs and the equivalence tests).
 void choose_fused(zq_model& m) {
     const char* e = std::getenv("ZQ_MODEL_FUSED");
     const auto& c = m.cfg;

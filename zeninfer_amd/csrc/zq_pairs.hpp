@@ -1,6 +1,5 @@
 // zq_pairs.hpp -- device helpers of the Q8_0 / Q4_0 block-pair GEMV kernels
-// (zq_gemv.hip) and the chained decode kernel (zq_chain.hip): range-limited
-// 16-byte buffer loads and the per-lane dot of one block pair with 64
+// (zq_gemv.hip): range-limited 16-byte buffer loads and the per-lane dot of one block pair with 64
 // activation values.
 #pragma once
 #include "zq_device.hpp"

@@ -52,14 +52,6 @@ class GemmTask(ctypes.Structure):
     _fields_ = [("weights", _P), ("Y", _P), ("rows", _S)]
 
 
-X_PLAIN, X_SILU_MUL, X_ADD_NORM = 0, 1, 2
-Y_STORE, Y_SILU_PAIR = 0, 1
-
-
-class ChainStage(ctypes.Structure):
-    _fields_ = [("tasks", ctypes.POINTER(GemvTask)), ("count", _S), ("cols", _S), ("kind", ctypes.c_int),
-                ("a", _P), ("b", _P), ("w", _P), ("r_out", _P), ("eps", ctypes.c_float), ("wait", ctypes.c_int),
-                ("epilogue", ctypes.c_int)]
 
 
 # Every symbol include/zq_hip.h declares, with (restype, argtypes).
@@ -98,12 +90,6 @@ SIGNATURES = {
     "zq_hip_gemm_dev": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _S, _S, _S, ctypes.c_int, _P, _S, _P]),
     "zq_hip_noalloc_scratch_bytes": (_S, []),
     "zq_hip_gemm_dev_noalloc": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _S, _S, _S, ctypes.c_int, _P]),
-    "zq_hip_chain_create": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(ChainStage), _S, ctypes.POINTER(_P)]),
-    "zq_hip_chain_launch": (ctypes.c_int, [_P, _P]),
-    "zq_hip_chain_check": (ctypes.c_int, [_P, ctypes.POINTER(ctypes.c_int)]),
-    "zq_hip_chain_set_spin_limit": (ctypes.c_int, [_P, ctypes.c_uint32]),
-    "zq_hip_chain_reset": (ctypes.c_int, [_P, _P]),
-    "zq_hip_chain_destroy": (None, [_P]),
     "zq_hip_quantize_acts_dev": (ctypes.c_int, [_P, _P, _P, _S, _S, _P]),
     "zq_hip_block_dots_dev": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _S, _S, _S, _P]),
     "zq_hip_dequantize_dev": (ctypes.c_int, [ctypes.c_int, _P, _P, _S, _S, _P]),
@@ -460,59 +446,6 @@ def gemm_dev_noalloc(fmt, w, X, Y, tokens, rows, cols, act=ACT_DEFAULT, stream=N
     _need(Y, 4 * tokens * rows, "gemm_dev_noalloc Y")
     return check(lib().zq_hip_gemm_dev_noalloc(fmt, _dptr(w), _dptr(X), _dptr(Y), tokens, rows, cols, act,
                                                _stream(stream)), "zq_hip_gemm_dev_noalloc")
-
-
-class Chain:
-    """A decode step's projections as one persistent launch (zq_hip_chain_*).
-    stages: list of dicts with keys tasks [(weights, y, rows)], cols, and
-    optionally kind (X_PLAIN), a (x), b, w, r_out, eps, wait (-1),
-    epilogue (Y_STORE)."""
-
-    def __init__(self, fmt, stages):
-        arr = (ChainStage * len(stages))()
-        self._keep = []
-        for i, st in enumerate(stages):
-            for w, y, r in st["tasks"]:
-                _need(w, weight_bytes(fmt, r, st["cols"]), f"chain stage {i} weights")
-                if y is not None:
-                    _need(y, 4 * r, f"chain stage {i} y")
-            for key in ("a", "b", "w", "r_out"):
-                if st.get(key) is not None:
-                    _check_device(st[key], f"chain stage {i} {key}")
-            t = (GemvTask * len(st["tasks"]))(*[GemvTask(_dptr(w), _dptr(y), r) for w, y, r in st["tasks"]])
-            self._keep.append(t)
-            arr[i] = ChainStage(ctypes.cast(t, ctypes.POINTER(GemvTask)), len(st["tasks"]), st["cols"],
-                                st.get("kind", X_PLAIN), _dptr(st.get("a")), _dptr(st.get("b")), _dptr(st.get("w")),
-                                _dptr(st.get("r_out")), st.get("eps", 0.0), st.get("wait", -1),
-                                st.get("epilogue", Y_STORE))
-        h = _P()
-        check(lib().zq_hip_chain_create(fmt, arr, len(stages), ctypes.byref(h)), "zq_hip_chain_create")
-        self._h = h
-
-    def launch(self, stream=None):
-        return check(lib().zq_hip_chain_launch(self._h, _stream(stream)), "zq_hip_chain_launch")
-
-    def timed_out(self):
-        t = ctypes.c_int()
-        check(lib().zq_hip_chain_check(self._h, ctypes.byref(t)), "zq_hip_chain_check")
-        return bool(t.value)
-
-    def set_spin_limit(self, polls):
-        return check(lib().zq_hip_chain_set_spin_limit(self._h, polls), "zq_hip_chain_set_spin_limit")
-
-    def reset(self, stream=None):
-        return check(lib().zq_hip_chain_reset(self._h, _stream(stream)), "zq_hip_chain_reset")
-
-    def close(self):
-        if getattr(self, "_h", None):
-            lib().zq_hip_chain_destroy(self._h)
-            self._h = None
-
-    def __del__(self):
-        try:
-            self.close()
-        except Exception:
-            pass
 
 
 def quantize_acts_dev(X, xq, xs, tokens, cols, stream=None):
