@@ -255,8 +255,8 @@ def test_config4_width_int8_prefill_within_quantisation_error(shallow, zq):
     (amax/127)/sqrt(12)/rms ~ 0.5% per GEMM input (amax ~ 2.1 rms for a
     Gaussian block).  On a well-conditioned model that keeps logits within 5%
     (the small model's bar against the reference runtime).  This random-init
-    model is not well conditioned: its attention scores have a spread of
-    ~60-90 (printed by the tap test above), so the softmax is nearly one-hot
+    model is not well conditioned: its attention scores have a standard
+    deviation of ~88 (printed by the tap tests above), so the softmax is nearly one-hot
     and a 0.5% change of q or k moves scores by ~0.3-0.5, enough to change
     which key wins for rows whose top two scores are that close.  Such rows
     change their attention output outright, and the logits move by far more
