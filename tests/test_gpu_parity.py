@@ -155,6 +155,50 @@ print('ok')
     assert r.returncode == 0 and "ok" in r.stdout, r.stdout + r.stderr
 
 
+@pytest.mark.parametrize("mode", ["0", "1"])
+def test_gemv_streaming_kernels_forced(zq, orc, mode):
+    """Both Q8_0 / Q4_0 streaming kernels on every shape class, whichever the
+    default selection would take: ZQ_GEMV_MFMA=1 (the MFMA kernel: 1..16
+    slices of 1024 columns, a partial last slice, several teams per
+    workgroup, two tasks of a batch) and =0 (the fp32-FMA kernel), against
+    the oracle; a non-finite activation makes every MFMA output NaN."""
+    import subprocess, sys, os
+    code = f"""
+import sys, numpy as np, torch
+sys.path.insert(0, {os.getcwd()!r})
+from oracle import oracle as O
+from zeninfer_amd import zq
+from tests.tolerance import assert_close
+o = O.Oracle(); zq.init()
+for fmt in (O.Q8_0, O.Q4_0):
+    for rows, cols in ((1, 256), (37, 1280), (300, 2816), (65, 4096), (33, 4352), (129, 9216), (70, 14336), (9, 16384)):
+        w = o.gen_weights(fmt, rows + cols, rows, cols); x = o.gen_normal(cols, cols)
+        wd = torch.zeros(zq.weight_bytes(fmt, rows, cols), dtype=torch.uint8, device='cuda:0'); wd[:w.size] = torch.from_numpy(w).cuda()
+        y = torch.empty(rows, device='cuda:0')
+        zq.gemv_dev(fmt, wd, torch.from_numpy(x).cuda(), y, rows, cols); torch.cuda.synchronize()
+        assert_close(y.cpu().numpy(), o.gemv_f32(fmt, w, x, rows, cols), f'forced {{fmt}} {{rows}}x{{cols}}')
+    # a batch of two tasks sharing x
+    cols = 5120
+    ws = [o.gen_weights(fmt, 77 + i, r, cols) for i, r in enumerate((50, 23))]
+    x = o.gen_normal(78, cols)
+    ys = zq.gemv_batch(fmt, ws, x, [50, 23], cols)
+    for w, y, r in zip(ws, ys, (50, 23)):
+        assert_close(y, o.gemv_f32(fmt, w, x, r, cols), 'forced batch')
+        zq.release(w)
+if {mode!r} == '1':
+    rows, cols = 40, 4352
+    w = o.gen_weights(O.Q8_0, 5, rows, cols); x = o.gen_normal(6, cols); x[1000] = np.inf
+    wd = torch.zeros(zq.weight_bytes(O.Q8_0, rows, cols), dtype=torch.uint8, device='cuda:0'); wd[:w.size] = torch.from_numpy(w).cuda()
+    y = torch.zeros(rows, device='cuda:0')
+    zq.gemv_dev(O.Q8_0, wd, torch.from_numpy(x).cuda(), y, rows, cols); torch.cuda.synchronize()
+    assert torch.isnan(y).all()
+print('ok')
+"""
+    env = dict(os.environ, ZQ_GEMV_MFMA=mode)
+    r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=240)
+    assert r.returncode == 0 and "ok" in r.stdout, r.stdout + r.stderr
+
+
 def test_gemv_batch_qkv(zq, orc):
     cols = 4096
     rows = [4096, 1024, 1024]
@@ -166,6 +210,8 @@ def test_gemv_batch_qkv(zq, orc):
     before = zq.stats()["batches"]
     zq.gemv_batch(O.Q8_0, ws, x, rows, cols)
     assert zq.stats()["batches"] == before + 1
+    for w in ws:  # residency is keyed by host address: a later array there must not find these
+        zq.release(w)
 
 
 @pytest.mark.parametrize("fmt", [O.Q8_0, O.Q4_0, O.Q6_K])
@@ -406,6 +452,8 @@ def test_ffn_gemv(zq, orc):
     # SiLU goes through expf: bound the error by the sum of |terms| of the down
     # projection (the GEMV bar relative to the magnitude that is summed)
     mag = np.abs(dd) @ np.abs(act)
+    for w in (g, u, d):
+        zq.release(w)
     assert np.all(np.abs(y - want) <= 1e-4 + 1e-5 * mag), np.max(np.abs(y - want) / (1e-4 + 1e-5 * mag))
 
 

@@ -1006,6 +1006,297 @@ __global__ __launch_bounds__(kThreads) void gemv_block_kernel(TaskTable tt, cons
     }
 }
 
+// ------------------------------------------------- MFMA streaming GEMV ---
+// Q8_0 / Q4_0 decode GEMV with the per-block integer dots on the matrix
+// cores.  x (fp32) is split exactly into four int8 "digit" vectors per 64-
+// element pair: X = trunc(x * 2^s) with one exponent s per pair such that
+// |X| < 2^30, and X = sum_j d_j 256^j with balanced digits d_j in [-128, 127]
+// (the bytes of (X + 0x80808080) ^ 0x80808080).  Each 32-element block dot
+// with one digit vector is then an exact int32 (|sum| < 2^20), computed by
+// v_mfma_i32_4x4x4_16b_i8: 16 independent 4x4x4 products per instruction,
+// product b = (4 weight rows of pair b) x (4 digit vectors of pair b), 8
+// instructions per block (K = 4 each), accumulating in C.  The lane of
+// product b and digit j then holds, for each of the 4 rows, the block's dot
+// with digit j; it adds float(dot) * d_w (v_fma_mix_f32 reads the fp16 scale
+// in place) for both blocks of the pair and scales the sum by 2^(8j - s),
+// exactly.  The only rounding is that of the fp32 sums (and of x below 2^-30
+// of its pair's largest element, which X drops), so the result is within the
+// fp32 reference's own rounding level.  Against the fp32-FMA kernel this
+// replaces ~2 VALU instructions per weight element by ~24 per 4096 elements,
+// so the decode tail after the last weight block shrinks.  Non-finite x makes
+// every output NaN.
+//
+// Work split: a wave owns a slice of 16 pairs (1024 columns) for the whole
+// kernel -- its digits stay in 16 VGPRs -- and each row block it streams 4
+// rows x 16 pairs (coalesced 16 B loads, stashed through LDS at a row stride
+// that makes the lane reads conflict-free), so S = ceil(pairs / 16) waves
+// cover a row and TEAMS = 16 / S teams of S waves share a workgroup
+// (4 x TEAMS rows per row block).  The S partial sums of a row are added
+// through LDS in slice order.
+typedef int v4i __attribute__((ext_vector_type(4)));
+constexpr int kMfmaPairs = 16;  // pairs per slice
+template <int FMT>
+struct MfmaGeo {
+    static constexpr int DW = FMT == kQ8_0 ? 17 : 9;       // dwords per pair
+    static constexpr int UPR = kMfmaPairs * DW / 4;         // 16 B units per row segment (68 / 36)
+    static constexpr int WROW = FMT == kQ8_0 ? 280 : 152;  // LDS dwords per stashed row (bank-conflict-free reads)
+    static constexpr int WBUF = 4 * WROW;                   // dwords per wave stash
+    static constexpr int NU = (4 * UPR + 63) / 64;          // 16 B loads per lane per row block
+};
+
+template <int FMT, int XPT, int D, int XK>
+__global__ __launch_bounds__(1024) void gemv_mfma_kernel(TaskTable tt, const float* __restrict__ x, uint32_t cols,
+                                                          uint32_t total_blocks, uint32_t S, uint32_t TEAMS,
+                                                          XPrologue pro) {
+    using G = MfmaGeo<FMT>;
+    constexpr int DW = G::DW;
+    extern __shared__ uint32_t lds[];
+    // LDS map: [0, NW*WBUF) weight stashes; then the digits (S*16 pairs x 68
+    // dwords: 16 float4 x 4 digits, 4 dwords of padding); then the pair
+    // exponents; then the partial sums [2][NW][4 rows][4 lane groups].
+    const uint32_t NW = S * TEAMS, NT = NW * 64;
+    const uint32_t pairs = cols >> 6;
+    const uint32_t spairs = S * kMfmaPairs;                 // pairs incl. the last slice's padding
+    uint32_t* gdig = lds + NW * G::WBUF;
+    int* sexp = reinterpret_cast<int*>(gdig + spairs * 68);
+    float* red = reinterpret_cast<float*>(sexp + spairs);
+    const uint32_t rb = pairs * DW * 4;
+    const int lane = threadIdx.x & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t team = wave / S, slice = wave % S;
+    const uint32_t p0 = slice * kMfmaPairs;
+    const uint32_t np = p0 < pairs ? min(uint32_t(kMfmaPairs), pairs - p0) : 0u;
+    const uint32_t seg = np * DW * 4;                      // valid bytes of a row segment
+    const int qb = lane >> 2, qi = lane & 3;               // product (pair) and row / digit of this lane
+    uint32_t* buf = lds + wave * G::WBUF;
+
+    // ---- x (or its producer's operands) first: loads retire in order
+    const uint32_t nx4 = cols >> 2;
+    const float4* x4 = reinterpret_cast<const float4*>(XK == kXPlain ? x : pro.a);
+    float4 xr[XPT], xb[XK == kXPlain ? 1 : XPT], xw[XK == kAddNorm ? XPT : 1];
+#pragma unroll
+    for (int k = 0; k < XPT; ++k) {
+        const uint32_t idx = min(threadIdx.x + uint32_t(k) * NT, nx4 - 1);
+        xr[k] = x4[idx];
+        if constexpr (XK == kSiluMul) xb[k] = reinterpret_cast<const float4*>(pro.b)[idx];
+        if constexpr (XK == kAddNorm) {
+            xb[k] = pro.b ? reinterpret_cast<const float4*>(pro.b)[idx] : make_float4(0, 0, 0, 0);
+            xw[k] = reinterpret_cast<const float4*>(pro.w)[idx];
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- weight ring: D row blocks in flight
+    auto locate = [&](uint32_t blk, uint32_t& row0, int& ti) {
+        // wave-uniform, so the task table is read with scalar loads
+        ti = __builtin_amdgcn_readfirstlane(find_task(tt, blk));
+        row0 = __builtin_amdgcn_readfirstlane((blk - tt.group_start[ti]) * (TEAMS * 4) + team * 4);
+    };
+    auto load = [&](uint32_t row0, int ti, uint4 (&u)[G::NU]) {
+        const GemvTask& t = tt.t[ti];
+        const __amdgpu_buffer_rsrc_t rs = span_rsrc(t.w, t.rows * rb);
+#pragma unroll
+        for (int m = 0; m < G::NU; ++m) {
+            const uint32_t unit = uint32_t(lane + 64 * m);
+            const uint32_t i = unit / G::UPR, o = unit - i * G::UPR;
+            const uint32_t row = min(row0 + i, t.rows - 1);
+            const uint32_t off = (i < 4 && 16 * o < seg) ? row * rb + p0 * DW * 4 + 16 * o : 0xFFFFFFF0u;
+            u[m] = span_load16(rs, off);
+        }
+    };
+    auto stash = [&](const uint4 (&u)[G::NU]) {
+#pragma unroll
+        for (int m = 0; m < G::NU; ++m) {
+            const uint32_t unit = uint32_t(lane + 64 * m);
+            const uint32_t i = unit / G::UPR, o = unit - i * G::UPR;
+            if (i < 4) reinterpret_cast<uint4*>(buf + i * G::WROW)[o] = u[m];
+        }
+    };
+    uint32_t blk = blockIdx.x;
+    uint4 u[D][G::NU];
+    uint32_t row0s[D];
+    int tis[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) {  // branch-free: a slot past the end re-reads the last block
+        const uint32_t b = min(blk + uint32_t(d) * gridDim.x, total_blocks - 1);
+        locate(b, row0s[d], tis[d]);
+        load(row0s[d], tis[d], u[d]);
+    }
+
+    // ---- x prologue, then x (fp32) into LDS
+    if constexpr (XK == kSiluMul) {
+        auto f = [](float g, float u) { return g / (1.0f + expf(-g)) * u; };
+#pragma unroll
+        for (int k = 0; k < XPT; ++k)
+            xr[k] = make_float4(f(xr[k].x, xb[k].x), f(xr[k].y, xb[k].y), f(xr[k].z, xb[k].z), f(xr[k].w, xb[k].w));
+    }
+    if constexpr (XK == kAddNorm) {
+        // v = a + b; sum of squares in double; inv = 1/sqrtf(float(ss/n) + eps);
+        // x = v * inv * w -- the arithmetic of rmsnorm_kernel
+        __shared__ double xred[16];
+        double ss = 0.0;
+#pragma unroll
+        for (int k = 0; k < XPT; ++k) {
+            xr[k] = make_float4(xr[k].x + xb[k].x, xr[k].y + xb[k].y, xr[k].z + xb[k].z, xr[k].w + xb[k].w);
+            if (threadIdx.x + uint32_t(k) * NT < nx4) {
+                ss += double(xr[k].x) * double(xr[k].x);
+                ss += double(xr[k].y) * double(xr[k].y);
+                ss += double(xr[k].z) * double(xr[k].z);
+                ss += double(xr[k].w) * double(xr[k].w);
+                if (pro.r_out && blockIdx.x == 0)
+                    reinterpret_cast<float4*>(pro.r_out)[threadIdx.x + uint32_t(k) * NT] = xr[k];
+            }
+        }
+        ss = wave_sum(ss);
+        if (lane == 0) xred[wave] = ss;
+        __syncthreads();
+        double tot = 0.0;
+        for (uint32_t i = 0; i < NW; ++i) tot += xred[i];
+        const float inv = 1.0f / sqrtf(float(tot / double(cols)) + pro.eps);
+#pragma unroll
+        for (int k = 0; k < XPT; ++k)
+            xr[k] = make_float4(xr[k].x * inv * xw[k].x, xr[k].y * inv * xw[k].y, xr[k].z * inv * xw[k].z,
+                                xr[k].w * inv * xw[k].w);
+    }
+    // ---- digits, straight from the registers: thread t holds float4 t + k*NT,
+    // so the 16 float4 of a pair sit in 16 consecutive lanes (NT % 64 == 0);
+    // their max comes from a 16-lane DPP reduction.  Digit j of the pair's
+    // float4 e lands at dword p*68 + 4e + j (one 16 B write per float4; the
+    // 68-dword pair stride makes the B reads below conflict-free).
+    int bad = 0;
+#pragma unroll
+    for (int k = 0; k < XPT; ++k) {
+        const uint32_t idx = threadIdx.x + uint32_t(k) * NT;
+        const float4 t = idx < nx4 ? xr[k] : make_float4(0, 0, 0, 0);
+        float am = fmaxf(fmaxf(fabsf(t.x), fabsf(t.y)), fmaxf(fabsf(t.z), fabsf(t.w)));
+        am = fmaxf(am, dpp_f<kDppXor1>(am));
+        am = fmaxf(am, dpp_f<kDppXor2>(am));
+        am = fmaxf(am, dpp_f<kDppHalfMirror>(am));
+        am = fmaxf(am, dpp_f<kDppMirror>(am));
+        bad |= !(am <= 3.402823466e38f);  // inf or NaN
+        const int s = 30 - (am > 0.0f && am <= 3.402823466e38f ? __builtin_amdgcn_frexp_expf(am) : 0);
+        const uint32_t y0 = uint32_t(int(ldexpf(t.x, s))) + 0x80808080u;
+        const uint32_t y1 = uint32_t(int(ldexpf(t.y, s))) + 0x80808080u;
+        const uint32_t y2 = uint32_t(int(ldexpf(t.z, s))) + 0x80808080u;
+        const uint32_t y3 = uint32_t(int(ldexpf(t.w, s))) + 0x80808080u;
+        const uint32_t t01a = __builtin_amdgcn_perm(y1, y0, 0x05010400u);
+        const uint32_t t01b = __builtin_amdgcn_perm(y1, y0, 0x07030602u);
+        const uint32_t t23a = __builtin_amdgcn_perm(y3, y2, 0x05010400u);
+        const uint32_t t23b = __builtin_amdgcn_perm(y3, y2, 0x07030602u);
+        if (idx < spairs * 16) {
+            const uint32_t p = idx >> 4, e = idx & 15;
+            *reinterpret_cast<uint4*>(gdig + p * 68 + 4 * e) =
+                make_uint4(__builtin_amdgcn_perm(t23a, t01a, 0x05040100u) ^ 0x80808080u,
+                           __builtin_amdgcn_perm(t23a, t01a, 0x07060302u) ^ 0x80808080u,
+                           __builtin_amdgcn_perm(t23b, t01b, 0x05040100u) ^ 0x80808080u,
+                           __builtin_amdgcn_perm(t23b, t01b, 0x07060302u) ^ 0x80808080u);
+            if (e == 0) sexp[p] = s;
+        }
+    }
+    const bool nan_out = __syncthreads_or(bad) != 0;
+    // this lane's B operand: digit qi of pair p0 + qb (16 dwords, K order)
+    int dig[16];
+    {
+        const uint32_t* src = gdig + (p0 + qb) * 68 + qi;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) dig[e] = int(src[4 * e]);
+    }
+    const int fexp = 8 * qi - sexp[p0 + qb];
+    // Q4_0: the codes enter the MFMA as n (0..15); the -8 offset is the C
+    // operand's start, -8 * (sum of the block's digits)
+    v4i c0 = {0, 0, 0, 0}, c1 = {0, 0, 0, 0};
+    if constexpr (FMT == kQ4_0) {
+        int s0 = 0, s1 = 0;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            s0 = __builtin_amdgcn_sdot4(dig[t], 0x01010101, s0, false);
+            s1 = __builtin_amdgcn_sdot4(dig[8 + t], 0x01010101, s1, false);
+        }
+        c0 = v4i{-8 * s0, -8 * s0, -8 * s0, -8 * s0};
+        c1 = v4i{-8 * s1, -8 * s1, -8 * s1, -8 * s1};
+    }
+
+    int parity = 0;
+    // One row block from ring slot d.  The stash is this wave's own LDS
+    // buffer (a wave's LDS accesses complete in order, so no barrier guards
+    // it); the partial sums alternate between two buffers, and the one
+    // barrier per row block separates a buffer's reads from its next writes.
+    auto step = [&](auto dc) {
+        constexpr int d = decltype(dc)::value;
+        stash(u[d]);
+        const uint32_t row0 = row0s[d];
+        const int ti = tis[d];
+        const uint32_t nblk = blk + uint32_t(D) * gridDim.x;
+        if (nblk < total_blocks) {
+            locate(nblk, row0s[d], tis[d]);
+            load(row0s[d], tis[d], u[d]);
+        }
+        const uint32_t* pr = buf + qi * G::WROW + qb * DW;  // A: row qi, pair qb
+        uint32_t q[DW];
+#pragma unroll
+        for (int k = 0; k < DW; ++k) q[k] = pr[k];
+        v4i e0 = c0, e1 = c1;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            int a0, a1;
+            if constexpr (FMT == kQ8_0) {
+                a0 = int(__builtin_amdgcn_alignbyte(q[t + 1], q[t], 2));
+                a1 = int(q[9 + t]);
+            } else {
+                const uint32_t w0 = __builtin_amdgcn_alignbyte(q[(t & 3) + 1], q[t & 3], 2);
+                a0 = int((t < 4 ? w0 : w0 >> 4) & 0x0F0F0F0Fu);
+                a1 = int((t < 4 ? q[5 + t] : q[1 + t] >> 4) & 0x0F0F0F0Fu);
+            }
+            e0 = __builtin_amdgcn_mfma_i32_4x4x4i8(a0, dig[t], e0, 0, 0, 0);
+            e1 = __builtin_amdgcn_mfma_i32_4x4x4i8(a1, dig[8 + t], e1, 0, 0, 0);
+        }
+        // scales of rows 0..3 of pair qb: d0 in the low half of dword 0, d1
+        // in the high half of dword 8 (Q8_0) / 4 (Q4_0)
+        float acc[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t* pi = buf + i * G::WROW + qb * DW;
+            const uint32_t w0 = pi[0], w1 = pi[FMT == kQ8_0 ? 8 : 4];
+            float a = float(e0[i]) * float(__builtin_bit_cast(_Float16, uint16_t(w0)));
+            a = fmaf(float(e1[i]), float(__builtin_bit_cast(_Float16, uint16_t(w1 >> 16))), a);
+            acc[i] = ldexpf(a, fexp);
+        }
+        // sum over the 4 digits (quad), then each lane keeps row (lane & 3)
+        // and sums its 16-lane row's 4 quads; lanes 16g + i then hold row i's
+        // sum over the pairs 4g .. 4g+3
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            acc[i] += dpp_f<kDppXor1>(acc[i]);
+            acc[i] += dpp_f<kDppXor2>(acc[i]);
+        }
+        float v = qi == 0 ? acc[0] : qi == 1 ? acc[1] : qi == 2 ? acc[2] : acc[3];
+        v += dpp_f<0x124>(v);  // row_ror:4
+        v += dpp_f<0x128>(v);  // row_ror:8
+        float* rp = red + parity * (16 * 16);
+        if ((lane & 15) < 4) rp[wave * 16 + qi * 4 + (lane >> 4)] = v;
+        __syncthreads();
+        if (slice == 0 && lane < 4) {
+            // slice order; every load issued before the adds
+            float4 w[16];
+#pragma unroll
+            for (uint32_t s2 = 0; s2 < 16; ++s2)
+                if (s2 < S) w[s2] = *reinterpret_cast<const float4*>(rp + (team * S + s2) * 16 + lane * 4);
+            float s = 0.0f;
+#pragma unroll
+            for (uint32_t s2 = 0; s2 < 16; ++s2)
+                if (s2 < S) s += ((w[s2].x + w[s2].y) + w[s2].z) + w[s2].w;
+            const GemvTask& t = tt.t[ti];
+            if (row0 + lane < t.rows) t.y[row0 + lane] = nan_out ? __builtin_nanf("") : s;
+        }
+        parity ^= 1;
+        blk += gridDim.x;
+    };
+    while (blk < total_blocks) {
+        step(std::integral_constant<int, 0>{});
+        if constexpr (D > 1) if (blk < total_blocks) step(std::integral_constant<int, 1>{});
+    }
+}
+
 int rows_per_wave(uint32_t total_rows) {
     static const int forced = [] {
         const char* e = getenv("ZQ_GEMV_ROWS_PER_WAVE");
@@ -1106,6 +1397,54 @@ hipError_t launch_stream_any(int R, TaskTable& tt, const float* x, uint32_t cols
     if (pairs <= 64) return launch_stream_r<FMT, 1>(R, tt, x, cols, stream);
     if (pairs <= 128) return launch_stream_r<FMT, 2>(R, tt, x, cols, stream);
     return launch_stream_r<FMT, 4>(R, tt, x, cols, stream);
+}
+
+// The MFMA streaming GEMV (gemv_mfma_kernel): S slices of 16 pairs per row,
+// TEAMS = 16 / S teams, one workgroup per CU.
+template <int FMT, int XK = kXPlain>
+hipError_t launch_mfma(TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream,
+                       const XPrologue& pro = XPrologue{}) {
+    using G = MfmaGeo<FMT>;
+    const uint32_t pairs = cols >> 6;
+    const uint32_t S = (pairs + kMfmaPairs - 1) / kMfmaPairs;
+    if (!S || S > 16) return hipErrorInvalidConfiguration;
+    const uint32_t TEAMS = 16 / S, NW = S * TEAMS, RB = 4 * TEAMS;
+    const size_t rb = size_t(pairs) * G::DW * 4;
+    uint32_t blocks = 0;
+    for (int i = 0; i < tt.count; ++i) {
+        if (size_t(tt.t[i].rows) * rb >= (size_t(1) << 32) - 16) return hipErrorInvalidConfiguration;
+        tt.group_start[i] = blocks;
+        blocks += (tt.t[i].rows + RB - 1) / RB;
+    }
+    tt.group_start[tt.count] = blocks;
+    const size_t lds = (size_t(NW) * G::WBUF + size_t(S) * kMfmaPairs * 69 + 512) * 4;
+    if (lds > lds_limit()) return hipErrorInvalidConfiguration;
+    const uint32_t grid = std::min<uint32_t>(blocks, uint32_t(cu_count()));
+    const uint32_t xpt = (S * kMfmaPairs * 16 + NW * 64 - 1) / (NW * 64);  // float4 per thread, padded pairs included
+#define ZQ_MFMA_LAUNCH(XPT)                                                                                        \
+    hipLaunchKernelGGL((gemv_mfma_kernel<FMT, XPT, 1, XK>), dim3(grid), dim3(NW * 64), lds, stream, tt, x, cols, \
+                       blocks, S, TEAMS, pro)
+    if (xpt <= 1) ZQ_MFMA_LAUNCH(1);
+    else if (xpt <= 2) ZQ_MFMA_LAUNCH(2);
+    else if (xpt <= 4) ZQ_MFMA_LAUNCH(4);
+    else return hipErrorInvalidConfiguration;
+#undef ZQ_MFMA_LAUNCH
+    return hipGetLastError();
+}
+// Which streaming kernel a shape takes.  Measured on MI355X (per launch,
+// Q8_0): the MFMA kernel wins where a CU streams many row blocks or long rows
+// (down 4096x14336: 15.0 -> 13.6 us; lm_head 128256x4096: 88.5 -> 80.6 us)
+// and loses a little on short launches of 4096-column rows (q/o 6.1 -> 7.1
+// us, gate|up 13.8 -> 14.1 us), whose fixed costs (the digit split, one more
+// barrier) are not amortised.  ZQ_GEMV_MFMA=0 / 1 forces the fp32-FMA / MFMA
+// kernel everywhere (A/B runs).
+bool mfma_gemv_for(uint32_t cols, uint32_t total_rows) {
+    static const int forced = [] {
+        const char* e = getenv("ZQ_GEMV_MFMA");
+        return e && (e[0] == '0' || e[0] == '1') ? e[0] - '0' : -1;
+    }();
+    if (forced >= 0) return forced == 1;
+    return cols > 4096 || total_rows >= 32768;
 }
 
 template <int FMT, int R, int S>
@@ -1306,6 +1645,10 @@ hipError_t launch_gemv(int fmt, const GemvTask* tasks, int count, const float* x
     bool w16 = true;
     for (int i = 0; i < count; ++i) w16 = w16 && (reinterpret_cast<uintptr_t>(tasks[i].w) & 15u) == 0;
     if (w16 && x16 && c % 256 == 0 && c / 64 <= 256) {
+        if (mfma_gemv_for(c, total_rows)) {
+            const hipError_t e = fmt == kQ8_0 ? launch_mfma<kQ8_0>(tt, x, c, stream) : launch_mfma<kQ4_0>(tt, x, c, stream);
+            if (e != hipErrorInvalidConfiguration) return e;
+        }
         const int Rx = xreg_rows(total_rows);
         return fmt == kQ8_0 ? launch_stream_any<kQ8_0>(Rx, tt, x, c, stream) : launch_stream_any<kQ4_0>(Rx, tt, x, c, stream);
     }
@@ -1353,6 +1696,18 @@ hipError_t launch_gemv_prologue(int fmt, const GemvTask* tasks, int count, const
         tt.t[i] = tasks[i];
     }
     const uint32_t c = static_cast<uint32_t>(cols);
+    uint32_t total_rows = 0;
+    for (int i = 0; i < count; ++i) total_rows += tasks[i].rows;
+    if (mfma_gemv_for(c, total_rows)) {
+        hipError_t e;
+        if (pro.kind == kSiluMul)
+            e = fmt == kQ8_0 ? launch_mfma<kQ8_0, kSiluMul>(tt, nullptr, c, stream, pro)
+                             : launch_mfma<kQ4_0, kSiluMul>(tt, nullptr, c, stream, pro);
+        else
+            e = fmt == kQ8_0 ? launch_mfma<kQ8_0, kAddNorm>(tt, nullptr, c, stream, pro)
+                             : launch_mfma<kQ4_0, kAddNorm>(tt, nullptr, c, stream, pro);
+        if (e != hipErrorInvalidConfiguration) return e;
+    }
     if (pro.kind == kSiluMul)
         return fmt == kQ8_0 ? launch_prologue_s<kQ8_0, kSiluMul>(tt, c, pro, stream)
                             : launch_prologue_s<kQ4_0, kSiluMul>(tt, c, pro, stream);
