@@ -1436,15 +1436,24 @@ hipError_t launch_mfma(TaskTable& tt, const float* x, uint32_t cols, hipStream_t
 // (down 4096x14336: 15.0 -> 13.6 us; lm_head 128256x4096: 88.5 -> 80.6 us)
 // and loses a little on short launches of 4096-column rows (q/o 6.1 -> 7.1
 // us, gate|up 13.8 -> 14.1 us), whose fixed costs (the digit split, one more
-// barrier) are not amortised.  ZQ_GEMV_MFMA=0 / 1 forces the fp32-FMA / MFMA
+// barrier) are not amortised.  Q4_0 gains only on long rows (4096x14336 11.6
+// -> 11.4 us) and loses on vocabulary-sized outputs (64.2 -> 69.6 us): its
+// pair holds twice the elements per byte, so twice the MFMAs per byte.  ZQ_GEMV_MFMA=0 / 1 forces the fp32-FMA / MFMA
 // kernel everywhere (A/B runs).
-bool mfma_gemv_for(uint32_t cols, uint32_t total_rows) {
+// With an x prologue the SiLU*up form measured slower on the MFMA kernel
+// (the down projection of the decoder: 15.3 -> 15.9 us), the add+RMSNorm
+// form faster at vocabulary size (lm_head 87.7 -> 83.5 us).
+int mfma_gemv_forced() {
     static const int forced = [] {
         const char* e = getenv("ZQ_GEMV_MFMA");
         return e && (e[0] == '0' || e[0] == '1') ? e[0] - '0' : -1;
     }();
-    if (forced >= 0) return forced == 1;
-    return cols > 4096 || total_rows >= 32768;
+    return forced;
+}
+bool mfma_gemv_for(int fmt, uint32_t cols, uint32_t total_rows, int xk = kXPlain) {
+    if (mfma_gemv_forced() >= 0) return mfma_gemv_forced() == 1;
+    const bool vocab = fmt == kQ8_0 && total_rows >= 32768;
+    return xk == kXPlain ? cols > 4096 || vocab : xk == kAddNorm && vocab;
 }
 
 template <int FMT, int R, int S>
@@ -1645,7 +1654,7 @@ hipError_t launch_gemv(int fmt, const GemvTask* tasks, int count, const float* x
     bool w16 = true;
     for (int i = 0; i < count; ++i) w16 = w16 && (reinterpret_cast<uintptr_t>(tasks[i].w) & 15u) == 0;
     if (w16 && x16 && c % 256 == 0 && c / 64 <= 256) {
-        if (mfma_gemv_for(c, total_rows)) {
+        if (mfma_gemv_for(fmt, c, total_rows)) {
             const hipError_t e = fmt == kQ8_0 ? launch_mfma<kQ8_0>(tt, x, c, stream) : launch_mfma<kQ4_0>(tt, x, c, stream);
             if (e != hipErrorInvalidConfiguration) return e;
         }
@@ -1698,7 +1707,7 @@ hipError_t launch_gemv_prologue(int fmt, const GemvTask* tasks, int count, const
     const uint32_t c = static_cast<uint32_t>(cols);
     uint32_t total_rows = 0;
     for (int i = 0; i < count; ++i) total_rows += tasks[i].rows;
-    if (mfma_gemv_for(c, total_rows)) {
+    if (mfma_gemv_for(fmt, c, total_rows, pro.kind)) {
         hipError_t e;
         if (pro.kind == kSiluMul)
             e = fmt == kQ8_0 ? launch_mfma<kQ8_0, kSiluMul>(tt, nullptr, c, stream, pro)
