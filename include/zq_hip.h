@@ -52,10 +52,13 @@ extern "C" {
 #define ZQ_FMT_Q6_K 14  /* 256 el / 210 B super-block            (src/quant.cpp:259)  */
 
 /* ---- GEMM activation handling -------------------------------------------- */
-#define ZQ_ACT_DEFAULT 0 /* Q8_0/Q4_0: int8 (the D3D12 default q8_0_gemm_i8 route,
-                            src/backends/d3d12/d3d12_backend.cpp:845-854); Q6_K, Q4_K,
-                            Q5_K: fp32 (their only reference routes) */
-#define ZQ_ACT_INT8 1    /* per-32 int8 activations, kernels/avx2.cpp:502-524 quantiser */
+#define ZQ_ACT_DEFAULT 0 /* fp32 for every format: the arithmetic of the functions this
+                            slot replaces (quant::gemm, src/quant.cpp:1613-1777, and
+                            zen::hip::gemm_q8_0, hip_backend.hip:127-177); the reference
+                            keeps int8 activations opt-in (quant.cpp:1083-1091) */
+#define ZQ_ACT_INT8 1    /* per-32 int8 activations, kernels/avx2.cpp:502-524 quantiser: the
+                            D3D12 prefill route's arithmetic (d3d12_backend.cpp:845-854);
+                            Q8_0 / Q4_0 only */
 #define ZQ_ACT_F32 2     /* fp32 activations, the reference CPU GEMM arithmetic          */
 
 /* Bytes of slack every device weight buffer must carry past its last block

@@ -68,6 +68,11 @@ def test_argument_errors_without_device():
     ws = L.zq_hip_gemm_workspace_bytes(zq.Q8_0, 4, 4096, 4096, zq.ACT_F32)
     assert ws > 0 and ws % (4 * 4096 * 4) == 0
     assert L.zq_hip_gemm_workspace_bytes(zq.Q8_0, 2048, 14336, 4096, zq.ACT_F32) == 0
+    # the default activation mode is fp32 for Q8_0 / Q4_0 too (int8 is opt-in)
+    for fmt in (zq.Q8_0, zq.Q4_0):
+        for m in (4, 2048):
+            assert (L.zq_hip_gemm_workspace_bytes(fmt, m, 4096, 4096, zq.ACT_DEFAULT)
+                    == L.zq_hip_gemm_workspace_bytes(fmt, m, 4096, 4096, zq.ACT_F32))
     # Q6_K also holds its split activations: f16 hi + lo [M][K] and the row
     # scales, 256-byte aligned, ahead of the partial sums
     split = lambda m, k: (m * k * 4 + m * 4 + 255) // 256 * 256

@@ -366,6 +366,19 @@ def test_lm_head_full_size_sampled_rows(zq, orc):
     assert_close(yh[pick], orc.gemv_f32(O.Q8_0, sub, x, len(pick), cols), "lm_head gemv")
 
 
+@pytest.mark.parametrize("fmt", [O.Q8_0, O.Q4_0])
+def test_gemm_default_is_fp32_activations(zq, orc, fmt):
+    # the drop-in quant::gemm keeps the reference CPU arithmetic unless the
+    # caller opts into int8 activations
+    m, n, k = 5, 300, 4096
+    w = orc.gen_weights(fmt, 3, n, k)
+    X = orc.gen_normal(4, m * k)
+    got = zq.gemm(fmt, w, X, m, n, k, zq.ACT_DEFAULT)
+    assert np.array_equal(got, zq.gemm(fmt, w, X, m, n, k, zq.ACT_F32))
+    assert_close(got, orc.gemm_f32(fmt, w, X, m, n, k), "default act")
+    zq.release(w)
+
+
 @pytest.mark.parametrize("fmt", [O.Q6_K, O.Q4_K, O.Q5_K])
 def test_gemm_declines_unsupported(zq, orc, fmt):
     w = orc.gen_weights(fmt, 1, 8, 256)
@@ -373,7 +386,7 @@ def test_gemm_declines_unsupported(zq, orc, fmt):
     with pytest.raises(zq.ZQError) as e:
         zq.gemm(fmt, w, X, 3, 8, 256, zq.ACT_INT8)
     assert e.value.status == zq.DECLINED
-    # the default activation mode of these formats is fp32
+    # the default activation mode is fp32 (for every format)
     assert_close(zq.gemm(fmt, w, X, 3, 8, 256, zq.ACT_DEFAULT), orc.gemm_f32(fmt, w, X, 3, 8, 256), "default act")
     zq.release(w)
 

@@ -234,9 +234,11 @@ bool valid_fmt(int fmt) {
 // gemm_q4k/q5k_kblk_avx2 and the D3D12 shaders/q8_0_gemm_q4k.hlsl).
 bool int8_fmt(int fmt) { return fmt == ZQ_FMT_Q4_0 || fmt == ZQ_FMT_Q8_0; }
 
+// ZQ_ACT_DEFAULT is fp32 activations for every format, as in the routes the
+// drop-in replaces; int8 activations are the caller's explicit choice.
 int resolve_act(int fmt, int act_mode) {
-    if (act_mode == ZQ_ACT_DEFAULT) return int8_fmt(fmt) ? ZQ_ACT_INT8 : ZQ_ACT_F32;
-    return act_mode;
+    (void)fmt;
+    return act_mode == ZQ_ACT_DEFAULT ? ZQ_ACT_F32 : act_mode;
 }
 
 // GEMM support check shared by the host and device entry points.

@@ -89,9 +89,22 @@ __global__ __launch_bounds__(kThreads) void quantize_acts_kernel(const float* __
 }
 
 // ------------------------------------------------------- tile mapping ---
+#ifndef ZQ_GEMM_XCD_BLOCKS
+#define ZQ_GEMM_XCD_BLOCKS 1
+#endif
 __device__ __forceinline__ void tile_of(uint32_t tiles_m, uint32_t tiles_n, uint32_t id, uint32_t& tm, uint32_t& tn) {
     const uint32_t total = tiles_m * tiles_n;
     uint32_t slot = id;
+    if (ZQ_GEMM_XCD_BLOCKS && tiles_m % 4 == 0 && tiles_n % 2 == 0) {
+        // XCD x (ids congruent to x mod 8) owns a quarter of the token tiles
+        // and half of the weight panels, walking its token tiles per panel:
+        // its activation rows stay in its L2, and each weight panel is read
+        // by two XCDs.
+        const uint32_t x = id % 8u, local = id / 8u, qm = tiles_m / 4;
+        tm = (x & 3u) * qm + local % qm;
+        tn = (x >> 2) * (tiles_n / 2) + local / qm;
+        return;
+    }
     if (total % 8u == 0) {
         const uint32_t per_xcd = total / 8u;
         slot = (id % 8u) * per_xcd + id / 8u;
