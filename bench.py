@@ -85,6 +85,39 @@ def summarize_trace(path):
         print(f"{len(d):6d} {np.mean(d) / 1e3:10.2f} {sum(d) / 1e6:10.3f}  {grid} {lds}  {name[:110]}")
 
 
+def summarize_gemm_sweep(path):
+    """Attribute a kernel_trace.csv of `--gemm-sweep-workload` to its calls
+    (each starts with the activation quantiser) and print per (M, N, K) the
+    mean per-call time of every kernel over the last 8 of its 16 calls and the
+    GEMM's TOPS (2*M*N*K over the GEMM kernel alone, and over the whole
+    call)."""
+    import csv
+    rows = [r for r in csv.DictReader(open(path))
+            if "synth" not in r["Kernel_Name"] and "distribution" not in r["Kernel_Name"]]
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    calls, cur = [], None
+    for r in rows:
+        name = r["Kernel_Name"].replace("void ", "").replace("zq::(anonymous namespace)::", "").split("(")[0]
+        if name.startswith("quantize_acts_kernel"):
+            cur = []
+            calls.append(cur)
+        if cur is not None:
+            cur.append((name, (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3))
+    shapes = [(M, N, K) for N, K in ((FFN, HIDDEN), (HIDDEN, FFN)) for M in (32, 128, 512, 2048)]
+    print(f"{'M':>5} {'N x K':>12}  {'gemm kernel':34s} {'gemm_us':>8} {'call_us':>8} {'TOPS_gemm':>9} {'TOPS_call':>9}  other kernels (us)")
+    for i, (M, N, K) in enumerate(shapes):
+        group = calls[16 * i + 8:16 * i + 16]
+        if len(group) < 8:
+            break
+        names = [n for n, _ in group[0]]
+        means = [sum(c[j][1] for c in group) / 8 for j in range(len(names))]
+        g = next(j for j, n in enumerate(names) if n.startswith("gemm_"))
+        ops = 2.0 * M * N * K
+        other = ", ".join(f"{names[j]} {means[j]:.2f}" for j in range(len(names)) if j != g)
+        print(f"{M:5d} {N:5d}x{K:<6d}  {names[g]:34s} {means[g]:8.2f} {sum(means):8.2f} "
+              f"{ops / means[g] / 1e6:9.1f} {ops / sum(means) / 1e6:9.1f}  {other}")
+
+
 def pmc_workload():
     """Few launches for rocprofv3 --pmc passes: a 256 MiB device copy (counter
     calibration), the 4096x14336 Q8_0 down GEMV on 4 distinct matrices, the
@@ -156,6 +189,38 @@ def measured_traffic():
             return int(json.load(f)["per_launch"]["traffic_bytes"])
     except (OSError, KeyError, ValueError):
         return None
+
+
+def gemm_sweep_workload():
+    """Config 2's int8 GEMM sweep for a kernel trace: M = 32, 128, 512, 2048 on
+    14336x4096 and 4096x14336 (Q8_0), 16 calls each rotating over 4 distinct
+    matrices, fp32 activations already in HBM (each call = quantiser + GEMM
+    [+ split-K reduction]).  16 back-to-back calls because the shader clock
+    settles lower under sustained MFMA load than in a short burst (the first
+    M = 2048 calls run ~15% faster than the later ones); the summary averages
+    the last 8, the regime bench.py's event timing measures."""
+    import torch
+    from zeninfer_amd import zq
+    zq.init()
+    dev, Q8 = "cuda:0", zq.Q8_0
+    for N, K in ((FFN, HIDDEN), (HIDDEN, FFN)):
+        ws = []
+        for i in range(4):
+            t = torch.empty(zq.weight_bytes(Q8, N, K), dtype=torch.uint8, device=dev)
+            zq.synth_weights_dev(Q8, 60 + i, t, N, K)
+            ws.append(t)
+        for M in (32, 128, 512, 2048):
+            X = torch.empty(M * K, device=dev)
+            zq.synth_normal_dev(3, X, M * K)
+            Y = torch.empty(M * N, device=dev)
+            wsb = zq.gemm_workspace_bytes(Q8, M, N, K, zq.ACT_INT8)
+            wsp = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+            torch.cuda.synchronize()
+            for i in range(16):
+                zq.gemm_dev(Q8, ws[i % 4], X, Y, M, N, K, zq.ACT_INT8, wsp, wsb)
+            torch.cuda.synchronize()
+            print(f"[gemm-sweep] M={M} N={N} K={K}: 16 calls", file=sys.stderr, flush=True)
+        del ws
 
 
 def cpu_host():
@@ -409,15 +474,24 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--summarize-trace")
+    ap.add_argument("--summarize-gemm-sweep")
     ap.add_argument("--pmc-workload", action="store_true")
+    ap.add_argument("--gemm-sweep-workload", action="store_true",
+                    help="only config 2's int8 GEMM sweep, 3 calls per shape (kernel-trace helper)")
     ap.add_argument("--model-only", action="store_true",
                     help="run only the config-4 decoder leg and print its JSON (profiling helper)")
     args = ap.parse_args()
     if args.summarize_trace:
         summarize_trace(args.summarize_trace)
         return 0
+    if args.summarize_gemm_sweep:
+        summarize_gemm_sweep(args.summarize_gemm_sweep)
+        return 0
     if args.pmc_workload:
         pmc_workload()
+        return 0
+    if args.gemm_sweep_workload:
+        gemm_sweep_workload()
         return 0
     if args.model_only:
         import torch
