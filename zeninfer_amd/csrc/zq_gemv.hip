@@ -1235,7 +1235,18 @@ __global__ __launch_bounds__(1024) void gemv_mfma_kernel(TaskTable tt, const flo
         uint32_t q[DW];
 #pragma unroll
         for (int k = 0; k < DW; ++k) q[k] = pr[k];
-        v4i e0 = c0, e1 = c1;
+        // scales of rows 0..3 of pair qb, read with the operands: d0 in the
+        // low half of dword 0, d1 in the high half of dword 8 (Q8_0) / 4 (Q4_0)
+        uint32_t sw0[4], sw1[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t* pi = buf + i * G::WROW + qb * DW;
+            sw0[i] = pi[0];
+            sw1[i] = pi[FMT == kQ8_0 ? 8 : 4];
+        }
+        // two accumulation chains per block (K slices 0-3 and 4-7), so
+        // dependent MFMAs are four deep instead of eight
+        v4i e0 = c0, e1 = c1, f0 = {0, 0, 0, 0}, f1 = {0, 0, 0, 0};
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
             int a0, a1;
@@ -1247,18 +1258,19 @@ __global__ __launch_bounds__(1024) void gemv_mfma_kernel(TaskTable tt, const flo
                 a0 = int((t < 4 ? w0 : w0 >> 4) & 0x0F0F0F0Fu);
                 a1 = int((t < 4 ? q[5 + t] : q[1 + t] >> 4) & 0x0F0F0F0Fu);
             }
-            e0 = __builtin_amdgcn_mfma_i32_4x4x4i8(a0, dig[t], e0, 0, 0, 0);
-            e1 = __builtin_amdgcn_mfma_i32_4x4x4i8(a1, dig[8 + t], e1, 0, 0, 0);
+            if (t < 4) {
+                e0 = __builtin_amdgcn_mfma_i32_4x4x4i8(a0, dig[t], e0, 0, 0, 0);
+                e1 = __builtin_amdgcn_mfma_i32_4x4x4i8(a1, dig[8 + t], e1, 0, 0, 0);
+            } else {
+                f0 = __builtin_amdgcn_mfma_i32_4x4x4i8(a0, dig[t], f0, 0, 0, 0);
+                f1 = __builtin_amdgcn_mfma_i32_4x4x4i8(a1, dig[8 + t], f1, 0, 0, 0);
+            }
         }
-        // scales of rows 0..3 of pair qb: d0 in the low half of dword 0, d1
-        // in the high half of dword 8 (Q8_0) / 4 (Q4_0)
         float acc[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint32_t* pi = buf + i * G::WROW + qb * DW;
-            const uint32_t w0 = pi[0], w1 = pi[FMT == kQ8_0 ? 8 : 4];
-            float a = float(e0[i]) * float(__builtin_bit_cast(_Float16, uint16_t(w0)));
-            a = fmaf(float(e1[i]), float(__builtin_bit_cast(_Float16, uint16_t(w1 >> 16))), a);
+            float a = float(e0[i] + f0[i]) * float(__builtin_bit_cast(_Float16, uint16_t(sw0[i])));
+            a = fmaf(float(e1[i] + f1[i]), float(__builtin_bit_cast(_Float16, uint16_t(sw1[i] >> 16))), a);
             acc[i] = ldexpf(a, fexp);
         }
         // sum over the 4 digits (quad), then each lane keeps row (lane & 3)
