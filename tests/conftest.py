@@ -48,6 +48,12 @@ def gpu_available():
 def zq():
     """The product library, initialised on the GPU; fails loudly if it cannot."""
     import zeninfer_amd.zq as z
+    try:  # torch's HIP runtime first: tests mix torch tensors with the library's device calls
+        import torch
+        if torch.cuda.is_available():
+            torch.cuda.init()
+    except ImportError:
+        pass
     z.lib()
     st = z.init()
     if st != 0:

@@ -272,9 +272,15 @@ __global__ __launch_bounds__(kThreads) void gemv_xreg_kernel(TaskTable tt, const
 // distinct banks).  Requires the slice-row byte ranges to be 16 B aligned:
 // cols % 256 == 0 and a 16 B aligned weight base.  The next row block's
 // loads are issued before the current block is decoded.
-template <int FMT, int R, int S, int NW, int D, int XK>
+// EP = 1 (S = 1, R = 1, NW = 16, two tasks of equal rows: gate, up): a row
+// block is 8 rows of both tasks, teams 0-7 the gate rows and 8-15 the same
+// up rows, and the block stores f = silu(gate.x) * (up.x) into the first
+// task's y (the expression of silu_mul_kernel), so the down projection reads
+// f as a plain vector.
+template <int FMT, int R, int S, int NW, int D, int XK, int EP = 0>
 __global__ __launch_bounds__(NW * 64) void gemv_stream_kernel(TaskTable tt, const float* __restrict__ x,
                                                                uint32_t cols, uint32_t total_blocks, XPrologue pro) {
+    static_assert(EP == 0 || (S == 1 && R == 1 && NW == 16), "the SiLU pair epilogue takes one row per wave");
     constexpr int DW = FMT == kQ8_0 ? 17 : 9;
     constexpr int NT = NW * 64;
     constexpr int TEAMS = NW / S;
@@ -300,9 +306,14 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_kernel(TaskTable tt, cons
     float* xs = reinterpret_cast<float*>(lds);
 
     auto locate = [&](uint32_t blk, const uint8_t*(&rowp)[R], uint32_t& row0, int& ti) {
-        ti = find_task(tt, blk);
+        if constexpr (EP == 1) {
+            ti = team >> 3;
+            row0 = blk * 8 + (team & 7);
+        } else {
+            ti = find_task(tt, blk);
+            row0 = (blk - tt.group_start[ti]) * (TEAMS * R) + team * R;
+        }
         const GemvTask& t = tt.t[ti];
-        row0 = (blk - tt.group_start[ti]) * (TEAMS * R) + team * R;
 #pragma unroll
         for (int r = 0; r < R; ++r)
             rowp[r] = t.w + (size_t)min(row0 + r, t.rows - 1) * rb + (size_t)(np ? p0 : 0) * DW * 4;
@@ -451,7 +462,16 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_kernel(TaskTable tt, cons
                     acc[r] = wave_sum(acc[r]);
                 }
                 const GemvTask& t = tt.t[ti];
-                if constexpr (S == 1) {
+                if constexpr (EP == 1) {
+                    // gate (teams 0-7) and up (teams 8-15) of the same 8 rows
+                    if (lane == 0) red[parity][wave][0] = acc[0];
+                    __syncthreads();
+                    if (wave < 8 && lane == 0 && row0 < t.rows) {
+                        const float g = red[parity][wave][0], u = red[parity][wave + 8][0];
+                        t.y[row0] = g / (1.0f + expf(-g)) * u;
+                    }
+                    parity ^= 1;
+                } else if constexpr (S == 1) {
 #pragma unroll
                     for (int r = 0; r < R; ++r)
                         if (lane == r && row0 + r < t.rows) t.y[row0 + r] = acc[r];
@@ -1369,7 +1389,7 @@ int cu_count() {
 // Workgroups per CU of the x-in-registers kernel.
 constexpr int kXregWgPerCu = 4;
 
-template <int FMT, int R, int S, int NW, int D, int XK = kXPlain>
+template <int FMT, int R, int S, int NW, int D, int XK = kXPlain, int EP = 0>
 hipError_t launch_stream(TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream,
                          const XPrologue& pro = XPrologue{}) {
     constexpr uint32_t RB = (NW / S) * R;
@@ -1379,20 +1399,21 @@ hipError_t launch_stream(TaskTable& tt, const float* x, uint32_t cols, hipStream
         tt.group_start[i] = blocks;
         blocks += (tt.t[i].rows + RB - 1) / RB;
     }
+    if (EP == 1) blocks = (tt.t[0].rows + 7) / 8;  // 8 rows of each task per block
     tt.group_start[tt.count] = blocks;
     size_t lds = size_t(NW) * R * 64 * DW * 4;
     if (S == 1 || NW > S) lds = std::max(lds, size_t(cols >> 6) * kPadStride * sizeof(float));
     if (lds > lds_limit()) return hipErrorInvalidConfiguration;
     static const int resident = [lds] {
         int n = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_stream_kernel<FMT, R, S, NW, D, XK>, NW * 64, lds) !=
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_stream_kernel<FMT, R, S, NW, D, XK, EP>, NW * 64, lds) !=
                 hipSuccess || n < 1)
             n = 1;
         return n;
     }();
     const uint32_t grid = std::min<uint32_t>(blocks, uint32_t(cu_count() * (NW == 16 ? 1 : resident)));
-    hipLaunchKernelGGL((gemv_stream_kernel<FMT, R, S, NW, D, XK>), dim3(grid), dim3(NW * 64), lds, stream, tt, x, cols,
-                       blocks, pro);
+    hipLaunchKernelGGL((gemv_stream_kernel<FMT, R, S, NW, D, XK, EP>), dim3(grid), dim3(NW * 64), lds, stream, tt, x,
+                       cols, blocks, pro);
     return hipGetLastError();
 }
 // One workgroup of 16 waves per CU, one row block prefetched (D = 1): the
@@ -1734,6 +1755,24 @@ hipError_t launch_gemv_prologue(int fmt, const GemvTask* tasks, int count, const
                             : launch_prologue_s<kQ4_0, kSiluMul>(tt, c, pro, stream);
     return fmt == kQ8_0 ? launch_prologue_s<kQ8_0, kAddNorm>(tt, c, pro, stream)
                         : launch_prologue_s<kQ4_0, kAddNorm>(tt, c, pro, stream);
+}
+
+hipError_t launch_gemv_prologue_silu_pair(int fmt, const GemvTask& gate, const GemvTask& up, const XPrologue& pro,
+                                          size_t cols, hipStream_t stream) {
+    if (!row_bytes(fmt, cols) || !pro.a || !gate.w || !gate.y || !up.w || !gate.rows) return hipErrorInvalidValue;
+    if ((fmt != kQ8_0 && fmt != kQ4_0) || cols % 256 || cols / 64 > 64 || up.rows != gate.rows)
+        return hipErrorInvalidConfiguration;
+    auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    if (!a16(pro.a) || !a16(pro.b) || !a16(pro.w) || !a16(pro.r_out) || !a16(gate.w) || !a16(up.w))
+        return hipErrorInvalidConfiguration;
+    if (pro.kind != kAddNorm || !pro.w) return hipErrorInvalidValue;
+    TaskTable tt{};
+    tt.count = 2;
+    tt.t[0] = gate;
+    tt.t[1] = GemvTask{up.w, gate.y, up.rows};
+    const uint32_t c = static_cast<uint32_t>(cols);
+    return fmt == kQ8_0 ? launch_stream<kQ8_0, 1, 1, 16, 1, kAddNorm, 1>(tt, nullptr, c, stream, pro)
+                        : launch_stream<kQ4_0, 1, 1, 16, 1, kAddNorm, 1>(tt, nullptr, c, stream, pro);
 }
 
 }  // namespace zq

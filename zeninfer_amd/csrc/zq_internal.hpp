@@ -45,6 +45,11 @@ constexpr int kXPlain = 0, kSiluMul = 1, kAddNorm = 2;
 // kernels instead.
 hipError_t launch_gemv_prologue(int fmt, const GemvTask* tasks, int count, const XPrologue& pro, size_t cols,
                                 hipStream_t stream);
+// gate|up with the add+RMSNorm prologue that stores f = silu(gate.x) *
+// (up.x) into gate.y (up.y unused): Q8_0 / Q4_0, cols % 256 == 0 and
+// cols <= 4096, equal rows; hipErrorInvalidConfiguration otherwise.
+hipError_t launch_gemv_prologue_silu_pair(int fmt, const GemvTask& gate, const GemvTask& up, const XPrologue& pro,
+                                          size_t cols, hipStream_t stream);
 
 // Per-32-element activation quantiser (int8 + fp32 scale per block).
 hipError_t launch_quantize_acts(const float* X, int8_t* xq, float* xs, size_t M, size_t K,

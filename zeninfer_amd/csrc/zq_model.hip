@@ -452,11 +452,23 @@ hipError_t enqueue_decode_fused(zq_model& m) {
         HIPCHK(zq::launch_gemv(L.o.fmt, &to, 1, m.att, QW, m.stream));
         zq::GemvTask tg[2] = {{L.gate.p, m.gate, F}, {L.up.p, m.up, F}};
         const zq::XPrologue pg{zq::kAddNorm, r, m.tmp, L.ffn_norm, ralt, c.rms_epsilon};
-        HIPCHK(zq::launch_gemv_prologue(L.gate.fmt, tg, 2, pg, E, m.stream));
-        std::swap(r, ralt);
         zq::GemvTask td = {L.down.p, m.tmp, E};
-        const zq::XPrologue pd{zq::kSiluMul, m.gate, m.up, nullptr, nullptr, 0.0f};
-        HIPCHK(zq::launch_gemv_prologue(L.down.fmt, &td, 1, pd, F, m.stream));
+        // gate|up storing silu(gate)*up itself, then a plain down GEMV; where
+        // that form does not apply, gate|up and a down GEMV with the SiLU*up
+        // prologue
+        const hipError_t ep = L.gate.fmt == L.up.fmt
+                                  ? zq::launch_gemv_prologue_silu_pair(L.gate.fmt, tg[0], tg[1], pg, E, m.stream)
+                                  : hipErrorInvalidConfiguration;
+        if (ep == hipSuccess) {
+            std::swap(r, ralt);
+            HIPCHK(zq::launch_gemv(L.down.fmt, &td, 1, m.gate, F, m.stream));
+        } else {
+            if (ep != hipErrorInvalidConfiguration) return ep;
+            HIPCHK(zq::launch_gemv_prologue(L.gate.fmt, tg, 2, pg, E, m.stream));
+            std::swap(r, ralt);
+            const zq::XPrologue pd{zq::kSiluMul, m.gate, m.up, nullptr, nullptr, 0.0f};
+            HIPCHK(zq::launch_gemv_prologue(L.down.fmt, &td, 1, pd, F, m.stream));
+        }
         delta = m.tmp;
     }
     zq::GemvTask th = {m.out.p, m.logits, c.vocab};
