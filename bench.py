@@ -700,7 +700,7 @@ def main():
                    "frac_hbm_peak_step": round(value / HBM_PEAK_GBS, 4), "graph_matches_eager": graph_ok},
         "roofline": {"bound": "hbm", "achieved": round(down_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(down_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-                     "kernel": "gemv_stream_kernel<Q8_0> (4 column slices x 16 waves) at 4096x14336, the down projection",
+                     "kernel": "gemv_mfma_kernel<Q8_0> (int8 MFMA on the exact digit split of x) at 4096x14336, the down projection",
                      "avg_launch_us": round(down_ms * 1e3, 2), "algorithmic_bytes_per_launch": down_bytes,
                      "read_ceiling": {"us": round(read_ms * 1e3, 2), "GB/s": round(read_gbs, 1),
                                       "frac": round(read_gbs / HBM_PEAK_GBS, 4),
