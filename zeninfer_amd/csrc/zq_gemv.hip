@@ -1047,12 +1047,12 @@ __global__ __launch_bounds__(kThreads) void gemv_block_kernel(TaskTable tt, cons
 // every output NaN.
 //
 // Work split: a wave owns a slice of 16 pairs (1024 columns) for the whole
-// kernel -- its digits stay in 16 VGPRs -- and each row block it streams 4
-// rows x 16 pairs (coalesced 16 B loads, stashed through LDS at a row stride
-// that makes the lane reads conflict-free), so S = ceil(pairs / 16) waves
-// cover a row and TEAMS = 16 / S teams of S waves share a workgroup
-// (4 x TEAMS rows per row block).  The S partial sums of a row are added
-// through LDS in slice order.
+// kernel -- its digits stay in 16 VGPRs -- and each row block it streams
+// ROWS = 4 (Q8_0) or 8 (Q4_0) rows x 16 pairs (coalesced 16 B loads, stashed
+// through LDS at a row stride that makes the lane reads conflict-free), so
+// S = ceil(pairs / 16) waves cover a row and TEAMS = 16 / S teams of S waves
+// share a workgroup (ROWS x TEAMS rows per row block).  The S partial sums
+// of a row are added through LDS in slice order.
 typedef int v4i __attribute__((ext_vector_type(4)));
 constexpr int kMfmaPairs = 16;  // pairs per slice
 template <int FMT>
@@ -1060,8 +1060,13 @@ struct MfmaGeo {
     static constexpr int DW = FMT == kQ8_0 ? 17 : 9;       // dwords per pair
     static constexpr int UPR = kMfmaPairs * DW / 4;         // 16 B units per row segment (68 / 36)
     static constexpr int WROW = FMT == kQ8_0 ? 280 : 152;  // LDS dwords per stashed row (bank-conflict-free reads)
-    static constexpr int WBUF = 4 * WROW;                   // dwords per wave stash
-    static constexpr int NU = (4 * UPR + 63) / 64;          // 16 B loads per lane per row block
+    // 4-row groups per wave step: Q4_0's 4 rows are half of Q8_0's bytes, and
+    // a step's cost is mostly its latency chain (stash, MFMAs, sums,
+    // barrier), so Q4_0 takes two groups per step
+    static constexpr int RG = FMT == kQ8_0 ? 1 : 2;
+    static constexpr int ROWS = 4 * RG;                     // rows per wave step
+    static constexpr int WBUF = ROWS * WROW;                // dwords per wave stash
+    static constexpr int NU = (ROWS * UPR + 63) / 64;       // 16 B loads per lane per row block
 };
 
 template <int FMT, int XPT, int D, int XK>
@@ -1073,7 +1078,7 @@ __global__ __launch_bounds__(1024) void gemv_mfma_kernel(TaskTable tt, const flo
     extern __shared__ uint32_t lds[];
     // LDS map: [0, NW*WBUF) weight stashes; then the digits (S*16 pairs x 68
     // dwords: 16 float4 x 4 digits, 4 dwords of padding); then the pair
-    // exponents; then the partial sums [2][NW][4 rows][4 lane groups].
+    // exponents; then the partial sums [2][NW][ROWS][4 lane groups].
     const uint32_t NW = S * TEAMS, NT = NW * 64;
     const uint32_t pairs = cols >> 6;
     const uint32_t spairs = S * kMfmaPairs;                 // pairs incl. the last slice's padding
@@ -1110,7 +1115,7 @@ __global__ __launch_bounds__(1024) void gemv_mfma_kernel(TaskTable tt, const flo
     auto locate = [&](uint32_t blk, uint32_t& row0, int& ti) {
         // wave-uniform, so the task table is read with scalar loads
         ti = __builtin_amdgcn_readfirstlane(find_task(tt, blk));
-        row0 = __builtin_amdgcn_readfirstlane((blk - tt.group_start[ti]) * (TEAMS * 4) + team * 4);
+        row0 = __builtin_amdgcn_readfirstlane((blk - tt.group_start[ti]) * (TEAMS * G::ROWS) + team * G::ROWS);
     };
     auto load = [&](uint32_t row0, int ti, uint4 (&u)[G::NU]) {
         const GemvTask& t = tt.t[ti];
@@ -1120,7 +1125,7 @@ __global__ __launch_bounds__(1024) void gemv_mfma_kernel(TaskTable tt, const flo
             const uint32_t unit = uint32_t(lane + 64 * m);
             const uint32_t i = unit / G::UPR, o = unit - i * G::UPR;
             const uint32_t row = min(row0 + i, t.rows - 1);
-            const uint32_t off = (i < 4 && 16 * o < seg) ? row * rb + p0 * DW * 4 + 16 * o : 0xFFFFFFF0u;
+            const uint32_t off = (i < G::ROWS && 16 * o < seg) ? row * rb + p0 * DW * 4 + 16 * o : 0xFFFFFFF0u;
             u[m] = span_load16(rs, off);
         }
     };
@@ -1129,7 +1134,7 @@ __global__ __launch_bounds__(1024) void gemv_mfma_kernel(TaskTable tt, const flo
         for (int m = 0; m < G::NU; ++m) {
             const uint32_t unit = uint32_t(lane + 64 * m);
             const uint32_t i = unit / G::UPR, o = unit - i * G::UPR;
-            if (i < 4) reinterpret_cast<uint4*>(buf + i * G::WROW)[o] = u[m];
+            if (i < G::ROWS) reinterpret_cast<uint4*>(buf + i * G::WROW)[o] = u[m];
         }
     };
     uint32_t blk = blockIdx.x;
@@ -1222,18 +1227,18 @@ __global__ __launch_bounds__(1024) void gemv_mfma_kernel(TaskTable tt, const flo
         for (int e = 0; e < 16; ++e) dig[e] = int(src[4 * e]);
     }
     const int fexp = 8 * qi - sexp[p0 + qb];
-    // Q4_0: the codes enter the MFMA as n (0..15); the -8 offset is the C
-    // operand's start, -8 * (sum of the block's digits)
-    v4i c0 = {0, 0, 0, 0}, c1 = {0, 0, 0, 0};
+    // Q4_0: the codes enter the MFMA as n (0..15); the -8 offset is added to
+    // each block's dot as -8 * (sum of the block's digits), one per lane
+    // (the lane's digit column is the same for its 4 rows)
+    int o0 = 0, o1 = 0;
     if constexpr (FMT == kQ4_0) {
-        int s0 = 0, s1 = 0;
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
-            s0 = __builtin_amdgcn_sdot4(dig[t], 0x01010101, s0, false);
-            s1 = __builtin_amdgcn_sdot4(dig[8 + t], 0x01010101, s1, false);
+            o0 = __builtin_amdgcn_sdot4(dig[t], 0x01010101, o0, false);
+            o1 = __builtin_amdgcn_sdot4(dig[8 + t], 0x01010101, o1, false);
         }
-        c0 = v4i{-8 * s0, -8 * s0, -8 * s0, -8 * s0};
-        c1 = v4i{-8 * s1, -8 * s1, -8 * s1, -8 * s1};
+        o0 *= -8;
+        o1 *= -8;
     }
 
     int parity = 0;
@@ -1251,68 +1256,73 @@ __global__ __launch_bounds__(1024) void gemv_mfma_kernel(TaskTable tt, const flo
             locate(nblk, row0s[d], tis[d]);
             load(row0s[d], tis[d], u[d]);
         }
-        const uint32_t* pr = buf + qi * G::WROW + qb * DW;  // A: row qi, pair qb
-        uint32_t q[DW];
+        float* rp = red + parity * (16 * 16 * G::RG);
 #pragma unroll
-        for (int k = 0; k < DW; ++k) q[k] = pr[k];
-        // scales of rows 0..3 of pair qb, read with the operands: d0 in the
-        // low half of dword 0, d1 in the high half of dword 8 (Q8_0) / 4 (Q4_0)
-        uint32_t sw0[4], sw1[4];
+        for (int g = 0; g < G::RG; ++g) {
+            const uint32_t* gb = buf + 4 * g * G::WROW;
+            const uint32_t* pr = gb + qi * G::WROW + qb * DW;  // A: row 4g + qi, pair qb
+            uint32_t q[DW];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t* pi = buf + i * G::WROW + qb * DW;
-            sw0[i] = pi[0];
-            sw1[i] = pi[FMT == kQ8_0 ? 8 : 4];
-        }
-        // two accumulation chains per block (K slices 0-3 and 4-7), so
-        // dependent MFMAs are four deep instead of eight
-        v4i e0 = c0, e1 = c1, f0 = {0, 0, 0, 0}, f1 = {0, 0, 0, 0};
+            for (int k = 0; k < DW; ++k) q[k] = pr[k];
+            // scales of rows 0..3 of pair qb, read with the operands: d0 in the
+            // low half of dword 0, d1 in the high half of dword 8 (Q8_0) / 4 (Q4_0)
+            uint32_t sw0[4], sw1[4];
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            int a0, a1;
-            if constexpr (FMT == kQ8_0) {
-                a0 = int(__builtin_amdgcn_alignbyte(q[t + 1], q[t], 2));
-                a1 = int(q[9 + t]);
-            } else {
-                const uint32_t w0 = __builtin_amdgcn_alignbyte(q[(t & 3) + 1], q[t & 3], 2);
-                a0 = int((t < 4 ? w0 : w0 >> 4) & 0x0F0F0F0Fu);
-                a1 = int((t < 4 ? q[5 + t] : q[1 + t] >> 4) & 0x0F0F0F0Fu);
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t* pi = gb + i * G::WROW + qb * DW;
+                sw0[i] = pi[0];
+                sw1[i] = pi[FMT == kQ8_0 ? 8 : 4];
             }
-            if (t < 4) {
-                e0 = __builtin_amdgcn_mfma_i32_4x4x4i8(a0, dig[t], e0, 0, 0, 0);
-                e1 = __builtin_amdgcn_mfma_i32_4x4x4i8(a1, dig[8 + t], e1, 0, 0, 0);
-            } else {
-                f0 = __builtin_amdgcn_mfma_i32_4x4x4i8(a0, dig[t], f0, 0, 0, 0);
-                f1 = __builtin_amdgcn_mfma_i32_4x4x4i8(a1, dig[8 + t], f1, 0, 0, 0);
+            // two accumulation chains per block (K slices 0-3 and 4-7), so
+            // dependent MFMAs are four deep instead of eight
+            v4i e0 = {0, 0, 0, 0}, e1 = {0, 0, 0, 0}, f0 = {0, 0, 0, 0}, f1 = {0, 0, 0, 0};
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                int a0, a1;
+                if constexpr (FMT == kQ8_0) {
+                    a0 = int(__builtin_amdgcn_alignbyte(q[t + 1], q[t], 2));
+                    a1 = int(q[9 + t]);
+                } else {
+                    const uint32_t w0 = __builtin_amdgcn_alignbyte(q[(t & 3) + 1], q[t & 3], 2);
+                    a0 = int((t < 4 ? w0 : w0 >> 4) & 0x0F0F0F0Fu);
+                    a1 = int((t < 4 ? q[5 + t] : q[1 + t] >> 4) & 0x0F0F0F0Fu);
+                }
+                if (t < 4) {
+                    e0 = __builtin_amdgcn_mfma_i32_4x4x4i8(a0, dig[t], e0, 0, 0, 0);
+                    e1 = __builtin_amdgcn_mfma_i32_4x4x4i8(a1, dig[8 + t], e1, 0, 0, 0);
+                } else {
+                    f0 = __builtin_amdgcn_mfma_i32_4x4x4i8(a0, dig[t], f0, 0, 0, 0);
+                    f1 = __builtin_amdgcn_mfma_i32_4x4x4i8(a1, dig[8 + t], f1, 0, 0, 0);
+                }
             }
-        }
-        float acc[4];
+            float acc[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            float a = float(e0[i] + f0[i]) * float(__builtin_bit_cast(_Float16, uint16_t(sw0[i])));
-            a = fmaf(float(e1[i] + f1[i]), float(__builtin_bit_cast(_Float16, uint16_t(sw1[i] >> 16))), a);
-            acc[i] = ldexpf(a, fexp);
-        }
-        // sum over the 4 digits (quad), then each lane keeps row (lane & 3)
-        // and sums its 16-lane row's 4 quads; lanes 16g + i then hold row i's
-        // sum over the pairs 4g .. 4g+3
+            for (int i = 0; i < 4; ++i) {
+                float a = float(e0[i] + f0[i] + o0) * float(__builtin_bit_cast(_Float16, uint16_t(sw0[i])));
+                a = fmaf(float(e1[i] + f1[i] + o1), float(__builtin_bit_cast(_Float16, uint16_t(sw1[i] >> 16))), a);
+                acc[i] = ldexpf(a, fexp);
+            }
+            // sum over the 4 digits (quad), then each lane keeps row (lane & 3)
+            // and sums its 16-lane row's 4 quads; lanes 16g' + i then hold row
+            // i's sum over the pairs 4g' .. 4g'+3
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            acc[i] += dpp_f<kDppXor1>(acc[i]);
-            acc[i] += dpp_f<kDppXor2>(acc[i]);
+            for (int i = 0; i < 4; ++i) {
+                acc[i] += dpp_f<kDppXor1>(acc[i]);
+                acc[i] += dpp_f<kDppXor2>(acc[i]);
+            }
+            float v = qi == 0 ? acc[0] : qi == 1 ? acc[1] : qi == 2 ? acc[2] : acc[3];
+            v += dpp_f<0x124>(v);  // row_ror:4
+            v += dpp_f<0x128>(v);  // row_ror:8
+            if ((lane & 15) < 4) rp[(wave * G::RG + g) * 16 + qi * 4 + (lane >> 4)] = v;
         }
-        float v = qi == 0 ? acc[0] : qi == 1 ? acc[1] : qi == 2 ? acc[2] : acc[3];
-        v += dpp_f<0x124>(v);  // row_ror:4
-        v += dpp_f<0x128>(v);  // row_ror:8
-        float* rp = red + parity * (16 * 16);
-        if ((lane & 15) < 4) rp[wave * 16 + qi * 4 + (lane >> 4)] = v;
         __syncthreads();
-        if (slice == 0 && lane < 4) {
+        if (slice == 0 && lane < G::ROWS) {
             // slice order; every load issued before the adds
+            const uint32_t g = lane >> 2, r = lane & 3;
             float4 w[16];
 #pragma unroll
             for (uint32_t s2 = 0; s2 < 16; ++s2)
-                if (s2 < S) w[s2] = *reinterpret_cast<const float4*>(rp + (team * S + s2) * 16 + lane * 4);
+                if (s2 < S) w[s2] = *reinterpret_cast<const float4*>(rp + ((team * S + s2) * G::RG + g) * 16 + r * 4);
             float s = 0.0f;
 #pragma unroll
             for (uint32_t s2 = 0; s2 < 16; ++s2)
@@ -1441,7 +1451,7 @@ hipError_t launch_mfma(TaskTable& tt, const float* x, uint32_t cols, hipStream_t
     const uint32_t pairs = cols >> 6;
     const uint32_t S = (pairs + kMfmaPairs - 1) / kMfmaPairs;
     if (!S || S > 16) return hipErrorInvalidConfiguration;
-    const uint32_t TEAMS = 16 / S, NW = S * TEAMS, RB = 4 * TEAMS;
+    const uint32_t TEAMS = 16 / S, NW = S * TEAMS, RB = G::ROWS * TEAMS;
     const size_t rb = size_t(pairs) * G::DW * 4;
     uint32_t blocks = 0;
     for (int i = 0; i < tt.count; ++i) {
@@ -1450,7 +1460,7 @@ hipError_t launch_mfma(TaskTable& tt, const float* x, uint32_t cols, hipStream_t
         blocks += (tt.t[i].rows + RB - 1) / RB;
     }
     tt.group_start[tt.count] = blocks;
-    const size_t lds = (size_t(NW) * G::WBUF + size_t(S) * kMfmaPairs * 69 + 512) * 4;
+    const size_t lds = (size_t(NW) * G::WBUF + size_t(S) * kMfmaPairs * 69 + 512 * G::RG) * 4;
     if (lds > lds_limit()) return hipErrorInvalidConfiguration;
     const uint32_t grid = std::min<uint32_t>(blocks, uint32_t(cu_count()));
     const uint32_t xpt = (S * kMfmaPairs * 16 + NW * 64 - 1) / (NW * 64);  // float4 per thread, padded pairs included
@@ -1469,9 +1479,10 @@ hipError_t launch_mfma(TaskTable& tt, const float* x, uint32_t cols, hipStream_t
 // (down 4096x14336: 15.0 -> 13.6 us; lm_head 128256x4096: 88.5 -> 80.6 us)
 // and loses a little on short launches of 4096-column rows (q/o 6.1 -> 7.1
 // us, gate|up 13.8 -> 14.1 us), whose fixed costs (the digit split, one more
-// barrier) are not amortised.  Q4_0 gains only on long rows (4096x14336 11.6
-// -> 11.4 us) and loses on vocabulary-sized outputs (64.2 -> 69.6 us): its
-// pair holds twice the elements per byte, so twice the MFMAs per byte.  ZQ_GEMV_MFMA=0 / 1 forces the fp32-FMA / MFMA
+// barrier) are not amortised.  Q4_0, with two 4-row groups per wave step,
+// wins from 8192 rows on (14336x4096 10.7 -> 10.4 us, 4096x14336 11.7 ->
+// 10.5 us, 128256x4096 64.4 -> 54.0 us) and loses on one-block launches
+// (4096x4096 4.7 -> 6.8 us).  ZQ_GEMV_MFMA=0 / 1 forces the fp32-FMA / MFMA
 // kernel everywhere (A/B runs).
 // With an x prologue the SiLU*up form measured slower on the MFMA kernel
 // (the down projection of the decoder: 15.3 -> 15.9 us), the add+RMSNorm
@@ -1486,7 +1497,8 @@ int mfma_gemv_forced() {
 bool mfma_gemv_for(int fmt, uint32_t cols, uint32_t total_rows, int xk = kXPlain) {
     if (mfma_gemv_forced() >= 0) return mfma_gemv_forced() == 1;
     const bool vocab = fmt == kQ8_0 && total_rows >= 32768;
-    return xk == kXPlain ? cols > 4096 || vocab : xk == kAddNorm && vocab;
+    const bool tall = fmt == kQ4_0 && total_rows >= 8192;
+    return xk == kXPlain ? cols > 4096 || vocab || tall : xk == kAddNorm && vocab;
 }
 
 template <int FMT, int R, int S>
