@@ -373,12 +373,15 @@ def format_sweep(torch, zq, dev):
     distinct replicas (>= 320 MB) that no launch reads from the MALL.  The
     GEMM uses each format's default activations: int8 for Q4_0, fp32 for the
     super-block formats (their only reference routes), reported against the
-    int8 or the fp32 MFMA peak.  Also the Q8_0 GEMM M sweep of config 2."""
+    int8 or the fp32 MFMA peak.  Each GEMV is set beside the plain streaming
+    read of the same weight bytes (read_ceiling_us).  Also the Q8_0 GEMM M
+    sweep of config 2."""
     out = {}
     X = torch.empty(512 * FFN, device=dev)
     zq.synth_normal_dev(31, X, 512 * FFN)
     xv = torch.empty(FFN, device=dev)
     zq.synth_normal_dev(32, xv, FFN)
+    sink = torch.empty(zq.read_probe_sink_bytes(), dtype=torch.uint8, device=dev)
     for fname, fmt in (("Q4_0", zq.Q4_0), ("Q6_K", zq.Q6_K), ("Q4_K", zq.Q4_K), ("Q5_K", zq.Q5_K)):
         res = {}
         for shape, N, K in (("gate/up 14336x4096", FFN, HIDDEN), ("down 4096x14336", HIDDEN, FFN)):
@@ -391,7 +394,10 @@ def format_sweep(torch, zq, dev):
                 ws.append(t)
             y = torch.empty(N, device=dev)
             ms = timed_launches_on(torch, lambda i: zq.gemv_dev(fmt, ws[i % nrep], xv[:K], y, N, K), 4 * nrep, nrep)
-            entry = {"gemv_us": round(ms * 1e3, 2), "gemv_GB_s": round(gemv_bytes(rb, N, K) / (ms * 1e-3) / 1e9, 1)}
+            # the same weight bytes read by the plain streaming-read probe, same timing
+            rms = timed_launches_on(torch, lambda i: zq.read_probe_dev(ws[i % nrep], N * rb, sink), 4 * nrep, nrep)
+            entry = {"gemv_us": round(ms * 1e3, 2), "gemv_GB_s": round(gemv_bytes(rb, N, K) / (ms * 1e-3) / 1e9, 1),
+                     "read_ceiling_us": round(rms * 1e3, 2), "frac_of_read_ceiling": round(rms / ms, 4)}
             act = zq.ACT_INT8 if fmt == zq.Q4_0 else zq.ACT_F32
             wsb = zq.gemm_workspace_bytes(fmt, 512, N, K, act)
             wsp = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
