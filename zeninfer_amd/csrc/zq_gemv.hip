@@ -1428,10 +1428,15 @@ hipError_t launch_stream(TaskTable& tt, const float* x, uint32_t cols, hipStream
 }
 // One workgroup of 16 waves per CU, one row block prefetched (D = 1): the
 // steady state already streams at ~6.9 TB/s on MI355X; deeper register rings
-// (8 waves x 2-3 blocks, 16 waves x 2 blocks) measured slower.
+// (8 waves x 2-3 blocks, 16 waves x 2 blocks) measured slower.  Outputs of at
+// most 2048 rows with one slice per row take 8-wave workgroups, two per CU
+// (Q8_0 1024x4096: 4.9 -> 4.5 us; 4096x4096 was slower: 5.9 -> 6.5 us).
 template <int FMT, int S>
 hipError_t launch_stream_r(int R, TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream) {
     (void)R;
+    uint32_t rows = 0;
+    for (int i = 0; i < tt.count; ++i) rows += tt.t[i].rows;
+    if (S == 1 && rows <= 2048) return launch_stream<FMT, 1, S, 8, 1>(tt, x, cols, stream);
     return launch_stream<FMT, 1, S, 16, 1>(tt, x, cols, stream);
 }
 template <int FMT>
