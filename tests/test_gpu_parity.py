@@ -118,6 +118,8 @@ GEMV_SHAPES = [
     (O.Q4_K, 33, 8192), (O.Q5_K, 9, 10240), (O.Q4_K, 17, 16384),
     # widths past the streaming kernels' 16384 (fallback kernels)
     (O.Q8_0, 17, 32768), (O.Q4_0, 9, 20480), (O.Q6_K, 5, 24576), (O.Q4_K, 9, 24576), (O.Q5_K, 3, 18432),
+    # Q6_K rows whose x (180 KB) does not fit in LDS: the fallback reads x from global memory
+    (O.Q6_K, 4, 45056),
 ]
 
 

@@ -502,11 +502,13 @@ __global__ __launch_bounds__(NW * 64) void gemv_stream_kernel(TaskTable tt, cons
 
 // ---------------------------------------------------------------- Q6_K ---
 // One lane = one 16-element unit (super-block sb, half h, l-quad l0).
-template <int R>
+// XG: x is read from global memory (rows too long to stage x in LDS).
+template <int R, bool XG = false>
 __global__ __launch_bounds__(kThreads) void gemv_q6k_kernel(TaskTable tt, const float* __restrict__ x,
                                                             uint32_t cols, uint32_t total_groups) {
-    extern __shared__ float xs[];
-    stage_x<false>(xs, x, cols);
+    extern __shared__ float xs_lds[];
+    if constexpr (!XG) stage_x<false>(xs_lds, x, cols);
+    const float* xs = XG ? x : xs_lds;
     const uint32_t nsb = cols >> 8;
     const uint32_t units = nsb * 16;
     const uint32_t rb = nsb * 210;
@@ -1543,8 +1545,11 @@ hipError_t launch_q6k(TaskTable& tt, const float* x, uint32_t cols, hipStream_t 
     }
     tt.group_start[tt.count] = groups;
     const uint32_t blocks = std::min<uint32_t>((groups + kWavesPerBlock - 1) / kWavesPerBlock, 4096u);
-    hipLaunchKernelGGL((gemv_q6k_kernel<R>), dim3(blocks), dim3(kThreads), size_t(cols) * sizeof(float), stream, tt,
-                       x, cols, groups);
+    if (size_t(cols) * sizeof(float) > lds_limit())
+        hipLaunchKernelGGL((gemv_q6k_kernel<R, true>), dim3(blocks), dim3(kThreads), 0, stream, tt, x, cols, groups);
+    else
+        hipLaunchKernelGGL((gemv_q6k_kernel<R>), dim3(blocks), dim3(kThreads), size_t(cols) * sizeof(float), stream, tt,
+                           x, cols, groups);
     return hipGetLastError();
 }
 template <int R, int S, int NW>
@@ -1693,7 +1698,6 @@ hipError_t launch_gemv(int fmt, const GemvTask* tasks, int count, const float* x
             const hipError_t e = launch_q6k_stream_any(tt, x, c, stream, total_rows);
             if (e != hipErrorInvalidConfiguration) return e;
         }
-        if (size_t(c) * 4 > lds_limit()) return hipErrorInvalidValue;
         for (int i = 0; i < count; ++i)
             if (reinterpret_cast<uintptr_t>(tasks[i].w) & 1u) return hipErrorInvalidValue;
         if (R == 4) return launch_q6k<4>(tt, x, c, stream);
