@@ -539,3 +539,43 @@ def test_long_rows_against_exact_product(zq, orc, fmt):
             what = f"{name} fmt={fmt} K={K}: gpu {e_gpu:.2f}, reference {e_ref:.2f} of the bar"
             print(what)
             assert e_gpu <= (1.0 if K == 14336 else max(1.0, e_ref)), what
+
+
+def test_host_api_concurrent_callers(zq, orc):
+    """The reference calls its kernels from several host threads (ComputePool
+    workers and the runtime); the host-pointer entry points serialise on the
+    backend's mutex.  Six threads run GEMVs and GEMMs at once on their own and
+    on shared weights (so uploads and residency lookups interleave), and every
+    result is checked against the oracle."""
+    import threading
+    shapes = [(O.Q8_0, 300, 4096), (O.Q4_0, 257, 2048), (O.Q6_K, 129, 4096), (O.Q4_K, 64, 2048)]
+    weights = [orc.gen_weights(f, 500 + i, r, c) for i, (f, r, c) in enumerate(shapes)]
+    xs = [orc.gen_normal(600 + i, c) for i, (_, _, c) in enumerate(shapes)]
+    Xs = [orc.gen_normal(700 + i, 9 * c) for i, (_, _, c) in enumerate(shapes)]
+    want_v = [orc.gemv_f32(f, w, x, r, c) for (f, r, c), w, x in zip(shapes, weights, xs)]
+    want_m = [orc.gemm_f32(f, w, X, 9, r, c) for (f, r, c), w, X in zip(shapes, weights, Xs)]
+    errors = []
+
+    def worker(t):
+        try:
+            for it in range(12):
+                i = (t + it) % len(shapes)
+                f, r, c = shapes[i]
+                if (t + it) % 3 == 2:
+                    got = zq.gemm(f, weights[i], Xs[i], 9, r, c, zq.ACT_F32)
+                    assert_close(got, want_m[i], f"thread {t} gemm {i}")
+                else:
+                    got = zq.gemv(f, weights[i], xs[i], r, c)
+                    assert_close(got, want_v[i], f"thread {t} gemv {i}")
+        except Exception as e:  # reported by the main thread
+            errors.append(e)
+
+    threads = [threading.Thread(target=worker, args=(t,)) for t in range(6)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join(timeout=120)
+    assert not any(th.is_alive() for th in threads), "a caller did not finish"
+    assert not errors, errors[0]
+    for w in weights:
+        zq.release(w)
