@@ -507,8 +507,8 @@ def main():
         print(json.dumps(model_config4()))
         return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this path has no multi-GPU leg in this build "
-              "(row-sharding design only; see DESIGN.md)", file=sys.stderr)
+        print("bench.py measures one GPU: this build has no multi-GPU leg (the projections would shard "
+              "by weight rows, one process per GPU; that is a design, not code)", file=sys.stderr)
         return 2
 
     import torch
