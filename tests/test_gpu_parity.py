@@ -579,3 +579,39 @@ def test_host_api_concurrent_callers(zq, orc):
     assert not errors, errors[0]
     for w in weights:
         zq.release(w)
+
+
+def test_random_gemv_and_gemm_shapes(zq, orc):
+    """Seeded random shapes through the device entry points: 60 GEMVs (1-3
+    tasks, every format, 32 to 16640 columns, ragged row counts) and 60 GEMMs
+    (both activation routes), each within the fp32 bar of the oracle."""
+    rng = np.random.default_rng(77)
+    fmts = [O.Q8_0, O.Q4_0, O.Q4_K, O.Q5_K, O.Q6_K]
+    for case in range(120):
+        fmt = fmts[case % 5]
+        b = 256 if fmt in (O.Q4_K, O.Q5_K, O.Q6_K) else 32
+        seed = int(rng.integers(1 << 30))
+        if case < 60:
+            cols = b * int(rng.choice([1, 3, 8, 20, 56, 65] if b == 256 else [1, 2, 3, 7, 64, 129, 448, 520]))
+            rows = [int(rng.choice([1, 7, 33, 100, 513, 2049])) for _ in range(int(rng.choice([1, 1, 2, 3])))]
+            ws = [orc.gen_weights(fmt, seed + i, r, cols) for i, r in enumerate(rows)]
+            x = orc.gen_normal(seed + 9, cols)
+            ys = [torch.empty(r, device=DEV) for r in rows]
+            tasks = [(dev_weights(zq, fmt, w, r, cols), y, r) for w, y, r in zip(ws, ys, rows)]
+            zq.gemv_batch_dev(fmt, to_dev(x), tasks, cols)
+            torch.cuda.synchronize()
+            for w, y, r in zip(ws, ys, rows):
+                assert_close(y.cpu().numpy(), orc.gemv_f32(fmt, w, x, r, cols), f"gemv fmt={fmt} {rows}x{cols}")
+        else:
+            K = b * int(rng.choice([1, 4, 16]) if b == 256 else rng.choice([2, 8, 64, 130]))
+            M, N = int(rng.choice([1, 17, 33, 64, 130])), int(rng.choice([7, 32, 129, 300]))
+            act = zq.ACT_INT8 if fmt in (O.Q8_0, O.Q4_0) and K % 64 == 0 and rng.random() < 0.5 else zq.ACT_F32
+            w = orc.gen_weights(fmt, seed, N, K)
+            X = orc.gen_normal(seed + 9, M * K)
+            Y = torch.empty(M * N, device=DEV)
+            wsb = zq.gemm_workspace_bytes(fmt, M, N, K, act)
+            wsp = torch.empty(max(wsb, 1), dtype=torch.uint8, device=DEV)
+            zq.gemm_dev(fmt, dev_weights(zq, fmt, w, N, K), to_dev(X), Y, M, N, K, act, wsp, wsb)
+            torch.cuda.synchronize()
+            want = orc.gemm_i8(fmt, w, X, M, N, K) if act == zq.ACT_INT8 else orc.gemm_f32(fmt, w, X, M, N, K)
+            assert_close(Y.cpu().numpy(), want, f"gemm fmt={fmt} act={act} M={M} N={N} K={K}")

@@ -372,3 +372,47 @@ def test_other_formats_match_reference(tmp_path, zq, ptype, down, out):
     assert ours == theirs
     m.close()
     ref.close()
+
+
+def test_random_decoder_shapes_match_reference(tmp_path, zq):
+    """Twelve seeded random llama configurations (head dim 64 / 128 / 256,
+    1-8 query heads over 1-8 kv heads, partial RoPE, FFN and vocabulary sizes
+    off the usual multiples, every projection format including Q6_K
+    ffn_down / output beside Q4_K / Q5_K, prompts of 1-70 tokens): fp32
+    prefill and three decode steps within the fp32 bar of the reference."""
+    if not os.path.exists(REF_LIB):
+        pytest.skip("oracle/_ref not built")
+    from oracle.oracle import ReferenceModel
+    from zeninfer_amd.model import Model, PREFILL_F32
+    rng = np.random.default_rng(2024)
+    done = 0
+    while done < 12:
+        hd = int(rng.choice([64, 128, 256]))
+        heads = int(rng.choice([1, 2, 4, 6, 8]))
+        kv = int(rng.choice([d for d in (1, 2, 3, 4, 8) if heads % d == 0]))
+        emb = hd * heads
+        if emb % 256 or emb > 2048:
+            continue
+        pt = int(rng.choice([G.GGML_Q8_0, G.GGML_Q4_0, G.GGML_Q4_K, G.GGML_Q5_K, G.GGML_Q6_K]))
+        down = G.GGML_Q6_K if pt in (G.GGML_Q4_K, G.GGML_Q5_K) and rng.random() < 0.5 else None
+        shape = G.LlamaShape(embedding=emb, layers=int(rng.choice([1, 2])), heads=heads, kv_heads=kv,
+                             ffn=int(rng.choice([256, 768, 1536, 2816])), vocab=int(rng.choice([300, 1000, 2051])),
+                             context=512, rope_dim=int(rng.choice([0, hd // 2])))
+        prompt = [int(t) for t in rng.integers(3, shape.vocab, size=int(rng.choice([1, 7, 33, 70])))]
+        path = tmp_path / f"r{done}.gguf"
+        G.synthetic_llama(path, shape, seed=int(rng.integers(1 << 30)), proj_type=pt, down_type=down, out_type=down)
+        what = f"{shape} type {pt}/{down} prompt {len(prompt)}"
+        ref = ReferenceModel(path)
+        m = Model.from_gguf(G.GGUFFile(path), max_positions=128)
+        m.set_prefill_mode(PREFILL_F32)
+        tok, lg = m.prefill(prompt)
+        ok, err, scale = close_to(lg, ref.prefill(prompt, capacity=128), 1e-4)
+        assert ok, (what, "prefill", err, scale)
+        for step in range(3):
+            nxt, lg = m.decode(tok)
+            ok, err, scale = close_to(lg, ref.step(tok, len(prompt) + step), 1e-4)
+            assert ok, (what, "decode", step, err, scale)
+            tok = nxt
+        m.close()
+        ref.close()
+        done += 1
