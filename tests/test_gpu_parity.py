@@ -201,6 +201,59 @@ print('ok')
     assert r.returncode == 0 and "ok" in r.stdout, r.stdout + r.stderr
 
 
+def test_residency_budget_eviction_within_a_call(zq, orc):
+    """Calls that read several host weights resolve all of them before any
+    launch.  With the residency budget lowered to about 2.7 weights: a batch
+    whose upload evicts a tensor it resolved earlier is re-resolved and still
+    matches the oracle; a batch, FFN or GEMM batch whose weights cannot be
+    resident together, and a batch that names one address with two shapes,
+    are declined (launching them would read freed device memory), and the
+    library keeps working afterwards."""
+    import subprocess, sys, os
+    code = f"""
+import sys, numpy as np
+sys.path.insert(0, {os.getcwd()!r})
+from oracle import oracle as O
+from zeninfer_amd import zq
+from tests.tolerance import assert_close
+o = O.Oracle(); zq.init(); zq.set_min_elements(0)
+F, R, C = O.Q8_0, 256, 4096
+w = [o.gen_weights(F, 300 + i, R, C) for i in range(3)]
+x = o.gen_normal(9, C)
+ref = [o.gemv_f32(F, wi, x, R, C) for wi in w]
+def declined(fn):
+    try:
+        fn()
+    except zq.ZQError as e:
+        assert e.status == zq.DECLINED, e
+        return True
+    return False
+assert_close(zq.gemv(F, w[0], x, R, C), ref[0], 'single')
+s0 = zq.stats()
+ys = zq.gemv_batch(F, [w[1], w[2]], x, [R, R], C)        # evicts w[0] and w[1] mid-call
+for y, r in zip(ys, ref[1:]):
+    assert_close(y, r, 'batch after eviction')
+assert zq.stats()['evictions'] > s0['evictions']
+assert declined(lambda: zq.gemv_batch(F, w, x, [R, R, R], C))
+assert declined(lambda: zq.gemv_batch(F, [w[1], w[1]], x, [R, R // 2], C))
+ffn_rows = R; down = o.gen_weights(F, 400, C, ffn_rows)
+assert declined(lambda: zq.ffn_gemv(F, w[0], w[1], down, x, ffn_rows, C, C))
+X = o.gen_normal(10, 4 * C)
+assert declined(lambda: zq.gemm_batch(F, w, X, 4, [R, R, R], C))
+st = zq.stats()
+assert st['resident_bytes'] <= 3000000, st
+for i in (2, 0, 1):
+    assert_close(zq.gemv(F, w[i], x, R, C), ref[i], f'after declines {{i}}')
+Ys = zq.gemm_batch(F, [w[0], w[1]], X, 4, [R, R], C)
+for wi, Y in zip(w, Ys):
+    assert_close(Y.reshape(4, R), o.gemm_f32(F, wi, X, 4, R, C).reshape(4, R), 'gemm batch')
+print('ok')
+"""
+    env = dict(os.environ, ZQ_HIP_RESIDENT_BUDGET="3000000")
+    r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0 and "ok" in r.stdout, r.stdout + r.stderr
+
+
 def test_gemv_batch_qkv(zq, orc):
     cols = 4096
     rows = [4096, 1024, 1024]

@@ -9,7 +9,8 @@
 // (format, rows, cols) and a different shape at the same address re-uploads
 // (reference contract, include/zen/hip_backend.h:52-58).  When the budget
 // (80% of device memory, as hip_backend.hip:459-475) would be exceeded,
-// every resident tensor is evicted first.
+// every resident tensor is evicted first; a call that reads several weights
+// is declined when they cannot be resident together.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -55,6 +56,7 @@ struct Backend {
     zq_hip_stats stats{};
     hipStream_t stream = nullptr;
     size_t budget = 0;
+    uint64_t frees = 0;  // bumped whenever a resident copy is freed
     size_t min_elements = 262144;
     std::unordered_map<const uint8_t*, Resident> resident;
     // staging
@@ -147,12 +149,17 @@ int init_locked(Backend& b) {
         return ZQ_ERR_NO_DEVICE;
     }
     b.budget = static_cast<size_t>(static_cast<double>(p.totalGlobalMem) * 0.8);
+    if (const char* rb = std::getenv("ZQ_HIP_RESIDENT_BUDGET")) {  // bytes; lower only, to rehearse eviction
+        const size_t v = std::strtoull(rb, nullptr, 10);
+        if (v > 0 && v < b.budget) b.budget = v;
+    }
     if (const char* me = std::getenv("ZEN_HIP_MIN_ELEMENTS")) b.min_elements = std::strtoull(me, nullptr, 10);
     b.initialised = true;
     return ZQ_OK;
 }
 
 void free_resident(Backend& b) {
+    if (!b.resident.empty()) ++b.frees;
     for (auto& kv : b.resident) (void)hipFree(kv.second.dev);
     b.stats.evictions += b.resident.size();
     b.resident.clear();
@@ -169,6 +176,7 @@ int ensure_resident(Backend& b, int fmt, const uint8_t* w, size_t rows, size_t c
             return ZQ_OK;
         }
         (void)hipFree(it->second.dev);
+        ++b.frees;
         b.stats.resident_bytes -= it->second.bytes;
         --b.stats.resident_tensors;
         b.resident.erase(it);
@@ -198,6 +206,41 @@ int ensure_resident(Backend& b, int fmt, const uint8_t* w, size_t rows, size_t c
     b.stats.upload_us += us_since(t0);
     *out = dev;
     return ZQ_OK;
+}
+
+// Device copies of every weight one call reads, resolved before any launch.
+// An upload that would overflow the budget evicts every resident tensor,
+// including ones this call resolved a moment earlier, so a pass that freed
+// anything is repeated, and the second pass must free nothing.  A set whose
+// distinct tensors do not fit the budget together, or one whose second pass
+// still frees (an allocation retried after an eviction, one address given
+// with two shapes), is declined: launching it would read freed memory.
+struct Want {
+    const uint8_t* w;
+    size_t rows, cols;
+};
+int resolve_set(Backend& b, int fmt, const Want* want, size_t n, const uint8_t** out) {
+    size_t need = 0;
+    for (size_t i = 0; i < n; ++i) {
+        bool seen = false;
+        for (size_t j = 0; j < i; ++j) seen = seen || want[j].w == want[i].w;
+        if (!seen) need += want[i].rows * zq::row_bytes(fmt, want[i].cols) + ZQ_WEIGHT_TAIL_PAD;
+    }
+    if (need > b.budget) {
+        ++b.stats.declined;
+        return ZQ_DECLINED;
+    }
+    for (int pass = 0; pass < 2; ++pass) {
+        const uint64_t frees = b.frees;
+        for (size_t i = 0; i < n; ++i) {
+            const int st = ensure_resident(b, fmt, want[i].w, want[i].rows, want[i].cols, &out[i]);
+            if (st == ZQ_DECLINED) ++b.stats.declined;
+            if (st != ZQ_OK) return st;
+        }
+        if (b.frees == frees) return ZQ_OK;
+    }
+    ++b.stats.declined;
+    return ZQ_DECLINED;
 }
 
 int ensure_scratch(Backend& b, size_t dev_bytes, size_t host_bytes) {
@@ -562,14 +605,11 @@ int gemv_batch_locked(Backend& b, int fmt, const float* x, const zq_gemv_task* t
         return ZQ_DECLINED;
     }
     zq::GemvTask dt[zq::kMaxTasks];
-    for (int pass = 0; pass < 2; ++pass)  // a later upload may evict an earlier one: resolve twice
-        for (size_t i = 0; i < count; ++i) {
-            const uint8_t* dw = nullptr;
-            st = ensure_resident(b, fmt, tasks[i].weights, tasks[i].rows, cols, &dw);
-            if (st == ZQ_DECLINED) ++b.stats.declined;
-            if (st != ZQ_OK) return st;
-            dt[i] = zq::GemvTask{dw, nullptr, static_cast<uint32_t>(tasks[i].rows)};
-        }
+    Want want[zq::kMaxTasks];
+    const uint8_t* dw[zq::kMaxTasks];
+    for (size_t i = 0; i < count; ++i) want[i] = Want{tasks[i].weights, tasks[i].rows, cols};
+    if ((st = resolve_set(b, fmt, want, count, dw)) != ZQ_OK) return st;
+    for (size_t i = 0; i < count; ++i) dt[i] = zq::GemvTask{dw[i], nullptr, static_cast<uint32_t>(tasks[i].rows)};
     const size_t xbytes = align_up(cols * sizeof(float), 256);
     const size_t ybytes = total_rows * sizeof(float);
     st = ensure_scratch(b, xbytes + ybytes, std::max(xbytes, ybytes));
@@ -609,13 +649,12 @@ int gemm_batch_locked(Backend& b, int fmt, const float* X, const zq_gemm_task* t
     }
     const uint8_t* dw[ZQ_MAX_BATCH];
     size_t rows[ZQ_MAX_BATCH];
-    for (int pass = 0; pass < 2; ++pass)
-        for (size_t i = 0; i < count; ++i) {
-            st = ensure_resident(b, fmt, tasks[i].weights, tasks[i].rows, cols, &dw[i]);
-            if (st == ZQ_DECLINED) ++b.stats.declined;
-            if (st != ZQ_OK) return st;
-            rows[i] = tasks[i].rows;
-        }
+    Want want[ZQ_MAX_BATCH];
+    for (size_t i = 0; i < count; ++i) {
+        want[i] = Want{tasks[i].weights, tasks[i].rows, cols};
+        rows[i] = tasks[i].rows;
+    }
+    if ((st = resolve_set(b, fmt, want, count, dw)) != ZQ_OK) return st;
     const size_t xbytes = align_up(tokens * cols * sizeof(float), 256);
     size_t ybytes = 0, ymax = 0;
     for (size_t i = 0; i < count; ++i) {
@@ -659,14 +698,10 @@ int ffn_gemv_locked(Backend& b, int fmt, const uint8_t* gate, const uint8_t* up,
         ++b.stats.declined;
         return ZQ_DECLINED;
     }
-    const uint8_t *dg = nullptr, *du = nullptr, *dd = nullptr;
-    for (int pass = 0; pass < 2; ++pass)
-        if ((st = ensure_resident(b, fmt, gate, ffn_rows, cols, &dg)) != ZQ_OK ||
-            (st = ensure_resident(b, fmt, up, ffn_rows, cols, &du)) != ZQ_OK ||
-            (st = ensure_resident(b, fmt, down, out_rows, ffn_rows, &dd)) != ZQ_OK) {
-            if (st == ZQ_DECLINED) ++b.stats.declined;
-            return st;
-        }
+    const Want want[3] = {{gate, ffn_rows, cols}, {up, ffn_rows, cols}, {down, out_rows, ffn_rows}};
+    const uint8_t* dev[3];
+    if ((st = resolve_set(b, fmt, want, 3, dev)) != ZQ_OK) return st;
+    const uint8_t *dg = dev[0], *du = dev[1], *dd = dev[2];
     const size_t xbytes = align_up(cols * sizeof(float), 256);
     const size_t hbytes = align_up(ffn_rows * sizeof(float), 256);
     const size_t ybytes = align_up(out_rows * sizeof(float), 256);
@@ -721,15 +756,10 @@ int ffn_residual_locked(Backend& b, int fmt, const uint8_t* wo, const uint8_t* w
         ++b.stats.declined;
         return ZQ_DECLINED;
     }
-    const uint8_t *dwo = nullptr, *dwg = nullptr, *dwu = nullptr, *dwd = nullptr;
-    for (int pass = 0; pass < 2; ++pass)
-        if ((st = ensure_resident(b, fmt, wo, hidden, attn_width, &dwo)) != ZQ_OK ||
-            (st = ensure_resident(b, fmt, wg, ffn_rows, hidden, &dwg)) != ZQ_OK ||
-            (st = ensure_resident(b, fmt, wu, ffn_rows, hidden, &dwu)) != ZQ_OK ||
-            (st = ensure_resident(b, fmt, wd, hidden, ffn_rows, &dwd)) != ZQ_OK) {
-            if (st == ZQ_DECLINED) ++b.stats.declined;
-            return st;
-        }
+    const Want want[4] = {{wo, hidden, attn_width}, {wg, ffn_rows, hidden}, {wu, ffn_rows, hidden}, {wd, hidden, ffn_rows}};
+    const uint8_t* dev[4];
+    if ((st = resolve_set(b, fmt, want, 4, dev)) != ZQ_OK) return st;
+    const uint8_t *dwo = dev[0], *dwg = dev[1], *dwu = dev[2], *dwd = dev[3];
     const size_t hb = align_up(hidden * sizeof(float), 256), ab = align_up(attn_width * sizeof(float), 256);
     const size_t wsb = zq_hip_ffn_residual_workspace_bytes(hidden, ffn_rows);
     st = ensure_scratch(b, 3 * hb + ab + wsb, std::max(hb, ab));
