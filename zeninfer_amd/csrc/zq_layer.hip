@@ -880,7 +880,11 @@ __global__ __launch_bounds__(kT) void attention_decode_kernel(
     }
     // ---- arrival; the last chunk of this kv head merges ----
     __shared__ uint32_t last;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // this thread's partial stores completed
+    // Every wave waits for its own agent-scope partial stores to be
+    // acknowledged (written through to the device-coherent level) before the
+    // barrier, so the arrival below follows all of them.  A workgroup-scope
+    // release fence would not do: it emits no wait for global stores.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     const uint32_t ns = pos / C + 1;
     uint32_t* cnt = reinterpret_cast<uint32_t*>(part + size_t(H) * splits * (D + 2)) + kh;
