@@ -290,6 +290,40 @@ def test_gemv_full_size_sampled_rows(zq, orc, fmt):
         assert_close(yh[pick], orc.gemv_f32(fmt, sub, x, len(pick), cols), f"full-size gemv fmt={fmt} {rows}x{cols}")
 
 
+@pytest.mark.parametrize("fmt,rows", [(O.Q8_0, 262144), (O.Q6_K, 340000)])
+def test_weights_over_4_gib(zq, orc, fmt, rows):
+    """A weight matrix past 4 GiB (a 256K-row vocabulary at 16384 columns):
+    kernels that address a whole matrix with 32-bit buffer offsets must
+    decline it, and the ones taken instead address rows from 64-bit bases.
+    Sampled rows (with the first and last) against the oracle, for the GEMV
+    and, for Q8_0, the int8 GEMM."""
+    cols = 16384
+    rb = zq.row_bytes(fmt, cols)
+    assert rows * rb > (1 << 32)
+    wd = torch.zeros(zq.weight_bytes(fmt, rows, cols), dtype=torch.uint8, device=DEV)
+    zq.synth_weights_dev(fmt, 404, wd, rows, cols)
+    x = orc.gen_normal(405, cols)
+    y = torch.empty(rows, device=DEV)
+    zq.gemv_dev(fmt, wd, to_dev(x), y, rows, cols)
+    pick = np.unique(np.concatenate([np.random.default_rng(406).choice(rows, 40, replace=False), [0, rows - 1]]))
+    sub = np.concatenate([wd[r * rb:(r + 1) * rb].cpu().numpy() for r in pick])
+    yh = y.cpu().numpy()
+    assert np.all(np.isfinite(yh))
+    assert_close(yh[pick], orc.gemv_f32(fmt, sub, x, len(pick), cols), f"gemv past 4 GiB fmt={fmt}")
+    if fmt == O.Q8_0:
+        m = 8
+        X = orc.gen_normal(407, m * cols)
+        Y = torch.empty(m * rows, device=DEV)
+        wsb = zq.gemm_workspace_bytes(fmt, m, rows, cols, zq.ACT_INT8)
+        ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=DEV)
+        zq.gemm_dev(fmt, wd, to_dev(X), Y, m, rows, cols, zq.ACT_INT8, ws, wsb)
+        Yh = Y.cpu().numpy().reshape(m, rows)
+        want = orc.gemm_i8(fmt, sub, X, m, len(pick), cols).reshape(m, len(pick))
+        assert_close(Yh[:, pick], want, "int8 gemm past 4 GiB")
+    del wd
+    torch.cuda.empty_cache()
+
+
 def test_device_synth_matches_host_generator(zq, orc):
     for fmt, rows, cols in ((O.Q8_0, 64, 4096), (O.Q4_0, 64, 4096), (O.Q6_K, 16, 4096), (O.Q4_K, 16, 4096),
                             (O.Q5_K, 16, 4096)):
