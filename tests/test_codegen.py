@@ -8,7 +8,13 @@ The arrival must follow the acknowledgement of all of the workgroup's
 partial stores, or the merging workgroup can read a partial that has not
 landed.  That ordering is an s_waitcnt vmcnt(0) between the last partial
 store (the sc1 stores) and the barrier before the counter's atomic add.
-A race would show up only rarely, so this checks the assembly directly."""
+A race would show up only rarely, so this checks the assembly directly.
+
+Two build rules are checked the same way over every HIP source: no packed
+fp32 arithmetic (the build disables the packed-fp32-ops feature; some forms
+have given wrong results on these parts), and no writes through the scalar
+data cache (stores, atomics, write-back or discard), which this code never
+needs."""
 import os
 import re
 import shutil
@@ -20,16 +26,28 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 
-def _device_asm(src, tmp_path):
+SOURCES = ["zq_backend.hip", "zq_gemv.hip", "zq_gemm.hip", "zq_misc.hip", "zq_layer.hip", "zq_model.hip"]
+
+
+@pytest.fixture(scope="module")
+def device_asm(tmp_path_factory):
+    """gfx950 assembly of every HIP source, with the library's own flags."""
     if not shutil.which(HIPCC) and not os.path.exists(HIPCC):
         pytest.skip("hipcc not available")
-    out = tmp_path / "k.s"
-    cmd = [HIPCC, "--offload-arch=gfx950", "-O3", "-std=c++17", "-fhip-fp32-correctly-rounded-divide-sqrt",
-           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "--cuda-device-only", "-S",
-           "-o", str(out), os.path.join(ROOT, "zeninfer_amd", "csrc", src)]
-    r = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
-    assert r.returncode == 0, r.stderr[-2000:]
-    return out.read_text()
+    from concurrent.futures import ThreadPoolExecutor
+    from zeninfer_amd.build import FLAGS
+    tmp = tmp_path_factory.mktemp("asm")
+    flags = [f for f in FLAGS if f not in ("-shared", "-fPIC")]
+
+    def one(src):
+        out = tmp / (src + ".s")
+        cmd = [HIPCC, *flags, "--cuda-device-only", "-S", "-o", str(out), os.path.join(ROOT, "zeninfer_amd", "csrc", src)]
+        r = subprocess.run(cmd, capture_output=True, text=True, timeout=900)
+        assert r.returncode == 0, r.stderr[-2000:]
+        return src, out.read_text()
+
+    with ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 1)) as ex:
+        return dict(ex.map(one, SOURCES))
 
 
 def _functions(asm, pattern):
@@ -41,9 +59,8 @@ def _functions(asm, pattern):
     return found
 
 
-def test_attention_arrival_follows_partial_stores(tmp_path):
-    asm = _device_asm("zq_layer.hip", tmp_path)
-    kernels = _functions(asm, "attention_decode_kernel")
+def test_attention_arrival_follows_partial_stores(device_asm):
+    kernels = _functions(device_asm["zq_layer.hip"], "attention_decode_kernel")
     assert kernels, "no attention_decode_kernel instantiation in the assembly"
     for name, body in kernels:
         lines = body.splitlines()
@@ -56,3 +73,16 @@ def test_attention_arrival_follows_partial_stores(tmp_path):
         barrier = [i for i, l in enumerate(between) if re.search(r"\bs_barrier\b", l)]
         assert wait and barrier and wait[0] < barrier[-1], (
             f"{name}: no s_waitcnt vmcnt(0) before the barrier between the last partial store and the counter")
+
+
+def test_no_packed_fp32_arithmetic(device_asm):
+    for src, asm in device_asm.items():
+        hits = re.findall(r"^\s*(v_pk_(?:fma|add|mul)_f32)\b", asm, re.M)
+        assert not hits, f"{src}: packed fp32 instructions {sorted(set(hits))}"
+
+
+def test_no_scalar_cache_writes(device_asm):
+    for src, asm in device_asm.items():
+        hits = re.findall(r"^\s*(s_(?:store|buffer_store|scratch_store|atomic|buffer_atomic)\w*|s_dcache_(?:wb|discard)\w*)\b",
+                          asm, re.M)
+        assert not hits, f"{src}: scalar-cache writes {sorted(set(hits))}"
