@@ -483,13 +483,21 @@ __device__ __forceinline__ void gemm_i8_direct_body(
     // of row r (p = r*G::W_STRIDE + d); a row's last unit runs 2 dwords past its
     // stage bytes into the row's next bytes (the matrix's tail pad after the
     // last row), unused.
+    // Rows 16-31 of every 32-row group are fetched 8 bytes early, so their
+    // stage bytes sit 2 dwords further into their LDS row: with the stride a
+    // multiple of 4 dwords the two halves of a B read then fall on disjoint
+    // banks (dword index = 0 or 2 mod 4), where they would pair up 2-way.
+    // Only a row clamped onto the tile's first row (past N) could reach
+    // before the tile; it reads offset 0 instead, and is never used.
     uint32_t w_off[G::W_PER_WAVE];
 #pragma unroll
     for (int i = 0; i < G::W_PER_WAVE; ++i) {
         const uint32_t u = uint32_t((wave + NW * i) * 64 + lane);
         const uint32_t r = min(4 * u / G::W_STRIDE, uint32_t(BN - 1));
         const uint32_t d = 4 * u - r * G::W_STRIDE;
-        w_off[i] = (min(n0 + r, N - 1) - n0) * rb + d * 4;
+        const uint32_t off = (min(n0 + r, N - 1) - n0) * rb + d * 4;
+        const uint32_t sh = (r & 16u) ? 8u : 0u;
+        w_off[i] = off >= sh ? off - sh : 0u;
     }
     uint32_t s_off[G::S_PER_WAVE];
 #pragma unroll
@@ -528,7 +536,7 @@ __device__ __forceinline__ void gemm_i8_direct_body(
 #pragma unroll
     for (int v = 0; v < 32; ++v) szero[v] = 0.0f;
     const uint32_t nrow = wn * 32 + l32;  // this lane's weight row within the tile
-    const uint32_t wrow = nrow * G::W_STRIDE;  // its first LDS dword
+    const uint32_t wrow = nrow * G::W_STRIDE + ((l32 & 16) ? 2u : 0u);  // its first LDS dword (rows 16-31 shifted)
 
     // LDS operands of one block, read one step ahead of their MFMAs.
     struct Ops {
