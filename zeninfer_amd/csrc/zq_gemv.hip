@@ -44,6 +44,7 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <mutex>
 
 namespace zq {
 
@@ -1416,14 +1417,26 @@ hipError_t launch_stream(TaskTable& tt, const float* x, uint32_t cols, hipStream
     size_t lds = size_t(NW) * R * 64 * DW * 4;
     if (S == 1 || NW > S) lds = std::max(lds, size_t(cols >> 6) * kPadStride * sizeof(float));
     if (lds > lds_limit()) return hipErrorInvalidConfiguration;
-    static const int resident = [lds] {
-        int n = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_stream_kernel<FMT, R, S, NW, D, XK, EP>, NW * 64, lds) !=
-                hipSuccess || n < 1)
-            n = 1;
-        return n;
-    }();
-    const uint32_t grid = std::min<uint32_t>(blocks, uint32_t(cu_count() * (NW == 16 ? 1 : resident)));
+    // workgroups per CU: one at 16 waves, else the occupancy at this LDS size
+    // (it depends on cols), cached per size
+    int resident = 1;
+    if constexpr (NW != 16) {
+        static std::mutex mu;
+        static size_t keys[8];
+        static int vals[8], nkeys = 0;
+        std::lock_guard<std::mutex> lock(mu);
+        int i = 0;
+        while (i < nkeys && keys[i] != lds) ++i;
+        if (i < nkeys) {
+            resident = vals[i];
+        } else {
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&resident, gemv_stream_kernel<FMT, R, S, NW, D, XK, EP>,
+                                                             NW * 64, lds) != hipSuccess || resident < 1)
+                resident = 1;
+            if (nkeys < 8) keys[nkeys] = lds, vals[nkeys++] = resident;
+        }
+    }
+    const uint32_t grid = std::min<uint32_t>(blocks, uint32_t(cu_count() * resident));
     hipLaunchKernelGGL((gemv_stream_kernel<FMT, R, S, NW, D, XK, EP>), dim3(grid), dim3(NW * 64), lds, stream, tt, x,
                        cols, blocks, pro);
     return hipGetLastError();
