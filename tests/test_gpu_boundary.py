@@ -167,3 +167,45 @@ def test_read_probe(zq):
     with pytest.raises(zq.ZQError) as e:
         zq.read_probe_dev(buf, 1000, sink)  # not a multiple of 16
     assert e.value.status == zq.ERR_ARG
+
+
+# ------------------------------------------------------ concurrent streams ---
+def test_device_calls_on_concurrent_streams(zq, orc):
+    """The device-pointer entry points keep no device state between calls:
+    GEMVs and GEMMs (int8 with split-K partials, fp32, a super-block format)
+    enqueued alternately on two streams, each call with its own output and
+    workspace, give bit-identical results to the same calls run one at a
+    time on one stream."""
+    cases = [(O.Q8_0, zq.ACT_INT8, 32, 14336, 4096), (O.Q8_0, zq.ACT_INT8, 200, 1024, 4096),
+             (O.Q4_0, zq.ACT_INT8, 7, 3000, 2048), (O.Q8_0, zq.ACT_F32, 5, 777, 1024),
+             (O.Q6_K, zq.ACT_F32, 40, 512, 2048), (O.Q4_K, zq.ACT_F32, 1, 4096, 4096)]
+    ops = []
+    for i, (fmt, act, m, n, k) in enumerate(cases):
+        w = dev_weights(zq, fmt, orc.gen_weights(fmt, 500 + i, n, k), n, k)
+        X = to_dev(orc.gen_normal(600 + i, m * k))
+        x = to_dev(orc.gen_normal(700 + i, k))
+        wsb = zq.gemm_workspace_bytes(fmt, m, n, k, act)
+        ops.append((fmt, act, m, n, k, w, X, x, wsb))
+
+    def run(streams):
+        # outputs and workspaces first (filled on the current stream), then
+        # every stream waits for that before its launches
+        outs = [(torch.full((m * n,), float("nan"), device=DEV), torch.full((n,), float("nan"), device=DEV),
+                 torch.empty(max(wsb, 1), dtype=torch.uint8, device=DEV)) for fmt, act, m, n, k, w, X, x, wsb in ops]
+        for s in streams:
+            s.wait_stream(torch.cuda.current_stream())
+        for j, ((fmt, act, m, n, k, w, X, x, wsb), (Y, y, ws)) in enumerate(zip(ops, outs)):
+            s = streams[j % len(streams)]
+            zq.gemm_dev(fmt, w, X, Y, m, n, k, act, ws, wsb, stream=s)
+            zq.gemv_dev(fmt, w, x, y, n, k, stream=s)
+        torch.cuda.synchronize()
+        return [(Y.cpu(), y.cpu()) for Y, y, _ in outs]
+
+    serial = run([torch.cuda.current_stream()])
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    for rep in range(3):
+        par = run([s1, s2])
+        for (Ya, ya), (Yb, yb), c in zip(serial, par, cases):
+            assert torch.equal(Ya, Yb) and torch.equal(ya, yb), f"concurrent streams differ: {c} rep {rep}"
+    for (Y, y), (fmt, act, m, n, k, *_), in zip(serial, ops):
+        assert torch.isfinite(Y).all() and torch.isfinite(y).all()
