@@ -209,3 +209,74 @@ def test_device_calls_on_concurrent_streams(zq, orc):
             assert torch.equal(Ya, Yb) and torch.equal(ya, yb), f"concurrent streams differ: {c} rep {rep}"
     for (Y, y), (fmt, act, m, n, k, *_), in zip(serial, ops):
         assert torch.isfinite(Y).all() and torch.isfinite(y).all()
+
+
+# ------------------------------------------------------------ graph capture ---
+def test_device_calls_under_graph_capture(zq, orc):
+    """Callers may capture the device-pointer calls in a HIP graph: an int8
+    GEMM with split-K partials, a GEMM batch, a GEMV, a GEMV batch, RMSNorm,
+    the fused FFN half-layer and the allocation-free GEMM are captured once
+    and replayed four times, with new inputs written eagerly between the
+    replays; every replay must equal eager calls on the same inputs bit for
+    bit."""
+    F, m, k, n, h, ffn = O.Q8_0, 32, 4096, 4096, 1024, 2048
+    W = dev_weights(zq, F, orc.gen_weights(F, 801, n, k), n, k)
+    Wb = [dev_weights(zq, F, orc.gen_weights(F, 802 + i, r, k), r, k) for i, r in enumerate((512, 256))]
+    wo, wg, wu, wd = (dev_weights(zq, F, orc.gen_weights(F, 810 + i, r, c), r, c)
+                      for i, (r, c) in enumerate(((h, h), (ffn, h), (ffn, h), (h, ffn))))
+    X = torch.empty(m * k, device=DEV)
+    x = torch.empty(k, device=DEV)
+    hx, ha, nw = (torch.empty(h, device=DEV) for _ in range(3))
+    wsb = zq.gemm_workspace_bytes(F, m, n, k, zq.ACT_INT8)
+    wsbb = zq.gemm_batch_workspace_bytes(F, [512, 256], m, k, zq.ACT_INT8)
+    wsf = zq.ffn_residual_workspace_bytes(h, ffn)
+
+    def outputs():
+        return {"gemm": torch.empty(m * n, device=DEV), "b0": torch.empty(m * 512, device=DEV),
+                "b1": torch.empty(m * 256, device=DEV), "gemv": torch.empty(n, device=DEV),
+                "v0": torch.empty(512, device=DEV), "v1": torch.empty(256, device=DEV),
+                "norm": torch.empty(m * k, device=DEV), "ffn": torch.empty(h, device=DEV),
+                "noalloc": torch.empty(m * n, device=DEV),
+                "ws": torch.empty(wsb, dtype=torch.uint8, device=DEV),
+                "wsb": torch.empty(wsbb, dtype=torch.uint8, device=DEV),
+                "wsf": torch.empty(wsf, dtype=torch.uint8, device=DEV)}
+
+    def calls(o, s):
+        zq.gemm_dev(F, W, X, o["gemm"], m, n, k, zq.ACT_INT8, o["ws"], wsb, stream=s)
+        zq.gemm_batch_dev(F, X, [(Wb[0], o["b0"], 512), (Wb[1], o["b1"], 256)], m, k, zq.ACT_INT8, o["wsb"], wsbb,
+                          stream=s)
+        zq.gemv_dev(F, W, x, o["gemv"], n, k, stream=s)
+        zq.gemv_batch_dev(F, x, [(Wb[0], o["v0"], 512), (Wb[1], o["v1"], 256)], k, stream=s)
+        zq.rms_norm_dev(X, x, o["norm"], m, k, 1e-5, stream=s)
+        zq.ffn_residual_fused_dev(F, wo, wg, wu, wd, nw, hx, ha, o["ffn"], h, h, ffn, 1e-5, o["wsf"], wsf, stream=s)
+        zq.gemm_dev_noalloc(F, W, X, o["noalloc"], m, n, k, zq.ACT_INT8, stream=s)
+
+    def fill(rep):
+        X.copy_(to_dev(orc.gen_normal(900 + rep, m * k)))
+        x.copy_(to_dev(orc.gen_normal(910 + rep, k)))
+        for i, t in enumerate((hx, ha, nw)):
+            t.copy_(to_dev(orc.gen_normal(920 + 3 * rep + i, h)))
+
+    fill(0)
+    cap = outputs()
+    calls(cap, torch.cuda.current_stream())  # eager once first (occupancy and other caches)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            calls(cap, s)
+    torch.cuda.synchronize()
+    for rep in range(4):
+        fill(rep + 1)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        ref = outputs()
+        calls(ref, torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        for key in ("gemm", "b0", "b1", "gemv", "v0", "v1", "norm", "ffn", "noalloc"):
+            assert torch.isfinite(ref[key]).all(), key
+            assert torch.equal(cap[key], ref[key]), f"graph replay {rep} differs from eager: {key}"
+    assert torch.equal(cap["noalloc"], cap["gemm"])
