@@ -38,7 +38,7 @@ extern "C" {
 /* ---- status codes ------------------------------------------------------ */
 #define ZQ_OK 0
 #define ZQ_DECLINED 1          /* valid call the backend does not take: use the CPU route */
-#define ZQ_ERR_ARG (-1)        /* invalid arguments (null pointer, bad shape/format)       */
+#define ZQ_ERR_ARG (-1)        /* invalid arguments: null pointer, bad shape/format, misaligned device operand */
 #define ZQ_ERR_NO_DEVICE (-2)  /* no usable gfx950 device / init failed                    */
 #define ZQ_ERR_OOM (-3)        /* device or host allocation failed                         */
 #define ZQ_ERR_HIP (-4)        /* a HIP runtime call or kernel launch failed               */

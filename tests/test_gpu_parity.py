@@ -702,3 +702,51 @@ def test_random_gemv_and_gemm_shapes(zq, orc):
             torch.cuda.synchronize()
             want = orc.gemm_i8(fmt, w, X, M, N, K) if act == zq.ACT_INT8 else orc.gemm_f32(fmt, w, X, M, N, K)
             assert_close(Y.cpu().numpy(), want, f"gemm fmt={fmt} act={act} M={M} N={N} K={K}")
+
+
+@pytest.mark.parametrize("fmt", [O.Q8_0, O.Q4_0, O.Q6_K, O.Q4_K, O.Q5_K])
+def test_misaligned_operands(zq, orc, fmt):
+    """Host-pointer calls take any host alignment (the library copies into
+    its own device buffers); device-pointer calls on misaligned weights or
+    activations either compute the right result or refuse with ZQ_ERR_ARG,
+    never a wrong one."""
+    rows, cols, m = 300, 2048, 5
+    w = orc.gen_weights(fmt, 950, rows, cols)
+    x = orc.gen_normal(951, cols)
+    X = orc.gen_normal(952, m * cols)
+    want_v = orc.gemv_f32(fmt, w, x, rows, cols)
+    want_m = orc.gemm_f32(fmt, w, X, m, rows, cols)
+    prev = zq.set_min_elements(0)
+    try:
+        for off in (1, 2, 3):
+            hw = np.empty(w.size + 8, np.uint8)[off:off + w.size]
+            hw[:] = w
+            hx = np.empty(cols + 2, np.float32)[1:1 + cols]
+            hx[:] = x
+            assert_close(zq.gemv(fmt, hw, hx, rows, cols), want_v, f"host gemv, weights +{off} B")
+            assert_close(zq.gemm(fmt, hw, X, m, rows, cols, zq.ACT_F32), want_m, f"host gemm, weights +{off} B")
+            zq.release(hw)
+        for woff, xoff in ((1, 0), (2, 0), (4, 0), (8, 0), (0, 1), (2, 3)):
+            buf = torch.zeros(zq.weight_bytes(fmt, rows, cols) + 16, dtype=torch.uint8, device=DEV)
+            buf[woff:woff + w.size] = to_dev(w)
+            xb = torch.zeros(cols + 8, device=DEV)
+            xb[xoff:xoff + cols] = to_dev(x)
+            Xb = torch.zeros(m * cols + 8, device=DEV)
+            Xb[xoff:xoff + m * cols] = to_dev(X)
+            y = torch.full((rows,), float("nan"), device=DEV)
+            Y = torch.full((m * rows,), float("nan"), device=DEV)
+            wsb = zq.gemm_workspace_bytes(fmt, m, rows, cols, zq.ACT_F32)
+            ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=DEV)
+            what = f"weights +{woff} B, activations +{4 * xoff} B"
+            for call, out, want in ((lambda: zq.gemv_dev(fmt, buf[woff:], xb[xoff:], y, rows, cols), y, want_v),
+                                    (lambda: zq.gemm_dev(fmt, buf[woff:], Xb[xoff:], Y, m, rows, cols, zq.ACT_F32,
+                                                         ws, wsb), Y, want_m)):
+                try:
+                    call()
+                except zq.ZQError as e:
+                    assert e.status == zq.ERR_ARG, f"{what}: {e}"
+                    continue
+                torch.cuda.synchronize()
+                assert_close(out.cpu().numpy(), want, f"device call, {what}")
+    finally:
+        zq.set_min_elements(prev)

@@ -93,6 +93,13 @@ void* scratch_ptr() {
     return g_scratch_ptr[dev];
 }
 
+// Status of a launcher's result: hipErrorInvalidValue is its refusal of the
+// arguments (a misaligned operand, a shape its kernels cannot take), any
+// other error a HIP failure.
+int launch_status(hipError_t e) {
+    return e == hipSuccess ? ZQ_OK : e == hipErrorInvalidValue ? ZQ_ERR_ARG : ZQ_ERR_HIP;
+}
+
 int fail_hip(Backend& b) {
     ++b.stats.errors;
     return ZQ_ERR_HIP;
@@ -302,8 +309,10 @@ int enqueue_gemm(int fmt, const uint8_t* w, const float* X, float* Y, size_t tok
         int8_t* xq = static_cast<int8_t*>(ws);
         float* xs = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + qbytes);
         float* part = pbytes ? reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + qbytes + sbytes) : nullptr;
-        if (zq::launch_quantize_acts(X, xq, xs, tokens, cols, s) != hipSuccess) return ZQ_ERR_HIP;
-        if (zq::launch_gemm_i8(fmt, w, xq, xs, Y, part, tokens, rows, cols, s) != hipSuccess) return ZQ_ERR_HIP;
+        if (const int ls = launch_status(zq::launch_quantize_acts(X, xq, xs, tokens, cols, s)); ls != ZQ_OK) return ls;
+        if (const int ls = launch_status(zq::launch_gemm_i8(fmt, w, xq, xs, Y, part, tokens, rows, cols, s));
+            ls != ZQ_OK)
+            return ls;
         *dispatches += pbytes ? 3 : 2;
         return ZQ_OK;
     }
@@ -311,8 +320,10 @@ int enqueue_gemm(int fmt, const uint8_t* w, const float* X, float* Y, size_t tok
     // activations (Q6_K, Q4_K, Q5_K) and split-K partial sums; with less the
     // GEMM runs with what fits
     uint32_t n = 0;
-    if (zq::launch_gemm_f32(fmt, w, X, Y, ws, ws ? ws_bytes : 0, tokens, rows, cols, s, &n) != hipSuccess)
-        return ZQ_ERR_HIP;
+    if (const int ls =
+            launch_status(zq::launch_gemm_f32(fmt, w, X, Y, ws, ws ? ws_bytes : 0, tokens, rows, cols, s, &n));
+        ls != ZQ_OK)
+        return ls;
     *dispatches += n;
     return ZQ_OK;
 }
@@ -342,20 +353,24 @@ int enqueue_gemm_batch(int fmt, const uint8_t* const* w, float* const* Y, const 
         int8_t* xq = static_cast<int8_t*>(ws);
         float* xs = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + qbytes);
         float* part = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + qbytes + sbytes);
-        if (zq::launch_quantize_acts(X, xq, xs, tokens, cols, s) != hipSuccess) return ZQ_ERR_HIP;
+        if (const int ls = launch_status(zq::launch_quantize_acts(X, xq, xs, tokens, cols, s)); ls != ZQ_OK) return ls;
         ++*dispatches;
         for (size_t i = 0; i < count; ++i) {
             const size_t pb = zq::gemm_i8_partial_bytes(tokens, rows[i], cols);
-            if (zq::launch_gemm_i8(fmt, w[i], xq, xs, Y[i], pb ? part : nullptr, tokens, rows[i], cols, s) != hipSuccess)
-                return ZQ_ERR_HIP;
+            if (const int ls = launch_status(
+                    zq::launch_gemm_i8(fmt, w[i], xq, xs, Y[i], pb ? part : nullptr, tokens, rows[i], cols, s));
+                ls != ZQ_OK)
+                return ls;
             *dispatches += pb ? 2 : 1;
         }
         return ZQ_OK;
     }
     for (size_t i = 0; i < count; ++i) {
         uint32_t n = 0;
-        if (zq::launch_gemm_f32(fmt, w[i], X, Y[i], ws, ws ? ws_bytes : 0, tokens, rows[i], cols, s, &n) != hipSuccess)
-            return ZQ_ERR_HIP;
+        if (const int ls = launch_status(
+                zq::launch_gemm_f32(fmt, w[i], X, Y[i], ws, ws ? ws_bytes : 0, tokens, rows[i], cols, s, &n));
+            ls != ZQ_OK)
+            return ls;
         *dispatches += n;
     }
     return ZQ_OK;
@@ -403,7 +418,7 @@ int enqueue_ffn_residual(int fmt, const uint8_t* wo, const uint8_t* wg, const ui
     float* u = reinterpret_cast<float*>(base + 3 * hb + fb);
     const uint32_t H = uint32_t(hidden), F = uint32_t(ffn_rows);
     zq::GemvTask to{wo, t0, H};
-    if (zq::launch_gemv(fmt, &to, 1, attn_out, attn_width, s) != hipSuccess) return ZQ_ERR_HIP;
+    if (const int ls = launch_status(zq::launch_gemv(fmt, &to, 1, attn_out, attn_width, s)); ls != ZQ_OK) return ls;
     zq::GemvTask gu[2] = {{wg, g, F}, {wu, u, F}};
     const zq::XPrologue norm{zq::kAddNorm, t0, x, norm_w, h1, eps};
     hipError_t e = zq::launch_gemv_prologue(fmt, gu, 2, norm, hidden, s);
@@ -431,7 +446,7 @@ int enqueue_ffn_residual(int fmt, const uint8_t* wo, const uint8_t* wg, const ui
     } else {
         ++*dispatches;
     }
-    if (zq::launch_add_to(h1, d, out, hidden, s) != hipSuccess) return ZQ_ERR_HIP;
+    if (const int ls = launch_status(zq::launch_add_to(h1, d, out, hidden, s)); ls != ZQ_OK) return ls;
     *dispatches += 2;
     return ZQ_OK;
 }
@@ -925,8 +940,10 @@ int zq_hip_gemv_batch_dev(int fmt, const float* x, const zq_gemv_task* tasks, si
         if (!tasks[i].weights || !tasks[i].y || !tasks[i].rows || tasks[i].rows > (1u << 30)) return ZQ_ERR_ARG;
         dt[i] = zq::GemvTask{tasks[i].weights, tasks[i].y, static_cast<uint32_t>(tasks[i].rows)};
     }
-    if (zq::launch_gemv(fmt, dt, static_cast<int>(count), x, cols, static_cast<hipStream_t>(stream)) != hipSuccess)
-        return ZQ_ERR_HIP;
+    if (const int ls = launch_status(
+            zq::launch_gemv(fmt, dt, static_cast<int>(count), x, cols, static_cast<hipStream_t>(stream)));
+        ls != ZQ_OK)
+        return ls;
     return ZQ_OK;
 }
 
@@ -1010,10 +1027,8 @@ int zq_hip_gemm_batch_dev(int fmt, const float* X, const zq_gemm_task* tasks, si
 int zq_hip_rms_norm_dev(const float* x, const float* weight, float* y, size_t rows, size_t cols, float eps,
                         void* stream) {
     if (!x || !weight || !y || !rows || !cols || rows > (1u << 24) || cols > (1u << 24)) return ZQ_ERR_ARG;
-    return zq::launch_rmsnorm(x, weight, y, uint32_t(rows), uint32_t(cols), eps, static_cast<hipStream_t>(stream)) ==
-                   hipSuccess
-               ? ZQ_OK
-               : ZQ_ERR_HIP;
+    return launch_status(zq::launch_rmsnorm(x, weight, y, uint32_t(rows), uint32_t(cols), eps,
+                         static_cast<hipStream_t>(stream)));
 }
 
 int zq_hip_ffn_residual_fused_dev(int fmt, const void* attn_output, const void* gate, const void* up, const void* down,
@@ -1032,35 +1047,27 @@ int zq_hip_ffn_residual_fused_dev(int fmt, const void* attn_output, const void* 
 
 int zq_hip_quantize_acts_dev(const float* X, int8_t* xq, float* xs, size_t tokens, size_t cols, void* stream) {
     if (!X || !xq || !xs || !tokens || !cols || cols % 32) return ZQ_ERR_ARG;
-    return zq::launch_quantize_acts(X, xq, xs, tokens, cols, static_cast<hipStream_t>(stream)) == hipSuccess
-               ? ZQ_OK
-               : ZQ_ERR_HIP;
+    return launch_status(zq::launch_quantize_acts(X, xq, xs, tokens, cols, static_cast<hipStream_t>(stream)));
 }
 
 int zq_hip_block_dots_dev(int fmt, const void* weights, const int8_t* xq, int32_t* out, size_t tokens, size_t rows,
                           size_t cols, void* stream) {
     if (!weights || !xq || !out || !tokens || !rows || !valid_fmt(fmt) || !zq::row_bytes(fmt, cols)) return ZQ_ERR_ARG;
     if (!int8_fmt(fmt) || cols % 64) return ZQ_DECLINED;
-    return zq::launch_block_dots(fmt, static_cast<const uint8_t*>(weights), xq, out, tokens, rows, cols,
-                                 static_cast<hipStream_t>(stream)) == hipSuccess
-               ? ZQ_OK
-               : ZQ_ERR_HIP;
+    return launch_status(zq::launch_block_dots(fmt, static_cast<const uint8_t*>(weights), xq, out, tokens, rows, cols,
+                                 static_cast<hipStream_t>(stream)));
 }
 
 int zq_hip_dequantize_dev(int fmt, const void* weights, float* out, size_t rows, size_t cols, void* stream) {
     if (!weights || !out || !rows || !valid_fmt(fmt) || !zq::row_bytes(fmt, cols)) return ZQ_ERR_ARG;
-    return zq::launch_dequantize(fmt, static_cast<const uint8_t*>(weights), out, rows, cols,
-                                 static_cast<hipStream_t>(stream)) == hipSuccess
-               ? ZQ_OK
-               : ZQ_ERR_HIP;
+    return launch_status(zq::launch_dequantize(fmt, static_cast<const uint8_t*>(weights), out, rows, cols,
+                                 static_cast<hipStream_t>(stream)));
 }
 
 int zq_hip_read_probe_dev(const void* buf, size_t bytes, void* sink, void* stream) {
     if (!buf || !sink || !bytes || bytes % 16 || (reinterpret_cast<uintptr_t>(buf) & 15u)) return ZQ_ERR_ARG;
-    return zq::launch_read_probe(buf, bytes, static_cast<uint32_t*>(sink), static_cast<hipStream_t>(stream)) ==
-                   hipSuccess
-               ? ZQ_OK
-               : ZQ_ERR_HIP;
+    return launch_status(zq::launch_read_probe(buf, bytes, static_cast<uint32_t*>(sink),
+                         static_cast<hipStream_t>(stream)));
 }
 size_t zq_hip_read_probe_sink_bytes(void) { return zq::read_probe_sink_bytes(); }
 
@@ -1097,15 +1104,13 @@ int zq_hip_mfma_peak(double* sclk_mhz, double* cycles_per_mfma, double* int8_top
 
 int zq_hip_synth_weights_dev(int fmt, uint64_t seed, void* weights, size_t rows, size_t cols, void* stream) {
     if (!weights || !rows || !valid_fmt(fmt) || !zq::row_bytes(fmt, cols)) return ZQ_ERR_ARG;
-    return zq::launch_synth_weights(fmt, seed, static_cast<uint8_t*>(weights), rows, cols,
-                                    static_cast<hipStream_t>(stream)) == hipSuccess
-               ? ZQ_OK
-               : ZQ_ERR_HIP;
+    return launch_status(zq::launch_synth_weights(fmt, seed, static_cast<uint8_t*>(weights), rows, cols,
+                                    static_cast<hipStream_t>(stream)));
 }
 
 int zq_hip_synth_normal_dev(uint64_t seed, float* out, size_t n, void* stream) {
     if (!out || !n) return ZQ_ERR_ARG;
-    return zq::launch_synth_normal(seed, out, n, static_cast<hipStream_t>(stream)) == hipSuccess ? ZQ_OK : ZQ_ERR_HIP;
+    return launch_status(zq::launch_synth_normal(seed, out, n, static_cast<hipStream_t>(stream)));
 }
 
 }  // extern "C"
