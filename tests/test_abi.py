@@ -5,6 +5,7 @@ import ctypes
 import os
 import re
 
+import numpy as np
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -137,3 +138,29 @@ def test_device_wrappers_reject_short_buffers(monkeypatch):
         zq.quantize_acts_dev(torch.empty(2 * 256), torch.empty(512, dtype=torch.int8), torch.empty(15), 2, 256)
     with pytest.raises(ValueError, match="contiguous"):
         zq.synth_normal_dev(1, torch.empty(8, 8).t(), 64)
+
+
+def test_host_wrappers_reject_strided_or_short_arrays():
+    """The host-pointer wrappers refuse, before any library call, a weight
+    array that is a strided view or shorter than rows x row_bytes, a short
+    activation array, and mismatched batch lists: the library reads the
+    bytes from the array's address."""
+    from zeninfer_amd import zq
+    rows, cols = 64, 256
+    wb = rows * zq.row_bytes(zq.Q8_0, cols)
+    w = np.zeros(wb, np.uint8)
+    x = np.zeros(cols, np.float32)
+    with pytest.raises(ValueError, match="gemv weights: must be a C-contiguous"):
+        zq.gemv(zq.Q8_0, np.zeros(2 * wb, np.uint8)[::2], x, rows, cols)
+    with pytest.raises(ValueError, match="gemv weights: array holds"):
+        zq.gemv(zq.Q8_0, w[:-1], x, rows, cols)
+    with pytest.raises(ValueError, match="gemv x"):
+        zq.gemv(zq.Q8_0, w, x[:-1], rows, cols)
+    with pytest.raises(ValueError, match="gemm X"):
+        zq.gemm(zq.Q8_0, w, np.zeros(3 * cols - 1, np.float32), 3, rows, cols)
+    with pytest.raises(ValueError, match="gemv_batch: 2 weight arrays but 1 row counts"):
+        zq.gemv_batch(zq.Q8_0, [w, w], x, [rows], cols)
+    with pytest.raises(ValueError, match="ffn_gemv down"):
+        zq.ffn_gemv(zq.Q8_0, w, w, w[: 10], x, rows, cols, cols)
+    with pytest.raises(ValueError, match="rms_norm weight"):
+        zq.rms_norm(np.zeros(2 * cols, np.float32), np.zeros(cols - 1, np.float32), 2, cols, 1e-5)

@@ -285,15 +285,45 @@ def set_min_elements(n):
 
 
 # ---- host-pointer API (numpy) ---------------------------------------------
+def _host(a, nbytes, what):
+    """A host array handed to the library by address must be a C-contiguous
+    numpy array of at least nbytes: the library reads nbytes from its first
+    byte, so a strided view would give it other bytes and a short array bytes
+    past its end.  Weights are not copied to make them so: residency is keyed
+    by their address."""
+    if not isinstance(a, np.ndarray) or not a.flags["C_CONTIGUOUS"]:
+        raise ValueError(f"{what}: must be a C-contiguous numpy array")
+    if a.nbytes < nbytes:
+        raise ValueError(f"{what}: array holds {a.nbytes} bytes, the call needs {nbytes}")
+    return a
+
+
+def _host_w(fmt, w, rows, cols, what):
+    return _host(w, rows * row_bytes(fmt, cols), what)
+
+
+def _host_f32(a, n, what):
+    return _host(np.ascontiguousarray(a, dtype=np.float32), 4 * n, what)
+
+
+def _same_len(ws, rows, what):
+    if len(ws) != len(rows):
+        raise ValueError(f"{what}: {len(ws)} weight arrays but {len(rows)} row counts")
+
+
 def gemv(fmt, w, x, rows, cols):
+    _host_w(fmt, w, rows, cols, "gemv weights")
+    x = _host_f32(x, cols, "gemv x")
     y = np.empty(rows, np.float32)
-    x = np.ascontiguousarray(x, dtype=np.float32)
     check(lib().zq_hip_gemv(fmt, _np_ptr(w), _np_ptr(x), _np_ptr(y), rows, cols), "zq_hip_gemv")
     return y
 
 
 def gemv_batch(fmt, ws, x, rows, cols):
-    x = np.ascontiguousarray(x, dtype=np.float32)
+    _same_len(ws, rows, "gemv_batch")
+    for w, r in zip(ws, rows):
+        _host_w(fmt, w, r, cols, "gemv_batch weights")
+    x = _host_f32(x, cols, "gemv_batch x")
     ys = [np.empty(r, np.float32) for r in rows]
     tasks = (GemvTask * len(ws))(*[GemvTask(w.ctypes.data, y.ctypes.data, r) for w, y, r in zip(ws, ys, rows)])
     check(lib().zq_hip_gemv_batch(fmt, _np_ptr(x), tasks, len(ws), cols), "zq_hip_gemv_batch")
@@ -301,15 +331,19 @@ def gemv_batch(fmt, ws, x, rows, cols):
 
 
 def gemm(fmt, w, X, tokens, rows, cols, act=ACT_DEFAULT):
+    _host_w(fmt, w, rows, cols, "gemm weights")
+    X = _host_f32(X, tokens * cols, "gemm X")
     Y = np.empty(tokens * rows, np.float32)
-    X = np.ascontiguousarray(X, dtype=np.float32)
     check(lib().zq_hip_gemm(fmt, _np_ptr(w), _np_ptr(X), _np_ptr(Y), tokens, rows, cols, act), "zq_hip_gemm")
     return Y
 
 
 def ffn_gemv(fmt, gate, up, down, x, ffn_rows, cols, out_rows):
+    _host_w(fmt, gate, ffn_rows, cols, "ffn_gemv gate")
+    _host_w(fmt, up, ffn_rows, cols, "ffn_gemv up")
+    _host_w(fmt, down, out_rows, ffn_rows, "ffn_gemv down")
+    x = _host_f32(x, cols, "ffn_gemv x")
     y = np.empty(out_rows, np.float32)
-    x = np.ascontiguousarray(x, dtype=np.float32)
     check(lib().zq_hip_ffn_gemv(fmt, _np_ptr(gate), _np_ptr(up), _np_ptr(down), _np_ptr(x), _np_ptr(y),
                                 ffn_rows, cols, out_rows), "zq_hip_ffn_gemv")
     return y
@@ -317,7 +351,10 @@ def ffn_gemv(fmt, gate, up, down, x, ffn_rows, cols, out_rows):
 
 def gemm_batch(fmt, ws, X, tokens, rows, cols, act=ACT_DEFAULT):
     """Y_i = X . W_i^T for every weight of ws (shared X), one submission."""
-    X = np.ascontiguousarray(X, dtype=np.float32)
+    _same_len(ws, rows, "gemm_batch")
+    for w, r in zip(ws, rows):
+        _host_w(fmt, w, r, cols, "gemm_batch weights")
+    X = _host_f32(X, tokens * cols, "gemm_batch X")
     Ys = [np.empty(tokens * r, np.float32) for r in rows]
     tasks = (GemmTask * len(ws))(*[GemmTask(w.ctypes.data, Y.ctypes.data, r) for w, Y, r in zip(ws, Ys, rows)])
     check(lib().zq_hip_gemm_batch(fmt, _np_ptr(X), tasks, len(ws), tokens, cols, act), "zq_hip_gemm_batch")
@@ -325,17 +362,21 @@ def gemm_batch(fmt, ws, X, tokens, rows, cols, act=ACT_DEFAULT):
 
 
 def rms_norm(x, w, rows, cols, eps):
-    x = np.ascontiguousarray(x, dtype=np.float32)
-    w = np.ascontiguousarray(w, dtype=np.float32)
+    x = _host_f32(x, rows * cols, "rms_norm x")
+    w = _host_f32(w, cols, "rms_norm weight")
     y = np.empty(rows * cols, np.float32)
     check(lib().zq_hip_rms_norm(_np_ptr(x), _np_ptr(w), _np_ptr(y), rows, cols, eps), "zq_hip_rms_norm")
     return y
 
 
 def ffn_residual_fused(fmt, wo, wg, wu, wd, norm_w, x, attn_out, hidden, attn_width, ffn_rows, eps):
-    x = np.ascontiguousarray(x, dtype=np.float32)
-    a = np.ascontiguousarray(attn_out, dtype=np.float32)
-    nw = np.ascontiguousarray(norm_w, dtype=np.float32)
+    _host_w(fmt, wo, hidden, attn_width, "ffn_residual_fused attn_output")
+    _host_w(fmt, wg, ffn_rows, hidden, "ffn_residual_fused gate")
+    _host_w(fmt, wu, ffn_rows, hidden, "ffn_residual_fused up")
+    _host_w(fmt, wd, hidden, ffn_rows, "ffn_residual_fused down")
+    x = _host_f32(x, hidden, "ffn_residual_fused x")
+    a = _host_f32(attn_out, attn_width, "ffn_residual_fused attn_out")
+    nw = _host_f32(norm_w, hidden, "ffn_residual_fused norm_weight")
     out = np.empty(hidden, np.float32)
     check(lib().zq_hip_ffn_residual_fused(fmt, _np_ptr(wo), _np_ptr(wg), _np_ptr(wu), _np_ptr(wd), _np_ptr(nw),
                                           _np_ptr(x), _np_ptr(a), _np_ptr(out), hidden, attn_width, ffn_rows, eps),
