@@ -750,3 +750,22 @@ def test_misaligned_operands(zq, orc, fmt):
                 assert_close(out.cpu().numpy(), want, f"device call, {what}")
     finally:
         zq.set_min_elements(prev)
+
+
+def test_shutdown_then_lazy_reinit(zq, orc):
+    """zq_hip_shutdown frees residency, staging and the stream; the next call
+    initialises again lazily (the reference's zen::hip::shutdown / init
+    contract, include/zen/hip_backend.h:46-50), re-uploads the weights and
+    gives the same result bit for bit."""
+    rows, cols = 512, 4096
+    w = orc.gen_weights(O.Q8_0, 960, rows, cols)
+    x = orc.gen_normal(961, cols)
+    y1 = zq.gemv(O.Q8_0, w, x, rows, cols)
+    zq.shutdown()
+    assert zq.stats()["resident_tensors"] == 0
+    uploads = zq.stats()["uploads"]
+    y2 = zq.gemv(O.Q8_0, w, x, rows, cols)
+    assert np.array_equal(y1, y2)
+    assert zq.stats()["uploads"] == uploads + 1
+    assert zq.info()["arch"].startswith("gfx950")
+    zq.release(w)
