@@ -205,6 +205,7 @@ int main(int argc, char** argv) {
     std::printf("%s ok=%ld declined=%ld bad=%ld err=%ld evictions=%llu uploads=%llu\n",
                 n_bad || n_err ? "stress FAILED" : "stress ok", n_ok.load(), n_declined.load(), n_bad.load(),
                 n_err.load(), static_cast<unsigned long long>(s.evictions), static_cast<unsigned long long>(s.uploads));
+    std::fflush(stdout);  // the verdict line survives whatever the runtime's teardown does
     zq_hip_shutdown();
     return n_bad || n_err ? 1 : 0;
 }
