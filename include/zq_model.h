@@ -57,8 +57,10 @@ typedef struct zq_model_config {
 int zq_model_load_gguf(const zq_gguf* gguf, uint32_t max_positions, zq_model_config* cfg_out, zq_model** model,
                        char* err, size_t err_cap);
 /* A random-init model of the given shape generated directly on the device
- * (Q8_0 weights with the bench generator, unit norms): the config-4 shape
- * without an 8.5 GB file.  cfg->max_positions is the KV capacity. */
+ * (weights with the bench generator, unit norms): the config-4 shape without
+ * an 8.5 GB file.  cfg->weight_format picks the projections' format (0 or 8 =
+ * Q8_0; 2 = Q4_0; 14 = Q6_K; 12 = Q4_K; 13 = Q5_K); the embedding table and
+ * the output projection are Q8_0.  cfg->max_positions is the KV capacity. */
 int zq_model_create_synthetic(const zq_model_config* cfg, uint64_t seed, zq_model** model, char* err, size_t err_cap);
 void zq_model_free(zq_model* model);
 int zq_model_set_prefill_mode(zq_model* model, int mode);

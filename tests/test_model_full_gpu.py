@@ -286,3 +286,48 @@ def test_config4_width_int8_prefill_within_quantisation_error(shallow, zq):
     assert ef <= 1e-4 * scale, (ef, scale)
     assert ei <= 0.25 * scale, (ei, scale)
     assert corr > 0.95, corr
+
+
+@pytest.mark.parametrize("fmt", [O.Q4_0, O.Q6_K, O.Q4_K, O.Q5_K])
+def test_config4_shape_other_formats(zq, fmt):
+    """The config-4 shape with the projections in the other formats (the
+    embedding table and output stay Q8_0, as in many real GGUFs): fp32
+    prefill and decode logits finite, HIP-graph decode bit-identical to
+    eager, and the prompt's last-token logits from prefill (the super-block
+    GEMM on the f16 MFMA, or the Q4_0 one) against the prompt fed one decode
+    step at a time (the streaming GEMVs) within the same bar as Q8_0."""
+    from zeninfer_amd.model import Model, PREFILL_F32
+    models = []
+    for graph in (True, False):
+        os.environ["ZQ_MODEL_GRAPH"] = "1" if graph else "0"
+        try:
+            models.append(Model.synthetic(seed=SEED + fmt, weight_format=fmt, **SHAPE))
+        finally:
+            os.environ.pop("ZQ_MODEL_GRAPH", None)
+    g, e = models
+    try:
+        for m in models:
+            m.set_prefill_mode(PREFILL_F32)
+        prompt = np.random.default_rng(SEED + fmt).integers(0, SHAPE["vocab"], size=12).tolist()
+        ng, lg = g.prefill(prompt)
+        ne, le = e.prefill(prompt)
+        assert np.all(np.isfinite(lg)) and np.array_equal(lg, le) and ng == ne
+        tok = ng
+        for _ in range(3):
+            ng, lg = g.decode(tok)
+            ne, le = e.decode(tok)
+            assert np.all(np.isfinite(lg))
+            assert np.array_equal(lg, le), "graph replay differs from eager decode"
+            assert ng == ne == int(np.argmax(lg))
+            tok = ng
+        _, lp = g.prefill(prompt)
+        g.prefill(prompt[:1], logits=False)
+        for t in prompt[1:-1]:
+            g.decode(t, logits=False)
+        _, ld = g.decode(prompt[-1])
+        scale = float(np.abs(lp).max())
+        err = float(np.abs(ld - lp).max())
+        assert err <= 1e-4 * scale, (fmt, err, scale)
+    finally:
+        g.close()
+        e.close()

@@ -714,21 +714,34 @@ int zq_model_create_synthetic(const zq_model_config* cfg, uint64_t seed, zq_mode
     if (!c.rope_dim) c.rope_dim = c.head_dim;
     if (!c.rope_base) c.rope_base = 10000.0f;
     if (!c.rms_epsilon) c.rms_epsilon = 1e-5f;
-    c.weight_format = zq::kQ8_0;
+    // the projections in the requested format (default Q8_0); the embedding
+    // table and the output projection stay Q8_0
+    const int pf = c.weight_format ? c.weight_format : zq::kQ8_0;
+    if (pf != zq::kQ8_0 && pf != zq::kQ4_0 && pf != zq::kQ6_K && pf != zq::kQ4_K && pf != zq::kQ5_K) {
+        delete m;
+        set_err(err, err_cap, "weight_format must be Q8_0, Q4_0, Q6_K, Q4_K or Q5_K");
+        return ZQ_ERR_ARG;
+    }
+    c.weight_format = pf;
     std::string e;
     if (!init_common(*m, e)) { delete m; set_err(err, err_cap, e); return ZQ_ERR_NO_DEVICE; }
     const uint32_t E = c.embedding, QW = c.heads * c.head_dim, KW = c.kv_heads * c.head_dim, F = c.ffn;
+    if (pf != zq::kQ8_0 && pf != zq::kQ4_0 && (E % 256 || QW % 256 || F % 256)) {
+        delete m;
+        set_err(err, err_cap, "super-block formats need hidden, attention and FFN widths that are multiples of 256");
+        return ZQ_ERR_ARG;
+    }
     // q and k are followed by k and v without padding (one Q|K|V weight)
-    struct W { Weight* w; uint32_t rows, cols; bool packed = false; };
-    std::vector<W> ws = {{&m->embd, c.vocab, E}, {&m->out, c.vocab, E}};
+    struct W { Weight* w; uint32_t rows, cols; int fmt; bool packed = false; };
+    std::vector<W> ws = {{&m->embd, c.vocab, E, zq::kQ8_0}, {&m->out, c.vocab, E, zq::kQ8_0}};
     for (auto& L : m->layers)
-        for (auto x : {W{&L.q, QW, E, true}, W{&L.k, KW, E, true}, W{&L.v, KW, E}, W{&L.o, E, QW}, W{&L.gate, F, E},
-                       W{&L.up, F, E}, W{&L.down, E, F}})
+        for (auto x : {W{&L.q, QW, E, pf, true}, W{&L.k, KW, E, pf, true}, W{&L.v, KW, E, pf}, W{&L.o, E, QW, pf},
+                       W{&L.gate, F, E, pf}, W{&L.up, F, E, pf}, W{&L.down, E, F, pf}})
             ws.push_back(x);
     auto advance = [](const W& w) {
-        return w.packed && (size_t(w.rows) * zq::row_bytes(zq::kQ8_0, w.cols)) % 16 == 0
-                   ? size_t(w.rows) * zq::row_bytes(zq::kQ8_0, w.cols)
-                   : align_up(zq_weight_bytes(zq::kQ8_0, w.rows, w.cols), kAlign);
+        return w.packed && (size_t(w.rows) * zq::row_bytes(w.fmt, w.cols)) % 16 == 0
+                   ? size_t(w.rows) * zq::row_bytes(w.fmt, w.cols)
+                   : align_up(zq_weight_bytes(w.fmt, w.rows, w.cols), kAlign);
     };
     size_t arena = align_up(size_t(E) * 4, kAlign);  // one shared unit norm vector
     for (const W& w : ws) arena += advance(w);
@@ -744,8 +757,8 @@ int zq_model_create_synthetic(const zq_model_config* cfg, uint64_t seed, zq_mode
     for (auto& L : m->layers) L.attn_norm = L.ffn_norm = unit;
     uint64_t s = seed;
     for (const W& w : ws) {
-        *w.w = Weight{p, zq::kQ8_0, w.rows, w.cols};
-        if (zq::launch_synth_weights(zq::kQ8_0, s++, p, w.rows, w.cols, m->stream) != hipSuccess) { delete m; return ZQ_ERR_HIP; }
+        *w.w = Weight{p, w.fmt, w.rows, w.cols};
+        if (zq::launch_synth_weights(w.fmt, s++, p, w.rows, w.cols, m->stream) != hipSuccess) { delete m; return ZQ_ERR_HIP; }
         p += advance(w);
     }
     if (hipStreamSynchronize(m->stream) != hipSuccess) { delete m; return ZQ_ERR_HIP; }
