@@ -26,6 +26,9 @@ formats_config3 BASELINE config 3 (Q4_0, Q6_K) plus Q4_K / Q5_K: GEMV GB/s and
 model_config4 BASELINE config 4 on the device-resident decoder (zq_model.h):
          prefill tok/s for a 512-token prompt and decode tok/s for 128
          greedy tokens of a Llama-3-8B-shaped random-init Q8_0 model.
+model_config4_formats the same workload with the projections in Q4_0, Q6_K,
+         Q4_K and Q5_K (embedding and output Q8_0): int8 prefill for Q4_0,
+         fp32 prefill for the super-block formats.
 cpu_baseline the reference's own AVX2 ComputePool path (compiled from the
          reference sources into oracle/_ref) on this host's cores (up to 16
          threads, the box's CPU share), on four layers' projections (0.93 GB);
@@ -446,6 +449,31 @@ def format_sweep(torch, zq, dev):
     return out
 
 
+def model_config4_formats():
+    """Config 4's workload (512-token prompt, 128 greedy tokens, second of two
+    runs) with the projections in the other formats; the embedding table and
+    the output projection stay Q8_0."""
+    import numpy as np
+    from zeninfer_amd import zq
+    from zeninfer_amd.model import Model, PREFILL_F32, PREFILL_INT8
+    prompt = np.random.default_rng(0x5EED0004).integers(0, VOCAB, size=512).tolist()
+    out = {}
+    for fmt, name in ((zq.Q4_0, "Q4_0"), (zq.Q6_K, "Q6_K"), (zq.Q4_K, "Q4_K"), (zq.Q5_K, "Q5_K")):
+        m = Model.synthetic(seed=0x5EED0004, embedding=HIDDEN, layers=LAYERS, heads=32, kv_heads=8, ffn=FFN,
+                            vocab=VOCAB, context=8192, max_positions=1024, rope_base=500000.0, rms_epsilon=1e-5,
+                            eos_token=0xFFFFFFFF, weight_format=fmt)
+        m.set_prefill_mode(PREFILL_INT8 if fmt == zq.Q4_0 else PREFILL_F32)
+        for _ in range(2):
+            toks, pm, dm = m.generate(prompt, 128)
+        mem = m.memory()
+        m.close()
+        steps = len(toks) - 1
+        out[name] = {"prefill": "int8" if fmt == zq.Q4_0 else "f32", "prefill_tok_s": round(512 / (pm * 1e-3), 1),
+                     "decode_tok_s": round(steps / (dm * 1e-3), 1), "weights_bytes": mem["weights"],
+                     "decode_weight_GB_s": round(mem["weights"] / (dm / steps * 1e-3) / 1e9, 1)}
+    return out
+
+
 def model_config4():
     """BASELINE config 4 through the device-resident decoder (include/zq_model.h):
     a random-init Llama-3-8B-shaped Q8_0 model generated on the device (no
@@ -668,6 +696,8 @@ def main():
 
     # ---- config 4: the device-resident decoder, prefill 512 + 128 greedy tokens
     model4 = model_config4()
+    model4_formats = model_config4_formats()
+    print(f"[bench] config-4 formats {json.dumps(model4_formats)}", file=sys.stderr, flush=True)
 
     cpu = cpu_policy = host = cpu_gemm = None
     if not args.no_cpu:
@@ -725,6 +755,7 @@ def main():
                                                                 "(16 cvt + 16 fma) x 2.2 cycles per 32x32x32 tile-block"}},
         "formats_config3": formats,
         "model_config4": model4,
+        "model_config4_formats": model4_formats,
         "cpu_baseline": cpu,
         "cpu_baseline_reference_policy": cpu_policy,
         "cpu_baseline_gemm_and_config3": cpu_gemm,
