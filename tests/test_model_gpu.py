@@ -230,6 +230,39 @@ def test_fused_decode_equals_unfused(tiny_path, zq):
         assert np.abs(la - lb).max() <= 1e-5 * np.abs(lb).max() + 1e-6
 
 
+@pytest.mark.parametrize("ptype", [G.GGML_Q4_K, G.GGML_Q5_K])
+@pytest.mark.parametrize("embedding,heads,kv_heads", [(256, 4, 2), (2304, 18, 6)])
+def test_kquant_silu_pair_decode_equals_unfused(tmp_path, zq, ptype, embedding, heads, kv_heads):
+    """Decode on Q4_K / Q5_K with gate|up as one paired GEMV that stores
+    silu(gate)*up (one gate row and one up row per team) against
+    ZQ_MODEL_FUSED=0 (gate|up GEMV, then the SiLU*up kernel).  Each row's sum
+    is the unpaired kernel's and the activation is the same expression, so the
+    logits are bit-identical.  Embedding 256 takes the one-slice form (S = 1),
+    2304 the slice-sum form (S = 2)."""
+    from zeninfer_amd.model import PREFILL_F32
+    shape = G.LlamaShape(embedding=embedding, layers=2, heads=heads, kv_heads=kv_heads, ffn=768, vocab=512,
+                         context=2048)
+    path = tmp_path / f"sp_{ptype}_{embedding}.gguf"
+    G.synthetic_llama(path, shape, seed=21, proj_type=ptype)
+    runs = []
+    for fused in ("1", "0"):
+        os.environ["ZQ_MODEL_FUSED"] = fused
+        try:
+            m = load(path, PREFILL_F32)
+        finally:
+            os.environ.pop("ZQ_MODEL_FUSED", None)
+        nxt, _ = m.prefill(PROMPT)
+        seq = []
+        for _ in range(6):
+            nxt, lg = m.decode(nxt)
+            seq.append((nxt, lg.copy()))
+        runs.append(seq)
+        m.close()
+    for (ta, la), (tb, lb) in zip(*runs):
+        assert ta == tb
+        np.testing.assert_array_equal(la, lb)
+
+
 @pytest.mark.parametrize("ptype,rope_dim", [(G.GGML_Q8_0, 0), (G.GGML_Q4_0, 0), (G.GGML_Q8_0, 62)])
 def test_fused_prefill_quantiser_equals_unfused(tmp_path, zq, ptype, rope_dim):
     """Int8 prefill with the activations quantised inside the RMSNorm and

@@ -834,13 +834,17 @@ __device__ __forceinline__ float kquant_dot(const uint4& h, const uint4& q, cons
 // LDS buffer, and each lane reads its header, nibble unit and fifth-bit unit
 // back with ds_read_b128.  R rows per team per block; the next block's loads
 // are issued before the current one is decoded; slices are summed in LDS.
-template <int FMT, int R, int S, int NW>
+// PAIR (R = 2, tasks gate and up of equal rows): a team's two rows are gate
+// row i and up row i, and it stores silu(gate_i) * up_i into gate's y -- the
+// two sums are the ones the unpaired kernel computes for those rows.
+template <int FMT, int R, int S, int NW, bool PAIR = false>
 __global__ __launch_bounds__(NW * 64) void gemv_kquant_stream_kernel(TaskTable tt, const float* __restrict__ x,
                                                                      uint32_t cols, uint32_t total_blocks) {
     constexpr uint32_t BB = FMT == kQ5_K ? 176 : 144;
     constexpr uint32_t QOFF = FMT == kQ5_K ? 48 : 16;
     constexpr uint32_t CUNITS = 8 * BB / 16;  // 16 B units of a full slice-row (72 / 88)
     constexpr int TEAMS = NW / S;
+    static_assert(!PAIR || R == 2, "a pair step holds one gate row and one up row");
     extern __shared__ uint4 klds[];           // [waves][R][CUNITS]
     __shared__ float red[2][NW][R];
     const uint32_t nsb = cols >> 8;
@@ -875,6 +879,14 @@ __global__ __launch_bounds__(NW * 64) void gemv_kquant_stream_kernel(TaskTable t
         }
     }
     auto locate = [&](uint32_t blk, const uint8_t*(&rowp)[R], uint32_t& row0, int& ti) {
+        if constexpr (PAIR) {
+            ti = 0;
+            row0 = blk * TEAMS + team;
+            const size_t off = (size_t)min(row0, tt.t[0].rows - 1) * rb + (size_t)sb0 * BB * (nsb_s != 0);
+            rowp[0] = tt.t[0].w + off;
+            rowp[1] = tt.t[1].w + off;
+            return;
+        }
         ti = find_task(tt, blk);
         const GemvTask& t = tt.t[ti];
         row0 = (blk - tt.group_start[ti]) * (TEAMS * R) + team * R;
@@ -937,10 +949,28 @@ __global__ __launch_bounds__(NW * 64) void gemv_kquant_stream_kernel(TaskTable t
             acc[r] = wave_sum(acc[r]);
         }
         const GemvTask& t = tt.t[tic];
-        if constexpr (S == 1) {
+        if constexpr (PAIR && S == 1) {
+            if (lane == 0 && row0c < t.rows) t.y[row0c] = acc[0] / (1.0f + expf(-acc[0])) * acc[1];
+        } else if constexpr (S == 1) {
 #pragma unroll
             for (int r = 0; r < R; ++r)
                 if (lane == r && row0c + r < t.rows) t.y[row0c + r] = acc[r];
+        } else if constexpr (PAIR) {
+            if (lane == 0) {
+                red[parity][wave][0] = acc[0];
+                red[parity][wave][1] = acc[1];
+            }
+            __syncthreads();
+            if (slice == 0 && lane == 0 && row0c < t.rows) {
+                float g = 0.0f, up = 0.0f;
+#pragma unroll
+                for (int s2 = 0; s2 < S; ++s2) {
+                    g += red[parity][team * S + s2][0];
+                    up += red[parity][team * S + s2][1];
+                }
+                t.y[row0c] = g / (1.0f + expf(-g)) * up;
+            }
+            parity ^= 1;
         } else {
             if (lane == 0) {
 #pragma unroll
@@ -1601,36 +1631,40 @@ hipError_t launch_q6k_stream_any(TaskTable& tt, const float* x, uint32_t cols, h
     return total_rows >= 4096 ? launch_q6k_stream_s<2>(tt, x, cols, stream) : launch_q6k_stream_s<1>(tt, x, cols, stream);
 }
 
-template <int FMT, int R, int S, int NW>
+template <int FMT, int R, int S, int NW, bool PAIR = false>
 hipError_t launch_kquant_stream(TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream, uint32_t wg_per_cu = 1) {
     constexpr uint32_t RB = (NW / S) * R;
     constexpr uint32_t CUNITS = 8 * (FMT == kQ5_K ? 176 : 144) / 16;
     uint32_t blocks = 0;
-    for (int i = 0; i < tt.count; ++i) {
-        tt.group_start[i] = blocks;
-        blocks += (tt.t[i].rows + RB - 1) / RB;
+    if (PAIR) {
+        blocks = (tt.t[0].rows + NW / S - 1) / (NW / S);  // one gate row and one up row per team
+    } else {
+        for (int i = 0; i < tt.count; ++i) {
+            tt.group_start[i] = blocks;
+            blocks += (tt.t[i].rows + RB - 1) / RB;
+        }
+        tt.group_start[tt.count] = blocks;
     }
-    tt.group_start[tt.count] = blocks;
     const uint32_t grid = std::min<uint32_t>(blocks, uint32_t(cu_count()) * wg_per_cu);
     const size_t lds = size_t(NW) * R * CUNITS * 16;
-    hipLaunchKernelGGL((gemv_kquant_stream_kernel<FMT, R, S, NW>), dim3(grid), dim3(NW * 64), lds, stream, tt, x, cols,
-                       blocks);
+    hipLaunchKernelGGL((gemv_kquant_stream_kernel<FMT, R, S, NW, PAIR>), dim3(grid), dim3(NW * 64), lds, stream, tt, x,
+                       cols, blocks);
     return hipGetLastError();
 }
 // 64-unit slices per row -> (S, waves per workgroup); two workgroups per CU
 // (measured faster than one 16-wave workgroup with the same rows per step:
 // Q4_K 14336x4096 15.2 -> 13.9 us, Q5_K 17.0 -> 15.4 us at 2 rows per step).
-template <int FMT, int R>
+template <int FMT, int R, bool PAIR = false>
 hipError_t launch_kquant_stream_s(TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream) {
     switch ((cols + 2047) / 2048) {
-    case 1: return launch_kquant_stream<FMT, R, 1, 8>(tt, x, cols, stream, 2);
-    case 2: return launch_kquant_stream<FMT, R, 2, 8>(tt, x, cols, stream, 2);
-    case 3: return launch_kquant_stream<FMT, R, 3, 6>(tt, x, cols, stream, 2);
-    case 4: return launch_kquant_stream<FMT, R, 4, 8>(tt, x, cols, stream, 2);
-    case 5: return launch_kquant_stream<FMT, R, 5, 5>(tt, x, cols, stream, 2);
-    case 6: return launch_kquant_stream<FMT, R, 6, 6>(tt, x, cols, stream, 2);
-    case 7: return launch_kquant_stream<FMT, R, 7, 7>(tt, x, cols, stream, 2);
-    case 8: return launch_kquant_stream<FMT, R, 8, 8>(tt, x, cols, stream, 2);
+    case 1: return launch_kquant_stream<FMT, R, 1, 8, PAIR>(tt, x, cols, stream, 2);
+    case 2: return launch_kquant_stream<FMT, R, 2, 8, PAIR>(tt, x, cols, stream, 2);
+    case 3: return launch_kquant_stream<FMT, R, 3, 6, PAIR>(tt, x, cols, stream, 2);
+    case 4: return launch_kquant_stream<FMT, R, 4, 8, PAIR>(tt, x, cols, stream, 2);
+    case 5: return launch_kquant_stream<FMT, R, 5, 5, PAIR>(tt, x, cols, stream, 2);
+    case 6: return launch_kquant_stream<FMT, R, 6, 6, PAIR>(tt, x, cols, stream, 2);
+    case 7: return launch_kquant_stream<FMT, R, 7, 7, PAIR>(tt, x, cols, stream, 2);
+    case 8: return launch_kquant_stream<FMT, R, 8, 8, PAIR>(tt, x, cols, stream, 2);
     default: return hipErrorInvalidConfiguration;
     }
 }
@@ -1807,6 +1841,23 @@ hipError_t launch_gemv_prologue_silu_pair(int fmt, const GemvTask& gate, const G
     const uint32_t c = static_cast<uint32_t>(cols);
     return fmt == kQ8_0 ? launch_stream<kQ8_0, 1, 1, 16, 1, kAddNorm, 1>(tt, nullptr, c, stream, pro)
                         : launch_stream<kQ4_0, 1, 1, 16, 1, kAddNorm, 1>(tt, nullptr, c, stream, pro);
+}
+
+hipError_t launch_gemv_silu_pair(int fmt, const GemvTask& gate, const GemvTask& up, const float* x, size_t cols,
+                                 hipStream_t stream) {
+    if (!x || !row_bytes(fmt, cols) || cols > (1u << 24) || !gate.w || !gate.y || !up.w || !gate.rows)
+        return hipErrorInvalidValue;
+    auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    if ((fmt != kQ4_K && fmt != kQ5_K) || cols > 16384 || up.rows != gate.rows || !a16(x) || !a16(gate.w) ||
+        !a16(up.w))
+        return hipErrorInvalidConfiguration;
+    TaskTable tt{};
+    tt.count = 2;
+    tt.t[0] = gate;
+    tt.t[1] = GemvTask{up.w, gate.y, up.rows};
+    const uint32_t c = static_cast<uint32_t>(cols);
+    return fmt == kQ4_K ? launch_kquant_stream_s<kQ4_K, 2, true>(tt, x, c, stream)
+                        : launch_kquant_stream_s<kQ5_K, 2, true>(tt, x, c, stream);
 }
 
 }  // namespace zq

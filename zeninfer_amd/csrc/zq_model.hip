@@ -93,7 +93,7 @@ struct zq_model {
     uint32_t cur_pos = 0;  // positions held in the cache
     bool use_graph = true;
     bool fused = false;    // decode step with norms and SiLU folded into the GEMVs
-    bool fuse_quant = true;  // prefill norms / SiLU*up also write the int8 activations
+    bool fuse_quant = true;  // prefill norms / SiLU*up also write the int8 activations; K-quant gate|up pair
     hipGraphExec_t decode_exec = nullptr;
     hipGraph_t decode_graph = nullptr;
 
@@ -383,7 +383,16 @@ hipError_t enqueue_layers(zq_model& m, uint32_t T) {
         const bool qgu = qin({&L.gate, &L.up});
         HIPCHK(zq::launch_add_rmsnorm(m.x, o_splits > 1 ? m.partial : m.tmp, L.ffn_norm, qgu ? nullptr : m.h, T, E,
                                       c.rms_epsilon, m.stream, qgu ? m.xq : nullptr, qgu ? m.xs : nullptr, o_splits));
-        if (T == 1) {
+        // decode on Q4_K / Q5_K: gate|up storing silu(gate)*up itself (the
+        // per-row sums and the activation of the separate launches)
+        bool act_done = false;
+        if (T == 1 && m.fuse_quant && L.gate.fmt == L.up.fmt) {
+            const hipError_t e = zq::launch_gemv_silu_pair(L.gate.fmt, {L.gate.p, m.act, F}, {L.up.p, m.up, F}, m.h, E,
+                                                           m.stream);
+            if (e != hipSuccess && e != hipErrorInvalidConfiguration) return e;
+            act_done = e == hipSuccess;
+        }
+        if (T == 1 && !act_done) {
             zq::GemvTask t[2] = {{L.gate.p, m.gate, F}, {L.up.p, m.up, F}};
             if (L.gate.fmt == L.up.fmt) {
                 HIPCHK(zq::launch_gemv(L.gate.fmt, t, 2, m.h, E, m.stream));
@@ -391,7 +400,7 @@ hipError_t enqueue_layers(zq_model& m, uint32_t T) {
                 HIPCHK(zq::launch_gemv(L.gate.fmt, &t[0], 1, m.h, E, m.stream));
                 HIPCHK(zq::launch_gemv(L.up.fmt, &t[1], 1, m.h, E, m.stream));
             }
-        } else {
+        } else if (T > 1) {
             bool qz = qgu;
             if (!qz) HIPCHK(quantize_for(m, {&L.gate, &L.up}, m.h, T, E, qz));
             HIPCHK(project(m, L.gate, m.h, m.gate, T, qz));
@@ -400,8 +409,9 @@ hipError_t enqueue_layers(zq_model& m, uint32_t T) {
             HIPCHK(tap(m, l, ZQ_TAP_UP, L.up, T, qz, m.up, 1));
         }
         const bool qd = qin({&L.down});
-        HIPCHK(zq::launch_silu_mul(m.gate, m.up, qd ? nullptr : m.act, size_t(T) * F, m.stream,
-                                   qd ? m.xq : nullptr, qd ? m.xs : nullptr));
+        if (!act_done)
+            HIPCHK(zq::launch_silu_mul(m.gate, m.up, qd ? nullptr : m.act, size_t(T) * F, m.stream,
+                                       qd ? m.xq : nullptr, qd ? m.xs : nullptr));
         if (T == 1) {
             zq::GemvTask t = {L.down.p, m.tmp, E};
             HIPCHK(zq::launch_gemv(L.down.fmt, &t, 1, m.act, F, m.stream));
