@@ -230,15 +230,16 @@ def test_fused_decode_equals_unfused(tiny_path, zq):
         assert np.abs(la - lb).max() <= 1e-5 * np.abs(lb).max() + 1e-6
 
 
-@pytest.mark.parametrize("ptype", [G.GGML_Q4_K, G.GGML_Q5_K])
-@pytest.mark.parametrize("embedding,heads,kv_heads", [(256, 4, 2), (2304, 18, 6)])
+@pytest.mark.parametrize("ptype,embedding,heads,kv_heads", [
+    (G.GGML_Q4_K, 256, 4, 2), (G.GGML_Q4_K, 2304, 18, 6), (G.GGML_Q5_K, 256, 4, 2), (G.GGML_Q5_K, 2304, 18, 6),
+    (G.GGML_Q6_K, 2048, 16, 4), (G.GGML_Q6_K, 4096, 32, 8)])
 def test_kquant_silu_pair_decode_equals_unfused(tmp_path, zq, ptype, embedding, heads, kv_heads):
-    """Decode on Q4_K / Q5_K with gate|up as one paired GEMV that stores
+    """Decode on Q4_K / Q5_K / Q6_K with gate|up as one paired GEMV that stores
     silu(gate)*up (one gate row and one up row per team) against
     ZQ_MODEL_FUSED=0 (gate|up GEMV, then the SiLU*up kernel).  Each row's sum
     is the unpaired kernel's and the activation is the same expression, so the
-    logits are bit-identical.  Embedding 256 takes the one-slice form (S = 1),
-    2304 the slice-sum form (S = 2)."""
+    logits are bit-identical.  Embedding 256 (Q6_K: 2048) takes the one-slice
+    form (S = 1), 2304 (Q6_K: 4096) the slice-sum form (S = 2)."""
     from zeninfer_amd.model import PREFILL_F32
     shape = G.LlamaShape(embedding=embedding, layers=2, heads=heads, kv_heads=kv_heads, ffn=768, vocab=512,
                          context=2048)

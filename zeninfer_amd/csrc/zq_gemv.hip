@@ -579,11 +579,13 @@ __global__ __launch_bounds__(kThreads) void gemv_q6k_kernel(TaskTable tt, const 
 // per-wave LDS buffer; lane L then decodes its two 16-element units (one
 // quarter of one half of super-block 2*(L/16) + k, a single sub-block scale)
 // from LDS.  Fields of odd super-blocks sit at 2 mod 4 and are assembled
-// with v_alignbyte.
-template <int R, int S, int NW>
+// with v_alignbyte.  PAIR as in the K-quant streaming kernel below: gate
+// row i and up row i per team, silu(gate_i) * up_i stored into gate's y.
+template <int R, int S, int NW, bool PAIR = false>
 __global__ __launch_bounds__(NW * 64) void gemv_q6k_stream_kernel(TaskTable tt, const float* __restrict__ x,
                                                                  uint32_t cols, uint32_t total_blocks) {
     constexpr int TEAMS = NW / S;
+    static_assert(!PAIR || R == 2, "a pair step holds one gate row and one up row");
     constexpr uint32_t CHUNK = 8 * 210;                  // bytes
     constexpr uint32_t CUNITS = CHUNK / 16;              // 105 dwordx4 units
     constexpr uint32_t BUFW = CHUNK / 4 + 4;             // dwords per row buffer (+pad for alignbyte reads)
@@ -616,6 +618,14 @@ __global__ __launch_bounds__(NW * 64) void gemv_q6k_stream_kernel(TaskTable tt, 
     }
     __builtin_amdgcn_sched_barrier(0);
     auto locate = [&](uint32_t blk, const uint8_t*(&rowp)[R], uint32_t& row0, int& ti) {
+        if constexpr (PAIR) {
+            ti = 0;
+            row0 = blk * TEAMS + team;
+            const size_t off = (size_t)min(row0, tt.t[0].rows - 1) * rb + (size_t)slice * CHUNK;
+            rowp[0] = tt.t[0].w + off;
+            rowp[1] = tt.t[1].w + off;
+            return;
+        }
         ti = find_task(tt, blk);
         const GemvTask& t = tt.t[ti];
         row0 = (blk - tt.group_start[ti]) * (TEAMS * R) + team * R;
@@ -723,10 +733,28 @@ __global__ __launch_bounds__(NW * 64) void gemv_q6k_stream_kernel(TaskTable tt, 
             acc[r] = wave_sum(a);
         }
         const GemvTask& t = tt.t[tic];
-        if constexpr (S == 1) {
+        if constexpr (PAIR && S == 1) {
+            if (lane == 0 && row0c < t.rows) t.y[row0c] = acc[0] / (1.0f + expf(-acc[0])) * acc[1];
+        } else if constexpr (S == 1) {
 #pragma unroll
             for (int r = 0; r < R; ++r)
                 if (lane == r && row0c + r < t.rows) t.y[row0c + r] = acc[r];
+        } else if constexpr (PAIR) {
+            if (lane == 0) {
+                red[parity][wave][0] = acc[0];
+                red[parity][wave][1] = acc[1];
+            }
+            __syncthreads();
+            if (slice == 0 && lane == 0 && row0c < t.rows) {
+                float g = 0.0f, up = 0.0f;
+#pragma unroll
+                for (int s2 = 0; s2 < S; ++s2) {
+                    g += red[parity][team * S + s2][0];
+                    up += red[parity][team * S + s2][1];
+                }
+                t.y[row0c] = g / (1.0f + expf(-g)) * up;
+            }
+            parity ^= 1;
         } else {
             if (lane == 0) {
 #pragma unroll
@@ -1595,35 +1623,40 @@ hipError_t launch_q6k(TaskTable& tt, const float* x, uint32_t cols, hipStream_t 
                            x, cols, groups);
     return hipGetLastError();
 }
-template <int R, int S, int NW>
+template <int R, int S, int NW, bool PAIR = false>
 hipError_t launch_q6k_stream(TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream, uint32_t wg_per_cu = 1) {
     constexpr uint32_t TEAMS = NW / S;
     uint32_t blocks = 0;
-    for (int i = 0; i < tt.count; ++i) {
-        tt.group_start[i] = blocks;
-        blocks += (tt.t[i].rows + TEAMS * R - 1) / (TEAMS * R);
+    if (PAIR) {
+        blocks = (tt.t[0].rows + TEAMS - 1) / TEAMS;  // one gate row and one up row per team
+    } else {
+        for (int i = 0; i < tt.count; ++i) {
+            tt.group_start[i] = blocks;
+            blocks += (tt.t[i].rows + TEAMS * R - 1) / (TEAMS * R);
+        }
+        tt.group_start[tt.count] = blocks;
     }
-    tt.group_start[tt.count] = blocks;
     const uint32_t grid = std::min<uint32_t>(blocks, uint32_t(cu_count()) * wg_per_cu);
     const size_t lds = size_t(NW) * R * (8 * 210 / 4 + 4) * 4;
-    hipLaunchKernelGGL((gemv_q6k_stream_kernel<R, S, NW>), dim3(grid), dim3(NW * 64), lds, stream, tt, x, cols, blocks);
+    hipLaunchKernelGGL((gemv_q6k_stream_kernel<R, S, NW, PAIR>), dim3(grid), dim3(NW * 64), lds, stream, tt, x, cols,
+                       blocks);
     return hipGetLastError();
 }
 // chunks per row -> (S, waves per workgroup); two workgroups per CU.  Two
 // 8-wave workgroups measured faster than one 16-wave one (the per-step
 // slice reduction then synchronises 8 waves, not 16), and 2 rows per step
 // faster than 1 or 4: 14336x4096 19.6 -> 17.0 us, lm_head 96.6 -> 89.5 us.
-template <int R>
+template <int R, bool PAIR = false>
 hipError_t launch_q6k_stream_s(TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream) {
     switch ((cols >> 8) / 8) {
-    case 1: return launch_q6k_stream<R, 1, 8>(tt, x, cols, stream, 2);
-    case 2: return launch_q6k_stream<R, 2, 8>(tt, x, cols, stream, 2);
-    case 3: return launch_q6k_stream<R, 3, 6>(tt, x, cols, stream, 2);
-    case 4: return launch_q6k_stream<R, 4, 8>(tt, x, cols, stream, 2);
-    case 5: return launch_q6k_stream<R, 5, 5>(tt, x, cols, stream, 2);
-    case 6: return launch_q6k_stream<R, 6, 6>(tt, x, cols, stream, 2);
-    case 7: return launch_q6k_stream<R, 7, 7>(tt, x, cols, stream, 2);
-    case 8: return launch_q6k_stream<R, 8, 8>(tt, x, cols, stream, 2);
+    case 1: return launch_q6k_stream<R, 1, 8, PAIR>(tt, x, cols, stream, 2);
+    case 2: return launch_q6k_stream<R, 2, 8, PAIR>(tt, x, cols, stream, 2);
+    case 3: return launch_q6k_stream<R, 3, 6, PAIR>(tt, x, cols, stream, 2);
+    case 4: return launch_q6k_stream<R, 4, 8, PAIR>(tt, x, cols, stream, 2);
+    case 5: return launch_q6k_stream<R, 5, 5, PAIR>(tt, x, cols, stream, 2);
+    case 6: return launch_q6k_stream<R, 6, 6, PAIR>(tt, x, cols, stream, 2);
+    case 7: return launch_q6k_stream<R, 7, 7, PAIR>(tt, x, cols, stream, 2);
+    case 8: return launch_q6k_stream<R, 8, 8, PAIR>(tt, x, cols, stream, 2);
     default: return hipErrorInvalidConfiguration;
     }
 }
@@ -1848,7 +1881,8 @@ hipError_t launch_gemv_silu_pair(int fmt, const GemvTask& gate, const GemvTask& 
     if (!x || !row_bytes(fmt, cols) || cols > (1u << 24) || !gate.w || !gate.y || !up.w || !gate.rows)
         return hipErrorInvalidValue;
     auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
-    if ((fmt != kQ4_K && fmt != kQ5_K) || cols > 16384 || up.rows != gate.rows || !a16(x) || !a16(gate.w) ||
+    const bool q6k = fmt == kQ6_K && cols % 2048 == 0;  // whole 8-super-block chunks
+    if ((fmt != kQ4_K && fmt != kQ5_K && !q6k) || cols > 16384 || up.rows != gate.rows || !a16(x) || !a16(gate.w) ||
         !a16(up.w))
         return hipErrorInvalidConfiguration;
     TaskTable tt{};
@@ -1856,6 +1890,7 @@ hipError_t launch_gemv_silu_pair(int fmt, const GemvTask& gate, const GemvTask& 
     tt.t[0] = gate;
     tt.t[1] = GemvTask{up.w, gate.y, up.rows};
     const uint32_t c = static_cast<uint32_t>(cols);
+    if (q6k) return launch_q6k_stream_s<2, true>(tt, x, c, stream);
     return fmt == kQ4_K ? launch_kquant_stream_s<kQ4_K, 2, true>(tt, x, c, stream)
                         : launch_kquant_stream_s<kQ5_K, 2, true>(tt, x, c, stream);
 }

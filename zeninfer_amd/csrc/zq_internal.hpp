@@ -51,8 +51,9 @@ hipError_t launch_gemv_prologue(int fmt, const GemvTask* tasks, int count, const
 hipError_t launch_gemv_prologue_silu_pair(int fmt, const GemvTask& gate, const GemvTask& up, const XPrologue& pro,
                                           size_t cols, hipStream_t stream);
 // gate|up over a plain x that stores f = silu(gate.x) * (up.x) into gate.y
-// (up.y unused): Q4_K / Q5_K, cols <= 16384, equal rows, 16-byte aligned x
-// and weights; hipErrorInvalidConfiguration otherwise.
+// (up.y unused): Q4_K / Q5_K, and Q6_K with cols % 2048 == 0; cols <= 16384,
+// equal rows, 16-byte aligned x and weights; hipErrorInvalidConfiguration
+// otherwise.
 hipError_t launch_gemv_silu_pair(int fmt, const GemvTask& gate, const GemvTask& up, const float* x, size_t cols,
                                  hipStream_t stream);
 

@@ -383,7 +383,7 @@ hipError_t enqueue_layers(zq_model& m, uint32_t T) {
         const bool qgu = qin({&L.gate, &L.up});
         HIPCHK(zq::launch_add_rmsnorm(m.x, o_splits > 1 ? m.partial : m.tmp, L.ffn_norm, qgu ? nullptr : m.h, T, E,
                                       c.rms_epsilon, m.stream, qgu ? m.xq : nullptr, qgu ? m.xs : nullptr, o_splits));
-        // decode on Q4_K / Q5_K: gate|up storing silu(gate)*up itself (the
+        // decode on Q4_K / Q5_K / Q6_K: gate|up storing silu(gate)*up itself (the
         // per-row sums and the activation of the separate launches)
         bool act_done = false;
         if (T == 1 && m.fuse_quant && L.gate.fmt == L.up.fmt) {
