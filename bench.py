@@ -514,6 +514,8 @@ def main():
                     help="only config 2's int8 GEMM sweep, 3 calls per shape (kernel-trace helper)")
     ap.add_argument("--model-only", action="store_true",
                     help="run only the config-4 decoder leg and print its JSON (profiling helper)")
+    ap.add_argument("--model-formats-only", action="store_true",
+                    help="run only the config-4 decoder leg in Q4_0 / Q6_K / Q4_K / Q5_K and print its JSON")
     args = ap.parse_args()
     if args.summarize_trace:
         summarize_trace(args.summarize_trace)
@@ -533,6 +535,13 @@ def main():
         torch.cuda.set_device(0)
         zq.init()
         print(json.dumps(model_config4()))
+        return 0
+    if args.model_formats_only:
+        import torch
+        from zeninfer_amd import zq
+        torch.cuda.set_device(0)
+        zq.init()
+        print(json.dumps(model_config4_formats()))
         return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU leg (the projections would shard "
