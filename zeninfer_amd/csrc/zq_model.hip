@@ -496,9 +496,10 @@ hipError_t enqueue_decode(zq_model& m) {
 
 // The fused decode covers Q8_0 / Q4_0 projections on the streaming GEMV's
 // shapes; anything else keeps the separate norm / activation kernels.
-// ZQ_MODEL_FUSED=0 disables it and, in prefill, the quantisers folded into
-// the norm / SiLU kernels and the split-K sums left to the GEMMs' readers
-// (A/B runs and the equivalence tests).
+// ZQ_MODEL_FUSED=0 disables it, the super-block formats' paired gate|up
+// GEMV and, in prefill, the quantisers folded into the norm / SiLU kernels
+// and the split-K sums left to the GEMMs' readers (A/B runs and the
+// equivalence tests).
 void choose_fused(zq_model& m) {
     const char* e = std::getenv("ZQ_MODEL_FUSED");
     const auto& c = m.cfg;
