@@ -107,7 +107,9 @@ def ffn_residual_ref(orc, fmt, wo, wg, wu, wd, nw, x, a, hidden, aw, ffn, eps):
 
 
 @pytest.mark.parametrize("fmt,hidden,aw,ffn", [(O.Q8_0, 1024, 1024, 2816), (O.Q4_0, 2048, 1024, 5632),
-                                                (O.Q6_K, 1024, 2048, 2816), (O.Q8_0, 4096, 4096, 14336)])
+                                                (O.Q6_K, 1024, 2048, 2816), (O.Q8_0, 4096, 4096, 14336),
+                                                (O.Q4_K, 1024, 1024, 2816), (O.Q5_K, 2304, 1024, 2816),
+                                                (O.Q6_K, 2048, 2048, 2816)])
 def test_ffn_residual_fused(zq, orc, fmt, hidden, aw, ffn):
     wo = orc.gen_weights(fmt, 740, hidden, aw)
     wg = orc.gen_weights(fmt, 741, ffn, hidden)

@@ -539,17 +539,24 @@ def test_small_shapes_declined_by_default(zq, orc):
     assert e.value.status == zq.DECLINED
 
 
-def test_ffn_gemv(zq, orc):
-    cols, ffn, out = 1024, 2816, 1024
-    g = orc.gen_weights(O.Q8_0, 61, ffn, cols)
-    u = orc.gen_weights(O.Q8_0, 62, ffn, cols)
-    d = orc.gen_weights(O.Q8_0, 63, out, ffn)
+@pytest.mark.parametrize("fmt,cols", [(O.Q8_0, 1024), (O.Q4_K, 1024), (O.Q5_K, 2304), (O.Q6_K, 2048),
+                                      (O.Q6_K, 4096)])
+def test_ffn_gemv(zq, orc, fmt, cols):
+    """gate|up, SiLU*up, down.  The super-block formats form silu(gate)*up in
+    one paired gate|up GEMV (Q6_K for widths that are multiples of 2048)."""
+    ffn, out = 2816, 1024
+    g = orc.gen_weights(fmt, 61, ffn, cols)
+    u = orc.gen_weights(fmt, 62, ffn, cols)
+    d = orc.gen_weights(fmt, 63, out, ffn)
     x = orc.gen_normal(64, cols)
-    y = zq.ffn_gemv(O.Q8_0, g, u, d, x, ffn, cols, out)
-    gv = orc.gemv_f32(O.Q8_0, g, x, ffn, cols).astype(np.float64)
-    uv = orc.gemv_f32(O.Q8_0, u, x, ffn, cols).astype(np.float64)
+    zq.reset_stats()
+    y = zq.ffn_gemv(fmt, g, u, d, x, ffn, cols, out)
+    # the route: paired gate|up + down, or gate|up + SiLU*up + down
+    assert zq.stats()["dispatches"] == (3 if fmt == O.Q8_0 else 2)
+    gv = orc.gemv_f32(fmt, g, x, ffn, cols).astype(np.float64)
+    uv = orc.gemv_f32(fmt, u, x, ffn, cols).astype(np.float64)
     act = gv / (1 + np.exp(-gv)) * uv
-    dd = orc.dequantize(O.Q8_0, d, out * ffn).reshape(out, ffn).astype(np.float64)
+    dd = orc.dequantize(fmt, d, out * ffn).reshape(out, ffn).astype(np.float64)
     want = dd @ act
     # SiLU goes through expf: bound the error by the sum of |terms| of the down
     # projection (the GEMV bar relative to the magnitude that is summed)

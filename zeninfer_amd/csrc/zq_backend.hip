@@ -389,8 +389,9 @@ bool ffn_residual_args_ok(int fmt, const void* wo, const void* wg, const void* w
 //   t0 = Wo . attn_out;  h1 = t0 + x;  h2 = rmsnorm(h1) * norm_w;
 //   g = Wg . h2;  u = Wu . h2;  f = silu(g) * u;  d = Wd . f;  out = h1 + d.
 // Q8_0 / Q4_0 on the streaming shapes fold the add + norm into the gate|up
-// GEMV and silu * up into the down GEMV; other formats run them as kernels
-// of their own.  x is read before out is written, so out may alias x.
+// GEMV and silu * up into the down GEMV; Q4_K / Q5_K / Q6_K form silu * up
+// in a paired gate|up GEMV; otherwise they run as kernels of their own.  x
+// is read before out is written, so out may alias x.
 int enqueue_ffn_residual(int fmt, const uint8_t* wo, const uint8_t* wg, const uint8_t* wu, const uint8_t* wd,
                          const float* norm_w, const float* x, const float* attn_out, float* out, size_t hidden,
                          size_t attn_width, size_t ffn_rows, float eps, void* ws, size_t ws_bytes, hipStream_t s,
@@ -422,22 +423,32 @@ int enqueue_ffn_residual(int fmt, const uint8_t* wo, const uint8_t* wg, const ui
     zq::GemvTask gu[2] = {{wg, g, F}, {wu, u, F}};
     const zq::XPrologue norm{zq::kAddNorm, t0, x, norm_w, h1, eps};
     hipError_t e = zq::launch_gemv_prologue(fmt, gu, 2, norm, hidden, s);
+    zq::GemvTask dn{wd, d, H};
+    bool paired = false;  // g already holds silu(gate) * up
     if (e == hipErrorInvalidConfiguration) {
-        // unfused: h1 = t0 + x, h2 = rmsnorm(h1) * w (into d), gate|up of h2
+        // unfused: h1 = t0 + x, h2 = rmsnorm(h1) * w (into d), then gate|up
+        // of h2 -- as one paired GEMV storing silu(gate) * up into g where the
+        // format takes it (Q4_K / Q5_K / Q6_K), else as a 2-task GEMV
         if (zq::launch_add_to(t0, x, h1, hidden, s) != hipSuccess ||
-            zq::launch_rmsnorm(h1, norm_w, d, 1, H, eps, s) != hipSuccess ||
-            zq::launch_gemv(fmt, gu, 2, d, hidden, s) != hipSuccess)
+            zq::launch_rmsnorm(h1, norm_w, d, 1, H, eps, s) != hipSuccess)
             return ZQ_ERR_HIP;
-        *dispatches += 3;
+        *dispatches += 2;
+        const hipError_t pe = zq::launch_gemv_silu_pair(fmt, gu[0], gu[1], d, hidden, s);
+        if (pe != hipSuccess && pe != hipErrorInvalidConfiguration) return ZQ_ERR_HIP;
+        paired = pe == hipSuccess;
+        if (!paired && zq::launch_gemv(fmt, gu, 2, d, hidden, s) != hipSuccess) return ZQ_ERR_HIP;
+        ++*dispatches;
     } else if (e != hipSuccess) {
         return ZQ_ERR_HIP;
     } else {
         ++*dispatches;
     }
-    zq::GemvTask dn{wd, d, H};
     const zq::XPrologue act{zq::kSiluMul, g, u, nullptr, nullptr, 0.0f};
-    e = zq::launch_gemv_prologue(fmt, &dn, 1, act, ffn_rows, s);
-    if (e == hipErrorInvalidConfiguration) {
+    e = paired ? hipErrorInvalidConfiguration : zq::launch_gemv_prologue(fmt, &dn, 1, act, ffn_rows, s);
+    if (paired) {
+        if (zq::launch_gemv(fmt, &dn, 1, g, ffn_rows, s) != hipSuccess) return ZQ_ERR_HIP;
+        ++*dispatches;
+    } else if (e == hipErrorInvalidConfiguration) {
         if (zq::launch_silu_mul(g, u, g, ffn_rows, s) != hipSuccess || zq::launch_gemv(fmt, &dn, 1, g, ffn_rows, s) != hipSuccess)
             return ZQ_ERR_HIP;
         *dispatches += 2;
@@ -732,11 +743,17 @@ int ffn_gemv_locked(Backend& b, int fmt, const uint8_t* gate, const uint8_t* up,
     if ((st = c.put(dx, x, cols * sizeof(float))) != ZQ_OK) return st;
     c.begin();
     zq::GemvTask gu[2] = {{dg, dgate, static_cast<uint32_t>(ffn_rows)}, {du, dup, static_cast<uint32_t>(ffn_rows)}};
-    if (zq::launch_gemv(fmt, gu, 2, dx, cols, b.stream) != hipSuccess) return fail_hip(b);
-    if (zq::launch_silu_mul(dgate, dup, dact, ffn_rows, b.stream) != hipSuccess) return fail_hip(b);
+    // Q4_K / Q5_K / Q6_K: gate|up as one paired GEMV storing silu(gate) * up
+    // (the same per-row sums and activation as the two launches below)
+    const hipError_t pe = zq::launch_gemv_silu_pair(fmt, {dg, dact, gu[0].rows}, gu[1], dx, cols, b.stream);
+    if (pe != hipSuccess && pe != hipErrorInvalidConfiguration) return fail_hip(b);
+    if (pe != hipSuccess) {
+        if (zq::launch_gemv(fmt, gu, 2, dx, cols, b.stream) != hipSuccess) return fail_hip(b);
+        if (zq::launch_silu_mul(dgate, dup, dact, ffn_rows, b.stream) != hipSuccess) return fail_hip(b);
+    }
     zq::GemvTask dn{dd, dy, static_cast<uint32_t>(out_rows)};
     if (zq::launch_gemv(fmt, &dn, 1, dact, ffn_rows, b.stream) != hipSuccess) return fail_hip(b);
-    c.launched(3);
+    c.launched(pe == hipSuccess ? 2 : 3);
     if ((st = c.end()) != ZQ_OK) return st;
     return c.get(y, dy, out_rows * sizeof(float));
 }
