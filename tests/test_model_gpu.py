@@ -234,12 +234,17 @@ def test_fused_decode_equals_unfused(tiny_path, zq):
     (G.GGML_Q4_K, 256, 4, 2), (G.GGML_Q4_K, 2304, 18, 6), (G.GGML_Q5_K, 256, 4, 2), (G.GGML_Q5_K, 2304, 18, 6),
     (G.GGML_Q6_K, 2048, 16, 4), (G.GGML_Q6_K, 4096, 32, 8)])
 def test_kquant_silu_pair_decode_equals_unfused(tmp_path, zq, ptype, embedding, heads, kv_heads):
-    """Decode on Q4_K / Q5_K / Q6_K with gate|up as one paired GEMV that stores
-    silu(gate)*up (one gate row and one up row per team) against
-    ZQ_MODEL_FUSED=0 (gate|up GEMV, then the SiLU*up kernel).  Each row's sum
-    is the unpaired kernel's and the activation is the same expression, so the
-    logits are bit-identical.  Embedding 256 (Q6_K: 2048) takes the one-slice
-    form (S = 1), 2304 (Q6_K: 4096) the slice-sum form (S = 2)."""
+    """Decode on Q4_K / Q5_K / Q6_K against ZQ_MODEL_FUSED=0 (gate|up GEMV,
+    SiLU*up kernel, add+RMSNorm kernels).  Q6_K: gate|up as one paired GEMV
+    that stores silu(gate)*up (one gate row and one up row per team); each
+    row's sum is the unpaired kernel's and the activation is the same
+    expression, so the logits are bit-identical.  Q4_K / Q5_K also carry the
+    residual adds and RMSNorms in the GEMVs (the o / down GEMVs add into the
+    residual and accumulate its sum of squares in double through atomics; QKV
+    and gate|up normalise x as they load it): the same arithmetic except the
+    order of the double sum of squares, so the logits agree to a few fp32 ulps
+    and the greedy tokens are identical.  Embedding 256 (Q6_K: 2048) takes the
+    one-slice form (S = 1), 2304 (Q6_K: 4096) the slice-sum form (S = 2)."""
     from zeninfer_amd.model import PREFILL_F32
     shape = G.LlamaShape(embedding=embedding, layers=2, heads=heads, kv_heads=kv_heads, ffn=768, vocab=512,
                          context=2048)
@@ -261,7 +266,10 @@ def test_kquant_silu_pair_decode_equals_unfused(tmp_path, zq, ptype, embedding, 
         m.close()
     for (ta, la), (tb, lb) in zip(*runs):
         assert ta == tb
-        np.testing.assert_array_equal(la, lb)
+        if ptype == G.GGML_Q6_K:
+            np.testing.assert_array_equal(la, lb)
+        else:
+            assert np.abs(la - lb).max() <= 1e-5 * np.abs(lb).max() + 1e-6
 
 
 @pytest.mark.parametrize("ptype,rope_dim", [(G.GGML_Q8_0, 0), (G.GGML_Q4_0, 0), (G.GGML_Q8_0, 62)])

@@ -865,14 +865,16 @@ __device__ __forceinline__ float kquant_dot(const uint4& h, const uint4& q, cons
 // PAIR (R = 2, tasks gate and up of equal rows): a team's two rows are gate
 // row i and up row i, and it stores silu(gate_i) * up_i into gate's y -- the
 // two sums are the ones the unpaired kernel computes for those rows.
-template <int FMT, int R, int S, int NW, bool PAIR = false>
+template <int FMT, int R, int S, int NW, bool PAIR = false, int RN = kRnNone>
 __global__ __launch_bounds__(NW * 64) void gemv_kquant_stream_kernel(TaskTable tt, const float* __restrict__ x,
-                                                                     uint32_t cols, uint32_t total_blocks) {
+                                                                     uint32_t cols, uint32_t total_blocks,
+                                                                     ResidNorm rn) {
     constexpr uint32_t BB = FMT == kQ5_K ? 176 : 144;
     constexpr uint32_t QOFF = FMT == kQ5_K ? 48 : 16;
     constexpr uint32_t CUNITS = 8 * BB / 16;  // 16 B units of a full slice-row (72 / 88)
     constexpr int TEAMS = NW / S;
     static_assert(!PAIR || R == 2, "a pair step holds one gate row and one up row");
+    static_assert(!(PAIR && RN == kRnAddOut), "a pair's output is not a residual");
     extern __shared__ uint4 klds[];           // [waves][R][CUNITS]
     __shared__ float red[2][NW][R];
     const uint32_t nsb = cols >> 8;
@@ -887,8 +889,11 @@ __global__ __launch_bounds__(NW * 64) void gemv_kquant_stream_kernel(TaskTable t
     const bool active = uint32_t(lane >> 3) < nsb_s;
     uint4* buf = klds + wave * (R * CUNITS);
 
-    // x first (loads retire in issue order)
+    // x first (loads retire in issue order); norm-in: the norm weight and the
+    // sum-of-squares slots too, applied once the first weight block is issued
     float xl[16], xh[16], sxl, sxh;
+    float wl[RN == kRnNormIn ? 16 : 1], wh[RN == kRnNormIn ? 16 : 1];
+    double slot = 0.0;
     {
         const uint32_t uu = active ? u : 0u;
         const uint32_t sb = uu >> 3, c = uu & 7u;
@@ -899,7 +904,24 @@ __global__ __launch_bounds__(NW * 64) void gemv_kquant_stream_kernel(TaskTable t
             a[i] = p[i];
             b[i] = p[8 + i];
         }
+        float4 wa[RN == kRnNormIn ? 4 : 1], wb[RN == kRnNormIn ? 4 : 1];
+        if constexpr (RN == kRnNormIn) {
+            const float4* pw = reinterpret_cast<const float4*>(rn.w + (reinterpret_cast<const float*>(p) - x));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                wa[i] = pw[i];
+                wb[i] = pw[8 + i];
+            }
+            slot = lane < kRnSlots ? rn.ss_in[lane] : 0.0;
+        }
         __builtin_amdgcn_sched_barrier(0);
+        if constexpr (RN == kRnNormIn) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                wl[4 * i] = wa[i].x; wl[4 * i + 1] = wa[i].y; wl[4 * i + 2] = wa[i].z; wl[4 * i + 3] = wa[i].w;
+                wh[4 * i] = wb[i].x; wh[4 * i + 1] = wb[i].y; wh[4 * i + 2] = wb[i].z; wh[4 * i + 3] = wb[i].w;
+            }
+        }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             xl[4 * i] = a[i].x; xl[4 * i + 1] = a[i].y; xl[4 * i + 2] = a[i].z; xl[4 * i + 3] = a[i].w;
@@ -937,14 +959,35 @@ __global__ __launch_bounds__(NW * 64) void gemv_kquant_stream_kernel(TaskTable t
             if (lane + 64 < int(CUNITS)) buf[r * CUNITS + lane + 64] = v[r][1];
         }
     };
+    // add-out: lane r's residual value of row row0 + r, fetched with the
+    // block's weights
+    auto resid = [&](uint32_t row0, int ti) {
+        const GemvTask& t = tt.t[ti];
+        return lane < R ? t.y[min(row0 + uint32_t(lane), t.rows - 1)] : 0.0f;
+    };
     uint32_t blk = blockIdx.x;
     uint4 v[R][2];
     uint32_t row0 = 0;
     int ti = 0;
+    float res = 0.0f;
+    double ssacc = 0.0;
     {
         const uint8_t* rowp[R];
         locate(min(blk, total_blocks - 1), rowp, row0, ti);
         load(rowp, v);
+        if constexpr (RN == kRnAddOut) res = resid(row0, ti);
+    }
+    if constexpr (RN == kRnNormIn) {
+        // x is the residual: v * inv * w, the RMSNorm kernel's arithmetic;
+        // after the first weight block is issued
+        __builtin_amdgcn_sched_barrier(0);
+        const double ss = wave_sum(slot);
+        const float inv = 1.0f / sqrtf(float(ss / double(cols)) + rn.eps);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            xl[i] = xl[i] * inv * wl[i];
+            xh[i] = xh[i] * inv * wh[i];
+        }
     }
     sxl = 0.0f;
     sxh = 0.0f;
@@ -962,11 +1005,23 @@ __global__ __launch_bounds__(NW * 64) void gemv_kquant_stream_kernel(TaskTable t
         const uint32_t nblk = blk + gridDim.x;
         const uint32_t row0c = row0;
         const int tic = ti;
+        const float resc = res;
         if (nblk < total_blocks) {
             const uint8_t* rowp[R];
             locate(nblk, rowp, row0, ti);
             load(rowp, v);
+            if constexpr (RN == kRnAddOut) res = resid(row0, ti);
         }
+        // the row value lane r stores: the sum, or the residual plus the sum
+        auto out = [&](float sum) {
+            if constexpr (RN == kRnAddOut) {
+                const float nv = resc + sum;
+                ssacc += double(nv) * double(nv);
+                return nv;
+            } else {
+                return sum;
+            }
+        };
         float acc[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -982,7 +1037,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kquant_stream_kernel(TaskTable t
         } else if constexpr (S == 1) {
 #pragma unroll
             for (int r = 0; r < R; ++r)
-                if (lane == r && row0c + r < t.rows) t.y[row0c + r] = acc[r];
+                if (lane == r && row0c + r < t.rows) t.y[row0c + r] = out(acc[r]);
         } else if constexpr (PAIR) {
             if (lane == 0) {
                 red[parity][wave][0] = acc[0];
@@ -1009,11 +1064,25 @@ __global__ __launch_bounds__(NW * 64) void gemv_kquant_stream_kernel(TaskTable t
                 float sum = 0.0f;
 #pragma unroll
                 for (int s2 = 0; s2 < S; ++s2) sum += red[parity][team * S + s2][lane];
-                if (row0c + lane < t.rows) t.y[row0c + lane] = sum;
+                if (row0c + lane < t.rows) t.y[row0c + lane] = out(sum);
             }
             parity ^= 1;
         }
         blk = nblk;
+    }
+    if constexpr (RN == kRnAddOut) {
+        // every wave leaves the loop together: one atomic per workgroup
+        __shared__ double ssw[NW];
+        const double sw = wave_sum(ssacc);
+        if (lane == 0) ssw[wave] = sw;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            double tot = 0.0;
+#pragma unroll
+            for (int i = 0; i < NW; ++i) tot += ssw[i];
+            atomicAdd(rn.ss_out + blockIdx.x % kRnSlots, tot);
+        }
+        if (blockIdx.x == 0 && threadIdx.x < kRnSlots && rn.ss_zero) rn.ss_zero[threadIdx.x] = 0.0;
     }
 }
 
@@ -1664,8 +1733,9 @@ hipError_t launch_q6k_stream_any(TaskTable& tt, const float* x, uint32_t cols, h
     return total_rows >= 4096 ? launch_q6k_stream_s<2>(tt, x, cols, stream) : launch_q6k_stream_s<1>(tt, x, cols, stream);
 }
 
-template <int FMT, int R, int S, int NW, bool PAIR = false>
-hipError_t launch_kquant_stream(TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream, uint32_t wg_per_cu = 1) {
+template <int FMT, int R, int S, int NW, bool PAIR = false, int RN = kRnNone>
+hipError_t launch_kquant_stream(TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream, uint32_t wg_per_cu = 1,
+                                const ResidNorm& rn = ResidNorm{}) {
     constexpr uint32_t RB = (NW / S) * R;
     constexpr uint32_t CUNITS = 8 * (FMT == kQ5_K ? 176 : 144) / 16;
     uint32_t blocks = 0;
@@ -1680,24 +1750,25 @@ hipError_t launch_kquant_stream(TaskTable& tt, const float* x, uint32_t cols, hi
     }
     const uint32_t grid = std::min<uint32_t>(blocks, uint32_t(cu_count()) * wg_per_cu);
     const size_t lds = size_t(NW) * R * CUNITS * 16;
-    hipLaunchKernelGGL((gemv_kquant_stream_kernel<FMT, R, S, NW, PAIR>), dim3(grid), dim3(NW * 64), lds, stream, tt, x,
-                       cols, blocks);
+    hipLaunchKernelGGL((gemv_kquant_stream_kernel<FMT, R, S, NW, PAIR, RN>), dim3(grid), dim3(NW * 64), lds, stream, tt,
+                       x, cols, blocks, rn);
     return hipGetLastError();
 }
 // 64-unit slices per row -> (S, waves per workgroup); two workgroups per CU
 // (measured faster than one 16-wave workgroup with the same rows per step:
 // Q4_K 14336x4096 15.2 -> 13.9 us, Q5_K 17.0 -> 15.4 us at 2 rows per step).
-template <int FMT, int R, bool PAIR = false>
-hipError_t launch_kquant_stream_s(TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream) {
+template <int FMT, int R, bool PAIR = false, int RN = kRnNone>
+hipError_t launch_kquant_stream_s(TaskTable& tt, const float* x, uint32_t cols, hipStream_t stream,
+                                  const ResidNorm& rn = ResidNorm{}) {
     switch ((cols + 2047) / 2048) {
-    case 1: return launch_kquant_stream<FMT, R, 1, 8, PAIR>(tt, x, cols, stream, 2);
-    case 2: return launch_kquant_stream<FMT, R, 2, 8, PAIR>(tt, x, cols, stream, 2);
-    case 3: return launch_kquant_stream<FMT, R, 3, 6, PAIR>(tt, x, cols, stream, 2);
-    case 4: return launch_kquant_stream<FMT, R, 4, 8, PAIR>(tt, x, cols, stream, 2);
-    case 5: return launch_kquant_stream<FMT, R, 5, 5, PAIR>(tt, x, cols, stream, 2);
-    case 6: return launch_kquant_stream<FMT, R, 6, 6, PAIR>(tt, x, cols, stream, 2);
-    case 7: return launch_kquant_stream<FMT, R, 7, 7, PAIR>(tt, x, cols, stream, 2);
-    case 8: return launch_kquant_stream<FMT, R, 8, 8, PAIR>(tt, x, cols, stream, 2);
+    case 1: return launch_kquant_stream<FMT, R, 1, 8, PAIR, RN>(tt, x, cols, stream, 2, rn);
+    case 2: return launch_kquant_stream<FMT, R, 2, 8, PAIR, RN>(tt, x, cols, stream, 2, rn);
+    case 3: return launch_kquant_stream<FMT, R, 3, 6, PAIR, RN>(tt, x, cols, stream, 2, rn);
+    case 4: return launch_kquant_stream<FMT, R, 4, 8, PAIR, RN>(tt, x, cols, stream, 2, rn);
+    case 5: return launch_kquant_stream<FMT, R, 5, 5, PAIR, RN>(tt, x, cols, stream, 2, rn);
+    case 6: return launch_kquant_stream<FMT, R, 6, 6, PAIR, RN>(tt, x, cols, stream, 2, rn);
+    case 7: return launch_kquant_stream<FMT, R, 7, 7, PAIR, RN>(tt, x, cols, stream, 2, rn);
+    case 8: return launch_kquant_stream<FMT, R, 8, 8, PAIR, RN>(tt, x, cols, stream, 2, rn);
     default: return hipErrorInvalidConfiguration;
     }
 }
@@ -1877,7 +1948,7 @@ hipError_t launch_gemv_prologue_silu_pair(int fmt, const GemvTask& gate, const G
 }
 
 hipError_t launch_gemv_silu_pair(int fmt, const GemvTask& gate, const GemvTask& up, const float* x, size_t cols,
-                                 hipStream_t stream) {
+                                 hipStream_t stream, const ResidNorm* rn) {
     if (!x || !row_bytes(fmt, cols) || cols > (1u << 24) || !gate.w || !gate.y || !up.w || !gate.rows)
         return hipErrorInvalidValue;
     auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
@@ -1890,9 +1961,43 @@ hipError_t launch_gemv_silu_pair(int fmt, const GemvTask& gate, const GemvTask& 
     tt.t[0] = gate;
     tt.t[1] = GemvTask{up.w, gate.y, up.rows};
     const uint32_t c = static_cast<uint32_t>(cols);
+    if (rn) {
+        if (q6k || !rn->ss_in || !a16(rn->w)) return hipErrorInvalidConfiguration;
+        return fmt == kQ4_K ? launch_kquant_stream_s<kQ4_K, 2, true, kRnNormIn>(tt, x, c, stream, *rn)
+                            : launch_kquant_stream_s<kQ5_K, 2, true, kRnNormIn>(tt, x, c, stream, *rn);
+    }
     if (q6k) return launch_q6k_stream_s<2, true>(tt, x, c, stream);
     return fmt == kQ4_K ? launch_kquant_stream_s<kQ4_K, 2, true>(tt, x, c, stream)
                         : launch_kquant_stream_s<kQ5_K, 2, true>(tt, x, c, stream);
+}
+
+bool gemv_resid_supported(int fmt, size_t cols) {
+    return (fmt == kQ4_K || fmt == kQ5_K) && cols && cols % 256 == 0 && cols <= 16384;
+}
+
+hipError_t launch_gemv_resid(int fmt, int mode, const GemvTask* tasks, int count, const float* x, size_t cols,
+                             const ResidNorm& rn, hipStream_t stream) {
+    if (count < 1 || count > kMaxTasks || !x || !row_bytes(fmt, cols)) return hipErrorInvalidValue;
+    if ((mode == kRnNormIn && (!rn.ss_in || !rn.w)) || (mode == kRnAddOut && !rn.ss_out) ||
+        (mode != kRnNormIn && mode != kRnAddOut))
+        return hipErrorInvalidValue;
+    auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    if (!gemv_resid_supported(fmt, cols) || !a16(x) || (mode == kRnNormIn && !a16(rn.w)))
+        return hipErrorInvalidConfiguration;
+    TaskTable tt{};
+    tt.count = count;
+    for (int i = 0; i < count; ++i) {
+        if (!tasks[i].w || !tasks[i].y || !tasks[i].rows) return hipErrorInvalidValue;
+        if (!a16(tasks[i].w)) return hipErrorInvalidConfiguration;
+        tt.t[i] = tasks[i];
+    }
+    const uint32_t c = static_cast<uint32_t>(cols);
+    // 2 rows per step: the projection-sized outputs' measured best
+    if (mode == kRnNormIn)
+        return fmt == kQ4_K ? launch_kquant_stream_s<kQ4_K, 2, false, kRnNormIn>(tt, x, c, stream, rn)
+                            : launch_kquant_stream_s<kQ5_K, 2, false, kRnNormIn>(tt, x, c, stream, rn);
+    return fmt == kQ4_K ? launch_kquant_stream_s<kQ4_K, 2, false, kRnAddOut>(tt, x, c, stream, rn)
+                        : launch_kquant_stream_s<kQ5_K, 2, false, kRnAddOut>(tt, x, c, stream, rn);
 }
 
 }  // namespace zq

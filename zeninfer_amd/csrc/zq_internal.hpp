@@ -50,12 +50,36 @@ hipError_t launch_gemv_prologue(int fmt, const GemvTask* tasks, int count, const
 // cols <= 4096, equal rows; hipErrorInvalidConfiguration otherwise.
 hipError_t launch_gemv_prologue_silu_pair(int fmt, const GemvTask& gate, const GemvTask& up, const XPrologue& pro,
                                           size_t cols, hipStream_t stream);
+// The decode residual stream carried between K-quant GEMVs without RMSNorm
+// launches.  An add-out GEMV adds each output row into the residual (y is
+// the residual: y_i += W_i . x), adds the new values' squares (in double)
+// into kRnSlots accumulator slots (ss_out, workgroup g into slot g %
+// kRnSlots) and clears the slots of ss_zero.  A norm-in GEMV takes x = the
+// residual and uses x * inv * w with inv = 1/sqrtf(float(ss/cols) + eps), ss
+// the slots of ss_in summed in slot order -- the RMSNorm kernel's formula.
+struct ResidNorm {
+    const double* ss_in;
+    const float* w;
+    double* ss_out;
+    double* ss_zero;
+    float eps;
+};
+constexpr int kRnNone = 0, kRnNormIn = 1, kRnAddOut = 2;
+constexpr int kRnSlots = 64;  // one per lane of the reading wave
+// Q4_K / Q5_K, cols % 256 == 0, cols <= 16384, 16-byte aligned x, weights and
+// norm weight; hipErrorInvalidConfiguration otherwise.
+hipError_t launch_gemv_resid(int fmt, int mode, const GemvTask* tasks, int count, const float* x, size_t cols,
+                             const ResidNorm& rn, hipStream_t stream);
+bool gemv_resid_supported(int fmt, size_t cols);
+
 // gate|up over a plain x that stores f = silu(gate.x) * (up.x) into gate.y
 // (up.y unused): Q4_K / Q5_K, and Q6_K with cols % 2048 == 0; cols <= 16384,
 // equal rows, 16-byte aligned x and weights; hipErrorInvalidConfiguration
 // otherwise.
+// With rn (Q4_K / Q5_K only), x is the residual and is normalised as a
+// norm-in GEMV's.
 hipError_t launch_gemv_silu_pair(int fmt, const GemvTask& gate, const GemvTask& up, const float* x, size_t cols,
-                                 hipStream_t stream);
+                                 hipStream_t stream, const ResidNorm* rn = nullptr);
 
 // Per-32-element activation quantiser (int8 + fp32 scale per block).
 hipError_t launch_quantize_acts(const float* X, int8_t* xq, float* xs, size_t M, size_t K,

@@ -89,11 +89,13 @@ struct zq_model {
     float* attn_part = nullptr;  // decode attention chunk partials
     float* qkv = nullptr;        // prefill output of the fused Q|K|V projection, [T][QW + 2 KW]
     void* argmax_part = nullptr;
+    double* ss = nullptr;  // 2 x zq::kRnSlots sum-of-squares slots of the residual-norm decode
 
     uint32_t cur_pos = 0;  // positions held in the cache
     bool use_graph = true;
     bool fused = false;    // decode step with norms and SiLU folded into the GEMVs
     bool fuse_quant = true;  // prefill norms / SiLU*up also write the int8 activations; K-quant gate|up pair
+    bool resid_norm = false;  // Q4_K / Q5_K decode with the norms carried by the GEMVs (zq::ResidNorm)
     hipGraphExec_t decode_exec = nullptr;
     hipGraph_t decode_graph = nullptr;
 
@@ -167,7 +169,9 @@ bool alloc_runtime(zq_model& m, std::string& e) {
     const size_t xq_bytes = align_up(T * widest, kAlign), xs_bytes = align_up(T * widest / 32 * 4, kAlign);
     const size_t attn_bytes = align_up(zq::attention_decode_partial_floats(c.heads, c.head_dim, c.max_positions) * 4, kAlign);
     const size_t arg_bytes = align_up(zq::argmax_partial_bytes(), kAlign);
-    total += xq_bytes + xs_bytes + align_up(partial, kAlign) + 3 * kAlign + align_up(T * 4, kAlign) + attn_bytes + arg_bytes;
+    const size_t ss_bytes = align_up(2 * zq::kRnSlots * sizeof(double), kAlign);
+    total += xq_bytes + xs_bytes + align_up(partial, kAlign) + 3 * kAlign + align_up(T * 4, kAlign) + attn_bytes + arg_bytes +
+             ss_bytes;
     void* arena;
     if (!dev_alloc(m, &arena, total)) { e = "device allocation failed (activations)"; return false; }
     m.act_bytes = total;
@@ -180,6 +184,10 @@ bool alloc_runtime(zq_model& m, std::string& e) {
     m.attn_part = reinterpret_cast<float*>(p); p += attn_bytes;
     if (hipMemset(m.attn_part, 0, attn_bytes) != hipSuccess) { e = "device memset failed (attention counters)"; return false; }
     m.argmax_part = p; p += arg_bytes;
+    m.ss = reinterpret_cast<double*>(p); p += ss_bytes;
+    // the residual-norm decode's first o GEMV adds into slots that start at 0;
+    // every decode step leaves them at 0 again
+    if (hipMemset(m.ss, 0, ss_bytes) != hipSuccess) { e = "device memset failed (norm slots)"; return false; }
     m.pos_dev = reinterpret_cast<uint32_t*>(p); p += kAlign;
     m.next_dev = reinterpret_cast<uint32_t*>(p); p += kAlign;
     p += kAlign;
@@ -487,9 +495,47 @@ hipError_t enqueue_decode_fused(zq_model& m) {
     return zq::launch_argmax(m.logits, c.vocab, m.next_dev, m.argmax_part, m.stream);
 }
 
+// Decode step on Q4_K / Q5_K projections with the residual adds and RMSNorms
+// carried by the GEMVs (zq::ResidNorm): the o and down GEMVs add their rows
+// into the residual x and their squares into slot set A (o) or B (down), and
+// clear the other set; QKV (from B) and the gate|up pair (from A) normalise x
+// as they load it.  Layer 0's input and the output norm keep their RMSNorm
+// launches.  Per layer: QKV, attention, o, gate|up, down.
+hipError_t enqueue_decode_resid(zq_model& m) {
+    const auto& c = m.cfg;
+    const uint32_t E = c.embedding, QW = c.heads * c.head_dim, KW = c.kv_heads * c.head_dim, F = c.ffn;
+    double* A = m.ss;
+    double* B = m.ss + zq::kRnSlots;
+    HIPCHK(zq::launch_rmsnorm(m.x, m.layers[0].attn_norm, m.h, 1, E, c.rms_epsilon, m.stream));
+    for (uint32_t l = 0; l < c.layers; ++l) {
+        Layer& L = m.layers[l];
+        zq::GemvTask tq[3] = {{L.q.p, m.q, QW}, {L.k.p, m.k, KW}, {L.v.p, m.v, KW}};
+        if (l == 0) {
+            HIPCHK(zq::launch_gemv(L.q.fmt, tq, 3, m.h, E, m.stream));
+        } else {
+            const zq::ResidNorm rq{B, L.attn_norm, nullptr, nullptr, c.rms_epsilon};
+            HIPCHK(zq::launch_gemv_resid(L.q.fmt, zq::kRnNormIn, tq, 3, m.x, E, rq, m.stream));
+        }
+        HIPCHK(zq::launch_attention_decode(m.q, m.k, m.v, L.kc, L.vc, m.cos_tab, m.sin_tab, m.attn_part, m.att,
+                                           m.pos_dev, c.heads, c.kv_heads, c.head_dim, m.pairs, c.max_positions,
+                                           m.attn_scale, m.stream));
+        const zq::GemvTask to{L.o.p, m.x, E};
+        const zq::ResidNorm ro{nullptr, nullptr, A, B, 0.0f};
+        HIPCHK(zq::launch_gemv_resid(L.o.fmt, zq::kRnAddOut, &to, 1, m.att, QW, ro, m.stream));
+        const zq::ResidNorm rg{A, L.ffn_norm, nullptr, nullptr, c.rms_epsilon};
+        HIPCHK(zq::launch_gemv_silu_pair(L.gate.fmt, {L.gate.p, m.act, F}, {L.up.p, m.up, F}, m.x, E, m.stream, &rg));
+        const zq::GemvTask td{L.down.p, m.x, E};
+        const zq::ResidNorm rd{nullptr, nullptr, B, A, 0.0f};
+        HIPCHK(zq::launch_gemv_resid(L.down.fmt, zq::kRnAddOut, &td, 1, m.act, F, rd, m.stream));
+    }
+    HIPCHK(zq::launch_rmsnorm(m.x, m.out_norm, m.h, 1, E, c.rms_epsilon, m.stream));
+    return enqueue_head(m, 0);
+}
+
 hipError_t enqueue_decode(zq_model& m) {
     HIPCHK(zq::launch_embed(m.embd.fmt, m.embd.p, m.tokens_dev, m.cfg.vocab, m.x, m.cfg.embedding, 1, m.stream));
     if (m.fused) return enqueue_decode_fused(m);
+    if (m.resid_norm) return enqueue_decode_resid(m);
     HIPCHK(enqueue_layers(m, 1));
     return enqueue_head(m, 0);
 }
@@ -511,6 +557,14 @@ void choose_fused(zq_model& m) {
             ok(L.down.fmt) && ok(L.o.fmt);
     m.fused = f;
     m.fuse_quant = !(e && e[0] == '0');
+    // Q4_K / Q5_K: every projection of every layer on the residual-norm GEMVs
+    const uint32_t QW = c.heads * c.head_dim, KW = c.kv_heads * c.head_dim;
+    auto rs = [&](const Weight& w, uint32_t cols) { return zq::gemv_resid_supported(w.fmt, cols); };
+    bool r = m.fuse_quant && !f && QW % 256 == 0 && KW > 0;
+    for (const Layer& L : m.layers)
+        r = r && rs(L.q, c.embedding) && L.k.fmt == L.q.fmt && L.v.fmt == L.q.fmt && rs(L.o, QW) &&
+            rs(L.gate, c.embedding) && L.up.fmt == L.gate.fmt && rs(L.down, c.ffn);
+    m.resid_norm = r;
 }
 
 int finish_outputs(zq_model& m, float* logits, uint32_t* next) {
