@@ -86,3 +86,26 @@ def test_no_scalar_cache_writes(device_asm):
         hits = re.findall(r"^\s*(s_(?:store|buffer_store|scratch_store|atomic|buffer_atomic)\w*|s_dcache_(?:wb|discard)\w*)\b",
                           asm, re.M)
         assert not hits, f"{src}: scalar-cache writes {sorted(set(hits))}"
+
+
+def test_no_kernel_spills_to_scratch(device_asm):
+    """Every kernel of the library runs without private (scratch) memory:
+    register spills on these streaming kernels cost more than any variant
+    that needs them was worth (a Q4_0 GEMV step of four row groups spilled
+    and was never run; a 64-K stage of the super-block GEMM spilled and was
+    slower), so a change that makes one spill fails here before any run.
+    Exempt: the int8 GEMMs' DOTS = true instantiations, the bit-exact test
+    hook that stores every block's integer dot instead of accumulating; no
+    product path launches them."""
+    dots_mode = re.compile(r"gemm_i8_\w*kernelILi\d+ELb1E")
+    bad, exempt = [], 0
+    for src, asm in device_asm.items():
+        for m in re.finditer(r"^\s*\.amdhsa_kernel (\S+)(.*?)\.end_amdhsa_kernel", asm, re.M | re.S):
+            size = re.search(r"\.amdhsa_private_segment_fixed_size (\d+)", m.group(2))
+            if size and int(size.group(1)) != 0:
+                if dots_mode.search(m.group(1)):
+                    exempt += 1
+                else:
+                    bad.append((src, m.group(1)[:120], int(size.group(1))))
+    assert not bad, bad
+    assert exempt <= 4  # today: the Q8_0 direct and tiled DOTS kernels
